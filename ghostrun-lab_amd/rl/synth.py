@@ -1,0 +1,427 @@
+"""Seed-generated workloads: synthetic NES cartridges (iNES images) and SMB-style RAM trajectories.
+
+The reference ships no ROMs (its README names the commercial carts it trains on), so the benchmark configs use
+cartridges generated here from a seed:
+
+* ``nrom_cart(seed)`` - NROM-128: 16 KB PRG of generated 6502 code (reset init, an NMI handler doing OAM DMA via
+  $4014 and nametable writes via $2006/$2007, a main loop reading $4016 and branching on the pad bits, RAM
+  counters and seeded arithmetic blocks) and 8 KB CHR of uniform-random 2bpp tiles.
+* ``mmc3_cart(seed)`` - MMC3: 256 KB PRG / 128 KB CHR. The main loop switches the $8000 PRG bank and calls into
+  it about every 200 instructions, switches CHR banks, arms the scanline IRQ at a line 20..220 that depends on
+  the console's own history, and splits the scroll on the sprite-0 hit.
+* ``smb_ram15(seed, n_envs, steps)`` - per env-step the 15 RAM bytes the SMB reward reader reads (x position as a
+  +-1..4 px random walk with 5% rollback jumps, world/level advancing with p 1e-3, lives lost with p 5e-4, BCD-like
+  score digits), packed as ``rl10_smb_run`` takes them.
+
+The RAM addresses the SMB reader reads (0x0E, 0x6D, 0x86, 0xB5, 0x75A-0x75F, 0x770, 0x772, 0x7DD-0x7E2) are never
+written by the generated carts, so their reward stays 0 and no episode ends except by the stall clock.
+"""
+from __future__ import annotations
+
+import numpy as np
+
+# ------------------------------------------------------------------------------------------- assembler
+
+_OPS = {
+    'ADC': dict(imm=0x69, zp=0x65, zpx=0x75, abs=0x6D, abx=0x7D, aby=0x79, izx=0x61, izy=0x71),
+    'AND': dict(imm=0x29, zp=0x25, zpx=0x35, abs=0x2D, abx=0x3D, aby=0x39, izx=0x21, izy=0x31),
+    'ASL': dict(acc=0x0A, zp=0x06, zpx=0x16, abs=0x0E, abx=0x1E),
+    'BCC': dict(rel=0x90), 'BCS': dict(rel=0xB0), 'BEQ': dict(rel=0xF0), 'BMI': dict(rel=0x30),
+    'BNE': dict(rel=0xD0), 'BPL': dict(rel=0x10), 'BVC': dict(rel=0x50), 'BVS': dict(rel=0x70),
+    'BIT': dict(zp=0x24, abs=0x2C),
+    'BRK': dict(imp=0x00), 'CLC': dict(imp=0x18), 'CLD': dict(imp=0xD8), 'CLI': dict(imp=0x58), 'CLV': dict(imp=0xB8),
+    'CMP': dict(imm=0xC9, zp=0xC5, zpx=0xD5, abs=0xCD, abx=0xDD, aby=0xD9, izx=0xC1, izy=0xD1),
+    'CPX': dict(imm=0xE0, zp=0xE4, abs=0xEC), 'CPY': dict(imm=0xC0, zp=0xC4, abs=0xCC),
+    'DEC': dict(zp=0xC6, zpx=0xD6, abs=0xCE, abx=0xDE), 'DEX': dict(imp=0xCA), 'DEY': dict(imp=0x88),
+    'EOR': dict(imm=0x49, zp=0x45, zpx=0x55, abs=0x4D, abx=0x5D, aby=0x59, izx=0x41, izy=0x51),
+    'INC': dict(zp=0xE6, zpx=0xF6, abs=0xEE, abx=0xFE), 'INX': dict(imp=0xE8), 'INY': dict(imp=0xC8),
+    'JMP': dict(abs=0x4C, ind=0x6C), 'JSR': dict(abs=0x20),
+    'LDA': dict(imm=0xA9, zp=0xA5, zpx=0xB5, abs=0xAD, abx=0xBD, aby=0xB9, izx=0xA1, izy=0xB1),
+    'LDX': dict(imm=0xA2, zp=0xA6, zpy=0xB6, abs=0xAE, aby=0xBE),
+    'LDY': dict(imm=0xA0, zp=0xA4, zpx=0xB4, abs=0xAC, abx=0xBC),
+    'LSR': dict(acc=0x4A, zp=0x46, zpx=0x56, abs=0x4E, abx=0x5E), 'NOP': dict(imp=0xEA),
+    'ORA': dict(imm=0x09, zp=0x05, zpx=0x15, abs=0x0D, abx=0x1D, aby=0x19, izx=0x01, izy=0x11),
+    'PHA': dict(imp=0x48), 'PHP': dict(imp=0x08), 'PLA': dict(imp=0x68), 'PLP': dict(imp=0x28),
+    'ROL': dict(acc=0x2A, zp=0x26, zpx=0x36, abs=0x2E, abx=0x3E),
+    'ROR': dict(acc=0x6A, zp=0x66, zpx=0x76, abs=0x6E, abx=0x7E),
+    'RTI': dict(imp=0x40), 'RTS': dict(imp=0x60),
+    'SBC': dict(imm=0xE9, zp=0xE5, zpx=0xF5, abs=0xED, abx=0xFD, aby=0xF9, izx=0xE1, izy=0xF1),
+    'SEC': dict(imp=0x38), 'SED': dict(imp=0xF8), 'SEI': dict(imp=0x78),
+    'STA': dict(zp=0x85, zpx=0x95, abs=0x8D, abx=0x9D, aby=0x99, izx=0x81, izy=0x91),
+    'STX': dict(zp=0x86, zpy=0x96, abs=0x8E), 'STY': dict(zp=0x84, zpx=0x94, abs=0x8C),
+    'TAX': dict(imp=0xAA), 'TAY': dict(imp=0xA8), 'TSX': dict(imp=0xBA), 'TXA': dict(imp=0x8A),
+    'TXS': dict(imp=0x9A), 'TYA': dict(imp=0x98),
+}
+_LEN = dict(imp=1, acc=1, imm=2, zp=2, zpx=2, zpy=2, izx=2, izy=2, rel=2, abs=3, abx=3, aby=3, ind=3)
+OPCODES = {op: (mn, mode) for mn, modes in _OPS.items() for mode, op in modes.items()}  # the 151 official ones
+
+
+class Asm:
+    """Two-pass 6502 assembler: ``a.op('LDA', 'imm', 5)``, labels by name, ``a.byte(...)`` for data."""
+
+    def __init__(self, origin: int):
+        self.origin = origin
+        self.items = []          # (kind, payload)
+        self.labels = {}
+        self.pc = origin
+
+    def label(self, name):
+        assert name not in self.labels, name
+        self.labels[name] = self.pc
+        return name
+
+    def op(self, mn, mode='imp', arg=None):
+        assert mode in _OPS[mn], (mn, mode)
+        self.items.append(('op', (mn, mode, arg, self.pc)))
+        self.pc += _LEN[mode]
+
+    def byte(self, *vals):
+        data = bytes(int(v) & 0xFF for v in vals)
+        self.items.append(('data', data))
+        self.pc += len(data)
+
+    def data(self, buf):
+        self.items.append(('data', bytes(buf)))
+        self.pc += len(buf)
+
+    def _val(self, arg):
+        return self.labels[arg] if isinstance(arg, str) else int(arg)
+
+    def assemble(self) -> bytes:
+        out = bytearray()
+        for kind, p in self.items:
+            if kind == 'data':
+                out += p
+                continue
+            mn, mode, arg, pc = p
+            out.append(_OPS[mn][mode])
+            if mode == 'rel':
+                d = self._val(arg) - (pc + 2)
+                assert -128 <= d <= 127, f'branch out of range at {pc:04x}'
+                out.append(d & 0xFF)
+            elif _LEN[mode] == 2:
+                v = self._val(arg)
+                assert 0 <= v <= 0xFF, (mn, mode, v)
+                out.append(v)
+            elif _LEN[mode] == 3:
+                v = self._val(arg)
+                out += bytes((v & 0xFF, (v >> 8) & 0xFF))
+        return bytes(out)
+
+
+def ines(prg: bytes, chr_: bytes, mapper: int, vertical: bool = True) -> bytes:
+    assert len(prg) % 16384 == 0 and len(chr_) % 8192 == 0
+    h = bytearray(b'NES\x1a')
+    h += bytes((len(prg) // 16384, len(chr_) // 8192, ((mapper & 15) << 4) | (1 if vertical else 0),
+                mapper & 0xF0))
+    h += bytes(8)
+    return bytes(h) + prg + chr_
+
+
+# ------------------------------------------------------------------------------------- code builders
+
+# zero-page / RAM map of the generated programs (none of the SMB reader's addresses)
+PAD, CTRL_SHADOW, PX, PY, ACNT, TSEL, BACC = 0x10, 0x11, 0x20, 0x21, 0x22, 0x23, 0x24
+CNT_LO, CNT_HI, NTP_LO, NTP_HI, FRAMES, NMIFLAG, BANK, IRQLINE = 0x30, 0x31, 0x32, 0x33, 0x40, 0x41, 0x42, 0x43
+SCRATCH_ZP = list(range(0x50, 0x6C))      # stays below 0x6D
+WORK_PAGE = 0x0300                        # 256 B work area
+OAM_PAGE = 0x0200
+
+
+def _filler(a: Asm, rng: np.random.Generator, nblocks: int, tag: str, table: str, with_prg_ram=False):
+    """Seeded blocks of 6502 work on RAM counters: arithmetic, shifts, table lookups, short loops and
+    data- and pad-dependent branches (so consoles with different pads take different paths)."""
+    zp = lambda: int(rng.choice(SCRATCH_ZP))  # noqa: E731
+    for i in range(nblocks):
+        k = int(rng.integers(0, 9 if with_prg_ram else 8))
+        lab = f'{tag}_{i}'
+        if k == 0:
+            a.op('LDA', 'zp', zp()); a.op('CLC'); a.op('ADC', 'zp', zp()); a.op('STA', 'zp', zp())
+        elif k == 1:
+            a.op('LDA', 'zp', zp()); a.op('ASL', 'acc'); a.op('EOR', 'imm', int(rng.integers(256)))
+            a.op('STA', 'zp', zp())
+        elif k == 2:
+            a.op('LDX', 'zp', zp()); a.op('LDA', 'abx', table); a.op('STA', 'abx', WORK_PAGE)
+        elif k == 3:
+            a.op('LDY', 'imm', int(rng.integers(3, 12)))
+            a.label(lab + 'l')
+            a.op('LDA', 'aby', WORK_PAGE); a.op('ADC', 'imm', int(rng.integers(256))); a.op('STA', 'aby', WORK_PAGE)
+            a.op('DEY'); a.op('BNE', 'rel', lab + 'l')
+        elif k == 4:
+            a.op('LDA', 'zp', zp()); a.op('AND', 'imm', int(1 << rng.integers(8))); a.op('BEQ', 'rel', lab)
+            a.op('INC', 'zp', zp()); a.op('LDA', 'zp', CNT_LO); a.op('STA', 'zp', zp())
+            a.label(lab)
+        elif k == 5:
+            a.op('LDA', 'zp', PAD); a.op('AND', 'imm', int(1 << rng.integers(8))); a.op('BNE', 'rel', lab)
+            a.op('LDA', 'zp', zp()); a.op('ROR', 'acc'); a.op('STA', 'zp', zp()); a.op('INC', 'abs', WORK_PAGE + int(rng.integers(256)))
+            a.label(lab)
+        elif k == 6:
+            a.op('LDA', 'zp', zp()); a.op('SEC'); a.op('SBC', 'zp', zp()); a.op('BCS', 'rel', lab)
+            a.op('EOR', 'imm', 0xFF); a.op('LSR', 'acc')
+            a.label(lab)
+            a.op('STA', 'zp', zp())
+        elif k == 7:
+            a.op('LDA', 'zp', PX); a.op('CMP', 'zp', PY); a.op('BCC', 'rel', lab)
+            a.op('LDA', 'zp', ACNT); a.op('AND', 'imm', 0x0F); a.op('TAX')
+            a.op('INC', 'zpx', 0x50); a.op('LDA', 'zpx', 0x50); a.op('STA', 'zp', zp())
+            a.label(lab)
+        else:
+            a.op('LDX', 'zp', zp()); a.op('LDA', 'abx', 0x6000); a.op('ADC', 'zp', zp()); a.op('STA', 'abx', 0x6000)
+
+
+def _read_pad(a: Asm, tag: str):
+    a.op('LDA', 'imm', 1); a.op('STA', 'abs', 0x4016); a.op('LDA', 'imm', 0); a.op('STA', 'abs', 0x4016)
+    a.op('LDX', 'imm', 8)
+    a.label(tag + 'rd')
+    a.op('LDA', 'abs', 0x4016); a.op('LSR', 'acc'); a.op('ROR', 'zp', PAD); a.op('DEX'); a.op('BNE', 'rel', tag + 'rd')
+
+
+def _pad_moves(a: Asm, table: str):
+    for bit, op, var, lab in ((0x80, 'INC', PX, 'nr'), (0x40, 'DEC', PX, 'nl'), (0x20, 'INC', PY, 'nd'),
+                              (0x10, 'DEC', PY, 'nu')):
+        a.op('LDA', 'zp', PAD); a.op('AND', 'imm', bit); a.op('BEQ', 'rel', 'mv_' + lab); a.op(op, 'zp', var)
+        a.label('mv_' + lab)
+    a.op('LDA', 'zp', PAD); a.op('AND', 'imm', 0x01); a.op('BEQ', 'rel', 'mv_na')
+    a.op('INC', 'zp', ACNT); a.op('LDA', 'zp', ACNT); a.op('AND', 'imm', 0x0F); a.op('TAX'); a.op('LDA', 'abx', table)
+    a.op('STA', 'zp', TSEL)
+    a.label('mv_na')
+    a.op('LDA', 'zp', PAD); a.op('AND', 'imm', 0x02); a.op('BEQ', 'rel', 'mv_nb')
+    a.op('LDA', 'zp', BACC); a.op('CLC'); a.op('ADC', 'zp', PX); a.op('STA', 'zp', BACC)
+    a.label('mv_nb')
+    a.op('INC', 'zp', CNT_LO); a.op('BNE', 'rel', 'mv_c1'); a.op('INC', 'zp', CNT_HI)
+    a.label('mv_c1')
+
+
+def _reset_common(a: Asm, ctrl: int, tables: dict):
+    a.op('SEI'); a.op('CLD'); a.op('LDX', 'imm', 0xFF); a.op('TXS')
+    a.op('LDA', 'imm', 0); a.op('STA', 'abs', 0x2000); a.op('STA', 'abs', 0x2001)
+    for k in range(2):
+        a.label(f'vw{k}'); a.op('BIT', 'abs', 0x2002); a.op('BPL', 'rel', f'vw{k}')
+    a.op('LDA', 'imm', 0); a.op('TAX')
+    a.label('clr')
+    for page in range(8):
+        a.op('STA', 'abx', page * 256)
+    a.op('INX'); a.op('BNE', 'rel', 'clr')
+    # palette
+    a.op('LDA', 'abs', 0x2002)
+    a.op('LDA', 'imm', 0x3F); a.op('STA', 'abs', 0x2006); a.op('LDA', 'imm', 0x00); a.op('STA', 'abs', 0x2006)
+    a.op('LDX', 'imm', 0)
+    a.label('pal'); a.op('LDA', 'abx', tables['pal']); a.op('STA', 'abs', 0x2007); a.op('INX'); a.op('CPX', 'imm', 32)
+    a.op('BNE', 'rel', 'pal')
+    # both nametables: the 256-byte table, offset by the page number
+    a.op('LDA', 'imm', 0x20); a.op('STA', 'abs', 0x2006); a.op('LDA', 'imm', 0x00); a.op('STA', 'abs', 0x2006)
+    a.op('LDY', 'imm', 8); a.op('LDX', 'imm', 0)
+    a.label('ntl'); a.op('TYA'); a.op('CLC'); a.op('ADC', 'abx', tables['nt']); a.op('STA', 'abs', 0x2007); a.op('INX')
+    a.op('BNE', 'rel', 'ntl'); a.op('DEY'); a.op('BNE', 'rel', 'ntl')
+    # OAM buffer
+    a.op('LDX', 'imm', 0)
+    a.label('oam'); a.op('LDA', 'abx', tables['oam']); a.op('STA', 'abx', OAM_PAGE); a.op('INX'); a.op('BNE', 'rel', 'oam')
+    a.op('LDA', 'imm', 0x80); a.op('STA', 'zp', PX); a.op('LDA', 'imm', 0x70); a.op('STA', 'zp', PY)
+    a.op('LDA', 'imm', 0x20); a.op('STA', 'zp', NTP_HI)
+    a.op('LDA', 'imm', ctrl); a.op('STA', 'zp', CTRL_SHADOW); a.op('STA', 'abs', 0x2000)
+    a.op('LDA', 'imm', 0x1E); a.op('STA', 'abs', 0x2001)
+
+
+def _nmi_common(a: Asm):
+    a.op('PHA'); a.op('TXA'); a.op('PHA'); a.op('TYA'); a.op('PHA')
+    a.op('LDA', 'imm', 0); a.op('STA', 'abs', 0x2003); a.op('LDA', 'imm', OAM_PAGE >> 8); a.op('STA', 'abs', 0x4014)
+    a.op('LDA', 'zp', PY); a.op('STA', 'abs', OAM_PAGE + 4); a.op('LDA', 'zp', PX); a.op('STA', 'abs', OAM_PAGE + 7)
+    a.op('LDA', 'abs', 0x2002)
+    a.op('LDA', 'zp', NTP_HI); a.op('STA', 'abs', 0x2006); a.op('LDA', 'zp', NTP_LO); a.op('STA', 'abs', 0x2006)
+    for v in (CNT_LO, CNT_HI, ACNT, PAD):
+        a.op('LDA', 'zp', v); a.op('STA', 'abs', 0x2007)
+    a.op('LDA', 'zp', NTP_LO); a.op('CLC'); a.op('ADC', 'imm', 4); a.op('STA', 'zp', NTP_LO)
+    a.op('LDA', 'zp', NTP_HI); a.op('ADC', 'imm', 0); a.op('AND', 'imm', 0x03); a.op('ORA', 'imm', 0x20)
+    a.op('STA', 'zp', NTP_HI)
+    a.op('LDA', 'zp', PX); a.op('STA', 'abs', 0x2005); a.op('LDA', 'imm', 0); a.op('STA', 'abs', 0x2005)
+    a.op('LDA', 'zp', CTRL_SHADOW); a.op('STA', 'abs', 0x2000)
+    a.op('INC', 'zp', FRAMES); a.op('LDA', 'imm', 1); a.op('STA', 'zp', NMIFLAG)
+
+
+def _nmi_end(a: Asm):
+    a.op('PLA'); a.op('TAY'); a.op('PLA'); a.op('TAX'); a.op('PLA'); a.op('RTI')
+
+
+def _tables(rng):
+    pal = rng.integers(0, 64, 32)
+    nt = rng.integers(0, 256, 256)
+    oam = np.empty(256, np.int64)
+    oam[0::4] = rng.integers(0, 0xF0, 64)
+    oam[1::4] = rng.integers(0, 256, 64)
+    oam[2::4] = rng.integers(0, 256, 64) & 0xE3
+    oam[3::4] = rng.integers(0, 256, 64)
+    mix = rng.integers(0, 256, 256)
+    return pal, nt, oam, mix
+
+
+def nrom_cart(seed: int = 0, blocks: int = 24) -> bytes:
+    """NROM-128 cartridge: 16 KB PRG (code at $C000, mirrored at $8000) + 8 KB random CHR."""
+    rng = np.random.default_rng([0x4E524F4D, seed])
+    pal, nt, oam, mix = _tables(rng)
+    a = Asm(0xC000)
+    tables = dict(pal='t_pal', nt='t_nt', oam='t_oam')
+    a.label('reset')
+    _reset_common(a, 0x90, tables)
+    a.label('main')
+    _read_pad(a, 'm')
+    _pad_moves(a, 't_mix')
+    _filler(a, rng, blocks, 'f', 't_mix')
+    a.op('JMP', 'abs', 'main')
+    a.label('nmi')
+    _nmi_common(a)
+    _nmi_end(a)
+    a.label('irq')
+    a.op('RTI')
+    for name, t in (('t_pal', pal), ('t_nt', nt), ('t_oam', oam), ('t_mix', mix)):
+        a.label(name)
+        a.data(bytes(int(v) for v in t))
+    code = a.assemble()
+    assert len(code) <= 0x3FFA, len(code)
+    prg = bytearray(16384)
+    prg[:len(code)] = code
+    vec = (a.labels['nmi'], a.labels['reset'], a.labels['irq'])
+    prg[0x3FFA:0x4000] = bytes(sum(((v & 0xFF, v >> 8) for v in vec), ()))
+    chr_ = rng.integers(0, 256, 8192, dtype=np.uint8).tobytes()
+    return ines(bytes(prg), chr_, 0, vertical=True)
+
+
+def mmc3_cart(seed: int = 0, blocks: int = 16, sub_blocks: int = 20) -> bytes:
+    """MMC3 cartridge: 256 KB PRG (32 x 8 KB; banks 0-29 hold seeded subroutines at $8000, bank 30 at $C000 and
+    bank 31 at $E000 are fixed), 128 KB random CHR, scanline IRQ split, sprite-0 split, PRG RAM use."""
+    rng = np.random.default_rng([0x4D4D4333, seed])
+    pal, nt, oam, mix = _tables(rng)
+    oam[0:4] = (24, int(rng.integers(256)), 0x00, 40)        # sprite 0 over the playfield near the top
+    banks = []
+    for b in range(30):   # switchable: a subroutine at $8000
+        s = Asm(0x8000)
+        _filler(s, rng, sub_blocks, f's{b}', 0x9F00, with_prg_ram=True)
+        s.op('RTS')
+        body = s.assemble()
+        page = bytearray(8192)
+        page[:len(body)] = body
+        page[0x1F00:0x2000] = rng.integers(0, 256, 256, dtype=np.uint8).tobytes()   # table at $9F00
+        banks.append(bytes(page))
+    # fixed banks: $C000-$DFFF tables + helpers, $E000-$FFFF code and vectors
+    a = Asm(0xC000)
+    for name, t in (('t_pal', pal), ('t_nt', nt), ('t_oam', oam), ('t_mix', mix)):
+        a.label(name)
+        a.data(bytes(int(v) for v in t))
+    a.label('chrsw')          # CHR banks: R0/R1 (background 2 KB) and R2..R5 (sprites) from the counters
+    for reg, var, mask in ((0, CNT_LO, 0x7E), (1, ACNT, 0x7E), (2, FRAMES, 0x7F), (5, BACC, 0x7F)):
+        a.op('LDA', 'imm', reg); a.op('STA', 'abs', 0x8000); a.op('LDA', 'zp', var); a.op('AND', 'imm', mask)
+        a.op('STA', 'abs', 0x8001)
+    a.op('RTS')
+    code_c = a.assemble()
+    assert len(code_c) <= 0x2000
+    a = Asm(0xE000)
+    a.labels.update({k: v for k, v in (('t_pal', 0xC000), ('t_nt', 0xC020), ('t_oam', 0xC120), ('t_mix', 0xC220),
+                                       ('chrsw', 0xC320))})
+    tables = dict(pal='t_pal', nt='t_nt', oam='t_oam')
+    a.label('reset')
+    a.op('LDA', 'imm', 0x40); a.op('STA', 'abs', 0x4017)            # (APU frame IRQ off; ignored here)
+    a.op('LDA', 'imm', 0x80); a.op('STA', 'abs', 0xA001)            # PRG RAM on
+    a.op('LDA', 'imm', 0); a.op('STA', 'abs', 0xA000)                # vertical mirroring
+    _reset_common(a, 0x88, tables)                                   # NMI on, sprites at $1000, BG at $0000
+    a.op('LDA', 'imm', 100); a.op('STA', 'zp', IRQLINE)
+    a.op('CLI')
+    a.label('main')
+    _read_pad(a, 'm')
+    _pad_moves(a, 't_mix')
+    # sprite-0 split once per frame, after the NMI (bounded wait)
+    a.op('LDA', 'zp', NMIFLAG); a.op('BEQ', 'rel', 's0_skip')
+    a.op('LDA', 'imm', 0); a.op('STA', 'zp', NMIFLAG)
+    a.op('LDX', 'imm', 0)
+    a.label('s0_w'); a.op('BIT', 'abs', 0x2002); a.op('BVS', 'rel', 's0_hit'); a.op('DEX'); a.op('BNE', 'rel', 's0_w')
+    a.label('s0_hit')
+    a.op('LDA', 'zp', BACC); a.op('STA', 'abs', 0x2005); a.op('LDA', 'imm', 0); a.op('STA', 'abs', 0x2005)
+    a.label('s0_skip')
+    # switch the $8000 bank (R6) and call the subroutine there
+    a.op('LDA', 'zp', CNT_LO); a.op('EOR', 'zp', PAD); a.op('AND', 'imm', 0x1F); a.op('CMP', 'imm', 30)
+    a.op('BCC', 'rel', 'bk_ok'); a.op('SBC', 'imm', 30)
+    a.label('bk_ok')
+    a.op('STA', 'zp', BANK)
+    a.op('LDA', 'imm', 6); a.op('STA', 'abs', 0x8000); a.op('LDA', 'zp', BANK); a.op('STA', 'abs', 0x8001)
+    a.op('JSR', 'abs', 0x8000)
+    _filler(a, rng, blocks, 'f', 't_mix', with_prg_ram=True)
+    a.op('LDA', 'zp', CNT_LO); a.op('AND', 'imm', 0x07); a.op('BNE', 'rel', 'no_chr'); a.op('JSR', 'abs', 'chrsw')
+    a.label('no_chr')
+    a.op('JMP', 'abs', 'main')
+    a.label('nmi')
+    _nmi_common(a)
+    # next frame's IRQ line: 20 + (frames * 7 + pad) mod 200
+    a.op('LDA', 'zp', FRAMES); a.op('ASL', 'acc'); a.op('ASL', 'acc'); a.op('ASL', 'acc'); a.op('SEC')
+    a.op('SBC', 'zp', FRAMES); a.op('CLC'); a.op('ADC', 'zp', PAD)
+    a.label('irq_mod'); a.op('CMP', 'imm', 200); a.op('BCC', 'rel', 'irq_ok'); a.op('SBC', 'imm', 200)
+    a.op('JMP', 'abs', 'irq_mod')
+    a.label('irq_ok')
+    a.op('CLC'); a.op('ADC', 'imm', 20); a.op('STA', 'zp', IRQLINE)
+    a.op('STA', 'abs', 0xC000); a.op('STA', 'abs', 0xC001); a.op('STA', 'abs', 0xE001)
+    _nmi_end(a)
+    a.label('irq')
+    a.op('PHA')
+    a.op('STA', 'abs', 0xE000)                                        # acknowledge + disable
+    a.op('LDA', 'imm', 0); a.op('STA', 'abs', 0x8000); a.op('LDA', 'zp', FRAMES); a.op('AND', 'imm', 0x7E)
+    a.op('STA', 'abs', 0x8001)                                        # background bank split
+    a.op('LDA', 'zp', PY); a.op('STA', 'abs', 0x2005); a.op('STA', 'abs', 0x2005)
+    a.op('PLA'); a.op('RTI')
+    code_e = a.assemble()
+    assert a.labels['t_mix'] == 0xC220 and len(code_e) <= 0x1FFA, len(code_e)
+    fixed_c = bytearray(8192)
+    fixed_c[:len(code_c)] = code_c
+    fixed_e = bytearray(8192)
+    fixed_e[:len(code_e)] = code_e
+    vec = (a.labels['nmi'], a.labels['reset'], a.labels['irq'])
+    fixed_e[0x1FFA:0x2000] = bytes(sum(((v & 0xFF, v >> 8) for v in vec), ()))
+    prg = b''.join(banks) + bytes(fixed_c) + bytes(fixed_e)
+    chr_ = rng.integers(0, 256, 128 * 1024, dtype=np.uint8).tobytes()
+    return ines(prg, chr_, 4, vertical=True)
+
+
+# ------------------------------------------------------------------------------- SMB RAM trajectories
+
+SMB_ADDRS = (0x0E, 0x6D, 0x86, 0xB5, 0x75A, 0x75C, 0x75F, 0x770, 0x772, 0x7DD, 0x7DE, 0x7DF, 0x7E0, 0x7E1, 0x7E2)
+
+
+def smb_ram15(seed: int, n_envs: int, steps: int) -> np.ndarray:
+    """uint8 [steps, n_envs, 16]: per env-step the SMB reader's 15 RAM bytes (SMB_ADDRS order), byte 15 = 0."""
+    rng = np.random.default_rng([0x534D4252, seed])
+    n = n_envs
+    x = np.full(n, 40, np.int64)
+    world = np.zeros(n, np.int64)
+    level = np.zeros(n, np.int64)
+    lives = np.full(n, 2, np.int64)
+    score = np.zeros(n, np.int64)       # in units of 10 points
+    mode = np.ones(n, np.int64)
+    out = np.zeros((steps, n, 16), np.uint8)
+    for t in range(steps):
+        u = rng.random((n, 6))
+        step = rng.integers(1, 5, n) * np.where(u[:, 0] < 0.8, 1, -1)
+        x = np.clip(x + step, 0, 0x7FFF)
+        back = u[:, 1] < 0.05                      # a one-step excursion back (a rollback when x >= ~760)
+        x_obs = np.where(back, np.maximum(x - rng.integers(760, 1400, n), 0), x)
+        adv = u[:, 2] < 1e-3
+        level = np.where(adv, level + 1, level)
+        world = np.where(adv & (level == 4), np.minimum(world + 1, 7), world)
+        level = np.where(level == 4, 0, level)
+        x = np.where(adv, 40, x)
+        die = u[:, 3] < 5e-4
+        lives = np.where(die, lives - 1, lives)
+        mode = np.where(lives < 0, 3, mode)
+        mode = np.where(adv & (world == 7) & (level == 3), 2, mode)
+        score = np.where(u[:, 4] < 0.1, score + rng.integers(1, 20, n), score) % 1000000
+        pit = u[:, 5] < 1e-4
+        routine = np.where(die, 6, 8)
+        b5 = np.where(pit, 2, 1)
+        digits = [(score // 10 ** (5 - k)) % 10 for k in range(6)]
+        cols = [routine, (x_obs >> 8) & 0xFF, x_obs & 0xFF, b5, lives & 0xFF, level, world, mode,
+                np.full(n, 3)] + digits
+        out[t, :, :15] = np.stack(cols, axis=1).astype(np.uint8)
+    return out
+
+
+def expand_ram(ram15: np.ndarray) -> np.ndarray:
+    """[..., 16] packed bytes -> [..., 2048] RAM images with the 15 bytes at their addresses, zeros elsewhere."""
+    full = np.zeros(ram15.shape[:-1] + (2048,), np.uint8)
+    for i, a in enumerate(SMB_ADDRS):
+        full[..., a] = ram15[..., i]
+    return full

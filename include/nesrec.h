@@ -1,0 +1,121 @@
+/* Console record: the complete state of one emulated NES console, as one contiguous block.
+ *
+ * Both the CPU oracle (oracle/) and the HIP library keep every console in this layout, so a
+ * whole console can be compared byte for byte between the two builds, restored from a boot
+ * snapshot with one copy, and saved/loaded for an exact resume.
+ *
+ * The reference keeps the same information as ~40 separate per-env arrays (rl/csrc/nes_machine.cuh:37-64,
+ * `bind_arrays`); the fields below cover the ones on the NROM/MMC1/MMC3 path.
+ *
+ * Layout rules: little-endian, no implicit padding (checked below), every memory block 256-byte aligned.
+ * Plain C so that gcc (oracle) and hipcc (device + host) read it identically.
+ */
+#ifndef NESREC_H
+#define NESREC_H
+#include <stddef.h>
+#include <stdint.h>
+
+#define NES_RAM_BYTES 2048u
+#define NES_NT_BYTES 2048u
+#define NES_OAM_BYTES 256u
+#define NES_PAL_BYTES 32u
+#define NES_PRGRAM_BYTES 8192u
+#define NES_CHRRAM_BYTES 8192u
+#define NES_LOG_HDR_WORDS 16u
+#define NES_LOG_EVENTS 256u
+#define NES_LOG_WORDS (NES_LOG_HDR_WORDS + 2u * NES_LOG_EVENTS)
+
+/* Frame timing (PPU dots). A frame is 262 lines of 341 dots; a decision frame ends at the vblank dot. */
+#define NES_DOTS_PER_LINE 341u
+#define NES_FRAME_DOTS (341u * 262u)          /* 89342 (rl/csrc/nes_machine.cuh:28) */
+#define NES_VBLANK_DOT (241u * 341u + 1u)     /* 82182 (rl/csrc/nes_machine.cuh:29) */
+#define NES_PRERENDER_DOT (261u * 341u + 1u)  /* 89002: flags cleared, frame log header captured */
+#define NES_BUDGET 200000u                    /* instructions per frame (rl/csrc/nes_machine.cuh:30) */
+#define NES_NO_HIT 0x7FFFFFFF
+
+/* Boards. */
+#define NES_BOARD_NROM 0u
+#define NES_BOARD_MMC1 1u
+#define NES_BOARD_MMC3 4u
+
+/* Frame-log event kinds (word 0 bits 24..31). Word 0 bits 0..23: event time + NES_LOG_TIME_BIAS, where the
+ * event time is in dots from the start of line 0 of the logged frame (pre-render line: negative).
+ * Word 1: value | aux << 8. */
+#define NES_LOG_TIME_BIAS 1024
+#define NES_EV_CTRL 1u    /* $2000 */
+#define NES_EV_MASK 2u    /* $2001 */
+#define NES_EV_SCROLL 3u  /* $2005, aux = write toggle before the write */
+#define NES_EV_ADDR 4u    /* $2006, aux = write toggle before the write */
+#define NES_EV_DATA 5u    /* $2007 access below the palette: address increments, aux = count */
+#define NES_EV_PAL 6u     /* $2007 palette write: value, aux = palette index (after mirroring) */
+#define NES_EV_CHR 7u     /* CHR 1 KB page change: value = page, aux = slot 0..7 */
+#define NES_EV_MIRROR 8u  /* nametable map change: value = nt_map packed 4 x 2 bits */
+
+/* Log header words: 0 count | overflow << 31, 1 ctrl | mask << 8 | fine x << 16, 2 v | t << 16,
+ * 3-4 CHR 1 KB page of each slot (8 bits each), 5 nt_map packed, 6-13 palette RAM, 14-15 zero. */
+#define NES_LOG_OVERFLOW 0x80000000u
+
+typedef struct NesRec {
+    /* ---- CPU, controller (0x00) ---- */
+    uint16_t pc;
+    uint8_t a, x, y, sp, p;
+    uint8_t irq_line;     /* cartridge IRQ line (MMC3) */
+    uint64_t cycles;      /* CPU cycles since power-on */
+    uint8_t nmi_pending;
+    uint8_t pad;          /* pad byte of the current frame (bit0 A .. bit7 Right) */
+    uint8_t shift;        /* controller 1 shift register */
+    uint8_t strobe;
+    uint32_t instr_lo;    /* emulated instructions since power-on (low 32 bits) */
+    /* ---- PPU (0x18) ---- */
+    uint32_t frame_dot;   /* 0..89341, 0 = line 0 dot 0 */
+    uint32_t frame;
+    uint16_t v, t;
+    uint8_t ctrl, mask, status, oam_addr;
+    uint8_t fx, w, read_buf, open_bus;
+    int32_t s0_dot;       /* frame dot of this frame's sprite-0 hit, NES_NO_HIT = none */
+    uint32_t log_frame;   /* frame whose lines the log describes */
+    uint16_t log_n;
+    uint8_t s0_valid;     /* 1: s0_dot is computed for the events logged so far */
+    uint8_t board;
+    uint64_t _ppu_res;
+    /* ---- DMC (0x40) ---- */
+    uint64_t dmc_byte_end;
+    uint64_t dmc_event;
+    uint16_t dmc_left;
+    uint8_t dmc_control, dmc_length, dmc_rate, dmc_full, _dmc0, _dmc1;
+    /* ---- mapper (0x58) ---- */
+    uint8_t mreg[16];
+    uint32_t prg_off[4];  /* byte offset in PRG of the 8 KB page at $8000/$A000/$C000/$E000 */
+    uint32_t chr_off[8];  /* byte offset in CHR of each 1 KB slot of $0000-$1FFF */
+    uint8_t nt_map[4];    /* physical 1 KB nametable (0/1) of each logical nametable */
+    uint32_t _res[25];    /* pad to 0x100 */
+    /* ---- memories ---- */
+    uint8_t ram[NES_RAM_BYTES];         /* 0x100 */
+    uint8_t nt[NES_NT_BYTES];           /* 0x900 */
+    uint8_t oam[NES_OAM_BYTES];         /* 0x1100 */
+    uint8_t pal[256];                   /* 0x1200: 32 used */
+    uint32_t log[NES_LOG_WORDS + 48];   /* 0x1300: header + events, padded to 256 B */
+    uint8_t prg_ram[NES_PRGRAM_BYTES];  /* 0x1C00 */
+    uint8_t chr_ram[NES_CHRRAM_BYTES];  /* 0x3C00 */
+} NesRec;                               /* 0x5C00 = 23552 bytes */
+
+#define NES_REC_BYTES 23552u
+
+#ifdef __cplusplus
+#define NESREC_ASSERT static_assert
+#else
+#define NESREC_ASSERT _Static_assert
+#endif
+NESREC_ASSERT(offsetof(NesRec, frame_dot) == 0x18, "layout");
+NESREC_ASSERT(offsetof(NesRec, dmc_byte_end) == 0x40, "layout");
+NESREC_ASSERT(offsetof(NesRec, mreg) == 0x58, "layout");
+NESREC_ASSERT(offsetof(NesRec, ram) == 0x100, "layout");
+NESREC_ASSERT(offsetof(NesRec, nt) == 0x900, "layout");
+NESREC_ASSERT(offsetof(NesRec, oam) == 0x1100, "layout");
+NESREC_ASSERT(offsetof(NesRec, pal) == 0x1200, "layout");
+NESREC_ASSERT(offsetof(NesRec, log) == 0x1300, "layout");
+NESREC_ASSERT(offsetof(NesRec, prg_ram) == 0x1C00, "layout");
+NESREC_ASSERT(offsetof(NesRec, chr_ram) == 0x3C00, "layout");
+NESREC_ASSERT(sizeof(NesRec) == NES_REC_BYTES, "layout");
+
+#endif

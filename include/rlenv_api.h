@@ -1,0 +1,86 @@
+/* C ABI of the batched NES environment step (HIP build: ghostrun-lab_amd/csrc -> librlenv_hip.so).
+ *
+ * A drop-in for the reference's rl/csrc/rlenv_api.h:8-47 and the GPU extras of rl/csrc/rlenv.cu:186-427: the
+ * same names, argument meanings and error behaviour, so rl/rlenv.py's ctypes loader (rl/rlenv.py:76-121) binds
+ * it unchanged. All buffers are device pointers; `stream` is a hipStream_t passed as void* (torch's current
+ * stream). Plain C types only. The CPU oracle (oracle/) exports the same entry points for tests, with host
+ * pointers, ignoring `stream`.
+ *
+ * Errors: int 0 = ok, non-zero = error with the message in rlenv_error(); rlenv_create returns NULL on error.
+ * Emulator faults are data (episode end 5), not errors.
+ */
+#ifndef RLENV_API_H
+#define RLENV_API_H
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Builds every game's boot snapshot (power-on, RAM 0xFF, the boot pad bytes frame by frame) and idle
+ * templates, and allocates n+1 console records per game (slot n = boot snapshot).
+ * Replaces rl/csrc/rlenv_api.h:10-12 (rlenv.cu:188-217). game_ids: reward10 game ids (0 = smb; the only
+ * reward reader built). roms: iNES images (mappers 0, 1, 4). device: HIP device index. */
+void* rlenv_create(int ngames, const int* game_ids, const uint8_t* const* roms, const size_t* rom_sizes,
+                   const uint8_t* const* boot_pads, const size_t* boot_sizes, const int* n_envs, uint64_t run_seed,
+                   int sticky, int idle_max, int dropout, int device);
+int rlenv_num_envs(void* h);                                   /* rlenv_api.h:13 */
+void rlenv_set_episode_level_end(void* h, int level);          /* rlenv_api.h:15 */
+/* rlenv_api.h:16-18: actions int16 [N], obs u8 [N,4,224,240], emph u8 [N,4,224], reward f32 [N], done u8 [N],
+ * masks u8 [N,19], timeline u8 [N,8,45], pads u8 [N,4], events u32 [N], info f32 [N,8]. */
+void rlenv_bind(void* h, const int16_t* actions, uint8_t* obs, uint8_t* emph, float* reward, uint8_t* done,
+                uint8_t* masks, uint8_t* timeline, uint8_t* pads, uint32_t* events, float* info);
+void rlenv_bind_parts(void* h, float* parts);                  /* rlenv_api.h:20: [N,7] */
+void rlenv_bind_obs(void* h, uint8_t* obs, uint8_t* emph);     /* rlenv_api.h:22 */
+int rlenv_start(void* h, void* stream);                        /* rlenv_api.h:40 */
+int rlenv_step(void* h, void* stream);                         /* rlenv_api.h:41 */
+size_t rlenv_state_bytes(void* h);                             /* rlenv_api.h:42 */
+int rlenv_save(void* h, uint8_t* host_out, void* stream);      /* rlenv_api.h:43 (synchronous) */
+int rlenv_load(void* h, const uint8_t* host_in, void* stream); /* rlenv_api.h:44 (synchronous) */
+const char* rlenv_error(void);                                 /* rlenv_api.h:45 (thread-local) */
+void rlenv_destroy(void* h);                                   /* rlenv_api.h:46 */
+
+/* GPU extras of rl/csrc/rlenv.cu. */
+int rlenv_num_games(void* h);                                                      /* rlenv.cu:249 */
+int rlenv_step_game(void* h, int gi, uint8_t* obs, uint8_t* emph, void* stream);    /* rlenv.cu:250-256 */
+int rlenv_step_range(void* h, int gi, int start, int count, uint8_t* obs, uint8_t* emph,
+                     void* stream);                                                /* rlenv.cu:258-268 */
+void rlenv_set_no_render(void* h, int v);                                          /* rlenv.cu:364-366 */
+void* rl_host_alloc(size_t bytes);                                                 /* rlenv.cu:371-378 */
+void rl_host_free(void* p);                                                        /* rlenv.cu:379 */
+int rl_pack6(const void* src, void* dst, size_t pixels, void* stream);             /* rlenv.cu:380-386 */
+int rl_unpack6(const void* src, void* dst, size_t pixels, void* stream);           /* rlenv.cu:387-393 */
+int rl_memcpy_async(void* dst, const void* src, size_t bytes, void* stream);       /* rlenv.cu:394-398 */
+int rl_gather_rows(void* dst, const void* src, const int64_t* rows, int nrows, size_t row_bytes,
+                   void* stream);                                                  /* rlenv.cu:400-409 */
+int rl_gather_envs(void* dst, const void* src, const int64_t* envs, int n, int T, int N, size_t row_bytes,
+                   void* stream);                                                  /* rlenv.cu:411-421 */
+
+/* Additions of this build for the benchmark workloads (no reference counterpart):
+ *  pad mode 1: actions hold raw pad bytes (0..255) instead of move ids; sticky repeats the previous frame's
+ *    byte; a dropped input clears its button bit.
+ *  end_p32: per decision, an episode also ends with probability end_p32 / 2^32 (end reason 7), drawn from
+ *    the env's own counter stream (seed of the episode, decision index).
+ *  gap_p32: P(a healthy dropout gap ends) per decision, default floor(2^32/35) as the reference's kGapP32.
+ *  ram hash: u64 [N], per decision the hash of the console's 2 KB RAM after its 4 frames.
+ *  read_consoles: console records (include/nesrec.h) of game gi, envs [first, first+count), to host memory
+ *    (synchronous). */
+void rlenv_set_pad_mode(void* h, int raw);
+void rlenv_set_end_prob(void* h, uint32_t end_p32);
+void rlenv_set_dropout_gap(void* h, uint32_t gap_p32);
+void rlenv_bind_ram_hash(void* h, uint64_t* ram_hash);
+int rlenv_read_consoles(void* h, int gi, int first, int count, uint8_t* host_out, void* stream);
+
+/* The reward10 SMB tracker on its own (benchmark config "reward10 standalone"): T steps of N envs.
+ * ram15: u8 [T, N, 16], per env-step the 15 RAM bytes the SMB reader reads, in the order
+ *   0x0E, 0x6D, 0x86, 0xB5, 0x75A, 0x75C, 0x75F, 0x770, 0x772, 0x7DD..0x7E2 (byte 15 unused);
+ * state: Rl10State [N] (include/rlenv_state.h), updated in place; reward f32 [T, N]; done u8 [T, N].
+ * frames = emulated frames per step. Follows rl/csrc/host_api.cpp:13-31 (rl10_replay) for game smb. */
+int rl10_smb_run(const uint8_t* ram15, int T, int N, int frames, void* state, float* reward, uint8_t* done,
+                 void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,122 @@
+"""Writes the golden fixtures in this directory from the reference's own host library.
+
+The reference's rl/csrc/host_api.cpp (reward10 + controller, compiled from its sources by oracle/Makefile.ref into
+oracle/_ref/librl_host.so) is the only part of the reference env that builds here. Its outputs on fixed inputs are
+stored as small .npz files; the tests check the oracle (and through it the HIP library) against them.
+
+    make -f oracle/Makefile.ref && python tests/golden/gen_golden.py
+
+Inputs: move ids and dropout inputs (exhaustive), a few schedule seeds, random (run_seed, env, episode) triples,
+the reference test's nine SMB rollback cases (rl/tests/test_reward_replay.py:122-143) and seeded SMB-style RAM
+trajectories (rl.synth.smb_ram15). Outputs are exactly what the reference functions return.
+"""
+from __future__ import annotations
+
+import ctypes
+import sys
+from pathlib import Path
+
+import numpy as np
+
+HERE = Path(__file__).resolve().parent
+ROOT = HERE.parents[1]
+sys.path.insert(0, str(ROOT / 'ghostrun-lab_amd'))
+from rl import synth  # noqa: E402
+
+REF_LIB = ROOT / 'oracle' / '_ref' / 'librl_host.so'
+
+
+def p(a):
+    return a.ctypes.data_as(ctypes.c_void_p)
+
+
+def load():
+    lib = ctypes.CDLL(str(REF_LIB))
+    P, I, U64, U32 = ctypes.c_void_p, ctypes.c_int, ctypes.c_uint64, ctypes.c_uint32
+    lib.rl10_replay.argtypes = [I, P, I, P, P, P, P, P, P, P]
+    lib.rlc_pad_table.argtypes = [P]
+    lib.rlc_legal_table.argtypes = [I, I, P, P]
+    lib.rlc_schedule.argtypes = [U64, I, I, P, P]
+    lib.rlc_episode_seed.argtypes = [U64, U32, U64]
+    lib.rlc_episode_seed.restype = U64
+    return lib
+
+
+def replay(lib, rams, frames):
+    n = len(rams)
+    rams = np.ascontiguousarray(rams, np.uint8)
+    frames = np.ascontiguousarray(frames, np.int32)
+    out = dict(reward=np.zeros(n, np.float64), done=np.zeros(n, np.uint8), events=np.zeros(n, np.uint32),
+               level=np.zeros(n, np.int32), deaths=np.zeros(n, np.int32), end=np.zeros(n, np.uint8))
+    ov = lib.rl10_replay(0, p(rams), n, p(frames), p(out['reward']), p(out['done']), p(out['events']),
+                         p(out['level']), p(out['deaths']), p(out['end']))
+    assert ov == 0
+    return out
+
+
+def rollback_rams():
+    """The nine two-snapshot cases of rl/tests/test_reward_replay.py:122-143 (SMB RAM bytes)."""
+    def ram(x, routine=8, level=15, mode=1):
+        r = np.zeros(2048, np.uint8)
+        r[0x770], r[0x772], r[0x0E], r[0x75A] = mode, 3, routine, 2
+        r[0x75F], r[0x75C] = level // 4, level % 4
+        r[0x6D], r[0x86] = (x // 256) % 256, x % 256
+        return r
+    cases = [([ram(750), ram(0)], True), ([ram(749), ram(0)], False), ([ram(1013), ram(-8)], True),
+             ([ram(1013), ram(0, routine=6)], False), ([ram(1013), ram(0, routine=7)], False),
+             ([ram(1013, routine=7), ram(0)], False), ([ram(1013), ram(0, level=16)], False),
+             ([ram(1013), ram(0, mode=0)], False), ([ram(1013, level=31), ram(0, level=31, mode=2)], False)]
+    return np.stack([np.stack(c) for c, _ in cases]), np.array([r for _, r in cases])
+
+
+def main():
+    lib = load()
+    pad = np.zeros(324 * 2, np.uint8)
+    lib.rlc_pad_table(p(pad))
+    legal = {}
+    for so, se in ((0, 0), (1, 0), (1, 1)):
+        out = np.zeros(9 * 324, np.uint8)
+        rest = np.zeros(9 * 324, np.int32)
+        lib.rlc_legal_table(so, se, p(out), p(rest))
+        legal[f'out_{so}{se}'] = out
+        legal[f'rest_{so}{se}'] = rest
+    np.savez_compressed(HERE / 'controller.npz', pad_table=pad, **legal)
+
+    seeds = np.array([1, 2, 12345, 2 ** 63 + 7, 0xDEADBEEFCAFEF00D], np.uint64)
+    n_long, n_tl = 600, 64
+    dropped = np.zeros((len(seeds), n_long), np.int8)
+    tls = np.zeros((len(seeds), n_tl, 8 * 45), np.uint8)
+    for i, s in enumerate(seeds):
+        lib.rlc_schedule(int(s), 1, n_long, p(dropped[i]), None)
+        d2 = np.zeros(n_tl, np.int8)
+        lib.rlc_schedule(int(s), 1, n_tl, p(d2), p(tls[i]))
+        assert (d2 == dropped[i, :n_tl]).all()
+    off = np.zeros(50, np.int8)
+    lib.rlc_schedule(99, 0, 50, p(off), None)
+    rng = np.random.default_rng(5)
+    triples = np.stack([rng.integers(0, 2 ** 63, 64, dtype=np.uint64),
+                        rng.integers(0, 2 ** 20, 64).astype(np.uint64),
+                        rng.integers(0, 2 ** 32, 64).astype(np.uint64)], 1)
+    ep = np.array([lib.rlc_episode_seed(int(a), int(b), int(c)) for a, b, c in triples], np.uint64)
+    np.savez_compressed(HERE / 'dropout.npz', seeds=seeds, dropped=dropped, timelines=tls, disabled=off,
+                        triples=triples, episode_seed=ep)
+
+    rb_rams, rb_flags = rollback_rams()
+    rb = [replay(lib, c, np.full(2, 4, np.int32)) for c in rb_rams]
+    traj = synth.smb_ram15(7, 16, 1024)             # [T, N, 16]
+    frames = np.full(1024, 4, np.int32)
+    frames[0] = 8                                   # the env's first update covers idle + 4 frames
+    res = [replay(lib, synth.expand_ram(traj[:, e]), frames) for e in range(traj.shape[1])]
+    stack = lambda k: np.stack([r[k] for r in res], 1)  # noqa: E731  [T, N]
+    np.savez_compressed(HERE / 'reward10_smb.npz',
+                        rollback_rams=rb_rams, rollback_flags=rb_flags,
+                        rollback_reward=np.stack([r['reward'] for r in rb]),
+                        rollback_events=np.stack([r['events'] for r in rb]),
+                        rollback_done=np.stack([r['done'] for r in rb]),
+                        traj=traj, frames=frames, reward=stack('reward'), done=stack('done'),
+                        events=stack('events'), level=stack('level'), deaths=stack('deaths'), end=stack('end'))
+    print('fixtures written:', sorted(x.name for x in HERE.glob('*.npz')))
+
+
+if __name__ == '__main__':
+    main()
