@@ -1,0 +1,1002 @@
+// HIP build of the batched NES environment step for MI355X (gfx950), behind the C ABI of include/rlenv_api.h.
+//
+// One decision of one game is this launch sequence on the caller's stream (the reference's phase order,
+// rl/csrc/rlenv_core.cuh:389-414 and rl/csrc/rlenv.cu:145-170):
+//   4 x (k_emu: one emulated frame of every console, k_render: its picture into obs slot f)
+//   k_finish: reward10 update, outputs, dropout advance; finished episodes reset their RL state and join the
+//             restart list (wave ballot + one atomic per wave)
+//   k_reset_copy: boot snapshot (or idle template) -> console record, one workgroup per listed console
+//   4 x (k_emu, k_render) over the restart list only (neutral frames of the new episode)
+//   k_reset_finish: first tracker update of new episodes; masks and dropout timeline of every env
+//
+// k_emu runs one console per lane with `cpw` consoles per wavefront (a launch parameter: with 8192 consoles the
+// machine has 1024 SIMDs, so fewer consoles per wave buys latency hiding and less divergence); the consoles' RAM
+// lives in LDS for the launch, copied in and out with coalesced whole-workgroup copies.
+// k_render draws one console-frame per wavefront: the line replay is wave-uniform, each lane composes 4 pixels,
+// sprites are selected with one ballot per line, and each output row is one coalesced 240-byte store.
+#include <hip/hip_runtime.h>
+
+#include <cstdio>
+#include <cstdlib>
+#include <ctime>
+#include <cstring>
+#include <stdexcept>
+#include <string>
+#include <vector>
+
+#include "env_dev.h"
+#include "nes_dev.h"
+#include "optab.h"
+#include "rlenv_api.h"
+#include "rlenv_state.h"
+
+using namespace nd;
+
+namespace {
+
+thread_local std::string g_error;
+
+// ============================================================================================ kernels
+struct EnvArrays {
+    Rl10State* st;
+    Dropout* drop;
+    uint64_t *target, *sticky_seed, *sticky_ctr;
+    uint32_t *ep_frame, *episode, *fault;
+    int16_t* prev_applied;
+    float* ep_ret;
+    int32_t *ep_len, *ep_maxlvl, *ep_idle;
+    uint8_t* resetting;
+};
+
+struct Outs {
+    const int16_t* actions;
+    uint8_t *obs, *emph, *done, *masks, *tl, *pads;
+    float *reward, *info, *parts;
+    uint32_t* events;
+    uint64_t* ram_hash;
+};
+
+struct Settings {
+    uint64_t run_seed;
+    int sticky, idle_max, idle_tmpl, dropout, no_render, episode_level_end, pad_mode;
+    uint32_t end_p32, gap_p32;
+};
+
+struct GameK {
+    NesRec* recs;          // n + 1 records, slot n = boot snapshot
+    const NesRec* idle;    // idle templates
+    Cart cart;
+    int n, offset, start_ok, select_ok;
+    uint64_t tmpl_target;
+    int32_t* list;         // restart list (env index within the game)
+    uint32_t* list_count;
+};
+
+enum : int { EMU_DECISION = 0, EMU_RESTART = 1, EMU_BOOT = 2 };
+
+struct EmuArgs {
+    GameK g;
+    EnvArrays e;
+    Outs o;
+    Settings s;
+    const uint32_t* optab;
+    int mode, f, cpw, use_list, e0, e1;
+    uint32_t boot_pad;
+    uint64_t boot_target;
+    uint32_t* boot_fault;
+    uint32_t budget;       // instructions per frame (NES_BUDGET; smaller only for diagnostics)
+};
+
+__device__ __forceinline__ int slot_count(const GameK& g, int use_list, int e0, int e1) {
+    return use_list ? (int)*g.list_count : e1 - e0;
+}
+__device__ __forceinline__ int slot_env(const GameK& g, int use_list, int e0, int k) {
+    return use_list ? g.list[k] : e0 + k;
+}
+
+// Per-frame pad byte of a decision frame (rl/csrc/rlenv_core.cuh:181-191): sticky repeat, dropout, turbo phase.
+__device__ uint32_t decision_pad(const EmuArgs& a, int ge, int f) {
+    const int d = ev::dropped_now(&a.e.drop[ge]);
+    uint64_t ctr = a.e.sticky_ctr[ge];
+    const uint64_t seed = a.e.sticky_seed[ge];
+    uint32_t pad;
+    if (a.s.pad_mode) {
+        uint32_t p = (uint16_t)a.o.actions[ge] & 0xFFu;
+        if (a.s.sticky && ev::rnd32(seed, ctr) < RLC_STICKY_P32) p = (uint16_t)a.e.prev_applied[ge] & 0xFFu;
+        pad = ev::restrict_pad(p, d);
+        a.e.prev_applied[ge] = (int16_t)pad;
+    } else {
+        ev::Move mv = ev::unpack((uint32_t)(int32_t)a.o.actions[ge]);
+        if (a.s.sticky && ev::rnd32(seed, ctr) < RLC_STICKY_P32)
+            mv = ev::restrict_move(ev::unpack((uint32_t)(int32_t)a.e.prev_applied[ge]), d, a.g.start_ok != 0,
+                                   a.g.select_ok != 0);
+        a.e.prev_applied[ge] = (int16_t)ev::pack(mv);
+        pad = ev::pad_of(mv, a.e.ep_frame[ge]);
+    }
+    a.e.sticky_ctr[ge] = ctr;
+    a.o.pads[(size_t)ge * RLE_FRAMES + f] = (uint8_t)pad;
+    return pad;
+}
+
+__global__ __launch_bounds__(64) void k_emu(EmuArgs a) {
+    extern __shared__ __align__(16) uint8_t smem[];
+    const int count = a.mode == EMU_BOOT ? 1 : slot_count(a.g, a.use_list, a.e0, a.e1);
+    const int first = (int)blockIdx.x * a.cpw;
+    if (first >= count) return;
+    const int lane = (int)threadIdx.x;
+    uint32_t* optab = reinterpret_cast<uint32_t*>(smem);
+    uint8_t* rams = smem + 1024;
+    for (int i = lane; i < 256; i += 64) optab[i] = a.optab[i];
+    const int nslot = min(a.cpw, count - first);
+    for (int j = 0; j < nslot; ++j) {
+        const int e = a.mode == EMU_BOOT ? a.e0 : slot_env(a.g, a.use_list, a.e0, first + j);
+        const uint32_t* src = reinterpret_cast<const uint32_t*>(a.g.recs[e].ram);
+        uint32_t* dst = reinterpret_cast<uint32_t*>(rams + j * kRamStride);
+        for (int w = lane; w < 512; w += 64) dst[w] = src[w];
+    }
+    __syncthreads();
+    if (lane < nslot) {
+        const int e = a.mode == EMU_BOOT ? a.e0 : slot_env(a.g, a.use_list, a.e0, first + lane);
+        NesRec* rec = &a.g.recs[e];
+        const Mem m{rec, rams + lane * kRamStride, a.g.cart};
+        const int ge = a.g.offset + e;
+        uint32_t pad = 0, fault = 0;
+        uint64_t target;
+        bool run = true;
+        if (a.mode == EMU_BOOT) {
+            pad = a.boot_pad;
+            target = a.boot_target;
+        } else {
+            if (a.mode == EMU_RESTART && a.e.resetting[ge] == 0) run = false;
+            if (a.mode == EMU_DECISION) pad = decision_pad(a, ge, a.f);
+            target = a.e.target[ge];
+            fault = a.e.fault[ge];
+        }
+        if (run) {
+            Con c;
+            con_load(c, rec);
+            c.pad = pad;
+            if (fault == 0) {
+                const uint32_t f = run_until(c, m, optab, target, a.budget);
+                if (f != 0) {
+                    if (a.mode == EMU_BOOT) atomicOr(a.boot_fault, 1u);
+                    else a.e.fault[ge] = f;
+                }
+            }
+            con_store(c, rec);
+            if (a.mode != EMU_BOOT) {
+                a.e.target[ge] = target + NES_FRAME_DOTS;
+                a.e.ep_frame[ge] += 1u;
+            }
+        }
+    }
+    __syncthreads();
+    for (int j = 0; j < nslot; ++j) {
+        const int e = a.mode == EMU_BOOT ? a.e0 : slot_env(a.g, a.use_list, a.e0, first + j);
+        uint32_t* dst = reinterpret_cast<uint32_t*>(a.g.recs[e].ram);
+        const uint32_t* src = reinterpret_cast<const uint32_t*>(rams + j * kRamStride);
+        for (int w = lane; w < 512; w += 64) dst[w] = src[w];
+    }
+}
+
+// Power-on of one console record.
+__global__ void k_power_on(NesRec* rec, Cart cart) {
+    if (threadIdx.x == 0 && blockIdx.x == 0) power_on(rec, cart);
+}
+
+// ----------------------------------------------------------------------------------------- render
+struct RenderArgs {
+    GameK g;
+    EnvArrays e;
+    Outs o;
+    Settings s;
+    int f, use_list, restart_pass, e0, e1;
+};
+
+// One console-frame per wavefront (blockDim 64): replay the frame log line by line (wave-uniform), each lane
+// composes 4 pixels of the 256-pixel line; rows 8..231, columns 8..247 go out as one 240-byte store per line.
+__global__ __launch_bounds__(64) void k_render(RenderArgs a) {
+    __shared__ __align__(16) uint8_t nt_s[2048];
+    __shared__ __align__(16) uint8_t oam_s[256];
+    __shared__ __align__(16) uint8_t pal_s[32];
+    const int count = slot_count(a.g, a.use_list, a.e0, a.e1);
+    const int k = (int)blockIdx.x;
+    if (k >= count) return;
+    const int e = slot_env(a.g, a.use_list, a.e0, k);
+    const int ge = a.g.offset + e;
+    if (a.restart_pass && a.e.resetting[ge] == 0) return;
+    if (a.s.no_render) return;
+    const int lane = (int)threadIdx.x;
+    const NesRec* rec = &a.g.recs[e];
+    for (int w = lane; w < 512; w += 64) reinterpret_cast<uint32_t*>(nt_s)[w] = reinterpret_cast<const uint32_t*>(rec->nt)[w];
+    reinterpret_cast<uint32_t*>(oam_s)[lane] = reinterpret_cast<const uint32_t*>(rec->oam)[lane];
+    Replay s;
+    rp_begin(s, rec->log, rec->log_n, pal_s);
+    __syncthreads();
+    const Mem m{const_cast<NesRec*>(rec), nullptr, a.g.cart};
+    uint8_t* obs = a.o.obs + ((size_t)ge * RLE_FRAMES + a.f) * RLE_OBS_PIXELS;
+    uint8_t* emph = a.o.emph + ((size_t)ge * RLE_FRAMES + a.f) * RLE_OBS_H;
+    const uint32_t my_sy = oam_s[4 * lane];
+    for (int l = 0; l < 232; ++l) {
+        if (l >= 8) {
+            const uint32_t mask = s.mask, ctrl = s.ctrl;
+            const bool bg_on = (mask & 0x08u) != 0, sp_on = (mask & 0x10u) != 0;
+            const int h = (ctrl & 0x20u) ? 16 : 8;
+            const int row_me = l - (int)my_sy - 1;
+            uint64_t sel = __ballot(sp_on && row_me >= 0 && row_me < h);
+            // background, 4 pixels
+            uint32_t bgv[4], bga[4];
+            const uint32_t x0 = 4u * (uint32_t)lane;
+            const uint32_t cy = (s.v >> 5) & 31u, fy = (s.v >> 12) & 7u, ntv = (s.v >> 11) & 1u;
+            uint32_t cached_slot = 0xFFFFFFFFu, lo = 0, hi = 0, pal_sel = 0;
+            for (int q = 0; q < 4; ++q) {
+                const uint32_t x = x0 + (uint32_t)q;
+                bgv[q] = 0;
+                bga[q] = 0;
+                if (!bg_on || (x < 8u && !(mask & 0x02u))) continue;
+                const uint32_t pos = x + s.fx, slot = pos >> 3;
+                if (slot != cached_slot) {
+                    cached_slot = slot;
+                    uint32_t cx = (s.v & 31u) + slot, nth = (s.v >> 10) & 1u;
+                    if (cx >= 32u) {
+                        cx -= 32u;
+                        nth ^= 1u;
+                    }
+                    const uint32_t base = 0x2000u | ((nth | (ntv << 1)) << 10);
+                    const uint32_t tile = nt_s[nt_index(s.nt_map, base | (cy << 5) | cx)];
+                    const uint32_t at = nt_s[nt_index(s.nt_map, base | 0x3C0u | ((cy >> 2) << 3) | (cx >> 2))];
+                    pal_sel = (at >> (((cy & 2u) << 1) | (cx & 2u))) & 3u;
+                    const uint32_t pa = ((ctrl & 0x10u) << 8) + tile * 16u + fy;
+                    lo = chr_byte_pk(m, s.chr_lo, s.chr_hi, pa);
+                    hi = chr_byte_pk(m, s.chr_lo, s.chr_hi, pa + 8u);
+                }
+                const uint32_t b = 7u - (pos & 7u);
+                bgv[q] = ((lo >> b) & 1u) | (((hi >> b) & 1u) << 1);
+                bga[q] = pal_sel;
+            }
+            // sprites: the first 8 in OAM order that cover this line
+            uint32_t spv[4] = {0, 0, 0, 0}, spa[4] = {0, 0, 0, 0}, spb[4] = {0, 0, 0, 0};
+            for (int n = 0; n < 8 && sel != 0; ++n) {
+                const uint32_t i = (uint32_t)__builtin_ctzll(sel);
+                sel &= sel - 1;
+                const uint32_t sy = oam_s[4 * i], tile = oam_s[4 * i + 1], attr = oam_s[4 * i + 2], sx = oam_s[4 * i + 3];
+                const uint32_t pa = sprite_row_addr(ctrl, tile, attr, (uint32_t)(l - (int)sy - 1));
+                const uint32_t plo = chr_byte_pk(m, s.chr_lo, s.chr_hi, pa), phi = chr_byte_pk(m, s.chr_lo, s.chr_hi, pa + 8u);
+                for (int q = 0; q < 4; ++q) {
+                    const uint32_t x = x0 + (uint32_t)q, col = x - sx;
+                    if (spv[q] || col >= 8u || (x < 8u && !(mask & 0x04u))) continue;
+                    const uint32_t b = (attr & 0x40u) ? col : 7u - col;
+                    const uint32_t p = ((plo >> b) & 1u) | (((phi >> b) & 1u) << 1);
+                    if (p) {
+                        spv[q] = p;
+                        spa[q] = attr & 3u;
+                        spb[q] = (attr >> 5) & 1u;
+                    }
+                }
+            }
+            uint32_t word = 0;
+            for (int q = 0; q < 4; ++q) {
+                uint32_t colour;
+                if (bgv[q] && (!spv[q] || spb[q])) colour = pal_s[bga[q] * 4u + bgv[q]];
+                else if (spv[q]) colour = pal_s[16u + spa[q] * 4u + spv[q]];
+                else colour = pal_s[0];
+                colour &= 0x3Fu;
+                if (mask & 1u) colour &= 0x30u;
+                word |= colour << (8 * q);
+            }
+            const int y = l - 8;
+            if (lane >= 2 && lane < 62) reinterpret_cast<uint32_t*>(obs + y * RLE_OBS_W)[lane - 2] = word;
+            if (lane == 0) emph[y] = (uint8_t)((mask >> 5) & 7u);
+        }
+        __syncthreads();   // palette writes of the replay below vs. reads above
+        rp_line_end(s, l, pal_s);
+        __syncthreads();
+    }
+}
+
+// ----------------------------------------------------------------------------------------- finish
+struct FinishArgs {
+    GameK g;
+    EnvArrays e;
+    Outs o;
+    Settings s;
+    int e0, e1;
+};
+
+__device__ uint64_t ram_hash(const uint8_t* ram) {
+    const uint4* w = reinterpret_cast<const uint4*>(ram);
+    uint64_t h = 0;
+    for (uint32_t k = 0; k < 128u; ++k) {
+        const uint4 q = w[k];
+        h += ev::mix64(((uint64_t)(4u * k) << 32) | q.x);
+        h += ev::mix64(((uint64_t)(4u * k + 1u) << 32) | q.y);
+        h += ev::mix64(((uint64_t)(4u * k + 2u) << 32) | q.z);
+        h += ev::mix64(((uint64_t)(4u * k + 3u) << 32) | q.w);
+    }
+    return h;
+}
+
+// RL part of the restart (rl/csrc/rlenv_core.cuh:208-263 without the record copy, which k_reset_copy does).
+__device__ void reset_rl(const GameK& g, const EnvArrays& e, const Settings& s, int ge) {
+    const uint32_t ep = ++e.episode[ge];
+    const uint64_t seed = ev::ep_seed(s.run_seed, (uint32_t)ge, ep);
+    const uint64_t sseed = ev::mix64(seed ^ 0x5717C4A55EEDull);
+    uint64_t ctr = 0;
+    int idle = 0;
+    if (s.idle_max > 0) idle = (int)ev::rnd_below(sseed, ctr, (uint32_t)(s.idle_max + 1));
+    e.sticky_seed[ge] = sseed;
+    e.sticky_ctr[ge] = ctr;
+    const int k = idle <= s.idle_tmpl ? idle : 0;
+    e.target[ge] = g.tmpl_target + (uint64_t)k * NES_FRAME_DOTS;
+    e.ep_frame[ge] = (uint32_t)k;
+    e.st[ge] = Rl10State{};
+    e.fault[ge] = 0;
+    Dropout d;
+    ev::drop_reset(d, seed, s.dropout != 0, s.gap_p32);
+    e.drop[ge] = d;
+    e.prev_applied[ge] = 0;
+    e.ep_idle[ge] = idle;
+    e.resetting[ge] = 1;
+}
+
+__device__ __forceinline__ void list_append(const GameK& g, bool want, int e) {
+    // one atomic per wavefront: the lanes that restart take consecutive list entries
+    const uint64_t b = __ballot(want);
+    if (b == 0) return;
+    const int lane = (int)(threadIdx.x & 63u);
+    const int leader = __builtin_ctzll(b);
+    uint32_t base = 0;
+    if (lane == leader) base = atomicAdd(g.list_count, (uint32_t)__popcll(b));
+    base = __shfl(base, leader);
+    if (want) g.list[base + (uint32_t)__popcll(b & ((1ull << lane) - 1ull))] = e;
+}
+
+__global__ __launch_bounds__(256) void k_finish(FinishArgs a) {
+    const int k = (int)(blockIdx.x * blockDim.x + threadIdx.x);
+    const bool valid = k < a.e1 - a.e0;
+    const int e = a.e0 + (valid ? k : 0);
+    const int ge = a.g.offset + e;
+    bool restart = false;
+    if (valid) {
+        const NesRec* rec = &a.g.recs[e];
+        if (a.o.ram_hash) a.o.ram_hash[ge] = ram_hash(rec->ram);
+        uint8_t b15[15];
+        ev::smb_gather(rec->ram, b15);
+        const Rl10Signals sig = ev::smb_signals(b15);
+        Rl10State st = a.e.st[ge];
+        const ev::Out u = ev::smb_update(sig, RLE_FRAMES, st);
+        a.e.st[ge] = st;
+        const bool faulted = a.e.fault[ge] != 0;
+        const bool level_clear = !u.done && !faulted && a.s.episode_level_end >= 0 && (u.events & ev::EV_LEVEL) &&
+                                 u.event_level == a.s.episode_level_end + 1;
+        bool synthetic = false;
+        if (a.s.end_p32 != 0 && !u.done && !faulted && !level_clear) {
+            uint64_t ctr = (uint64_t)(uint32_t)a.e.ep_len[ge];
+            const uint64_t es = ev::mix64(ev::ep_seed(a.s.run_seed, (uint32_t)ge, a.e.episode[ge]) ^ 0xE9D5EEDull);
+            synthetic = ev::rnd32(es, ctr) < a.s.end_p32;
+        }
+        const bool done = u.done || faulted || level_clear || synthetic;
+        const float r = faulted ? 0.0f : (float)u.reward;
+        a.o.reward[ge] = r;
+        if (a.o.parts)
+            for (int q = 0; q < RLE_PARTS; ++q) a.o.parts[(size_t)ge * RLE_PARTS + q] = faulted ? 0.0f : (float)u.part[q];
+        a.o.done[ge] = done ? 1 : 0;
+        a.o.events[ge] = u.events;
+        const float ret = a.e.ep_ret[ge] + r;
+        a.e.ep_ret[ge] = ret;
+        const int32_t len = a.e.ep_len[ge] + 1;
+        a.e.ep_len[ge] = len;
+        if (u.event_level > a.e.ep_maxlvl[ge]) a.e.ep_maxlvl[ge] = u.event_level;
+        Dropout d = a.e.drop[ge];
+        ev::drop_advance(d, a.s.dropout != 0, a.s.gap_p32);
+        a.e.drop[ge] = d;
+        if (done) {
+            float* inf = a.o.info + (size_t)ge * RLE_INFO;
+            inf[0] = ret;
+            inf[1] = (float)len;
+            inf[2] = (float)(faulted ? RLE_END_FAULT : level_clear ? RLE_END_LEVEL_CLEAR
+                                                                   : synthetic ? RLE_END_SYNTHETIC : st.end_reason);
+            inf[3] = (float)st.deaths;
+            inf[4] = (float)a.e.ep_maxlvl[ge];
+            inf[5] = st.overflow ? 1.0f : 0.0f;
+            inf[6] = (float)a.e.ep_idle[ge];
+            inf[7] = (float)a.e.episode[ge];
+            reset_rl(a.g, a.e, a.s, ge);
+            restart = true;
+        }
+    }
+    list_append(a.g, restart, e);
+}
+
+// Start: every env of the range restarts (rl/csrc/rlenv_core.cuh:400-404).
+__global__ __launch_bounds__(256) void k_start(FinishArgs a) {
+    const int k = (int)(blockIdx.x * blockDim.x + threadIdx.x);
+    const bool valid = k < a.e1 - a.e0;
+    const int e = a.e0 + (valid ? k : 0);
+    if (valid) reset_rl(a.g, a.e, a.s, a.g.offset + e);
+    list_append(a.g, valid, e);
+}
+
+// Boot snapshot (slot n) or idle template k-1 -> the listed console's record; one workgroup per entry.
+__global__ __launch_bounds__(256) void k_reset_copy(FinishArgs a) {
+    const uint32_t count = *a.g.list_count;
+    for (uint32_t k = blockIdx.x; k < count; k += gridDim.x) {
+        const int e = a.g.list[k];
+        const int idle = a.e.ep_idle[a.g.offset + e];
+        const int t = idle <= a.s.idle_tmpl ? idle : 0;
+        const uint4* src = reinterpret_cast<const uint4*>(t == 0 ? &a.g.recs[a.g.n] : &a.g.idle[t - 1]);
+        uint4* dst = reinterpret_cast<uint4*>(&a.g.recs[e]);
+        for (uint32_t i = threadIdx.x; i < NES_REC_BYTES / 16u; i += blockDim.x) dst[i] = src[i];
+    }
+}
+
+// First tracker update of restarted envs; masks and dropout timeline of every env (rl/csrc/rlenv_core.cuh:138-148,
+// 327-342). The last block clears the restart list for the next decision.
+__global__ __launch_bounds__(256) void k_reset_finish(FinishArgs a) {
+    const int k = (int)(blockIdx.x * blockDim.x + threadIdx.x);
+    if (k < a.e1 - a.e0) {
+        const int e = a.e0 + k, ge = a.g.offset + e;
+        if (a.e.resetting[ge]) {
+            uint8_t b15[15];
+            ev::smb_gather(a.g.recs[e].ram, b15);
+            Rl10State st = a.e.st[ge];
+            (void)ev::smb_update(ev::smb_signals(b15), a.e.ep_idle[ge] + RLE_FRAMES, st);
+            a.e.st[ge] = st;
+            a.e.ep_ret[ge] = 0.0f;
+            a.e.ep_len[ge] = 0;
+            a.e.ep_maxlvl[ge] = 0;
+            a.e.resetting[ge] = 0;
+        }
+        const Dropout* d = &a.e.drop[ge];
+        const int dr = ev::dropped_now(d);
+        uint8_t* mk = a.o.masks + (size_t)ge * RLE_MASK_BYTES;
+        for (uint32_t i = 0; i < 9; ++i) mk[i] = (dr >= 0 && dr < 4 && (ev::dpad_bits(i) & (ev::B_UP << dr))) ? 0 : 1;
+        mk[9] = 1;
+        mk[10] = dr == 4 ? 0 : 1;
+        mk[11] = dr == 6 ? 0 : 1;
+        mk[12] = 1;
+        mk[13] = dr == 5 ? 0 : 1;
+        mk[14] = dr == 7 ? 0 : 1;
+        mk[15] = 1;
+        mk[16] = a.g.start_ok ? 1 : 0;
+        mk[17] = 1;
+        mk[18] = a.g.select_ok ? 1 : 0;
+        uint32_t* tl = reinterpret_cast<uint32_t*>(a.o.tl + (size_t)ge * RLE_TIMELINE_BYTES);
+        for (int i = 0; i < RLE_TIMELINE_BYTES / 4; ++i) tl[i] = 0;
+        uint8_t* tb = a.o.tl + (size_t)ge * RLE_TIMELINE_BYTES;
+        for (uint32_t j = 0; j < RLE_TIMELINE; ++j) {
+            const int b = d->ring[(d->head + j) & (RLC_RING - 1)];
+            if (b >= 0) tb[b * RLE_TIMELINE + j] = 1;
+        }
+    }
+}
+
+__global__ void k_list_clear(uint32_t* count) {
+    if (threadIdx.x == 0 && blockIdx.x == 0) *count = 0;
+}
+
+// ------------------------------------------------------------------------------------- codec, gathers
+// pack6: 4 colour indices (6 bits) -> 3 bytes, little-endian v = p0 | p1 << 6 | p2 << 12 | p3 << 18
+// (rl/csrc/rlenv.cu:127-134). Each thread packs 16 pixels: one 16-byte load, one 12-byte store.
+__global__ __launch_bounds__(256) void k_pack6(const uint8_t* __restrict__ src, uint8_t* __restrict__ dst, size_t groups) {
+    const size_t t = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const size_t g0 = t * 4u;
+    if (g0 >= groups) return;
+    if (g0 + 4u <= groups) {
+        const uint4 q = reinterpret_cast<const uint4*>(src)[t];
+        const uint32_t w[4] = {q.x, q.y, q.z, q.w};
+        uint32_t v[4];
+        for (int i = 0; i < 4; ++i)
+            v[i] = (w[i] & 0x3Fu) | ((w[i] >> 2) & 0xFC0u) | ((w[i] >> 4) & 0x3F000u) | ((w[i] >> 6) & 0xFC0000u);
+        uint32_t* o = reinterpret_cast<uint32_t*>(dst + 12u * t);
+        o[0] = v[0] | (v[1] << 24);
+        o[1] = (v[1] >> 8) | (v[2] << 16);
+        o[2] = (v[2] >> 16) | (v[3] << 8);
+    } else {
+        for (size_t g = g0; g < groups; ++g) {
+            const uint32_t v = src[4 * g] | ((uint32_t)src[4 * g + 1] << 6) | ((uint32_t)src[4 * g + 2] << 12) |
+                               ((uint32_t)src[4 * g + 3] << 18);
+            dst[3 * g] = (uint8_t)v;
+            dst[3 * g + 1] = (uint8_t)(v >> 8);
+            dst[3 * g + 2] = (uint8_t)(v >> 16);
+        }
+    }
+}
+
+__global__ __launch_bounds__(256) void k_unpack6(const uint8_t* __restrict__ src, uint8_t* __restrict__ dst, size_t groups) {
+    const size_t t = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const size_t g0 = t * 4u;
+    if (g0 >= groups) return;
+    if (g0 + 4u <= groups) {
+        const uint32_t* in = reinterpret_cast<const uint32_t*>(src + 12u * t);
+        const uint32_t a0 = in[0], a1 = in[1], a2 = in[2];
+        const uint32_t v[4] = {a0 & 0xFFFFFFu, (a0 >> 24) | ((a1 & 0xFFFFu) << 8), (a1 >> 16) | ((a2 & 0xFFu) << 16),
+                               a2 >> 8};
+        uint32_t w[4];
+        for (int i = 0; i < 4; ++i)
+            w[i] = (v[i] & 63u) | (((v[i] >> 6) & 63u) << 8) | (((v[i] >> 12) & 63u) << 16) | (((v[i] >> 18) & 63u) << 24);
+        reinterpret_cast<uint4*>(dst)[t] = make_uint4(w[0], w[1], w[2], w[3]);
+    } else {
+        for (size_t g = g0; g < groups; ++g) {
+            const uint32_t v = src[3 * g] | ((uint32_t)src[3 * g + 1] << 8) | ((uint32_t)src[3 * g + 2] << 16);
+            dst[4 * g] = v & 63u;
+            dst[4 * g + 1] = (v >> 6) & 63u;
+            dst[4 * g + 2] = (v >> 12) & 63u;
+            dst[4 * g + 3] = (v >> 18) & 63u;
+        }
+    }
+}
+
+__global__ void k_gather_rows(uint4* __restrict__ dst, const uint4* __restrict__ src, const int64_t* rows, size_t row_vecs) {
+    const size_t j = blockIdx.x;
+    const uint4* s = src + (size_t)rows[j] * row_vecs;
+    uint4* d = dst + j * row_vecs;
+    for (size_t i = blockIdx.y * blockDim.x + threadIdx.x; i < row_vecs; i += (size_t)gridDim.y * blockDim.x) d[i] = s[i];
+}
+
+// Standalone reward10 SMB tracker: one env per lane, T steps; per step one 16-byte load and a 5-byte result.
+__global__ __launch_bounds__(256) void k_rl10_smb(const uint8_t* __restrict__ ram15, int T, int N, int frames,
+                                                  Rl10State* __restrict__ state, float* __restrict__ reward,
+                                                  uint8_t* __restrict__ done) {
+    const int e = (int)(blockIdx.x * blockDim.x + threadIdx.x);
+    if (e >= N) return;
+    Rl10State st = state[e];
+    for (int t = 0; t < T; ++t) {
+        const uint4 q = reinterpret_cast<const uint4*>(ram15)[(size_t)t * N + e];
+        uint8_t b[16];
+        memcpy(b, &q, 16);
+        const ev::Out u = ev::smb_update(ev::smb_signals(b), frames, st);
+        reward[(size_t)t * N + e] = (float)u.reward;
+        done[(size_t)t * N + e] = u.done ? 1 : 0;
+    }
+    state[e] = st;
+}
+
+// ============================================================================================== host
+struct DevMem {
+    std::vector<void*> blocks;
+    void* alloc(size_t n) {
+        void* p = nullptr;
+        if (hipMalloc(&p, n ? n : 1) != hipSuccess) throw std::runtime_error("hipMalloc failed");
+        blocks.push_back(p);
+        return p;
+    }
+    template <class T> T* zeros(size_t count) {
+        T* p = static_cast<T*>(alloc(sizeof(T) * count));
+        if (hipMemset(p, 0, sizeof(T) * count) != hipSuccess) throw std::runtime_error("hipMemset failed");
+        return p;
+    }
+    void upload(void* dst, const void* src, size_t n) {
+        if (hipMemcpy(dst, src, n, hipMemcpyHostToDevice) != hipSuccess) throw std::runtime_error("upload failed");
+    }
+    ~DevMem() {
+        for (void* p : blocks) (void)hipFree(p);
+    }
+};
+
+struct GameH {
+    GameK k;
+    int game;
+};
+
+struct Env {
+    DevMem mem;
+    int device = 0;
+    int total = 0;
+    std::vector<GameH> games;
+    EnvArrays e{};
+    Outs o{};
+    Settings s{};
+    uint32_t* optab = nullptr;
+    int cpw = 16;
+    uint32_t budget = NES_BUDGET;
+};
+
+// iNES -> cart description; the PRG is padded to a power of two by repeating a short image (NROM-128).
+struct Parsed {
+    std::vector<uint8_t> prg, chr;
+    uint32_t board = 0, mirroring = 0;
+};
+
+Parsed parse_ines(const uint8_t* rom, size_t size) {
+    if (size < 16 || std::memcmp(rom, "NES\x1A", 4) != 0) throw std::runtime_error("not an iNES image");
+    const size_t prg = (size_t)rom[4] * 16384u, chr = (size_t)rom[5] * 8192u;
+    const uint32_t mapper = (rom[6] >> 4) | (rom[7] & 0xF0u);
+    const size_t skip = 16u + ((rom[6] & 4u) ? 512u : 0u);
+    if (rom[6] & 8u) throw std::runtime_error("four-screen nametables are not supported");
+    if (mapper != 0 && mapper != 1 && mapper != 4)
+        throw std::runtime_error("unsupported mapper " + std::to_string(mapper) + " (supported: 0 NROM, 1 MMC1, 4 MMC3)");
+    if (prg == 0 || skip + prg + chr > size) throw std::runtime_error("truncated iNES image");
+    Parsed p;
+    size_t padded = 8192;
+    while (padded < prg) padded <<= 1;
+    p.prg.resize(padded);
+    for (size_t o = 0; o < padded; o += prg) std::memcpy(p.prg.data() + o, rom + skip, std::min(prg, padded - o));
+    p.chr.assign(rom + skip + prg, rom + skip + prg + chr);
+    p.board = mapper;
+    p.mirroring = rom[6] & 1u;
+    return p;
+}
+
+// RLENV_TRACE=1: synchronise after every launch and print its name and time (diagnostics).
+bool trace_on() {
+    static const bool on = std::getenv("RLENV_TRACE") != nullptr;
+    return on;
+}
+void trace(const char* what, hipStream_t st) {
+    if (!trace_on()) return;
+    static double t0 = 0;
+    const hipError_t e = hipStreamSynchronize(st);
+    timespec ts;
+    clock_gettime(CLOCK_MONOTONIC, &ts);
+    const double now = ts.tv_sec + ts.tv_nsec * 1e-9;
+    std::fprintf(stderr, "[rlenv] %-14s %s %.3f ms\n", what, hipGetErrorString(e), t0 ? (now - t0) * 1e3 : 0.0);
+    std::fflush(stderr);
+    t0 = now;
+}
+
+int check(const char* what) {
+    const hipError_t err = hipGetLastError();
+    if (err != hipSuccess) {
+        g_error = std::string(what) + ": " + hipGetErrorString(err);
+        return 1;
+    }
+    return 0;
+}
+
+FinishArgs finish_args(const Env& env, const GameK& g, int e0, int e1, const Outs& o) {
+    return FinishArgs{g, env.e, o, env.s, e0, e1};
+}
+
+void launch_emu(const Env& env, const GameK& g, const Outs& o, int mode, int f, bool use_list, int e0, int e1,
+                hipStream_t st) {
+    EmuArgs a{g, env.e, o, env.s, env.optab, mode, f, env.cpw, use_list ? 1 : 0, e0, e1, 0, 0, nullptr, env.budget};
+    const int n = use_list ? g.n : e1 - e0;
+    const int blocks = (n + env.cpw - 1) / env.cpw;
+    const size_t lds = 1024u + (size_t)env.cpw * kRamStride;
+    if (blocks > 0) hipLaunchKernelGGL(k_emu, dim3(blocks), dim3(64), lds, st, a);
+    trace(mode == EMU_DECISION ? "emu" : "emu_restart", st);
+}
+
+void launch_render(const Env& env, const GameK& g, const Outs& o, int f, bool use_list, bool restart, int e0, int e1,
+                   hipStream_t st) {
+    RenderArgs a{g, env.e, o, env.s, f, use_list ? 1 : 0, restart ? 1 : 0, e0, e1};
+    const int n = use_list ? g.n : e1 - e0;
+    if (n > 0) hipLaunchKernelGGL(k_render, dim3(n), dim3(64), 0, st, a);
+    trace(restart ? "render_restart" : "render", st);
+}
+
+// The restart half of a decision / start: snapshot copy, 4 neutral frames with pictures, first tracker update.
+void restart_phases(const Env& env, const GameK& g, const Outs& o, int e0, int e1, hipStream_t st) {
+    const FinishArgs fa = finish_args(env, g, e0, e1, o);
+    const int n = e1 - e0;
+    hipLaunchKernelGGL(k_reset_copy, dim3(std::min(std::max(n, 1), 2048)), dim3(256), 0, st, fa);
+    trace("reset_copy", st);
+    // (idle frames beyond the copied template never occur: the template count equals idle_max)
+    for (int f = 0; f < RLE_FRAMES; ++f) {
+        launch_emu(env, g, o, EMU_RESTART, f, true, e0, e1, st);
+        launch_render(env, g, o, f, true, true, e0, e1, st);
+    }
+    hipLaunchKernelGGL(k_reset_finish, dim3((n + 255) / 256), dim3(256), 0, st, fa);
+    hipLaunchKernelGGL(k_list_clear, dim3(1), dim3(1), 0, st, g.list_count);
+    trace("reset_finish", st);
+}
+
+void decision_phases(const Env& env, const GameK& g, const Outs& o, int e0, int e1, hipStream_t st) {
+    const int n = e1 - e0;
+    if (n <= 0) return;
+    for (int f = 0; f < RLE_FRAMES; ++f) {
+        launch_emu(env, g, o, EMU_DECISION, f, false, e0, e1, st);
+        launch_render(env, g, o, f, false, false, e0, e1, st);
+    }
+    hipLaunchKernelGGL(k_finish, dim3((n + 255) / 256), dim3(256), 0, st, finish_args(env, g, e0, e1, o));
+    trace("finish", st);
+    restart_phases(env, g, o, e0, e1, st);
+}
+
+void boot_game(Env& env, GameH& gh, const uint8_t* pads, size_t npads) {
+    GameK& g = gh.k;
+    hipLaunchKernelGGL(k_power_on, dim3(1), dim3(1), 0, 0, &g.recs[g.n], g.cart);
+    trace("power_on", 0);
+    uint32_t* fault = env.mem.zeros<uint32_t>(1);
+    uint64_t target = NES_VBLANK_DOT;
+    auto frame = [&](NesRec* base, int index, uint32_t pad) {
+        GameK one = g;
+        one.recs = base;
+        EmuArgs a{one, env.e, env.o, env.s, env.optab, EMU_BOOT, 0, 1, 0, index, index + 1, pad, target, fault,
+                  env.budget};
+        hipLaunchKernelGGL(k_emu, dim3(1), dim3(64), 1024u + kRamStride, 0, a);
+        target += NES_FRAME_DOTS;
+    };
+    for (size_t i = 0; i < npads; ++i) frame(g.recs, g.n, pads[i]);
+    g.tmpl_target = target;
+    NesRec* idle = const_cast<NesRec*>(g.idle);
+    for (int k = 1; k <= env.s.idle_tmpl; ++k) {
+        const NesRec* src = k == 1 ? &g.recs[g.n] : &idle[k - 2];
+        if (hipMemcpy(&idle[k - 1], src, sizeof(NesRec), hipMemcpyDeviceToDevice) != hipSuccess)
+            throw std::runtime_error("idle template copy failed");
+        frame(idle, k - 1, 0);
+    }
+    uint32_t host_fault = 0;
+    if (hipMemcpy(&host_fault, fault, 4, hipMemcpyDeviceToHost) != hipSuccess) throw std::runtime_error("boot sync failed");
+    if (check("boot")) throw std::runtime_error(g_error);
+    if (host_fault) throw std::runtime_error("emulator fault during boot of game " + std::to_string(gh.game));
+}
+
+template <class F>
+void for_each_state(Env& env, F&& f) {
+    for (auto& gh : env.games) f(gh.k.recs, sizeof(NesRec) * ((size_t)gh.k.n + 1));
+    const size_t N = (size_t)env.total;
+    f(env.e.st, N * sizeof(Rl10State));
+    f(env.e.drop, N * sizeof(Dropout));
+    f(env.e.target, N * 8); f(env.e.ep_frame, N * 4); f(env.e.prev_applied, N * 2); f(env.e.sticky_seed, N * 8);
+    f(env.e.sticky_ctr, N * 8); f(env.e.episode, N * 4); f(env.e.ep_ret, N * 4); f(env.e.ep_len, N * 4);
+    f(env.e.ep_maxlvl, N * 4); f(env.e.ep_idle, N * 4); f(env.e.fault, N * 4);
+}
+
+}  // namespace
+
+// ============================================================================================ C ABI
+extern "C" {
+
+void* rlenv_create(int ngames, const int* game_ids, const uint8_t* const* roms, const size_t* rom_sizes,
+                   const uint8_t* const* boot_pads, const size_t* boot_sizes, const int* n_envs, uint64_t run_seed,
+                   int sticky, int idle_max, int dropout, int device) {
+    Env* env = nullptr;
+    try {
+        if (hipSetDevice(device) != hipSuccess) throw std::runtime_error("hipSetDevice failed");
+        env = new Env();
+        env->device = device;
+        if (const char* v = std::getenv("RLENV_CPW")) env->cpw = std::max(1, std::min(64, std::atoi(v)));
+        if (const char* v = std::getenv("RLENV_BUDGET")) env->budget = (uint32_t)std::max(1, std::min((int)NES_BUDGET, std::atoi(v)));
+        if (hipFuncSetAttribute(reinterpret_cast<const void*>(k_emu), hipFuncAttributeMaxDynamicSharedMemorySize,
+                                (int)(1024u + 64u * kRamStride)) != hipSuccess)
+            throw std::runtime_error("hipFuncSetAttribute(k_emu) failed");
+        env->s.run_seed = run_seed;
+        env->s.sticky = sticky;
+        env->s.idle_max = idle_max;
+        env->s.idle_tmpl = idle_max > 0 ? idle_max : 0;
+        env->s.dropout = dropout;
+        env->s.episode_level_end = -1;
+        env->s.gap_p32 = RLC_GAP_P32;
+        uint32_t tab[256];
+        build_optab(tab);
+        env->optab = static_cast<uint32_t*>(env->mem.alloc(sizeof(tab)));
+        env->mem.upload(env->optab, tab, sizeof(tab));
+        for (int i = 0; i < ngames; ++i) env->total += n_envs[i];
+        const size_t N = (size_t)env->total;
+        EnvArrays& e = env->e;
+        e.st = env->mem.zeros<Rl10State>(N);
+        e.drop = env->mem.zeros<Dropout>(N);
+        e.target = env->mem.zeros<uint64_t>(N);
+        e.sticky_seed = env->mem.zeros<uint64_t>(N);
+        e.sticky_ctr = env->mem.zeros<uint64_t>(N);
+        e.ep_frame = env->mem.zeros<uint32_t>(N);
+        e.episode = env->mem.zeros<uint32_t>(N);
+        {
+            std::vector<uint32_t> init(N, 0xFFFFFFFFu);
+            env->mem.upload(e.episode, init.data(), N * 4);
+        }
+        e.fault = env->mem.zeros<uint32_t>(N);
+        e.prev_applied = env->mem.zeros<int16_t>(N);
+        e.ep_ret = env->mem.zeros<float>(N);
+        e.ep_len = env->mem.zeros<int32_t>(N);
+        e.ep_maxlvl = env->mem.zeros<int32_t>(N);
+        e.ep_idle = env->mem.zeros<int32_t>(N);
+        e.resetting = env->mem.zeros<uint8_t>(N);
+        int offset = 0;
+        for (int i = 0; i < ngames; ++i) {
+            if (game_ids[i] != 0)
+                throw std::runtime_error("game id " + std::to_string(game_ids[i]) +
+                                         ": only the smb reward reader (0) is built");
+            const Parsed p = parse_ines(roms[i], rom_sizes[i]);
+            GameH gh{};
+            gh.game = game_ids[i];
+            GameK& g = gh.k;
+            g.n = n_envs[i];
+            g.offset = offset;
+            offset += g.n;
+            g.start_ok = 0;   // smb: Start/Select not allowed (rl/csrc/reward10_consts.h:28)
+            g.select_ok = 0;
+            // widened PRG: word i = bytes i, i+1, i+2 (the instruction window at i)
+            std::vector<uint32_t> wide(p.prg.size());
+            for (size_t k = 0; k < p.prg.size(); ++k) {
+                const size_t k1 = std::min(k + 1, p.prg.size() - 1), k2 = std::min(k + 2, p.prg.size() - 1);
+                wide[k] = p.prg[k] | ((uint32_t)p.prg[k1] << 8) | ((uint32_t)p.prg[k2] << 16);
+            }
+            uint32_t* prgw = static_cast<uint32_t*>(env->mem.alloc(wide.size() * 4));
+            env->mem.upload(prgw, wide.data(), wide.size() * 4);
+            uint8_t* chr = nullptr;
+            if (!p.chr.empty()) {
+                chr = static_cast<uint8_t*>(env->mem.alloc(p.chr.size()));
+                env->mem.upload(chr, p.chr.data(), p.chr.size());
+            }
+            uint32_t chr_pages = p.chr.empty() ? 8u : (uint32_t)(p.chr.size() / 1024u);
+            if (chr_pages & (chr_pages - 1u)) throw std::runtime_error("CHR size must be a power of two");
+            g.cart = Cart{prgw, chr, (uint32_t)(p.prg.size() / 8192u), chr_pages, p.board, p.mirroring};
+            g.recs = env->mem.zeros<NesRec>((size_t)g.n + 1);
+            g.idle = env->mem.zeros<NesRec>((size_t)std::max(env->s.idle_tmpl, 1));
+            g.list = env->mem.zeros<int32_t>((size_t)std::max(g.n, 1));
+            g.list_count = env->mem.zeros<uint32_t>(1);
+            env->games.push_back(gh);
+            boot_game(*env, env->games.back(), boot_pads[i], boot_sizes[i]);
+        }
+        if (hipDeviceSynchronize() != hipSuccess || check("create")) throw std::runtime_error(g_error);
+        return env;
+    } catch (const std::exception& ex) {
+        g_error = ex.what();
+        delete env;
+        return nullptr;
+    }
+}
+
+int rlenv_num_envs(void* h) { return static_cast<Env*>(h)->total; }
+int rlenv_num_games(void* h) { return (int)static_cast<Env*>(h)->games.size(); }
+void rlenv_set_episode_level_end(void* h, int level) { static_cast<Env*>(h)->s.episode_level_end = level; }
+void rlenv_set_no_render(void* h, int v) { static_cast<Env*>(h)->s.no_render = v; }
+void rlenv_set_pad_mode(void* h, int raw) { static_cast<Env*>(h)->s.pad_mode = raw; }
+void rlenv_set_end_prob(void* h, uint32_t p) { static_cast<Env*>(h)->s.end_p32 = p; }
+void rlenv_set_dropout_gap(void* h, uint32_t p) { static_cast<Env*>(h)->s.gap_p32 = p; }
+void rlenv_bind_ram_hash(void* h, uint64_t* out) { static_cast<Env*>(h)->o.ram_hash = out; }
+
+void rlenv_bind(void* h, const int16_t* actions, uint8_t* obs, uint8_t* emph, float* reward, uint8_t* done,
+                uint8_t* masks, uint8_t* tl, uint8_t* pads, uint32_t* events, float* info) {
+    Outs& o = static_cast<Env*>(h)->o;
+    o.actions = actions; o.obs = obs; o.emph = emph; o.reward = reward; o.done = done; o.masks = masks;
+    o.tl = tl; o.pads = pads; o.events = events; o.info = info;
+}
+void rlenv_bind_parts(void* h, float* parts) { static_cast<Env*>(h)->o.parts = parts; }
+void rlenv_bind_obs(void* h, uint8_t* obs, uint8_t* emph) {
+    Outs& o = static_cast<Env*>(h)->o;
+    o.obs = obs;
+    o.emph = emph;
+}
+
+int rlenv_start(void* h, void* stream) {
+    Env& env = *static_cast<Env*>(h);
+    const hipStream_t st = static_cast<hipStream_t>(stream);
+    for (auto& gh : env.games) {
+        const FinishArgs fa = finish_args(env, gh.k, 0, gh.k.n, env.o);
+        hipLaunchKernelGGL(k_start, dim3((gh.k.n + 255) / 256), dim3(256), 0, st, fa);
+        trace("start", st);
+        restart_phases(env, gh.k, env.o, 0, gh.k.n, st);
+    }
+    return check("start");
+}
+
+int rlenv_step(void* h, void* stream) {
+    Env& env = *static_cast<Env*>(h);
+    const hipStream_t st = static_cast<hipStream_t>(stream);
+    for (auto& gh : env.games) decision_phases(env, gh.k, env.o, 0, gh.k.n, st);
+    return check("step");
+}
+
+int rlenv_step_game(void* h, int gi, uint8_t* obs, uint8_t* emph, void* stream) {
+    Env& env = *static_cast<Env*>(h);
+    if (gi < 0 || gi >= (int)env.games.size()) { g_error = "step_game: bad game"; return 1; }
+    Outs o = env.o;
+    o.obs = obs;
+    o.emph = emph;
+    decision_phases(env, env.games[gi].k, o, 0, env.games[gi].k.n, static_cast<hipStream_t>(stream));
+    return check("step_game");
+}
+
+int rlenv_step_range(void* h, int gi, int start, int count, uint8_t* obs, uint8_t* emph, void* stream) {
+    Env& env = *static_cast<Env*>(h);
+    if (gi < 0 || gi >= (int)env.games.size()) { g_error = "step_range: bad game"; return 1; }
+    const GameK& g = env.games[gi].k;
+    if (start < 0 || count <= 0 || start + count > g.n) { g_error = "step_range: bad range"; return 1; }
+    Outs o = env.o;
+    o.obs = obs;
+    o.emph = emph;
+    decision_phases(env, g, o, start, start + count, static_cast<hipStream_t>(stream));
+    return check("step_range");
+}
+
+size_t rlenv_state_bytes(void* h) {
+    size_t n = 0;
+    for_each_state(*static_cast<Env*>(h), [&](void*, size_t b) { n += b; });
+    return n;
+}
+
+int rlenv_save(void* h, uint8_t* out, void* stream) {
+    const hipStream_t s = static_cast<hipStream_t>(stream);
+    int bad = 0;
+    for_each_state(*static_cast<Env*>(h), [&](void* p, size_t b) {
+        bad |= hipMemcpyAsync(out, p, b, hipMemcpyDeviceToHost, s) != hipSuccess;
+        out += b;
+    });
+    bad |= hipStreamSynchronize(s) != hipSuccess;
+    if (bad) g_error = "save failed";
+    return bad;
+}
+
+int rlenv_load(void* h, const uint8_t* in, void* stream) {
+    const hipStream_t s = static_cast<hipStream_t>(stream);
+    int bad = 0;
+    for_each_state(*static_cast<Env*>(h), [&](void* p, size_t b) {
+        bad |= hipMemcpyAsync(p, in, b, hipMemcpyHostToDevice, s) != hipSuccess;
+        in += b;
+    });
+    bad |= hipStreamSynchronize(s) != hipSuccess;
+    if (bad) g_error = "load failed";
+    return bad;
+}
+
+int rlenv_read_consoles(void* h, int gi, int first, int count, uint8_t* out, void* stream) {
+    Env& env = *static_cast<Env*>(h);
+    if (gi < 0 || gi >= (int)env.games.size() || first < 0 || count < 0 || first + count > env.games[gi].k.n + 1) {
+        g_error = "read_consoles: bad range";
+        return 1;
+    }
+    const hipStream_t s = static_cast<hipStream_t>(stream);
+    if (hipMemcpyAsync(out, &env.games[gi].k.recs[first], sizeof(NesRec) * (size_t)count, hipMemcpyDeviceToHost, s) !=
+            hipSuccess ||
+        hipStreamSynchronize(s) != hipSuccess) {
+        g_error = "read_consoles failed";
+        return 1;
+    }
+    return 0;
+}
+
+const char* rlenv_error(void) { return g_error.c_str(); }
+void rlenv_destroy(void* h) { delete static_cast<Env*>(h); }
+
+void* rl_host_alloc(size_t bytes) {
+    void* p = nullptr;
+    if (hipHostMalloc(&p, bytes, hipHostMallocPortable) != hipSuccess) {
+        g_error = "hipHostMalloc failed";
+        return nullptr;
+    }
+    return p;
+}
+void rl_host_free(void* p) { (void)hipHostFree(p); }
+
+int rl_pack6(const void* src, void* dst, size_t pixels, void* stream) {
+    if (pixels % 4) { g_error = "pack6: pixel count must be divisible by four"; return 1; }
+    const size_t groups = pixels / 4, threads = (groups + 3) / 4;
+    if (groups)
+        hipLaunchKernelGGL(k_pack6, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, static_cast<hipStream_t>(stream),
+                           static_cast<const uint8_t*>(src), static_cast<uint8_t*>(dst), groups);
+    return check("pack6");
+}
+int rl_unpack6(const void* src, void* dst, size_t pixels, void* stream) {
+    if (pixels % 4) { g_error = "unpack6: pixel count must be divisible by four"; return 1; }
+    const size_t groups = pixels / 4, threads = (groups + 3) / 4;
+    if (groups)
+        hipLaunchKernelGGL(k_unpack6, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, static_cast<hipStream_t>(stream),
+                           static_cast<const uint8_t*>(src), static_cast<uint8_t*>(dst), groups);
+    return check("unpack6");
+}
+int rl_memcpy_async(void* dst, const void* src, size_t bytes, void* stream) {
+    if (hipMemcpyAsync(dst, src, bytes, hipMemcpyDefault, static_cast<hipStream_t>(stream)) != hipSuccess)
+        return check("memcpy");
+    return 0;
+}
+int rl_gather_rows(void* dst, const void* src, const int64_t* rows, int nrows, size_t row_bytes, void* stream) {
+    if (row_bytes % 16) { g_error = "gather_rows: row bytes must be a multiple of 16"; return 1; }
+    if (nrows > 0)
+        hipLaunchKernelGGL(k_gather_rows, dim3(nrows, 32), dim3(256), 0, static_cast<hipStream_t>(stream),
+                           static_cast<uint4*>(dst), static_cast<const uint4*>(src), rows, row_bytes / 16);
+    return check("gather");
+}
+int rl_gather_envs(void* dst, const void* src, const int64_t* envs, int n, int T, int N, size_t row_bytes, void* stream) {
+    const hipStream_t s = static_cast<hipStream_t>(stream);
+    for (int j = 0; j < n; ++j) {
+        if (hipMemcpy2DAsync(static_cast<char*>(dst) + (size_t)j * row_bytes, (size_t)n * row_bytes,
+                             static_cast<const char*>(src) + (size_t)envs[j] * row_bytes, (size_t)N * row_bytes,
+                             row_bytes, (size_t)T, hipMemcpyDefault, s) != hipSuccess)
+            return check("gather2d");
+    }
+    return 0;
+}
+
+int rl10_smb_run(const uint8_t* ram15, int T, int N, int frames, void* state, float* reward, uint8_t* done,
+                 void* stream) {
+    if (N > 0)
+        hipLaunchKernelGGL(k_rl10_smb, dim3((N + 255) / 256), dim3(256), 0, static_cast<hipStream_t>(stream), ram15, T, N,
+                           frames, static_cast<Rl10State*>(state), reward, done);
+    return check("rl10_smb_run");
+}
+
+}  // extern "C"

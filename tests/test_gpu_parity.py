@@ -1,0 +1,67 @@
+"""HIP library vs the CPU oracle, every output of every decision, bit for bit (the reference's own check is
+rl/tests/gpu_check.py:28-53: GPU vs CPU build, every output every step)."""
+import numpy as np
+import pytest
+import torch
+
+from helpers import HIP_LIB, ORACLE_LIB, REC_BYTES
+from rl import synth
+from rl.rlenv import RlEnv
+
+OUTS = ('obs', 'emph', 'reward', 'done', 'masks', 'timeline', 'pads', 'events', 'info', 'parts', 'ram_hash')
+
+
+def pair(n, cart, **kw):
+    cpu = RlEnv({'smb': n}, device='cpu', roms={'smb': cart}, lib_path=ORACLE_LIB, ram_hash=True, **kw)
+    gpu = RlEnv({'smb': n}, device='cuda', roms={'smb': cart}, lib_path=HIP_LIB, ram_hash=True, **kw)
+    return cpu, gpu
+
+
+def compare(cpu, gpu, where):
+    torch.cuda.synchronize()
+    for k in OUTS:
+        a, b = getattr(cpu, k).numpy(), getattr(gpu, k).cpu().numpy()
+        if not np.array_equal(a, b):
+            bad = np.argwhere(a != b)
+            raise AssertionError(f'{where}: {k} differs at {len(bad)} places, first {bad[:3].tolist()}')
+    ca, cb = cpu.consoles(0), gpu.consoles(0)
+    if not np.array_equal(ca, cb):
+        env, off = np.argwhere(ca != cb)[0]
+        raise AssertionError(f'{where}: console record {env} differs first at byte 0x{off:x}')
+
+
+def run(cpu, gpu, steps, seed, pad_mode, check_every=1):
+    g = torch.Generator().manual_seed(seed)
+    cpu.start()
+    gpu.start()
+    compare(cpu, gpu, 'start')
+    for t in range(steps):
+        hi = 256 if pad_mode else 324
+        act = torch.randint(0, hi, (cpu.n,), generator=g, dtype=torch.int16)
+        cpu.actions.copy_(act)
+        gpu.actions.copy_(act.cuda())
+        cpu.step()
+        gpu.step()
+        if (t + 1) % check_every == 0 or t == steps - 1:
+            compare(cpu, gpu, f'step {t}')
+
+
+@pytest.mark.gpu
+def test_nrom_raw_pads_sticky():
+    print('case: NROM seed 1, 16 consoles, raw pads, sticky, 24 decisions', flush=True)
+    cpu, gpu = pair(16, synth.nrom_cart(1), seed=5, sticky=True, idle_max=0, dropout=False, pad_mode=True)
+    run(cpu, gpu, 24, 0, True)
+
+
+@pytest.mark.gpu
+def test_nrom_moves_dropout_idle_ends():
+    print('case: NROM seed 2, 16 consoles, move ids, dropout, idle 0..6, Geometric(1/8) ends', flush=True)
+    cpu, gpu = pair(16, synth.nrom_cart(2), seed=7, sticky=True, idle_max=6, dropout=True, end_prob=1 / 8)
+    run(cpu, gpu, 24, 1, False)
+
+
+@pytest.mark.gpu
+def test_mmc3_stress():
+    print('case: MMC3 seed 3, 16 consoles, raw pads, IRQ + sprite-0 + bank switches', flush=True)
+    cpu, gpu = pair(16, synth.mmc3_cart(3), seed=9, sticky=True, idle_max=0, dropout=False, pad_mode=True)
+    run(cpu, gpu, 16, 2, True)
