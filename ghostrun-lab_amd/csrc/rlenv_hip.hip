@@ -579,6 +579,63 @@ struct GameH {
     int game;
 };
 
+// Kernel classes of a decision, for the per-kernel clock (rlenv_kernel_times).
+enum KClass : int {
+    KC_EMU = 0, KC_RENDER, KC_FINISH, KC_RESET_COPY, KC_EMU_RESTART, KC_RENDER_RESTART, KC_RESET_FINISH, KC_COUNT
+};
+
+// Optional per-launch HIP-event clock: when on, every launch of a decision is bracketed by two events on its
+// stream; the durations are summed per kernel class when read. Events are recycled through a pool.
+struct KernelClock {
+    bool on = false;
+    struct Mark { int cls; hipEvent_t a, b; };
+    std::vector<hipEvent_t> pool;
+    std::vector<Mark> marks;
+    hipEvent_t take() {
+        if (!pool.empty()) {
+            hipEvent_t ev = pool.back();
+            pool.pop_back();
+            return ev;
+        }
+        hipEvent_t ev = nullptr;
+        if (hipEventCreate(&ev) != hipSuccess) throw std::runtime_error("hipEventCreate failed");
+        return ev;
+    }
+    template <class F> void run(int cls, hipStream_t st, F&& launch) {
+        if (!on) {
+            launch();
+            return;
+        }
+        Mark m{cls, take(), take()};
+        (void)hipEventRecord(m.a, st);
+        launch();
+        (void)hipEventRecord(m.b, st);
+        marks.push_back(m);
+    }
+    // Sums and forgets the recorded launches (waits for them). Returns 0, or 1 on a HIP error.
+    int drain(double* ms, int64_t* count) {
+        int bad = 0;
+        for (const Mark& m : marks) {
+            float t = 0.f;
+            bad |= hipEventSynchronize(m.b) != hipSuccess;
+            bad |= hipEventElapsedTime(&t, m.a, m.b) != hipSuccess;
+            ms[m.cls] += t;
+            count[m.cls] += 1;
+            pool.push_back(m.a);
+            pool.push_back(m.b);
+        }
+        marks.clear();
+        return bad;
+    }
+    ~KernelClock() {
+        for (const Mark& m : marks) {
+            (void)hipEventDestroy(m.a);
+            (void)hipEventDestroy(m.b);
+        }
+        for (hipEvent_t ev : pool) (void)hipEventDestroy(ev);
+    }
+};
+
 struct Env {
     DevMem mem;
     int device = 0;
@@ -590,6 +647,7 @@ struct Env {
     uint32_t* optab = nullptr;
     int cpw = 16;
     uint32_t budget = NES_BUDGET;
+    mutable KernelClock clock;
 };
 
 // iNES -> cart description; the PRG is padded to a power of two by repeating a short image (NROM-128).
@@ -654,7 +712,9 @@ void launch_emu(const Env& env, const GameK& g, const Outs& o, int mode, int f, 
     const int n = use_list ? g.n : e1 - e0;
     const int blocks = (n + env.cpw - 1) / env.cpw;
     const size_t lds = 1024u + (size_t)env.cpw * kRamStride;
-    if (blocks > 0) hipLaunchKernelGGL(k_emu, dim3(blocks), dim3(64), lds, st, a);
+    if (blocks > 0)
+        env.clock.run(mode == EMU_DECISION ? KC_EMU : KC_EMU_RESTART, st,
+                      [&] { hipLaunchKernelGGL(k_emu, dim3(blocks), dim3(64), lds, st, a); });
     trace(mode == EMU_DECISION ? "emu" : "emu_restart", st);
 }
 
@@ -662,7 +722,9 @@ void launch_render(const Env& env, const GameK& g, const Outs& o, int f, bool us
                    hipStream_t st) {
     RenderArgs a{g, env.e, o, env.s, f, use_list ? 1 : 0, restart ? 1 : 0, e0, e1};
     const int n = use_list ? g.n : e1 - e0;
-    if (n > 0) hipLaunchKernelGGL(k_render, dim3(n), dim3(64), 0, st, a);
+    if (n > 0)
+        env.clock.run(restart ? KC_RENDER_RESTART : KC_RENDER, st,
+                      [&] { hipLaunchKernelGGL(k_render, dim3(n), dim3(64), 0, st, a); });
     trace(restart ? "render_restart" : "render", st);
 }
 
@@ -670,14 +732,17 @@ void launch_render(const Env& env, const GameK& g, const Outs& o, int f, bool us
 void restart_phases(const Env& env, const GameK& g, const Outs& o, int e0, int e1, hipStream_t st) {
     const FinishArgs fa = finish_args(env, g, e0, e1, o);
     const int n = e1 - e0;
-    hipLaunchKernelGGL(k_reset_copy, dim3(std::min(std::max(n, 1), 2048)), dim3(256), 0, st, fa);
+    env.clock.run(KC_RESET_COPY, st, [&] {
+        hipLaunchKernelGGL(k_reset_copy, dim3(std::min(std::max(n, 1), 2048)), dim3(256), 0, st, fa);
+    });
     trace("reset_copy", st);
     // (idle frames beyond the copied template never occur: the template count equals idle_max)
     for (int f = 0; f < RLE_FRAMES; ++f) {
         launch_emu(env, g, o, EMU_RESTART, f, true, e0, e1, st);
         launch_render(env, g, o, f, true, true, e0, e1, st);
     }
-    hipLaunchKernelGGL(k_reset_finish, dim3((n + 255) / 256), dim3(256), 0, st, fa);
+    env.clock.run(KC_RESET_FINISH, st,
+                  [&] { hipLaunchKernelGGL(k_reset_finish, dim3((n + 255) / 256), dim3(256), 0, st, fa); });
     hipLaunchKernelGGL(k_list_clear, dim3(1), dim3(1), 0, st, g.list_count);
     trace("reset_finish", st);
 }
@@ -689,7 +754,8 @@ void decision_phases(const Env& env, const GameK& g, const Outs& o, int e0, int 
         launch_emu(env, g, o, EMU_DECISION, f, false, e0, e1, st);
         launch_render(env, g, o, f, false, false, e0, e1, st);
     }
-    hipLaunchKernelGGL(k_finish, dim3((n + 255) / 256), dim3(256), 0, st, finish_args(env, g, e0, e1, o));
+    const FinishArgs fa = finish_args(env, g, e0, e1, o);
+    env.clock.run(KC_FINISH, st, [&] { hipLaunchKernelGGL(k_finish, dim3((n + 255) / 256), dim3(256), 0, st, fa); });
     trace("finish", st);
     restart_phases(env, g, o, e0, e1, st);
 }
@@ -936,6 +1002,15 @@ int rlenv_read_consoles(void* h, int gi, int first, int count, uint8_t* out, voi
         g_error = "read_consoles failed";
         return 1;
     }
+    return 0;
+}
+
+void rlenv_set_kernel_timing(void* h, int on) { static_cast<Env*>(h)->clock.on = on != 0; }
+
+int rlenv_kernel_times(void* h, double* ms, int64_t* count, int n) {
+    if (n < KC_COUNT) { g_error = "kernel_times: need room for every kernel class"; return 1; }
+    for (int i = 0; i < n; ++i) { ms[i] = 0.0; count[i] = 0; }
+    if (static_cast<Env*>(h)->clock.drain(ms, count)) { g_error = "kernel_times: event query failed"; return 1; }
     return 0;
 }
 

@@ -861,3 +861,12 @@ void orc_smb_observe(const uint8_t* ram, void* signals_out) {
     gather15(ram, b15);
     *(Rl10Signals*)signals_out = observe_smb(b15);
 }
+/* OpenMP threads of the oracle's parallel loops (the CPU baseline times 1 and all host threads). */
+void orc_set_threads(int n) { omp_set_num_threads(n > 0 ? n : 1); }
+/* The oracle has no device work to time: the per-kernel clock reads zero launches. */
+void rlenv_set_kernel_timing(void* h, int on) { (void)h; (void)on; }
+int rlenv_kernel_times(void* h, double* ms, int64_t* count, int n) {
+    (void)h;
+    for (int i = 0; i < n; ++i) { ms[i] = 0.0; count[i] = 0; }
+    return 0;
+}
