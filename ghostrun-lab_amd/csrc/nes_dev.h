@@ -66,9 +66,17 @@ struct Cart {
 
 struct Mem {
     NesRec* rec;
-    uint8_t* ram;           // this console's RAM in LDS
+    uint8_t* ram;           // this console's 2 KB CPU RAM (LDS)
+    uint8_t* nt;            // 2 KB nametable RAM, 256 B OAM, 32 B palette: the record's, or LDS copies of them
+    uint8_t* oam;
+    uint8_t* pal;
     Cart cart;
 };
+
+// The memories of a console record, with the CPU RAM at `ram`.
+__device__ __forceinline__ Mem mem_of(NesRec* rec, uint8_t* ram, const Cart& cart) {
+    return Mem{rec, ram, rec->nt, rec->oam, rec->pal, cart};
+}
 
 __device__ __forceinline__ uint32_t sel4(uint32_t i, uint32_t a, uint32_t b, uint32_t c, uint32_t d) {
     return i & 2u ? (i & 1u ? d : c) : (i & 1u ? b : a);
@@ -380,8 +388,8 @@ __device__ inline uint32_t rp_bg(const Replay& s, const Mem& m, uint32_t x, uint
     }
     const uint32_t cy = (s.v >> 5) & 31u, fy = (s.v >> 12) & 7u;
     const uint32_t base = 0x2000u | ((nth | (((s.v >> 11) & 1u) << 1)) << 10);
-    const uint32_t tile = m.rec->nt[nt_index(s.nt_map, base | (cy << 5) | cx)];
-    const uint32_t at = m.rec->nt[nt_index(s.nt_map, base | 0x3C0u | ((cy >> 2) << 3) | (cx >> 2))];
+    const uint32_t tile = m.nt[nt_index(s.nt_map, base | (cy << 5) | cx)];
+    const uint32_t at = m.nt[nt_index(s.nt_map, base | 0x3C0u | ((cy >> 2) << 3) | (cx >> 2))];
     *pal_sel = (at >> (((cy & 2u) << 1) | (cx & 2u))) & 3u;
     const uint32_t pa = ((s.ctrl & 0x10u) << 8) + tile * 16u + fy;
     const uint32_t lo = chr_byte_pk(m, s.chr_lo, s.chr_hi, pa), hi = chr_byte_pk(m, s.chr_lo, s.chr_hi, pa + 8u);
@@ -397,7 +405,7 @@ __device__ inline uint32_t sprite_row_addr(uint32_t ctrl, uint32_t tile, uint32_
 
 // First sprite-0 hit of the logged frame from the events logged so far (frame dot), kNoHit if none.
 __device__ __forceinline__ int32_t sprite0_scan(const Mem m, uint32_t log_n) {
-    const uint8_t* oam = m.rec->oam;
+    const uint8_t* oam = m.oam;
     const int y0 = oam[0], x0 = oam[3];
     if (y0 >= 239) return (int32_t)kNoHit;
     const uint32_t tile = oam[1], attr = oam[2];
@@ -472,7 +480,7 @@ __device__ inline void log_capture(Con& c, const Mem& m) {
         p0 |= ((co[i] >> 10) & 0xFFu) << (8 * i);
         p1 |= ((co[4 + i] >> 10) & 0xFFu) << (8 * i);
     }
-    const uint32_t* pal = reinterpret_cast<const uint32_t*>(m.rec->pal);
+    const uint32_t* pal = reinterpret_cast<const uint32_t*>(m.pal);
     h[0] = 0;
     h[1] = c.ctrl | (c.mask << 8) | (c.fx << 16);
     h[2] = c.v | (c.t << 16);
@@ -557,10 +565,10 @@ __device__ inline void log_event(Con& c, const Mem& m, const Access& ac, uint32_
 __device__ inline uint32_t ppu_mem_read(const Con& c, const Mem& m, uint32_t a) {
     a &= 0x3FFFu;
     if (a < 0x2000u) return chr_byte(m, m.rec->chr_off, a);
-    if (a < 0x3F00u) return m.rec->nt[nt_index(c.nt_map, a)];
+    if (a < 0x3F00u) return m.nt[nt_index(c.nt_map, a)];
     uint32_t i = a & 0x1Fu;
     if ((i & 0x13u) == 0x10u) i &= 0x0Fu;
-    return m.rec->pal[i];
+    return m.pal[i];
 }
 
 __device__ __forceinline__ uint32_t vinc(const Con& c) { return (c.ctrl & 4u) ? 32u : 1u; }
@@ -574,7 +582,7 @@ __device__ inline uint32_t io_read(Con& c, const Mem& m, const Access& ac, uint3
             c.status &= 0x7Fu;
             c.w = 0;
         } else if (reg == 4) {
-            v = m.rec->oam[c.oam_addr];
+            v = m.oam[c.oam_addr];
         } else if (reg == 7) {
             const uint32_t pa = c.v & 0x3FFFu;
             if (pa < 0x3F00u) {
@@ -633,7 +641,7 @@ __device__ inline void ppu_reg_write(Con& c, const Mem& m, const Access& ac, uin
     } else if (reg == 3) {
         c.oam_addr = v;
     } else if (reg == 4) {
-        m.rec->oam[c.oam_addr] = (uint8_t)v;
+        m.oam[c.oam_addr] = (uint8_t)v;
         c.oam_addr = (c.oam_addr + 1u) & 0xFFu;
         c.s0_valid = 0;
     } else if (reg == 5) {
@@ -665,12 +673,12 @@ __device__ inline void ppu_reg_write(Con& c, const Mem& m, const Access& ac, uin
             }
             log_event(c, m, ac, NES_EV_DATA, 0, 1);
         } else if (pa < 0x3F00u) {
-            m.rec->nt[nt_index(c.nt_map, pa)] = (uint8_t)v;
+            m.nt[nt_index(c.nt_map, pa)] = (uint8_t)v;
             log_event(c, m, ac, NES_EV_DATA, 0, 1);
         } else {
             uint32_t i = pa & 0x1Fu;
             if ((i & 0x13u) == 0x10u) i &= 0x0Fu;
-            m.rec->pal[i] = (uint8_t)(v & 0x3Fu);
+            m.pal[i] = (uint8_t)(v & 0x3Fu);
             log_event(c, m, ac, NES_EV_PAL, v & 0x3Fu, i);
         }
         c.v = (c.v + vinc(c)) & 0x7FFFu;
@@ -682,7 +690,7 @@ __device__ inline void io_write(Con& c, const Mem& m, Access& ac, uint32_t a, ui
         ppu_reg_write(c, m, ac, a & 7u, v);
     } else if (a == 0x4014u) {
         // OAM DMA: 256 bytes of CPU page v through the bus (normally RAM in LDS)
-        uint8_t* oam = m.rec->oam;
+        uint8_t* oam = m.oam;
         for (uint32_t i = 0; i < 256u; ++i) {
             const uint32_t src = (v << 8) | i;
             const uint32_t b = src < 0x2000u ? m.ram[src & 0x7FFu] : bus_read(c, m, ac, src);
@@ -993,7 +1001,7 @@ __device__ inline void power_on(NesRec* rec, const Cart& cart) {
     for (uint32_t i = 0; i < NES_REC_BYTES; ++i) bytes[i] = 0;
     rec->board = (uint8_t)cart.board;
     Con c = {};
-    const Mem m{rec, nullptr, cart};
+    const Mem m = mem_of(rec, nullptr, cart);
     uint8_t* r = rec->mreg;
     if (cart.board == NES_BOARD_MMC1) {
         r[0] = 0x0C;

@@ -11,7 +11,7 @@ enum Mn { ORA, AND, EOR, ADC, STA, LDA, CMP, SBC, ASL, ROL, LSR, ROR, STX, LDX, 
           BPL, BMI, BVC, BVS, BCC, BCS, BNE, BEQ, CLC, SEC, CLI, SEI, CLV, CLD, SED, TAX, TAY, TXA, TYA, TSX, TXS,
           INX, INY, DEX, DEY, NOP, PHA, PHP, PLA, PLP, JMP, JSR, RTS, RTI, BRK };
 
-inline uint32_t rw_cycles(bool store, uint32_t mode) {
+constexpr uint32_t rw_cycles(bool store, uint32_t mode) {
     switch (mode) {
         case M_IMM: return 2;
         case M_ZP: return 3;
@@ -22,7 +22,7 @@ inline uint32_t rw_cycles(bool store, uint32_t mode) {
     }
 }
 
-inline uint32_t descriptor(Mn mn, uint32_t mode) {
+constexpr uint32_t descriptor(Mn mn, uint32_t mode) {
     const uint32_t pen = (mode == M_ABX || mode == M_ABY || mode == M_IZY) ? D_PEN : 0u;
     const uint32_t rd = mode == M_IMM ? 0u : D_READ;
     switch (mn) {
@@ -85,47 +85,58 @@ inline uint32_t descriptor(Mn mn, uint32_t mode) {
     }
 }
 
-inline void build_optab(uint32_t* t) {
-    for (int i = 0; i < 256; ++i) t[i] = 0;   // G_ILL
-    // column-group instructions: opcode = aaa << 5 | bbb << 2 | 01
-    static const uint32_t g1_mode[8] = {M_IZX, M_ZP, M_IMM, M_ABS, M_IZY, M_ZPX, M_ABY, M_ABX};
-    static const Mn g1[8] = {ORA, AND, EOR, ADC, STA, LDA, CMP, SBC};
+struct OpRow { uint8_t op; Mn mn; uint32_t mode; };
+// column-group instructions: opcode = aaa << 5 | bbb << 2 | 01
+constexpr uint32_t kG1Mode[8] = {M_IZX, M_ZP, M_IMM, M_ABS, M_IZY, M_ZPX, M_ABY, M_ABX};
+constexpr Mn kG1[8] = {ORA, AND, EOR, ADC, STA, LDA, CMP, SBC};
+// read-modify-write shifts and INC/DEC: opcode = aaa << 5 | bbb << 2 | 10
+constexpr Mn kG2[8] = {ASL, ROL, LSR, ROR, STX, LDX, DEC, INC};
+constexpr OpRow kRest[] = {
+    {0x86, STX, M_ZP}, {0x8E, STX, M_ABS}, {0x96, STX, M_ZPY},
+    {0xA2, LDX, M_IMM}, {0xA6, LDX, M_ZP}, {0xAE, LDX, M_ABS}, {0xB6, LDX, M_ZPY}, {0xBE, LDX, M_ABY},
+    {0x84, STY, M_ZP}, {0x8C, STY, M_ABS}, {0x94, STY, M_ZPX},
+    {0xA0, LDY, M_IMM}, {0xA4, LDY, M_ZP}, {0xAC, LDY, M_ABS}, {0xB4, LDY, M_ZPX}, {0xBC, LDY, M_ABX},
+    {0xC0, CPY, M_IMM}, {0xC4, CPY, M_ZP}, {0xCC, CPY, M_ABS},
+    {0xE0, CPX, M_IMM}, {0xE4, CPX, M_ZP}, {0xEC, CPX, M_ABS},
+    {0x24, BIT, M_ZP}, {0x2C, BIT, M_ABS},
+    {0x10, BPL, M_REL}, {0x30, BMI, M_REL}, {0x50, BVC, M_REL}, {0x70, BVS, M_REL},
+    {0x90, BCC, M_REL}, {0xB0, BCS, M_REL}, {0xD0, BNE, M_REL}, {0xF0, BEQ, M_REL},
+    {0x18, CLC, M_IMP}, {0x38, SEC, M_IMP}, {0x58, CLI, M_IMP}, {0x78, SEI, M_IMP}, {0xB8, CLV, M_IMP},
+    {0xD8, CLD, M_IMP}, {0xF8, SED, M_IMP},
+    {0xAA, TAX, M_IMP}, {0xA8, TAY, M_IMP}, {0x8A, TXA, M_IMP}, {0x98, TYA, M_IMP}, {0xBA, TSX, M_IMP},
+    {0x9A, TXS, M_IMP}, {0xE8, INX, M_IMP}, {0xC8, INY, M_IMP}, {0xCA, DEX, M_IMP}, {0x88, DEY, M_IMP},
+    {0xEA, NOP, M_IMP}, {0x48, PHA, M_IMP}, {0x08, PHP, M_IMP}, {0x68, PLA, M_IMP}, {0x28, PLP, M_IMP},
+    {0x4C, JMP, M_ABS}, {0x6C, JMP, M_IND}, {0x20, JSR, M_ABS}, {0x60, RTS, M_IMP}, {0x40, RTI, M_IMP},
+    {0x00, BRK, M_IMP},
+};
+
+struct Optab { uint32_t t[256]; };
+
+constexpr Optab make_optab() {
+    Optab o{};   // all G_ILL
     for (uint32_t a = 0; a < 8; ++a)
         for (uint32_t b = 0; b < 8; ++b) {
-            if (g1[a] == STA && g1_mode[b] == M_IMM) continue;
-            t[(a << 5) | (b << 2) | 1u] = descriptor(g1[a], g1_mode[b]);
+            if (kG1[a] == STA && kG1Mode[b] == M_IMM) continue;
+            o.t[(a << 5) | (b << 2) | 1u] = descriptor(kG1[a], kG1Mode[b]);
         }
-    // read-modify-write shifts and INC/DEC: opcode = aaa << 5 | bbb << 2 | 10
-    static const Mn g2[8] = {ASL, ROL, LSR, ROR, STX, LDX, DEC, INC};
     for (uint32_t a = 0; a < 8; ++a) {
-        const Mn mn = g2[a];
+        const Mn mn = kG2[a];
         if (mn == STX || mn == LDX) continue;
-        t[(a << 5) | (1u << 2) | 2u] = descriptor(mn, M_ZP);
-        t[(a << 5) | (3u << 2) | 2u] = descriptor(mn, M_ABS);
-        t[(a << 5) | (5u << 2) | 2u] = descriptor(mn, M_ZPX);
-        t[(a << 5) | (7u << 2) | 2u] = descriptor(mn, M_ABX);
-        if (a < 4) t[(a << 5) | (2u << 2) | 2u] = descriptor(mn, M_IMP);   // accumulator
+        o.t[(a << 5) | (1u << 2) | 2u] = descriptor(mn, M_ZP);
+        o.t[(a << 5) | (3u << 2) | 2u] = descriptor(mn, M_ABS);
+        o.t[(a << 5) | (5u << 2) | 2u] = descriptor(mn, M_ZPX);
+        o.t[(a << 5) | (7u << 2) | 2u] = descriptor(mn, M_ABX);
+        if (a < 4) o.t[(a << 5) | (2u << 2) | 2u] = descriptor(mn, M_IMP);   // accumulator
     }
-    struct { uint8_t op; Mn mn; uint32_t mode; } rest[] = {
-        {0x86, STX, M_ZP}, {0x8E, STX, M_ABS}, {0x96, STX, M_ZPY},
-        {0xA2, LDX, M_IMM}, {0xA6, LDX, M_ZP}, {0xAE, LDX, M_ABS}, {0xB6, LDX, M_ZPY}, {0xBE, LDX, M_ABY},
-        {0x84, STY, M_ZP}, {0x8C, STY, M_ABS}, {0x94, STY, M_ZPX},
-        {0xA0, LDY, M_IMM}, {0xA4, LDY, M_ZP}, {0xAC, LDY, M_ABS}, {0xB4, LDY, M_ZPX}, {0xBC, LDY, M_ABX},
-        {0xC0, CPY, M_IMM}, {0xC4, CPY, M_ZP}, {0xCC, CPY, M_ABS},
-        {0xE0, CPX, M_IMM}, {0xE4, CPX, M_ZP}, {0xEC, CPX, M_ABS},
-        {0x24, BIT, M_ZP}, {0x2C, BIT, M_ABS},
-        {0x10, BPL, M_REL}, {0x30, BMI, M_REL}, {0x50, BVC, M_REL}, {0x70, BVS, M_REL},
-        {0x90, BCC, M_REL}, {0xB0, BCS, M_REL}, {0xD0, BNE, M_REL}, {0xF0, BEQ, M_REL},
-        {0x18, CLC, M_IMP}, {0x38, SEC, M_IMP}, {0x58, CLI, M_IMP}, {0x78, SEI, M_IMP}, {0xB8, CLV, M_IMP},
-        {0xD8, CLD, M_IMP}, {0xF8, SED, M_IMP},
-        {0xAA, TAX, M_IMP}, {0xA8, TAY, M_IMP}, {0x8A, TXA, M_IMP}, {0x98, TYA, M_IMP}, {0xBA, TSX, M_IMP},
-        {0x9A, TXS, M_IMP}, {0xE8, INX, M_IMP}, {0xC8, INY, M_IMP}, {0xCA, DEX, M_IMP}, {0x88, DEY, M_IMP},
-        {0xEA, NOP, M_IMP}, {0x48, PHA, M_IMP}, {0x08, PHP, M_IMP}, {0x68, PLA, M_IMP}, {0x28, PLP, M_IMP},
-        {0x4C, JMP, M_ABS}, {0x6C, JMP, M_IND}, {0x20, JSR, M_ABS}, {0x60, RTS, M_IMP}, {0x40, RTI, M_IMP},
-        {0x00, BRK, M_IMP},
-    };
-    for (const auto& r : rest) t[r.op] = descriptor(r.mn, r.mode);
+    for (const OpRow& r : kRest) o.t[r.op] = descriptor(r.mn, r.mode);
+    return o;
 }
 
+// The descriptor table at compile time: the wave interpreter specialises each opcode's code on its entry.
+constexpr Optab kOptab = make_optab();
+
+inline void build_optab(uint32_t* t) {
+    for (int i = 0; i < 256; ++i) t[i] = kOptab.t[i];
+}
 
 }  // namespace nd

@@ -9,9 +9,10 @@
 //   4 x (k_emu, k_render) over the restart list only (neutral frames of the new episode)
 //   k_reset_finish: first tracker update of new episodes; masks and dropout timeline of every env
 //
-// k_emu runs one console per lane with `cpw` consoles per wavefront (a launch parameter: with 8192 consoles the
-// machine has 1024 SIMDs, so fewer consoles per wave buys latency hiding and less divergence); the consoles' RAM
-// lives in LDS for the launch, copied in and out with coalesced whole-workgroup copies.
+// k_emu_w (the default) gives each console a whole wavefront: the console index comes from blockIdx, so its state
+// is wave-uniform and the 6502 runs on the scalar unit (uniform branches, SGPRs) with a per-opcode fast path
+// (wave_dev.h); the console's RAM, nametables, OAM, palette and cold state live in LDS for the launch. 8192 consoles
+// are 8192 waves, 8 per SIMD. k_emu (RLENV_EMU=lane) runs one console per lane, `cpw` consoles per wavefront.
 // k_render draws one console-frame per wavefront: the line replay is wave-uniform, each lane composes 4 pixels,
 // sprites are selected with one ballot per line, and each output row is one coalesced 240-byte store.
 #include <hip/hip_runtime.h>
@@ -28,6 +29,7 @@
 #include "nes_dev.h"
 #include "optab.h"
 #include "rlenv_api.h"
+#include "wave_dev.h"
 #include "rlenv_state.h"
 
 using namespace nd;
@@ -95,7 +97,7 @@ __device__ __forceinline__ int slot_env(const GameK& g, int use_list, int e0, in
 }
 
 // Per-frame pad byte of a decision frame (rl/csrc/rlenv_core.cuh:181-191): sticky repeat, dropout, turbo phase.
-__device__ uint32_t decision_pad(const EmuArgs& a, int ge, int f) {
+__device__ __forceinline__ uint32_t decision_pad(const EmuArgs& a, int ge, int f) {
     const int d = ev::dropped_now(&a.e.drop[ge]);
     uint64_t ctr = a.e.sticky_ctr[ge];
     const uint64_t seed = a.e.sticky_seed[ge];
@@ -138,7 +140,7 @@ __global__ __launch_bounds__(64) void k_emu(EmuArgs a) {
     if (lane < nslot) {
         const int e = a.mode == EMU_BOOT ? a.e0 : slot_env(a.g, a.use_list, a.e0, first + lane);
         NesRec* rec = &a.g.recs[e];
-        const Mem m{rec, rams + lane * kRamStride, a.g.cart};
+        const Mem m = mem_of(rec, rams + lane * kRamStride, a.g.cart);
         const int ge = a.g.offset + e;
         uint32_t pad = 0, fault = 0;
         uint64_t target;
@@ -179,6 +181,79 @@ __global__ __launch_bounds__(64) void k_emu(EmuArgs a) {
     }
 }
 
+// The opcode descriptors in constant memory: the wave-uniform generic step reads them through the scalar cache.
+__constant__ Optab c_optab = kOptab;
+
+// Copies n bytes (a multiple of 16, 16-byte aligned) with the 64 lanes of the wavefront.
+__device__ __forceinline__ void wave_copy16(void* dst, const void* src, uint32_t n, int lane) {
+    uint4* d = static_cast<uint4*>(dst);
+    const uint4* s = static_cast<const uint4*>(src);
+    for (uint32_t i = (uint32_t)lane; i < n / 16u; i += 64u) d[i] = s[i];
+}
+
+// Per-wavefront LDS of one console: CPU RAM, nametables, OAM, palette and the console state.
+struct WaveLds {
+    uint8_t ram[NES_RAM_BYTES];
+    uint8_t nt[NES_NT_BYTES];
+    uint8_t oam[NES_OAM_BYTES];
+    uint8_t pal[NES_PAL_BYTES];
+    Con cs;
+};
+
+// One console per wavefront (blockDim 64): the console index comes from blockIdx only, so every emulator value is
+// wave-uniform; lane 0 runs the 6502 on the scalar unit (SGPRs, uniform branches) with the console's memories in
+// LDS, the 64 lanes copy them in and out.
+template <uint32_t B>
+__global__ __launch_bounds__(64) void k_emu_w(EmuArgs a) {
+    __shared__ __align__(16) WaveLds L;
+    const int count = a.mode == EMU_BOOT ? 1 : slot_count(a.g, a.use_list, a.e0, a.e1);
+    const int k = (int)blockIdx.x;
+    if (k >= count) return;
+    const int lane = (int)threadIdx.x;
+    const int e = a.mode == EMU_BOOT ? a.e0 : slot_env(a.g, a.use_list, a.e0, k);
+    const int ge = a.g.offset + e;
+    if (a.mode == EMU_RESTART && a.e.resetting[ge] == 0) return;
+    NesRec* rec = &a.g.recs[e];
+    wave_copy16(L.ram, rec->ram, NES_RAM_BYTES, lane);
+    wave_copy16(L.nt, rec->nt, NES_NT_BYTES, lane);
+    wave_copy16(L.oam, rec->oam, NES_OAM_BYTES, lane);
+    wave_copy16(L.pal, rec->pal, NES_PAL_BYTES, lane);
+    __syncthreads();
+    if (lane == 0) {
+        uint32_t pad = 0, fault = 0;
+        uint64_t target;
+        if (a.mode == EMU_BOOT) {
+            pad = a.boot_pad;
+            target = a.boot_target;
+        } else {
+            if (a.mode == EMU_DECISION) pad = decision_pad(a, ge, a.f);
+            target = a.e.target[ge];
+            fault = a.e.fault[ge];
+        }
+        Con& cs = L.cs;
+        con_load(cs, rec);
+        cs.pad = pad;
+        const Mem m{rec, L.ram, L.nt, L.oam, L.pal, a.g.cart};
+        if (fault == 0) {
+            const uint32_t f = run_until_wave<B>(cs, m, c_optab.t, target, a.budget);
+            if (f != 0) {
+                if (a.mode == EMU_BOOT) atomicOr(a.boot_fault, 1u);
+                else a.e.fault[ge] = f;
+            }
+        }
+        con_store(cs, rec);
+        if (a.mode != EMU_BOOT) {
+            a.e.target[ge] = target + NES_FRAME_DOTS;
+            a.e.ep_frame[ge] += 1u;
+        }
+    }
+    __syncthreads();
+    wave_copy16(rec->ram, L.ram, NES_RAM_BYTES, lane);
+    wave_copy16(rec->nt, L.nt, NES_NT_BYTES, lane);
+    wave_copy16(rec->oam, L.oam, NES_OAM_BYTES, lane);
+    wave_copy16(rec->pal, L.pal, NES_PAL_BYTES, lane);
+}
+
 // Power-on of one console record.
 __global__ void k_power_on(NesRec* rec, Cart cart) {
     if (threadIdx.x == 0 && blockIdx.x == 0) power_on(rec, cart);
@@ -213,7 +288,7 @@ __global__ __launch_bounds__(64) void k_render(RenderArgs a) {
     Replay s;
     rp_begin(s, rec->log, rec->log_n, pal_s);
     __syncthreads();
-    const Mem m{const_cast<NesRec*>(rec), nullptr, a.g.cart};
+    const Mem m = mem_of(const_cast<NesRec*>(rec), nullptr, a.g.cart);
     uint8_t* obs = a.o.obs + ((size_t)ge * RLE_FRAMES + a.f) * RLE_OBS_PIXELS;
     uint8_t* emph = a.o.emph + ((size_t)ge * RLE_FRAMES + a.f) * RLE_OBS_H;
     const uint32_t my_sy = oam_s[4 * lane];
@@ -646,6 +721,7 @@ struct Env {
     Settings s{};
     uint32_t* optab = nullptr;
     int cpw = 16;
+    bool emu_wave = true;    // k_emu_w (one console per wavefront); RLENV_EMU=lane selects k_emu
     uint32_t budget = NES_BUDGET;
     mutable KernelClock clock;
 };
@@ -710,11 +786,17 @@ void launch_emu(const Env& env, const GameK& g, const Outs& o, int mode, int f, 
                 hipStream_t st) {
     EmuArgs a{g, env.e, o, env.s, env.optab, mode, f, env.cpw, use_list ? 1 : 0, e0, e1, 0, 0, nullptr, env.budget};
     const int n = use_list ? g.n : e1 - e0;
-    const int blocks = (n + env.cpw - 1) / env.cpw;
+    const int blocks = env.emu_wave ? n : (n + env.cpw - 1) / env.cpw;
     const size_t lds = 1024u + (size_t)env.cpw * kRamStride;
     if (blocks > 0)
-        env.clock.run(mode == EMU_DECISION ? KC_EMU : KC_EMU_RESTART, st,
-                      [&] { hipLaunchKernelGGL(k_emu, dim3(blocks), dim3(64), lds, st, a); });
+        env.clock.run(mode == EMU_DECISION ? KC_EMU : KC_EMU_RESTART, st, [&] {
+            if (env.emu_wave) {
+                if (g.cart.board == NES_BOARD_MMC3) hipLaunchKernelGGL(k_emu_w<NES_BOARD_MMC3>, dim3(blocks), dim3(64), 0, st, a);
+                else if (g.cart.board == NES_BOARD_MMC1) hipLaunchKernelGGL(k_emu_w<NES_BOARD_MMC1>, dim3(blocks), dim3(64), 0, st, a);
+                else hipLaunchKernelGGL(k_emu_w<NES_BOARD_NROM>, dim3(blocks), dim3(64), 0, st, a);
+            }
+            else hipLaunchKernelGGL(k_emu, dim3(blocks), dim3(64), lds, st, a);
+        });
     trace(mode == EMU_DECISION ? "emu" : "emu_restart", st);
 }
 
@@ -814,6 +896,7 @@ void* rlenv_create(int ngames, const int* game_ids, const uint8_t* const* roms, 
         env = new Env();
         env->device = device;
         if (const char* v = std::getenv("RLENV_CPW")) env->cpw = std::max(1, std::min(64, std::atoi(v)));
+        if (const char* v = std::getenv("RLENV_EMU")) env->emu_wave = std::strcmp(v, "lane") != 0;
         if (const char* v = std::getenv("RLENV_BUDGET")) env->budget = (uint32_t)std::max(1, std::min((int)NES_BUDGET, std::atoi(v)));
         if (hipFuncSetAttribute(reinterpret_cast<const void*>(k_emu), hipFuncAttributeMaxDynamicSharedMemorySize,
                                 (int)(1024u + 64u * kRamStride)) != hipSuccess)

@@ -1,0 +1,312 @@
+// Wave-uniform fast path of the 6502 interpreter (gfx950).
+//
+// A console owned by a whole wavefront has wave-uniform state, so the compiler keeps it in SGPRs and runs it on the
+// scalar unit with uniform branches. This header adds the fast path that makes that cheap: `switch (opcode)` where
+// each case is the generic step (nes_dev.h cpu_step) specialised at compile time on that opcode's descriptor
+// (optab.h kOptab), so an instruction is straight-line scalar code with no table decode. Instruction bytes come
+// through the scalar data cache (constant address space loads of the widened PRG image).
+//
+// The fast path covers every official opcode whose memory operands are CPU RAM ($0000-$1FFF) or, for reads, PRG
+// ($8000-$FFFF). Anything else - I/O registers, PRG RAM, open bus, a store or read-modify-write at $8000+ (a mapper
+// write), BRK, an opcode outside the official set, a pending NMI or IRQ, code outside PRG - returns 0 before any
+// state changes and the caller runs the generic step instead, so the semantics are exactly cpu_step's
+// (third_party/nesle-extensions.patch:823-862 and rl/csrc/nes_machine.cuh:67-103 in kdcyberdude/ghostrun-lab).
+#pragma once
+#include "nes_dev.h"
+#include "optab.h"
+
+namespace nd {
+
+typedef __attribute__((address_space(4))) const uint32_t ConstU32;
+
+// Registers the fast loop keeps live: the CPU registers, the cycle counter and the PRG page offsets. Everything
+// else about the console (PPU, controller, DMC, mapper) stays in the console state in LDS and only the generic
+// step, the PPU settle and the idle fast-forward touch it, so the loop's live set is small enough to stay in SGPRs.
+struct Hot {
+    uint32_t pc, a, x, y, sp, p;
+    uint64_t cycles;
+    uint32_t prg0, prg1, prg2, prg3;
+};
+
+__device__ __forceinline__ void hot_load(Hot& h, const Con& c) {
+    h.pc = c.pc; h.a = c.a; h.x = c.x; h.y = c.y; h.sp = c.sp; h.p = c.p; h.cycles = c.cycles;
+    h.prg0 = c.prg0; h.prg1 = c.prg1; h.prg2 = c.prg2; h.prg3 = c.prg3;
+}
+// (the PRG offsets change only in the generic step, which writes them to the console state itself)
+__device__ __forceinline__ void hot_store(const Hot& h, Con& c) {
+    c.pc = h.pc; c.a = h.a; c.x = h.x; c.y = h.y; c.sp = h.sp; c.p = h.p; c.cycles = h.cycles;
+}
+
+__device__ __forceinline__ uint32_t hget(const Hot& h, uint32_t code, uint32_t opd) {
+    return code == R_A ? h.a : code == R_X ? h.x : code == R_Y ? h.y : code == R_SP ? h.sp : opd;
+}
+__device__ __forceinline__ void hset(Hot& h, uint32_t code, uint32_t v) {
+    if (code == R_A) h.a = v;
+    else if (code == R_X) h.x = v;
+    else if (code == R_Y) h.y = v;
+    else if (code == R_SP) h.sp = v;
+}
+__device__ __forceinline__ void hnz(Hot& h, uint32_t v) {
+    h.p = (h.p & ~(FL_N | FL_Z)) | (v & 0x80u) | ((v & 0xFFu) ? 0u : FL_Z);
+}
+__device__ __forceinline__ void hpush(Hot& h, const Mem& m, uint32_t v) {
+    m.ram[0x100u | h.sp] = (uint8_t)v;
+    h.sp = (h.sp - 1u) & 0xFFu;
+}
+__device__ __forceinline__ uint32_t hpull(Hot& h, const Mem& m) {
+    h.sp = (h.sp + 1u) & 0xFFu;
+    return m.ram[0x100u | h.sp];
+}
+
+// Byte offset in the PRG image of CPU address `addr` ($8000-$FFFF). NROM maps the image linearly (mirrored).
+template <uint32_t B>
+__device__ __forceinline__ uint32_t prg_index(const Hot& h, const Mem& m, uint32_t addr) {
+    if constexpr (B == NES_BOARD_NROM) return addr & 0x7FFFu & (m.cart.prg_pages8 * 8192u - 1u);
+    else return sel4((addr >> 13) & 3u, h.prg0, h.prg1, h.prg2, h.prg3) + (addr & 0x1FFFu);
+}
+
+// Widened PRG word at `idx` (bytes idx, idx+1, idx+2) through a scalar load: the image is read-only for the
+// whole kernel.
+__device__ __forceinline__ uint32_t prg_wide(const Mem& m, uint32_t idx) {
+    return ((ConstU32*)m.cart.prgw)[idx];
+}
+
+// One instruction of opcode descriptor D at pc (operand bytes lo, hi). Returns its CPU cycles (the DMC is serviced
+// by the caller), or 0 with nothing changed when the generic step must run it.
+template <uint32_t B, uint32_t D>
+__device__ __forceinline__ uint32_t fx(Hot& h, const Mem& m, uint32_t pc, uint32_t lo, uint32_t hi) {
+    constexpr uint32_t mode = D & 15u, grp = (D >> 8) & 15u, sub = (D >> 12) & 15u;
+    constexpr uint32_t src = (D >> 16) & 7u, dst = (D >> 19) & 7u;
+    constexpr bool rd = (D & D_READ) != 0, wr = (D & D_WRITE) != 0, pen = (D & D_PEN) != 0;
+    constexpr bool zpage = mode == M_ZP || mode == M_ZPX || mode == M_ZPY;
+    if constexpr (grp == G_ILL || grp == G_BRK) {
+        return 0;
+    } else {
+        uint32_t cyc = (D >> 4) & 15u;
+        const uint32_t base = lo | (hi << 8);
+        uint32_t ea = 0;
+        if constexpr (mode == M_ZP) {
+            ea = lo;
+        } else if constexpr (mode == M_ZPX) {
+            ea = (lo + h.x) & 0xFFu;
+        } else if constexpr (mode == M_ZPY) {
+            ea = (lo + h.y) & 0xFFu;
+        } else if constexpr (mode == M_ABS || mode == M_IND) {
+            ea = base;
+        } else if constexpr (mode == M_ABX || mode == M_ABY) {
+            ea = (base + (mode == M_ABX ? h.x : h.y)) & 0xFFFFu;
+            if constexpr (pen) cyc += ((base ^ ea) & 0xFF00u) ? 1u : 0u;
+        } else if constexpr (mode == M_IZX) {
+            const uint32_t ptr = (lo + h.x) & 0xFFu;
+            ea = m.ram[ptr] | ((uint32_t)m.ram[(ptr + 1u) & 0xFFu] << 8);
+        } else if constexpr (mode == M_IZY) {
+            const uint32_t b2 = m.ram[lo] | ((uint32_t)m.ram[(lo + 1u) & 0xFFu] << 8);
+            ea = (b2 + h.y) & 0xFFFFu;
+            if constexpr (pen) cyc += ((b2 ^ ea) & 0xFF00u) ? 1u : 0u;
+        }
+        // memory class: bail out before any side effect
+        if constexpr (!zpage && (rd || wr)) {
+            if (ea >= 0x2000u && (wr || ea < 0x8000u)) return 0;
+        }
+        uint32_t opd = lo;
+        if constexpr (rd) {
+            if constexpr (zpage) opd = m.ram[ea];
+            else opd = ea < 0x2000u ? (uint32_t)m.ram[ea & 0x7FFu] : (prg_wide(m, prg_index<B>(h, m, ea)) & 0xFFu);
+        }
+        constexpr uint32_t len = mode == M_IMP ? 1u : ((mode >= M_ABS && mode <= M_ABY) || mode == M_IND) ? 3u : 2u;
+        uint32_t npc = (pc + len) & 0xFFFFu, res = 0;
+        if constexpr (grp == G_LD) {
+            res = hget(h, src, opd);
+            hset(h, dst, res);
+            if constexpr (dst != R_SP) hnz(h, res);
+        } else if constexpr (grp == G_ST) {
+            res = hget(h, src, 0);
+        } else if constexpr (grp == G_INCDEC) {
+            res = (hget(h, src, opd) + (sub ? 0xFFu : 1u)) & 0xFFu;
+            hset(h, dst, res);
+            hnz(h, res);
+        } else if constexpr (grp == G_ALU) {
+            if constexpr (sub <= 2) {
+                h.a = sub == 0 ? (h.a | opd) : sub == 1 ? (h.a & opd) : (h.a ^ opd);
+                hnz(h, h.a);
+            } else if constexpr (sub <= 4) {
+                const uint32_t mv = sub == 4 ? (opd ^ 0xFFu) : opd;
+                const uint32_t sum = h.a + mv + (h.p & FL_C);
+                const uint32_t ov = (~(h.a ^ mv) & (h.a ^ sum) & 0x80u) ? FL_V : 0u;
+                h.p = (h.p & ~(FL_C | FL_V)) | (sum >> 8) | ov;
+                h.a = sum & 0xFFu;
+                hnz(h, h.a);
+            } else if constexpr (sub == 5) {
+                const uint32_t r = hget(h, src, 0);
+                h.p = (h.p & ~FL_C) | (r >= opd ? FL_C : 0u);
+                hnz(h, (r - opd) & 0xFFu);
+            } else {
+                h.p = (h.p & ~(FL_N | FL_V | FL_Z)) | (opd & 0xC0u) | ((h.a & opd) ? 0u : FL_Z);
+            }
+        } else if constexpr (grp == G_SHIFT) {
+            const uint32_t in = hget(h, src, opd), cin = h.p & FL_C;
+            uint32_t cout;
+            if constexpr (sub == 0) { res = (in << 1) & 0xFFu; cout = in >> 7; }
+            else if constexpr (sub == 1) { res = in >> 1; cout = in & 1u; }
+            else if constexpr (sub == 2) { res = ((in << 1) | cin) & 0xFFu; cout = in >> 7; }
+            else { res = (in >> 1) | (cin << 7); cout = in & 1u; }
+            h.p = (h.p & ~FL_C) | cout;
+            hset(h, dst, res);
+            hnz(h, res);
+        } else if constexpr (grp == G_BR) {
+            const bool set = ((h.p >> (sub & 7u)) & 1u) != 0;
+            if (set == ((sub & 8u) != 0)) {
+                const uint32_t tgt = (npc + (uint32_t)(int32_t)(int8_t)lo) & 0xFFFFu;
+                cyc += ((npc ^ tgt) & 0xFF00u) ? 2u : 1u;
+                npc = tgt;
+            }
+        } else if constexpr (grp == G_FLAG) {
+            constexpr uint32_t bitm = 1u << (sub & 7u);
+            h.p = (sub & 8u) ? (h.p | bitm) : (h.p & ~bitm);
+        } else if constexpr (grp == G_PUSH) {
+            hpush(h, m, src == R_A ? h.a : (h.p | FL_B | FL_U));
+        } else if constexpr (grp == G_PULL) {
+            const uint32_t v = hpull(h, m);
+            if constexpr (dst == R_A) {
+                h.a = v;
+                hnz(h, v);
+            } else {
+                h.p = (v & ~FL_B) | FL_U;
+            }
+        } else if constexpr (grp == G_JMP) {
+            if constexpr (mode == M_IND) {
+                const uint32_t a1 = (base & 0xFF00u) | ((base + 1u) & 0xFFu);
+                if ((base >= 0x2000u && base < 0x8000u) || (a1 >= 0x2000u && a1 < 0x8000u)) return 0;
+                const uint32_t l8 = base < 0x2000u ? (uint32_t)m.ram[base & 0x7FFu]
+                                                   : (prg_wide(m, prg_index<B>(h, m, base)) & 0xFFu);
+                const uint32_t h8 = a1 < 0x2000u ? (uint32_t)m.ram[a1 & 0x7FFu]
+                                                 : (prg_wide(m, prg_index<B>(h, m, a1)) & 0xFFu);
+                npc = l8 | (h8 << 8);
+            } else {
+                npc = base;
+            }
+        } else if constexpr (grp == G_JSR) {
+            const uint32_t ret = (pc + 2u) & 0xFFFFu;
+            hpush(h, m, ret >> 8);
+            hpush(h, m, ret & 0xFFu);
+            npc = base;
+        } else if constexpr (grp == G_RTS) {
+            const uint32_t l8 = hpull(h, m), h8 = hpull(h, m);
+            npc = (((h8 << 8) | l8) + 1u) & 0xFFFFu;
+        } else if constexpr (grp == G_RTI) {
+            h.p = (hpull(h, m) & ~FL_B) | FL_U;
+            const uint32_t l8 = hpull(h, m), h8 = hpull(h, m);
+            npc = (h8 << 8) | l8;
+        }
+        if constexpr (wr) {
+            if constexpr (zpage) m.ram[ea] = (uint8_t)res;
+            else m.ram[ea & 0x7FFu] = (uint8_t)res;
+        }
+        h.pc = npc;
+        h.cycles += cyc;
+        return cyc;
+    }
+}
+
+#define ND_FX(n) \
+    case n: return fx<B, kOptab.t[n]>(h, m, pc, lo, hi);
+#define ND_FX16(h)                                                                                                    \
+    ND_FX(h + 0x0) ND_FX(h + 0x1) ND_FX(h + 0x2) ND_FX(h + 0x3) ND_FX(h + 0x4) ND_FX(h + 0x5) ND_FX(h + 0x6)          \
+    ND_FX(h + 0x7) ND_FX(h + 0x8) ND_FX(h + 0x9) ND_FX(h + 0xA) ND_FX(h + 0xB) ND_FX(h + 0xC) ND_FX(h + 0xD)          \
+    ND_FX(h + 0xE) ND_FX(h + 0xF)
+
+// The fast path for the instruction at h.pc: its cycles, or 0 (nothing changed) for the generic step.
+template <uint32_t B>
+__device__ __forceinline__ uint32_t fast_step(Hot& h, const Mem& m, uint32_t* op_out) {
+    const uint32_t pc = h.pc;
+    if (pc < 0x8000u || (pc & 0x1FFFu) > 0x1FFDu) return 0;
+    const uint32_t word = prg_wide(m, prg_index<B>(h, m, pc));
+    const uint32_t op = word & 0xFFu, lo = (word >> 8) & 0xFFu, hi = (word >> 16) & 0xFFu;
+    *op_out = op;
+    switch (op) {
+        ND_FX16(0x00) ND_FX16(0x10) ND_FX16(0x20) ND_FX16(0x30) ND_FX16(0x40) ND_FX16(0x50) ND_FX16(0x60)
+        ND_FX16(0x70) ND_FX16(0x80) ND_FX16(0x90) ND_FX16(0xA0) ND_FX16(0xB0) ND_FX16(0xC0) ND_FX16(0xD0)
+        ND_FX16(0xE0) ND_FX16(0xF0)
+        default: return 0;
+    }
+}
+#undef ND_FX16
+#undef ND_FX
+
+// run_until (nes_dev.h) with the fast path first, for a console whose state `cs` lives in LDS: the same PPU
+// settling, event horizon, idle-loop fast-forward, budget and fault handling, so the console ends in exactly the
+// state run_until leaves. The fast loop keeps only Hot and a few flags live; the generic step, the settle and the
+// fast-forward work on `cs` (CPU registers written back before and reloaded after each of them).
+template <uint32_t B>
+__device__ __forceinline__ uint32_t run_until_wave(Con& cs, const Mem& m, const uint32_t* optab, uint64_t target,
+                                                   uint32_t budget = NES_BUDGET) {
+    uint32_t instructions = 0, fault = 0, pending = 0;
+    uint32_t to_event = dots_to_event(cs, m);
+    Hot h;
+    hot_load(h, cs);
+    uint64_t dmc_event = cs.dmc_event;
+    uint32_t nmi = cs.nmi_pending, irq = cs.irq_line, s0v = cs.s0_valid;
+    while (instructions < budget) {
+        if (pending >= to_event) {
+            ppu_advance(cs, m, pending);   // touches no CPU register
+            pending = 0;
+            nmi = cs.nmi_pending;
+            irq = cs.irq_line;
+            if (abs_dot(cs) >= target) break;
+            to_event = dots_to_event(cs, m);
+            s0v = cs.s0_valid;
+        }
+        uint32_t op = 0, pc0 = h.pc, cyc = 0;
+        if (!nmi && !(irq && !(h.p & FL_I))) cyc = fast_step<B>(h, m, &op);
+        if (cyc != 0) {
+            if (h.cycles >= dmc_event) {
+                const uint32_t s = dmc_service(m.rec, h.cycles, 1);
+                dmc_event = m.rec->dmc_event;
+                h.cycles += s;
+                cyc += s;
+            }
+        } else {
+            hot_store(h, cs);
+            cs.dmc_event = dmc_event;
+            const int32_t start_rel =
+                (int32_t)((int64_t)abs_dot(cs) + pending - (int64_t)cs.log_frame * NES_FRAME_DOTS);
+            cyc = cpu_step(cs, m, optab, start_rel, &fault, &op, &pc0);
+            hot_load(h, cs);
+            dmc_event = cs.dmc_event;
+            nmi = cs.nmi_pending;
+            irq = cs.irq_line;
+            s0v = cs.s0_valid;
+            if (fault) break;
+        }
+        pending += 3u * cyc;
+        ++instructions;
+        if (!s0v) {
+            to_event = dots_to_event(cs, m);
+            s0v = cs.s0_valid;
+        }
+        if (op == 0x4Cu && h.pc == pc0) {
+            hot_store(h, cs);
+            cs.dmc_event = dmc_event;
+            ppu_advance(cs, m, pending);
+            pending = 0;
+            nmi = cs.nmi_pending;
+            irq = cs.irq_line;
+            if (abs_dot(cs) >= target) break;
+            fast_forward(cs, m);
+            h.cycles = cs.cycles;
+            dmc_event = cs.dmc_event;
+            nmi = cs.nmi_pending;
+            irq = cs.irq_line;
+            to_event = dots_to_event(cs, m);
+            s0v = cs.s0_valid;
+            if (abs_dot(cs) >= target) break;
+        }
+    }
+    hot_store(h, cs);
+    cs.dmc_event = dmc_event;
+    cs.instr += instructions;
+    if (pending) ppu_advance(cs, m, pending);
+    return fault;
+}
+
+}  // namespace nd
