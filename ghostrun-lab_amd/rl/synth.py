@@ -9,6 +9,9 @@ cartridges generated here from a seed:
 * ``mmc3_cart(seed)`` - MMC3: 256 KB PRG / 128 KB CHR. The main loop switches the $8000 PRG bank and calls into
   it about every 200 instructions, switches CHR banks, arms the scanline IRQ at a line 20..220 that depends on
   the console's own history, and splits the scroll on the sprite-0 hit.
+* ``smb_like_cart(seed)`` - NROM-128 that writes the RAM bytes the SMB reward reader reads (position, level,
+  lives, score, dying, mode) from the pad, idling in a JMP-to-self loop with its logic in the NMI as SMB does,
+  so rewards, deaths, level changes, game over and the idle fast-forward all run.
 * ``smb_ram15(seed, n_envs, steps)`` - per env-step the 15 RAM bytes the SMB reward reader reads (x position as a
   +-1..4 px random walk with 5% rollback jumps, world/level advancing with p 1e-3, lives lost with p 5e-4, BCD-like
   score digits), packed as ``rl10_smb_run`` takes them.
@@ -375,6 +378,86 @@ def mmc3_cart(seed: int = 0, blocks: int = 16, sub_blocks: int = 20) -> bytes:
     prg = b''.join(banks) + bytes(fixed_c) + bytes(fixed_e)
     chr_ = rng.integers(0, 256, 128 * 1024, dtype=np.uint8).tobytes()
     return ines(prg, chr_, 4, vertical=True)
+
+
+DCNT, DYCNT = 0x44, 0x45                  # frames Down has been held, frames spent dying
+
+
+def smb_like_cart(seed: int = 0) -> bytes:
+    """NROM-128 cartridge that plays like the SMB reward reader expects (it writes the reader's RAM bytes), so the
+    env's reward, death, level and game-over paths all run. SMB's structure: the main loop is a JMP-to-self idle
+    loop and everything happens in the NMI (OAM DMA, nametable and scroll writes, pad read, game logic).
+
+    In play (mode $0770 = 1, task $0772 = 3, routine $0E = 8): Right moves the position ($6D page, $86 x) 2 px
+    forward, Left 1 px back, A adds 10 points (score digits $07E1-$07E2), holding Down for 24 frames starts dying
+    (routine 6); page 3 is the next level ($075C, then world $075F), world 8 wins (mode 2, world 7). Dying lasts 30
+    frames, then a life ($075A) is lost and play resumes at the level start; losing a life at 0 is game over
+    (mode 3)."""
+    rng = np.random.default_rng([0x534D424C, seed])
+    pal, nt, oam, mix = _tables(rng)
+    a = Asm(0xC000)
+    tables = dict(pal='t_pal', nt='t_nt', oam='t_oam')
+    a.label('reset')
+    _reset_common(a, 0x90, tables)
+    for addr, v in ((0x0770, 1), (0x0772, 3), (0x000E, 8), (0x075A, 2), (0x0086, 40)):
+        a.op('LDA', 'imm', v); a.op('STA', 'abs', addr)
+    a.label('idle')
+    a.op('JMP', 'abs', 'idle')
+    a.label('nmi')
+    _nmi_common(a)
+    _read_pad(a, 'n')
+    a.op('LDA', 'abs', 0x0770); a.op('CMP', 'imm', 1); a.op('BEQ', 'rel', 'inplay'); a.op('JMP', 'abs', 'done')
+    a.label('inplay')
+    a.op('LDA', 'zp', 0x0E); a.op('CMP', 'imm', 8); a.op('BEQ', 'rel', 'alive'); a.op('JMP', 'abs', 'dying')
+    a.label('alive')
+    a.op('LDA', 'zp', PAD); a.op('AND', 'imm', 0x80); a.op('BEQ', 'rel', 'noright')
+    a.op('LDA', 'zp', 0x86); a.op('CLC'); a.op('ADC', 'imm', 2); a.op('STA', 'zp', 0x86)
+    a.op('LDA', 'zp', 0x6D); a.op('ADC', 'imm', 0); a.op('STA', 'zp', 0x6D)
+    a.label('noright')
+    a.op('LDA', 'zp', PAD); a.op('AND', 'imm', 0x40); a.op('BEQ', 'rel', 'noleft')
+    a.op('LDA', 'zp', 0x86); a.op('SEC'); a.op('SBC', 'imm', 1); a.op('STA', 'zp', 0x86)
+    a.op('LDA', 'zp', 0x6D); a.op('SBC', 'imm', 0); a.op('STA', 'zp', 0x6D)
+    a.label('noleft')
+    a.op('LDA', 'zp', PAD); a.op('AND', 'imm', 0x01); a.op('BEQ', 'rel', 'noa')
+    a.op('INC', 'abs', 0x07E2); a.op('LDA', 'abs', 0x07E2); a.op('CMP', 'imm', 10); a.op('BCC', 'rel', 'noa')
+    a.op('LDA', 'imm', 0); a.op('STA', 'abs', 0x07E2); a.op('INC', 'abs', 0x07E1)
+    a.label('noa')
+    a.op('LDA', 'zp', PAD); a.op('AND', 'imm', 0x20); a.op('BEQ', 'rel', 'nodown')
+    a.op('INC', 'zp', DCNT); a.op('LDA', 'zp', DCNT); a.op('CMP', 'imm', 24); a.op('BCC', 'rel', 'moved')
+    a.op('LDA', 'imm', 6); a.op('STA', 'zp', 0x0E); a.op('LDA', 'imm', 0); a.op('STA', 'zp', DCNT)
+    a.op('JMP', 'abs', 'done')
+    a.label('nodown')
+    a.op('LDA', 'imm', 0); a.op('STA', 'zp', DCNT)
+    a.label('moved')
+    a.op('LDA', 'zp', 0x6D); a.op('BMI', 'rel', 'done_n'); a.op('CMP', 'imm', 3); a.op('BCC', 'rel', 'done_n')
+    a.op('INC', 'abs', 0x075C); a.op('LDA', 'imm', 0); a.op('STA', 'zp', 0x6D); a.op('LDA', 'imm', 40)
+    a.op('STA', 'zp', 0x86)
+    a.op('LDA', 'abs', 0x075C); a.op('CMP', 'imm', 4); a.op('BCC', 'rel', 'done_n')
+    a.op('LDA', 'imm', 0); a.op('STA', 'abs', 0x075C); a.op('INC', 'abs', 0x075F)
+    a.op('LDA', 'abs', 0x075F); a.op('CMP', 'imm', 8); a.op('BCC', 'rel', 'done_n')
+    a.op('LDA', 'imm', 7); a.op('STA', 'abs', 0x075F); a.op('LDA', 'imm', 2); a.op('STA', 'abs', 0x0770)
+    a.label('done_n')
+    a.op('JMP', 'abs', 'done')
+    a.label('dying')
+    a.op('INC', 'zp', DYCNT); a.op('LDA', 'zp', DYCNT); a.op('CMP', 'imm', 30); a.op('BCC', 'rel', 'done')
+    a.op('LDA', 'imm', 0); a.op('STA', 'zp', DYCNT); a.op('LDA', 'imm', 8); a.op('STA', 'zp', 0x0E)
+    a.op('LDA', 'imm', 0); a.op('STA', 'zp', 0x6D); a.op('LDA', 'imm', 40); a.op('STA', 'zp', 0x86)
+    a.op('DEC', 'abs', 0x075A); a.op('BPL', 'rel', 'done')
+    a.op('LDA', 'imm', 3); a.op('STA', 'abs', 0x0770)
+    a.label('done')
+    _nmi_end(a)
+    a.label('irq')
+    a.op('RTI')
+    for name, t in (('t_pal', pal), ('t_nt', nt), ('t_oam', oam), ('t_mix', mix)):
+        a.label(name)
+        a.data(bytes(int(v) for v in t))
+    code = a.assemble()
+    prg = bytearray(16384)
+    prg[:len(code)] = code
+    vec = (a.labels['nmi'], a.labels['reset'], a.labels['irq'])
+    prg[0x3FFA:0x4000] = bytes(sum(((v & 0xFF, v >> 8) for v in vec), ()))
+    chr_ = rng.integers(0, 256, 8192, dtype=np.uint8).tobytes()
+    return ines(bytes(prg), chr_, 0, vertical=True)
 
 
 # ------------------------------------------------------------------------------- SMB RAM trajectories

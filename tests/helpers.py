@@ -15,9 +15,11 @@ REC_BYTES = 23552
 
 # NesRec field offsets (include/nesrec.h)
 OFF = dict(pc=0x00, a=0x02, x=0x03, y=0x04, sp=0x05, p=0x06, irq_line=0x07, cycles=0x08, nmi_pending=0x10, pad=0x11,
-           instr=0x14, frame_dot=0x18, frame=0x1C, v=0x20, t=0x22, ctrl=0x24, mask=0x25, status=0x26, log_n=0x34,
-           log_frame=0x30, ram=0x100, nt=0x900, oam=0x1100, pal=0x1200, log=0x1300, prg_ram=0x1C00, chr_ram=0x3C00,
-           mreg=0x58, prg_off=0x68, chr_off=0x78, nt_map=0x98)
+           shift=0x12, strobe=0x13, instr=0x14, frame_dot=0x18, frame=0x1C, v=0x20, t=0x22, ctrl=0x24, mask=0x25,
+           status=0x26, oam_addr=0x27, fx=0x28, w=0x29, read_buf=0x2A, open_bus=0x2B, s0_dot=0x2C, log_frame=0x30,
+           log_n=0x34, s0_valid=0x36, dmc_byte_end=0x40, dmc_event=0x48, dmc_left=0x50, ram=0x100, nt=0x900,
+           oam=0x1100, pal=0x1200, log=0x1300, prg_ram=0x1C00, chr_ram=0x3C00, mreg=0x58, prg_off=0x68, chr_off=0x78,
+           nt_map=0x98)
 
 _oracle = None
 
@@ -85,6 +87,9 @@ class Console:
         self.rec = np.zeros(REC_BYTES, np.uint8)
         self.lib.orc_power_on(ptr(self.rec), ptr(self.cart))
 
+    def cart_ptr(self):
+        return ptr(self.cart)
+
     def u(self, name, fmt='B'):
         return struct.unpack_from('<' + fmt, self.rec, OFF[name])[0]
 
@@ -107,6 +112,12 @@ class Console:
 
     def write(self, addr, value):
         self.lib.orc_bus_write(ptr(self.rec), ptr(self.cart), addr, value)
+
+    def mem(self, name, n):
+        return self.rec[OFF[name]:OFF[name] + n]
+
+    def words(self, name, n):
+        return self.rec[OFF[name]:OFF[name] + 4 * n].view(np.uint32)
 
     def render_full(self):
         pix = np.zeros((240, 256), np.uint8)

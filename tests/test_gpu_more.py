@@ -1,0 +1,138 @@
+"""More HIP-vs-oracle parity: rewards and restarts, full-size console independence, the GPU extras of the ABI
+(step_range, pack6/unpack6) and the standalone reward10 kernel against the reference's golden fixture."""
+import ctypes
+
+import numpy as np
+import pytest
+import torch
+
+from helpers import GOLDEN, HIP_LIB, ORACLE_LIB, oracle, ptr
+from rl import synth
+from rl.rlenv import RlEnv
+from test_gpu_parity import compare, pair, run
+
+
+def tptr(t):
+    return ctypes.c_void_p(t.data_ptr())
+
+
+@pytest.mark.gpu
+def test_smb_like_rewards_restarts_moves():
+    print('case: SMB-like cart seed 1, 16 consoles, move ids, sticky, dropout, idle 0..6, 40 decisions', flush=True)
+    cpu, gpu = pair(16, synth.smb_like_cart(1), seed=11, sticky=True, idle_max=6, dropout=True)
+    run(cpu, gpu, 40, 3, False)
+
+
+@pytest.mark.gpu
+def test_smb_like_raw_pads_level_end_and_ends():
+    print('case: SMB-like cart seed 2, 24 consoles, raw pads, level end 0, Geometric(1/16) ends, 40 decisions',
+          flush=True)
+    cpu, gpu = pair(24, synth.smb_like_cart(2), seed=12, sticky=True, idle_max=3, dropout=True, pad_mode=True,
+                    end_prob=1 / 16, dropout_gap=0.05)
+    cpu.set_episode_level_end(0)
+    gpu.set_episode_level_end(0)
+    run(cpu, gpu, 40, 4, True)
+
+
+@pytest.mark.gpu
+def test_full_size_console_independence():
+    """8192 consoles; with no per-console randomness (no sticky, dropout, idle or synthetic ends) a console's
+    outputs depend only on its own pad stream, so consoles 0, 4095 and 8191 must equal an oracle run of those
+    streams."""
+    print('case: NROM seed 1, 8192 consoles x 8 decisions, consoles 0/4095/8191 vs oracle', flush=True)
+    cart = synth.nrom_cart(1)
+    kw = dict(seed=1, sticky=False, idle_max=0, dropout=False, pad_mode=True, ram_hash=True, roms={'smb': cart})
+    gpu = RlEnv({'smb': 8192}, device='cuda', lib_path=HIP_LIB, **kw)
+    cpu = RlEnv({'smb': 3}, device='cpu', lib_path=ORACLE_LIB, **kw)
+    pick = torch.tensor([0, 4095, 8191])
+    g = torch.Generator().manual_seed(0)
+    gpu.start()
+    cpu.start()
+    for t in range(8):
+        act = torch.randint(0, 256, (8192,), generator=g, dtype=torch.int16)
+        gpu.actions.copy_(act.cuda())
+        cpu.actions.copy_(act[pick])
+        gpu.step()
+        cpu.step()
+        torch.cuda.synchronize()
+        for k in ('obs', 'emph', 'reward', 'done', 'ram_hash', 'pads'):
+            assert torch.equal(getattr(gpu, k)[pick.cuda()].cpu(), getattr(cpu, k)), (t, k)
+
+
+@pytest.mark.gpu
+def test_step_range_equals_step():
+    print('case: SMB-like cart, 16 consoles, step vs two step_range halves, 12 decisions', flush=True)
+    kw = dict(seed=5, sticky=True, idle_max=2, dropout=True, pad_mode=True, roms={'smb': synth.smb_like_cart(3)})
+    a = RlEnv({'smb': 16}, device='cuda', lib_path=HIP_LIB, **kw)
+    b = RlEnv({'smb': 16}, device='cuda', lib_path=HIP_LIB, **kw)
+    a.start()
+    b.start()
+    g = torch.Generator().manual_seed(1)
+    for t in range(12):
+        act = torch.randint(0, 256, (16,), generator=g, dtype=torch.int16).cuda()
+        a.actions.copy_(act)
+        b.actions.copy_(act)
+        a.step()
+        b.step_range(0, 0, 5, b.obs, b.emph)
+        b.step_range(0, 5, 11, b.obs, b.emph)
+        torch.cuda.synchronize()
+        for k in ('obs', 'emph', 'reward', 'done', 'masks', 'timeline', 'pads', 'events'):
+            assert torch.equal(getattr(a, k), getattr(b, k)), (t, k)
+
+
+@pytest.mark.gpu
+def test_pack6_unpack6_on_device():
+    print('case: pack6/unpack6, 2 x 4 x 224 x 240 frames + odd count', flush=True)
+    lib = ctypes.CDLL(str(HIP_LIB))
+    lib.rl_pack6.argtypes = lib.rl_unpack6.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t,
+                                                       ctypes.c_void_p]
+    g = torch.Generator().manual_seed(0)
+    for n in (2 * 4 * 224 * 240, 4 * 13):
+        px = torch.randint(0, 64, (n,), generator=g, dtype=torch.uint8)
+        d = px.cuda()
+        packed = torch.empty(n // 4 * 3, dtype=torch.uint8, device='cuda')
+        back = torch.empty(n, dtype=torch.uint8, device='cuda')
+        s = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+        assert lib.rl_pack6(tptr(d), tptr(packed), n, s) == 0
+        assert lib.rl_unpack6(tptr(packed), tptr(back), n, s) == 0
+        torch.cuda.synchronize()
+        want = np.zeros(n // 4 * 3, np.uint8)
+        pxn = px.numpy()
+        assert oracle().rl_pack6(ptr(pxn), ptr(want), n, None) == 0
+        assert np.array_equal(packed.cpu().numpy(), want) and torch.equal(back.cpu(), px)
+    assert lib.rl_pack6(tptr(d), tptr(packed), 6, s) != 0
+
+
+@pytest.mark.gpu
+def test_reward10_kernel_matches_reference_fixture_and_oracle():
+    print('case: rl10_smb_run, golden 16 x 1024 and synthetic 512 x 256', flush=True)
+    lib = ctypes.CDLL(str(HIP_LIB))
+    lib.rl10_smb_run.argtypes = [ctypes.c_void_p, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_void_p,
+                                 ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p]
+    s = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    gold = np.load(GOLDEN / 'reward10_smb.npz')
+    traj = torch.from_numpy(gold['traj']).cuda()        # [1024, 16, 16]; the first step covers 8 frames
+    T, N = traj.shape[:2]
+    state = torch.zeros(N * 80, dtype=torch.uint8, device='cuda')
+    rew = torch.zeros(T, N, dtype=torch.float32, device='cuda')
+    done = torch.zeros(T, N, dtype=torch.uint8, device='cuda')
+    assert lib.rl10_smb_run(tptr(traj[:1].contiguous()), 1, N, 8, tptr(state), tptr(rew), tptr(done), s) == 0
+    assert lib.rl10_smb_run(tptr(traj[1:].contiguous()), T - 1, N, 4, tptr(state), tptr(rew[1:]), tptr(done[1:]),
+                            s) == 0
+    torch.cuda.synchronize()
+    assert np.array_equal(rew.cpu().numpy(), gold['reward'].astype(np.float32))
+    assert np.array_equal(done.cpu().numpy(), gold['done'])
+    ram = synth.smb_ram15(21, 512, 256)
+    T, N = ram.shape[:2]
+    want_r = np.zeros((T, N), np.float32)
+    want_d = np.zeros((T, N), np.uint8)
+    st = np.zeros(N * 80, np.uint8)
+    assert oracle().rl10_smb_run(ptr(ram), T, N, 4, ptr(st), ptr(want_r), ptr(want_d), None) == 0
+    d_ram = torch.from_numpy(ram).cuda()
+    state = torch.zeros(N * 80, dtype=torch.uint8, device='cuda')
+    rew = torch.zeros(T, N, dtype=torch.float32, device='cuda')
+    done = torch.zeros(T, N, dtype=torch.uint8, device='cuda')
+    assert lib.rl10_smb_run(tptr(d_ram), T, N, 4, tptr(state), tptr(rew), tptr(done), s) == 0
+    torch.cuda.synchronize()
+    assert np.array_equal(rew.cpu().numpy(), want_r) and np.array_equal(done.cpu().numpy(), want_d)
+    assert np.array_equal(state.cpu().numpy(), st)

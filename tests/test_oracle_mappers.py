@@ -1,0 +1,259 @@
+"""Known-answer tests of the oracle's cartridge boards (NROM, MMC1, MMC3) and its DMC.
+
+MMC3: restates the reference's register case third_party/nesle-extensions.patch:4638-4673 (R0-R7 = 00 3A 4A 5D 6E 61
+0A 04, bank select $46, $A000 = 1 on 128 KB PRG / 128 KB CHR) by writing the registers through the CPU bus, plus
+the scanline counter (reload, count down once per rendered line at dot 266, IRQ at zero, $E000 acknowledge).
+MMC1: the serial port and the bank modes written from the board's documented register meanings (16 KB PRG banks,
+4 KB CHR banks), not from the oracle's page arithmetic.
+DMC: restates the sample-channel cases of patch:4105-4205 (status bit 4, 4-cycle fetch steals, loop, rate change,
+no steal in the idle fast-forward) with the same 4-cycle instruction driver as the reference test.
+"""
+import numpy as np
+import pytest
+
+from helpers import Console
+from rl import synth
+
+KB = 1024
+
+
+def cart(mapper, prg_kb, chr_kb, vertical=True):
+    prg = bytearray(prg_kb * KB)
+    for i in range(0, len(prg), 8 * KB):                 # tag every 8 KB page with its number
+        prg[i] = i // (8 * KB)
+    last = len(prg) - 8 * KB
+    prg[last + 0x10:last + 0x14] = bytes((0xEA, 0x4C, 0x10, 0xE0))  # $E010: NOP; JMP $E010
+    prg[-6:] = bytes((0x10, 0xE0, 0x10, 0xE0, 0x10, 0xE0))
+    return synth.ines(bytes(prg), bytes(chr_kb * KB), mapper, vertical=vertical)
+
+
+def pages(con):
+    return ([int(x) // (8 * KB) for x in con.words('prg_off', 4)], [int(x) // KB for x in con.words('chr_off', 8)],
+            [int(x) for x in con.mem('nt_map', 4)])
+
+
+# ----------------------------------------------------------------------------------------------- NROM
+
+def test_nrom_128_is_mirrored_and_header_mirroring():
+    con = Console(cart(0, 16, 8, vertical=False))
+    prg, chr_, nt = pages(con)
+    assert [con.read(a) for a in (0x8000, 0xA000, 0xC000, 0xE000)] == [0, 1, 0, 1]
+    assert chr_ == list(range(8)) and nt == [0, 0, 1, 1]
+    assert pages(Console(cart(0, 32, 8)))[2] == [0, 1, 0, 1]
+
+
+# ----------------------------------------------------------------------------------------------- MMC3
+
+def mmc3_write_regs(con, regs, select, mirror):
+    for r, v in enumerate(regs):
+        con.write(0x8000, r)
+        con.write(0x8001, v)
+    con.write(0x8000, select)
+    con.write(0xA000, mirror)
+
+
+def test_mmc3_register_case_of_the_reference():
+    con = Console(cart(4, 128, 128))
+    mmc3_write_regs(con, (0, 0x3A, 0x4A, 0x5D, 0x6E, 0x61, 0x0A, 0x04), 0x46, 1)
+    prg, chr_, nt = pages(con)
+    # PRG mode 1: R6 at $C000, the second-last page at $8000, R7 at $A000, the last page fixed at $E000
+    assert prg == [0x7E & 15, 0x04, 0x0A, 15]
+    assert [con.read(a) for a in (0x8000, 0xA000, 0xC000)] == [14, 4, 10]
+    # no CHR inversion: R0/R1 as 2 KB banks at $0000/$0800, R2-R5 as 1 KB banks at $1000-$1C00
+    assert chr_[2:4] == [0x3A, 0x3B] and chr_[4] == 0x4A and chr_[7] == 0x61 and chr_[0:2] == [0, 1]
+    assert nt == [0, 0, 1, 1]                            # $A000 bit 0 = 1: horizontal
+
+
+def test_mmc3_chr_inversion_and_prg_mode0():
+    con = Console(cart(4, 256, 128))
+    mmc3_write_regs(con, (0x10, 0x21, 0x30, 0x31, 0x32, 0x33, 0x05, 0x06), 0x80, 0)
+    prg, chr_, nt = pages(con)
+    assert prg == [5, 6, 30, 31]
+    assert chr_ == [0x30, 0x31, 0x32, 0x33, 0x10, 0x11, 0x20, 0x21] and nt == [0, 1, 0, 1]
+
+
+def test_mmc3_scanline_irq():
+    con = Console(cart(4, 128, 128))
+    con.write(0xC000, 3)                                 # latch 3
+    con.write(0xC001, 0)                                 # reload at the next clock
+    con.write(0xE001, 0)                                 # enable
+    con.write(0x2001, 0x18)                              # rendering on: clocks at dot 266 of lines 0-239
+    con.set('p', 0x24)                                   # I set: the line stays asserted
+    while con.u('frame_dot', 'I') < 3 * 341 + 266:
+        assert con.u('irq_line') == 0
+        con.step()
+    assert con.u('irq_line') == 1                        # clock 1 reloads 3, clocks 2-4 count 2, 1, 0
+    assert con.u('frame_dot', 'I') < 3 * 341 + 266 + 20
+    con.write(0xE000, 0)                                 # acknowledge and disable
+    assert con.u('irq_line') == 0
+
+
+# ----------------------------------------------------------------------------------------------- MMC1
+
+def mmc1_write(con, addr, value):
+    for i in range(5):
+        con.write(addr, (value >> i) & 1)
+
+
+def mmc1_model(control, chr0, chr1, prg, banks16):
+    """Board documentation: PRG 16 KB banks by mode, CHR 4 KB banks (8 KB mode ignores bit 0 of CHR0)."""
+    mode = (control >> 2) & 3
+    b = prg & 15
+    if mode in (0, 1):
+        lo, hi = b & ~1, (b & ~1) + 1
+    elif mode == 2:
+        lo, hi = 0, b
+    else:
+        lo, hi = b, banks16 - 1
+    prg8 = [2 * lo, 2 * lo + 1, 2 * hi, 2 * hi + 1]
+    if control & 0x10:
+        c4 = [chr0, chr1]
+    else:
+        c4 = [chr0 & ~1, (chr0 & ~1) + 1]
+    chr1k = [4 * c4[0] + i for i in range(4)] + [4 * c4[1] + i for i in range(4)]
+    nt = {0: [0, 0, 0, 0], 1: [1, 1, 1, 1], 2: [0, 1, 0, 1], 3: [0, 0, 1, 1]}[control & 3]
+    return prg8, chr1k, nt
+
+
+@pytest.mark.parametrize('control', [0x00, 0x05, 0x0A, 0x0F, 0x12, 0x1C, 0x1F])
+def test_mmc1_modes(control):
+    con = Console(cart(1, 128, 128))
+    mmc1_write(con, 0x8000, control)
+    mmc1_write(con, 0xA000, 0x09)
+    mmc1_write(con, 0xC000, 0x16)
+    mmc1_write(con, 0xE000, 0x05)
+    prg8, chr1k, nt = mmc1_model(control, 0x09, 0x16, 0x05, 8)
+    got = pages(con)
+    assert got[0] == [p % 16 for p in prg8] and got[1] == [c % 128 for c in chr1k] and got[2] == nt
+
+
+def test_mmc1_reset_bit_and_power_on():
+    con = Console(cart(1, 128, 128))
+    assert pages(con)[0][2:] == [14, 15]                 # power-on: last 16 KB fixed at $C000
+    con.write(0x8000, 1)
+    con.write(0x8000, 1)
+    con.write(0x8000, 0x80)                              # reset: shift cleared, PRG mode 3
+    mmc1_write(con, 0xE000, 0x02)
+    assert pages(con)[0] == [4, 5, 14, 15]
+
+
+def test_mmc1_prg_ram_enable():
+    con = Console(cart(1, 128, 128))
+    con.write(0x6000, 0x5A)
+    assert con.read(0x6000) == 0x5A
+    mmc1_write(con, 0xE000, 0x10)                        # bit 4 disables PRG RAM
+    con.write(0x6000, 0x11)
+    assert con.read(0x6000) != 0x11
+    mmc1_write(con, 0xE000, 0x00)
+    assert con.read(0x6000) == 0x5A
+
+
+# ------------------------------------------------------------------------------------------------ DMC
+
+KBYTE = 8 * 54                                           # rate 15: 54 CPU cycles per bit
+
+
+class Dmc:
+    """The reference test's driver: 4-cycle instructions, the DMC serviced after each one."""
+
+    def __init__(self):
+        self.con = Console(cart(0, 16, 8))
+        self.now = 1000
+        self.stolen = 0
+        self.con.lib.orc_dmc_reset(self.con.rec.ctypes.data, self.now)
+
+    def write(self, a, v):
+        self.con.write(a, v)
+
+    def status(self):
+        return self.con.read(0x4015)
+
+    def event(self):
+        return self.con.u('dmc_event', 'Q')
+
+    def service(self, now, steal):
+        return self.con.lib.orc_dmc_service(self.con.rec.ctypes.data, now, steal)
+
+    def run(self, cycles):
+        end = self.now + cycles
+        while self.now < end:
+            self.now += 4
+            if self.now >= self.event():
+                s = self.service(self.now, 1)
+                self.now += s
+                self.stolen += s
+
+
+def test_dmc_power_on_is_silent():
+    m = Dmc()
+    assert m.status() == 0
+    m.run(100 * KBYTE)
+    assert m.stolen == 0 and m.event() == 2 ** 64 - 1
+
+
+def test_dmc_seventeen_byte_sample():
+    m = Dmc()
+    m.run(3 * KBYTE + 100)
+    m.write(0x4010, 0x0F)
+    m.write(0x4013, 0x01)
+    m.write(0x4015, 0x1F)
+    assert m.status() == 0x10
+    m.run(4)
+    assert m.stolen == 4
+    m.run(15 * KBYTE - 2 * 4)
+    assert m.status() == 0x10
+    m.run(2 * KBYTE)
+    assert m.status() == 0x00 and m.stolen == 17 * 4
+    m.run(10 * KBYTE)
+    assert m.stolen == 17 * 4
+    m.write(0x4015, 0x10)
+    assert m.status() == 0x10
+
+
+def test_dmc_restart_while_playing_and_stop():
+    m = Dmc()
+    m.write(0x4010, 0x0F)
+    m.write(0x4013, 0x01)
+    m.write(0x4015, 0x10)
+    m.run(4 * KBYTE)
+    assert 4 <= m.stolen // 4 <= 5
+    m.write(0x4015, 0x10)
+    m.run(4 * KBYTE)
+    assert 8 <= m.stolen // 4 <= 9
+    m.write(0x4015, 0x00)
+    assert m.status() == 0
+    before = m.stolen
+    m.run(4 * KBYTE)
+    assert m.stolen == before
+
+
+def test_dmc_loop():
+    m = Dmc()
+    m.write(0x4010, 0x4F)
+    m.write(0x4013, 0x00)
+    m.write(0x4015, 0x10)
+    m.run(100 * KBYTE)
+    assert m.status() == 0x10 and 100 * 4 <= m.stolen <= 101 * 4
+
+
+def test_dmc_rate_change_from_the_next_bit_clock():
+    m = Dmc()
+    m.write(0x4010, 0x4F)
+    m.write(0x4015, 0x10)
+    m.run(10 * KBYTE)
+    m.write(0x4010, 0x40)
+    m.run(8 * 428)
+    before = m.stolen
+    m.run(20 * 8 * 428)
+    assert 19 * 4 <= m.stolen - before <= 21 * 4
+
+
+def test_dmc_fast_forward_steals_nothing():
+    m = Dmc()
+    m.write(0x4010, 0x0F)
+    m.write(0x4013, 0x01)
+    m.write(0x4015, 0x10)
+    start = m.now
+    assert m.service(start, 0) == 0
+    assert m.service(start + 10 * KBYTE, 0) == 0 and m.status() == 0x10
+    assert m.service(start + 17 * KBYTE, 0) == 0 and m.status() == 0x00
