@@ -43,7 +43,8 @@ METRIC = 'emulated NES frames/sec and decisions/sec at 8192 consoles, 1 MI355X'
 ORACLE_LIB = ROOT / 'oracle' / '_build' / 'liboracle_rlenv.so'
 TRAFFIC = ROOT / 'profiles' / 'traffic.json'
 HBM_PEAK_GBPS = 8000.0
-KERNELS = ('k_emu', 'k_render', 'k_finish', 'k_reset_copy', 'k_emu_restart', 'k_render_restart', 'k_reset_finish')
+KERNELS = ('k_emu', 'k_render', 'k_finish', 'k_reset_copy', 'k_emu_restart', 'k_render_restart', 'k_reset_finish',
+           'k_decision')
 
 # Algorithmic bytes per console per launch (outputs written + inputs read by the path, not state traffic).
 PICTURE_BYTES = 224 * 240 + 224            # one frame's colour indices + emphasis
@@ -57,6 +58,7 @@ ALG_BYTES = {
     'k_reset_finish': 19 + 360,             # masks, timeline
 }
 DECISION_BYTES = 4 * (PICTURE_BYTES + 1) + 2 + 4 + 1 + 4 + 28 + 19 + 360   # 216,358 B per console per decision
+ALG_BYTES['k_decision'] = DECISION_BYTES + 8                          # the fused decision, RAM hash included
 
 
 def parse():

@@ -97,7 +97,8 @@ __device__ __forceinline__ int slot_env(const GameK& g, int use_list, int e0, in
 }
 
 // Per-frame pad byte of a decision frame (rl/csrc/rlenv_core.cuh:181-191): sticky repeat, dropout, turbo phase.
-__device__ __forceinline__ uint32_t decision_pad(const EmuArgs& a, int ge, int f) {
+template <class Args>
+__device__ __forceinline__ uint32_t decision_pad(const Args& a, int ge, int f) {
     const int d = ev::dropped_now(&a.e.drop[ge]);
     uint64_t ctr = a.e.sticky_ctr[ge];
     const uint64_t seed = a.e.sticky_seed[ge];
@@ -268,29 +269,17 @@ struct RenderArgs {
     int f, use_list, restart_pass, e0, e1;
 };
 
-// One console-frame per wavefront (blockDim 64): replay the frame log line by line (wave-uniform), each lane
-// composes 4 pixels of the 256-pixel line; rows 8..231, columns 8..247 go out as one 240-byte store per line.
-__global__ __launch_bounds__(64) void k_render(RenderArgs a) {
-    __shared__ __align__(16) uint8_t nt_s[2048];
-    __shared__ __align__(16) uint8_t oam_s[256];
-    __shared__ __align__(16) uint8_t pal_s[32];
-    const int count = slot_count(a.g, a.use_list, a.e0, a.e1);
-    const int k = (int)blockIdx.x;
-    if (k >= count) return;
-    const int e = slot_env(a.g, a.use_list, a.e0, k);
-    const int ge = a.g.offset + e;
-    if (a.restart_pass && a.e.resetting[ge] == 0) return;
-    if (a.s.no_render) return;
-    const int lane = (int)threadIdx.x;
-    const NesRec* rec = &a.g.recs[e];
-    for (int w = lane; w < 512; w += 64) reinterpret_cast<uint32_t*>(nt_s)[w] = reinterpret_cast<const uint32_t*>(rec->nt)[w];
-    reinterpret_cast<uint32_t*>(oam_s)[lane] = reinterpret_cast<const uint32_t*>(rec->oam)[lane];
-    Replay s;
-    rp_begin(s, rec->log, rec->log_n, pal_s);
+// The picture of the frame a console has logged, drawn by one wavefront: the frame log is replayed line by line
+// (wave-uniform state), each lane composes 4 pixels of the 256-pixel line, the sprites of a line are picked with
+// one ballot over the 64 OAM entries, and lines 8..231, columns 8..247 go out as one 240-byte row store each
+// (rl/csrc/nes_machine.cuh:133-155). nt/oam: the console's nametables and OAM as of the frame's vblank (LDS);
+// pal: 32 bytes of LDS for the replayed palette.
+__device__ __forceinline__ void render_wave(const NesRec* rec, uint32_t log_n, const uint8_t* nt_s, const uint8_t* oam_s,
+                                            uint8_t* pal_s, const Cart& cart, uint8_t* obs, uint8_t* emph, int lane) {
+    Replay s;   // wave-uniform: every lane replays the same log (and stores the same palette bytes)
+    rp_begin(s, rec->log, log_n, pal_s);
     __syncthreads();
-    const Mem m = mem_of(const_cast<NesRec*>(rec), nullptr, a.g.cart);
-    uint8_t* obs = a.o.obs + ((size_t)ge * RLE_FRAMES + a.f) * RLE_OBS_PIXELS;
-    uint8_t* emph = a.o.emph + ((size_t)ge * RLE_FRAMES + a.f) * RLE_OBS_H;
+    const Mem m = mem_of(const_cast<NesRec*>(rec), nullptr, cart);
     const uint32_t my_sy = oam_s[4 * lane];
     for (int l = 0; l < 232; ++l) {
         if (l >= 8) {
@@ -369,6 +358,27 @@ __global__ __launch_bounds__(64) void k_render(RenderArgs a) {
     }
 }
 
+// One console-frame per wavefront (blockDim 64).
+__global__ __launch_bounds__(64) void k_render(RenderArgs a) {
+    __shared__ __align__(16) uint8_t nt_s[2048];
+    __shared__ __align__(16) uint8_t oam_s[256];
+    __shared__ __align__(16) uint8_t pal_s[32];
+    const int count = slot_count(a.g, a.use_list, a.e0, a.e1);
+    const int k = (int)blockIdx.x;
+    if (k >= count) return;
+    const int e = slot_env(a.g, a.use_list, a.e0, k);
+    const int ge = a.g.offset + e;
+    if (a.restart_pass && a.e.resetting[ge] == 0) return;
+    if (a.s.no_render) return;
+    const int lane = (int)threadIdx.x;
+    const NesRec* rec = &a.g.recs[e];
+    for (int w = lane; w < 512; w += 64) reinterpret_cast<uint32_t*>(nt_s)[w] = reinterpret_cast<const uint32_t*>(rec->nt)[w];
+    reinterpret_cast<uint32_t*>(oam_s)[lane] = reinterpret_cast<const uint32_t*>(rec->oam)[lane];
+    uint8_t* obs = a.o.obs + ((size_t)ge * RLE_FRAMES + a.f) * RLE_OBS_PIXELS;
+    uint8_t* emph = a.o.emph + ((size_t)ge * RLE_FRAMES + a.f) * RLE_OBS_H;
+    render_wave(rec, rec->log_n, nt_s, oam_s, pal_s, a.g.cart, obs, emph, lane);
+}
+
 // ----------------------------------------------------------------------------------------- finish
 struct FinishArgs {
     GameK g;
@@ -378,7 +388,7 @@ struct FinishArgs {
     int e0, e1;
 };
 
-__device__ uint64_t ram_hash(const uint8_t* ram) {
+__device__ __forceinline__ uint64_t ram_hash(const uint8_t* ram) {
     const uint4* w = reinterpret_cast<const uint4*>(ram);
     uint64_t h = 0;
     for (uint32_t k = 0; k < 128u; ++k) {
@@ -392,7 +402,7 @@ __device__ uint64_t ram_hash(const uint8_t* ram) {
 }
 
 // RL part of the restart (rl/csrc/rlenv_core.cuh:208-263 without the record copy, which k_reset_copy does).
-__device__ void reset_rl(const GameK& g, const EnvArrays& e, const Settings& s, int ge) {
+__device__ __forceinline__ void reset_rl(const GameK& g, const EnvArrays& e, const Settings& s, int ge) {
     const uint32_t ep = ++e.episode[ge];
     const uint64_t seed = ev::ep_seed(s.run_seed, (uint32_t)ge, ep);
     const uint64_t sseed = ev::mix64(seed ^ 0x5717C4A55EEDull);
@@ -550,6 +560,220 @@ __global__ void k_list_clear(uint32_t* count) {
     if (threadIdx.x == 0 && blockIdx.x == 0) *count = 0;
 }
 
+#ifdef RLENV_FUSED_KERNEL
+// ------------------------------------------------------------------------------------- fused decision
+// k_decision: one wavefront owns one console for a whole decision (or a start). Lane 0 runs the emulator on the
+// scalar unit and the RL bookkeeping; all 64 lanes move the console between HBM and LDS, draw each frame, hash
+// the RAM and copy the boot snapshot on a restart. The phase order per console is the reference's
+// (rl/csrc/rlenv_core.cuh:389-414): 4 x (frame, render), finish, [restart: snapshot, 4 x (neutral frame, render),
+// first tracker update], masks + timeline. Every phase is a function of the console's own state, so running them
+// console by console equals running each phase over all consoles.
+enum : int { DEC_STEP = 0, DEC_START = 1 };
+
+struct DecArgs {
+    GameK g;
+    EnvArrays e;
+    Outs o;
+    Settings s;
+    int mode, e0, e1;
+    uint32_t budget;
+};
+
+// RAM hash by the 64 lanes: lane l hashes words 8l..8l+7, then a butterfly sum (integer addition mod 2^64, so the
+// order does not change the result).
+__device__ __forceinline__ uint64_t ram_hash_wave(const uint8_t* ram, int lane) {
+    const uint4* w = reinterpret_cast<const uint4*>(ram) + 2 * lane;
+    uint64_t h = 0;
+    for (int j = 0; j < 2; ++j) {
+        const uint4 q = w[j];
+        const uint64_t k = 8u * (uint32_t)lane + 4u * (uint32_t)j;
+        h += ev::mix64((k << 32) | q.x);
+        h += ev::mix64(((k + 1u) << 32) | q.y);
+        h += ev::mix64(((k + 2u) << 32) | q.z);
+        h += ev::mix64(((k + 3u) << 32) | q.w);
+    }
+    for (int off = 32; off > 0; off >>= 1) {
+        const uint32_t lo = __shfl_xor((uint32_t)h, off), hi = __shfl_xor((uint32_t)(h >> 32), off);
+        h += ((uint64_t)hi << 32) | lo;
+    }
+    return h;
+}
+
+// Console record (HBM) -> LDS memories, and the console state for lane 0.
+__device__ __forceinline__ void console_in(WaveLds& L, const NesRec* rec, int lane) {
+    wave_copy16(L.ram, rec->ram, NES_RAM_BYTES, lane);
+    wave_copy16(L.nt, rec->nt, NES_NT_BYTES, lane);
+    wave_copy16(L.oam, rec->oam, NES_OAM_BYTES, lane);
+    wave_copy16(L.pal, rec->pal, NES_PAL_BYTES, lane);
+    if (lane == 0) con_load(L.cs, rec);
+}
+
+__device__ __forceinline__ void console_out(WaveLds& L, NesRec* rec, int lane) {
+    if (lane == 0) con_store(L.cs, rec);
+    wave_copy16(rec->ram, L.ram, NES_RAM_BYTES, lane);
+    wave_copy16(rec->nt, L.nt, NES_NT_BYTES, lane);
+    wave_copy16(rec->oam, L.oam, NES_OAM_BYTES, lane);
+    wave_copy16(rec->pal, L.pal, NES_PAL_BYTES, lane);
+}
+
+// One emulated frame of the console in LDS (lane 0): the env's frame step (rl/csrc/rlenv_core.cuh:160-177).
+template <uint32_t B>
+__device__ __forceinline__ void frame_lane0(const DecArgs& a, WaveLds& L, const Mem& m, int ge, uint32_t pad) {
+    const uint64_t target = a.e.target[ge];
+    L.cs.pad = pad;
+    if (a.e.fault[ge] == 0) {
+        const uint32_t f = run_until_wave<B>(L.cs, m, c_optab.t, target, a.budget);
+        if (f != 0) a.e.fault[ge] = f;
+    }
+    a.e.target[ge] = target + NES_FRAME_DOTS;
+    a.e.ep_frame[ge] += 1u;
+}
+
+// Finish of the decision (lane 0): rl/csrc/rlenv_core.cuh:266-309. Returns whether the episode ended (then the RL
+// state is already reset for the next one).
+__device__ __forceinline__ bool finish_lane0(const DecArgs& a, const WaveLds& L, int ge) {
+    uint8_t b15[15];
+    ev::smb_gather(L.ram, b15);
+    const Rl10Signals sig = ev::smb_signals(b15);
+    Rl10State st = a.e.st[ge];
+    const ev::Out u = ev::smb_update(sig, RLE_FRAMES, st);
+    a.e.st[ge] = st;
+    const bool faulted = a.e.fault[ge] != 0;
+    const bool level_clear = !u.done && !faulted && a.s.episode_level_end >= 0 && (u.events & ev::EV_LEVEL) &&
+                             u.event_level == a.s.episode_level_end + 1;
+    bool synthetic = false;
+    if (a.s.end_p32 != 0 && !u.done && !faulted && !level_clear) {
+        uint64_t ctr = (uint64_t)(uint32_t)a.e.ep_len[ge];
+        const uint64_t es = ev::mix64(ev::ep_seed(a.s.run_seed, (uint32_t)ge, a.e.episode[ge]) ^ 0xE9D5EEDull);
+        synthetic = ev::rnd32(es, ctr) < a.s.end_p32;
+    }
+    const bool done = u.done || faulted || level_clear || synthetic;
+    const float r = faulted ? 0.0f : (float)u.reward;
+    a.o.reward[ge] = r;
+    if (a.o.parts)
+        for (int q = 0; q < RLE_PARTS; ++q) a.o.parts[(size_t)ge * RLE_PARTS + q] = faulted ? 0.0f : (float)u.part[q];
+    a.o.done[ge] = done ? 1 : 0;
+    a.o.events[ge] = u.events;
+    const float ret = a.e.ep_ret[ge] + r;
+    a.e.ep_ret[ge] = ret;
+    const int32_t len = a.e.ep_len[ge] + 1;
+    a.e.ep_len[ge] = len;
+    if (u.event_level > a.e.ep_maxlvl[ge]) a.e.ep_maxlvl[ge] = u.event_level;
+    Dropout d = a.e.drop[ge];
+    ev::drop_advance(d, a.s.dropout != 0, a.s.gap_p32);
+    a.e.drop[ge] = d;
+    if (done) {
+        float* inf = a.o.info + (size_t)ge * RLE_INFO;
+        inf[0] = ret;
+        inf[1] = (float)len;
+        inf[2] = (float)(faulted ? RLE_END_FAULT : level_clear ? RLE_END_LEVEL_CLEAR
+                                                               : synthetic ? RLE_END_SYNTHETIC : st.end_reason);
+        inf[3] = (float)st.deaths;
+        inf[4] = (float)a.e.ep_maxlvl[ge];
+        inf[5] = st.overflow ? 1.0f : 0.0f;
+        inf[6] = (float)a.e.ep_idle[ge];
+        inf[7] = (float)a.e.episode[ge];
+        reset_rl(a.g, a.e, a.s, ge);
+    }
+    return done;
+}
+
+// First tracker update of a new episode, then masks and timeline (lane 0): rl/csrc/rlenv_core.cuh:138-148, 327-342.
+__device__ __forceinline__ void controls_lane0(const DecArgs& a, const WaveLds& L, int ge) {
+    if (a.e.resetting[ge]) {
+        uint8_t b15[15];
+        ev::smb_gather(L.ram, b15);
+        Rl10State st = a.e.st[ge];
+        (void)ev::smb_update(ev::smb_signals(b15), a.e.ep_idle[ge] + RLE_FRAMES, st);
+        a.e.st[ge] = st;
+        a.e.ep_ret[ge] = 0.0f;
+        a.e.ep_len[ge] = 0;
+        a.e.ep_maxlvl[ge] = 0;
+        a.e.resetting[ge] = 0;
+    }
+    const Dropout* d = &a.e.drop[ge];
+    const int dr = ev::dropped_now(d);
+    uint8_t* mk = a.o.masks + (size_t)ge * RLE_MASK_BYTES;
+    for (uint32_t i = 0; i < 9; ++i) mk[i] = (dr >= 0 && dr < 4 && (ev::dpad_bits(i) & (ev::B_UP << dr))) ? 0 : 1;
+    mk[9] = 1;
+    mk[10] = dr == 4 ? 0 : 1;
+    mk[11] = dr == 6 ? 0 : 1;
+    mk[12] = 1;
+    mk[13] = dr == 5 ? 0 : 1;
+    mk[14] = dr == 7 ? 0 : 1;
+    mk[15] = 1;
+    mk[16] = a.g.start_ok ? 1 : 0;
+    mk[17] = 1;
+    mk[18] = a.g.select_ok ? 1 : 0;
+    uint32_t* tl = reinterpret_cast<uint32_t*>(a.o.tl + (size_t)ge * RLE_TIMELINE_BYTES);
+    for (int i = 0; i < RLE_TIMELINE_BYTES / 4; ++i) tl[i] = 0;
+    uint8_t* tb = a.o.tl + (size_t)ge * RLE_TIMELINE_BYTES;
+    for (uint32_t j = 0; j < RLE_TIMELINE; ++j) {
+        const int b = d->ring[(d->head + j) & (RLC_RING - 1)];
+        if (b >= 0) tb[b * RLE_TIMELINE + j] = 1;
+    }
+}
+
+template <uint32_t B>
+__global__ __launch_bounds__(64) void k_decision(DecArgs a) {
+    __shared__ __align__(16) WaveLds L;
+    __shared__ __align__(16) uint8_t pal_r[32];
+    __shared__ int restart_s;
+    const int e = a.e0 + (int)blockIdx.x;
+    if (e >= a.e1) return;
+    const int lane = (int)threadIdx.x;
+    const int ge = a.g.offset + e;
+    NesRec* rec = &a.g.recs[e];
+    const Mem m{rec, L.ram, L.nt, L.oam, L.pal, a.g.cart};
+    const bool render = a.s.no_render == 0;
+    if (a.mode == DEC_STEP) {
+        console_in(L, rec, lane);
+        __syncthreads();
+        for (int f = 0; f < RLE_FRAMES; ++f) {
+            if (lane == 0) frame_lane0<B>(a, L, m, ge, decision_pad(a, ge, f));
+            __syncthreads();
+            if (render)
+                render_wave(rec, L.cs.log_n, L.nt, L.oam, pal_r, a.g.cart,
+                            a.o.obs + ((size_t)ge * RLE_FRAMES + f) * RLE_OBS_PIXELS,
+                            a.o.emph + ((size_t)ge * RLE_FRAMES + f) * RLE_OBS_H, lane);
+        }
+        if (a.o.ram_hash) {
+            const uint64_t h = ram_hash_wave(L.ram, lane);
+            if (lane == 0) a.o.ram_hash[ge] = h;
+        }
+        if (lane == 0) restart_s = finish_lane0(a, L, ge) ? 1 : 0;
+    } else {
+        if (lane == 0) {
+            reset_rl(a.g, a.e, a.s, ge);
+            restart_s = 1;
+        }
+    }
+    __syncthreads();
+    if (restart_s) {
+        const int idle = a.e.ep_idle[ge];
+        const int t = idle <= a.s.idle_tmpl ? idle : 0;
+        const NesRec* src = t == 0 ? &a.g.recs[a.g.n] : &a.g.idle[t - 1];
+        __syncthreads();
+        wave_copy16(rec, src, NES_REC_BYTES, lane);
+        __syncthreads();
+        console_in(L, rec, lane);
+        __syncthreads();
+        for (int f = 0; f < RLE_FRAMES; ++f) {
+            if (lane == 0) frame_lane0<B>(a, L, m, ge, 0u);
+            __syncthreads();
+            if (render)
+                render_wave(rec, L.cs.log_n, L.nt, L.oam, pal_r, a.g.cart,
+                            a.o.obs + ((size_t)ge * RLE_FRAMES + f) * RLE_OBS_PIXELS,
+                            a.o.emph + ((size_t)ge * RLE_FRAMES + f) * RLE_OBS_H, lane);
+        }
+    }
+    if (lane == 0) controls_lane0(a, L, ge);
+    __syncthreads();
+    console_out(L, rec, lane);
+}
+
+#endif  // RLENV_FUSED_KERNEL
+
 // ------------------------------------------------------------------------------------- codec, gathers
 // pack6: 4 colour indices (6 bits) -> 3 bytes, little-endian v = p0 | p1 << 6 | p2 << 12 | p3 << 18
 // (rl/csrc/rlenv.cu:127-134). Each thread packs 16 pixels: one 16-byte load, one 12-byte store.
@@ -656,7 +880,8 @@ struct GameH {
 
 // Kernel classes of a decision, for the per-kernel clock (rlenv_kernel_times).
 enum KClass : int {
-    KC_EMU = 0, KC_RENDER, KC_FINISH, KC_RESET_COPY, KC_EMU_RESTART, KC_RENDER_RESTART, KC_RESET_FINISH, KC_COUNT
+    KC_EMU = 0, KC_RENDER, KC_FINISH, KC_RESET_COPY, KC_EMU_RESTART, KC_RENDER_RESTART, KC_RESET_FINISH, KC_DECISION,
+    KC_COUNT
 };
 
 // Optional per-launch HIP-event clock: when on, every launch of a decision is bracketed by two events on its
@@ -722,6 +947,8 @@ struct Env {
     uint32_t* optab = nullptr;
     int cpw = 16;
     bool emu_wave = true;    // k_emu_w (one console per wavefront); RLENV_EMU=lane selects k_emu
+    bool fused = false;      // per-phase kernels; RLENV_FUSED=1 selects one k_decision launch per decision (a build
+                             // with -DRLENV_FUSED_KERNEL)
     uint32_t budget = NES_BUDGET;
     mutable KernelClock clock;
 };
@@ -829,9 +1056,29 @@ void restart_phases(const Env& env, const GameK& g, const Outs& o, int e0, int e
     trace("reset_finish", st);
 }
 
+#ifdef RLENV_FUSED_KERNEL
+void launch_decision(const Env& env, const GameK& g, const Outs& o, int mode, int e0, int e1, hipStream_t st) {
+    const DecArgs a{g, env.e, o, env.s, mode, e0, e1, env.budget};
+    const int n = e1 - e0;
+    if (n <= 0) return;
+    env.clock.run(KC_DECISION, st, [&] {
+        if (g.cart.board == NES_BOARD_MMC3) hipLaunchKernelGGL(k_decision<NES_BOARD_MMC3>, dim3(n), dim3(64), 0, st, a);
+        else if (g.cart.board == NES_BOARD_MMC1) hipLaunchKernelGGL(k_decision<NES_BOARD_MMC1>, dim3(n), dim3(64), 0, st, a);
+        else hipLaunchKernelGGL(k_decision<NES_BOARD_NROM>, dim3(n), dim3(64), 0, st, a);
+    });
+    trace(mode == DEC_STEP ? "decision" : "decision_start", st);
+}
+#endif
+
 void decision_phases(const Env& env, const GameK& g, const Outs& o, int e0, int e1, hipStream_t st) {
     const int n = e1 - e0;
     if (n <= 0) return;
+#ifdef RLENV_FUSED_KERNEL
+    if (env.fused) {
+        launch_decision(env, g, o, DEC_STEP, e0, e1, st);
+        return;
+    }
+#endif
     for (int f = 0; f < RLE_FRAMES; ++f) {
         launch_emu(env, g, o, EMU_DECISION, f, false, e0, e1, st);
         launch_render(env, g, o, f, false, false, e0, e1, st);
@@ -897,6 +1144,7 @@ void* rlenv_create(int ngames, const int* game_ids, const uint8_t* const* roms, 
         env->device = device;
         if (const char* v = std::getenv("RLENV_CPW")) env->cpw = std::max(1, std::min(64, std::atoi(v)));
         if (const char* v = std::getenv("RLENV_EMU")) env->emu_wave = std::strcmp(v, "lane") != 0;
+        if (const char* v = std::getenv("RLENV_FUSED")) env->fused = std::strcmp(v, "1") == 0;
         if (const char* v = std::getenv("RLENV_BUDGET")) env->budget = (uint32_t)std::max(1, std::min((int)NES_BUDGET, std::atoi(v)));
         if (hipFuncSetAttribute(reinterpret_cast<const void*>(k_emu), hipFuncAttributeMaxDynamicSharedMemorySize,
                                 (int)(1024u + 64u * kRamStride)) != hipSuccess)
@@ -1005,6 +1253,12 @@ int rlenv_start(void* h, void* stream) {
     Env& env = *static_cast<Env*>(h);
     const hipStream_t st = static_cast<hipStream_t>(stream);
     for (auto& gh : env.games) {
+#ifdef RLENV_FUSED_KERNEL
+        if (env.fused) {
+            launch_decision(env, gh.k, env.o, DEC_START, 0, gh.k.n, st);
+            continue;
+        }
+#endif
         const FinishArgs fa = finish_args(env, gh.k, 0, gh.k.n, env.o);
         hipLaunchKernelGGL(k_start, dim3((gh.k.n + 255) / 256), dim3(256), 0, st, fa);
         trace("start", st);
@@ -1091,7 +1345,7 @@ int rlenv_read_consoles(void* h, int gi, int first, int count, uint8_t* out, voi
 void rlenv_set_kernel_timing(void* h, int on) { static_cast<Env*>(h)->clock.on = on != 0; }
 
 int rlenv_kernel_times(void* h, double* ms, int64_t* count, int n) {
-    if (n < KC_COUNT) { g_error = "kernel_times: need room for every kernel class"; return 1; }
+    if (n < KC_COUNT) { g_error = "kernel_times: need room for every kernel class (8)"; return 1; }
     for (int i = 0; i < n; ++i) { ms[i] = 0.0; count[i] = 0; }
     if (static_cast<Env*>(h)->clock.drain(ms, count)) { g_error = "kernel_times: event query failed"; return 1; }
     return 0;

@@ -49,13 +49,19 @@ __device__ __forceinline__ void hset(Hot& h, uint32_t code, uint32_t v) {
 __device__ __forceinline__ void hnz(Hot& h, uint32_t v) {
     h.p = (h.p & ~(FL_N | FL_Z)) | (v & 0x80u) | ((v & 0xFFu) ? 0u : FL_Z);
 }
+// A CPU RAM byte (LDS) as a scalar: the value is wave-uniform, and in an SGPR the code that uses it stays on the
+// scalar unit (SCC branches instead of VALU compares and VCC branches).
+__device__ __forceinline__ uint32_t rd8(const Mem& m, uint32_t a) {
+    return (uint32_t)__builtin_amdgcn_readfirstlane((int)m.ram[a]);
+}
+
 __device__ __forceinline__ void hpush(Hot& h, const Mem& m, uint32_t v) {
     m.ram[0x100u | h.sp] = (uint8_t)v;
     h.sp = (h.sp - 1u) & 0xFFu;
 }
 __device__ __forceinline__ uint32_t hpull(Hot& h, const Mem& m) {
     h.sp = (h.sp + 1u) & 0xFFu;
-    return m.ram[0x100u | h.sp];
+    return rd8(m, 0x100u | h.sp);
 }
 
 // Byte offset in the PRG image of CPU address `addr` ($8000-$FFFF). NROM maps the image linearly (mirrored).
@@ -71,8 +77,8 @@ __device__ __forceinline__ uint32_t prg_wide(const Mem& m, uint32_t idx) {
     return ((ConstU32*)m.cart.prgw)[idx];
 }
 
-// One instruction of opcode descriptor D at pc (operand bytes lo, hi). Returns its CPU cycles (the DMC is serviced
-// by the caller), or 0 with nothing changed when the generic step must run it.
+// One instruction of opcode descriptor D at pc (operand bytes lo, hi). Returns its CPU cycles (the caller adds them
+// to the cycle counter and services the DMC), or 0 with nothing changed when the generic step must run it.
 template <uint32_t B, uint32_t D>
 __device__ __forceinline__ uint32_t fx(Hot& h, const Mem& m, uint32_t pc, uint32_t lo, uint32_t hi) {
     constexpr uint32_t mode = D & 15u, grp = (D >> 8) & 15u, sub = (D >> 12) & 15u;
@@ -98,9 +104,9 @@ __device__ __forceinline__ uint32_t fx(Hot& h, const Mem& m, uint32_t pc, uint32
             if constexpr (pen) cyc += ((base ^ ea) & 0xFF00u) ? 1u : 0u;
         } else if constexpr (mode == M_IZX) {
             const uint32_t ptr = (lo + h.x) & 0xFFu;
-            ea = m.ram[ptr] | ((uint32_t)m.ram[(ptr + 1u) & 0xFFu] << 8);
+            ea = rd8(m, ptr) | (rd8(m, (ptr + 1u) & 0xFFu) << 8);
         } else if constexpr (mode == M_IZY) {
-            const uint32_t b2 = m.ram[lo] | ((uint32_t)m.ram[(lo + 1u) & 0xFFu] << 8);
+            const uint32_t b2 = rd8(m, lo) | (rd8(m, (lo + 1u) & 0xFFu) << 8);
             ea = (b2 + h.y) & 0xFFFFu;
             if constexpr (pen) cyc += ((b2 ^ ea) & 0xFF00u) ? 1u : 0u;
         }
@@ -110,8 +116,8 @@ __device__ __forceinline__ uint32_t fx(Hot& h, const Mem& m, uint32_t pc, uint32
         }
         uint32_t opd = lo;
         if constexpr (rd) {
-            if constexpr (zpage) opd = m.ram[ea];
-            else opd = ea < 0x2000u ? (uint32_t)m.ram[ea & 0x7FFu] : (prg_wide(m, prg_index<B>(h, m, ea)) & 0xFFu);
+            if constexpr (zpage) opd = rd8(m, ea);
+            else opd = ea < 0x2000u ? rd8(m, ea & 0x7FFu) : (prg_wide(m, prg_index<B>(h, m, ea)) & 0xFFu);
         }
         constexpr uint32_t len = mode == M_IMP ? 1u : ((mode >= M_ABS && mode <= M_ABY) || mode == M_IND) ? 3u : 2u;
         uint32_t npc = (pc + len) & 0xFFFFu, res = 0;
@@ -177,9 +183,9 @@ __device__ __forceinline__ uint32_t fx(Hot& h, const Mem& m, uint32_t pc, uint32
             if constexpr (mode == M_IND) {
                 const uint32_t a1 = (base & 0xFF00u) | ((base + 1u) & 0xFFu);
                 if ((base >= 0x2000u && base < 0x8000u) || (a1 >= 0x2000u && a1 < 0x8000u)) return 0;
-                const uint32_t l8 = base < 0x2000u ? (uint32_t)m.ram[base & 0x7FFu]
+                const uint32_t l8 = base < 0x2000u ? rd8(m, base & 0x7FFu)
                                                    : (prg_wide(m, prg_index<B>(h, m, base)) & 0xFFu);
-                const uint32_t h8 = a1 < 0x2000u ? (uint32_t)m.ram[a1 & 0x7FFu]
+                const uint32_t h8 = a1 < 0x2000u ? rd8(m, a1 & 0x7FFu)
                                                  : (prg_wide(m, prg_index<B>(h, m, a1)) & 0xFFu);
                 npc = l8 | (h8 << 8);
             } else {
@@ -203,8 +209,7 @@ __device__ __forceinline__ uint32_t fx(Hot& h, const Mem& m, uint32_t pc, uint32
             else m.ram[ea & 0x7FFu] = (uint8_t)res;
         }
         h.pc = npc;
-        h.cycles += cyc;
-        return cyc;
+        return cyc;   // the caller adds the cycles and services the DMC, as cpu_step does after its cycle count
     }
 }
 
@@ -233,10 +238,18 @@ __device__ __forceinline__ uint32_t fast_step(Hot& h, const Mem& m, uint32_t* op
 #undef ND_FX16
 #undef ND_FX
 
+// Cycles from `now` until the DMC's next event, saturated to 32 bits (an idle DMC is never reached within a frame).
+__device__ __forceinline__ uint32_t dmc_distance(uint64_t now, uint64_t event) {
+    if (event <= now) return 0;
+    const uint64_t d = event - now;
+    return d > 0xFFFFFFFFull ? 0xFFFFFFFFu : (uint32_t)d;
+}
+
 // run_until (nes_dev.h) with the fast path first, for a console whose state `cs` lives in LDS: the same PPU
 // settling, event horizon, idle-loop fast-forward, budget and fault handling, so the console ends in exactly the
-// state run_until leaves. The fast loop keeps only Hot and a few flags live; the generic step, the settle and the
-// fast-forward work on `cs` (CPU registers written back before and reloaded after each of them).
+// state run_until leaves. The fast loop keeps only Hot and a few flags live, and counts CPU cycles in 32 bits
+// since the last flush into h.cycles (a frame is ~30k cycles); the generic step, the settle and the fast-forward
+// work on `cs` (registers written back before and reloaded after each of them).
 template <uint32_t B>
 __device__ __forceinline__ uint32_t run_until_wave(Con& cs, const Mem& m, const uint32_t* optab, uint64_t target,
                                                    uint32_t budget = NES_BUDGET) {
@@ -245,6 +258,8 @@ __device__ __forceinline__ uint32_t run_until_wave(Con& cs, const Mem& m, const 
     Hot h;
     hot_load(h, cs);
     uint64_t dmc_event = cs.dmc_event;
+    uint32_t ecyc = 0;                                     // cycles not yet added to h.cycles
+    uint32_t dmc_in = dmc_distance(h.cycles, dmc_event);   // from h.cycles to the DMC event
     uint32_t nmi = cs.nmi_pending, irq = cs.irq_line, s0v = cs.s0_valid;
     while (instructions < budget) {
         if (pending >= to_event) {
@@ -257,34 +272,65 @@ __device__ __forceinline__ uint32_t run_until_wave(Con& cs, const Mem& m, const 
             s0v = cs.s0_valid;
         }
         uint32_t op = 0, pc0 = h.pc, cyc = 0;
-        if (!nmi && !(irq && !(h.p & FL_I))) cyc = fast_step<B>(h, m, &op);
-        if (cyc != 0) {
-            if (h.cycles >= dmc_event) {
-                const uint32_t s = dmc_service(m.rec, h.cycles, 1);
-                dmc_event = m.rec->dmc_event;
-                h.cycles += s;
-                cyc += s;
-            }
-        } else {
-            hot_store(h, cs);
-            cs.dmc_event = dmc_event;
-            const int32_t start_rel =
-                (int32_t)((int64_t)abs_dot(cs) + pending - (int64_t)cs.log_frame * NES_FRAME_DOTS);
-            cyc = cpu_step(cs, m, optab, start_rel, &fault, &op, &pc0);
-            hot_load(h, cs);
-            dmc_event = cs.dmc_event;
-            nmi = cs.nmi_pending;
-            irq = cs.irq_line;
-            s0v = cs.s0_valid;
-            if (fault) break;
+        // counted: the instruction's cycles are already in pending / instructions. burst: no interrupt can be
+        // taken, the sprite-0 horizon is current and only the fast path's registers are live, so fast
+        // instructions run back to back until one cannot run there (cyc = 0, nothing changed), the DMC is due,
+        // an idle jump, the PPU event horizon or the budget; otherwise at most one fast instruction runs and the
+        // bookkeeping below is done for it.
+        uint32_t counted = 0;
+        const uint32_t burst = (s0v != 0u) & ((nmi | irq) == 0u);
+        if (burst || (nmi | irq) == 0u || (nmi == 0u && (h.p & FL_I))) {
+            do {
+                pc0 = h.pc;
+                cyc = fast_step<B>(h, m, &op);
+                if (cyc == 0) break;
+                ecyc += cyc;
+                if (ecyc >= dmc_in || !burst) break;
+                pending += 3u * cyc;
+                ++instructions;
+                counted = 1;
+                if (op == 0x4Cu && h.pc == pc0) break;
+                counted = 0;
+            } while (pending < to_event && instructions < budget);
+            if (burst && cyc != 0 && !counted && ecyc < dmc_in) continue;   // horizon or budget: back to the top
         }
-        pending += 3u * cyc;
-        ++instructions;
-        if (!s0v) {
-            to_event = dots_to_event(cs, m);
-            s0v = cs.s0_valid;
+        if (!counted) {
+            if (cyc != 0) {
+                if (ecyc >= dmc_in) {
+                    h.cycles += ecyc;
+                    ecyc = 0;
+                    const uint32_t s = dmc_service(m.rec, h.cycles, 1);
+                    dmc_event = m.rec->dmc_event;
+                    h.cycles += s;
+                    cyc += s;
+                    dmc_in = dmc_distance(h.cycles, dmc_event);
+                }
+            } else {
+                h.cycles += ecyc;
+                ecyc = 0;
+                hot_store(h, cs);
+                cs.dmc_event = dmc_event;
+                const int32_t start_rel =
+                    (int32_t)((int64_t)abs_dot(cs) + pending - (int64_t)cs.log_frame * NES_FRAME_DOTS);
+                cyc = cpu_step(cs, m, optab, start_rel, &fault, &op, &pc0);
+                hot_load(h, cs);
+                dmc_event = cs.dmc_event;
+                dmc_in = dmc_distance(h.cycles, dmc_event);
+                nmi = cs.nmi_pending;
+                irq = cs.irq_line;
+                s0v = cs.s0_valid;
+                if (fault) break;
+            }
+            pending += 3u * cyc;
+            ++instructions;
+            if (!s0v) {
+                to_event = dots_to_event(cs, m);
+                s0v = cs.s0_valid;
+            }
         }
         if (op == 0x4Cu && h.pc == pc0) {
+            h.cycles += ecyc;
+            ecyc = 0;
             hot_store(h, cs);
             cs.dmc_event = dmc_event;
             ppu_advance(cs, m, pending);
@@ -295,6 +341,7 @@ __device__ __forceinline__ uint32_t run_until_wave(Con& cs, const Mem& m, const 
             fast_forward(cs, m);
             h.cycles = cs.cycles;
             dmc_event = cs.dmc_event;
+            dmc_in = dmc_distance(h.cycles, dmc_event);
             nmi = cs.nmi_pending;
             irq = cs.irq_line;
             to_event = dots_to_event(cs, m);
@@ -302,6 +349,7 @@ __device__ __forceinline__ uint32_t run_until_wave(Con& cs, const Mem& m, const 
             if (abs_dot(cs) >= target) break;
         }
     }
+    h.cycles += ecyc;
     hot_store(h, cs);
     cs.dmc_event = dmc_event;
     cs.instr += instructions;
