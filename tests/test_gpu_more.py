@@ -60,6 +60,37 @@ def test_full_size_console_independence():
 
 
 @pytest.mark.gpu
+def test_resume_blob_equals_oracle_and_cross_loads():
+    """The exact-resume blob (rlenv_save) of the HIP build equals the oracle's byte for byte, and an oracle blob
+    loaded into a fresh HIP env continues exactly as the oracle does (the reference's resume check is
+    rl/tests/gpu_check.py:56-74)."""
+    print('case: SMB-like cart seed 4, 12 consoles, ends + dropout + idle, save after 10, 10 more decisions',
+          flush=True)
+    kw = dict(seed=21, sticky=True, idle_max=3, dropout=True, pad_mode=True, end_prob=0.1)
+    cart = synth.smb_like_cart(4)
+    cpu, gpu = pair(12, cart, **kw)
+    run(cpu, gpu, 10, 6, True)
+    sd_cpu, sd_gpu = cpu.state_dict(), gpu.state_dict()
+    assert sd_cpu['env'].shape == sd_gpu['env'].shape
+    assert np.array_equal(sd_cpu['env'], sd_gpu['env'])
+    fresh = RlEnv({'smb': 12}, device='cuda', roms={'smb': cart}, lib_path=HIP_LIB, ram_hash=True, **kw)
+    fresh.load_state_dict(sd_cpu)
+    g = torch.Generator().manual_seed(8)
+    for t in range(10):
+        act = torch.randint(0, 256, (12,), generator=g, dtype=torch.int16)
+        cpu.actions.copy_(act)
+        fresh.actions.copy_(act.cuda())
+        cpu.step()
+        fresh.step()
+        torch.cuda.synchronize()
+        for k in ('obs', 'emph', 'reward', 'done', 'masks', 'timeline', 'pads', 'events', 'parts', 'ram_hash'):
+            assert torch.equal(getattr(cpu, k), getattr(fresh, k).cpu()), (t, k)
+        d = cpu.done.bool()                              # info is written at episode end and is not in the blob
+        assert torch.equal(cpu.info[d], fresh.info.cpu()[d]), t
+        assert np.array_equal(cpu.consoles(0), fresh.consoles(0)), t
+
+
+@pytest.mark.gpu
 def test_step_range_equals_step():
     print('case: SMB-like cart, 16 consoles, step vs two step_range halves, 12 decisions', flush=True)
     kw = dict(seed=5, sticky=True, idle_max=2, dropout=True, pad_mode=True, roms={'smb': synth.smb_like_cart(3)})
