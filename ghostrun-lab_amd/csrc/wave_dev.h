@@ -28,9 +28,17 @@ struct Hot {
     uint32_t prg0, prg1, prg2, prg3;
 };
 
+// A wave-uniform value read from LDS, as a scalar (an LDS load lands in a VGPR; without this the compiler moves every
+// use of it to the vector unit, with lane-mask compares instead of SCC branches).
+__device__ __forceinline__ uint32_t uni(uint32_t v) { return (uint32_t)__builtin_amdgcn_readfirstlane((int)v); }
+__device__ __forceinline__ uint64_t uni64(uint64_t v) {
+    return (uint64_t)uni((uint32_t)v) | ((uint64_t)uni((uint32_t)(v >> 32)) << 32);
+}
+
 __device__ __forceinline__ void hot_load(Hot& h, const Con& c) {
-    h.pc = c.pc; h.a = c.a; h.x = c.x; h.y = c.y; h.sp = c.sp; h.p = c.p; h.cycles = c.cycles;
-    h.prg0 = c.prg0; h.prg1 = c.prg1; h.prg2 = c.prg2; h.prg3 = c.prg3;
+    h.pc = uni(c.pc); h.a = uni(c.a); h.x = uni(c.x); h.y = uni(c.y); h.sp = uni(c.sp); h.p = uni(c.p);
+    h.cycles = uni64(c.cycles);
+    h.prg0 = uni(c.prg0); h.prg1 = uni(c.prg1); h.prg2 = uni(c.prg2); h.prg3 = uni(c.prg3);
 }
 // (the PRG offsets change only in the generic step, which writes them to the console state itself)
 __device__ __forceinline__ void hot_store(const Hot& h, Con& c) {
@@ -64,6 +72,24 @@ __device__ __forceinline__ uint32_t hpull(Hot& h, const Mem& m) {
     return rd8(m, 0x100u | h.sp);
 }
 
+// Controller port 1 ($4016), the one I/O register the fast path serves itself: the same read and write as the
+// bus (nes_dev.h io_read / io_write), on the console state in LDS.
+__device__ __forceinline__ uint32_t port_read(Con& cs) {
+    uint32_t bit;
+    if (uni(cs.strobe)) {
+        bit = uni(cs.pad) & 1u;
+    } else {
+        const uint32_t s = uni(cs.shift);
+        bit = s & 1u;
+        cs.shift = (s >> 1) | 0x80u;
+    }
+    return 0x40u | bit;
+}
+__device__ __forceinline__ void port_write(Con& cs, uint32_t v) {
+    cs.strobe = v & 1u;
+    if (v & 1u) cs.shift = uni(cs.pad);
+}
+
 // Byte offset in the PRG image of CPU address `addr` ($8000-$FFFF). NROM maps the image linearly (mirrored).
 template <uint32_t B>
 __device__ __forceinline__ uint32_t prg_index(const Hot& h, const Mem& m, uint32_t addr) {
@@ -80,7 +106,7 @@ __device__ __forceinline__ uint32_t prg_wide(const Mem& m, uint32_t idx) {
 // One instruction of opcode descriptor D at pc (operand bytes lo, hi). Returns its CPU cycles (the caller adds them
 // to the cycle counter and services the DMC), or 0 with nothing changed when the generic step must run it.
 template <uint32_t B, uint32_t D>
-__device__ __forceinline__ uint32_t fx(Hot& h, const Mem& m, uint32_t pc, uint32_t lo, uint32_t hi) {
+__device__ __forceinline__ uint32_t fx(Hot& h, const Mem& m, Con& cs, uint32_t pc, uint32_t lo, uint32_t hi) {
     constexpr uint32_t mode = D & 15u, grp = (D >> 8) & 15u, sub = (D >> 12) & 15u;
     constexpr uint32_t src = (D >> 16) & 7u, dst = (D >> 19) & 7u;
     constexpr bool rd = (D & D_READ) != 0, wr = (D & D_WRITE) != 0, pen = (D & D_PEN) != 0;
@@ -110,14 +136,20 @@ __device__ __forceinline__ uint32_t fx(Hot& h, const Mem& m, uint32_t pc, uint32
             ea = (b2 + h.y) & 0xFFFFu;
             if constexpr (pen) cyc += ((b2 ^ ea) & 0xFF00u) ? 1u : 0u;
         }
-        // memory class: bail out before any side effect
+        // memory class: bail out before any side effect. A plain read or a plain write may also be the controller
+        // port; a read-modify-write of an I/O register and any write at $8000+ (a mapper) go to the generic step.
         if constexpr (!zpage && (rd || wr)) {
-            if (ea >= 0x2000u && (wr || ea < 0x8000u)) return 0;
+            if (ea >= 0x2000u && (wr || ea < 0x8000u)) {
+                if constexpr (rd && wr) return 0;
+                else if (ea != 0x4016u) return 0;
+            }
         }
         uint32_t opd = lo;
         if constexpr (rd) {
             if constexpr (zpage) opd = rd8(m, ea);
-            else opd = ea < 0x2000u ? rd8(m, ea & 0x7FFu) : (prg_wide(m, prg_index<B>(h, m, ea)) & 0xFFu);
+            else if (ea < 0x2000u) opd = rd8(m, ea & 0x7FFu);
+            else if (ea >= 0x8000u) opd = prg_wide(m, prg_index<B>(h, m, ea)) & 0xFFu;
+            else opd = port_read(cs);
         }
         constexpr uint32_t len = mode == M_IMP ? 1u : ((mode >= M_ABS && mode <= M_ABY) || mode == M_IND) ? 3u : 2u;
         uint32_t npc = (pc + len) & 0xFFFFu, res = 0;
@@ -190,6 +222,7 @@ __device__ __forceinline__ uint32_t fx(Hot& h, const Mem& m, uint32_t pc, uint32
                 npc = l8 | (h8 << 8);
             } else {
                 npc = base;
+                if (npc == pc) return 0;   // the idle loop: the generic step runs it, then the fast-forward
             }
         } else if constexpr (grp == G_JSR) {
             const uint32_t ret = (pc + 2u) & 0xFFFFu;
@@ -206,6 +239,7 @@ __device__ __forceinline__ uint32_t fx(Hot& h, const Mem& m, uint32_t pc, uint32
         }
         if constexpr (wr) {
             if constexpr (zpage) m.ram[ea] = (uint8_t)res;
+            else if (!rd && ea >= 0x2000u) port_write(cs, res);
             else m.ram[ea & 0x7FFu] = (uint8_t)res;
         }
         h.pc = npc;
@@ -214,7 +248,7 @@ __device__ __forceinline__ uint32_t fx(Hot& h, const Mem& m, uint32_t pc, uint32
 }
 
 #define ND_FX(n) \
-    case n: return fx<B, kOptab.t[n]>(h, m, pc, lo, hi);
+    case n: return fx<B, kOptab.t[n]>(h, m, cs, pc, lo, hi);
 #define ND_FX16(h)                                                                                                    \
     ND_FX(h + 0x0) ND_FX(h + 0x1) ND_FX(h + 0x2) ND_FX(h + 0x3) ND_FX(h + 0x4) ND_FX(h + 0x5) ND_FX(h + 0x6)          \
     ND_FX(h + 0x7) ND_FX(h + 0x8) ND_FX(h + 0x9) ND_FX(h + 0xA) ND_FX(h + 0xB) ND_FX(h + 0xC) ND_FX(h + 0xD)          \
@@ -222,9 +256,11 @@ __device__ __forceinline__ uint32_t fx(Hot& h, const Mem& m, uint32_t pc, uint32
 
 // The fast path for the instruction at h.pc: its cycles, or 0 (nothing changed) for the generic step.
 template <uint32_t B>
-__device__ __forceinline__ uint32_t fast_step(Hot& h, const Mem& m, uint32_t* op_out) {
+__device__ __forceinline__ uint32_t fast_step(Hot& h, const Mem& m, Con& cs, uint32_t* op_out) {
     const uint32_t pc = h.pc;
-    if (pc < 0x8000u || (pc & 0x1FFFu) > 0x1FFDu) return 0;
+    // code in PRG ($8000+) and the 3-byte window inside one 8 KB page: pc >= $8000 and (pc & $1FFF) <= $1FFD,
+    // as one compare ((pc + 2) & $9FFF keeps bit 15 and the page offset of the window's last byte)
+    if (((pc + 2u) & 0x9FFFu) < 0x8002u) return 0;
     const uint32_t word = prg_wide(m, prg_index<B>(h, m, pc));
     const uint32_t op = word & 0xFFu, lo = (word >> 8) & 0xFFu, hi = (word >> 16) & 0xFFu;
     *op_out = op;
@@ -247,105 +283,124 @@ __device__ __forceinline__ uint32_t dmc_distance(uint64_t now, uint64_t event) {
 
 // run_until (nes_dev.h) with the fast path first, for a console whose state `cs` lives in LDS: the same PPU
 // settling, event horizon, idle-loop fast-forward, budget and fault handling, so the console ends in exactly the
-// state run_until leaves. The fast loop keeps only Hot and a few flags live, and counts CPU cycles in 32 bits
-// since the last flush into h.cycles (a frame is ~30k cycles); the generic step, the settle and the fast-forward
-// work on `cs` (registers written back before and reloaded after each of them).
+// state run_until leaves. The fast loop keeps only Hot and a few scalars live and counts CPU cycles in 32 bits since
+// the last flush into h.cycles (a frame is ~30k cycles); the generic step, the settle and the fast-forward work on
+// `cs` (registers written back before and reloaded after each of them).
 template <uint32_t B>
 __device__ __forceinline__ uint32_t run_until_wave(Con& cs, const Mem& m, const uint32_t* optab, uint64_t target,
                                                    uint32_t budget = NES_BUDGET) {
     uint32_t instructions = 0, fault = 0, pending = 0;
-    uint32_t to_event = dots_to_event(cs, m);
+    uint32_t to_event = uni(dots_to_event(cs, m));
     Hot h;
     hot_load(h, cs);
-    uint64_t dmc_event = cs.dmc_event;
+    uint64_t dmc_event = uni64(cs.dmc_event);
     uint32_t ecyc = 0;                                     // cycles not yet added to h.cycles
-    uint32_t dmc_in = dmc_distance(h.cycles, dmc_event);   // from h.cycles to the DMC event
-    uint32_t nmi = cs.nmi_pending, irq = cs.irq_line, s0v = cs.s0_valid;
+    uint32_t dmc_in = dmc_distance(h.cycles, dmc_event);   // from h.cycles to the DMC event; ecyc <= dmc_in here
+    uint32_t nmi = uni(cs.nmi_pending), irq = uni(cs.irq_line), s0v = uni(cs.s0_valid);
+    // The last fast instruction took the cycle count to the DMC event: service it, then count the instruction with
+    // the stolen cycles (cpu_step's order).
+    auto dmc_due = [&](uint32_t cyc) {
+        h.cycles += ecyc;
+        ecyc = 0;
+        const uint32_t s = dmc_service(m.rec, h.cycles, 1);
+        dmc_event = uni64(m.rec->dmc_event);
+        h.cycles += s;
+        dmc_in = dmc_distance(h.cycles, dmc_event);
+        pending += 3u * (cyc + s);
+        ++instructions;
+    };
     while (instructions < budget) {
         if (pending >= to_event) {
             ppu_advance(cs, m, pending);   // touches no CPU register
             pending = 0;
-            nmi = cs.nmi_pending;
-            irq = cs.irq_line;
+            nmi = uni(cs.nmi_pending);
+            irq = uni(cs.irq_line);
             if (abs_dot(cs) >= target) break;
-            to_event = dots_to_event(cs, m);
-            s0v = cs.s0_valid;
+            to_event = uni(dots_to_event(cs, m));
+            s0v = uni(cs.s0_valid);
         }
         uint32_t op = 0, pc0 = h.pc, cyc = 0;
-        // counted: the instruction's cycles are already in pending / instructions. burst: no interrupt can be
-        // taken, the sprite-0 horizon is current and only the fast path's registers are live, so fast
-        // instructions run back to back until one cannot run there (cyc = 0, nothing changed), the DMC is due,
-        // an idle jump, the PPU event horizon or the budget; otherwise at most one fast instruction runs and the
-        // bookkeeping below is done for it.
-        uint32_t counted = 0;
-        const uint32_t burst = (s0v != 0u) & ((nmi | irq) == 0u);
-        if (burst || (nmi | irq) == 0u || (nmi == 0u && (h.p & FL_I))) {
+        if (s0v != 0u && (nmi | irq) == 0u) {
+            // Burst: no interrupt can be taken and the sprite-0 horizon is current, so fast instructions run back to
+            // back until one needs the generic step (cyc = 0, nothing changed) or the cycles used reach `room`, the
+            // nearest of: the DMC event, the PPU event horizon (3 dots a cycle) and the instruction budget (every
+            // instruction takes at least 2 cycles, so the burst never passes it).
+            const uint32_t room = min(min(dmc_in - ecyc, (to_event - pending + 2u) / 3u), 2u * (budget - instructions));
+            uint32_t used = 0, n = 0;
             do {
-                pc0 = h.pc;
-                cyc = fast_step<B>(h, m, &op);
-                if (cyc == 0) break;
-                ecyc += cyc;
-                if (ecyc >= dmc_in || !burst) break;
-                pending += 3u * cyc;
-                ++instructions;
-                counted = 1;
-                if (op == 0x4Cu && h.pc == pc0) break;
-                counted = 0;
-            } while (pending < to_event && instructions < budget);
-            if (burst && cyc != 0 && !counted && ecyc < dmc_in) continue;   // horizon or budget: back to the top
-        }
-        if (!counted) {
-            if (cyc != 0) {
+                cyc = fast_step<B>(h, m, cs, &op);
+                used += cyc;
+                ++n;
+            } while (cyc != 0u && used < room);
+            ecyc += used;
+            if (cyc != 0u) {
                 if (ecyc >= dmc_in) {
-                    h.cycles += ecyc;
-                    ecyc = 0;
-                    const uint32_t s = dmc_service(m.rec, h.cycles, 1);
-                    dmc_event = m.rec->dmc_event;
-                    h.cycles += s;
-                    cyc += s;
-                    dmc_in = dmc_distance(h.cycles, dmc_event);
+                    pending += 3u * (used - cyc);
+                    instructions += n - 1u;
+                    dmc_due(cyc);
+                } else {
+                    pending += 3u * used;   // the event horizon or the budget: back to the top
+                    instructions += n;
                 }
-            } else {
-                h.cycles += ecyc;
-                ecyc = 0;
-                hot_store(h, cs);
-                cs.dmc_event = dmc_event;
-                const int32_t start_rel =
-                    (int32_t)((int64_t)abs_dot(cs) + pending - (int64_t)cs.log_frame * NES_FRAME_DOTS);
-                cyc = cpu_step(cs, m, optab, start_rel, &fault, &op, &pc0);
-                hot_load(h, cs);
-                dmc_event = cs.dmc_event;
-                dmc_in = dmc_distance(h.cycles, dmc_event);
-                nmi = cs.nmi_pending;
-                irq = cs.irq_line;
-                s0v = cs.s0_valid;
-                if (fault) break;
+                continue;
             }
-            pending += 3u * cyc;
-            ++instructions;
-            if (!s0v) {
-                to_event = dots_to_event(cs, m);
-                s0v = cs.s0_valid;
+            pending += 3u * used;           // the last one needs the generic step
+            instructions += n - 1u;
+        } else if ((nmi | irq) == 0u || (nmi == 0u && (h.p & FL_I))) {
+            // no interrupt is taken, but the sprite-0 horizon is stale or an IRQ waits behind the I flag: one fast
+            // instruction, then the horizon is refreshed
+            cyc = fast_step<B>(h, m, cs, &op);
+            if (cyc != 0u) {
+                ecyc += cyc;
+                if (ecyc >= dmc_in) {
+                    dmc_due(cyc);
+                } else {
+                    pending += 3u * cyc;
+                    ++instructions;
+                }
+                if (!s0v) {
+                    to_event = uni(dots_to_event(cs, m));
+                    s0v = uni(cs.s0_valid);
+                }
+                continue;
             }
+        }
+        // the generic step: I/O, interrupts, the idle loop, BRK, faults, code outside PRG
+        h.cycles += ecyc;
+        ecyc = 0;
+        hot_store(h, cs);
+        cs.dmc_event = dmc_event;
+        const int32_t start_rel = (int32_t)((int64_t)abs_dot(cs) + pending - (int64_t)cs.log_frame * NES_FRAME_DOTS);
+        cyc = cpu_step(cs, m, optab, start_rel, &fault, &op, &pc0);
+        hot_load(h, cs);
+        dmc_event = uni64(cs.dmc_event);
+        dmc_in = dmc_distance(h.cycles, dmc_event);
+        nmi = uni(cs.nmi_pending);
+        irq = uni(cs.irq_line);
+        s0v = uni(cs.s0_valid);
+        if (fault) break;
+        pending += 3u * cyc;
+        ++instructions;
+        if (!s0v) {
+            to_event = uni(dots_to_event(cs, m));
+            s0v = uni(cs.s0_valid);
         }
         if (op == 0x4Cu && h.pc == pc0) {
-            h.cycles += ecyc;
-            ecyc = 0;
             hot_store(h, cs);
             cs.dmc_event = dmc_event;
             ppu_advance(cs, m, pending);
             pending = 0;
-            nmi = cs.nmi_pending;
-            irq = cs.irq_line;
+            nmi = uni(cs.nmi_pending);
+            irq = uni(cs.irq_line);
             if (abs_dot(cs) >= target) break;
             fast_forward(cs, m);
-            h.cycles = cs.cycles;
-            dmc_event = cs.dmc_event;
+            h.cycles = uni64(cs.cycles);
+            dmc_event = uni64(cs.dmc_event);
             dmc_in = dmc_distance(h.cycles, dmc_event);
-            nmi = cs.nmi_pending;
-            irq = cs.irq_line;
-            to_event = dots_to_event(cs, m);
-            s0v = cs.s0_valid;
+            nmi = uni(cs.nmi_pending);
+            irq = uni(cs.irq_line);
+            to_event = uni(dots_to_event(cs, m));
+            s0v = uni(cs.s0_valid);
             if (abs_dot(cs) >= target) break;
         }
     }
