@@ -136,20 +136,28 @@ __device__ __forceinline__ uint32_t fx(Hot& h, const Mem& m, Con& cs, uint32_t p
             ea = (b2 + h.y) & 0xFFFFu;
             if constexpr (pen) cyc += ((b2 ^ ea) & 0xFF00u) ? 1u : 0u;
         }
-        // memory class: bail out before any side effect. A plain read or a plain write may also be the controller
-        // port; a read-modify-write of an I/O register and any write at $8000+ (a mapper) go to the generic step.
-        if constexpr (!zpage && (rd || wr)) {
-            if (ea >= 0x2000u && (wr || ea < 0x8000u)) {
-                if constexpr (rd && wr) return 0;
-                else if (ea != 0x4016u) return 0;
+        // Memory class, decided before any side effect (every check below comes before the first state change):
+        // RAM, PRG reads and the controller port run here; any other I/O register, a read-modify-write outside RAM
+        // and any write at $8000+ (a mapper) go to the generic step. Written as chains of single compares: boolean
+        // combinations of uniform conditions become lane-mask arithmetic.
+        if constexpr (!zpage && rd && wr) {
+            if (ea >= 0x2000u) return 0;
+        }
+        if constexpr (!zpage && wr && !rd) {
+            if (ea >= 0x2000u) {
+                if (ea != 0x4016u) return 0;
             }
         }
         uint32_t opd = lo;
         if constexpr (rd) {
-            if constexpr (zpage) opd = rd8(m, ea);
-            else if (ea < 0x2000u) opd = rd8(m, ea & 0x7FFu);
-            else if (ea >= 0x8000u) opd = prg_wide(m, prg_index<B>(h, m, ea)) & 0xFFu;
-            else opd = port_read(cs);
+            if constexpr (zpage || wr) {
+                opd = rd8(m, ea & 0x7FFu);
+            } else {
+                if (ea < 0x2000u) opd = rd8(m, ea & 0x7FFu);
+                else if (ea >= 0x8000u) opd = prg_wide(m, prg_index<B>(h, m, ea)) & 0xFFu;
+                else if (ea == 0x4016u) opd = port_read(cs);
+                else return 0;
+            }
         }
         constexpr uint32_t len = mode == M_IMP ? 1u : ((mode >= M_ABS && mode <= M_ABY) || mode == M_IND) ? 3u : 2u;
         uint32_t npc = (pc + len) & 0xFFFFu, res = 0;
@@ -238,9 +246,9 @@ __device__ __forceinline__ uint32_t fx(Hot& h, const Mem& m, Con& cs, uint32_t p
             npc = (h8 << 8) | l8;
         }
         if constexpr (wr) {
-            if constexpr (zpage) m.ram[ea] = (uint8_t)res;
-            else if (!rd && ea >= 0x2000u) port_write(cs, res);
-            else m.ram[ea & 0x7FFu] = (uint8_t)res;
+            if constexpr (zpage || rd) m.ram[ea & 0x7FFu] = (uint8_t)res;
+            else if (ea < 0x2000u) m.ram[ea & 0x7FFu] = (uint8_t)res;
+            else port_write(cs, res);
         }
         h.pc = npc;
         return cyc;   // the caller adds the cycles and services the DMC, as cpu_step does after its cycle count
@@ -320,43 +328,35 @@ __device__ __forceinline__ uint32_t run_until_wave(Con& cs, const Mem& m, const 
             s0v = uni(cs.s0_valid);
         }
         uint32_t op = 0, pc0 = h.pc, cyc = 0;
-        if (s0v != 0u && (nmi | irq) == 0u) {
-            // Burst: no interrupt can be taken and the sprite-0 horizon is current, so fast instructions run back to
-            // back until one needs the generic step (cyc = 0, nothing changed) or the cycles used reach `room`, the
-            // nearest of: the DMC event, the PPU event horizon (3 dots a cycle) and the instruction budget (every
-            // instruction takes at least 2 cycles, so the burst never passes it).
-            const uint32_t room = min(min(dmc_in - ecyc, (to_event - pending + 2u) / 3u), 2u * (budget - instructions));
-            uint32_t used = 0, n = 0;
-            do {
+        if (((nmi | (irq & ~(h.p >> 2))) & 1u) == 0u) {   // no NMI, and no IRQ unless the I flag masks it
+            // Fast instructions. With the sprite-0 horizon current and no IRQ asserted (a masked one is taken as soon
+            // as CLI, PLP or RTI clears the I flag) this is a burst: they run back to back until one
+            // needs the generic step (cyc = 0, nothing changed) or the cycles used reach `room`, the nearest of the
+            // DMC event, the PPU event horizon (3 dots a cycle) and the instruction budget (every instruction takes
+            // at least 2 cycles, so a burst never passes it). Otherwise one instruction runs and the horizon is
+            // refreshed after it. lm1 = room - 1, and `cyc - 1 >= lm1` (unsigned) is "cyc == 0 or cyc >= room".
+            uint32_t lm1 = 0;
+            if ((s0v & ~irq) & 1u)
+                lm1 = uni(max(min(min(dmc_in - ecyc, (to_event - pending + 2u) / 3u), 2u * (budget - instructions)),
+                              1u) - 1u);
+            const uint32_t lm1_0 = lm1;
+            uint32_t n = 0;
+            for (;;) {
                 cyc = fast_step<B>(h, m, cs, &op);
-                used += cyc;
                 ++n;
-            } while (cyc != 0u && used < room);
+                if (cyc - 1u >= lm1) break;
+                lm1 -= cyc;
+            }
+            const uint32_t used = lm1_0 - lm1 + cyc;   // cycles of the n instructions
             ecyc += used;
             if (cyc != 0u) {
-                if (ecyc >= dmc_in) {
+                if (ecyc >= dmc_in) {   // the last one took the cycle count to the DMC event
                     pending += 3u * (used - cyc);
                     instructions += n - 1u;
                     dmc_due(cyc);
-                } else {
-                    pending += 3u * used;   // the event horizon or the budget: back to the top
+                } else {                // the event horizon or the budget: back to the top
+                    pending += 3u * used;
                     instructions += n;
-                }
-                continue;
-            }
-            pending += 3u * used;           // the last one needs the generic step
-            instructions += n - 1u;
-        } else if ((nmi | irq) == 0u || (nmi == 0u && (h.p & FL_I))) {
-            // no interrupt is taken, but the sprite-0 horizon is stale or an IRQ waits behind the I flag: one fast
-            // instruction, then the horizon is refreshed
-            cyc = fast_step<B>(h, m, cs, &op);
-            if (cyc != 0u) {
-                ecyc += cyc;
-                if (ecyc >= dmc_in) {
-                    dmc_due(cyc);
-                } else {
-                    pending += 3u * cyc;
-                    ++instructions;
                 }
                 if (!s0v) {
                     to_event = uni(dots_to_event(cs, m));
@@ -364,6 +364,8 @@ __device__ __forceinline__ uint32_t run_until_wave(Con& cs, const Mem& m, const 
                 }
                 continue;
             }
+            pending += 3u * used;       // the last one needs the generic step
+            instructions += n - 1u;
         }
         // the generic step: I/O, interrupts, the idle loop, BRK, faults, code outside PRG
         h.cycles += ecyc;
