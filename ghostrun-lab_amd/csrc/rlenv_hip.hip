@@ -1210,7 +1210,17 @@ void* rlenv_create(int ngames, const int* game_ids, const uint8_t* const* roms, 
             }
             uint32_t chr_pages = p.chr.empty() ? 8u : (uint32_t)(p.chr.size() / 1024u);
             if (chr_pages & (chr_pages - 1u)) throw std::runtime_error("CHR size must be a power of two");
-            g.cart = Cart{prgw, chr, (uint32_t)(p.prg.size() / 8192u), chr_pages, p.board, p.mirroring};
+            uint32_t* fetchw = nullptr;
+            if (p.board == NES_BOARD_NROM) {
+                std::vector<uint32_t> f(kFetchWords, 0x02u);
+                const size_t mask = (p.prg.size() - 1u) & 0x7FFFu;
+                for (uint32_t a = 0x8000u; a <= 0xFFFDu; ++a)
+                    f[a] = p.prg[a & mask] | ((uint32_t)p.prg[(a + 1u) & mask] << 8) |
+                           ((uint32_t)p.prg[(a + 2u) & mask] << 16);
+                fetchw = static_cast<uint32_t*>(env->mem.alloc(f.size() * 4));
+                env->mem.upload(fetchw, f.data(), f.size() * 4);
+            }
+            g.cart = Cart{prgw, fetchw, chr, (uint32_t)(p.prg.size() / 8192u), chr_pages, p.board, p.mirroring};
             g.recs = env->mem.zeros<NesRec>((size_t)g.n + 1);
             g.idle = env->mem.zeros<NesRec>((size_t)std::max(env->s.idle_tmpl, 1));
             g.list = env->mem.zeros<int32_t>((size_t)std::max(g.n, 1));

@@ -22,8 +22,11 @@ typedef __attribute__((address_space(4))) const uint32_t ConstU32;
 // Registers the fast loop keeps live: the CPU registers, the cycle counter and the PRG page offsets. Everything
 // else about the console (PPU, controller, DMC, mapper) stays in the console state in LDS and only the generic
 // step, the PPU settle and the idle fast-forward touch it, so the loop's live set is small enough to stay in SGPRs.
+// N and Z are kept lazily, as the values they are taken from: N = bit 7 of nv, Z = (zv == 0); the N and Z bits of
+// p are stale in between and are rebuilt when p is stored or pushed. pc may run one past $FFFF after the last
+// instruction of the address space; it is wrapped when stored (the fast path sends such a pc to the generic step).
 struct Hot {
-    uint32_t pc, a, x, y, sp, p;
+    uint32_t pc, a, x, y, sp, p, nv, zv;
     uint64_t cycles;
     uint32_t prg0, prg1, prg2, prg3;
 };
@@ -35,14 +38,21 @@ __device__ __forceinline__ uint64_t uni64(uint64_t v) {
     return (uint64_t)uni((uint32_t)v) | ((uint64_t)uni((uint32_t)(v >> 32)) << 32);
 }
 
+// p with N and Z rebuilt from the lazy values.
+__device__ __forceinline__ uint32_t hflags(const Hot& h) {
+    return (h.p & ~(FL_N | FL_Z)) | (h.nv & FL_N) | (h.zv ? 0u : FL_Z);
+}
+
 __device__ __forceinline__ void hot_load(Hot& h, const Con& c) {
     h.pc = uni(c.pc); h.a = uni(c.a); h.x = uni(c.x); h.y = uni(c.y); h.sp = uni(c.sp); h.p = uni(c.p);
+    h.nv = h.p;
+    h.zv = ~h.p & FL_Z;
     h.cycles = uni64(c.cycles);
     h.prg0 = uni(c.prg0); h.prg1 = uni(c.prg1); h.prg2 = uni(c.prg2); h.prg3 = uni(c.prg3);
 }
 // (the PRG offsets change only in the generic step, which writes them to the console state itself)
 __device__ __forceinline__ void hot_store(const Hot& h, Con& c) {
-    c.pc = h.pc; c.a = h.a; c.x = h.x; c.y = h.y; c.sp = h.sp; c.p = h.p; c.cycles = h.cycles;
+    c.pc = h.pc & 0xFFFFu; c.a = h.a; c.x = h.x; c.y = h.y; c.sp = h.sp; c.p = hflags(h); c.cycles = h.cycles;
 }
 
 __device__ __forceinline__ uint32_t hget(const Hot& h, uint32_t code, uint32_t opd) {
@@ -54,8 +64,9 @@ __device__ __forceinline__ void hset(Hot& h, uint32_t code, uint32_t v) {
     else if (code == R_Y) h.y = v;
     else if (code == R_SP) h.sp = v;
 }
-__device__ __forceinline__ void hnz(Hot& h, uint32_t v) {
-    h.p = (h.p & ~(FL_N | FL_Z)) | (v & 0x80u) | ((v & 0xFFu) ? 0u : FL_Z);
+__device__ __forceinline__ void hnz(Hot& h, uint32_t v) {   // v < 256
+    h.nv = v;
+    h.zv = v;
 }
 // A CPU RAM byte (LDS) as a scalar: the value is wave-uniform, and in an SGPR the code that uses it stays on the
 // scalar unit (SCC branches instead of VALU compares and VCC branches).
@@ -160,7 +171,7 @@ __device__ __forceinline__ uint32_t fx(Hot& h, const Mem& m, Con& cs, uint32_t p
             }
         }
         constexpr uint32_t len = mode == M_IMP ? 1u : ((mode >= M_ABS && mode <= M_ABY) || mode == M_IND) ? 3u : 2u;
-        uint32_t npc = (pc + len) & 0xFFFFu, res = 0;
+        uint32_t npc = pc + len, res = 0;   // pc <= $FFFD here; $10000 is wrapped when stored
         if constexpr (grp == G_LD) {
             res = hget(h, src, opd);
             hset(h, dst, res);
@@ -187,7 +198,9 @@ __device__ __forceinline__ uint32_t fx(Hot& h, const Mem& m, Con& cs, uint32_t p
                 h.p = (h.p & ~FL_C) | (r >= opd ? FL_C : 0u);
                 hnz(h, (r - opd) & 0xFFu);
             } else {
-                h.p = (h.p & ~(FL_N | FL_V | FL_Z)) | (opd & 0xC0u) | ((h.a & opd) ? 0u : FL_Z);
+                h.p = (h.p & ~FL_V) | (opd & FL_V);
+                h.nv = opd;
+                h.zv = h.a & opd;
             }
         } else if constexpr (grp == G_SHIFT) {
             const uint32_t in = hget(h, src, opd), cin = h.p & FL_C;
@@ -200,9 +213,13 @@ __device__ __forceinline__ uint32_t fx(Hot& h, const Mem& m, Con& cs, uint32_t p
             hset(h, dst, res);
             hnz(h, res);
         } else if constexpr (grp == G_BR) {
-            const bool set = ((h.p >> (sub & 7u)) & 1u) != 0;
+            constexpr uint32_t bit = sub & 7u;
+            bool set;
+            if constexpr (bit == 7u) set = (h.nv & FL_N) != 0;
+            else if constexpr (bit == 1u) set = h.zv == 0;
+            else set = ((h.p >> bit) & 1u) != 0;
             if (set == ((sub & 8u) != 0)) {
-                const uint32_t tgt = (npc + (uint32_t)(int32_t)(int8_t)lo) & 0xFFFFu;
+                const uint32_t tgt = npc + (uint32_t)(int32_t)(int8_t)lo;   // wrapped when stored
                 cyc += ((npc ^ tgt) & 0xFF00u) ? 2u : 1u;
                 npc = tgt;
             }
@@ -210,7 +227,7 @@ __device__ __forceinline__ uint32_t fx(Hot& h, const Mem& m, Con& cs, uint32_t p
             constexpr uint32_t bitm = 1u << (sub & 7u);
             h.p = (sub & 8u) ? (h.p | bitm) : (h.p & ~bitm);
         } else if constexpr (grp == G_PUSH) {
-            hpush(h, m, src == R_A ? h.a : (h.p | FL_B | FL_U));
+            hpush(h, m, src == R_A ? h.a : (hflags(h) | FL_B | FL_U));
         } else if constexpr (grp == G_PULL) {
             const uint32_t v = hpull(h, m);
             if constexpr (dst == R_A) {
@@ -218,6 +235,8 @@ __device__ __forceinline__ uint32_t fx(Hot& h, const Mem& m, Con& cs, uint32_t p
                 hnz(h, v);
             } else {
                 h.p = (v & ~FL_B) | FL_U;
+                h.nv = h.p;
+                h.zv = ~h.p & FL_Z;
             }
         } else if constexpr (grp == G_JMP) {
             if constexpr (mode == M_IND) {
@@ -233,15 +252,17 @@ __device__ __forceinline__ uint32_t fx(Hot& h, const Mem& m, Con& cs, uint32_t p
                 if (npc == pc) return 0;   // the idle loop: the generic step runs it, then the fast-forward
             }
         } else if constexpr (grp == G_JSR) {
-            const uint32_t ret = (pc + 2u) & 0xFFFFu;
+            const uint32_t ret = pc + 2u;   // <= $FFFF
             hpush(h, m, ret >> 8);
             hpush(h, m, ret & 0xFFu);
             npc = base;
         } else if constexpr (grp == G_RTS) {
             const uint32_t l8 = hpull(h, m), h8 = hpull(h, m);
-            npc = (((h8 << 8) | l8) + 1u) & 0xFFFFu;
+            npc = ((h8 << 8) | l8) + 1u;
         } else if constexpr (grp == G_RTI) {
             h.p = (hpull(h, m) & ~FL_B) | FL_U;
+            h.nv = h.p;
+            h.zv = ~h.p & FL_Z;
             const uint32_t l8 = hpull(h, m), h8 = hpull(h, m);
             npc = (h8 << 8) | l8;
         }
@@ -266,10 +287,15 @@ __device__ __forceinline__ uint32_t fx(Hot& h, const Mem& m, Con& cs, uint32_t p
 template <uint32_t B>
 __device__ __forceinline__ uint32_t fast_step(Hot& h, const Mem& m, Con& cs, uint32_t* op_out) {
     const uint32_t pc = h.pc;
-    // code in PRG ($8000+) and the 3-byte window inside one 8 KB page: pc >= $8000 and (pc & $1FFF) <= $1FFD,
-    // as one compare ((pc + 2) & $9FFF keeps bit 15 and the page offset of the window's last byte)
-    if (((pc + 2u) & 0x9FFFu) < 0x8002u) return 0;
-    const uint32_t word = prg_wide(m, prg_index<B>(h, m, pc));
+    uint32_t word;
+    if constexpr (B == NES_BOARD_NROM) {
+        word = ((ConstU32*)m.cart.fetchw)[pc];   // pc <= $1007E (a branch just past $FFFF); $02 outside PRG
+    } else {
+        // code in PRG ($8000+) and the 3-byte window inside one 8 KB page: pc >= $8000 and (pc & $1FFF) <= $1FFD,
+        // as one compare ((pc + 2) & $9FFF keeps bit 15 and the page offset of the window's last byte)
+        if (((pc + 2u) & 0x9FFFu) < 0x8002u) return 0;
+        word = prg_wide(m, prg_index<B>(h, m, pc));
+    }
     const uint32_t op = word & 0xFFu, lo = (word >> 8) & 0xFFu, hi = (word >> 16) & 0xFFu;
     *op_out = op;
     switch (op) {
