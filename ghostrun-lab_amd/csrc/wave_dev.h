@@ -289,14 +289,16 @@ __device__ __forceinline__ uint32_t fast_step(Hot& h, const Mem& m, Con& cs, uin
     const uint32_t pc = h.pc;
     uint32_t word;
     if constexpr (B == NES_BOARD_NROM) {
-        word = ((ConstU32*)m.cart.fetchw)[pc];   // pc <= $1007E (a branch just past $FFFF); $02 outside PRG
+        // pc <= $1007E (a branch just past $FFFF); $02 outside PRG. The mask only tells the compiler that the
+        // index is a small 32-bit value, so the load takes it as a scalar byte offset (no 64-bit address add).
+        word = ((ConstU32*)m.cart.fetchw)[pc & 0x1FFFFu];
     } else {
         // code in PRG ($8000+) and the 3-byte window inside one 8 KB page: pc >= $8000 and (pc & $1FFF) <= $1FFD,
         // as one compare ((pc + 2) & $9FFF keeps bit 15 and the page offset of the window's last byte)
         if (((pc + 2u) & 0x9FFFu) < 0x8002u) return 0;
         word = prg_wide(m, prg_index<B>(h, m, pc));
     }
-    const uint32_t op = word & 0xFFu, lo = (word >> 8) & 0xFFu, hi = (word >> 16) & 0xFFu;
+    const uint32_t op = word & 0xFFu, lo = (word >> 8) & 0xFFu, hi = word >> 16;   // bits 24-31 are 0
     *op_out = op;
     switch (op) {
         ND_FX16(0x00) ND_FX16(0x10) ND_FX16(0x20) ND_FX16(0x30) ND_FX16(0x40) ND_FX16(0x50) ND_FX16(0x60)
