@@ -127,9 +127,16 @@ def cart_of(w, seed):
     return synth.nrom_cart(seed) if w['cart'] == 'nrom' else synth.mmc3_cart(seed)
 
 
+# Boot: the reference records each game's boot pad bytes from power-on through its boot sequence and takes the
+# boot snapshot after them (rl/rlenv.py:142-170, rl/csrc/rlenv_build.hpp:193-209), so a restart resumes at the end of
+# the boot, never at power-on. The seed-generated carts boot in 4 frames (two vblank waits, RAM clear, palette and
+# nametable upload); their boot sequence is 4 neutral pad bytes.
+BOOT_FRAMES = 4
+
+
 def env_kwargs(w, args, cart):
     kw = dict(seed=args.seed, sticky=w['sticky'], idle_max=0, dropout=w['dropout'], pad_mode=True, ram_hash=True,
-              roms={'smb': cart}, end_prob=w['end_prob'])
+              roms={'smb': cart}, end_prob=w['end_prob'], boot={'smb': bytes(BOOT_FRAMES)})
     if w['dropout']:
         kw['dropout_gap'] = 1 / 60   # mean gap 60 decisions, mean run 15: 20 % of decisions with a dropped input
     return kw

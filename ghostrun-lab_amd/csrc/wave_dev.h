@@ -83,8 +83,8 @@ __device__ __forceinline__ uint32_t hpull(Hot& h, const Mem& m) {
     return rd8(m, 0x100u | h.sp);
 }
 
-// Controller port 1 ($4016), the one I/O register the fast path serves itself: the same read and write as the
-// bus (nes_dev.h io_read / io_write), on the console state in LDS.
+// Controller port 1 ($4016), one of the two I/O registers the fast path serves itself: the same read and write as
+// the bus (nes_dev.h io_read / io_write), on the console state in LDS.
 __device__ __forceinline__ uint32_t port_read(Con& cs) {
     uint32_t bit;
     if (uni(cs.strobe)) {
@@ -95,6 +95,17 @@ __device__ __forceinline__ uint32_t port_read(Con& cs) {
         cs.shift = (s >> 1) | 0x80u;
     }
     return 0x40u | bit;
+}
+// PPU status ($2002 and its mirrors): the bus's read (nes_dev.h io_read) - the value, then vblank and the write
+// toggle cleared. Status bits change only at PPU events, and the fast path runs only short of the next one, so the
+// status in the console state is the one the read sees.
+__device__ __forceinline__ uint32_t status_read(Con& cs) {
+    const uint32_t st = uni(cs.status);
+    const uint32_t v = (st & 0xE0u) | (uni(cs.open_bus) & 0x1Fu);
+    cs.status = st & 0x7Fu;
+    cs.w = 0;
+    cs.open_bus = v;
+    return v;
 }
 __device__ __forceinline__ void port_write(Con& cs, uint32_t v) {
     cs.strobe = v & 1u;
@@ -148,9 +159,9 @@ __device__ __forceinline__ uint32_t fx(Hot& h, const Mem& m, Con& cs, uint32_t p
             if constexpr (pen) cyc += ((b2 ^ ea) & 0xFF00u) ? 1u : 0u;
         }
         // Memory class, decided before any side effect (every check below comes before the first state change):
-        // RAM, PRG reads and the controller port run here; any other I/O register, a read-modify-write outside RAM
-        // and any write at $8000+ (a mapper) go to the generic step. Written as chains of single compares: boolean
-        // combinations of uniform conditions become lane-mask arithmetic.
+        // RAM, PRG reads, the controller port and PPU status reads run here; any other I/O register, a
+        // read-modify-write outside RAM and any write at $8000+ (a mapper) go to the generic step. Written as
+        // chains of single compares: boolean combinations of uniform conditions become lane-mask arithmetic.
         if constexpr (!zpage && rd && wr) {
             if (ea >= 0x2000u) return 0;
         }
@@ -167,6 +178,7 @@ __device__ __forceinline__ uint32_t fx(Hot& h, const Mem& m, Con& cs, uint32_t p
                 if (ea < 0x2000u) opd = rd8(m, ea & 0x7FFu);
                 else if (ea >= 0x8000u) opd = prg_wide(m, prg_index<B>(h, m, ea)) & 0xFFu;
                 else if (ea == 0x4016u) opd = port_read(cs);
+                else if ((ea & 0xE007u) == 0x2002u) opd = status_read(cs);
                 else return 0;
             }
         }

@@ -35,6 +35,17 @@ def test_smb_like_raw_pads_level_end_and_ends():
 
 
 @pytest.mark.gpu
+def test_boot_sequence_snapshot_and_restarts():
+    """Boot pads run on the device before the snapshot (rl/csrc/rlenv_build.hpp:193-209): restarts resume after the
+    cart's 4-frame boot, as the reference's recorded boot sequences do."""
+    print('case: NROM seed 5, 16 consoles, boot 4 neutral + 2 pressed frames, Geometric(1/6) ends, 24 decisions',
+          flush=True)
+    cpu, gpu = pair(16, synth.nrom_cart(5), seed=13, sticky=True, idle_max=2, dropout=True, pad_mode=True,
+                    end_prob=1 / 6, boot={'smb': bytes(4) + bytes((0x80, 0x81))})
+    run(cpu, gpu, 24, 5, True)
+
+
+@pytest.mark.gpu
 def test_full_size_console_independence():
     """8192 consoles; with no per-console randomness (no sticky, dropout, idle or synthetic ends) a console's
     outputs depend only on its own pad stream, so consoles 0, 4095 and 8191 must equal an oracle run of those
