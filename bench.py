@@ -49,6 +49,7 @@ METRIC = 'emulated NES frames/sec and decisions/sec at 8192 consoles, 1 MI355X'
 ORACLE_LIB = ROOT / 'oracle' / '_build' / 'liboracle_rlenv.so'
 COUNTERS = ROOT / 'profiles' / 'counters.json'
 HBM_PEAK_GBPS = 8000.0
+SALU_PEAK = 256 * 2.4e9                    # one scalar ALU per CU (256 CUs) at the 2.4 GHz peak engine clock
 KERNELS = ('k_emu', 'k_render', 'k_finish', 'k_reset_copy', 'k_emu_restart', 'k_render_restart', 'k_reset_finish',
            'k_decision')
 
@@ -271,6 +272,9 @@ def bench_env(args):
                step_output_gbps=round(out_bytes * N * K / dt / 1e9, 3))
     if kern:
         out['roofline'] = _roofline(kern, N)
+        iss = _issue_roofline(args.workload, kern, K, dt, out['emulated_instructions_per_s'])
+        if iss:
+            out['issue_roofline'] = iss
         out['kernels'] = kern
         counters = _counters(args.workload)
         if counters:
@@ -306,8 +310,30 @@ def _roofline(kern, n):
              frac=round(d['achieved_gbps'] / HBM_PEAK_GBPS, 6), traffic=_traffic(dom, n))
     if dom in ('k_emu', 'k_emu_restart'):
         r['note'] = ('the 6502 interpreter: one console per wavefront on the scalar unit, bound by scalar issue '
-                     '(see counters), not by HBM; its algorithmic bytes are the action read and the pad byte written')
+                     '(issue_roofline), not by HBM; its algorithmic bytes are the action read and the pad byte written')
     return r
+
+
+def _issue_roofline(workload, kern, K, dt, ips):
+    """Scalar-issue roofline of the emulator kernel: SALU instructions per second against one scalar ALU per CU at
+    the peak engine clock. SALU instructions per emulated instruction come from the committed counter run of the same
+    workload (SQ_INSTS_SALU); the emulated instructions and the kernel's time are measured in this run. VALU
+    utilisation of the two frame kernels is reported beside it from the same counter run."""
+    c = _counters(workload) or {}
+    e = c.get('k_emu')
+    if not e or 'k_emu' not in kern:
+        return None
+    restart = kern.get('k_emu_restart', {}).get('ms_per_step', 0.0)
+    if restart > 0.05 * kern['k_emu']['ms_per_step']:
+        return None                          # restart frames would count in the instructions but not in k_emu time
+    salu = e['per_emulated_instruction']['salu']
+    emu_s = kern['k_emu']['ms_per_step'] * K / 1e3
+    achieved = ips * dt / emu_s * salu
+    out = dict(kernel='k_emu', bound='salu', unit='SALU instr/s', achieved=round(achieved / 1e9, 1) * 1e9,
+               peak=SALU_PEAK, frac=round(achieved / SALU_PEAK, 4), salu_per_emulated_instruction=salu,
+               counter_SALUBusy_pct=e.get('SALUBusy_pct'))
+    out['valu_busy_pct'] = {k: v.get('VALUBusy_pct') for k, v in c.items() if isinstance(v, dict)}
+    return out
 
 
 def _summary():
@@ -315,8 +341,11 @@ def _summary():
 
 
 def _counters(workload):
-    """Issue and utilisation figures of the dominant kernels from the committed counter summary, if present."""
-    return _summary().get('workloads', {}).get(workload)
+    """Issue and utilisation figures of the frame kernels from the committed counter summary, if present."""
+    keep = ('kernel', 'SALUBusy_pct', 'VALUBusy_pct', 'VALUUtilization_pct', 'per_emulated_instruction',
+            'wave_state_pct')
+    w = _summary().get('workloads', {}).get(workload)
+    return {k: {f: v[f] for f in keep if f in v} for k, v in w.items()} if w else None
 
 
 def _traffic(kernel, n):
