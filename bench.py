@@ -51,7 +51,7 @@ COUNTERS = ROOT / 'profiles' / 'counters.json'
 HBM_PEAK_GBPS = 8000.0
 SALU_PEAK = 256 * 2.4e9                    # one scalar ALU per CU (256 CUs) at the 2.4 GHz peak engine clock
 KERNELS = ('k_emu', 'k_render', 'k_finish', 'k_reset_copy', 'k_emu_restart', 'k_render_restart', 'k_reset_finish',
-           'k_decision')
+           'k_emu_idle', 'k_archive')
 
 # Algorithmic bytes per console per launch (outputs written + inputs read by the path, not state traffic).
 PICTURE_BYTES = 224 * 240 + 224            # one frame's colour indices + emphasis
@@ -63,9 +63,10 @@ ALG_BYTES = {
     'k_emu_restart': 0,
     'k_render_restart': 0,
     'k_reset_finish': 19 + 360,             # masks, timeline
+    'k_emu_idle': 0,
+    'k_archive': 0,
 }
 DECISION_BYTES = 4 * (PICTURE_BYTES + 1) + 2 + 4 + 1 + 4 + 28 + 19 + 360   # 216,358 B per console per decision
-ALG_BYTES['k_decision'] = DECISION_BYTES + 8
 PACK6_BYTES = 4 * 224 * 240 * 3 // 4 + 896 + 420                       # 162,596 B per console per decision
 RL10_STEP_BYTES = 20                                                      # 15 RAM bytes read + f32 reward + done
 

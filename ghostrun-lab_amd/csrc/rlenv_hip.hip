@@ -48,6 +48,7 @@ struct EnvArrays {
     float* ep_ret;
     int32_t *ep_len, *ep_maxlvl, *ep_idle;
     uint8_t* resetting;
+    int32_t* ep_start;     // [N] slot the episode started from, -1 = boot snapshot; nullptr without level starts
 };
 
 struct Outs {
@@ -56,12 +57,29 @@ struct Outs {
     float *reward, *info, *parts;
     uint32_t* events;
     uint64_t* ram_hash;
+    int32_t *start_out, *level_out;   // level starts: start slot of a finished episode, level after the decision
+    float* progress_out;              // within-level progress / progress unit, NaN = not valid
 };
 
 struct Settings {
     uint64_t run_seed;
     int sticky, idle_max, idle_tmpl, dropout, no_render, episode_level_end, pad_mode;
     uint32_t end_p32, gap_p32;
+};
+
+// Saved level starts and places of one game (rl/csrc/rlenv_core.cuh:60-74): slot s < levels is level s, saved on the
+// tracker's level event; slots levels..cap-1 are places, saved on request. A saved console is a whole record.
+struct LevelK {
+    int cap, levels;                 // cap 0: off
+    NesRec* rec;                     // [cap]
+    Rl10State* st;                   // [cap]
+    uint64_t* target;                // [cap]
+    uint32_t* frame;                 // [cap]
+    int32_t* deaths;                 // [cap], -1 = nothing saved
+    unsigned long long* claim;       // [cap] (deaths << 32 | env) of this decision's best arrival, ~0 = none
+    uint32_t* cdf;                   // [cap] cumulative slot weights * 2^32
+    uint32_t thresh;                 // P(a new episode starts from a saved slot) * 2^32
+    int weighted;                    // 1: pick by cdf, 0: uniform over the saved slots
 };
 
 struct GameK {
@@ -72,9 +90,10 @@ struct GameK {
     uint64_t tmpl_target;
     int32_t* list;         // restart list (env index within the game)
     uint32_t* list_count;
+    LevelK lv;
 };
 
-enum : int { EMU_DECISION = 0, EMU_RESTART = 1, EMU_BOOT = 2 };
+enum : int { EMU_DECISION = 0, EMU_RESTART = 1, EMU_BOOT = 2, EMU_IDLE = 3 };
 
 struct EmuArgs {
     GameK g;
@@ -214,6 +233,14 @@ __global__ __launch_bounds__(64) void k_emu_w(EmuArgs a) {
     const int e = a.mode == EMU_BOOT ? a.e0 : slot_env(a.g, a.use_list, a.e0, k);
     const int ge = a.g.offset + e;
     if (a.mode == EMU_RESTART && a.e.resetting[ge] == 0) return;
+    // EMU_IDLE: a restart from a saved level start emulates all of its idle frames (pad 0) in this one launch; a
+    // restart from the boot snapshot copied a template that holds them (rl/csrc/rlenv_core.cuh:312-318)
+    int frames = 1;
+    if (a.mode == EMU_IDLE) {
+        if (a.e.resetting[ge] == 0 || a.e.ep_start == nullptr || a.e.ep_start[ge] < 0) return;
+        frames = a.e.ep_idle[ge];
+        if (frames <= 0) return;
+    }
     NesRec* rec = &a.g.recs[e];
     wave_copy16(L.ram, rec->ram, NES_RAM_BYTES, lane);
     wave_copy16(L.nt, rec->nt, NES_NT_BYTES, lane);
@@ -233,19 +260,23 @@ __global__ __launch_bounds__(64) void k_emu_w(EmuArgs a) {
         }
         Con& cs = L.cs;
         con_load(cs, rec);
-        cs.pad = pad;
         const Mem m{rec, L.ram, L.nt, L.oam, L.pal, a.g.cart};
-        if (fault == 0) {
-            const uint32_t f = run_until_wave<B>(cs, m, c_optab.t, target, a.budget);
-            if (f != 0) {
-                if (a.mode == EMU_BOOT) atomicOr(a.boot_fault, 1u);
-                else a.e.fault[ge] = f;
+        for (int i = 0; i < frames; ++i) {   // a faulted console stays put; its target and frame still advance
+            cs.pad = pad;
+            if (fault == 0) {
+                const uint32_t f = run_until_wave<B>(cs, m, c_optab.t, target, a.budget);
+                if (f != 0) {
+                    if (a.mode == EMU_BOOT) atomicOr(a.boot_fault, 1u);
+                    else a.e.fault[ge] = f;
+                    fault = f;
+                }
             }
+            target += NES_FRAME_DOTS;
         }
         con_store(cs, rec);
         if (a.mode != EMU_BOOT) {
-            a.e.target[ge] = target + NES_FRAME_DOTS;
-            a.e.ep_frame[ge] += 1u;
+            a.e.target[ge] = target;
+            a.e.ep_frame[ge] += (uint32_t)frames;
         }
     }
     __syncthreads();
@@ -409,12 +440,35 @@ __device__ __forceinline__ void reset_rl(const GameK& g, const EnvArrays& e, con
     uint64_t ctr = 0;
     int idle = 0;
     if (s.idle_max > 0) idle = (int)ev::rnd_below(sseed, ctr, (uint32_t)(s.idle_max + 1));
+    // a level start? (rl/csrc/rlenv_core.cuh:220-236: drawn only when level starts are on, after the idle count)
+    int lv = -1;
+    const LevelK& L = g.lv;
+    if (L.cap > 0 && L.thresh != 0 && ev::rnd32(sseed, ctr) < L.thresh) {
+        uint32_t saved = 0;
+        for (int q = 0; q < L.cap; ++q) saved += L.deaths[q] >= 0 ? 1u : 0u;
+        if (L.weighted) {
+            const uint32_t u = ev::rnd32(sseed, ctr);
+            for (int q = 0; q < L.cap && lv < 0; ++q)
+                if (u < L.cdf[q]) lv = q;
+        } else if (saved > 0) {
+            uint32_t pick = ev::rnd_below(sseed, ctr, saved);
+            for (int q = 0; q < L.cap && lv < 0; ++q)
+                if (L.deaths[q] >= 0 && pick-- == 0) lv = q;
+        }
+    }
     e.sticky_seed[ge] = sseed;
     e.sticky_ctr[ge] = ctr;
-    const int k = idle <= s.idle_tmpl ? idle : 0;
-    e.target[ge] = g.tmpl_target + (uint64_t)k * NES_FRAME_DOTS;
-    e.ep_frame[ge] = (uint32_t)k;
-    e.st[ge] = Rl10State{};
+    if (lv >= 0) {
+        e.target[ge] = L.target[lv];
+        e.ep_frame[ge] = L.frame[lv];
+        e.st[ge] = L.st[lv];
+    } else {
+        const int k = idle <= s.idle_tmpl ? idle : 0;
+        e.target[ge] = g.tmpl_target + (uint64_t)k * NES_FRAME_DOTS;
+        e.ep_frame[ge] = (uint32_t)k;
+        e.st[ge] = Rl10State{};
+    }
+    if (e.ep_start) e.ep_start[ge] = lv;
     e.fault[ge] = 0;
     Dropout d;
     ev::drop_reset(d, seed, s.dropout != 0, s.gap_p32);
@@ -475,7 +529,17 @@ __global__ __launch_bounds__(256) void k_finish(FinishArgs a) {
         Dropout d = a.e.drop[ge];
         ev::drop_advance(d, a.s.dropout != 0, a.s.gap_p32);
         a.e.drop[ge] = d;
+        // level-start claim: the arrival with the fewest deaths, then the lowest env index (rlenv_core.cuh:288-291)
+        if (a.g.lv.cap > 0 && !done && (u.events & ev::EV_LEVEL) && u.event_level >= 0 && u.event_level < a.g.lv.levels) {
+            const unsigned long long dd = (unsigned long long)(uint32_t)(st.deaths < 0 ? 0 : st.deaths);
+            atomicMin(&a.g.lv.claim[u.event_level], (dd << 32) | (uint32_t)e);
+        }
+        if (a.o.level_out) a.o.level_out[ge] = st.has_best_level ? st.best_level : -1;
+        if (a.o.progress_out)
+            a.o.progress_out[ge] = st.has_prev && st.prev.progress_valid ? (float)(st.prev.progress / ev::kSmbUnit)
+                                                                          : __builtin_nanf("");
         if (done) {
+            if (a.o.start_out) a.o.start_out[ge] = a.e.ep_start ? a.e.ep_start[ge] : -1;
             float* inf = a.o.info + (size_t)ge * RLE_INFO;
             inf[0] = ret;
             inf[1] = (float)len;
@@ -508,8 +572,10 @@ __global__ __launch_bounds__(256) void k_reset_copy(FinishArgs a) {
     for (uint32_t k = blockIdx.x; k < count; k += gridDim.x) {
         const int e = a.g.list[k];
         const int idle = a.e.ep_idle[a.g.offset + e];
+        const int lv = a.e.ep_start ? a.e.ep_start[a.g.offset + e] : -1;
         const int t = idle <= a.s.idle_tmpl ? idle : 0;
-        const uint4* src = reinterpret_cast<const uint4*>(t == 0 ? &a.g.recs[a.g.n] : &a.g.idle[t - 1]);
+        const uint4* src = reinterpret_cast<const uint4*>(lv >= 0 ? &a.g.lv.rec[lv]
+                                                          : t == 0 ? &a.g.recs[a.g.n] : &a.g.idle[t - 1]);
         uint4* dst = reinterpret_cast<uint4*>(&a.g.recs[e]);
         for (uint32_t i = threadIdx.x; i < NES_REC_BYTES / 16u; i += blockDim.x) dst[i] = src[i];
     }
@@ -529,7 +595,8 @@ __global__ __launch_bounds__(256) void k_reset_finish(FinishArgs a) {
             a.e.st[ge] = st;
             a.e.ep_ret[ge] = 0.0f;
             a.e.ep_len[ge] = 0;
-            a.e.ep_maxlvl[ge] = 0;
+            const int sl = a.e.ep_start ? a.e.ep_start[ge] : -1;   // a place: its level is the tracker's
+            a.e.ep_maxlvl[ge] = sl >= a.g.lv.levels ? (st.has_best_level ? st.best_level : 0) : sl > 0 ? sl : 0;
             a.e.resetting[ge] = 0;
         }
         const Dropout* d = &a.e.drop[ge];
@@ -560,219 +627,55 @@ __global__ void k_list_clear(uint32_t* count) {
     if (threadIdx.x == 0 && blockIdx.x == 0) *count = 0;
 }
 
-#ifdef RLENV_FUSED_KERNEL
-// ------------------------------------------------------------------------------------- fused decision
-// k_decision: one wavefront owns one console for a whole decision (or a start). Lane 0 runs the emulator on the
-// scalar unit and the RL bookkeeping; all 64 lanes move the console between HBM and LDS, draw each frame, hash
-// the RAM and copy the boot snapshot on a restart. The phase order per console is the reference's
-// (rl/csrc/rlenv_core.cuh:389-414): 4 x (frame, render), finish, [restart: snapshot, 4 x (neutral frame, render),
-// first tracker update], masks + timeline. Every phase is a function of the console's own state, so running them
-// console by console equals running each phase over all consoles.
-enum : int { DEC_STEP = 0, DEC_START = 1 };
-
-struct DecArgs {
-    GameK g;
-    EnvArrays e;
-    Outs o;
-    Settings s;
-    int mode, e0, e1;
-    uint32_t budget;
-};
-
-// RAM hash by the 64 lanes: lane l hashes words 8l..8l+7, then a butterfly sum (integer addition mod 2^64, so the
-// order does not change the result).
-__device__ __forceinline__ uint64_t ram_hash_wave(const uint8_t* ram, int lane) {
-    const uint4* w = reinterpret_cast<const uint4*>(ram) + 2 * lane;
-    uint64_t h = 0;
-    for (int j = 0; j < 2; ++j) {
-        const uint4 q = w[j];
-        const uint64_t k = 8u * (uint32_t)lane + 4u * (uint32_t)j;
-        h += ev::mix64((k << 32) | q.x);
-        h += ev::mix64(((k + 1u) << 32) | q.y);
-        h += ev::mix64(((k + 2u) << 32) | q.z);
-        h += ev::mix64(((k + 3u) << 32) | q.w);
+// Level-start saves after a decision's finish, one workgroup per level slot (rl/csrc/rlenv_core.cuh:343-387): the
+// claimed arrival replaces the saved one when nothing is saved yet or it has no more deaths (the newest on ties).
+// The claim is wave-uniform per workgroup, so every thread takes the same branch.
+__global__ __launch_bounds__(256) void k_archive(FinishArgs a) {
+    const int q = (int)blockIdx.x;
+    const LevelK& L = a.g.lv;
+    const unsigned long long cl = L.claim[q];
+    if (cl == ~0ull) return;
+    const bool take = L.deaths[q] < 0 || (int32_t)(cl >> 32) <= L.deaths[q];
+    const int e = (int)(cl & 0xFFFFFFFFull);
+    if (take) {
+        const uint4* src = reinterpret_cast<const uint4*>(&a.g.recs[e]);
+        uint4* dst = reinterpret_cast<uint4*>(&L.rec[q]);
+        for (uint32_t i = threadIdx.x; i < NES_REC_BYTES / 16u; i += blockDim.x) dst[i] = src[i];
     }
-    for (int off = 32; off > 0; off >>= 1) {
-        const uint32_t lo = __shfl_xor((uint32_t)h, off), hi = __shfl_xor((uint32_t)(h >> 32), off);
-        h += ((uint64_t)hi << 32) | lo;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        if (take) {
+            const int ge = a.g.offset + e;
+            L.st[q] = a.e.st[ge];
+            L.target[q] = a.e.target[ge];
+            L.frame[q] = a.e.ep_frame[ge];
+            L.deaths[q] = (int32_t)(cl >> 32);
+        }
+        L.claim[q] = ~0ull;
     }
-    return h;
 }
 
-// Console record (HBM) -> LDS memories, and the console state for lane 0.
-__device__ __forceinline__ void console_in(WaveLds& L, const NesRec* rec, int lane) {
-    wave_copy16(L.ram, rec->ram, NES_RAM_BYTES, lane);
-    wave_copy16(L.nt, rec->nt, NES_NT_BYTES, lane);
-    wave_copy16(L.oam, rec->oam, NES_OAM_BYTES, lane);
-    wave_copy16(L.pal, rec->pal, NES_PAL_BYTES, lane);
-    if (lane == 0) con_load(L.cs, rec);
-}
-
-__device__ __forceinline__ void console_out(WaveLds& L, NesRec* rec, int lane) {
-    if (lane == 0) con_store(L.cs, rec);
-    wave_copy16(rec->ram, L.ram, NES_RAM_BYTES, lane);
-    wave_copy16(rec->nt, L.nt, NES_NT_BYTES, lane);
-    wave_copy16(rec->oam, L.oam, NES_OAM_BYTES, lane);
-    wave_copy16(rec->pal, L.pal, NES_PAL_BYTES, lane);
-}
-
-// One emulated frame of the console in LDS (lane 0): the env's frame step (rl/csrc/rlenv_core.cuh:160-177).
-template <uint32_t B>
-__device__ __forceinline__ void frame_lane0(const DecArgs& a, WaveLds& L, const Mem& m, int ge, uint32_t pad) {
-    const uint64_t target = a.e.target[ge];
-    L.cs.pad = pad;
-    if (a.e.fault[ge] == 0) {
-        const uint32_t f = run_until_wave<B>(L.cs, m, c_optab.t, target, a.budget);
-        if (f != 0) a.e.fault[ge] = f;
-    }
-    a.e.target[ge] = target + NES_FRAME_DOTS;
-    a.e.ep_frame[ge] += 1u;
-}
-
-// Finish of the decision (lane 0): rl/csrc/rlenv_core.cuh:266-309. Returns whether the episode ended (then the RL
-// state is already reset for the next one).
-__device__ __forceinline__ bool finish_lane0(const DecArgs& a, const WaveLds& L, int ge) {
-    uint8_t b15[15];
-    ev::smb_gather(L.ram, b15);
-    const Rl10Signals sig = ev::smb_signals(b15);
-    Rl10State st = a.e.st[ge];
-    const ev::Out u = ev::smb_update(sig, RLE_FRAMES, st);
-    a.e.st[ge] = st;
-    const bool faulted = a.e.fault[ge] != 0;
-    const bool level_clear = !u.done && !faulted && a.s.episode_level_end >= 0 && (u.events & ev::EV_LEVEL) &&
-                             u.event_level == a.s.episode_level_end + 1;
-    bool synthetic = false;
-    if (a.s.end_p32 != 0 && !u.done && !faulted && !level_clear) {
-        uint64_t ctr = (uint64_t)(uint32_t)a.e.ep_len[ge];
-        const uint64_t es = ev::mix64(ev::ep_seed(a.s.run_seed, (uint32_t)ge, a.e.episode[ge]) ^ 0xE9D5EEDull);
-        synthetic = ev::rnd32(es, ctr) < a.s.end_p32;
-    }
-    const bool done = u.done || faulted || level_clear || synthetic;
-    const float r = faulted ? 0.0f : (float)u.reward;
-    a.o.reward[ge] = r;
-    if (a.o.parts)
-        for (int q = 0; q < RLE_PARTS; ++q) a.o.parts[(size_t)ge * RLE_PARTS + q] = faulted ? 0.0f : (float)u.part[q];
-    a.o.done[ge] = done ? 1 : 0;
-    a.o.events[ge] = u.events;
-    const float ret = a.e.ep_ret[ge] + r;
-    a.e.ep_ret[ge] = ret;
-    const int32_t len = a.e.ep_len[ge] + 1;
-    a.e.ep_len[ge] = len;
-    if (u.event_level > a.e.ep_maxlvl[ge]) a.e.ep_maxlvl[ge] = u.event_level;
-    Dropout d = a.e.drop[ge];
-    ev::drop_advance(d, a.s.dropout != 0, a.s.gap_p32);
-    a.e.drop[ge] = d;
-    if (done) {
-        float* inf = a.o.info + (size_t)ge * RLE_INFO;
-        inf[0] = ret;
-        inf[1] = (float)len;
-        inf[2] = (float)(faulted ? RLE_END_FAULT : level_clear ? RLE_END_LEVEL_CLEAR
-                                                               : synthetic ? RLE_END_SYNTHETIC : st.end_reason);
-        inf[3] = (float)st.deaths;
-        inf[4] = (float)a.e.ep_maxlvl[ge];
-        inf[5] = st.overflow ? 1.0f : 0.0f;
-        inf[6] = (float)a.e.ep_idle[ge];
-        inf[7] = (float)a.e.episode[ge];
-        reset_rl(a.g, a.e, a.s, ge);
-    }
-    return done;
-}
-
-// First tracker update of a new episode, then masks and timeline (lane 0): rl/csrc/rlenv_core.cuh:138-148, 327-342.
-__device__ __forceinline__ void controls_lane0(const DecArgs& a, const WaveLds& L, int ge) {
-    if (a.e.resetting[ge]) {
-        uint8_t b15[15];
-        ev::smb_gather(L.ram, b15);
+// Place saves (rl/csrc/rlenv.cu:100-108): workgroup j copies env env[j] of the game into slot slot[j], skipped where
+// the slot is a level slot or out of range. The no-progress clock restarts at a place (rlenv_core.cuh:366-375).
+__global__ __launch_bounds__(256) void k_place_save(FinishArgs a, const int32_t* env, const int32_t* slot) {
+    const int q = slot[blockIdx.x], e = env[blockIdx.x];
+    const LevelK& L = a.g.lv;
+    if (q < L.levels || q >= L.cap || e < 0 || e >= a.g.n) return;
+    const uint4* src = reinterpret_cast<const uint4*>(&a.g.recs[e]);
+    uint4* dst = reinterpret_cast<uint4*>(&L.rec[q]);
+    for (uint32_t i = threadIdx.x; i < NES_REC_BYTES / 16u; i += blockDim.x) dst[i] = src[i];
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        const int ge = a.g.offset + e;
         Rl10State st = a.e.st[ge];
-        (void)ev::smb_update(ev::smb_signals(b15), a.e.ep_idle[ge] + RLE_FRAMES, st);
-        a.e.st[ge] = st;
-        a.e.ep_ret[ge] = 0.0f;
-        a.e.ep_len[ge] = 0;
-        a.e.ep_maxlvl[ge] = 0;
-        a.e.resetting[ge] = 0;
-    }
-    const Dropout* d = &a.e.drop[ge];
-    const int dr = ev::dropped_now(d);
-    uint8_t* mk = a.o.masks + (size_t)ge * RLE_MASK_BYTES;
-    for (uint32_t i = 0; i < 9; ++i) mk[i] = (dr >= 0 && dr < 4 && (ev::dpad_bits(i) & (ev::B_UP << dr))) ? 0 : 1;
-    mk[9] = 1;
-    mk[10] = dr == 4 ? 0 : 1;
-    mk[11] = dr == 6 ? 0 : 1;
-    mk[12] = 1;
-    mk[13] = dr == 5 ? 0 : 1;
-    mk[14] = dr == 7 ? 0 : 1;
-    mk[15] = 1;
-    mk[16] = a.g.start_ok ? 1 : 0;
-    mk[17] = 1;
-    mk[18] = a.g.select_ok ? 1 : 0;
-    uint32_t* tl = reinterpret_cast<uint32_t*>(a.o.tl + (size_t)ge * RLE_TIMELINE_BYTES);
-    for (int i = 0; i < RLE_TIMELINE_BYTES / 4; ++i) tl[i] = 0;
-    uint8_t* tb = a.o.tl + (size_t)ge * RLE_TIMELINE_BYTES;
-    for (uint32_t j = 0; j < RLE_TIMELINE; ++j) {
-        const int b = d->ring[(d->head + j) & (RLC_RING - 1)];
-        if (b >= 0) tb[b * RLE_TIMELINE + j] = 1;
+        st.idle_frames = 0;
+        L.st[q] = st;
+        L.target[q] = a.e.target[ge];
+        L.frame[q] = a.e.ep_frame[ge];
+        L.deaths[q] = 0;
     }
 }
 
-template <uint32_t B>
-__global__ __launch_bounds__(64) void k_decision(DecArgs a) {
-    __shared__ __align__(16) WaveLds L;
-    __shared__ __align__(16) uint8_t pal_r[32];
-    __shared__ int restart_s;
-    const int e = a.e0 + (int)blockIdx.x;
-    if (e >= a.e1) return;
-    const int lane = (int)threadIdx.x;
-    const int ge = a.g.offset + e;
-    NesRec* rec = &a.g.recs[e];
-    const Mem m{rec, L.ram, L.nt, L.oam, L.pal, a.g.cart};
-    const bool render = a.s.no_render == 0;
-    if (a.mode == DEC_STEP) {
-        console_in(L, rec, lane);
-        __syncthreads();
-        for (int f = 0; f < RLE_FRAMES; ++f) {
-            if (lane == 0) frame_lane0<B>(a, L, m, ge, decision_pad(a, ge, f));
-            __syncthreads();
-            if (render)
-                render_wave(rec, L.cs.log_n, L.nt, L.oam, pal_r, a.g.cart,
-                            a.o.obs + ((size_t)ge * RLE_FRAMES + f) * RLE_OBS_PIXELS,
-                            a.o.emph + ((size_t)ge * RLE_FRAMES + f) * RLE_OBS_H, lane);
-        }
-        if (a.o.ram_hash) {
-            const uint64_t h = ram_hash_wave(L.ram, lane);
-            if (lane == 0) a.o.ram_hash[ge] = h;
-        }
-        if (lane == 0) restart_s = finish_lane0(a, L, ge) ? 1 : 0;
-    } else {
-        if (lane == 0) {
-            reset_rl(a.g, a.e, a.s, ge);
-            restart_s = 1;
-        }
-    }
-    __syncthreads();
-    if (restart_s) {
-        const int idle = a.e.ep_idle[ge];
-        const int t = idle <= a.s.idle_tmpl ? idle : 0;
-        const NesRec* src = t == 0 ? &a.g.recs[a.g.n] : &a.g.idle[t - 1];
-        __syncthreads();
-        wave_copy16(rec, src, NES_REC_BYTES, lane);
-        __syncthreads();
-        console_in(L, rec, lane);
-        __syncthreads();
-        for (int f = 0; f < RLE_FRAMES; ++f) {
-            if (lane == 0) frame_lane0<B>(a, L, m, ge, 0u);
-            __syncthreads();
-            if (render)
-                render_wave(rec, L.cs.log_n, L.nt, L.oam, pal_r, a.g.cart,
-                            a.o.obs + ((size_t)ge * RLE_FRAMES + f) * RLE_OBS_PIXELS,
-                            a.o.emph + ((size_t)ge * RLE_FRAMES + f) * RLE_OBS_H, lane);
-        }
-    }
-    if (lane == 0) controls_lane0(a, L, ge);
-    __syncthreads();
-    console_out(L, rec, lane);
-}
-
-#endif  // RLENV_FUSED_KERNEL
 
 // ------------------------------------------------------------------------------------- codec, gathers
 // pack6: 4 colour indices (6 bits) -> 3 bytes, little-endian v = p0 | p1 << 6 | p2 << 12 | p3 << 18
@@ -880,8 +783,8 @@ struct GameH {
 
 // Kernel classes of a decision, for the per-kernel clock (rlenv_kernel_times).
 enum KClass : int {
-    KC_EMU = 0, KC_RENDER, KC_FINISH, KC_RESET_COPY, KC_EMU_RESTART, KC_RENDER_RESTART, KC_RESET_FINISH, KC_DECISION,
-    KC_COUNT
+    KC_EMU = 0, KC_RENDER, KC_FINISH, KC_RESET_COPY, KC_EMU_RESTART, KC_RENDER_RESTART, KC_RESET_FINISH, KC_EMU_IDLE,
+    KC_ARCHIVE, KC_COUNT
 };
 
 // Optional per-launch HIP-event clock: when on, every launch of a decision is bracketed by two events on its
@@ -947,9 +850,8 @@ struct Env {
     uint32_t* optab = nullptr;
     int cpw = 16;
     bool emu_wave = true;    // k_emu_w (one console per wavefront); RLENV_EMU=lane selects k_emu
-    bool fused = false;      // per-phase kernels; RLENV_FUSED=1 selects one k_decision launch per decision (a build
-                             // with -DRLENV_FUSED_KERNEL)
     uint32_t budget = NES_BUDGET;
+    int lv_cap = 0;          // level starts / places per game (0 = off)
     mutable KernelClock clock;
 };
 
@@ -1013,18 +915,20 @@ void launch_emu(const Env& env, const GameK& g, const Outs& o, int mode, int f, 
                 hipStream_t st) {
     EmuArgs a{g, env.e, o, env.s, env.optab, mode, f, env.cpw, use_list ? 1 : 0, e0, e1, 0, 0, nullptr, env.budget};
     const int n = use_list ? g.n : e1 - e0;
-    const int blocks = env.emu_wave ? n : (n + env.cpw - 1) / env.cpw;
+    const bool wave = env.emu_wave || mode == EMU_IDLE;   // the idle-frame pass exists in the wave kernel only
+    const int blocks = wave ? n : (n + env.cpw - 1) / env.cpw;
     const size_t lds = 1024u + (size_t)env.cpw * kRamStride;
+    const int cls = mode == EMU_DECISION ? KC_EMU : mode == EMU_IDLE ? KC_EMU_IDLE : KC_EMU_RESTART;
     if (blocks > 0)
-        env.clock.run(mode == EMU_DECISION ? KC_EMU : KC_EMU_RESTART, st, [&] {
-            if (env.emu_wave) {
+        env.clock.run(cls, st, [&] {
+            if (wave) {
                 if (g.cart.board == NES_BOARD_MMC3) hipLaunchKernelGGL(k_emu_w<NES_BOARD_MMC3>, dim3(blocks), dim3(64), 0, st, a);
                 else if (g.cart.board == NES_BOARD_MMC1) hipLaunchKernelGGL(k_emu_w<NES_BOARD_MMC1>, dim3(blocks), dim3(64), 0, st, a);
                 else hipLaunchKernelGGL(k_emu_w<NES_BOARD_NROM>, dim3(blocks), dim3(64), 0, st, a);
             }
             else hipLaunchKernelGGL(k_emu, dim3(blocks), dim3(64), lds, st, a);
         });
-    trace(mode == EMU_DECISION ? "emu" : "emu_restart", st);
+    trace(mode == EMU_DECISION ? "emu" : mode == EMU_IDLE ? "emu_idle" : "emu_restart", st);
 }
 
 void launch_render(const Env& env, const GameK& g, const Outs& o, int f, bool use_list, bool restart, int e0, int e1,
@@ -1045,7 +949,9 @@ void restart_phases(const Env& env, const GameK& g, const Outs& o, int e0, int e
         hipLaunchKernelGGL(k_reset_copy, dim3(std::min(std::max(n, 1), 2048)), dim3(256), 0, st, fa);
     });
     trace("reset_copy", st);
-    // (idle frames beyond the copied template never occur: the template count equals idle_max)
+    // Idle frames: a restart from the boot snapshot copied the template that holds them (the template count equals
+    // idle_max); one from a saved level start emulates them here.
+    if (g.lv.cap > 0 && env.s.idle_max > 0) launch_emu(env, g, o, EMU_IDLE, 0, true, e0, e1, st);
     for (int f = 0; f < RLE_FRAMES; ++f) {
         launch_emu(env, g, o, EMU_RESTART, f, true, e0, e1, st);
         launch_render(env, g, o, f, true, true, e0, e1, st);
@@ -1056,29 +962,10 @@ void restart_phases(const Env& env, const GameK& g, const Outs& o, int e0, int e
     trace("reset_finish", st);
 }
 
-#ifdef RLENV_FUSED_KERNEL
-void launch_decision(const Env& env, const GameK& g, const Outs& o, int mode, int e0, int e1, hipStream_t st) {
-    const DecArgs a{g, env.e, o, env.s, mode, e0, e1, env.budget};
-    const int n = e1 - e0;
-    if (n <= 0) return;
-    env.clock.run(KC_DECISION, st, [&] {
-        if (g.cart.board == NES_BOARD_MMC3) hipLaunchKernelGGL(k_decision<NES_BOARD_MMC3>, dim3(n), dim3(64), 0, st, a);
-        else if (g.cart.board == NES_BOARD_MMC1) hipLaunchKernelGGL(k_decision<NES_BOARD_MMC1>, dim3(n), dim3(64), 0, st, a);
-        else hipLaunchKernelGGL(k_decision<NES_BOARD_NROM>, dim3(n), dim3(64), 0, st, a);
-    });
-    trace(mode == DEC_STEP ? "decision" : "decision_start", st);
-}
-#endif
 
 void decision_phases(const Env& env, const GameK& g, const Outs& o, int e0, int e1, hipStream_t st) {
     const int n = e1 - e0;
     if (n <= 0) return;
-#ifdef RLENV_FUSED_KERNEL
-    if (env.fused) {
-        launch_decision(env, g, o, DEC_STEP, e0, e1, st);
-        return;
-    }
-#endif
     for (int f = 0; f < RLE_FRAMES; ++f) {
         launch_emu(env, g, o, EMU_DECISION, f, false, e0, e1, st);
         launch_render(env, g, o, f, false, false, e0, e1, st);
@@ -1086,6 +973,11 @@ void decision_phases(const Env& env, const GameK& g, const Outs& o, int e0, int 
     const FinishArgs fa = finish_args(env, g, e0, e1, o);
     env.clock.run(KC_FINISH, st, [&] { hipLaunchKernelGGL(k_finish, dim3((n + 255) / 256), dim3(256), 0, st, fa); });
     trace("finish", st);
+    if (g.lv.cap > 0) {   // level-start saves, before any restart (restarts read the saves of earlier decisions)
+        env.clock.run(KC_ARCHIVE, st,
+                      [&] { hipLaunchKernelGGL(k_archive, dim3(g.lv.levels), dim3(256), 0, st, fa); });
+        trace("archive", st);
+    }
     restart_phases(env, g, o, e0, e1, st);
 }
 
@@ -1127,6 +1019,17 @@ void for_each_state(Env& env, F&& f) {
     f(env.e.target, N * 8); f(env.e.ep_frame, N * 4); f(env.e.prev_applied, N * 2); f(env.e.sticky_seed, N * 8);
     f(env.e.sticky_ctr, N * 8); f(env.e.episode, N * 4); f(env.e.ep_ret, N * 4); f(env.e.ep_len, N * 4);
     f(env.e.ep_maxlvl, N * 4); f(env.e.ep_idle, N * 4); f(env.e.fault, N * 4);
+    // level starts last, so a state saved without them is a prefix (rl/csrc/rlenv_build.hpp:269-279)
+    if (env.lv_cap > 0) {
+        f(env.e.ep_start, N * 4);
+        for (auto& gh : env.games) {
+            const LevelK& L = gh.k.lv;
+            const size_t C = (size_t)L.cap;
+            f(L.rec, C * sizeof(NesRec));
+            f(L.st, C * sizeof(Rl10State));
+            f(L.target, C * 8); f(L.frame, C * 4); f(L.deaths, C * 4);
+        }
+    }
 }
 
 }  // namespace
@@ -1144,7 +1047,6 @@ void* rlenv_create(int ngames, const int* game_ids, const uint8_t* const* roms, 
         env->device = device;
         if (const char* v = std::getenv("RLENV_CPW")) env->cpw = std::max(1, std::min(64, std::atoi(v)));
         if (const char* v = std::getenv("RLENV_EMU")) env->emu_wave = std::strcmp(v, "lane") != 0;
-        if (const char* v = std::getenv("RLENV_FUSED")) env->fused = std::strcmp(v, "1") == 0;
         if (const char* v = std::getenv("RLENV_BUDGET")) env->budget = (uint32_t)std::max(1, std::min((int)NES_BUDGET, std::atoi(v)));
         if (hipFuncSetAttribute(reinterpret_cast<const void*>(k_emu), hipFuncAttributeMaxDynamicSharedMemorySize,
                                 (int)(1024u + 64u * kRamStride)) != hipSuccess)
@@ -1263,12 +1165,6 @@ int rlenv_start(void* h, void* stream) {
     Env& env = *static_cast<Env*>(h);
     const hipStream_t st = static_cast<hipStream_t>(stream);
     for (auto& gh : env.games) {
-#ifdef RLENV_FUSED_KERNEL
-        if (env.fused) {
-            launch_decision(env, gh.k, env.o, DEC_START, 0, gh.k.n, st);
-            continue;
-        }
-#endif
         const FinishArgs fa = finish_args(env, gh.k, 0, gh.k.n, env.o);
         hipLaunchKernelGGL(k_start, dim3((gh.k.n + 255) / 256), dim3(256), 0, st, fa);
         trace("start", st);
@@ -1336,6 +1232,112 @@ int rlenv_load(void* h, const uint8_t* in, void* stream) {
     return bad;
 }
 
+// ---------------------------------------------------------------- level starts / places (rl/csrc/rlenv.cu:300-362)
+int rlenv_enable_places(void* h, int cap, int levels) {
+    Env& env = *static_cast<Env*>(h);
+    if (env.lv_cap != 0 || cap <= 0 || levels <= 0 || levels > cap) {
+        g_error = "level starts: enable once, 0 < levels <= cap";
+        return 1;
+    }
+    try {
+        for (auto& gh : env.games) {
+            LevelK& L = gh.k.lv;
+            L.cap = cap;
+            L.levels = levels;
+            L.rec = env.mem.zeros<NesRec>((size_t)cap);
+            L.st = env.mem.zeros<Rl10State>((size_t)cap);
+            L.target = env.mem.zeros<uint64_t>((size_t)cap);
+            L.frame = env.mem.zeros<uint32_t>((size_t)cap);
+            L.deaths = env.mem.zeros<int32_t>((size_t)cap);
+            L.claim = env.mem.zeros<unsigned long long>((size_t)cap);
+            L.cdf = env.mem.zeros<uint32_t>((size_t)cap);
+            const std::vector<int32_t> none((size_t)cap, -1);
+            const std::vector<unsigned long long> free_((size_t)cap, ~0ull);
+            env.mem.upload(L.deaths, none.data(), (size_t)cap * 4);
+            env.mem.upload(L.claim, free_.data(), (size_t)cap * 8);
+            L.thresh = 0;
+            L.weighted = 0;
+        }
+        env.e.ep_start = env.mem.zeros<int32_t>((size_t)env.total);
+        const std::vector<int32_t> boot((size_t)env.total, -1);
+        env.mem.upload(env.e.ep_start, boot.data(), (size_t)env.total * 4);
+    } catch (const std::exception& ex) {
+        g_error = ex.what();
+        return 1;
+    }
+    env.lv_cap = cap;
+    return 0;
+}
+int rlenv_enable_level_starts(void* h, int cap) { return rlenv_enable_places(h, cap, cap); }
+void rlenv_set_level_plan(void* h, int gi, double p, const uint32_t* cdf) {
+    Env& env = *static_cast<Env*>(h);
+    if (gi < 0 || gi >= (int)env.games.size()) return;
+    LevelK& L = env.games[gi].k.lv;
+    if (L.cap == 0) return;
+    L.thresh = (uint32_t)(p <= 0.0 ? 0.0 : p >= 1.0 ? 4294967295.0 : p * 4294967296.0);
+    L.weighted = cdf != nullptr;
+    if (cdf) env.mem.upload(L.cdf, cdf, (size_t)L.cap * 4);
+}
+void rlenv_bind_start(void* h, int32_t* out) { static_cast<Env*>(h)->o.start_out = out; }
+void rlenv_bind_level(void* h, int32_t* out) { static_cast<Env*>(h)->o.level_out = out; }
+void rlenv_bind_progress(void* h, float* out) { static_cast<Env*>(h)->o.progress_out = out; }
+int rlenv_level_deaths(void* h, int gi, int32_t* out, void* stream) {
+    Env& env = *static_cast<Env*>(h);
+    if (gi < 0 || gi >= (int)env.games.size()) { g_error = "level_deaths: bad game"; return 1; }
+    const LevelK& L = env.games[gi].k.lv;
+    if (L.cap == 0) return 0;
+    const hipStream_t s = static_cast<hipStream_t>(stream);
+    if (hipMemcpyAsync(out, L.deaths, (size_t)L.cap * 4, hipMemcpyDeviceToHost, s) != hipSuccess ||
+        hipStreamSynchronize(s) != hipSuccess) {
+        g_error = "level_deaths failed";
+        return 1;
+    }
+    return 0;
+}
+int rlenv_place_save(void* h, int gi, const int32_t* env_idx, const int32_t* slot_idx, int count, void* stream) {
+    Env& env = *static_cast<Env*>(h);
+    if (gi < 0 || gi >= (int)env.games.size()) { g_error = "place_save: bad game"; return 1; }
+    const GameK& g = env.games[gi].k;
+    if (g.lv.cap == 0 || count <= 0) return 0;
+    const FinishArgs fa = finish_args(env, g, 0, g.n, env.o);
+    hipLaunchKernelGGL(k_place_save, dim3(count), dim3(256), 0, static_cast<hipStream_t>(stream), fa, env_idx, slot_idx);
+    return check("place_save");
+}
+int rlenv_place_copy(void* h, int gi, const int32_t* src, const int32_t* dst, int count, void* stream) {
+    Env& env = *static_cast<Env*>(h);
+    if (gi < 0 || gi >= (int)env.games.size()) { g_error = "place_copy: bad game"; return 1; }
+    const LevelK& L = env.games[gi].k.lv;
+    const hipStream_t s = static_cast<hipStream_t>(stream);
+    int bad = 0;
+    for (int i = 0; i < count; ++i) {
+        if (src[i] < 0 || dst[i] < 0 || src[i] >= L.cap || dst[i] >= L.cap) {
+            g_error = "place_copy: bad slot";
+            return 1;
+        }
+        const size_t a = (size_t)src[i], b = (size_t)dst[i];
+        const auto d2d = [&](void* to, const void* from, size_t n) {
+            bad |= hipMemcpyAsync(to, from, n, hipMemcpyDeviceToDevice, s) != hipSuccess;
+        };
+        d2d(L.rec + b, L.rec + a, sizeof(NesRec));
+        d2d(L.st + b, L.st + a, sizeof(Rl10State));
+        d2d(L.target + b, L.target + a, 8);
+        d2d(L.frame + b, L.frame + a, 4);
+        d2d(L.deaths + b, L.deaths + a, 4);
+    }
+    bad |= hipStreamSynchronize(s) != hipSuccess;
+    if (bad) g_error = "place_copy failed";
+    return bad;
+}
+void rlenv_level_layout(void* h, int gi, uint32_t* out) {
+    const Env& env = *static_cast<Env*>(h);
+    const LevelK& L = env.games[gi].k.lv;
+    out[0] = (uint32_t)sizeof(NesRec);
+    out[1] = 0;   // key words per env: the SMB reader keeps none
+    out[2] = (uint32_t)sizeof(Rl10State);
+    out[3] = (uint32_t)L.cap;
+    out[4] = (uint32_t)L.levels;
+}
+
 int rlenv_read_consoles(void* h, int gi, int first, int count, uint8_t* out, void* stream) {
     Env& env = *static_cast<Env*>(h);
     if (gi < 0 || gi >= (int)env.games.size() || first < 0 || count < 0 || first + count > env.games[gi].k.n + 1) {
@@ -1355,7 +1357,7 @@ int rlenv_read_consoles(void* h, int gi, int first, int count, uint8_t* out, voi
 void rlenv_set_kernel_timing(void* h, int on) { static_cast<Env*>(h)->clock.on = on != 0; }
 
 int rlenv_kernel_times(void* h, double* ms, int64_t* count, int n) {
-    if (n < KC_COUNT) { g_error = "kernel_times: need room for every kernel class (8)"; return 1; }
+    if (n < KC_COUNT) { g_error = "kernel_times: need room for every kernel class (9)"; return 1; }
     for (int i = 0; i < n; ++i) { ms[i] = 0.0; count[i] = 0; }
     if (static_cast<Env*>(h)->clock.drain(ms, count)) { g_error = "kernel_times: event query failed"; return 1; }
     return 0;

@@ -68,6 +68,13 @@ def _load(path: Path):
     lib.rlenv_set_dropout_gap.argtypes = [P, U32]
     lib.rlenv_bind_ram_hash.argtypes = [P, P]
     lib.rlenv_read_consoles.argtypes = [P, I, I, I, P, P]
+    lib.rlenv_enable_level_starts.argtypes = [P, I]
+    lib.rlenv_enable_places.argtypes = [P, I, I]
+    lib.rlenv_set_level_plan.argtypes = [P, I, ctypes.c_double, P]
+    lib.rlenv_bind_start.argtypes = lib.rlenv_bind_level.argtypes = lib.rlenv_bind_progress.argtypes = [P, P]
+    lib.rlenv_level_deaths.argtypes = [P, I, P, P]
+    lib.rlenv_place_save.argtypes = lib.rlenv_place_copy.argtypes = [P, I, P, P, I, P]
+    lib.rlenv_level_layout.argtypes = [P, I, P]
     lib.rl_pack6.argtypes = [P, P, SZ, P]
     lib.rl_unpack6.argtypes = [P, P, SZ, P]
     lib.rl10_smb_run.argtypes = [P, I, I, I, P, P, P, P]
@@ -98,9 +105,11 @@ class RlEnv:
                  lib_path=None, level_cap=0, level_slots=None, boot=None, pad_mode=False, end_prob=0.0,
                  dropout_gap=None, ram_hash=False):
         """counts: game slug -> number of envs (envs are laid out in GAMES order). roms: slug -> iNES path or bytes.
-        level_cap must be 0 (level starts are not built yet)."""
-        if level_cap:
-            raise NotImplementedError('level starts / places are not built in this library yet')
+        level_cap > 0: save level starts (levels 0..level_cap-1 of each game), used by new episodes with the chance
+        set by set_level_prob / set_level_plan (default 0); self.start_level: the slot a finished episode started
+        from (-1 = boot snapshot, valid where done); self.level_now / self.progress_now: the level and within-level
+        progress after each decision. level_slots < level_cap: only slots 0..level_slots-1 are level starts, the rest
+        are places filled by place_save (rl/rlenv.py:172-238 of the reference)."""
         self.device = torch.device(device)
         self.games = [g for g in GAMES if counts.get(g, 0) > 0]
         self.counts = [int(counts[g]) for g in self.games]
@@ -153,9 +162,19 @@ class RlEnv:
                             _ptr(self.events), _ptr(self.info))
         self.parts = torch.zeros(N, NUM_PARTS, dtype=torch.float32, device=d)
         self.lib.rlenv_bind_parts(self.h, _ptr(self.parts))
-        self.level_cap = 0
-        self.level_slots = 0
+        self.level_cap = int(level_cap)
+        self.level_slots = int(level_slots if level_slots is not None else level_cap)
         self.start_level = torch.full((N,), -1, dtype=torch.int32, device=d)
+        if self.level_cap > 0:
+            ok = (self.lib.rlenv_enable_places(self.h, self.level_cap, self.level_slots)
+                  if self.level_slots < self.level_cap else self.lib.rlenv_enable_level_starts(self.h, self.level_cap))
+            if ok != 0:
+                raise RuntimeError(self.lib.rlenv_error().decode())
+            self.lib.rlenv_bind_start(self.h, _ptr(self.start_level))
+            self.level_now = torch.full((N,), -1, dtype=torch.int32, device=d)
+            self.lib.rlenv_bind_level(self.h, _ptr(self.level_now))
+            self.progress_now = torch.full((N,), float('nan'), dtype=torch.float32, device=d)
+            self.lib.rlenv_bind_progress(self.h, _ptr(self.progress_now))
         self.lib.rlenv_set_pad_mode(self.h, int(bool(pad_mode)))
         if end_prob:
             self.lib.rlenv_set_end_prob(self.h, min(int(float(end_prob) * 2 ** 32), 2 ** 32 - 1))
@@ -167,7 +186,87 @@ class RlEnv:
             self.lib.rlenv_bind_ram_hash(self.h, _ptr(self.ram_hash))
 
     def set_level_prob(self, prob: float):
-        assert prob == 0, 'level starts are not built yet'
+        """Chance that a new episode starts from a saved level start (uniform over each game's saved slots)."""
+        assert self.level_cap > 0 or prob == 0
+        for gi in range(len(self.games)):
+            self.set_level_plan(gi, prob)
+
+    def set_level_plan(self, gi, prob, weights=None):
+        """Game gi's chance of a level start and its slot weights ([level_cap], weight only on saved slots, sum 1;
+        None = uniform over the saved slots). Call between decisions."""
+        if self.level_cap == 0:
+            return
+        cdf = None
+        if weights is not None:
+            w = np.asarray(weights, np.float64)
+            cdf = np.minimum(np.cumsum(w) * 2.0 ** 32, 2.0 ** 32 - 1).astype(np.uint32)
+            cdf[np.flatnonzero(w)[-1]:] = 2 ** 32 - 1   # the last weighted slot takes the rounding remainder
+        self._sync()
+        self.lib.rlenv_set_level_plan(self.h, gi, float(prob),
+                                      None if cdf is None else cdf.ctypes.data_as(ctypes.c_void_p))
+
+    def saved_levels(self):
+        """game slug -> {slot: deaths of the saved arrival} over the level slots (synchronous)."""
+        out = {}
+        for gi, g in enumerate(self.games):
+            buf = np.full(max(self.level_cap, 1), -1, np.int32)
+            if self.level_cap > 0:
+                self._sync()
+                if self.lib.rlenv_level_deaths(self.h, gi, buf.ctypes.data_as(ctypes.c_void_p), self._stream()) != 0:
+                    raise RuntimeError(self.lib.rlenv_error().decode())
+            out[g] = {int(s): int(v) for s, v in enumerate(buf[:self.level_slots]) if v >= 0}
+        return out
+
+    def place_save(self, gi, env_idx, slot_idx):
+        """After a step, on the current stream: env env_idx[j] (index within game gi) -> place slot slot_idx[j]
+        (skipped where < level_slots). int32 tensors on the env's device."""
+        assert env_idx.dtype == torch.int32 and slot_idx.dtype == torch.int32
+        assert env_idx.is_contiguous() and slot_idx.is_contiguous() and env_idx.numel() == slot_idx.numel()
+        if self.lib.rlenv_place_save(self.h, gi, _ptr(env_idx), _ptr(slot_idx), int(env_idx.numel()),
+                                     self._stream()) != 0:
+            raise RuntimeError(self.lib.rlenv_error().decode())
+
+    def place_copy(self, gi, src, dst):
+        """Slot src[j] -> slot dst[j] of game gi (the whole saved state), synchronous."""
+        a, b = np.ascontiguousarray(src, np.int32), np.ascontiguousarray(dst, np.int32)
+        if len(a) != len(b):
+            raise ValueError('place_copy: src and dst differ in length')
+        if len(a) and self.lib.rlenv_place_copy(self.h, gi, a.ctypes.data_as(ctypes.c_void_p),
+                                                b.ctypes.data_as(ctypes.c_void_p), len(a), self._stream()) != 0:
+            raise RuntimeError(self.lib.rlenv_error().decode())
+
+    def level_layout(self, gi):
+        out = np.zeros(5, np.uint32)
+        self.lib.rlenv_level_layout(self.h, gi, out.ctypes.data_as(ctypes.c_void_p))
+        return dict(stride=int(out[0]), key_cap=int(out[1]), st=int(out[2]), cap=int(out[3]), levels=int(out[4]))
+
+    def _archive_sizes(self, cap):
+        """Byte sizes of the level-start tail of the state blob per game for `cap` slots: saved consoles, trackers,
+        key words, targets, frames, deaths (the order the library saves them in)."""
+        out = []
+        for gi in range(len(self.games)):
+            lay = self.level_layout(gi)
+            out.append([cap * lay['stride'], cap * lay['st'], cap * lay['key_cap'] * 4, cap * 8, cap * 4, cap * 4])
+        return out
+
+    def _grow_archive(self, buf, old_cap, need):
+        """A state saved with old_cap slots per game -> this env's level_cap (the new slots empty); None when buf is
+        not such a state."""
+        old, new = self._archive_sizes(old_cap), self._archive_sizes(self.level_cap)
+        old_tail = sum(map(sum, old))
+        if len(buf) - old_tail + sum(map(sum, new)) != need:
+            return None
+        parts, o = [buf[:len(buf) - old_tail]], len(buf) - old_tail
+        for so, sn in zip(old, new):
+            for k, (a, b) in enumerate(zip(so, sn)):
+                parts.append(buf[o:o + a])
+                o += a
+                parts.append(np.full(b - a, 0xFF if k == 5 else 0, np.uint8))   # deaths -1 = empty
+        return np.concatenate(parts)
+
+    def _sync(self):
+        if self.device.type == 'cuda':
+            torch.cuda.synchronize(self.device)
 
     def drop_obs_buffers(self):
         """Free the default picture outputs (a caller that always binds its own via bind_obs)."""
@@ -236,9 +335,18 @@ class RlEnv:
         return dict(env=buf, outputs=outs, games=self.games, counts=self.counts, level_cap=self.level_cap)
 
     def load_state_dict(self, sd):
+        """Exact resume. A state saved with fewer level slots grows into this env's (new slots empty); a state
+        saved without level starts gets an empty archive (its level-start tail is this fresh env's)."""
         assert sd['games'] == self.games and sd['counts'] == self.counts, 'env layout changed'
         buf = np.ascontiguousarray(sd['env'])
-        assert len(buf) == self.lib.rlenv_state_bytes(self.h), 'env state size changed'
+        need = self.lib.rlenv_state_bytes(self.h)
+        old_cap = int(sd.get('level_cap', 0))
+        if len(buf) < need and self.level_cap > old_cap > 0:
+            grown = self._grow_archive(buf, old_cap, need)
+            buf = buf if grown is None else grown
+        if len(buf) < need and self.level_cap > 0 and old_cap == 0:
+            buf = np.concatenate([buf, self.state_dict()['env'][len(buf):]])
+        assert len(buf) == need, 'env state size changed'
         if self.lib.rlenv_load(self.h, buf.ctypes.data_as(ctypes.c_void_p), self._stream()) != 0:
             raise RuntimeError(self.lib.rlenv_error().decode())
         for k, v in sd['outputs'].items():

@@ -33,6 +33,29 @@ void rlenv_bind(void* h, const int16_t* actions, uint8_t* obs, uint8_t* emph, fl
                 uint8_t* masks, uint8_t* timeline, uint8_t* pads, uint32_t* events, float* info);
 void rlenv_bind_parts(void* h, float* parts);                  /* rlenv_api.h:20: [N,7] */
 void rlenv_bind_obs(void* h, uint8_t* obs, uint8_t* emph);     /* rlenv_api.h:22 */
+/* Level starts and places (rlenv_api.h:22-39; rl/csrc/rlenv_core.cuh:14-20). enable: room for `cap` saved starts
+ * per game, the first `levels` of them level starts (saved on the tracker's level event, the arrival with the fewest
+ * deaths kept, the newest on ties), the rest places (saved by place_save); call once, before start/load; error if
+ * called twice or 0 < levels <= cap does not hold. set_level_plan: game gi's chance p that a new episode starts from
+ * a saved slot, and its cumulative slot weights * 2^32 (cap entries; NULL = uniform over the saved slots); call
+ * between decisions. bind_start/level/progress: outputs [N] int32 start slot of a finished episode (-1 = boot
+ * snapshot; valid where done), [N] int32 level after each decision (-1 = unknown), [N] float within-level progress /
+ * progress unit (NaN = not valid). level_deaths: deaths of game gi's saves (-1 = empty), cap entries, to host memory
+ * (synchronous). place_save: env_idx[j] (index within game gi) -> slot_idx[j] (skipped where < levels), device
+ * arrays, on `stream` after a step. place_copy: slot src[j] -> dst[j], host arrays, synchronous. level_layout: out[5]
+ * = bytes of one saved console, key words per env, sizeof(Rl10State), cap, levels. */
+int rlenv_enable_level_starts(void* h, int cap);                                       /* rlenv_api.h:26 */
+int rlenv_enable_places(void* h, int cap, int levels);                                 /* rlenv_api.h:36 */
+void rlenv_set_level_plan(void* h, int gi, double p, const uint32_t* cdf);             /* rlenv_api.h:27 */
+void rlenv_bind_start(void* h, int32_t* start_out);                                    /* rlenv_api.h:28 */
+void rlenv_bind_level(void* h, int32_t* level_out);                                    /* rlenv_api.h:29 */
+void rlenv_bind_progress(void* h, float* progress_out);                                /* rlenv_api.h:30 */
+int rlenv_level_deaths(void* h, int gi, int32_t* host_out, void* stream);              /* rlenv_api.h:31 */
+int rlenv_place_save(void* h, int gi, const int32_t* env_idx, const int32_t* slot_idx, int count,
+                     void* stream);                                                    /* rlenv_api.h:37 */
+int rlenv_place_copy(void* h, int gi, const int32_t* src, const int32_t* dst, int count,
+                     void* stream);                                                    /* rlenv_api.h:38 */
+void rlenv_level_layout(void* h, int gi, uint32_t* out);                               /* rlenv_api.h:39 */
 int rlenv_start(void* h, void* stream);                        /* rlenv_api.h:40 */
 int rlenv_step(void* h, void* stream);                         /* rlenv_api.h:41 */
 size_t rlenv_state_bytes(void* h);                             /* rlenv_api.h:42 */
@@ -73,9 +96,9 @@ void rlenv_bind_ram_hash(void* h, uint64_t* ram_hash);
 int rlenv_read_consoles(void* h, int gi, int first, int count, uint8_t* host_out, void* stream);
 /* Per-kernel clock (no reference counterpart; the measurement harness reads it): when on, every launch of a
  * start/step is bracketed by two HIP events on its stream. rlenv_kernel_times waits for the recorded launches,
- * writes the summed milliseconds and launch counts per kernel class into ms[n] / count[n] (n >= 8; classes:
- * 0 emu, 1 render, 2 finish, 3 reset_copy, 4 emu_restart, 5 render_restart, 6 reset_finish - the per-phase
- * kernels - and 7 decision, the fused one-launch decision) and forgets them. */
+ * writes the summed milliseconds and launch counts per kernel class into ms[n] / count[n] (n >= 9; classes:
+ * 0 emu, 1 render, 2 finish, 3 reset_copy, 4 emu_restart, 5 render_restart, 6 reset_finish, 7 emu_idle (idle
+ * frames of level starts), 8 archive (level-start saves)) and forgets them. */
 void rlenv_set_kernel_timing(void* h, int on);
 int rlenv_kernel_times(void* h, double* ms, int64_t* count, int n);
 

@@ -12,7 +12,7 @@
  *                             ph_reset_idle, ph_reset_frame, ph_reset_finish_controls, env_start, env_step)
  *   build ................... rl/csrc/rlenv_build.hpp:193-366 (boot on the host, slot n = snapshot, idle
  *                             templates, episode counters start at 0xFFFFFFFF)
- *   resume blob order ....... rl/csrc/rlenv_build.hpp:412-437
+ *   resume blob order ....... rl/csrc/rlenv_build.hpp:253-280
  *   pack6 ................... rl/csrc/rlenv.cu:127-142
  */
 #include <math.h>
@@ -352,6 +352,18 @@ typedef struct Game {
     NesRec* recs;      /* n + 1 records; slot n = boot snapshot */
     NesRec* idle;      /* idle_max templates: the snapshot after k = 1..idle_max neutral frames */
     uint64_t tmpl_target;
+    /* level starts / places (rl/csrc/rlenv_core.cuh:60-74; lv_cap = 0: off): slot s < lv_levels is level s, saved on
+     * the level event; slots lv_levels..lv_cap-1 are places, saved on request. One saved console is a whole record. */
+    int lv_cap, lv_levels;
+    NesRec* lv_rec;           /* [lv_cap] */
+    Rl10State* lv_st;         /* [lv_cap] */
+    uint64_t* lv_target;      /* [lv_cap] */
+    uint32_t* lv_frame;       /* [lv_cap] */
+    int32_t* lv_deaths;       /* [lv_cap], -1 = nothing saved */
+    uint64_t* lv_claim;       /* [lv_cap] (deaths << 32 | env) of this decision's best arrival, ~0 = none */
+    uint32_t* lv_cdf;         /* [lv_cap] cumulative level weights * 2^32 */
+    uint32_t lv_thresh;       /* P(a new episode starts from a saved level) * 2^32 */
+    int lv_weighted;
 } Game;
 
 typedef struct Env {
@@ -367,12 +379,16 @@ typedef struct Env {
     float* ep_ret;
     int32_t *ep_len, *ep_maxlvl, *ep_idle;
     uint8_t* resetting;
+    int lv_cap;               /* level starts on (every game has the same cap) */
+    int32_t* ep_start;        /* [N] slot the current episode started from, -1 = boot snapshot (with lv_cap) */
     /* bound buffers */
     const int16_t* actions;
     uint8_t *obs, *emph, *done, *masks, *tl, *pads;
     float *reward, *info, *parts;
     uint32_t* events;
     uint64_t* ram_hash;
+    int32_t *start_out, *level_out;
+    float* progress_out;
     /* settings */
     uint64_t run_seed;
     int sticky, idle_max, dropout, no_render, episode_level_end, pad_mode;
@@ -427,11 +443,33 @@ static void reset_state(Env* E, Game* g, int e) {
     E->sticky_ctr[ge] = 0;
     int idle = 0;
     if (E->idle_max > 0) idle = (int)rand_below(E->sticky_seed[ge], &E->sticky_ctr[ge], (uint32_t)(E->idle_max + 1));
-    const int k = idle <= E->idle_tmpl ? idle : 0;
-    memcpy(&g->recs[e], k == 0 ? &g->recs[g->n] : &g->idle[k - 1], sizeof(NesRec));
-    E->target[ge] = g->tmpl_target + (uint64_t)k * NES_FRAME_DOTS;
-    E->ep_frame[ge] = (uint32_t)k;
-    rl10_reset(&E->st[ge]);
+    /* a level start? (rlenv_core.cuh:220-236; drawn only when level starts are on) */
+    int lv = -1;
+    if (g->lv_cap > 0 && g->lv_thresh != 0 && rand_u32(E->sticky_seed[ge], &E->sticky_ctr[ge]) < g->lv_thresh) {
+        uint32_t saved = 0;
+        for (int s = 0; s < g->lv_cap; ++s) saved += g->lv_deaths[s] >= 0 ? 1u : 0u;
+        if (g->lv_weighted) {
+            const uint32_t u = rand_u32(E->sticky_seed[ge], &E->sticky_ctr[ge]);
+            for (int s = 0; s < g->lv_cap && lv < 0; ++s)
+                if (u < g->lv_cdf[s]) lv = s;
+        } else if (saved > 0) {
+            uint32_t pick = rand_below(E->sticky_seed[ge], &E->sticky_ctr[ge], saved);
+            for (int s = 0; s < g->lv_cap && lv < 0; ++s)
+                if (g->lv_deaths[s] >= 0 && pick-- == 0) lv = s;
+        }
+    }
+    const int k = lv < 0 && idle <= E->idle_tmpl ? idle : 0;
+    memcpy(&g->recs[e], lv >= 0 ? &g->lv_rec[lv] : k == 0 ? &g->recs[g->n] : &g->idle[k - 1], sizeof(NesRec));
+    if (lv >= 0) {
+        E->target[ge] = g->lv_target[lv];
+        E->ep_frame[ge] = g->lv_frame[lv];
+        E->st[ge] = g->lv_st[lv];
+    } else {
+        E->target[ge] = g->tmpl_target + (uint64_t)k * NES_FRAME_DOTS;
+        E->ep_frame[ge] = (uint32_t)k;
+        rl10_reset(&E->st[ge]);
+    }
+    if (E->ep_start) E->ep_start[ge] = lv;
     E->fault[ge] = 0;
     dropout_reset(&E->drop[ge], seed, E->dropout != 0, E->gap_p32);
     E->prev_applied[ge] = 0;
@@ -476,7 +514,21 @@ static void ph_finish(Env* E, Game* g, int e) {
     ++E->ep_len[ge];
     if (u.event_level > E->ep_maxlvl[ge]) E->ep_maxlvl[ge] = u.event_level;
     dropout_advance(&E->drop[ge], E->dropout != 0, E->gap_p32);
+    /* level-start claim: the arrival with the fewest deaths, then the lowest env index (rlenv_core.cuh:288-291) */
+    if (g->lv_cap > 0 && !done && (u.events & EV_LEVEL) && u.event_level >= 0 && u.event_level < g->lv_levels) {
+        const uint64_t d = (uint64_t)(uint32_t)(E->st[ge].deaths < 0 ? 0 : E->st[ge].deaths);
+        const uint64_t v = (d << 32) | (uint32_t)e;
+        uint64_t cur = __atomic_load_n(&g->lv_claim[u.event_level], __ATOMIC_RELAXED);
+        while (v < cur && !__atomic_compare_exchange_n(&g->lv_claim[u.event_level], &cur, v, 1, __ATOMIC_RELAXED,
+                                                       __ATOMIC_RELAXED)) {
+        }
+    }
+    if (E->level_out) E->level_out[ge] = E->st[ge].has_best_level ? E->st[ge].best_level : -1;
+    if (E->progress_out)
+        E->progress_out[ge] = E->st[ge].has_prev && E->st[ge].prev.progress_valid
+                                  ? (float)(E->st[ge].prev.progress / SMB_PROGRESS_UNIT) : NAN;
     if (done) {
+        if (E->start_out) E->start_out[ge] = E->ep_start ? E->ep_start[ge] : -1;
         float* inf = E->info + (size_t)ge * RLE_INFO;
         inf[0] = E->ep_ret[ge];
         inf[1] = (float)E->ep_len[ge];
@@ -495,7 +547,8 @@ static void ph_finish(Env* E, Game* g, int e) {
 static void ph_reset_idle(Env* E, Game* g, int e) {
     const int ge = g->offset + e;
     if (E->resetting[ge] == 0) return;
-    const int done = E->ep_idle[ge] <= E->idle_tmpl ? E->ep_idle[ge] : 0;
+    const int lv = E->ep_start && E->ep_start[ge] >= 0;   /* a level start: every idle frame is emulated */
+    const int done = !lv && E->ep_idle[ge] <= E->idle_tmpl ? E->ep_idle[ge] : 0;
     for (int i = done; i < E->ep_idle[ge]; ++i) emu_frame(E, g, e, ge, 0);
 }
 
@@ -513,7 +566,8 @@ static void ph_reset_finish_controls(Env* E, Game* g, int e) {
         (void)rl10_update(b15, E->ep_idle[ge] + RLE_FRAMES, &E->st[ge]);
         E->ep_ret[ge] = 0.0f;
         E->ep_len[ge] = 0;
-        E->ep_maxlvl[ge] = 0;
+        const int sl = E->ep_start ? E->ep_start[ge] : -1;   /* a place: its level is the tracker's */
+        E->ep_maxlvl[ge] = sl >= g->lv_levels ? (E->st[ge].has_best_level ? E->st[ge].best_level : 0) : sl > 0 ? sl : 0;
         E->resetting[ge] = 0;
     }
     write_controls(E, g, ge);
@@ -564,11 +618,13 @@ static void env_free(Env* E) {
         free(E->games[i].rom);
         free(E->games[i].recs);
         free(E->games[i].idle);
+        free(E->games[i].lv_rec); free(E->games[i].lv_st); free(E->games[i].lv_target); free(E->games[i].lv_frame);
+        free(E->games[i].lv_deaths); free(E->games[i].lv_claim); free(E->games[i].lv_cdf);
     }
     free(E->games);
     free(E->st); free(E->drop); free(E->target); free(E->sticky_seed); free(E->sticky_ctr);
     free(E->ep_frame); free(E->episode); free(E->fault); free(E->prev_applied); free(E->ep_ret);
-    free(E->ep_len); free(E->ep_maxlvl); free(E->ep_idle); free(E->resetting);
+    free(E->ep_len); free(E->ep_maxlvl); free(E->ep_idle); free(E->resetting); free(E->ep_start);
     free(E);
 }
 
@@ -695,11 +751,121 @@ int rlenv_step(void* h, void* stream) {
         Game* g = game_of(E, k, &e);
         env_step_one(E, g, e);
     }
+    /* level-start saves after every env's finish; restarts read the saves only in reset_state, so doing them after
+     * the whole step equals the GPU's order (rlenv_core.cuh:343-387, rl/csrc/rlenv_cpu.cpp:108-117) */
+    for (int i = 0; i < E->ngames; ++i) {
+        Game* g = &E->games[i];
+        for (int s = 0; s < g->lv_levels; ++s) {
+            const uint64_t cl = g->lv_claim[s];
+            if (cl == ~0ull) continue;
+            const int take = g->lv_deaths[s] < 0 || (int32_t)(cl >> 32) <= g->lv_deaths[s];
+            if (take) {
+                const int e = (int)(cl & 0xFFFFFFFFull), ge = g->offset + e;
+                g->lv_rec[s] = g->recs[e];
+                g->lv_st[s] = E->st[ge];
+                g->lv_target[s] = E->target[ge];
+                g->lv_frame[s] = E->ep_frame[ge];
+                g->lv_deaths[s] = (int32_t)(cl >> 32);
+            }
+            g->lv_claim[s] = ~0ull;
+        }
+    }
     return 0;
 }
 
+/* ---------------------------------------------------------------------------- level starts / places
+ * rl/csrc/rlenv_api.h:22-39, rl/csrc/rlenv_build.hpp:210-251, rl/csrc/rlenv_cpu.cpp:119-170. */
+int rlenv_enable_places(void* h, int cap, int levels) {
+    Env* E = (Env*)h;
+    if (E->lv_cap != 0 || cap <= 0 || levels <= 0 || levels > cap) {
+        snprintf(g_err, sizeof(g_err), "level starts: enable once, 0 < levels <= cap");
+        return 1;
+    }
+    for (int i = 0; i < E->ngames; ++i) {
+        Game* g = &E->games[i];
+        g->lv_cap = cap;
+        g->lv_levels = levels;
+        g->lv_rec = (NesRec*)xcalloc((size_t)cap, sizeof(NesRec));
+        g->lv_st = (Rl10State*)xcalloc((size_t)cap, sizeof(Rl10State));
+        g->lv_target = (uint64_t*)xcalloc((size_t)cap, 8);
+        g->lv_frame = (uint32_t*)xcalloc((size_t)cap, 4);
+        g->lv_deaths = (int32_t*)xcalloc((size_t)cap, 4);
+        g->lv_claim = (uint64_t*)xcalloc((size_t)cap, 8);
+        g->lv_cdf = (uint32_t*)xcalloc((size_t)cap, 4);
+        for (int s = 0; s < cap; ++s) {
+            g->lv_deaths[s] = -1;
+            g->lv_claim[s] = ~0ull;
+        }
+    }
+    E->ep_start = (int32_t*)xcalloc((size_t)E->total, 4);
+    for (int k = 0; k < E->total; ++k) E->ep_start[k] = -1;
+    E->lv_cap = cap;
+    return 0;
+}
+int rlenv_enable_level_starts(void* h, int cap) { return rlenv_enable_places(h, cap, cap); }
+void rlenv_set_level_plan(void* h, int gi, double p, const uint32_t* cdf) {
+    Game* g = &((Env*)h)->games[gi];
+    if (g->lv_cap == 0) return;
+    g->lv_thresh = (uint32_t)(p <= 0.0 ? 0.0 : p >= 1.0 ? 4294967295.0 : p * 4294967296.0);
+    g->lv_weighted = cdf != NULL;
+    if (cdf) memcpy(g->lv_cdf, cdf, (size_t)g->lv_cap * 4);
+}
+void rlenv_bind_start(void* h, int32_t* out) { ((Env*)h)->start_out = out; }
+void rlenv_bind_level(void* h, int32_t* out) { ((Env*)h)->level_out = out; }
+void rlenv_bind_progress(void* h, float* out) { ((Env*)h)->progress_out = out; }
+int rlenv_level_deaths(void* h, int gi, int32_t* out, void* stream) {
+    (void)stream;
+    const Game* g = &((Env*)h)->games[gi];
+    if (g->lv_cap) memcpy(out, g->lv_deaths, (size_t)g->lv_cap * 4);
+    return 0;
+}
+/* env_idx[j] -> slot_idx[j] (skipped where the slot is a level slot or out of range); host arrays here */
+int rlenv_place_save(void* h, int gi, const int32_t* env_idx, const int32_t* slot_idx, int count, void* stream) {
+    (void)stream;
+    Env* E = (Env*)h;
+    Game* g = &E->games[gi];
+    for (int j = 0; j < count && g->lv_cap > 0; ++j) {
+        const int s = slot_idx[j], e = env_idx[j];
+        if (s < g->lv_levels || s >= g->lv_cap || e < 0 || e >= g->n) continue;
+        const int ge = g->offset + e;
+        g->lv_rec[s] = g->recs[e];
+        g->lv_st[s] = E->st[ge];
+        g->lv_st[s].idle_frames = 0;   /* the no-progress clock restarts at a place (rlenv_core.cuh:366-375) */
+        g->lv_target[s] = E->target[ge];
+        g->lv_frame[s] = E->ep_frame[ge];
+        g->lv_deaths[s] = 0;
+    }
+    return 0;
+}
+int rlenv_place_copy(void* h, int gi, const int32_t* src, const int32_t* dst, int count, void* stream) {
+    (void)stream;
+    Game* g = &((Env*)h)->games[gi];
+    for (int j = 0; j < count; ++j) {
+        if (src[j] < 0 || dst[j] < 0 || src[j] >= g->lv_cap || dst[j] >= g->lv_cap) {
+            snprintf(g_err, sizeof(g_err), "place_copy: bad slot");
+            return 1;
+        }
+        const int a = src[j], b = dst[j];
+        g->lv_rec[b] = g->lv_rec[a];
+        g->lv_st[b] = g->lv_st[a];
+        g->lv_target[b] = g->lv_target[a];
+        g->lv_frame[b] = g->lv_frame[a];
+        g->lv_deaths[b] = g->lv_deaths[a];
+    }
+    return 0;
+}
+/* stride of one saved console, key words per env (none for the SMB reader), sizeof(Rl10State), cap, levels */
+void rlenv_level_layout(void* h, int gi, uint32_t* out) {
+    const Game* g = &((Env*)h)->games[gi];
+    out[0] = (uint32_t)sizeof(NesRec);
+    out[1] = 0;
+    out[2] = (uint32_t)sizeof(Rl10State);
+    out[3] = (uint32_t)g->lv_cap;
+    out[4] = (uint32_t)g->lv_levels;
+}
+
 /* Resume blob: per game every console record (n + 1, snapshot slot included), then the per-env arrays in
- * the reference's order (rl/csrc/rlenv_build.hpp:412-425). */
+ * the reference's order (rl/csrc/rlenv_build.hpp:253-268). */
 typedef void (*visit_fn)(void* p, size_t bytes, void* ctx);
 static void for_each_state(Env* E, visit_fn f, void* ctx) {
     for (int i = 0; i < E->ngames; ++i) f(E->games[i].recs, sizeof(NesRec) * ((size_t)E->games[i].n + 1), ctx);
@@ -710,6 +876,17 @@ static void for_each_state(Env* E, visit_fn f, void* ctx) {
     f(E->sticky_seed, N * 8, ctx); f(E->sticky_ctr, N * 8, ctx); f(E->episode, N * 4, ctx);
     f(E->ep_ret, N * 4, ctx); f(E->ep_len, N * 4, ctx); f(E->ep_maxlvl, N * 4, ctx);
     f(E->ep_idle, N * 4, ctx); f(E->fault, N * 4, ctx);
+    /* level starts last, so a state saved without them is a prefix (rl/csrc/rlenv_build.hpp:269-279) */
+    if (E->lv_cap > 0) {
+        f(E->ep_start, N * 4, ctx);
+        for (int i = 0; i < E->ngames; ++i) {
+            Game* g = &E->games[i];
+            const size_t L = (size_t)g->lv_cap;
+            f(g->lv_rec, L * sizeof(NesRec), ctx);
+            f(g->lv_st, L * sizeof(Rl10State), ctx);
+            f(g->lv_target, L * 8, ctx); f(g->lv_frame, L * 4, ctx); f(g->lv_deaths, L * 4, ctx);
+        }
+    }
 }
 static void v_count(void* p, size_t b, void* ctx) { (void)p; *(size_t*)ctx += b; }
 static void v_save(void* p, size_t b, void* ctx) { uint8_t** o = (uint8_t**)ctx; memcpy(*o, p, b); *o += b; }
