@@ -145,60 +145,50 @@ def env_kwargs(w, args, cart):
 
 
 class Pack6Sink:
-    """The trainer's pack6 observation store: per decision the frames are packed on the device (3/4 of the bytes)
-    and, for 'host', copied into a ring of pinned host slots on a second stream (rl/train.py:174-294)."""
+    """Where each decision's pictures go. 'device': packed 6 bits per pixel on the device (3/4 of the bytes) into a
+    staging buffer. 'host': the trainer's pinned-host store (rl.hostobs.HostObs, rl/train.py:174-294): the env draws
+    into two alternating device slots, each packed and copied into a ring of pinned host rows on a side stream while
+    the next decision runs."""
 
     def __init__(self, env, mode, slots):
         import torch
         self.env, self.mode = env, mode
-        self.px = env.n * 4 * 224 * 240
         self.lib = env.lib
-        self.lib.rl_pack6.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p]
-        self.slots = slots if mode == 'host' else 1
-        self.staging = [torch.empty(self.px // 4 * 3, dtype=torch.uint8, device=env.device) for _ in range(self.slots)]
-        self.host = []
-        if mode == 'host':
-            self.lib.rl_host_alloc.restype = ctypes.c_void_p
-            self.lib.rl_host_alloc.argtypes = [ctypes.c_size_t]
-            self.lib.rl_host_free.argtypes = [ctypes.c_void_p]
-            self.lib.rl_memcpy_async.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p]
-            for _ in range(self.slots):
-                p = self.lib.rl_host_alloc(self.px // 4 * 3)
-                if not p:
-                    raise RuntimeError('rl_host_alloc failed')
-                self.host.append(p)
-            self.side = torch.cuda.Stream(device=env.device)
-            self.copied = [None] * self.slots
         self.t = 0
+        if mode == 'host':
+            from rl.hostobs import HostObs
+            self.store = HostObs(env.lib, slots, env.n, env.device, 1, regions=1, nslots=2, pack6=True)
+            self.emph = env.emph
+        else:
+            self.px = env.n * 4 * 224 * 240
+            self.lib.rl_pack6.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p]
+            self.staging = torch.empty(self.px // 4 * 3, dtype=torch.uint8, device=env.device)
 
-    def __call__(self):
-        import torch
-        k = self.t % self.slots
-        cur = torch.cuda.current_stream(self.env.device)
-        if self.mode == 'host' and self.copied[k] is not None:
-            cur.wait_event(self.copied[k])            # the slot's previous copy has left the staging buffer
-        st = ctypes.c_void_p(cur.cuda_stream)
-        if self.lib.rl_pack6(ctypes.c_void_p(self.env.obs.data_ptr()), ctypes.c_void_p(self.staging[k].data_ptr()),
-                             self.px, st) != 0:
-            raise RuntimeError(self.lib.rlenv_error().decode())
+    def before(self):
+        """Ahead of a decision: point the env's pictures at the ring slot it draws into."""
         if self.mode == 'host':
-            packed = torch.cuda.Event()
-            packed.record(cur)
-            self.side.wait_event(packed)
-            if self.lib.rl_memcpy_async(ctypes.c_void_p(self.host[k]), ctypes.c_void_p(self.staging[k].data_ptr()),
-                                        self.px // 4 * 3, ctypes.c_void_p(self.side.cuda_stream)) != 0:
+            tt = self.t % self.store.T
+            self.store.before_write(tt - 1)
+            self.env.bind_obs(self.store.slot(0, tt), self.emph)
+
+    def after(self):
+        import torch
+        if self.mode == 'host':
+            self.store.saved(0, self.t % self.store.T)
+        else:
+            st = ctypes.c_void_p(torch.cuda.current_stream(self.env.device).cuda_stream)
+            if self.lib.rl_pack6(ctypes.c_void_p(self.env.obs.data_ptr()), ctypes.c_void_p(self.staging.data_ptr()),
+                                 self.px, st) != 0:
                 raise RuntimeError(self.lib.rlenv_error().decode())
-            ev = torch.cuda.Event()
-            ev.record(self.side)
-            self.copied[k] = ev
         self.t += 1
 
+    def obs(self):
+        """The pictures of the last decision."""
+        return self.store.slot(0, (self.t - 1) % self.store.T) if self.mode == 'host' else self.env.obs
+
     def close(self):
-        import torch
-        torch.cuda.synchronize()
-        for p in self.host:
-            self.lib.rl_host_free(ctypes.c_void_p(p))
-        self.host = []
+        if self.mode == 'host':
+            self.store.close()
 
 
 def bench_env(args):
@@ -221,12 +211,15 @@ def bench_env(args):
     env.start()
     for t in range(W):
         env.actions.copy_(pads[t])
+        if sink:
+            sink.before()
         env.step()
         if sink:
-            sink()
+            sink.after()
     torch.cuda.synchronize()
     ncmp = min(args.cpu_consoles, N)
-    snap = {k: getattr(env, k)[:ncmp].cpu().numpy() for k in ('obs', 'emph', 'reward', 'done', 'ram_hash')}
+    snap = {k: getattr(env, k)[:ncmp].cpu().numpy() for k in ('emph', 'reward', 'done', 'ram_hash')}
+    snap['obs'] = (sink.obs() if sink else env.obs)[:ncmp].cpu().numpy()
     instr0 = _instructions(env)
     print('[bench] warmup done', file=sys.stderr, flush=True)
 
@@ -240,9 +233,11 @@ def bench_env(args):
     t0 = time.perf_counter()
     for t in range(W, W + K):
         env.actions.copy_(pads[t])
+        if sink:
+            sink.before()
         env.step()
         if sink:
-            sink()
+            sink.after()
         if w['end_prob']:
             ends += env.done.sum()
     torch.cuda.synchronize()

@@ -94,8 +94,9 @@ def test_places_weighted_plan():
     env_idx = [1, 6, 3]
     slot_idx = [2, 4, 0]                                  # slot 0 is a level slot: skipped
     cpu.place_save(0, torch.tensor(env_idx, dtype=torch.int32), torch.tensor(slot_idx, dtype=torch.int32))
-    gpu.place_save(0, torch.tensor(env_idx, dtype=torch.int32, device='cuda'),
-                   torch.tensor(slot_idx, dtype=torch.int32, device='cuda'))
+    env_d = torch.tensor(env_idx, dtype=torch.int32, device='cuda')
+    slot_d = torch.tensor(slot_idx, dtype=torch.int32, device='cuda')
+    gpu.place_save(0, env_d, slot_d)
     for e in (cpu, gpu):
         e.place_copy(0, [4], [3])
         e.set_level_plan(0, 0.9, np.array([0, 0, 0.25, 0.25, 0.5]))
