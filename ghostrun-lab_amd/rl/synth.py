@@ -380,6 +380,97 @@ def mmc3_cart(seed: int = 0, blocks: int = 16, sub_blocks: int = 20) -> bytes:
     return ines(prg, chr_, 4, vertical=True)
 
 
+MMC1_CTRL = 0x46                          # the MMC1 cart's shadow of its control register
+
+
+def _mmc1_write(a: Asm, addr: int):
+    """MMC1 serial port: the 5 low bits of A, least significant first (A is shifted out)."""
+    for _ in range(4):
+        a.op('STA', 'abs', addr); a.op('LSR', 'acc')
+    a.op('STA', 'abs', addr)
+
+
+def mmc1_cart(seed: int = 0, blocks: int = 16, sub_blocks: int = 16) -> bytes:
+    """MMC1 cartridge in the layout of the MMC1 games of the set: 128 KB PRG in 16 KB banks (mode 3: banks 0-6
+    switched in at $8000, bank 7 fixed at $C000), 8 KB CHR RAM filled by the program, PRG RAM at $6000.
+    The main loop switches the $8000 bank through the serial port and calls the subroutine there, works on PRG RAM,
+    and flips the mirroring now and then; the NMI rewrites one CHR RAM tile per frame (an animated tile)."""
+    rng = np.random.default_rng([0x4D4D4331, seed])
+    pal, nt, oam, mix = _tables(rng)
+    banks = []
+    for b in range(7):   # switchable: a subroutine at $8000
+        s = Asm(0x8000)
+        _filler(s, rng, sub_blocks, f'b{b}', 0xBF00, with_prg_ram=True)
+        s.op('RTS')
+        body = s.assemble()
+        page = bytearray(16384)
+        page[:len(body)] = body
+        page[0x3F00:0x4000] = rng.integers(0, 256, 256, dtype=np.uint8).tobytes()   # table at $BF00
+        banks.append(bytes(page))
+    tiles = rng.integers(0, 256, 4096, dtype=np.uint8)
+    a = Asm(0xE000)
+    a.labels.update({k: v for k, v in (('t_pal', 0xC000), ('t_nt', 0xC020), ('t_oam', 0xC120), ('t_mix', 0xC220),
+                                       ('t_tiles', 0xD000))})
+    tables = dict(pal='t_pal', nt='t_nt', oam='t_oam')
+    a.label('reset')
+    a.op('SEI'); a.op('LDA', 'imm', 0x80); a.op('STA', 'abs', 0x8000)   # serial port reset: PRG mode 3
+    a.op('LDA', 'imm', 0x0E); _mmc1_write(a, 0x8000)                      # vertical, PRG mode 3, CHR 8 KB
+    a.op('LDA', 'imm', 0); _mmc1_write(a, 0xE000)                         # bank 0, PRG RAM on
+    _reset_common(a, 0x80, tables)                                        # NMI on, BG and sprites at $0000
+    a.op('LDA', 'imm', 0); a.op('STA', 'abs', 0x2000); a.op('STA', 'abs', 0x2001)   # NMI and rendering off: upload
+    a.op('LDA', 'abs', 0x2002); a.op('LDA', 'imm', 0); a.op('STA', 'abs', 0x2006); a.op('STA', 'abs', 0x2006)
+    a.op('LDY', 'imm', 0)
+    for half in range(2):                                                 # 2 x 4 KB of tiles
+        for page in range(16):
+            a.label(f'up{half}_{page}')
+            a.op('LDA', 'aby', 0xD000 + page * 256)
+            if half:
+                a.op('EOR', 'imm', 0x5A)
+            a.op('STA', 'abs', 0x2007); a.op('INY'); a.op('BNE', 'rel', f'up{half}_{page}')
+    a.op('LDA', 'imm', 0x0E); a.op('STA', 'zp', MMC1_CTRL)
+    a.op('LDA', 'zp', CTRL_SHADOW); a.op('STA', 'abs', 0x2000); a.op('LDA', 'imm', 0x1E); a.op('STA', 'abs', 0x2001)
+    a.label('main')
+    _read_pad(a, 'm')
+    _pad_moves(a, 't_mix')
+    a.op('LDA', 'zp', CNT_LO); a.op('EOR', 'zp', PAD); a.op('AND', 'imm', 0x07); a.op('CMP', 'imm', 7)
+    a.op('BCC', 'rel', 'bk_ok'); a.op('LDA', 'imm', 3)
+    a.label('bk_ok')
+    a.op('STA', 'zp', BANK); _mmc1_write(a, 0xE000)
+    a.op('JSR', 'abs', 0x8000)
+    _filler(a, rng, blocks, 'f', 't_mix', with_prg_ram=True)
+    a.op('LDA', 'zp', CNT_LO); a.op('AND', 'imm', 0x1F); a.op('BNE', 'rel', 'no_mir')
+    a.op('LDA', 'zp', MMC1_CTRL); a.op('EOR', 'imm', 0x01); a.op('STA', 'zp', MMC1_CTRL); _mmc1_write(a, 0x8000)   # V <-> H
+    a.label('no_mir')
+    a.op('JMP', 'abs', 'main')
+    a.label('nmi')
+    _nmi_common(a)
+    # one CHR RAM tile per frame: tile (FRAMES & 63) of pattern table 0 from the tile table, shifted by the frame
+    a.op('LDA', 'abs', 0x2002)
+    a.op('LDA', 'zp', FRAMES); a.op('AND', 'imm', 0x3F); a.op('LSR', 'acc'); a.op('LSR', 'acc'); a.op('LSR', 'acc')
+    a.op('LSR', 'acc'); a.op('STA', 'abs', 0x2006)
+    a.op('LDA', 'zp', FRAMES); a.op('ASL', 'acc'); a.op('ASL', 'acc'); a.op('ASL', 'acc'); a.op('ASL', 'acc')
+    a.op('STA', 'abs', 0x2006)
+    a.op('LDX', 'imm', 16); a.op('LDY', 'zp', FRAMES)
+    a.label('tile')
+    a.op('LDA', 'aby', 0xD000); a.op('STA', 'abs', 0x2007); a.op('INY'); a.op('DEX'); a.op('BNE', 'rel', 'tile')
+    a.op('LDA', 'zp', PX); a.op('STA', 'abs', 0x2005); a.op('LDA', 'imm', 0); a.op('STA', 'abs', 0x2005)
+    a.op('LDA', 'zp', CTRL_SHADOW); a.op('STA', 'abs', 0x2000)
+    _nmi_end(a)
+    a.label('irq')
+    a.op('RTI')
+    code = a.assemble()
+    assert len(code) <= 0x1FFA, len(code)
+    fixed = bytearray(16384)
+    for name, t in (('t_pal', pal), ('t_nt', nt), ('t_oam', oam), ('t_mix', mix)):
+        off = a.labels[name] - 0xC000
+        fixed[off:off + len(t)] = bytes(int(v) for v in t)
+    fixed[0x1000:0x2000] = tiles.tobytes()
+    fixed[0x2000:0x2000 + len(code)] = code
+    vec = (a.labels['nmi'], a.labels['reset'], a.labels['irq'])
+    fixed[0x3FFA:0x4000] = bytes(sum(((v & 0xFF, v >> 8) for v in vec), ()))
+    return ines(b''.join(banks) + bytes(fixed), b'', 1, vertical=True)
+
+
 DCNT, DYCNT = 0x44, 0x45                  # frames Down has been held, frames spent dying
 
 

@@ -65,3 +65,20 @@ def test_mmc3_stress():
     print('case: MMC3 seed 3, 16 consoles, raw pads, IRQ + sprite-0 + bank switches', flush=True)
     cpu, gpu = pair(16, synth.mmc3_cart(3), seed=9, sticky=True, idle_max=0, dropout=False, pad_mode=True)
     run(cpu, gpu, 16, 2, True)
+
+
+@pytest.mark.gpu
+def test_mmc1_chr_ram_bank_switches():
+    print('case: MMC1 seed 2, 16 consoles, 8-frame boot, raw pads, sticky, Geometric(1/8) ends, 20 decisions',
+          flush=True)
+    cpu, gpu = pair(16, synth.mmc1_cart(2), seed=17, sticky=True, idle_max=2, dropout=True, pad_mode=True,
+                    end_prob=1 / 8, boot={'smb': bytes(8)})
+    run(cpu, gpu, 20, 3, True)
+
+
+@pytest.mark.gpu
+def test_mmc1_from_power_on():
+    print('case: MMC1 seed 3, 8 consoles, boot from power-on (CHR RAM upload in the decisions), 12 decisions',
+          flush=True)
+    cpu, gpu = pair(8, synth.mmc1_cart(3), seed=18, sticky=False, idle_max=0, dropout=False, pad_mode=True)
+    run(cpu, gpu, 12, 4, True)

@@ -148,6 +148,24 @@ def test_mmc1_prg_ram_enable():
     assert con.read(0x6000) == 0x5A
 
 
+def test_mmc1_synthetic_cart_switches_banks_mirroring_and_chr_ram():
+    """The seed-generated MMC1 cart (the GPU parity case) does what it is for: it uploads its tiles into CHR RAM,
+    switches the $8000 bank, flips the mirroring, keeps a CHR RAM tile animated and works in PRG RAM."""
+    con = Console(synth.mmc1_cart(1))
+    t, seen_prg, seen_nt, chr_sums = 82182, set(), set(), []
+    for f in range(40):
+        con.set('pad', [0x81, 0x40, 0x02, 0x90][f % 4])
+        assert con.run_until(t) == 0
+        t += 89342
+        prg, _, nt = pages(con)
+        seen_prg.add(prg[0])
+        seen_nt.add(tuple(nt))
+        chr_sums.append(int(con.rec[0x3C00:0x5C00].astype(np.int64).sum()))
+    assert len(seen_prg) >= 4 and len(seen_nt) == 2
+    assert chr_sums[10] > 0 and len(set(chr_sums[10:])) > 5
+    assert con.rec[0x1C00:0x3C00].any()
+
+
 # ------------------------------------------------------------------------------------------------ DMC
 
 KBYTE = 8 * 54                                           # rate 15: 54 CPU cycles per bit
