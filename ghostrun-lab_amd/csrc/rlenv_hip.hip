@@ -319,37 +319,36 @@ __device__ __forceinline__ void render_wave(const NesRec* rec, uint32_t log_n, c
             const int h = (ctrl & 0x20u) ? 16 : 8;
             const int row_me = l - (int)my_sy - 1;
             uint64_t sel = __ballot(sp_on && row_me >= 0 && row_me < h);
-            // background, 4 pixels
-            uint32_t bgv[4], bga[4];
+            // background, 4 pixels: the lane's pixels x0..x0+3 lie in tile slots A = (x0 + fx) / 8 and A + 1; both
+            // are fetched by every lane (no per-lane branches) and each pixel selects its own
+            uint32_t bgv[4] = {0, 0, 0, 0}, bga[4] = {0, 0, 0, 0};
             const uint32_t x0 = 4u * (uint32_t)lane;
-            const uint32_t cy = (s.v >> 5) & 31u, fy = (s.v >> 12) & 7u, ntv = (s.v >> 11) & 1u;
-            uint32_t cached_slot = 0xFFFFFFFFu, lo = 0, hi = 0, pal_sel = 0;
-            for (int q = 0; q < 4; ++q) {
-                const uint32_t x = x0 + (uint32_t)q;
-                bgv[q] = 0;
-                bga[q] = 0;
-                if (!bg_on || (x < 8u && !(mask & 0x02u))) continue;
-                const uint32_t pos = x + s.fx, slot = pos >> 3;
-                if (slot != cached_slot) {
-                    cached_slot = slot;
-                    uint32_t cx = (s.v & 31u) + slot, nth = (s.v >> 10) & 1u;
-                    if (cx >= 32u) {
-                        cx -= 32u;
-                        nth ^= 1u;
-                    }
+            if (bg_on) {
+                const uint32_t cy = (s.v >> 5) & 31u, fy = (s.v >> 12) & 7u, ntv = (s.v >> 11) & 1u;
+                const uint32_t pos0 = x0 + s.fx, slot_a = pos0 >> 3;
+                uint32_t lo[2], hi[2], ps[2];
+                for (int k = 0; k < 2; ++k) {
+                    const uint32_t c = (s.v & 31u) + slot_a + (uint32_t)k;   // < 64; the slot-33 fetch is unused
+                    const uint32_t wrap = c >= 32u ? 1u : 0u;
+                    const uint32_t cx = c - 32u * wrap, nth = ((s.v >> 10) & 1u) ^ wrap;
                     const uint32_t base = 0x2000u | ((nth | (ntv << 1)) << 10);
-                    const uint32_t tile = nt_s[nt_index(s.nt_map, base | (cy << 5) | cx)];
-                    const uint32_t at = nt_s[nt_index(s.nt_map, base | 0x3C0u | ((cy >> 2) << 3) | (cx >> 2))];
-                    pal_sel = (at >> (((cy & 2u) << 1) | (cx & 2u))) & 3u;
+                    const uint32_t tile = nt_s[nt_index(s.nt_map, base | (cy << 5) | (cx & 31u))];
+                    const uint32_t at = nt_s[nt_index(s.nt_map, base | 0x3C0u | ((cy >> 2) << 3) | ((cx & 31u) >> 2))];
+                    ps[k] = (at >> (((cy & 2u) << 1) | (cx & 2u))) & 3u;
                     const uint32_t pa = ((ctrl & 0x10u) << 8) + tile * 16u + fy;
-                    lo = chr_byte_pk(m, s.chr_lo, s.chr_hi, pa);
-                    hi = chr_byte_pk(m, s.chr_lo, s.chr_hi, pa + 8u);
+                    lo[k] = chr_byte_pk(m, s.chr_lo, s.chr_hi, pa);
+                    hi[k] = chr_byte_pk(m, s.chr_lo, s.chr_hi, pa + 8u);
                 }
-                const uint32_t b = 7u - (pos & 7u);
-                bgv[q] = ((lo >> b) & 1u) | (((hi >> b) & 1u) << 1);
-                bga[q] = pal_sel;
+                for (int q = 0; q < 4; ++q) {
+                    const uint32_t pos = pos0 + (uint32_t)q, k = (pos >> 3) - slot_a, b = 7u - (pos & 7u);
+                    const uint32_t plo = k ? lo[1] : lo[0], phi = k ? hi[1] : hi[0];
+                    const uint32_t v = ((plo >> b) & 1u) | (((phi >> b) & 1u) << 1);
+                    const bool clip = x0 + (uint32_t)q < 8u && !(mask & 0x02u);
+                    bgv[q] = clip ? 0u : v;
+                    bga[q] = k ? ps[1] : ps[0];
+                }
             }
-            // sprites: the first 8 in OAM order that cover this line
+            // sprites: the first 8 in OAM order that cover this line; per pixel the first opaque one wins
             uint32_t spv[4] = {0, 0, 0, 0}, spa[4] = {0, 0, 0, 0}, spb[4] = {0, 0, 0, 0};
             for (int n = 0; n < 8 && sel != 0; ++n) {
                 const uint32_t i = (uint32_t)__builtin_ctzll(sel);
@@ -357,16 +356,15 @@ __device__ __forceinline__ void render_wave(const NesRec* rec, uint32_t log_n, c
                 const uint32_t sy = oam_s[4 * i], tile = oam_s[4 * i + 1], attr = oam_s[4 * i + 2], sx = oam_s[4 * i + 3];
                 const uint32_t pa = sprite_row_addr(ctrl, tile, attr, (uint32_t)(l - (int)sy - 1));
                 const uint32_t plo = chr_byte_pk(m, s.chr_lo, s.chr_hi, pa), phi = chr_byte_pk(m, s.chr_lo, s.chr_hi, pa + 8u);
+                const uint32_t flip = (attr & 0x40u) ? 0u : 7u, pal_hi = attr & 3u, behind = (attr >> 5) & 1u;
                 for (int q = 0; q < 4; ++q) {
                     const uint32_t x = x0 + (uint32_t)q, col = x - sx;
-                    if (spv[q] || col >= 8u || (x < 8u && !(mask & 0x04u))) continue;
-                    const uint32_t b = (attr & 0x40u) ? col : 7u - col;
+                    const uint32_t b = (flip ^ col) & 7u;   // col, or 7 - col when not flipped
                     const uint32_t p = ((plo >> b) & 1u) | (((phi >> b) & 1u) << 1);
-                    if (p) {
-                        spv[q] = p;
-                        spa[q] = attr & 3u;
-                        spb[q] = (attr >> 5) & 1u;
-                    }
+                    const bool take = spv[q] == 0u && col < 8u && !(x < 8u && !(mask & 0x04u)) && p != 0u;
+                    spv[q] = take ? p : spv[q];
+                    spa[q] = take ? pal_hi : spa[q];
+                    spb[q] = take ? behind : spb[q];
                 }
             }
             uint32_t word = 0;
