@@ -57,7 +57,7 @@ struct Con {
 
 struct Cart {
     const uint32_t* prgw;   // widened PRG
-    const uint32_t* fetchw; // NROM: instruction window of every CPU address (kFetchWords entries), else nullptr
+    const uint32_t* fetchw; // NROM: instruction window of every CPU address (kFetchWords x 2 words), else nullptr
     const uint8_t* chr;     // CHR ROM, nullptr = CHR RAM in the record
     uint32_t prg_pages8;    // 8 KB pages (power of two)
     uint32_t chr_pages1;    // 1 KB pages (power of two)
@@ -65,9 +65,10 @@ struct Cart {
     uint32_t mirroring;     // header: 0 horizontal, 1 vertical
 };
 
-// NROM instruction-fetch table: entry a = the bytes at CPU addresses a, a+1, a+2 through the NROM mapping, for
-// $8000 <= a <= $FFFD; every other entry (RAM, I/O, the last two bytes, and a pc just past $FFFF) holds opcode $02,
-// which no fast-path handler runs, so the generic step fetches it.
+// NROM instruction-fetch table: entry a = {opcode, operand word} (two dwords: the byte at CPU address a, and the
+// bytes at a+1 | a+2 << 8) through the NROM mapping, for $8000 <= a <= $FFFD; every other entry (RAM, I/O, the last
+// two bytes, and a pc just past $FFFF) holds opcode $02, which no fast-path handler runs, so the generic step
+// fetches it.
 constexpr uint32_t kFetchWords = 0x10100u;
 
 struct Mem {

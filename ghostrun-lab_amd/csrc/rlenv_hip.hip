@@ -1112,11 +1112,13 @@ void* rlenv_create(int ngames, const int* game_ids, const uint8_t* const* roms, 
             if (chr_pages & (chr_pages - 1u)) throw std::runtime_error("CHR size must be a power of two");
             uint32_t* fetchw = nullptr;
             if (p.board == NES_BOARD_NROM) {
-                std::vector<uint32_t> f(kFetchWords, 0x02u);
+                std::vector<uint32_t> f(2u * kFetchWords, 0u);
+                for (uint32_t a = 0; a < kFetchWords; ++a) f[2u * a] = 0x02u;
                 const size_t mask = (p.prg.size() - 1u) & 0x7FFFu;
-                for (uint32_t a = 0x8000u; a <= 0xFFFDu; ++a)
-                    f[a] = p.prg[a & mask] | ((uint32_t)p.prg[(a + 1u) & mask] << 8) |
-                           ((uint32_t)p.prg[(a + 2u) & mask] << 16);
+                for (uint32_t a = 0x8000u; a <= 0xFFFDu; ++a) {
+                    f[2u * a] = p.prg[a & mask];
+                    f[2u * a + 1u] = p.prg[(a + 1u) & mask] | ((uint32_t)p.prg[(a + 2u) & mask] << 8);
+                }
                 fetchw = static_cast<uint32_t*>(env->mem.alloc(f.size() * 4));
                 env->mem.upload(fetchw, f.data(), f.size() * 4);
             }

@@ -18,6 +18,7 @@
 namespace nd {
 
 typedef __attribute__((address_space(4))) const uint32_t ConstU32;
+typedef __attribute__((address_space(4))) const uint64_t ConstU64;
 
 // Registers the fast loop keeps live: the CPU registers, the cycle counter and the PRG page offsets. Everything
 // else about the console (PPU, controller, DMC, mapper) stays in the console state in LDS and only the generic
@@ -128,7 +129,7 @@ __device__ __forceinline__ uint32_t prg_wide(const Mem& m, uint32_t idx) {
 // One instruction of opcode descriptor D at pc (operand bytes lo, hi). Returns its CPU cycles (the caller adds them
 // to the cycle counter and services the DMC), or 0 with nothing changed when the generic step must run it.
 template <uint32_t B, uint32_t D>
-__device__ __forceinline__ uint32_t fx(Hot& h, const Mem& m, Con& cs, uint32_t pc, uint32_t lo, uint32_t hi) {
+__device__ __forceinline__ uint32_t fx(Hot& h, const Mem& m, Con& cs, uint32_t pc, uint32_t base) {
     constexpr uint32_t mode = D & 15u, grp = (D >> 8) & 15u, sub = (D >> 12) & 15u;
     constexpr uint32_t src = (D >> 16) & 7u, dst = (D >> 19) & 7u;
     constexpr bool rd = (D & D_READ) != 0, wr = (D & D_WRITE) != 0, pen = (D & D_PEN) != 0;
@@ -137,7 +138,7 @@ __device__ __forceinline__ uint32_t fx(Hot& h, const Mem& m, Con& cs, uint32_t p
         return 0;
     } else {
         uint32_t cyc = (D >> 4) & 15u;
-        const uint32_t base = lo | (hi << 8);
+        const uint32_t lo = base & 0xFFu;   // base: the two operand bytes, lo | hi << 8
         uint32_t ea = 0;
         if constexpr (mode == M_ZP) {
             ea = lo;
@@ -289,7 +290,7 @@ __device__ __forceinline__ uint32_t fx(Hot& h, const Mem& m, Con& cs, uint32_t p
 }
 
 #define ND_FX(n) \
-    case n: return fx<B, kOptab.t[n]>(h, m, cs, pc, lo, hi);
+    case n: return fx<B, kOptab.t[n]>(h, m, cs, pc, base);
 #define ND_FX16(h)                                                                                                    \
     ND_FX(h + 0x0) ND_FX(h + 0x1) ND_FX(h + 0x2) ND_FX(h + 0x3) ND_FX(h + 0x4) ND_FX(h + 0x5) ND_FX(h + 0x6)          \
     ND_FX(h + 0x7) ND_FX(h + 0x8) ND_FX(h + 0x9) ND_FX(h + 0xA) ND_FX(h + 0xB) ND_FX(h + 0xC) ND_FX(h + 0xD)          \
@@ -299,18 +300,22 @@ __device__ __forceinline__ uint32_t fx(Hot& h, const Mem& m, Con& cs, uint32_t p
 template <uint32_t B>
 __device__ __forceinline__ uint32_t fast_step(Hot& h, const Mem& m, Con& cs, uint32_t* op_out) {
     const uint32_t pc = h.pc;
-    uint32_t word;
+    uint32_t op, base;
     if constexpr (B == NES_BOARD_NROM) {
-        // pc <= $1007E (a branch just past $FFFF); $02 outside PRG. The mask only tells the compiler that the
-        // index is a small 32-bit value, so the load takes it as a scalar byte offset (no 64-bit address add).
-        word = ((ConstU32*)m.cart.fetchw)[pc & 0x1FFFFu];
+        // pc <= $1007E (a branch just past $FFFF); $02 outside PRG. The entry is the opcode and the operand word
+        // as two dwords (no field extraction); the mask only tells the compiler that the index is a small 32-bit
+        // value, so the load takes it as a scalar byte offset (no 64-bit address add).
+        const uint64_t w = ((ConstU64*)m.cart.fetchw)[pc & 0x1FFFFu];
+        op = (uint32_t)w;
+        base = (uint32_t)(w >> 32);
     } else {
         // code in PRG ($8000+) and the 3-byte window inside one 8 KB page: pc >= $8000 and (pc & $1FFF) <= $1FFD,
         // as one compare ((pc + 2) & $9FFF keeps bit 15 and the page offset of the window's last byte)
         if (((pc + 2u) & 0x9FFFu) < 0x8002u) return 0;
-        word = prg_wide(m, prg_index<B>(h, m, pc));
+        const uint32_t word = prg_wide(m, prg_index<B>(h, m, pc));
+        op = word & 0xFFu;
+        base = word >> 8;   // bits 24-31 of the word are 0
     }
-    const uint32_t op = word & 0xFFu, lo = (word >> 8) & 0xFFu, hi = word >> 16;   // bits 24-31 are 0
     *op_out = op;
     switch (op) {
         ND_FX16(0x00) ND_FX16(0x10) ND_FX16(0x20) ND_FX16(0x30) ND_FX16(0x40) ND_FX16(0x50) ND_FX16(0x60)
