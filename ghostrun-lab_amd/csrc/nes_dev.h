@@ -65,11 +65,29 @@ struct Cart {
     uint32_t mirroring;     // header: 0 horizontal, 1 vertical
 };
 
-// NROM instruction-fetch table: entry a = {opcode, operand word} (two dwords: the byte at CPU address a, and the
-// bytes at a+1 | a+2 << 8) through the NROM mapping, for $8000 <= a <= $FFFD; every other entry (RAM, I/O, the last
-// two bytes, and a pc just past $FFFF) holds opcode $02, which no fast-path handler runs, so the generic step
-// fetches it.
+// NROM instruction-fetch table: entry a = {dispatch key, operand word} (two dwords: the opcode at CPU address a, or
+// its hot key for the opcodes of kHotOps, and the bytes at a+1 | a+2 << 8) through the NROM mapping, for
+// $8000 <= a <= $FFFD; every other entry (RAM, I/O, the last two bytes, and a pc just past $FFFF) holds opcode $02,
+// which no fast-path handler runs, so the generic step fetches it.
 constexpr uint32_t kFetchWords = 0x10100u;
+
+// Opcodes the NROM fetch table stores as hot keys $100 + i (i = index here) instead of the opcode: the interpreter
+// dispatches a hot key through a switch of 32 cases (5 compares) after one range check, and every other opcode
+// through the switch over all 256 (8 compares). The list is the common core of 6502 game code: loads and stores of
+// A, the conditional branches, subroutine calls, counters, and the immediate-operand arithmetic and shifts.
+constexpr uint32_t kHotOps[32] = {
+    0xA9u, 0xA5u, 0xADu, 0xBDu, 0xB9u, 0xB1u, 0xA2u, 0xA6u, 0xA0u,   // LDA #, zp, abs, abs,X, abs,Y, (zp),Y; LDX #, zp; LDY #
+    0x85u, 0x8Du, 0x9Du, 0x99u,                                      // STA zp, abs, abs,X, abs,Y
+    0xD0u, 0xF0u, 0x10u, 0x90u, 0xB0u,                               // BNE BEQ BPL BCC BCS
+    0x20u, 0x60u, 0x4Cu,                                             // JSR RTS JMP
+    0xE8u, 0xCAu, 0xC8u, 0x88u,                                      // INX DEX INY DEY
+    0xC9u, 0x29u, 0x18u, 0x69u, 0x4Au, 0x0Au, 0xAAu};                // CMP # AND # CLC ADC # LSR A ASL A TAX
+constexpr uint32_t kHotKey = 0x100u;
+constexpr bool is_hot(uint32_t op) {
+    for (uint32_t i = 0; i < 32u; ++i)
+        if (kHotOps[i] == op) return true;
+    return false;
+}
 
 struct Mem {
     NesRec* rec;
@@ -281,6 +299,7 @@ struct Replay {
     uint32_t chr_lo, chr_hi;   // 1 KB CHR page of slots 0-3 / 4-7, 8 bits each
     uint32_t nt_map;
     uint32_t ev, count;
+    int32_t next;              // time of event ev (INT32_MAX when none is left)
     const uint32_t* events;
 };
 
@@ -326,8 +345,18 @@ __device__ inline void rp_apply(Replay& s, uint32_t i, uint8_t* pal) {
     }
 }
 
+__device__ __forceinline__ void rp_next(Replay& s) {
+    s.next = s.ev < s.count ? rp_time(s, s.ev) : INT32_MAX;
+}
+
+// Applies the events before `time`; the time of the next one is kept in a register, so a check with nothing to apply
+// reads no memory.
 __device__ inline void rp_until(Replay& s, int32_t time, uint8_t* pal) {
-    while (s.ev < s.count && rp_time(s, s.ev) < time) rp_apply(s, s.ev++, pal);
+    while (s.next < time) {
+        rp_apply(s, s.ev, pal);
+        ++s.ev;
+        rp_next(s);
+    }
 }
 
 __device__ inline void rp_yinc(Replay& s) {
@@ -363,7 +392,8 @@ __device__ inline void rp_line_end(Replay& s, int l, uint8_t* pal) {
     rp_until(s, base + 320, pal);
 }
 
-__device__ inline void rp_begin(Replay& s, const uint32_t* log, uint32_t log_n, uint8_t* pal) {
+// events: the log's event words (from `log` + NES_LOG_HDR_WORDS on), in place or a copy of them.
+__device__ inline void rp_begin(Replay& s, const uint32_t* log, uint32_t log_n, uint8_t* pal, const uint32_t* events) {
     const uint32_t h1 = log[1], h2 = log[2], h3 = log[3], h4 = log[4];
     s.ctrl = h1 & 0xFFu;
     s.mask = (h1 >> 8) & 0xFFu;
@@ -379,9 +409,10 @@ __device__ inline void rp_begin(Replay& s, const uint32_t* log, uint32_t log_n, 
             pal[4 * i] = (uint8_t)w; pal[4 * i + 1] = (uint8_t)(w >> 8);
             pal[4 * i + 2] = (uint8_t)(w >> 16); pal[4 * i + 3] = (uint8_t)(w >> 24);
         }
-    s.events = log + NES_LOG_HDR_WORDS;
+    s.events = events;
     s.count = log_n < NES_LOG_EVENTS ? log_n : NES_LOG_EVENTS;
     s.ev = 0;
+    rp_next(s);
     rp_line_end(s, -1, pal);
 }
 
@@ -417,7 +448,7 @@ __device__ __forceinline__ int32_t sprite0_scan(const Mem m, uint32_t log_n) {
     if (y0 >= 239) return (int32_t)kNoHit;
     const uint32_t tile = oam[1], attr = oam[2];
     Replay s;
-    rp_begin(s, m.rec->log, log_n, nullptr);
+    rp_begin(s, m.rec->log, log_n, nullptr, m.rec->log + NES_LOG_HDR_WORDS);
     for (int l = 0; l < 240; ++l) {
         const int h = (s.ctrl & 0x20u) ? 16 : 8;
         const int row = l - y0 - 1;

@@ -304,11 +304,12 @@ struct RenderArgs {
 // (wave-uniform state), each lane composes 4 pixels of the 256-pixel line, the sprites of a line are picked with
 // one ballot over the 64 OAM entries, and lines 8..231, columns 8..247 go out as one 240-byte row store each
 // (rl/csrc/nes_machine.cuh:133-155). nt/oam: the console's nametables and OAM as of the frame's vblank (LDS);
-// pal: 32 bytes of LDS for the replayed palette.
+// pal: 32 bytes of LDS for the replayed palette; ev_s: the log's events, copied to LDS.
 __device__ __forceinline__ void render_wave(const NesRec* rec, uint32_t log_n, const uint8_t* nt_s, const uint8_t* oam_s,
-                                            uint8_t* pal_s, const Cart& cart, uint8_t* obs, uint8_t* emph, int lane) {
+                                            uint8_t* pal_s, const uint32_t* ev_s, const Cart& cart, uint8_t* obs,
+                                            uint8_t* emph, int lane) {
     Replay s;   // wave-uniform: every lane replays the same log (and stores the same palette bytes)
-    rp_begin(s, rec->log, log_n, pal_s);
+    rp_begin(s, rec->log, log_n, pal_s, ev_s);
     __syncthreads();
     const Mem m = mem_of(const_cast<NesRec*>(rec), nullptr, cart);
     const uint32_t my_sy = oam_s[4 * lane];
@@ -368,12 +369,10 @@ __device__ __forceinline__ void render_wave(const NesRec* rec, uint32_t log_n, c
                 }
             }
             uint32_t word = 0;
-            for (int q = 0; q < 4; ++q) {
-                uint32_t colour;
-                if (bgv[q] && (!spv[q] || spb[q])) colour = pal_s[bga[q] * 4u + bgv[q]];
-                else if (spv[q]) colour = pal_s[16u + spa[q] * 4u + spv[q]];
-                else colour = pal_s[0];
-                colour &= 0x3Fu;
+            for (int q = 0; q < 4; ++q) {   // palette entry: background over a sprite behind it, else the sprite
+                const uint32_t sp_idx = spv[q] ? 16u + spa[q] * 4u + spv[q] : 0u;
+                const uint32_t idx = (bgv[q] && (!spv[q] || spb[q])) ? bga[q] * 4u + bgv[q] : sp_idx;
+                uint32_t colour = pal_s[idx] & 0x3Fu;
                 if (mask & 1u) colour &= 0x30u;
                 word |= colour << (8 * q);
             }
@@ -392,6 +391,7 @@ __global__ __launch_bounds__(64) void k_render(RenderArgs a) {
     __shared__ __align__(16) uint8_t nt_s[2048];
     __shared__ __align__(16) uint8_t oam_s[256];
     __shared__ __align__(16) uint8_t pal_s[32];
+    __shared__ __align__(16) uint32_t ev_s[2 * NES_LOG_EVENTS];
     const int count = slot_count(a.g, a.use_list, a.e0, a.e1);
     const int k = (int)blockIdx.x;
     if (k >= count) return;
@@ -403,9 +403,12 @@ __global__ __launch_bounds__(64) void k_render(RenderArgs a) {
     const NesRec* rec = &a.g.recs[e];
     for (int w = lane; w < 512; w += 64) reinterpret_cast<uint32_t*>(nt_s)[w] = reinterpret_cast<const uint32_t*>(rec->nt)[w];
     reinterpret_cast<uint32_t*>(oam_s)[lane] = reinterpret_cast<const uint32_t*>(rec->oam)[lane];
+    const uint32_t log_n = rec->log_n, ev_words = 2u * (log_n < NES_LOG_EVENTS ? log_n : NES_LOG_EVENTS);
+    for (uint32_t w = (uint32_t)lane; w < ev_words; w += 64u) ev_s[w] = rec->log[NES_LOG_HDR_WORDS + w];
+    __syncthreads();
     uint8_t* obs = a.o.obs + ((size_t)ge * RLE_FRAMES + a.f) * RLE_OBS_PIXELS;
     uint8_t* emph = a.o.emph + ((size_t)ge * RLE_FRAMES + a.f) * RLE_OBS_H;
-    render_wave(rec, rec->log_n, nt_s, oam_s, pal_s, a.g.cart, obs, emph, lane);
+    render_wave(rec, log_n, nt_s, oam_s, pal_s, ev_s, a.g.cart, obs, emph, lane);
 }
 
 // ----------------------------------------------------------------------------------------- finish
@@ -1116,7 +1119,10 @@ void* rlenv_create(int ngames, const int* game_ids, const uint8_t* const* roms, 
                 for (uint32_t a = 0; a < kFetchWords; ++a) f[2u * a] = 0x02u;
                 const size_t mask = (p.prg.size() - 1u) & 0x7FFFu;
                 for (uint32_t a = 0x8000u; a <= 0xFFFDu; ++a) {
-                    f[2u * a] = p.prg[a & mask];
+                    const uint32_t op = p.prg[a & mask];
+                    uint32_t hot = 0;
+                    while (hot < 32u && kHotOps[hot] != op) ++hot;
+                    f[2u * a] = hot < 32u ? kHotKey + hot : op;
                     f[2u * a + 1u] = p.prg[(a + 1u) & mask] | ((uint32_t)p.prg[(a + 2u) & mask] << 8);
                 }
                 fetchw = static_cast<uint32_t*>(env->mem.alloc(f.size() * 4));

@@ -19,18 +19,22 @@ namespace nd {
 
 typedef __attribute__((address_space(4))) const uint32_t ConstU32;
 typedef __attribute__((address_space(4))) const uint64_t ConstU64;
+typedef __attribute__((address_space(4))) const uint8_t ConstU8;
 
 // Registers the fast loop keeps live: the CPU registers, the cycle counter and the PRG page offsets. Everything
 // else about the console (PPU, controller, DMC, mapper) stays in the console state in LDS and only the generic
 // step, the PPU settle and the idle fast-forward touch it, so the loop's live set is small enough to stay in SGPRs.
 // N and Z are kept lazily, as the values they are taken from: N = bit 7 of nv, Z = (zv == 0); the N and Z bits of
-// p are stale in between and are rebuilt when p is stored or pushed. pc may run one past $FFFF after the last
-// instruction of the address space; it is wrapped when stored (the fast path sends such a pc to the generic step).
+// p are stale in between and are rebuilt when p is stored or pushed. pc is held shifted left by pc_shift(board):
+// on NROM times 8, the byte offset of its fetch-table entry, so the fetch needs no address arithmetic. It may run
+// one past $FFFF after the last instruction of the address space and is wrapped when stored (the fast path sends
+// such a pc to the generic step).
 struct Hot {
     uint32_t pc, a, x, y, sp, p, nv, zv;
     uint64_t cycles;
     uint32_t prg0, prg1, prg2, prg3;
 };
+constexpr uint32_t pc_shift(uint32_t board) { return board == NES_BOARD_NROM ? 3u : 0u; }
 
 // A wave-uniform value read from LDS, as a scalar (an LDS load lands in a VGPR; without this the compiler moves every
 // use of it to the vector unit, with lane-mask compares instead of SCC branches).
@@ -44,16 +48,19 @@ __device__ __forceinline__ uint32_t hflags(const Hot& h) {
     return (h.p & ~(FL_N | FL_Z)) | (h.nv & FL_N) | (h.zv ? 0u : FL_Z);
 }
 
+template <uint32_t B>
 __device__ __forceinline__ void hot_load(Hot& h, const Con& c) {
-    h.pc = uni(c.pc); h.a = uni(c.a); h.x = uni(c.x); h.y = uni(c.y); h.sp = uni(c.sp); h.p = uni(c.p);
+    h.pc = uni(c.pc) << pc_shift(B); h.a = uni(c.a); h.x = uni(c.x); h.y = uni(c.y); h.sp = uni(c.sp); h.p = uni(c.p);
     h.nv = h.p;
     h.zv = ~h.p & FL_Z;
     h.cycles = uni64(c.cycles);
     h.prg0 = uni(c.prg0); h.prg1 = uni(c.prg1); h.prg2 = uni(c.prg2); h.prg3 = uni(c.prg3);
 }
 // (the PRG offsets change only in the generic step, which writes them to the console state itself)
+template <uint32_t B>
 __device__ __forceinline__ void hot_store(const Hot& h, Con& c) {
-    c.pc = h.pc & 0xFFFFu; c.a = h.a; c.x = h.x; c.y = h.y; c.sp = h.sp; c.p = hflags(h); c.cycles = h.cycles;
+    c.pc = (h.pc >> pc_shift(B)) & 0xFFFFu; c.a = h.a; c.x = h.x; c.y = h.y; c.sp = h.sp; c.p = hflags(h);
+    c.cycles = h.cycles;
 }
 
 __device__ __forceinline__ uint32_t hget(const Hot& h, uint32_t code, uint32_t opd) {
@@ -126,10 +133,12 @@ __device__ __forceinline__ uint32_t prg_wide(const Mem& m, uint32_t idx) {
     return ((ConstU32*)m.cart.prgw)[idx];
 }
 
-// One instruction of opcode descriptor D at pc (operand bytes lo, hi). Returns its CPU cycles (the caller adds them
-// to the cycle counter and services the DMC), or 0 with nothing changed when the generic step must run it.
+// One instruction of opcode descriptor D at pcs = pc << pc_shift(B) (operand bytes lo, hi). Returns its CPU cycles
+// (the caller adds them to the cycle counter and services the DMC), or 0 with nothing changed when the generic step
+// must run it.
 template <uint32_t B, uint32_t D>
-__device__ __forceinline__ uint32_t fx(Hot& h, const Mem& m, Con& cs, uint32_t pc, uint32_t base) {
+__device__ __forceinline__ uint32_t fx(Hot& h, const Mem& m, Con& cs, uint32_t pcs, uint32_t base) {
+    constexpr uint32_t PS = pc_shift(B);
     constexpr uint32_t mode = D & 15u, grp = (D >> 8) & 15u, sub = (D >> 12) & 15u;
     constexpr uint32_t src = (D >> 16) & 7u, dst = (D >> 19) & 7u;
     constexpr bool rd = (D & D_READ) != 0, wr = (D & D_WRITE) != 0, pen = (D & D_PEN) != 0;
@@ -184,7 +193,7 @@ __device__ __forceinline__ uint32_t fx(Hot& h, const Mem& m, Con& cs, uint32_t p
             }
         }
         constexpr uint32_t len = mode == M_IMP ? 1u : ((mode >= M_ABS && mode <= M_ABY) || mode == M_IND) ? 3u : 2u;
-        uint32_t npc = pc + len, res = 0;   // pc <= $FFFD here; $10000 is wrapped when stored
+        uint32_t npc = pcs + (len << PS), res = 0;   // pc <= $FFFD here; $10000 is wrapped when stored
         if constexpr (grp == G_LD) {
             res = hget(h, src, opd);
             hset(h, dst, res);
@@ -232,8 +241,8 @@ __device__ __forceinline__ uint32_t fx(Hot& h, const Mem& m, Con& cs, uint32_t p
             else if constexpr (bit == 1u) set = h.zv == 0;
             else set = ((h.p >> bit) & 1u) != 0;
             if (set == ((sub & 8u) != 0)) {
-                const uint32_t tgt = npc + (uint32_t)(int32_t)(int8_t)lo;   // wrapped when stored
-                cyc += ((npc ^ tgt) & 0xFF00u) ? 2u : 1u;
+                const uint32_t tgt = npc + ((uint32_t)(int32_t)(int8_t)lo << PS);   // wrapped when stored
+                cyc += ((npc ^ tgt) & (0xFF00u << PS)) ? 2u : 1u;
                 npc = tgt;
             }
         } else if constexpr (grp == G_FLAG) {
@@ -259,25 +268,25 @@ __device__ __forceinline__ uint32_t fx(Hot& h, const Mem& m, Con& cs, uint32_t p
                                                    : (prg_wide(m, prg_index<B>(h, m, base)) & 0xFFu);
                 const uint32_t h8 = a1 < 0x2000u ? rd8(m, a1 & 0x7FFu)
                                                  : (prg_wide(m, prg_index<B>(h, m, a1)) & 0xFFu);
-                npc = l8 | (h8 << 8);
+                npc = (l8 | (h8 << 8)) << PS;
             } else {
-                npc = base;
-                if (npc == pc) return 0;   // the idle loop: the generic step runs it, then the fast-forward
+                npc = base << PS;
+                if (npc == pcs) return 0;   // the idle loop: the generic step runs it, then the fast-forward
             }
         } else if constexpr (grp == G_JSR) {
-            const uint32_t ret = pc + 2u;   // <= $FFFF
+            const uint32_t ret = (pcs >> PS) + 2u;   // <= $FFFF
             hpush(h, m, ret >> 8);
             hpush(h, m, ret & 0xFFu);
-            npc = base;
+            npc = base << PS;
         } else if constexpr (grp == G_RTS) {
             const uint32_t l8 = hpull(h, m), h8 = hpull(h, m);
-            npc = ((h8 << 8) | l8) + 1u;
+            npc = (((h8 << 8) | l8) + 1u) << PS;
         } else if constexpr (grp == G_RTI) {
             h.p = (hpull(h, m) & ~FL_B) | FL_U;
             h.nv = h.p;
             h.zv = ~h.p & FL_Z;
             const uint32_t l8 = hpull(h, m), h8 = hpull(h, m);
-            npc = (h8 << 8) | l8;
+            npc = ((h8 << 8) | l8) << PS;
         }
         if constexpr (wr) {
             if constexpr (zpage || rd) m.ram[ea & 0x7FFu] = (uint8_t)res;
@@ -289,34 +298,22 @@ __device__ __forceinline__ uint32_t fx(Hot& h, const Mem& m, Con& cs, uint32_t p
     }
 }
 
-#define ND_FX(n) \
-    case n: return fx<B, kOptab.t[n]>(h, m, cs, pc, base);
+// (on NROM a hot opcode never reaches the switch over all opcodes: its case merges into the default)
+#define ND_FX(n)                                                      \
+    case n:                                                           \
+        if constexpr (B == NES_BOARD_NROM && is_hot(n)) return 0;     \
+        else return fx<B, kOptab.t[n]>(h, m, cs, pcs, base);
+#define ND_HOT(i) \
+    case kHotKey + i: return fx<B, kOptab.t[kHotOps[i]]>(h, m, cs, pcs, base);
+#define ND_HOT8(i) ND_HOT(i) ND_HOT(i + 1) ND_HOT(i + 2) ND_HOT(i + 3) ND_HOT(i + 4) ND_HOT(i + 5) ND_HOT(i + 6) ND_HOT(i + 7)
 #define ND_FX16(h)                                                                                                    \
     ND_FX(h + 0x0) ND_FX(h + 0x1) ND_FX(h + 0x2) ND_FX(h + 0x3) ND_FX(h + 0x4) ND_FX(h + 0x5) ND_FX(h + 0x6)          \
     ND_FX(h + 0x7) ND_FX(h + 0x8) ND_FX(h + 0x9) ND_FX(h + 0xA) ND_FX(h + 0xB) ND_FX(h + 0xC) ND_FX(h + 0xD)          \
     ND_FX(h + 0xE) ND_FX(h + 0xF)
 
-// The fast path for the instruction at h.pc: its cycles, or 0 (nothing changed) for the generic step.
+// The opcodes' switch (on NROM without the hot ones, which never reach it).
 template <uint32_t B>
-__device__ __forceinline__ uint32_t fast_step(Hot& h, const Mem& m, Con& cs, uint32_t* op_out) {
-    const uint32_t pc = h.pc;
-    uint32_t op, base;
-    if constexpr (B == NES_BOARD_NROM) {
-        // pc <= $1007E (a branch just past $FFFF); $02 outside PRG. The entry is the opcode and the operand word
-        // as two dwords (no field extraction); the mask only tells the compiler that the index is a small 32-bit
-        // value, so the load takes it as a scalar byte offset (no 64-bit address add).
-        const uint64_t w = ((ConstU64*)m.cart.fetchw)[pc & 0x1FFFFu];
-        op = (uint32_t)w;
-        base = (uint32_t)(w >> 32);
-    } else {
-        // code in PRG ($8000+) and the 3-byte window inside one 8 KB page: pc >= $8000 and (pc & $1FFF) <= $1FFD,
-        // as one compare ((pc + 2) & $9FFF keeps bit 15 and the page offset of the window's last byte)
-        if (((pc + 2u) & 0x9FFFu) < 0x8002u) return 0;
-        const uint32_t word = prg_wide(m, prg_index<B>(h, m, pc));
-        op = word & 0xFFu;
-        base = word >> 8;   // bits 24-31 of the word are 0
-    }
-    *op_out = op;
+__device__ __forceinline__ uint32_t fx_all(Hot& h, const Mem& m, Con& cs, uint32_t pcs, uint32_t op, uint32_t base) {
     switch (op) {
         ND_FX16(0x00) ND_FX16(0x10) ND_FX16(0x20) ND_FX16(0x30) ND_FX16(0x40) ND_FX16(0x50) ND_FX16(0x60)
         ND_FX16(0x70) ND_FX16(0x80) ND_FX16(0x90) ND_FX16(0xA0) ND_FX16(0xB0) ND_FX16(0xC0) ND_FX16(0xD0)
@@ -324,8 +321,43 @@ __device__ __forceinline__ uint32_t fast_step(Hot& h, const Mem& m, Con& cs, uin
         default: return 0;
     }
 }
+
+// The hot keys' switch (NROM).
+template <uint32_t B>
+__device__ __forceinline__ uint32_t fx_hot(Hot& h, const Mem& m, Con& cs, uint32_t pcs, uint32_t op, uint32_t base) {
+    switch (op) {
+        ND_HOT8(0) ND_HOT8(8) ND_HOT8(16) ND_HOT8(24)
+        default: __builtin_unreachable();   // the fetch table holds no other key >= kHotKey
+    }
+}
+
+// The fast path for the instruction at h.pc: its cycles, or 0 (nothing changed) for the generic step.
+template <uint32_t B>
+__device__ __forceinline__ uint32_t fast_step(Hot& h, const Mem& m, Con& cs, uint32_t* op_out) {
+    const uint32_t pcs = h.pc;
+    if constexpr (B == NES_BOARD_NROM) {
+        // pc <= $1007E (a branch just past $FFFF); $02 outside PRG. The entry is the key (the opcode, or a hot key
+        // $100 + i for kHotOps[i]) and the operand word as two dwords (no field extraction), at byte offset
+        // pcs = pc * 8: a scalar load with an SGPR offset.
+        const uint64_t w = *(const ConstU64*)((ConstU8*)m.cart.fetchw + pcs);
+        const uint32_t op = (uint32_t)w, base = (uint32_t)(w >> 32);
+        *op_out = op;
+        if (op >= kHotKey) return fx_hot<B>(h, m, cs, pcs, op, base);
+        return fx_all<B>(h, m, cs, pcs, op, base);
+    } else {
+        // code in PRG ($8000+) and the 3-byte window inside one 8 KB page: pc >= $8000 and (pc & $1FFF) <= $1FFD,
+        // as one compare ((pc + 2) & $9FFF keeps bit 15 and the page offset of the window's last byte)
+        if (((pcs + 2u) & 0x9FFFu) < 0x8002u) return 0;
+        const uint32_t word = prg_wide(m, prg_index<B>(h, m, pcs));
+        const uint32_t op = word & 0xFFu, base = word >> 8;   // bits 24-31 of the word are 0
+        *op_out = op;
+        return fx_all<B>(h, m, cs, pcs, op, base);
+    }
+}
 #undef ND_FX16
 #undef ND_FX
+#undef ND_HOT8
+#undef ND_HOT
 
 // Cycles from `now` until the DMC's next event, saturated to 32 bits (an idle DMC is never reached within a frame).
 __device__ __forceinline__ uint32_t dmc_distance(uint64_t now, uint64_t event) {
@@ -345,7 +377,7 @@ __device__ __forceinline__ uint32_t run_until_wave(Con& cs, const Mem& m, const 
     uint32_t instructions = 0, fault = 0, pending = 0;
     uint32_t to_event = uni(dots_to_event(cs, m));
     Hot h;
-    hot_load(h, cs);
+    hot_load<B>(h, cs);
     uint64_t dmc_event = uni64(cs.dmc_event);
     uint32_t ecyc = 0;                                     // cycles not yet added to h.cycles
     uint32_t dmc_in = dmc_distance(h.cycles, dmc_event);   // from h.cycles to the DMC event; ecyc <= dmc_in here
@@ -372,7 +404,7 @@ __device__ __forceinline__ uint32_t run_until_wave(Con& cs, const Mem& m, const 
             to_event = uni(dots_to_event(cs, m));
             s0v = uni(cs.s0_valid);
         }
-        uint32_t op = 0, pc0 = h.pc, cyc = 0;
+        uint32_t op = 0, pc0 = 0, cyc = 0;
         if (((nmi | (irq & ~(h.p >> 2))) & 1u) == 0u) {   // no NMI, and no IRQ unless the I flag masks it
             // Fast instructions. With the sprite-0 horizon current and no IRQ asserted (a masked one is taken as soon
             // as CLI, PLP or RTI clears the I flag) this is a burst: they run back to back until one
@@ -415,11 +447,11 @@ __device__ __forceinline__ uint32_t run_until_wave(Con& cs, const Mem& m, const 
         // the generic step: I/O, interrupts, the idle loop, BRK, faults, code outside PRG
         h.cycles += ecyc;
         ecyc = 0;
-        hot_store(h, cs);
+        hot_store<B>(h, cs);
         cs.dmc_event = dmc_event;
         const int32_t start_rel = (int32_t)((int64_t)abs_dot(cs) + pending - (int64_t)cs.log_frame * NES_FRAME_DOTS);
         cyc = cpu_step(cs, m, optab, start_rel, &fault, &op, &pc0);
-        hot_load(h, cs);
+        hot_load<B>(h, cs);
         dmc_event = uni64(cs.dmc_event);
         dmc_in = dmc_distance(h.cycles, dmc_event);
         nmi = uni(cs.nmi_pending);
@@ -432,8 +464,8 @@ __device__ __forceinline__ uint32_t run_until_wave(Con& cs, const Mem& m, const 
             to_event = uni(dots_to_event(cs, m));
             s0v = uni(cs.s0_valid);
         }
-        if (op == 0x4Cu && h.pc == pc0) {
-            hot_store(h, cs);
+        if (op == 0x4Cu && h.pc == pc0 << pc_shift(B)) {
+            hot_store<B>(h, cs);
             cs.dmc_event = dmc_event;
             ppu_advance(cs, m, pending);
             pending = 0;
@@ -452,7 +484,7 @@ __device__ __forceinline__ uint32_t run_until_wave(Con& cs, const Mem& m, const 
         }
     }
     h.cycles += ecyc;
-    hot_store(h, cs);
+    hot_store<B>(h, cs);
     cs.dmc_event = dmc_event;
     cs.instr += instructions;
     if (pending) ppu_advance(cs, m, pending);
