@@ -133,9 +133,12 @@ __device__ __forceinline__ uint32_t prg_wide(const Mem& m, uint32_t idx) {
     return ((ConstU32*)m.cart.prgw)[idx];
 }
 
-// One instruction of opcode descriptor D at pcs = pc << pc_shift(B) (operand bytes lo, hi). Returns its CPU cycles
-// (the caller adds them to the cycle counter and services the DMC), or 0 with nothing changed when the generic step
-// must run it.
+// A fast-path result: the instruction needs the generic step (nothing changed). As a take off the burst counter
+// (cycles << 14) - 1 it stands for 0 cycles.
+constexpr uint32_t kGeneric = 0xFFFFFFFFu;
+
+// One instruction of opcode descriptor D at pcs = pc << pc_shift(B) (operand bytes lo, hi). Returns what it takes
+// off the burst counter, (CPU cycles << 14) - 1, or kGeneric with nothing changed when the generic step must run it.
 template <uint32_t B, uint32_t D>
 __device__ __forceinline__ uint32_t fx(Hot& h, const Mem& m, Con& cs, uint32_t pcs, uint32_t base) {
     constexpr uint32_t PS = pc_shift(B);
@@ -144,7 +147,7 @@ __device__ __forceinline__ uint32_t fx(Hot& h, const Mem& m, Con& cs, uint32_t p
     constexpr bool rd = (D & D_READ) != 0, wr = (D & D_WRITE) != 0, pen = (D & D_PEN) != 0;
     constexpr bool zpage = mode == M_ZP || mode == M_ZPX || mode == M_ZPY;
     if constexpr (grp == G_ILL || grp == G_BRK) {
-        return 0;
+        return kGeneric;
     } else {
         uint32_t cyc = (D >> 4) & 15u;
         const uint32_t lo = base & 0xFFu;   // base: the two operand bytes, lo | hi << 8
@@ -173,11 +176,11 @@ __device__ __forceinline__ uint32_t fx(Hot& h, const Mem& m, Con& cs, uint32_t p
         // read-modify-write outside RAM and any write at $8000+ (a mapper) go to the generic step. Written as
         // chains of single compares: boolean combinations of uniform conditions become lane-mask arithmetic.
         if constexpr (!zpage && rd && wr) {
-            if (ea >= 0x2000u) return 0;
+            if (ea >= 0x2000u) return kGeneric;
         }
         if constexpr (!zpage && wr && !rd) {
             if (ea >= 0x2000u) {
-                if (ea != 0x4016u) return 0;
+                if (ea != 0x4016u) return kGeneric;
             }
         }
         uint32_t opd = lo;
@@ -189,7 +192,7 @@ __device__ __forceinline__ uint32_t fx(Hot& h, const Mem& m, Con& cs, uint32_t p
                 else if (ea >= 0x8000u) opd = prg_wide(m, prg_index<B>(h, m, ea)) & 0xFFu;
                 else if (ea == 0x4016u) opd = port_read(cs);
                 else if ((ea & 0xE007u) == 0x2002u) opd = status_read(cs);
-                else return 0;
+                else return kGeneric;
             }
         }
         constexpr uint32_t len = mode == M_IMP ? 1u : ((mode >= M_ABS && mode <= M_ABY) || mode == M_IND) ? 3u : 2u;
@@ -263,7 +266,7 @@ __device__ __forceinline__ uint32_t fx(Hot& h, const Mem& m, Con& cs, uint32_t p
         } else if constexpr (grp == G_JMP) {
             if constexpr (mode == M_IND) {
                 const uint32_t a1 = (base & 0xFF00u) | ((base + 1u) & 0xFFu);
-                if ((base >= 0x2000u && base < 0x8000u) || (a1 >= 0x2000u && a1 < 0x8000u)) return 0;
+                if ((base >= 0x2000u && base < 0x8000u) || (a1 >= 0x2000u && a1 < 0x8000u)) return kGeneric;
                 const uint32_t l8 = base < 0x2000u ? rd8(m, base & 0x7FFu)
                                                    : (prg_wide(m, prg_index<B>(h, m, base)) & 0xFFu);
                 const uint32_t h8 = a1 < 0x2000u ? rd8(m, a1 & 0x7FFu)
@@ -271,7 +274,7 @@ __device__ __forceinline__ uint32_t fx(Hot& h, const Mem& m, Con& cs, uint32_t p
                 npc = (l8 | (h8 << 8)) << PS;
             } else {
                 npc = base << PS;
-                if (npc == pcs) return 0;   // the idle loop: the generic step runs it, then the fast-forward
+                if (npc == pcs) return kGeneric;   // the idle loop: the generic step runs it, then the fast-forward
             }
         } else if constexpr (grp == G_JSR) {
             const uint32_t ret = (pcs >> PS) + 2u;   // <= $FFFF
@@ -294,14 +297,14 @@ __device__ __forceinline__ uint32_t fx(Hot& h, const Mem& m, Con& cs, uint32_t p
             else port_write(cs, res);
         }
         h.pc = npc;
-        return cyc;   // the caller adds the cycles and services the DMC, as cpu_step does after its cycle count
+        return (cyc << 14) - 1u;   // the caller adds the cycles and services the DMC, as cpu_step does after its count
     }
 }
 
 // (on NROM a hot opcode never reaches the switch over all opcodes: its case merges into the default)
 #define ND_FX(n)                                                      \
     case n:                                                           \
-        if constexpr (B == NES_BOARD_NROM && is_hot(n)) return 0;     \
+        if constexpr (B == NES_BOARD_NROM && is_hot(n)) return kGeneric;     \
         else return fx<B, kOptab.t[n]>(h, m, cs, pcs, base);
 #define ND_HOT(i) \
     case kHotKey + i: return fx<B, kOptab.t[kHotOps[i]]>(h, m, cs, pcs, base);
@@ -318,7 +321,7 @@ __device__ __forceinline__ uint32_t fx_all(Hot& h, const Mem& m, Con& cs, uint32
         ND_FX16(0x00) ND_FX16(0x10) ND_FX16(0x20) ND_FX16(0x30) ND_FX16(0x40) ND_FX16(0x50) ND_FX16(0x60)
         ND_FX16(0x70) ND_FX16(0x80) ND_FX16(0x90) ND_FX16(0xA0) ND_FX16(0xB0) ND_FX16(0xC0) ND_FX16(0xD0)
         ND_FX16(0xE0) ND_FX16(0xF0)
-        default: return 0;
+        default: return kGeneric;
     }
 }
 
@@ -331,7 +334,8 @@ __device__ __forceinline__ uint32_t fx_hot(Hot& h, const Mem& m, Con& cs, uint32
     }
 }
 
-// The fast path for the instruction at h.pc: its cycles, or 0 (nothing changed) for the generic step.
+// The fast path for the instruction at h.pc: (its cycles << 14) - 1, or kGeneric (nothing changed) for the generic
+// step.
 template <uint32_t B>
 __device__ __forceinline__ uint32_t fast_step(Hot& h, const Mem& m, Con& cs, uint32_t* op_out) {
     const uint32_t pcs = h.pc;
@@ -347,7 +351,7 @@ __device__ __forceinline__ uint32_t fast_step(Hot& h, const Mem& m, Con& cs, uin
     } else {
         // code in PRG ($8000+) and the 3-byte window inside one 8 KB page: pc >= $8000 and (pc & $1FFF) <= $1FFD,
         // as one compare ((pc + 2) & $9FFF keeps bit 15 and the page offset of the window's last byte)
-        if (((pcs + 2u) & 0x9FFFu) < 0x8002u) return 0;
+        if (((pcs + 2u) & 0x9FFFu) < 0x8002u) return kGeneric;
         const uint32_t word = prg_wide(m, prg_index<B>(h, m, pcs));
         const uint32_t op = word & 0xFFu, base = word >> 8;   // bits 24-31 of the word are 0
         *op_out = op;
@@ -411,19 +415,24 @@ __device__ __forceinline__ uint32_t run_until_wave(Con& cs, const Mem& m, const 
             // needs the generic step (cyc = 0, nothing changed) or the cycles used reach `room`, the nearest of the
             // DMC event, the PPU event horizon (3 dots a cycle) and the instruction budget (every instruction takes
             // at least 2 cycles, so a burst never passes it). Otherwise one instruction runs and the horizon is
-            // refreshed after it. lm1 = room - 1, and `cyc - 1 >= lm1` (unsigned) is "cyc == 0 or cyc >= room".
+            // refreshed after it. lm1 = room - 1 (< 2^15: the horizon is less than a frame, 89342 dots, away).
+            // One register counts both: v = lm1 << 14 | instructions run (< 2^14: half the room at most), and each
+            // instruction takes (cyc << 14) - 1 off it (a constant for most handlers). v < take exactly when
+            // cyc > lm1, "cyc == 0 or cyc >= room" (kGeneric stands for a cyc of 0).
             uint32_t lm1 = 0;
             if ((s0v & ~irq) & 1u)
                 lm1 = uni(max(min(min(dmc_in - ecyc, (to_event - pending + 2u) / 3u), 2u * (budget - instructions)),
                               1u) - 1u);
             const uint32_t lm1_0 = lm1;
-            uint32_t n = 0;
+            uint32_t v = lm1 << 14, take;
             for (;;) {
-                cyc = fast_step<B>(h, m, cs, &op);
-                ++n;
-                if (cyc - 1u >= lm1) break;
-                lm1 -= cyc;
+                take = fast_step<B>(h, m, cs, &op);
+                if (v < take) break;
+                v -= take;
             }
+            cyc = (take + 1u) >> 14;               // 0 for kGeneric
+            lm1 = v >> 14;
+            const uint32_t n = (v & 0x3FFFu) + 1u;
             const uint32_t used = lm1_0 - lm1 + cyc;   // cycles of the n instructions
             ecyc += used;
             if (cyc != 0u) {
