@@ -982,6 +982,34 @@ void decision_phases(const Env& env, const GameK& g, const Outs& o, int e0, int 
     restart_phases(env, g, o, e0, e1, st);
 }
 
+// NROM fetch-table entry of the instruction at CPU address a (opcode op, next bytes b1 b2): the dispatch key (a hot
+// key for the opcodes of kHotOps, except a branch whose target is on another page) and the decoded operand word the
+// handlers take (wave_dev.h fx): the operand byte of a two-byte instruction, a branch's target times 8 (pc past
+// $FFFF not wrapped, as the interpreter counts it), JMP's and JSR's target times 8, else b1 | b2 << 8.
+void fetch_entry(uint32_t* e, uint32_t a, uint32_t op, uint32_t b1, uint32_t b2) {
+    const uint32_t d = kOptab.t[op], mode = d & 15u, grp = (d >> 8) & 15u;
+    uint32_t base = b1 | (b2 << 8);
+    bool cross = false;
+    if (grp == G_ILL || grp == G_BRK) {
+        e[0] = op;   // the generic step runs (and faults on) it
+        e[1] = base;
+        return;
+    }
+    if (mode == M_IMM || mode == M_ZP || mode == M_ZPX || mode == M_ZPY || mode == M_IZX || mode == M_IZY) {
+        base = b1;
+    } else if (mode == M_REL) {
+        const uint32_t tgt = a + 2u + (uint32_t)(int32_t)(int8_t)b1;
+        cross = ((a + 2u) ^ tgt) & 0xFF00u;
+        base = tgt << 3;
+    } else if (op == 0x4Cu || op == 0x20u) {
+        base <<= 3;
+    }
+    uint32_t hot = 0;
+    while (hot < 32u && kHotOps[hot] != op) ++hot;
+    e[0] = hot < 32u && !cross ? kHotKey + hot : op;
+    e[1] = base;
+}
+
 void boot_game(Env& env, GameH& gh, const uint8_t* pads, size_t npads) {
     GameK& g = gh.k;
     hipLaunchKernelGGL(k_power_on, dim3(1), dim3(1), 0, 0, &g.recs[g.n], g.cart);
@@ -1118,13 +1146,8 @@ void* rlenv_create(int ngames, const int* game_ids, const uint8_t* const* roms, 
                 std::vector<uint32_t> f(2u * kFetchWords, 0u);
                 for (uint32_t a = 0; a < kFetchWords; ++a) f[2u * a] = 0x02u;
                 const size_t mask = (p.prg.size() - 1u) & 0x7FFFu;
-                for (uint32_t a = 0x8000u; a <= 0xFFFDu; ++a) {
-                    const uint32_t op = p.prg[a & mask];
-                    uint32_t hot = 0;
-                    while (hot < 32u && kHotOps[hot] != op) ++hot;
-                    f[2u * a] = hot < 32u ? kHotKey + hot : op;
-                    f[2u * a + 1u] = p.prg[(a + 1u) & mask] | ((uint32_t)p.prg[(a + 2u) & mask] << 8);
-                }
+                for (uint32_t a = 0x8000u; a <= 0xFFFDu; ++a)
+                    fetch_entry(&f[2u * a], a, p.prg[a & mask], p.prg[(a + 1u) & mask], p.prg[(a + 2u) & mask]);
                 fetchw = static_cast<uint32_t*>(env->mem.alloc(f.size() * 4));
                 env->mem.upload(fetchw, f.data(), f.size() * 4);
             }

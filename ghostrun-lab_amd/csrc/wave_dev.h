@@ -18,7 +18,6 @@
 namespace nd {
 
 typedef __attribute__((address_space(4))) const uint32_t ConstU32;
-typedef __attribute__((address_space(4))) const uint64_t ConstU64;
 typedef __attribute__((address_space(4))) const uint8_t ConstU8;
 
 // Registers the fast loop keeps live: the CPU registers, the cycle counter and the PRG page offsets. Everything
@@ -139,9 +138,13 @@ constexpr uint32_t kGeneric = 0xFFFFFFFFu;
 
 // One instruction of opcode descriptor D at pcs = pc << pc_shift(B) (operand bytes lo, hi). Returns what it takes
 // off the burst counter, (CPU cycles << 14) - 1, or kGeneric with nothing changed when the generic step must run it.
-template <uint32_t B, uint32_t D>
+// On NROM the operand word comes decoded from the fetch table (kFetchWords): the operand byte of a two-byte
+// instruction, a branch's target times 8, JMP's and JSR's target times 8, else lo | hi << 8. HOT: a hot key (a branch
+// that stays on its page). On the other boards base is the two bytes after the opcode.
+template <uint32_t B, uint32_t D, bool HOT = false>
 __device__ __forceinline__ uint32_t fx(Hot& h, const Mem& m, Con& cs, uint32_t pcs, uint32_t base) {
     constexpr uint32_t PS = pc_shift(B);
+    constexpr bool pre = B == NES_BOARD_NROM;
     constexpr uint32_t mode = D & 15u, grp = (D >> 8) & 15u, sub = (D >> 12) & 15u;
     constexpr uint32_t src = (D >> 16) & 7u, dst = (D >> 19) & 7u;
     constexpr bool rd = (D & D_READ) != 0, wr = (D & D_WRITE) != 0, pen = (D & D_PEN) != 0;
@@ -150,7 +153,9 @@ __device__ __forceinline__ uint32_t fx(Hot& h, const Mem& m, Con& cs, uint32_t p
         return kGeneric;
     } else {
         uint32_t cyc = (D >> 4) & 15u;
-        const uint32_t lo = base & 0xFFu;   // base: the two operand bytes, lo | hi << 8
+        constexpr bool two = mode == M_IMM || mode == M_ZP || mode == M_ZPX || mode == M_ZPY || mode == M_IZX ||
+                             mode == M_IZY;
+        const uint32_t lo = (pre && two) ? base : (base & 0xFFu);
         uint32_t ea = 0;
         if constexpr (mode == M_ZP) {
             ea = lo;
@@ -185,7 +190,9 @@ __device__ __forceinline__ uint32_t fx(Hot& h, const Mem& m, Con& cs, uint32_t p
         }
         uint32_t opd = lo;
         if constexpr (rd) {
-            if constexpr (zpage || wr) {
+            if constexpr (pre && mode == M_ZP) {
+                opd = rd8(m, ea);   // the fetch table's operand byte: < $100
+            } else if constexpr (zpage || wr) {
                 opd = rd8(m, ea & 0x7FFu);
             } else {
                 if (ea < 0x2000u) opd = rd8(m, ea & 0x7FFu);
@@ -244,8 +251,9 @@ __device__ __forceinline__ uint32_t fx(Hot& h, const Mem& m, Con& cs, uint32_t p
             else if constexpr (bit == 1u) set = h.zv == 0;
             else set = ((h.p >> bit) & 1u) != 0;
             if (set == ((sub & 8u) != 0)) {
-                const uint32_t tgt = npc + ((uint32_t)(int32_t)(int8_t)lo << PS);   // wrapped when stored
-                cyc += ((npc ^ tgt) & (0xFF00u << PS)) ? 2u : 1u;
+                const uint32_t tgt = pre ? base : npc + ((uint32_t)(int32_t)(int8_t)lo << PS);   // wrapped when stored
+                if constexpr (HOT) cyc += 1u;
+                else cyc += ((npc ^ tgt) & (0xFF00u << PS)) ? 2u : 1u;
                 npc = tgt;
             }
         } else if constexpr (grp == G_FLAG) {
@@ -273,14 +281,14 @@ __device__ __forceinline__ uint32_t fx(Hot& h, const Mem& m, Con& cs, uint32_t p
                                                  : (prg_wide(m, prg_index<B>(h, m, a1)) & 0xFFu);
                 npc = (l8 | (h8 << 8)) << PS;
             } else {
-                npc = base << PS;
+                npc = pre ? base : base << PS;
                 if (npc == pcs) return kGeneric;   // the idle loop: the generic step runs it, then the fast-forward
             }
         } else if constexpr (grp == G_JSR) {
             const uint32_t ret = (pcs >> PS) + 2u;   // <= $FFFF
             hpush(h, m, ret >> 8);
             hpush(h, m, ret & 0xFFu);
-            npc = base << PS;
+            npc = pre ? base : base << PS;
         } else if constexpr (grp == G_RTS) {
             const uint32_t l8 = hpull(h, m), h8 = hpull(h, m);
             npc = (((h8 << 8) | l8) + 1u) << PS;
@@ -292,7 +300,8 @@ __device__ __forceinline__ uint32_t fx(Hot& h, const Mem& m, Con& cs, uint32_t p
             npc = ((h8 << 8) | l8) << PS;
         }
         if constexpr (wr) {
-            if constexpr (zpage || rd) m.ram[ea & 0x7FFu] = (uint8_t)res;
+            if constexpr (pre && mode == M_ZP) m.ram[ea] = (uint8_t)res;
+            else if constexpr (zpage || rd) m.ram[ea & 0x7FFu] = (uint8_t)res;
             else if (ea < 0x2000u) m.ram[ea & 0x7FFu] = (uint8_t)res;
             else port_write(cs, res);
         }
@@ -301,13 +310,16 @@ __device__ __forceinline__ uint32_t fx(Hot& h, const Mem& m, Con& cs, uint32_t p
     }
 }
 
-// (on NROM a hot opcode never reaches the switch over all opcodes: its case merges into the default)
-#define ND_FX(n)                                                      \
-    case n:                                                           \
-        if constexpr (B == NES_BOARD_NROM && is_hot(n)) return kGeneric;     \
-        else return fx<B, kOptab.t[n]>(h, m, cs, pcs, base);
+// (on NROM a hot opcode other than a branch never reaches the switch over all opcodes: its case merges into the
+// default; a branch to another page comes here with its opcode)
+#define ND_FX(n)                                                                              \
+    case n:                                                                                   \
+        if constexpr (B == NES_BOARD_NROM && is_hot(n) && (kOptab.t[n] & 15u) != M_REL)      \
+            return kGeneric;                                                                  \
+        else                                                                                  \
+            return fx<B, kOptab.t[n]>(h, m, cs, pcs, base);
 #define ND_HOT(i) \
-    case kHotKey + i: return fx<B, kOptab.t[kHotOps[i]]>(h, m, cs, pcs, base);
+    case kHotKey + i: return fx<B, kOptab.t[kHotOps[i]], true>(h, m, cs, pcs, base);
 #define ND_HOT8(i) ND_HOT(i) ND_HOT(i + 1) ND_HOT(i + 2) ND_HOT(i + 3) ND_HOT(i + 4) ND_HOT(i + 5) ND_HOT(i + 6) ND_HOT(i + 7)
 #define ND_FX16(h)                                                                                                    \
     ND_FX(h + 0x0) ND_FX(h + 0x1) ND_FX(h + 0x2) ND_FX(h + 0x3) ND_FX(h + 0x4) ND_FX(h + 0x5) ND_FX(h + 0x6)          \
@@ -343,11 +355,15 @@ __device__ __forceinline__ uint32_t fast_step(Hot& h, const Mem& m, Con& cs, uin
         // pc <= $1007E (a branch just past $FFFF); $02 outside PRG. The entry is the key (the opcode, or a hot key
         // $100 + i for kHotOps[i]) and the operand word as two dwords (no field extraction), at byte offset
         // pcs = pc * 8: a scalar load with an SGPR offset.
-        const uint64_t w = *(const ConstU64*)((ConstU8*)m.cart.fetchw + pcs);
-        const uint32_t op = (uint32_t)w, base = (uint32_t)(w >> 32);
+        // (two 32-bit loads, which the compiler pairs into one 64-bit load: read as the halves of a 64-bit value,
+        // base's compares would become 64-bit ones, which the scalar unit has only for equality)
+        ConstU32* e = (ConstU32*)((ConstU8*)m.cart.fetchw + pcs);
+        const uint32_t op = e[0], base = e[1];
         *op_out = op;
-        if (op >= kHotKey) return fx_hot<B>(h, m, cs, pcs, op, base);
-        return fx_all<B>(h, m, cs, pcs, op, base);
+        if (__builtin_expect(op >= kHotKey, 1)) return fx_hot<B>(h, m, cs, pcs, op, base);
+        // (read back as an opaque scalar: with the range op < $100 known the compiler narrows the switch to 8 bits
+        // and widens it again with two masks)
+        return fx_all<B>(h, m, cs, pcs, uni(op), base);
     } else {
         // code in PRG ($8000+) and the 3-byte window inside one 8 KB page: pc >= $8000 and (pc & $1FFF) <= $1FFD,
         // as one compare ((pc + 2) & $9FFF keeps bit 15 and the page offset of the window's last byte)
