@@ -23,13 +23,14 @@ typedef __attribute__((address_space(4))) const uint8_t ConstU8;
 // Registers the fast loop keeps live: the CPU registers, the cycle counter and the PRG page offsets. Everything
 // else about the console (PPU, controller, DMC, mapper) stays in the console state in LDS and only the generic
 // step, the PPU settle and the idle fast-forward touch it, so the loop's live set is small enough to stay in SGPRs.
-// N and Z are kept lazily, as the values they are taken from: N = bit 7 of nv, Z = (zv == 0); the N and Z bits of
-// p are stale in between and are rebuilt when p is stored or pushed. pc is held shifted left by pc_shift(board):
-// on NROM times 8, the byte offset of its fetch-table entry, so the fetch needs no address arithmetic. It may run
-// one past $FFFF after the last instruction of the address space and is wrapped when stored (the fast path sends
-// such a pc to the generic step).
+// N and Z are kept lazily in one value nz: N = (nz >= $80), Z = (low byte of nz == 0). An instruction that sets both
+// from a result r stores r itself; BIT, whose N comes from the operand, adds the operand's bit 7 as bit 8. The N and
+// Z bits of p are stale in between and are rebuilt when p is stored or pushed. pc is held shifted left by
+// pc_shift(board): on NROM times 8, the byte offset of its fetch-table entry, so the fetch needs no address
+// arithmetic. It may run one past $FFFF after the last instruction of the address space and is wrapped when stored
+// (the fast path sends such a pc to the generic step).
 struct Hot {
-    uint32_t pc, a, x, y, sp, p, nv, zv;
+    uint32_t pc, a, x, y, sp, p, nz;
     uint64_t cycles;
     uint32_t prg0, prg1, prg2, prg3;
 };
@@ -42,16 +43,20 @@ __device__ __forceinline__ uint64_t uni64(uint64_t v) {
     return (uint64_t)uni((uint32_t)v) | ((uint64_t)uni((uint32_t)(v >> 32)) << 32);
 }
 
-// p with N and Z rebuilt from the lazy values.
+// The lazy N and Z of a status byte p: bit 8 = N, and a low byte that is 0 exactly when Z is set.
+__device__ __forceinline__ uint32_t nz_of_p(uint32_t p) {
+    return ((p & FL_N) << 1) | ((p & FL_Z) ? 0u : 1u);
+}
+
+// p with N and Z rebuilt from the lazy value.
 __device__ __forceinline__ uint32_t hflags(const Hot& h) {
-    return (h.p & ~(FL_N | FL_Z)) | (h.nv & FL_N) | (h.zv ? 0u : FL_Z);
+    return (h.p & ~(FL_N | FL_Z)) | (h.nz >= 0x80u ? FL_N : 0u) | ((h.nz & 0xFFu) ? 0u : FL_Z);
 }
 
 template <uint32_t B>
 __device__ __forceinline__ void hot_load(Hot& h, const Con& c) {
     h.pc = uni(c.pc) << pc_shift(B); h.a = uni(c.a); h.x = uni(c.x); h.y = uni(c.y); h.sp = uni(c.sp); h.p = uni(c.p);
-    h.nv = h.p;
-    h.zv = ~h.p & FL_Z;
+    h.nz = nz_of_p(h.p);
     h.cycles = uni64(c.cycles);
     h.prg0 = uni(c.prg0); h.prg1 = uni(c.prg1); h.prg2 = uni(c.prg2); h.prg3 = uni(c.prg3);
 }
@@ -72,8 +77,7 @@ __device__ __forceinline__ void hset(Hot& h, uint32_t code, uint32_t v) {
     else if (code == R_SP) h.sp = v;
 }
 __device__ __forceinline__ void hnz(Hot& h, uint32_t v) {   // v < 256
-    h.nv = v;
-    h.zv = v;
+    h.nz = v;
 }
 // A CPU RAM byte (LDS) as a scalar: the value is wave-uniform, and in an SGPR the code that uses it stays on the
 // scalar unit (SCC branches instead of VALU compares and VCC branches).
@@ -231,8 +235,7 @@ __device__ __forceinline__ uint32_t fx(Hot& h, const Mem& m, Con& cs, uint32_t p
                 hnz(h, (r - opd) & 0xFFu);
             } else {
                 h.p = (h.p & ~FL_V) | (opd & FL_V);
-                h.nv = opd;
-                h.zv = h.a & opd;
+                h.nz = (h.a & opd) | ((opd & 0x80u) << 1);   // N from the operand, Z from A & operand
             }
         } else if constexpr (grp == G_SHIFT) {
             const uint32_t in = hget(h, src, opd), cin = h.p & FL_C;
@@ -247,8 +250,8 @@ __device__ __forceinline__ uint32_t fx(Hot& h, const Mem& m, Con& cs, uint32_t p
         } else if constexpr (grp == G_BR) {
             constexpr uint32_t bit = sub & 7u;
             bool set;
-            if constexpr (bit == 7u) set = (h.nv & FL_N) != 0;
-            else if constexpr (bit == 1u) set = h.zv == 0;
+            if constexpr (bit == 7u) set = h.nz >= 0x80u;
+            else if constexpr (bit == 1u) set = (h.nz & 0xFFu) == 0u;
             else set = ((h.p >> bit) & 1u) != 0;
             if (set == ((sub & 8u) != 0)) {
                 const uint32_t tgt = pre ? base : npc + ((uint32_t)(int32_t)(int8_t)lo << PS);   // wrapped when stored
@@ -268,8 +271,7 @@ __device__ __forceinline__ uint32_t fx(Hot& h, const Mem& m, Con& cs, uint32_t p
                 hnz(h, v);
             } else {
                 h.p = (v & ~FL_B) | FL_U;
-                h.nv = h.p;
-                h.zv = ~h.p & FL_Z;
+                h.nz = nz_of_p(h.p);
             }
         } else if constexpr (grp == G_JMP) {
             if constexpr (mode == M_IND) {
@@ -294,8 +296,7 @@ __device__ __forceinline__ uint32_t fx(Hot& h, const Mem& m, Con& cs, uint32_t p
             npc = (((h8 << 8) | l8) + 1u) << PS;
         } else if constexpr (grp == G_RTI) {
             h.p = (hpull(h, m) & ~FL_B) | FL_U;
-            h.nv = h.p;
-            h.zv = ~h.p & FL_Z;
+            h.nz = nz_of_p(h.p);
             const uint32_t l8 = hpull(h, m), h8 = hpull(h, m);
             npc = ((h8 << 8) | l8) << PS;
         }
