@@ -306,8 +306,8 @@ struct RenderArgs {
 // (rl/csrc/nes_machine.cuh:133-155). nt/oam: the console's nametables and OAM as of the frame's vblank (LDS);
 // pal: 32 bytes of LDS for the replayed palette; ev_s: the log's events, copied to LDS.
 __device__ __forceinline__ void render_wave(const NesRec* rec, uint32_t log_n, const uint8_t* nt_s, const uint8_t* oam_s,
-                                            uint8_t* pal_s, const uint32_t* ev_s, const Cart& cart, uint8_t* obs,
-                                            uint8_t* emph, int lane) {
+                                            uint8_t* pal_s, const uint32_t* ev_s, uint32_t* spr_s, uint32_t* slot_s,
+                                            const Cart& cart, uint8_t* obs, uint8_t* emph, int lane) {
     Replay s;   // wave-uniform: every lane replays the same log (and stores the same palette bytes)
     rp_begin(s, rec->log, log_n, pal_s, ev_s);
     __syncthreads();
@@ -319,7 +319,7 @@ __device__ __forceinline__ void render_wave(const NesRec* rec, uint32_t log_n, c
             const bool bg_on = (mask & 0x08u) != 0, sp_on = (mask & 0x10u) != 0;
             const int h = (ctrl & 0x20u) ? 16 : 8;
             const int row_me = l - (int)my_sy - 1;
-            uint64_t sel = __ballot(sp_on && row_me >= 0 && row_me < h);
+            const uint64_t sel = __ballot(sp_on && row_me >= 0 && row_me < h);
             // background, 4 pixels: the lane's pixels x0..x0+3 lie in tile slots A = (x0 + fx) / 8 and A + 1; both
             // are fetched by every lane (no per-lane branches) and each pixel selects its own
             uint32_t bgv[4] = {0, 0, 0, 0}, bga[4] = {0, 0, 0, 0};
@@ -349,23 +349,39 @@ __device__ __forceinline__ void render_wave(const NesRec* rec, uint32_t log_n, c
                     bga[q] = k ? ps[1] : ps[0];
                 }
             }
-            // sprites: the first 8 in OAM order that cover this line; per pixel the first opaque one wins
+            // sprites: the first 8 in OAM order that cover this line; per pixel the first opaque one wins. One pass
+            // for all of them: lane j draws pixel j & 7 of the line's sprite j >> 3 into the line buffer spr_s with
+            // an LDS max over (7 - sprite rank) << 5 | behind << 4 | palette << 2 | value, so the lowest-ranked
+            // opaque sprite wins each pixel; slot_s maps rank -> OAM index.
             uint32_t spv[4] = {0, 0, 0, 0}, spa[4] = {0, 0, 0, 0}, spb[4] = {0, 0, 0, 0};
-            for (int n = 0; n < 8 && sel != 0; ++n) {
-                const uint32_t i = (uint32_t)__builtin_ctzll(sel);
-                sel &= sel - 1;
-                const uint32_t sy = oam_s[4 * i], tile = oam_s[4 * i + 1], attr = oam_s[4 * i + 2], sx = oam_s[4 * i + 3];
-                const uint32_t pa = sprite_row_addr(ctrl, tile, attr, (uint32_t)(l - (int)sy - 1));
-                const uint32_t plo = chr_byte_pk(m, s.chr_lo, s.chr_hi, pa), phi = chr_byte_pk(m, s.chr_lo, s.chr_hi, pa + 8u);
-                const uint32_t flip = (attr & 0x40u) ? 0u : 7u, pal_hi = attr & 3u, behind = (attr >> 5) & 1u;
+            if (sel != 0) {
+                const uint32_t below = __builtin_amdgcn_mbcnt_hi((uint32_t)(sel >> 32),
+                                                                 __builtin_amdgcn_mbcnt_lo((uint32_t)sel, 0u));
+                if (((sel >> lane) & 1u) && below < 8u) slot_s[below] = (uint32_t)lane;
+                const uint32_t count = min((uint32_t)__builtin_popcountll(sel), 8u);
+                __syncthreads();
+                const uint32_t k = (uint32_t)lane >> 3, px = (uint32_t)lane & 7u;
+                if (k < count) {
+                    const uint32_t i = slot_s[k];
+                    const uint32_t e = reinterpret_cast<const uint32_t*>(oam_s)[i];
+                    const uint32_t sy = e & 0xFFu, tile = (e >> 8) & 0xFFu, attr = (e >> 16) & 0xFFu, sx = e >> 24;
+                    const uint32_t pa = sprite_row_addr(ctrl, tile, attr, (uint32_t)(l - (int)sy - 1));
+                    const uint32_t plo = chr_byte_pk(m, s.chr_lo, s.chr_hi, pa);
+                    const uint32_t phi = chr_byte_pk(m, s.chr_lo, s.chr_hi, pa + 8u);
+                    const uint32_t b = (attr & 0x40u) ? px : 7u - px;
+                    const uint32_t v = ((plo >> b) & 1u) | (((phi >> b) & 1u) << 1);
+                    const uint32_t x = sx + px;
+                    if (v != 0u && x < 256u && !(x < 8u && !(mask & 0x04u)))
+                        atomicMax(&spr_s[x], ((7u - k) << 5) | (((attr >> 5) & 1u) << 4) | ((attr & 3u) << 2) | v);
+                }
+                __syncthreads();
+                const uint4 got = reinterpret_cast<uint4*>(spr_s)[lane];
+                reinterpret_cast<uint4*>(spr_s)[lane] = make_uint4(0u, 0u, 0u, 0u);
+                const uint32_t g[4] = {got.x, got.y, got.z, got.w};
                 for (int q = 0; q < 4; ++q) {
-                    const uint32_t x = x0 + (uint32_t)q, col = x - sx;
-                    const uint32_t b = (flip ^ col) & 7u;   // col, or 7 - col when not flipped
-                    const uint32_t p = ((plo >> b) & 1u) | (((phi >> b) & 1u) << 1);
-                    const bool take = spv[q] == 0u && col < 8u && !(x < 8u && !(mask & 0x04u)) && p != 0u;
-                    spv[q] = take ? p : spv[q];
-                    spa[q] = take ? pal_hi : spa[q];
-                    spb[q] = take ? behind : spb[q];
+                    spv[q] = g[q] & 3u;
+                    spa[q] = (g[q] >> 2) & 3u;
+                    spb[q] = (g[q] >> 4) & 1u;
                 }
             }
             uint32_t word = 0;
@@ -392,6 +408,8 @@ __global__ __launch_bounds__(64) void k_render(RenderArgs a) {
     __shared__ __align__(16) uint8_t oam_s[256];
     __shared__ __align__(16) uint8_t pal_s[32];
     __shared__ __align__(16) uint32_t ev_s[2 * NES_LOG_EVENTS];
+    __shared__ __align__(16) uint32_t spr_s[256];   // the line's sprite pixels (0 = none)
+    __shared__ uint32_t slot_s[8];
     const int count = slot_count(a.g, a.use_list, a.e0, a.e1);
     const int k = (int)blockIdx.x;
     if (k >= count) return;
@@ -405,10 +423,11 @@ __global__ __launch_bounds__(64) void k_render(RenderArgs a) {
     reinterpret_cast<uint32_t*>(oam_s)[lane] = reinterpret_cast<const uint32_t*>(rec->oam)[lane];
     const uint32_t log_n = rec->log_n, ev_words = 2u * (log_n < NES_LOG_EVENTS ? log_n : NES_LOG_EVENTS);
     for (uint32_t w = (uint32_t)lane; w < ev_words; w += 64u) ev_s[w] = rec->log[NES_LOG_HDR_WORDS + w];
+    reinterpret_cast<uint4*>(spr_s)[lane] = make_uint4(0u, 0u, 0u, 0u);
     __syncthreads();
     uint8_t* obs = a.o.obs + ((size_t)ge * RLE_FRAMES + a.f) * RLE_OBS_PIXELS;
     uint8_t* emph = a.o.emph + ((size_t)ge * RLE_FRAMES + a.f) * RLE_OBS_H;
-    render_wave(rec, log_n, nt_s, oam_s, pal_s, ev_s, a.g.cart, obs, emph, lane);
+    render_wave(rec, log_n, nt_s, oam_s, pal_s, ev_s, spr_s, slot_s, a.g.cart, obs, emph, lane);
 }
 
 // ----------------------------------------------------------------------------------------- finish
