@@ -300,6 +300,13 @@ struct RenderArgs {
     int f, use_list, restart_pass, e0, e1;
 };
 
+// Bit i of byte b at bit 4i (the 8 bits of a pattern byte spread to the low bits of 8 nibbles).
+__device__ __forceinline__ uint32_t nibbles8(uint32_t b) {
+    b = (b | (b << 12)) & 0x000F000Fu;
+    b = (b | (b << 6)) & 0x03030303u;
+    return (b | (b << 3)) & 0x11111111u;
+}
+
 // The picture of the frame a console has logged, drawn by one wavefront: the frame log is replayed line by line
 // (wave-uniform state), each lane composes 4 pixels of the 256-pixel line, the sprites of a line are picked with
 // one ballot over the 64 OAM entries, and lines 8..231, columns 8..247 go out as one 240-byte row store each
@@ -307,7 +314,7 @@ struct RenderArgs {
 // pal: 32 bytes of LDS for the replayed palette; ev_s: the log's events, copied to LDS.
 __device__ __forceinline__ void render_wave(const NesRec* rec, uint32_t log_n, const uint8_t* nt_s, const uint8_t* oam_s,
                                             uint8_t* pal_s, const uint32_t* ev_s, uint32_t* spr_s, uint32_t* slot_s,
-                                            const Cart& cart, uint8_t* obs, uint8_t* emph, int lane) {
+                                            uint32_t* tile_s, const Cart& cart, uint8_t* obs, uint8_t* emph, int lane) {
     Replay s;   // wave-uniform: every lane replays the same log (and stores the same palette bytes)
     rp_begin(s, rec->log, log_n, pal_s, ev_s);
     __syncthreads();
@@ -320,33 +327,35 @@ __device__ __forceinline__ void render_wave(const NesRec* rec, uint32_t log_n, c
             const int h = (ctrl & 0x20u) ? 16 : 8;
             const int row_me = l - (int)my_sy - 1;
             const uint64_t sel = __ballot(sp_on && row_me >= 0 && row_me < h);
-            // background, 4 pixels: the lane's pixels x0..x0+3 lie in tile slots A = (x0 + fx) / 8 and A + 1; both
-            // are fetched by every lane (no per-lane branches) and each pixel selects its own
+            // background: lane t < 34 fetches tile slot t of the line (its nametable tile, attribute and two pattern
+            // bytes) into tile_s[t] as 8 nibbles palette << 2 | value, leftmost pixel in the top nibble; then each
+            // lane takes its pixels x0..x0+3, which lie in slots A = (x0 + fx) / 8 and A + 1, out of the two words
             uint32_t bgv[4] = {0, 0, 0, 0}, bga[4] = {0, 0, 0, 0};
             const uint32_t x0 = 4u * (uint32_t)lane;
             if (bg_on) {
                 const uint32_t cy = (s.v >> 5) & 31u, fy = (s.v >> 12) & 7u, ntv = (s.v >> 11) & 1u;
-                const uint32_t pos0 = x0 + s.fx, slot_a = pos0 >> 3;
-                uint32_t lo[2], hi[2], ps[2];
-                for (int k = 0; k < 2; ++k) {
-                    const uint32_t c = (s.v & 31u) + slot_a + (uint32_t)k;   // < 64; the slot-33 fetch is unused
+                if (lane < 34) {
+                    const uint32_t c = (s.v & 31u) + (uint32_t)lane;   // < 64; slot 33 is read, never used
                     const uint32_t wrap = c >= 32u ? 1u : 0u;
                     const uint32_t cx = c - 32u * wrap, nth = ((s.v >> 10) & 1u) ^ wrap;
                     const uint32_t base = 0x2000u | ((nth | (ntv << 1)) << 10);
                     const uint32_t tile = nt_s[nt_index(s.nt_map, base | (cy << 5) | (cx & 31u))];
                     const uint32_t at = nt_s[nt_index(s.nt_map, base | 0x3C0u | ((cy >> 2) << 3) | ((cx & 31u) >> 2))];
-                    ps[k] = (at >> (((cy & 2u) << 1) | (cx & 2u))) & 3u;
+                    const uint32_t ps = (at >> (((cy & 2u) << 1) | (cx & 2u))) & 3u;
                     const uint32_t pa = ((ctrl & 0x10u) << 8) + tile * 16u + fy;
-                    lo[k] = chr_byte_pk(m, s.chr_lo, s.chr_hi, pa);
-                    hi[k] = chr_byte_pk(m, s.chr_lo, s.chr_hi, pa + 8u);
+                    const uint32_t lo = chr_byte_pk(m, s.chr_lo, s.chr_hi, pa);
+                    const uint32_t hi = chr_byte_pk(m, s.chr_lo, s.chr_hi, pa + 8u);
+                    tile_s[lane] = nibbles8(lo) | (nibbles8(hi) << 1) | (ps * 0x44444444u);
                 }
+                __syncthreads();
+                const uint32_t pos0 = x0 + s.fx, slot_a = pos0 >> 3;
+                const uint64_t w = (((uint64_t)tile_s[slot_a] << 32) | tile_s[slot_a + 1u]) << (4u * (pos0 & 7u));
+                const uint32_t top = (uint32_t)(w >> 32);   // the lane's 4 pixels in the top 16 bits
                 for (int q = 0; q < 4; ++q) {
-                    const uint32_t pos = pos0 + (uint32_t)q, k = (pos >> 3) - slot_a, b = 7u - (pos & 7u);
-                    const uint32_t plo = k ? lo[1] : lo[0], phi = k ? hi[1] : hi[0];
-                    const uint32_t v = ((plo >> b) & 1u) | (((phi >> b) & 1u) << 1);
+                    const uint32_t nib = (top >> (28u - 4u * (uint32_t)q)) & 15u;
                     const bool clip = x0 + (uint32_t)q < 8u && !(mask & 0x02u);
-                    bgv[q] = clip ? 0u : v;
-                    bga[q] = k ? ps[1] : ps[0];
+                    bgv[q] = clip ? 0u : nib & 3u;
+                    bga[q] = nib >> 2;
                 }
             }
             // sprites: the first 8 in OAM order that cover this line; per pixel the first opaque one wins. One pass
@@ -410,6 +419,7 @@ __global__ __launch_bounds__(64) void k_render(RenderArgs a) {
     __shared__ __align__(16) uint32_t ev_s[2 * NES_LOG_EVENTS];
     __shared__ __align__(16) uint32_t spr_s[256];   // the line's sprite pixels (0 = none)
     __shared__ uint32_t slot_s[8];
+    __shared__ uint32_t tile_s[34];                 // the line's background tile slots
     const int count = slot_count(a.g, a.use_list, a.e0, a.e1);
     const int k = (int)blockIdx.x;
     if (k >= count) return;
@@ -427,7 +437,7 @@ __global__ __launch_bounds__(64) void k_render(RenderArgs a) {
     __syncthreads();
     uint8_t* obs = a.o.obs + ((size_t)ge * RLE_FRAMES + a.f) * RLE_OBS_PIXELS;
     uint8_t* emph = a.o.emph + ((size_t)ge * RLE_FRAMES + a.f) * RLE_OBS_H;
-    render_wave(rec, log_n, nt_s, oam_s, pal_s, ev_s, spr_s, slot_s, a.g.cart, obs, emph, lane);
+    render_wave(rec, log_n, nt_s, oam_s, pal_s, ev_s, spr_s, slot_s, tile_s, a.g.cart, obs, emph, lane);
 }
 
 // ----------------------------------------------------------------------------------------- finish
