@@ -57,7 +57,7 @@ struct Con {
 
 struct Cart {
     const uint32_t* prgw;   // widened PRG
-    const uint32_t* fetchw; // NROM: instruction window of every CPU address (kFetchWords x 2 words), else nullptr
+    const uint32_t* fetchw; // decoded instructions: NROM by CPU address (kFetchWords x 2 words), else by PRG offset
     const uint8_t* chr;     // CHR ROM, nullptr = CHR RAM in the record
     uint32_t prg_pages8;    // 8 KB pages (power of two)
     uint32_t chr_pages1;    // 1 KB pages (power of two)
@@ -65,10 +65,11 @@ struct Cart {
     uint32_t mirroring;     // header: 0 horizontal, 1 vertical
 };
 
-// NROM instruction-fetch table: entry a = {dispatch key, operand word} (two dwords: the opcode at CPU address a, or
-// its hot key for the opcodes of kHotOps, and the bytes at a+1 | a+2 << 8) through the NROM mapping, for
+// Instruction-fetch table (fast path): entry = {dispatch key, operand word}, two dwords: the opcode, or its hot key
+// for the opcodes of kHotOps, and the decoded operand. NROM: entry a for CPU address a through the NROM mapping, for
 // $8000 <= a <= $FFFD; every other entry (RAM, I/O, the last two bytes, and a pc just past $FFFF) holds opcode $02,
-// which no fast-path handler runs, so the generic step fetches it.
+// which no fast-path handler runs, so the generic step fetches it. Banked boards: one entry per PRG byte offset (the
+// last two of each 8 KB page hold $02: an instruction there runs into the next CPU page).
 constexpr uint32_t kFetchWords = 0x10100u;
 
 // Opcodes the NROM fetch table stores as hot keys $100 + i (i = index here) instead of the opcode: the interpreter

@@ -1011,11 +1011,13 @@ void decision_phases(const Env& env, const GameK& g, const Outs& o, int e0, int 
     restart_phases(env, g, o, e0, e1, st);
 }
 
-// NROM fetch-table entry of the instruction at CPU address a (opcode op, next bytes b1 b2): the dispatch key (a hot
-// key for the opcodes of kHotOps, except a branch whose target is on another page) and the decoded operand word the
-// handlers take (wave_dev.h fx): the operand byte of a two-byte instruction, a branch's target times 8 (pc past
-// $FFFF not wrapped, as the interpreter counts it), JMP's and JSR's target times 8, else b1 | b2 << 8.
-void fetch_entry(uint32_t* e, uint32_t a, uint32_t op, uint32_t b1, uint32_t b2) {
+// Fetch-table entry of the instruction at a (NROM: a CPU address; banked boards: a PRG byte offset, whose low 13
+// bits are those of the CPU address wherever its 8 KB page is mapped), opcode op, next bytes b1 b2: the dispatch key
+// (a hot key for the opcodes of kHotOps, except a branch whose target is on another page) and the decoded operand
+// word the handlers take (wave_dev.h fx): the operand byte of a two-byte instruction; a branch's target times 8
+// (NROM; pc past $FFFF not wrapped, as the interpreter counts it) or its sign-extended offset (banked); JMP's and
+// JSR's target (times 8 on NROM); else b1 | b2 << 8.
+void fetch_entry(uint32_t* e, uint32_t a, uint32_t op, uint32_t b1, uint32_t b2, bool nrom) {
     const uint32_t d = kOptab.t[op], mode = d & 15u, grp = (d >> 8) & 15u;
     uint32_t base = b1 | (b2 << 8);
     bool cross = false;
@@ -1027,10 +1029,10 @@ void fetch_entry(uint32_t* e, uint32_t a, uint32_t op, uint32_t b1, uint32_t b2)
     if (mode == M_IMM || mode == M_ZP || mode == M_ZPX || mode == M_ZPY || mode == M_IZX || mode == M_IZY) {
         base = b1;
     } else if (mode == M_REL) {
-        const uint32_t tgt = a + 2u + (uint32_t)(int32_t)(int8_t)b1;
-        cross = ((a + 2u) ^ tgt) & 0xFF00u;
-        base = tgt << 3;
-    } else if (op == 0x4Cu || op == 0x20u) {
+        const uint32_t off = (uint32_t)(int32_t)(int8_t)b1, tgt = a + 2u + off;
+        cross = ((a + 2u) ^ tgt) & 0xFF00u;   // the page of pc + 2 and of the target (low bits of a suffice)
+        base = nrom ? tgt << 3 : off;
+    } else if (nrom && (op == 0x4Cu || op == 0x20u)) {
         base <<= 3;
     }
     uint32_t hot = 0;
@@ -1170,16 +1172,23 @@ void* rlenv_create(int ngames, const int* game_ids, const uint8_t* const* roms, 
             }
             uint32_t chr_pages = p.chr.empty() ? 8u : (uint32_t)(p.chr.size() / 1024u);
             if (chr_pages & (chr_pages - 1u)) throw std::runtime_error("CHR size must be a power of two");
-            uint32_t* fetchw = nullptr;
-            if (p.board == NES_BOARD_NROM) {
-                std::vector<uint32_t> f(2u * kFetchWords, 0u);
+            std::vector<uint32_t> f;
+            if (p.board == NES_BOARD_NROM) {   // by CPU address
+                f.assign(2u * kFetchWords, 0u);
                 for (uint32_t a = 0; a < kFetchWords; ++a) f[2u * a] = 0x02u;
                 const size_t mask = (p.prg.size() - 1u) & 0x7FFFu;
                 for (uint32_t a = 0x8000u; a <= 0xFFFDu; ++a)
-                    fetch_entry(&f[2u * a], a, p.prg[a & mask], p.prg[(a + 1u) & mask], p.prg[(a + 2u) & mask]);
-                fetchw = static_cast<uint32_t*>(env->mem.alloc(f.size() * 4));
-                env->mem.upload(fetchw, f.data(), f.size() * 4);
+                    fetch_entry(&f[2u * a], a, p.prg[a & mask], p.prg[(a + 1u) & mask], p.prg[(a + 2u) & mask],
+                                true);
+            } else {                            // by PRG offset; the last two bytes of each 8 KB page hold $02
+                f.assign(2u * p.prg.size(), 0u);
+                for (uint32_t o = 0; o < p.prg.size(); ++o) {
+                    if ((o & 0x1FFFu) > 0x1FFDu) f[2u * o] = 0x02u;
+                    else fetch_entry(&f[2u * o], o, p.prg[o], p.prg[o + 1u], p.prg[o + 2u], false);
+                }
             }
+            uint32_t* fetchw = static_cast<uint32_t*>(env->mem.alloc(f.size() * 4));
+            env->mem.upload(fetchw, f.data(), f.size() * 4);
             g.cart = Cart{prgw, fetchw, chr, (uint32_t)(p.prg.size() / 8192u), chr_pages, p.board, p.mirroring};
             g.recs = env->mem.zeros<NesRec>((size_t)g.n + 1);
             g.idle = env->mem.zeros<NesRec>((size_t)std::max(env->s.idle_tmpl, 1));

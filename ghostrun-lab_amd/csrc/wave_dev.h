@@ -142,13 +142,13 @@ constexpr uint32_t kGeneric = 0xFFFFFFFFu;
 
 // One instruction of opcode descriptor D at pcs = pc << pc_shift(B) (operand bytes lo, hi). Returns what it takes
 // off the burst counter, (CPU cycles << 14) - 1, or kGeneric with nothing changed when the generic step must run it.
-// On NROM the operand word comes decoded from the fetch table (kFetchWords): the operand byte of a two-byte
-// instruction, a branch's target times 8, JMP's and JSR's target times 8, else lo | hi << 8. HOT: a hot key (a branch
-// that stays on its page). On the other boards base is the two bytes after the opcode.
+// The operand word comes decoded from the fetch table (kFetchWords): the operand byte of a two-byte instruction; a
+// branch's target times 8 (NROM) or its sign-extended offset (banked boards); JMP's and JSR's target (times 8 on NROM);
+// else lo | hi << 8. HOT: a hot key (a branch that stays on its page).
 template <uint32_t B, uint32_t D, bool HOT = false>
 __device__ __forceinline__ uint32_t fx(Hot& h, const Mem& m, Con& cs, uint32_t pcs, uint32_t base) {
     constexpr uint32_t PS = pc_shift(B);
-    constexpr bool pre = B == NES_BOARD_NROM;
+    constexpr bool nrom = B == NES_BOARD_NROM;
     constexpr uint32_t mode = D & 15u, grp = (D >> 8) & 15u, sub = (D >> 12) & 15u;
     constexpr uint32_t src = (D >> 16) & 7u, dst = (D >> 19) & 7u;
     constexpr bool rd = (D & D_READ) != 0, wr = (D & D_WRITE) != 0, pen = (D & D_PEN) != 0;
@@ -159,7 +159,7 @@ __device__ __forceinline__ uint32_t fx(Hot& h, const Mem& m, Con& cs, uint32_t p
         uint32_t cyc = (D >> 4) & 15u;
         constexpr bool two = mode == M_IMM || mode == M_ZP || mode == M_ZPX || mode == M_ZPY || mode == M_IZX ||
                              mode == M_IZY;
-        const uint32_t lo = (pre && two) ? base : (base & 0xFFu);
+        const uint32_t lo = two ? base : (base & 0xFFu);
         uint32_t ea = 0;
         if constexpr (mode == M_ZP) {
             ea = lo;
@@ -194,7 +194,7 @@ __device__ __forceinline__ uint32_t fx(Hot& h, const Mem& m, Con& cs, uint32_t p
         }
         uint32_t opd = lo;
         if constexpr (rd) {
-            if constexpr (pre && mode == M_ZP) {
+            if constexpr (mode == M_ZP) {
                 opd = rd8(m, ea);   // the fetch table's operand byte: < $100
             } else if constexpr (zpage || wr) {
                 opd = rd8(m, ea & 0x7FFu);
@@ -254,7 +254,7 @@ __device__ __forceinline__ uint32_t fx(Hot& h, const Mem& m, Con& cs, uint32_t p
             else if constexpr (bit == 1u) set = (h.nz & 0xFFu) == 0u;
             else set = ((h.p >> bit) & 1u) != 0;
             if (set == ((sub & 8u) != 0)) {
-                const uint32_t tgt = pre ? base : npc + ((uint32_t)(int32_t)(int8_t)lo << PS);   // wrapped when stored
+                const uint32_t tgt = nrom ? base : npc + base;   // wrapped when stored
                 if constexpr (HOT) cyc += 1u;
                 else cyc += ((npc ^ tgt) & (0xFF00u << PS)) ? 2u : 1u;
                 npc = tgt;
@@ -283,14 +283,14 @@ __device__ __forceinline__ uint32_t fx(Hot& h, const Mem& m, Con& cs, uint32_t p
                                                  : (prg_wide(m, prg_index<B>(h, m, a1)) & 0xFFu);
                 npc = (l8 | (h8 << 8)) << PS;
             } else {
-                npc = pre ? base : base << PS;
+                npc = base;
                 if (npc == pcs) return kGeneric;   // the idle loop: the generic step runs it, then the fast-forward
             }
         } else if constexpr (grp == G_JSR) {
             const uint32_t ret = (pcs >> PS) + 2u;   // <= $FFFF
             hpush(h, m, ret >> 8);
             hpush(h, m, ret & 0xFFu);
-            npc = pre ? base : base << PS;
+            npc = base;
         } else if constexpr (grp == G_RTS) {
             const uint32_t l8 = hpull(h, m), h8 = hpull(h, m);
             npc = (((h8 << 8) | l8) + 1u) << PS;
@@ -301,7 +301,7 @@ __device__ __forceinline__ uint32_t fx(Hot& h, const Mem& m, Con& cs, uint32_t p
             npc = ((h8 << 8) | l8) << PS;
         }
         if constexpr (wr) {
-            if constexpr (pre && mode == M_ZP) m.ram[ea] = (uint8_t)res;
+            if constexpr (mode == M_ZP) m.ram[ea] = (uint8_t)res;
             else if constexpr (zpage || rd) m.ram[ea & 0x7FFu] = (uint8_t)res;
             else if (ea < 0x2000u) m.ram[ea & 0x7FFu] = (uint8_t)res;
             else port_write(cs, res);
@@ -311,11 +311,11 @@ __device__ __forceinline__ uint32_t fx(Hot& h, const Mem& m, Con& cs, uint32_t p
     }
 }
 
-// (on NROM a hot opcode other than a branch never reaches the switch over all opcodes: its case merges into the
-// default; a branch to another page comes here with its opcode)
+// (a hot opcode other than a branch never reaches the switch over all opcodes: its case merges into the default; a
+// branch to another page comes here with its opcode)
 #define ND_FX(n)                                                                              \
     case n:                                                                                   \
-        if constexpr (B == NES_BOARD_NROM && is_hot(n) && (kOptab.t[n] & 15u) != M_REL)      \
+        if constexpr (is_hot(n) && (kOptab.t[n] & 15u) != M_REL)                              \
             return kGeneric;                                                                  \
         else                                                                                  \
             return fx<B, kOptab.t[n]>(h, m, cs, pcs, base);
@@ -327,7 +327,7 @@ __device__ __forceinline__ uint32_t fx(Hot& h, const Mem& m, Con& cs, uint32_t p
     ND_FX(h + 0x7) ND_FX(h + 0x8) ND_FX(h + 0x9) ND_FX(h + 0xA) ND_FX(h + 0xB) ND_FX(h + 0xC) ND_FX(h + 0xD)          \
     ND_FX(h + 0xE) ND_FX(h + 0xF)
 
-// The opcodes' switch (on NROM without the hot ones, which never reach it).
+// The opcodes' switch (without the hot ones, which never reach it).
 template <uint32_t B>
 __device__ __forceinline__ uint32_t fx_all(Hot& h, const Mem& m, Con& cs, uint32_t pcs, uint32_t op, uint32_t base) {
     switch (op) {
@@ -338,7 +338,7 @@ __device__ __forceinline__ uint32_t fx_all(Hot& h, const Mem& m, Con& cs, uint32
     }
 }
 
-// The hot keys' switch (NROM).
+// The hot keys' switch.
 template <uint32_t B>
 __device__ __forceinline__ uint32_t fx_hot(Hot& h, const Mem& m, Con& cs, uint32_t pcs, uint32_t op, uint32_t base) {
     switch (op) {
@@ -348,32 +348,26 @@ __device__ __forceinline__ uint32_t fx_hot(Hot& h, const Mem& m, Con& cs, uint32
 }
 
 // The fast path for the instruction at h.pc: (its cycles << 14) - 1, or kGeneric (nothing changed) for the generic
-// step.
+// step. The instruction comes decoded from the fetch table: on NROM at byte offset pcs = pc * 8 (pc <= $1007E, a
+// branch just past $FFFF; $02 outside PRG), a scalar load with an SGPR offset; on the banked boards at the PRG offset
+// of pc ($02 in the last two bytes of a page), for pc in PRG.
 template <uint32_t B>
 __device__ __forceinline__ uint32_t fast_step(Hot& h, const Mem& m, Con& cs, uint32_t* op_out) {
     const uint32_t pcs = h.pc;
-    if constexpr (B == NES_BOARD_NROM) {
-        // pc <= $1007E (a branch just past $FFFF); $02 outside PRG. The entry is the key (the opcode, or a hot key
-        // $100 + i for kHotOps[i]) and the operand word as two dwords (no field extraction), at byte offset
-        // pcs = pc * 8: a scalar load with an SGPR offset.
-        // (two 32-bit loads, which the compiler pairs into one 64-bit load: read as the halves of a 64-bit value,
-        // base's compares would become 64-bit ones, which the scalar unit has only for equality)
-        ConstU32* e = (ConstU32*)((ConstU8*)m.cart.fetchw + pcs);
-        const uint32_t op = e[0], base = e[1];
-        *op_out = op;
-        if (__builtin_expect(op >= kHotKey, 1)) return fx_hot<B>(h, m, cs, pcs, op, base);
-        // (read back as an opaque scalar: with the range op < $100 known the compiler narrows the switch to 8 bits
-        // and widens it again with two masks)
-        return fx_all<B>(h, m, cs, pcs, uni(op), base);
-    } else {
-        // code in PRG ($8000+) and the 3-byte window inside one 8 KB page: pc >= $8000 and (pc & $1FFF) <= $1FFD,
-        // as one compare ((pc + 2) & $9FFF keeps bit 15 and the page offset of the window's last byte)
-        if (((pcs + 2u) & 0x9FFFu) < 0x8002u) return kGeneric;
-        const uint32_t word = prg_wide(m, prg_index<B>(h, m, pcs));
-        const uint32_t op = word & 0xFFu, base = word >> 8;   // bits 24-31 of the word are 0
-        *op_out = op;
-        return fx_all<B>(h, m, cs, pcs, op, base);
+    uint32_t off = pcs;
+    if constexpr (B != NES_BOARD_NROM) {
+        if (pcs - 0x8000u >= 0x8000u) return kGeneric;   // pc outside $8000-$FFFF (one past $FFFF included)
+        off = prg_index<B>(h, m, pcs) << 3;
     }
+    // (two 32-bit loads, which the compiler pairs into one 64-bit load: read as the halves of a 64-bit value,
+    // base's compares would become 64-bit ones, which the scalar unit has only for equality)
+    ConstU32* e = (ConstU32*)((ConstU8*)m.cart.fetchw + off);
+    const uint32_t op = e[0], base = e[1];
+    *op_out = op;
+    if (__builtin_expect(op >= kHotKey, 1)) return fx_hot<B>(h, m, cs, pcs, op, base);
+    // (read back as an opaque scalar: with the range op < $100 known the compiler narrows the switch to 8 bits and
+    // widens it again with two masks)
+    return fx_all<B>(h, m, cs, pcs, uni(op), base);
 }
 #undef ND_FX16
 #undef ND_FX
