@@ -222,9 +222,11 @@ struct WaveLds {
 
 // One console per wavefront (blockDim 64): the console index comes from blockIdx only, so every emulator value is
 // wave-uniform; lane 0 runs the 6502 on the scalar unit (SGPRs, uniform branches) with the console's memories in
-// LDS, the 64 lanes copy them in and out.
+// LDS, the 64 lanes copy them in and out. Eight waves per SIMD: 8192 consoles fill 256 CUs x 4 SIMDs x 8 in one
+// round (left to itself the compiler takes 71 VGPRs, 7 waves, and the eighth wave of every SIMD runs after the
+// others).
 template <uint32_t B>
-__global__ __launch_bounds__(64) void k_emu_w(EmuArgs a) {
+__global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(8, 8))) void k_emu_w(EmuArgs a) {
     __shared__ __align__(16) WaveLds L;
     const int count = a.mode == EMU_BOOT ? 1 : slot_count(a.g, a.use_list, a.e0, a.e1);
     const int k = (int)blockIdx.x;
@@ -1157,11 +1159,17 @@ void* rlenv_create(int ngames, const int* game_ids, const uint8_t* const* roms, 
             offset += g.n;
             g.start_ok = 0;   // smb: Start/Select not allowed (rl/csrc/reward10_consts.h:28)
             g.select_ok = 0;
-            // widened PRG: word i = bytes i, i+1, i+2 (the instruction window at i)
-            std::vector<uint32_t> wide(p.prg.size());
-            for (size_t k = 0; k < p.prg.size(); ++k) {
-                const size_t k1 = std::min(k + 1, p.prg.size() - 1), k2 = std::min(k + 2, p.prg.size() - 1);
-                wide[k] = p.prg[k] | ((uint32_t)p.prg[k1] << 8) | ((uint32_t)p.prg[k2] << 16);
+            // widened PRG: word i = bytes i, i+1, i+2 (the instruction window at i); an NROM image is widened to
+            // 32 KB (a 16 KB one mirrored, as the CPU sees it) so that the fast path indexes it by address & $7FFF
+            std::vector<uint8_t> img(p.prg);
+            if (p.board == NES_BOARD_NROM) {
+                img.resize(32768u);
+                for (size_t k = p.prg.size(); k < img.size(); ++k) img[k] = p.prg[k % p.prg.size()];
+            }
+            std::vector<uint32_t> wide(img.size());
+            for (size_t k = 0; k < img.size(); ++k) {
+                const size_t k1 = std::min(k + 1, img.size() - 1), k2 = std::min(k + 2, img.size() - 1);
+                wide[k] = img[k] | ((uint32_t)img[k1] << 8) | ((uint32_t)img[k2] << 16);
             }
             uint32_t* prgw = static_cast<uint32_t*>(env->mem.alloc(wide.size() * 4));
             env->mem.upload(prgw, wide.data(), wide.size() * 4);

@@ -126,7 +126,7 @@ __device__ __forceinline__ void port_write(Con& cs, uint32_t v) {
 // Byte offset in the PRG image of CPU address `addr` ($8000-$FFFF). NROM maps the image linearly (mirrored).
 template <uint32_t B>
 __device__ __forceinline__ uint32_t prg_index(const Hot& h, const Mem& m, uint32_t addr) {
-    if constexpr (B == NES_BOARD_NROM) return addr & 0x7FFFu & (m.cart.prg_pages8 * 8192u - 1u);
+    if constexpr (B == NES_BOARD_NROM) return addr & 0x7FFFu;   // the NROM image is 32 KB (16 KB mirrored)
     else return sel4((addr >> 13) & 3u, h.prg0, h.prg1, h.prg2, h.prg3) + (addr & 0x1FFFu);
 }
 
