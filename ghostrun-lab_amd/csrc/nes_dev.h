@@ -63,10 +63,11 @@ struct Cart {
     uint32_t chr_pages1;    // 1 KB pages (power of two)
     uint32_t board;
     uint32_t mirroring;     // header: 0 horizontal, 1 vertical
+    uint32_t bus_conflicts; // CNROM declared with AND-type bus conflicts (NES 2.0 submapper 2)
 };
 
 // Instruction-fetch table (fast path): entry = {dispatch key, operand word}, two dwords: the opcode, or its hot key
-// for the opcodes of kHotOps, and the decoded operand. NROM: entry a for CPU address a through the NROM mapping, for
+// for the opcodes of kHotOps, and the decoded operand. NROM and CNROM (fixed PRG): entry a for CPU address a, for
 // $8000 <= a <= $FFFD; every other entry (RAM, I/O, the last two bytes, and a pc just past $FFFF) holds opcode $02,
 // which no fast-path handler runs, so the generic step fetches it. Banked boards: one entry per PRG byte offset (the
 // last two of each 8 KB page hold $02: an instruction there runs into the next CPU page).
@@ -182,9 +183,10 @@ __device__ inline void map_sync(Con& c, const Mem& m) {
         map_set_chr(m, 3u ^ f, r[1] | 1u);
         for (uint32_t i = 0; i < 4; ++i) map_set_chr(m, (4u + i) ^ f, r[2 + i]);
         map_set_nt(c, m, (r[9] & 1u) ? 0u : 1u);
-    } else {
+    } else {   // NROM; CNROM: the 8 KB CHR bank in register 0 (patch:2982-2990)
+        const uint32_t chr8 = m.cart.board == NES_BOARD_CNROM ? r[0] : 0u;
         for (uint32_t i = 0; i < 4; ++i) map_set_prg(c, m, i, i);
-        for (uint32_t i = 0; i < 8; ++i) map_set_chr(m, i, i);
+        for (uint32_t i = 0; i < 8; ++i) map_set_chr(m, i, chr8 * 8u + i);
         map_set_nt(c, m, m.cart.mirroring ? 1u : 0u);
     }
 }
@@ -221,6 +223,10 @@ __device__ inline void map_write(Con& c, const Mem& m, uint32_t addr, uint32_t v
             else r[13] = 1;
             return;
         }
+        map_sync(c, m);
+    } else if (m.cart.board == NES_BOARD_CNROM) {   // the bank latch, ANDed with the ROM byte under a bus conflict
+        const uint32_t rom = m.cart.prgw[m.rec->prg_off[(addr >> 13) & 3u] + (addr & 0x1FFFu)] & 0xFFu;
+        r[0] = (uint8_t)(m.cart.bus_conflicts ? (v & rom) : v);
         map_sync(c, m);
     }
 }

@@ -890,7 +890,7 @@ struct Env {
 // iNES -> cart description; the PRG is padded to a power of two by repeating a short image (NROM-128).
 struct Parsed {
     std::vector<uint8_t> prg, chr;
-    uint32_t board = 0, mirroring = 0;
+    uint32_t board = 0, mirroring = 0, bus_conflicts = 0;
 };
 
 Parsed parse_ines(const uint8_t* rom, size_t size) {
@@ -899,8 +899,9 @@ Parsed parse_ines(const uint8_t* rom, size_t size) {
     const uint32_t mapper = (rom[6] >> 4) | (rom[7] & 0xF0u);
     const size_t skip = 16u + ((rom[6] & 4u) ? 512u : 0u);
     if (rom[6] & 8u) throw std::runtime_error("four-screen nametables are not supported");
-    if (mapper != 0 && mapper != 1 && mapper != 4)
-        throw std::runtime_error("unsupported mapper " + std::to_string(mapper) + " (supported: 0 NROM, 1 MMC1, 4 MMC3)");
+    if (mapper != 0 && mapper != 1 && mapper != 3 && mapper != 4)
+        throw std::runtime_error("unsupported mapper " + std::to_string(mapper) +
+                                 " (supported: 0 NROM, 1 MMC1, 3 CNROM, 4 MMC3)");
     if (prg == 0 || skip + prg + chr > size) throw std::runtime_error("truncated iNES image");
     Parsed p;
     size_t padded = 8192;
@@ -910,6 +911,8 @@ Parsed parse_ines(const uint8_t* rom, size_t size) {
     p.chr.assign(rom + skip + prg, rom + skip + prg + chr);
     p.board = mapper;
     p.mirroring = rom[6] & 1u;
+    // CNROM bus conflicts only when the header declares them: NES 2.0, submapper 2 (patch:4008)
+    p.bus_conflicts = mapper == 3u && (rom[7] & 0x0Cu) == 0x08u && (rom[8] >> 4) == 2u;
     return p;
 }
 
@@ -956,7 +959,7 @@ void launch_emu(const Env& env, const GameK& g, const Outs& o, int mode, int f, 
             if (wave) {
                 if (g.cart.board == NES_BOARD_MMC3) hipLaunchKernelGGL(k_emu_w<NES_BOARD_MMC3>, dim3(blocks), dim3(64), 0, st, a);
                 else if (g.cart.board == NES_BOARD_MMC1) hipLaunchKernelGGL(k_emu_w<NES_BOARD_MMC1>, dim3(blocks), dim3(64), 0, st, a);
-                else hipLaunchKernelGGL(k_emu_w<NES_BOARD_NROM>, dim3(blocks), dim3(64), 0, st, a);
+                else hipLaunchKernelGGL(k_emu_w<NES_BOARD_NROM>, dim3(blocks), dim3(64), 0, st, a);   // NROM, CNROM
             }
             else hipLaunchKernelGGL(k_emu, dim3(blocks), dim3(64), lds, st, a);
         });
@@ -1159,10 +1162,12 @@ void* rlenv_create(int ngames, const int* game_ids, const uint8_t* const* roms, 
             offset += g.n;
             g.start_ok = 0;   // smb: Start/Select not allowed (rl/csrc/reward10_consts.h:28)
             g.select_ok = 0;
-            // widened PRG: word i = bytes i, i+1, i+2 (the instruction window at i); an NROM image is widened to
-            // 32 KB (a 16 KB one mirrored, as the CPU sees it) so that the fast path indexes it by address & $7FFF
+            // widened PRG: word i = bytes i, i+1, i+2 (the instruction window at i); a fixed NROM or CNROM image is
+            // widened to 32 KB (a 16 KB one mirrored, as the CPU sees it), so that the fast path (the NROM one for
+            // both: CNROM switches only CHR) indexes it by address & $7FFF
             std::vector<uint8_t> img(p.prg);
-            if (p.board == NES_BOARD_NROM) {
+            const bool fixed32 = p.board == NES_BOARD_NROM || p.board == NES_BOARD_CNROM;   // the NROM fast path
+            if (fixed32) {
                 img.resize(32768u);
                 for (size_t k = p.prg.size(); k < img.size(); ++k) img[k] = p.prg[k % p.prg.size()];
             }
@@ -1181,7 +1186,7 @@ void* rlenv_create(int ngames, const int* game_ids, const uint8_t* const* roms, 
             uint32_t chr_pages = p.chr.empty() ? 8u : (uint32_t)(p.chr.size() / 1024u);
             if (chr_pages & (chr_pages - 1u)) throw std::runtime_error("CHR size must be a power of two");
             std::vector<uint32_t> f;
-            if (p.board == NES_BOARD_NROM) {   // by CPU address
+            if (fixed32) {   // by CPU address
                 f.assign(2u * kFetchWords, 0u);
                 for (uint32_t a = 0; a < kFetchWords; ++a) f[2u * a] = 0x02u;
                 const size_t mask = (p.prg.size() - 1u) & 0x7FFFu;
@@ -1197,7 +1202,8 @@ void* rlenv_create(int ngames, const int* game_ids, const uint8_t* const* roms, 
             }
             uint32_t* fetchw = static_cast<uint32_t*>(env->mem.alloc(f.size() * 4));
             env->mem.upload(fetchw, f.data(), f.size() * 4);
-            g.cart = Cart{prgw, fetchw, chr, (uint32_t)(p.prg.size() / 8192u), chr_pages, p.board, p.mirroring};
+            g.cart = Cart{prgw, fetchw, chr, (uint32_t)(p.prg.size() / 8192u), chr_pages, p.board, p.mirroring,
+                          p.bus_conflicts};
             g.recs = env->mem.zeros<NesRec>((size_t)g.n + 1);
             g.idle = env->mem.zeros<NesRec>((size_t)std::max(env->s.idle_tmpl, 1));
             g.list = env->mem.zeros<int32_t>((size_t)std::max(g.n, 1));

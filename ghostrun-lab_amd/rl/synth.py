@@ -112,12 +112,15 @@ class Asm:
         return bytes(out)
 
 
-def ines(prg: bytes, chr_: bytes, mapper: int, vertical: bool = True) -> bytes:
+def ines(prg: bytes, chr_: bytes, mapper: int, vertical: bool = True, submapper: int = None) -> bytes:
+    """iNES image; with a submapper, an NES 2.0 header (byte 7 bits 2-3 = 2, submapper in byte 8 bits 4-7)."""
     assert len(prg) % 16384 == 0 and len(chr_) % 8192 == 0
     h = bytearray(b'NES\x1a')
     h += bytes((len(prg) // 16384, len(chr_) // 8192, ((mapper & 15) << 4) | (1 if vertical else 0),
-                mapper & 0xF0))
+                (mapper & 0xF0) | (0x08 if submapper is not None else 0)))
     h += bytes(8)
+    if submapper is not None:
+        h[8] = (submapper & 15) << 4
     return bytes(h) + prg + chr_
 
 
@@ -286,6 +289,52 @@ def nrom_cart(seed: int = 0, blocks: int = 24) -> bytes:
     prg[0x3FFA:0x4000] = bytes(sum(((v & 0xFF, v >> 8) for v in vec), ()))
     chr_ = rng.integers(0, 256, 8192, dtype=np.uint8).tobytes()
     return ines(bytes(prg), chr_, 0, vertical=True)
+
+
+def cnrom_cart(seed: int = 0, blocks: int = 24, conflicts: bool = False) -> bytes:
+    """CNROM cartridge: 32 KB PRG at $8000, 32 KB CHR in four 8 KB banks. The NMI selects bank FRAMES & 3 and the
+    main loop selects one mid-frame from the counter and the pad, both by storing the bank number over a ROM byte
+    that holds it (no bus conflict). With conflicts, the header declares AND-type bus conflicts (NES 2.0 submapper 2)
+    and the main loop also stores $FF over a byte holding 2 when pad bit 6 is set: bank 2 there, bank 3 without
+    conflicts."""
+    rng = np.random.default_rng([0x434E524D, seed])
+    pal, nt, oam, mix = _tables(rng)
+    a = Asm(0x8000)
+    tables = dict(pal='t_pal', nt='t_nt', oam='t_oam')
+    a.label('reset')
+    _reset_common(a, 0x90, tables)
+    a.label('main')
+    _read_pad(a, 'm')
+    _pad_moves(a, 't_mix')
+    _filler(a, rng, blocks // 2, 'f', 't_mix')
+    a.op('LDA', 'zp', CNT_LO); a.op('EOR', 'zp', PAD); a.op('AND', 'imm', 3); a.op('TAX')
+    a.op('STA', 'abx', 't_bank')
+    a.op('LDA', 'zp', PAD); a.op('AND', 'imm', 0x40); a.op('BEQ', 'rel', 'no_cf')
+    a.op('LDA', 'imm', 0xFF); a.op('STA', 'abs', 't_two')
+    a.label('no_cf')
+    _filler(a, rng, blocks - blocks // 2, 'g', 't_mix')
+    a.op('JMP', 'abs', 'main')
+    a.label('nmi')
+    _nmi_common(a)
+    a.op('LDA', 'zp', FRAMES); a.op('AND', 'imm', 3); a.op('TAX'); a.op('STA', 'abx', 't_bank')
+    _nmi_end(a)
+    a.label('irq')
+    a.op('RTI')
+    a.label('t_bank')
+    a.data(bytes((0, 1, 2, 3)))
+    a.label('t_two')
+    a.data(bytes((2,)))
+    for name, t in (('t_pal', pal), ('t_nt', nt), ('t_oam', oam), ('t_mix', mix)):
+        a.label(name)
+        a.data(bytes(int(v) for v in t))
+    code = a.assemble()
+    assert len(code) <= 0x7FFA, len(code)
+    prg = bytearray(32768)
+    prg[:len(code)] = code
+    vec = (a.labels['nmi'], a.labels['reset'], a.labels['irq'])
+    prg[0x7FFA:0x8000] = bytes(sum(((v & 0xFF, v >> 8) for v in vec), ()))
+    chr_ = rng.integers(0, 256, 32768, dtype=np.uint8).tobytes()
+    return ines(bytes(prg), chr_, 3, vertical=True, submapper=2 if conflicts else None)
 
 
 def mmc3_cart(seed: int = 0, blocks: int = 16, sub_blocks: int = 20) -> bytes:

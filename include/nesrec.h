@@ -36,6 +36,7 @@
 /* Boards. */
 #define NES_BOARD_NROM 0u
 #define NES_BOARD_MMC1 1u
+#define NES_BOARD_CNROM 3u                    /* 32 KB PRG fixed, 8 KB CHR bank latch (patch:3418) */
 #define NES_BOARD_MMC3 4u
 
 /* Frame-log event kinds (word 0 bits 24..31). Word 0 bits 0..23: event time + NES_LOG_TIME_BIAS, where the

@@ -1,10 +1,12 @@
-"""Known-answer tests of the oracle's cartridge boards (NROM, MMC1, MMC3) and its DMC.
+"""Known-answer tests of the oracle's cartridge boards (NROM, CNROM, MMC1, MMC3) and its DMC.
 
 MMC3: restates the reference's register case third_party/nesle-extensions.patch:4638-4673 (R0-R7 = 00 3A 4A 5D 6E 61
 0A 04, bank select $46, $A000 = 1 on 128 KB PRG / 128 KB CHR) by writing the registers through the CPU bus, plus
 the scanline counter (reload, count down once per rendered line at dot 266, IRQ at zero, $E000 acknowledge).
 MMC1: the serial port and the bank modes written from the board's documented register meanings (16 KB PRG banks,
 4 KB CHR banks), not from the oracle's page arithmetic.
+CNROM: the bank latch and its declared AND-type bus conflicts from the board's behaviour as the reference states it
+(patch:2982-2990, 3124-3127, 4008), checked on a cart whose PRG pages are tagged with their numbers.
 DMC: restates the sample-channel cases of patch:4105-4205 (status bit 4, 4-cycle fetch steals, loop, rate change,
 no steal in the idle fast-forward) with the same 4-cycle instruction driver as the reference test.
 """
@@ -40,6 +42,64 @@ def test_nrom_128_is_mirrored_and_header_mirroring():
     assert [con.read(a) for a in (0x8000, 0xA000, 0xC000, 0xE000)] == [0, 1, 0, 1]
     assert chr_ == list(range(8)) and nt == [0, 0, 1, 1]
     assert pages(Console(cart(0, 32, 8)))[2] == [0, 1, 0, 1]
+
+
+# ---------------------------------------------------------------------------------------------- CNROM
+
+def cnrom_cart(conflicts):
+    """32 KB PRG (8 KB pages tagged with their number), 32 KB CHR; NES 2.0 submapper 2 when conflicts."""
+    prg = bytearray(32 * KB)
+    for i in range(0, len(prg), 8 * KB):
+        prg[i] = i // (8 * KB)
+    prg[0x7FF0] = 0x0C                                   # a ROM byte with bits 2-3 set
+    prg[0x6010:0x6014] = bytes((0xEA, 0x4C, 0x10, 0xE0))
+    prg[-6:] = bytes((0x10, 0xE0, 0x10, 0xE0, 0x10, 0xE0))
+    return synth.ines(bytes(prg), bytes(32 * KB), 3, submapper=2 if conflicts else None)
+
+
+def test_cnrom_bank_latch():
+    """The 8 KB CHR bank is the written value, masked to the CHR size; PRG stays fixed (patch:2982-2990,
+    3124-3127)."""
+    con = Console(cnrom_cart(False))
+    prg, chr_, nt = pages(con)
+    assert chr_ == list(range(8)) and [con.read(a) for a in (0x8000, 0xA000, 0xC000, 0xE000)] == [0, 1, 2, 3]
+    con.write(0x8000, 2)
+    assert pages(con)[1] == list(range(16, 24))
+    con.write(0xFFF0, 7)                                 # 4 banks: 7 -> 3
+    assert pages(con)[1] == list(range(24, 32))
+    assert [con.read(a) for a in (0x8000, 0xA000, 0xC000, 0xE000)] == [0, 1, 2, 3]
+
+
+def test_cnrom_declared_bus_conflicts():
+    """Declared AND-type bus conflicts (NES 2.0 submapper 2): the latch takes value AND the ROM byte under the
+    address; the same writes on an iNES 1.0 header take the value (patch:4008)."""
+    con = Console(cnrom_cart(True))
+    con.write(0xA000, 3)                                 # ROM byte 1
+    assert pages(con)[1] == list(range(8, 16))
+    con.write(0xFFF0, 0xFF)                              # ROM byte $0C -> 0x0C & 3 = 0 after the mask
+    assert pages(con)[1] == list(range(8))
+    con.write(0xC000, 0x07)                              # ROM byte 2
+    assert pages(con)[1] == list(range(16, 24))
+    plain = Console(cnrom_cart(False))
+    plain.write(0xA000, 3)
+    assert pages(plain)[1] == list(range(24, 32))
+
+
+@pytest.mark.parametrize('conflicts', [False, True])
+def test_cnrom_synthetic_cart_switches_chr(conflicts):
+    """The seed-generated CNROM cart (the GPU parity case) selects all four CHR banks, some of them mid-frame
+    (frame-log CHR events), with and without declared bus conflicts."""
+    con = Console(synth.cnrom_cart(1, conflicts=conflicts))
+    t, banks, events = 82182, set(), 0
+    for f in range(40):
+        con.set('pad', [0x81, 0x40, 0x02, 0xC0][f % 4])
+        assert con.run_until(t) == 0
+        t += 89342
+        banks.add(pages(con)[1][0] // 8)
+        n = con.u('log_n', 'H')
+        log = con.words('log', 16 + 2 * 256)
+        events += sum(1 for i in range(min(n, 256)) if (int(log[16 + 2 * i]) >> 24) == 7)   # NES_EV_CHR
+    assert banks == {0, 1, 2, 3} and events > 0
 
 
 # ----------------------------------------------------------------------------------------------- MMC3
