@@ -63,7 +63,7 @@ struct Cart {
     uint32_t chr_pages1;    // 1 KB pages (power of two)
     uint32_t board;
     uint32_t mirroring;     // header: 0 horizontal, 1 vertical
-    uint32_t bus_conflicts; // CNROM declared with AND-type bus conflicts (NES 2.0 submapper 2)
+    uint32_t bus_conflicts; // UxROM / CNROM declared with AND-type bus conflicts (NES 2.0 submapper 2)
 };
 
 // Instruction-fetch table (fast path): entry = {dispatch key, operand word}, two dwords: the opcode, or its hot key
@@ -183,6 +183,14 @@ __device__ inline void map_sync(Con& c, const Mem& m) {
         map_set_chr(m, 3u ^ f, r[1] | 1u);
         for (uint32_t i = 0; i < 4; ++i) map_set_chr(m, (4u + i) ^ f, r[2 + i]);
         map_set_nt(c, m, (r[9] & 1u) ? 0u : 1u);
+    } else if (m.cart.board == NES_BOARD_UXROM) {   // the 16 KB bank in register 0, the last one fixed at $C000
+        const uint32_t last = m.cart.prg_pages8 / 2u - 1u;
+        map_set_prg(c, m, 0, r[0] * 2u);
+        map_set_prg(c, m, 1, r[0] * 2u + 1u);
+        map_set_prg(c, m, 2, last * 2u);
+        map_set_prg(c, m, 3, last * 2u + 1u);
+        for (uint32_t i = 0; i < 8; ++i) map_set_chr(m, i, i);
+        map_set_nt(c, m, m.cart.mirroring ? 1u : 0u);
     } else {   // NROM; CNROM: the 8 KB CHR bank in register 0 (patch:2982-2990)
         const uint32_t chr8 = m.cart.board == NES_BOARD_CNROM ? r[0] : 0u;
         for (uint32_t i = 0; i < 4; ++i) map_set_prg(c, m, i, i);
@@ -224,7 +232,8 @@ __device__ inline void map_write(Con& c, const Mem& m, uint32_t addr, uint32_t v
             return;
         }
         map_sync(c, m);
-    } else if (m.cart.board == NES_BOARD_CNROM) {   // the bank latch, ANDed with the ROM byte under a bus conflict
+    } else if (m.cart.board == NES_BOARD_CNROM || m.cart.board == NES_BOARD_UXROM) {
+        // the bank latch, ANDed with the ROM byte under a bus conflict
         const uint32_t rom = m.cart.prgw[m.rec->prg_off[(addr >> 13) & 3u] + (addr & 0x1FFFu)] & 0xFFu;
         r[0] = (uint8_t)(m.cart.bus_conflicts ? (v & rom) : v);
         map_sync(c, m);

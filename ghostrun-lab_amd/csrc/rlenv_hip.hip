@@ -899,9 +899,9 @@ Parsed parse_ines(const uint8_t* rom, size_t size) {
     const uint32_t mapper = (rom[6] >> 4) | (rom[7] & 0xF0u);
     const size_t skip = 16u + ((rom[6] & 4u) ? 512u : 0u);
     if (rom[6] & 8u) throw std::runtime_error("four-screen nametables are not supported");
-    if (mapper != 0 && mapper != 1 && mapper != 3 && mapper != 4)
+    if (mapper > 4u)
         throw std::runtime_error("unsupported mapper " + std::to_string(mapper) +
-                                 " (supported: 0 NROM, 1 MMC1, 3 CNROM, 4 MMC3)");
+                                 " (supported: 0 NROM, 1 MMC1, 2 UxROM, 3 CNROM, 4 MMC3)");
     if (prg == 0 || skip + prg + chr > size) throw std::runtime_error("truncated iNES image");
     Parsed p;
     size_t padded = 8192;
@@ -911,8 +911,8 @@ Parsed parse_ines(const uint8_t* rom, size_t size) {
     p.chr.assign(rom + skip + prg, rom + skip + prg + chr);
     p.board = mapper;
     p.mirroring = rom[6] & 1u;
-    // CNROM bus conflicts only when the header declares them: NES 2.0, submapper 2 (patch:4008)
-    p.bus_conflicts = mapper == 3u && (rom[7] & 0x0Cu) == 0x08u && (rom[8] >> 4) == 2u;
+    // UxROM / CNROM bus conflicts only when the header declares them: NES 2.0, submapper 2 (patch:4008)
+    p.bus_conflicts = (mapper == 2u || mapper == 3u) && (rom[7] & 0x0Cu) == 0x08u && (rom[8] >> 4) == 2u;
     return p;
 }
 
@@ -957,9 +957,11 @@ void launch_emu(const Env& env, const GameK& g, const Outs& o, int mode, int f, 
     if (blocks > 0)
         env.clock.run(cls, st, [&] {
             if (wave) {
-                if (g.cart.board == NES_BOARD_MMC3) hipLaunchKernelGGL(k_emu_w<NES_BOARD_MMC3>, dim3(blocks), dim3(64), 0, st, a);
-                else if (g.cart.board == NES_BOARD_MMC1) hipLaunchKernelGGL(k_emu_w<NES_BOARD_MMC1>, dim3(blocks), dim3(64), 0, st, a);
-                else hipLaunchKernelGGL(k_emu_w<NES_BOARD_NROM>, dim3(blocks), dim3(64), 0, st, a);   // NROM, CNROM
+                // the fast path knows two kinds of board: fixed 32 KB PRG (NROM, CNROM) and banked PRG (the rest)
+                if (g.cart.board == NES_BOARD_NROM || g.cart.board == NES_BOARD_CNROM)
+                    hipLaunchKernelGGL(k_emu_w<NES_BOARD_NROM>, dim3(blocks), dim3(64), 0, st, a);
+                else
+                    hipLaunchKernelGGL(k_emu_w<NES_BOARD_MMC3>, dim3(blocks), dim3(64), 0, st, a);
             }
             else hipLaunchKernelGGL(k_emu, dim3(blocks), dim3(64), lds, st, a);
         });

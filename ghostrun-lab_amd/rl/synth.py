@@ -337,6 +337,64 @@ def cnrom_cart(seed: int = 0, blocks: int = 24, conflicts: bool = False) -> byte
     return ines(bytes(prg), chr_, 3, vertical=True, submapper=2 if conflicts else None)
 
 
+def uxrom_cart(seed: int = 0, blocks: int = 16, sub_blocks: int = 16, conflicts: bool = False) -> bytes:
+    """UxROM cartridge: 128 KB PRG in 16 KB banks (banks 0-6 hold seeded subroutines at $8000, bank 7 is fixed at
+    $C000), 8 KB random CHR. The main loop selects a bank from the counter and the pad by storing the bank number
+    over a ROM byte that holds it, and calls the subroutine there. With conflicts, the header declares AND-type bus
+    conflicts (NES 2.0 submapper 2) and the main loop also stores $FF over a byte holding 5 when pad bit 6 is set:
+    bank 5 there, bank 7 without conflicts."""
+    rng = np.random.default_rng([0x55584F4D, seed])
+    pal, nt, oam, mix = _tables(rng)
+    banks = []
+    for b in range(7):
+        s = Asm(0x8000)
+        _filler(s, rng, sub_blocks, f'b{b}', 0xBF00)
+        s.op('RTS')
+        body = s.assemble()
+        page = bytearray(16384)
+        page[:len(body)] = body
+        page[0x3F00:0x4000] = rng.integers(0, 256, 256, dtype=np.uint8).tobytes()   # table at $BF00
+        banks.append(bytes(page))
+    a = Asm(0xC000)
+    tables = dict(pal='t_pal', nt='t_nt', oam='t_oam')
+    a.op('RTS')                                          # bank 7 at $8000 (the $FF store): the call returns
+    a.label('reset')
+    _reset_common(a, 0x90, tables)
+    a.label('main')
+    _read_pad(a, 'm')
+    _pad_moves(a, 't_mix')
+    a.op('LDA', 'zp', CNT_LO); a.op('EOR', 'zp', PAD); a.op('AND', 'imm', 7); a.op('CMP', 'imm', 7)
+    a.op('BCC', 'rel', 'bk_ok'); a.op('LDA', 'imm', 2)
+    a.label('bk_ok')
+    a.op('TAX'); a.op('STA', 'abx', 't_bank')
+    a.op('LDA', 'zp', PAD); a.op('AND', 'imm', 0x40); a.op('BEQ', 'rel', 'no_cf')
+    a.op('LDA', 'imm', 0xFF); a.op('STA', 'abs', 't_five')
+    a.label('no_cf')
+    a.op('JSR', 'abs', 0x8000)
+    _filler(a, rng, blocks, 'f', 't_mix')
+    a.op('JMP', 'abs', 'main')
+    a.label('nmi')
+    _nmi_common(a)
+    _nmi_end(a)
+    a.label('irq')
+    a.op('RTI')
+    a.label('t_bank')
+    a.data(bytes(range(8)))
+    a.label('t_five')
+    a.data(bytes((5,)))
+    for name, t in (('t_pal', pal), ('t_nt', nt), ('t_oam', oam), ('t_mix', mix)):
+        a.label(name)
+        a.data(bytes(int(v) for v in t))
+    code = a.assemble()
+    assert len(code) <= 0x3FFA, len(code)
+    fixed = bytearray(16384)
+    fixed[:len(code)] = code
+    vec = (a.labels['nmi'], a.labels['reset'], a.labels['irq'])
+    fixed[0x3FFA:0x4000] = bytes(sum(((v & 0xFF, v >> 8) for v in vec), ()))
+    chr_ = rng.integers(0, 256, 8192, dtype=np.uint8).tobytes()
+    return ines(b''.join(banks) + bytes(fixed), chr_, 2, vertical=False, submapper=2 if conflicts else None)
+
+
 def mmc3_cart(seed: int = 0, blocks: int = 16, sub_blocks: int = 20) -> bytes:
     """MMC3 cartridge: 256 KB PRG (32 x 8 KB; banks 0-29 hold seeded subroutines at $8000, bank 30 at $C000 and
     bank 31 at $E000 are fixed), 128 KB random CHR, scanline IRQ split, sprite-0 split, PRG RAM use."""

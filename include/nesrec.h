@@ -36,6 +36,7 @@
 /* Boards. */
 #define NES_BOARD_NROM 0u
 #define NES_BOARD_MMC1 1u
+#define NES_BOARD_UXROM 2u                    /* 16 KB PRG bank at $8000, the last 16 KB fixed at $C000 */
 #define NES_BOARD_CNROM 3u                    /* 32 KB PRG fixed, 8 KB CHR bank latch (patch:3418) */
 #define NES_BOARD_MMC3 4u
 

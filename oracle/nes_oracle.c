@@ -50,8 +50,8 @@ int orc_parse_ines(const uint8_t* rom, uint32_t size, uint8_t* prg_buf, uint32_t
         snprintf(err, err_len, "four-screen nametables are not supported");
         return -1;
     }
-    if (mapper != 0 && mapper != 1 && mapper != 3 && mapper != 4) {
-        snprintf(err, err_len, "unsupported mapper %u (supported: 0 NROM, 1 MMC1, 3 CNROM, 4 MMC3)", mapper);
+    if (mapper > 4u) {
+        snprintf(err, err_len, "unsupported mapper %u (supported: 0 NROM, 1 MMC1, 2 UxROM, 3 CNROM, 4 MMC3)", mapper);
         return -1;
     }
     if (prg == 0 || 16u + trainer + prg + chr > size) {
@@ -75,9 +75,10 @@ int orc_parse_ines(const uint8_t* rom, uint32_t size, uint8_t* prg_buf, uint32_t
     cart->chr_size = chr ? chr : NES_CHRRAM_BYTES;
     cart->board = (uint8_t)mapper;
     cart->mirroring = (uint8_t)(rom[6] & 1u);
-    /* CNROM bus conflicts only when the header declares them: NES 2.0 (byte 7 bits 2-3 = 2), submapper 2
+    /* UxROM / CNROM bus conflicts only when the header declares them: NES 2.0 (byte 7 bits 2-3 = 2), submapper 2
      * (patch:4008, layout.bus_conflicts = mapper 3 && declared) */
-    cart->bus_conflicts = (uint8_t)(mapper == 3u && (rom[7] & 0x0Cu) == 0x08u && (rom[8] >> 4) == 2u);
+    cart->bus_conflicts =
+        (uint8_t)((mapper == 2u || mapper == 3u) && (rom[7] & 0x0Cu) == 0x08u && (rom[8] >> 4) == 2u);
     return 0;
 }
 
@@ -98,7 +99,7 @@ static void set_chr1(NesRec* r, const NesCart* c, int slot, uint32_t page) {
 }
 
 /* MMC1 registers: 0 control, 1 CHR0, 2 CHR1, 3 PRG, 4 shift, 5 shift count.
- * CNROM register: 0 the 8 KB CHR bank.
+ * UxROM register: 0 the 16 KB PRG bank at $8000. CNROM register: 0 the 8 KB CHR bank.
  * MMC3 registers: 0-7 R0-R7, 8 bank select, 9 mirroring, 10 PRG RAM protect, 11 IRQ latch, 12 IRQ counter,
  * 13 IRQ enabled, 14 IRQ reload. (patch:2917-2919, 2991-3063) */
 static void mapper_sync(NesRec* r, const NesCart* c) {
@@ -148,6 +149,14 @@ static void mapper_sync(NesRec* r, const NesCart* c) {
         set_chr1(r, c, 6 ^ f, m[4]);
         set_chr1(r, c, 7 ^ f, m[5]);
         set_nt_map(r, (m[9] & 1u) ? 0u : 1u);
+    } else if (c->board == NES_BOARD_UXROM) { /* the 16 KB bank in register 0, the last one fixed at $C000 */
+        const uint32_t last = c->prg_size / 16384u - 1u;
+        set_prg8(r, c, 0, m[0] * 2u);
+        set_prg8(r, c, 1, m[0] * 2u + 1u);
+        set_prg8(r, c, 2, last * 2u);
+        set_prg8(r, c, 3, last * 2u + 1u);
+        for (int i = 0; i < 8; ++i) set_chr1(r, c, i, (uint32_t)i);
+        set_nt_map(r, c->mirroring ? 1u : 0u);
     } else { /* NROM; CNROM: the 8 KB CHR bank in register 0 (patch:2982-2990) */
         const uint32_t chr8 = c->board == NES_BOARD_CNROM ? m[0] : 0u;
         for (int i = 0; i < 4; ++i) set_prg8(r, c, i, (uint32_t)i);
@@ -195,8 +204,8 @@ static void mapper_write(NesRec* r, const NesCart* c, uint16_t addr, uint8_t v) 
             default: m[13] = 1; return;
         }
         mapper_sync(r, c);
-    } else if (c->board == NES_BOARD_CNROM) { /* the bank latch, ANDed with the ROM byte under a bus conflict
-                                               * (patch:3124-3127, 3281-3283) */
+    } else if (c->board == NES_BOARD_CNROM || c->board == NES_BOARD_UXROM) {
+        /* the bank latch, ANDed with the ROM byte under a bus conflict (patch:3124-3127, 3281-3283) */
         const uint8_t rom = c->prg[r->prg_off[(addr >> 13) & 3u] + (addr & 0x1FFFu)];
         m[0] = c->bus_conflicts ? (uint8_t)(v & rom) : v;
         mapper_sync(r, c);

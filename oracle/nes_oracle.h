@@ -38,7 +38,7 @@ typedef struct NesCart {
     uint32_t chr_size;
     uint8_t board;         /* NES_BOARD_* */
     uint8_t mirroring;     /* header arrangement: 0 horizontal, 1 vertical */
-    uint8_t bus_conflicts; /* CNROM declared with AND-type bus conflicts (NES 2.0 submapper 2) */
+    uint8_t bus_conflicts; /* UxROM / CNROM declared with AND-type bus conflicts (NES 2.0 submapper 2) */
 } NesCart;
 
 /* iNES parse into a cart view over `rom` (PRG copied into `prg_buf` padded to a power of two).

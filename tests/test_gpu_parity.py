@@ -87,6 +87,16 @@ def test_cnrom_chr_bank_switches(conflicts):
 
 
 @pytest.mark.gpu
+@pytest.mark.parametrize('conflicts', [False, True])
+def test_uxrom_prg_bank_switches(conflicts):
+    print(f'case: UxROM seed 2, bus conflicts {conflicts}, 16 consoles, raw pads, sticky, Geometric(1/8) ends, '
+          '16 decisions', flush=True)
+    cpu, gpu = pair(16, synth.uxrom_cart(2, conflicts=conflicts), seed=23, sticky=True, idle_max=1, dropout=True,
+                    pad_mode=True, end_prob=1 / 8)
+    run(cpu, gpu, 16, 6, True)
+
+
+@pytest.mark.gpu
 def test_mmc1_from_power_on():
     print('case: MMC1 seed 3, 8 consoles, boot from power-on (CHR RAM upload in the decisions), 12 decisions',
           flush=True)

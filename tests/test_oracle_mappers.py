@@ -1,11 +1,11 @@
-"""Known-answer tests of the oracle's cartridge boards (NROM, CNROM, MMC1, MMC3) and its DMC.
+"""Known-answer tests of the oracle's cartridge boards (NROM, UxROM, CNROM, MMC1, MMC3) and its DMC.
 
 MMC3: restates the reference's register case third_party/nesle-extensions.patch:4638-4673 (R0-R7 = 00 3A 4A 5D 6E 61
 0A 04, bank select $46, $A000 = 1 on 128 KB PRG / 128 KB CHR) by writing the registers through the CPU bus, plus
 the scanline counter (reload, count down once per rendered line at dot 266, IRQ at zero, $E000 acknowledge).
 MMC1: the serial port and the bank modes written from the board's documented register meanings (16 KB PRG banks,
 4 KB CHR banks), not from the oracle's page arithmetic.
-CNROM: the bank latch and its declared AND-type bus conflicts from the board's behaviour as the reference states it
+UxROM / CNROM: the bank latch and its declared AND-type bus conflicts from the board's behaviour as the reference states it
 (patch:2982-2990, 3124-3127, 4008), checked on a cart whose PRG pages are tagged with their numbers.
 DMC: restates the sample-channel cases of patch:4105-4205 (status bit 4, 4-cycle fetch steals, loop, rate change,
 no steal in the idle fast-forward) with the same 4-cycle instruction driver as the reference test.
@@ -100,6 +100,44 @@ def test_cnrom_synthetic_cart_switches_chr(conflicts):
         log = con.words('log', 16 + 2 * 256)
         events += sum(1 for i in range(min(n, 256)) if (int(log[16 + 2 * i]) >> 24) == 7)   # NES_EV_CHR
     assert banks == {0, 1, 2, 3} and events > 0
+
+
+# ---------------------------------------------------------------------------------------------- UxROM
+
+def test_uxrom_bank_at_8000_last_bank_fixed():
+    """The 16 KB bank at $8000 is the written value, masked to the PRG size; the last 16 KB stay at $C000."""
+    con = Console(cart(2, 128, 8))
+    assert [con.read(a) for a in (0x8000, 0xA000, 0xC000, 0xE000)] == [0, 1, 14, 15]
+    con.write(0xC000, 3)                                 # no conflicts declared: ROM byte 14 does not matter
+    assert [con.read(a) for a in (0x8000, 0xA000, 0xC000, 0xE000)] == [6, 7, 14, 15]
+    con.write(0x8001, 0x0B)                              # 8 banks: 11 -> 3
+    assert pages(con)[0] == [6, 7, 14, 15] and pages(con)[1] == list(range(8))
+
+
+def test_uxrom_declared_bus_conflicts():
+    """Declared AND-type bus conflicts: the bank is value AND the ROM byte under the address."""
+    prg = bytearray(128 * KB)
+    for i in range(0, len(prg), 8 * KB):
+        prg[i] = i // (8 * KB)
+    prg[-6:] = bytes((0x10, 0xE0, 0x10, 0xE0, 0x10, 0xE0))
+    con = Console(synth.ines(bytes(prg), bytes(8 * KB), 2, submapper=2))
+    con.write(0xC000, 0x07)                              # ROM byte 14: 7 & 14 = 6
+    assert pages(con)[0] == [12, 13, 14, 15]
+    con.write(0xA000, 0x07)                              # ROM byte at $A000 = tag of page 13: 7 & 13 = 5
+    assert pages(con)[0] == [10, 11, 14, 15]
+
+
+@pytest.mark.parametrize('conflicts', [False, True])
+def test_uxrom_synthetic_cart_switches_banks(conflicts):
+    """The seed-generated UxROM cart (the GPU parity case) selects the switchable banks and calls into them."""
+    con = Console(synth.uxrom_cart(1, conflicts=conflicts))
+    t, seen = 82182, set()
+    for f in range(40):
+        con.set('pad', [0x81, 0x40, 0x02, 0xC0][f % 4])
+        assert con.run_until(t) == 0
+        t += 89342
+        seen.add(pages(con)[0][0] // 2)
+    assert len(seen) >= 4
 
 
 # ----------------------------------------------------------------------------------------------- MMC3
