@@ -23,6 +23,19 @@ typedef struct Rl10State {        /* RewardTracker */
     Rl10Signals prev;
 } Rl10State;                      /* 80 bytes */
 
+/* The game readers' own state (rl/csrc/reward10.cuh:87-101, the reader part of rl10::EnvState): what the Castlevania,
+ * Zelda, Excitebike, Contra, Final Mission, Kage, Tecmo Bowl and Punch-Out readers carry between updates. */
+typedef struct Rl10Reader {
+    uint8_t has_stage, has_floor, has_base, has_key, has_cam, has_own, has_drive, has_week;
+    uint8_t has_fight, has_prev_hp, _p0[6];
+    int32_t stage, floor_y, base_items, base_containers;
+    int32_t key_a, key_b, cam, core_max;
+    int32_t own, opp, week, fight;
+    int32_t damage, prev_hp;
+    uint32_t cells, rooms;
+    double key_d, dist, best_arc, drive_start, drive_best;
+} Rl10Reader;                     /* 120 bytes */
+
 #define RLC_RING 64
 typedef struct Dropout {
     uint64_t seed, counter;       /* the schedule's own generator */
@@ -34,9 +47,11 @@ typedef struct Dropout {
 } Dropout;                        /* 96 bytes */
 
 #ifdef __cplusplus
-static_assert(sizeof(Rl10Signals) == 40 && sizeof(Rl10State) == 80 && sizeof(Dropout) == 96, "layout");
+static_assert(sizeof(Rl10Signals) == 40 && sizeof(Rl10State) == 80 && sizeof(Dropout) == 96 &&
+              sizeof(Rl10Reader) == 120, "layout");
 #else
-_Static_assert(sizeof(Rl10Signals) == 40 && sizeof(Rl10State) == 80 && sizeof(Dropout) == 96, "layout");
+_Static_assert(sizeof(Rl10Signals) == 40 && sizeof(Rl10State) == 80 && sizeof(Dropout) == 96 &&
+               sizeof(Rl10Reader) == 120, "layout");
 #endif
 
 /* Env constants (rl/rlenv.py:34-38, rl/csrc/rlenv_core.cuh:33-38, rl/csrc/controller.cuh:24-32). */

@@ -23,6 +23,7 @@
 
 #include "nes_oracle.h"
 #include "rlenv_api.h"
+#include "rl10_games.h"
 #include "rlenv_state.h"
 
 static __thread char g_err[256];
@@ -338,6 +339,22 @@ static Rl10Update rl10_update(const uint8_t* b15, int frames, Rl10State* e) {
     return rl10_update_sig(&s, frames, e, &kSmbConsts);
 }
 
+/* RewardTracker.update for any game (rl/csrc/reward10.cuh:546-548): the game's reader on the 2 KB RAM (SMB's own
+ * above, the others in include/rl10_games.h), then the tracker with the game's constants. rd/keys/cap: the env's
+ * reader state and key set (unused by SMB). */
+static Rl10Update rl10_update_game(int game, const uint8_t* ram, int frames, Rl10State* e, Rl10Reader* rd,
+                                   uint32_t* keys, uint32_t cap) {
+    if (game == RL10_SMB) {
+        uint8_t b15[15];
+        for (int i = 0; i < 15; ++i) b15[i] = ram[kSmbAddr[i]];
+        return rl10_update(b15, frames, e);
+    }
+    const Rl10Game gc = rl10_game(game);
+    const Rl10Consts G = {gc.progress_unit, gc.score_unit, gc.stall_frames, gc.idle_per_frame, gc.death_from_lives};
+    const Rl10Signals s = rl10_observe(game, ram, e, rd, keys, cap);
+    return rl10_update_sig(&s, frames, e, &G);
+}
+
 static void gather15(const uint8_t* ram, uint8_t* b15) {
     for (int i = 0; i < 15; ++i) b15[i] = ram[kSmbAddr[i]];
 }
@@ -349,6 +366,8 @@ typedef struct Game {
     uint8_t* prg;      /* padded PRG image */
     uint8_t* rom;      /* iNES copy (CHR points into it) */
     int game, n, offset, start_ok, select_ok;
+    uint32_t kcap;     /* key-set entries per env (rl10_keyset_capacity) */
+    uint32_t* keys;    /* [n * kcap] */
     NesRec* recs;      /* n + 1 records; slot n = boot snapshot */
     NesRec* idle;      /* idle_max templates: the snapshot after k = 1..idle_max neutral frames */
     uint64_t tmpl_target;
@@ -357,6 +376,8 @@ typedef struct Game {
     int lv_cap, lv_levels;
     NesRec* lv_rec;           /* [lv_cap] */
     Rl10State* lv_st;         /* [lv_cap] */
+    Rl10Reader* lv_rd;        /* [lv_cap] */
+    uint32_t* lv_keys;        /* [lv_cap * kcap] */
     uint64_t* lv_target;      /* [lv_cap] */
     uint32_t* lv_frame;       /* [lv_cap] */
     int32_t* lv_deaths;       /* [lv_cap], -1 = nothing saved */
@@ -372,6 +393,7 @@ typedef struct Env {
     int idle_tmpl;
     /* per env */
     Rl10State* st;
+    Rl10Reader* rd;
     Dropout* drop;
     uint64_t *target, *sticky_seed, *sticky_ctr;
     uint32_t *ep_frame, *episode, *fault;
@@ -460,14 +482,19 @@ static void reset_state(Env* E, Game* g, int e) {
     }
     const int k = lv < 0 && idle <= E->idle_tmpl ? idle : 0;
     memcpy(&g->recs[e], lv >= 0 ? &g->lv_rec[lv] : k == 0 ? &g->recs[g->n] : &g->idle[k - 1], sizeof(NesRec));
+    uint32_t* keys = g->keys + (size_t)e * g->kcap;
     if (lv >= 0) {
         E->target[ge] = g->lv_target[lv];
         E->ep_frame[ge] = g->lv_frame[lv];
         E->st[ge] = g->lv_st[lv];
+        E->rd[ge] = g->lv_rd[lv];
+        memcpy(keys, g->lv_keys + (size_t)lv * g->kcap, (size_t)g->kcap * 4u);
     } else {
         E->target[ge] = g->tmpl_target + (uint64_t)k * NES_FRAME_DOTS;
         E->ep_frame[ge] = (uint32_t)k;
-        rl10_reset(&E->st[ge]);
+        rl10_reset(&E->st[ge]);   /* and the reader and its key set (reward10.cuh:531-532) */
+        memset(&E->rd[ge], 0, sizeof(Rl10Reader));
+        memset(keys, 0, (size_t)g->kcap * 4u);
     }
     if (E->ep_start) E->ep_start[ge] = lv;
     E->fault[ge] = 0;
@@ -491,9 +518,8 @@ static void write_controls(Env* E, Game* g, int ge) {
 
 static void ph_finish(Env* E, Game* g, int e) {
     const int ge = g->offset + e;
-    uint8_t b15[15];
-    gather15(g->recs[e].ram, b15);
-    const Rl10Update u = rl10_update(b15, RLE_FRAMES, &E->st[ge]);
+    const Rl10Update u = rl10_update_game(g->game, g->recs[e].ram, RLE_FRAMES, &E->st[ge], &E->rd[ge],
+                                          g->keys + (size_t)e * g->kcap, g->kcap);
     const int faulted = E->fault[ge] != 0;
     const int level_clear = !u.done && !faulted && E->episode_level_end >= 0 && (u.events & EV_LEVEL) &&
                             u.event_level == E->episode_level_end + 1;
@@ -526,7 +552,7 @@ static void ph_finish(Env* E, Game* g, int e) {
     if (E->level_out) E->level_out[ge] = E->st[ge].has_best_level ? E->st[ge].best_level : -1;
     if (E->progress_out)
         E->progress_out[ge] = E->st[ge].has_prev && E->st[ge].prev.progress_valid
-                                  ? (float)(E->st[ge].prev.progress / SMB_PROGRESS_UNIT) : NAN;
+                                  ? (float)(E->st[ge].prev.progress / rl10_game(g->game).progress_unit) : NAN;
     if (done) {
         if (E->start_out) E->start_out[ge] = E->ep_start ? E->ep_start[ge] : -1;
         float* inf = E->info + (size_t)ge * RLE_INFO;
@@ -561,9 +587,8 @@ static void ph_reset_frame(Env* E, Game* g, int e) {
 static void ph_reset_finish_controls(Env* E, Game* g, int e) {
     const int ge = g->offset + e;
     if (E->resetting[ge] != 0) {
-        uint8_t b15[15];
-        gather15(g->recs[e].ram, b15);
-        (void)rl10_update(b15, E->ep_idle[ge] + RLE_FRAMES, &E->st[ge]);
+        (void)rl10_update_game(g->game, g->recs[e].ram, E->ep_idle[ge] + RLE_FRAMES, &E->st[ge], &E->rd[ge],
+                               g->keys + (size_t)e * g->kcap, g->kcap);
         E->ep_ret[ge] = 0.0f;
         E->ep_len[ge] = 0;
         const int sl = E->ep_start ? E->ep_start[ge] : -1;   /* a place: its level is the tracker's */
@@ -620,9 +645,10 @@ static void env_free(Env* E) {
         free(E->games[i].idle);
         free(E->games[i].lv_rec); free(E->games[i].lv_st); free(E->games[i].lv_target); free(E->games[i].lv_frame);
         free(E->games[i].lv_deaths); free(E->games[i].lv_claim); free(E->games[i].lv_cdf);
+        free(E->games[i].lv_rd); free(E->games[i].lv_keys); free(E->games[i].keys);
     }
     free(E->games);
-    free(E->st); free(E->drop); free(E->target); free(E->sticky_seed); free(E->sticky_ctr);
+    free(E->st); free(E->rd); free(E->drop); free(E->target); free(E->sticky_seed); free(E->sticky_ctr);
     free(E->ep_frame); free(E->episode); free(E->fault); free(E->prev_applied); free(E->ep_ret);
     free(E->ep_len); free(E->ep_maxlvl); free(E->ep_idle); free(E->resetting); free(E->ep_start);
     free(E);
@@ -644,12 +670,15 @@ void* rlenv_create(int ngames, const int* game_ids, const uint8_t* const* roms, 
     E->gap_p32 = RLC_GAP_P32;
     for (int i = 0; i < ngames; ++i) {
         Game* g = &E->games[i];
-        if (game_ids[i] != 0) {
-            snprintf(g_err, sizeof(g_err), "game id %d: only the smb reward reader (0) is built", game_ids[i]);
+        if (game_ids[i] < 0 || game_ids[i] >= RL10_NUM_GAMES) {
+            snprintf(g_err, sizeof(g_err), "game id %d: the reward10 games are 0..%d", game_ids[i],
+                     RL10_NUM_GAMES - 1);
             env_free(E);
             return NULL;
         }
         g->game = game_ids[i];
+        g->kcap = rl10_keyset_capacity(g->game);
+        g->keys = (uint32_t*)xcalloc((size_t)n_envs[i] * g->kcap + 1u, 4);
         g->n = n_envs[i];
         g->offset = E->total;
         E->total += n_envs[i];
@@ -686,11 +715,12 @@ void* rlenv_create(int ngames, const int* game_ids, const uint8_t* const* roms, 
             target += NES_FRAME_DOTS;
             g->idle[k - 1] = tmp;
         }
-        g->start_ok = 0; /* smb: Start/Select not allowed (reward10_consts.h:28) */
-        g->select_ok = 0;
+        g->start_ok = rl10_game(g->game).start_ok;   /* reward10_consts.h:25-37 */
+        g->select_ok = rl10_game(g->game).select_ok;
     }
     const size_t N = (size_t)E->total;
     E->st = (Rl10State*)xcalloc(N, sizeof(Rl10State));
+    E->rd = (Rl10Reader*)xcalloc(N, sizeof(Rl10Reader));
     E->drop = (Dropout*)xcalloc(N, sizeof(Dropout));
     E->target = (uint64_t*)xcalloc(N, 8);
     E->sticky_seed = (uint64_t*)xcalloc(N, 8);
@@ -763,6 +793,8 @@ int rlenv_step(void* h, void* stream) {
                 const int e = (int)(cl & 0xFFFFFFFFull), ge = g->offset + e;
                 g->lv_rec[s] = g->recs[e];
                 g->lv_st[s] = E->st[ge];
+                g->lv_rd[s] = E->rd[ge];
+                memcpy(g->lv_keys + (size_t)s * g->kcap, g->keys + (size_t)e * g->kcap, (size_t)g->kcap * 4u);
                 g->lv_target[s] = E->target[ge];
                 g->lv_frame[s] = E->ep_frame[ge];
                 g->lv_deaths[s] = (int32_t)(cl >> 32);
@@ -787,6 +819,8 @@ int rlenv_enable_places(void* h, int cap, int levels) {
         g->lv_levels = levels;
         g->lv_rec = (NesRec*)xcalloc((size_t)cap, sizeof(NesRec));
         g->lv_st = (Rl10State*)xcalloc((size_t)cap, sizeof(Rl10State));
+        g->lv_rd = (Rl10Reader*)xcalloc((size_t)cap, sizeof(Rl10Reader));
+        g->lv_keys = (uint32_t*)xcalloc((size_t)cap * g->kcap + 1u, 4);
         g->lv_target = (uint64_t*)xcalloc((size_t)cap, 8);
         g->lv_frame = (uint32_t*)xcalloc((size_t)cap, 4);
         g->lv_deaths = (int32_t*)xcalloc((size_t)cap, 4);
@@ -831,6 +865,8 @@ int rlenv_place_save(void* h, int gi, const int32_t* env_idx, const int32_t* slo
         g->lv_rec[s] = g->recs[e];
         g->lv_st[s] = E->st[ge];
         g->lv_st[s].idle_frames = 0;   /* the no-progress clock restarts at a place (rlenv_core.cuh:366-375) */
+        g->lv_rd[s] = E->rd[ge];
+        memcpy(g->lv_keys + (size_t)s * g->kcap, g->keys + (size_t)e * g->kcap, (size_t)g->kcap * 4u);
         g->lv_target[s] = E->target[ge];
         g->lv_frame[s] = E->ep_frame[ge];
         g->lv_deaths[s] = 0;
@@ -848,17 +884,19 @@ int rlenv_place_copy(void* h, int gi, const int32_t* src, const int32_t* dst, in
         const int a = src[j], b = dst[j];
         g->lv_rec[b] = g->lv_rec[a];
         g->lv_st[b] = g->lv_st[a];
+        g->lv_rd[b] = g->lv_rd[a];
+        memmove(g->lv_keys + (size_t)b * g->kcap, g->lv_keys + (size_t)a * g->kcap, (size_t)g->kcap * 4u);
         g->lv_target[b] = g->lv_target[a];
         g->lv_frame[b] = g->lv_frame[a];
         g->lv_deaths[b] = g->lv_deaths[a];
     }
     return 0;
 }
-/* stride of one saved console, key words per env (none for the SMB reader), sizeof(Rl10State), cap, levels */
+/* stride of one saved console, key words per env (the game's key set), sizeof(Rl10State), cap, levels */
 void rlenv_level_layout(void* h, int gi, uint32_t* out) {
     const Game* g = &((Env*)h)->games[gi];
     out[0] = (uint32_t)sizeof(NesRec);
-    out[1] = 0;
+    out[1] = g->kcap;
     out[2] = (uint32_t)sizeof(Rl10State);
     out[3] = (uint32_t)g->lv_cap;
     out[4] = (uint32_t)g->lv_levels;
@@ -868,9 +906,13 @@ void rlenv_level_layout(void* h, int gi, uint32_t* out) {
  * the reference's order (rl/csrc/rlenv_build.hpp:253-268). */
 typedef void (*visit_fn)(void* p, size_t bytes, void* ctx);
 static void for_each_state(Env* E, visit_fn f, void* ctx) {
-    for (int i = 0; i < E->ngames; ++i) f(E->games[i].recs, sizeof(NesRec) * ((size_t)E->games[i].n + 1), ctx);
+    for (int i = 0; i < E->ngames; ++i) {
+        f(E->games[i].recs, sizeof(NesRec) * ((size_t)E->games[i].n + 1), ctx);
+        f(E->games[i].keys, (size_t)E->games[i].n * E->games[i].kcap * 4u, ctx);
+    }
     const size_t N = (size_t)E->total;
     f(E->st, N * sizeof(Rl10State), ctx);
+    f(E->rd, N * sizeof(Rl10Reader), ctx);
     f(E->drop, N * sizeof(Dropout), ctx);
     f(E->target, N * 8, ctx); f(E->ep_frame, N * 4, ctx); f(E->prev_applied, N * 2, ctx);
     f(E->sticky_seed, N * 8, ctx); f(E->sticky_ctr, N * 8, ctx); f(E->episode, N * 4, ctx);
@@ -884,6 +926,8 @@ static void for_each_state(Env* E, visit_fn f, void* ctx) {
             const size_t L = (size_t)g->lv_cap;
             f(g->lv_rec, L * sizeof(NesRec), ctx);
             f(g->lv_st, L * sizeof(Rl10State), ctx);
+            f(g->lv_rd, L * sizeof(Rl10Reader), ctx);
+            f(g->lv_keys, L * g->kcap * 4u, ctx);
             f(g->lv_target, L * 8, ctx); f(g->lv_frame, L * 4, ctx); f(g->lv_deaths, L * 4, ctx);
         }
     }
@@ -975,13 +1019,15 @@ int rl10_smb_run(const uint8_t* ram15, int T, int N, int frames, void* state, fl
 /* Test hooks with the signatures of the reference's rl/csrc/host_api.cpp:13-66. */
 int orc_rl10_replay(int game, const uint8_t* ram, int n, const int* frames, double* reward, uint8_t* done,
                     uint32_t* events, int* event_level, int* deaths, uint8_t* end_reason) {
-    if (game != 0) return -1;
+    if (game < 0 || game >= RL10_NUM_GAMES) return -1;
     Rl10State e;
+    Rl10Reader rd;
     rl10_reset(&e);
+    memset(&rd, 0, sizeof(rd));
+    const uint32_t cap = rl10_keyset_capacity(game);
+    uint32_t* keys = (uint32_t*)xcalloc(cap + 1u, 4);
     for (int i = 0; i < n; ++i) {
-        uint8_t b15[15];
-        gather15(ram + (size_t)i * 2048u, b15);
-        const Rl10Update u = rl10_update(b15, frames[i], &e);
+        const Rl10Update u = rl10_update_game(game, ram + (size_t)i * 2048u, frames[i], &e, &rd, keys, cap);
         reward[i] = u.reward;
         done[i] = (uint8_t)u.done;
         events[i] = u.events;
@@ -989,6 +1035,7 @@ int orc_rl10_replay(int game, const uint8_t* ram, int n, const int* frames, doub
         deaths[i] = e.deaths;
         end_reason[i] = e.end_reason;
     }
+    free(keys);
     return e.overflow ? 1 : 0;
 }
 void orc_pad_table(uint8_t* out) {

@@ -7,8 +7,10 @@ stored as small .npz files; the tests check the oracle (and through it the HIP l
     make -f oracle/Makefile.ref && python tests/golden/gen_golden.py
 
 Inputs: move ids and dropout inputs (exhaustive), a few schedule seeds, random (run_seed, env, episode) triples,
-the reference test's nine SMB rollback cases (rl/tests/test_reward_replay.py:122-143) and seeded SMB-style RAM
-trajectories (rl.synth.smb_ram15). Outputs are exactly what the reference functions return.
+the reference test's nine SMB rollback cases (rl/tests/test_reward_replay.py:122-143), seeded SMB-style RAM
+trajectories (rl.synth.smb_ram15) and seeded RAM trajectories of the eleven other games' readers
+(reward10_ram.py; only the outputs are stored, the tests regenerate the RAM). Outputs are exactly what the
+reference functions return.
 """
 from __future__ import annotations
 
@@ -21,6 +23,7 @@ import numpy as np
 HERE = Path(__file__).resolve().parent
 ROOT = HERE.parents[1]
 sys.path.insert(0, str(ROOT / 'ghostrun-lab_amd'))
+sys.path.insert(0, str(HERE))
 from rl import synth  # noqa: E402
 
 REF_LIB = ROOT / 'oracle' / '_ref' / 'librl_host.so'
@@ -42,16 +45,20 @@ def load():
     return lib
 
 
-def replay(lib, rams, frames):
+def replay(lib, rams, frames, game=0):
     n = len(rams)
     rams = np.ascontiguousarray(rams, np.uint8)
     frames = np.ascontiguousarray(frames, np.int32)
     out = dict(reward=np.zeros(n, np.float64), done=np.zeros(n, np.uint8), events=np.zeros(n, np.uint32),
                level=np.zeros(n, np.int32), deaths=np.zeros(n, np.int32), end=np.zeros(n, np.uint8))
-    ov = lib.rl10_replay(0, p(rams), n, p(frames), p(out['reward']), p(out['done']), p(out['events']),
+    ov = lib.rl10_replay(game, p(rams), n, p(frames), p(out['reward']), p(out['done']), p(out['events']),
                          p(out['level']), p(out['deaths']), p(out['end']))
-    assert ov == 0
+    out['overflow'] = ov
+    assert game != 0 or ov == 0
     return out
+
+
+GAME_EPISODES, GAME_STEPS = 24, 40   # per game other than SMB (reward10_ram trajectories)
 
 
 def rollback_rams():
@@ -115,6 +122,14 @@ def main():
                         rollback_done=np.stack([r['done'] for r in rb]),
                         traj=traj, frames=frames, reward=stack('reward'), done=stack('done'),
                         events=stack('events'), level=stack('level'), deaths=stack('deaths'), end=stack('end'))
+    from reward10_ram import GAMES, trajectory
+    games = {}
+    for gi, name in enumerate(GAMES[1:], start=1):
+        res = [replay(lib, *trajectory(name, ep, GAME_STEPS), game=gi) for ep in range(GAME_EPISODES)]
+        for k in ('reward', 'done', 'events', 'level', 'deaths', 'end'):
+            games[f'{name}_{k}'] = np.stack([r[k] for r in res])
+        games[f'{name}_overflow'] = np.array([r['overflow'] for r in res], np.int32)
+    np.savez_compressed(HERE / 'reward10_games.npz', episodes=GAME_EPISODES, steps=GAME_STEPS, **games)
     print('fixtures written:', sorted(x.name for x in HERE.glob('*.npz')))
 
 
