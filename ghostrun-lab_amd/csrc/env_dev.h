@@ -1,6 +1,7 @@
 // Device side of the env around the console: controller moves and pad bytes, the counter RNG, the button-dropout
-// schedule (rl/csrc/controller.cuh:41-189) and the reward10 tracker with the SMB reader
-// (rl/csrc/reward10.cuh:143-158, 546-632; constants rl/csrc/reward10_consts.h:24-39). Integer-only where the
+// schedule (rl/csrc/controller.cuh:41-189) and the reward10 tracker with the game readers (SMB's here, the other
+// eleven shared with the CPU build in include/rl10_games.h; rl/csrc/reward10.cuh:143-524, 546-632; constants
+// rl/csrc/reward10_consts.h:11-39). Integer-only where the
 // reference is, double in Python's evaluation order for the reward (built with -ffp-contract=off).
 #pragma once
 #ifndef ND_HOST_BUILD
@@ -9,6 +10,7 @@
 #include <stdint.h>
 
 #include "rlenv_state.h"
+#include "rl10_games.h"
 
 namespace ev {
 
@@ -120,14 +122,13 @@ __device__ inline void drop_advance(Dropout& s, bool on, uint32_t p32) {
     s.ring[(s.head + RLE_TIMELINE - 1) & (RLC_RING - 1)] = (int8_t)(on ? column_next(s, p32) : -1);
 }
 
-// ------------------------------------------------------------------------------------- reward10 SMB
+// ------------------------------------------------------------------------------------- reward10 tracker
 constexpr double kWProgress = 0x1.0000000000000p+0, kWLevel = 0x1.0000000000000p+0;
 constexpr double kWDeath = -0x1.999999999999ap-4, kWStall = -0x1.999999999999ap-4;
 constexpr double kWScore = 0x1.47ae147ae147bp-6, kScoreCap = 0x1.999999999999ap-4;
 constexpr double kScoreBudget = 0x1.999999999999ap-3, kWWin = 0x1.4000000000000p+2;
 constexpr double kWRollback = -0x1.47ae147ae147bp-6, kRollbackDrop = 0x1.0000000000000p-2;
-constexpr double kSmbUnit = 0x1.7700000000000p+11, kSmbScoreUnit = 0x1.9000000000000p+7;
-constexpr double kSmbStall = 0x1.c200000000000p+12, kSmbIdle = -0x1.0624dd2f1a9fcp-12;
+constexpr double kWDamage = -0x1.0000000000000p-2;
 enum : uint32_t { EV_SKIP = 1, EV_LEVEL = 2, EV_DEATH = 4, EV_WON = 8, EV_GAMEOVER = 16, EV_STALL = 32, EV_ROLLBACK = 64 };
 
 struct Out {
@@ -158,7 +159,8 @@ __device__ inline Rl10Signals smb_signals(const uint8_t* b) {
     return s;
 }
 
-__device__ inline Out smb_update(const Rl10Signals& s, int frames, Rl10State& e) {
+// RewardTracker.update (rl/csrc/reward10.cuh:546-632) with one game's constants G (reward10_consts.h:24-37).
+__device__ inline Out update(const Rl10Signals& s, int frames, Rl10State& e, const Rl10Game& G) {
     Out o = {};
     const bool had = e.has_prev != 0;
     const Rl10Signals p = e.prev;
@@ -196,7 +198,7 @@ __device__ inline Out smb_update(const Rl10Signals& s, int frames, Rl10State& e)
                 e.has_best_progress = 1;
                 e.best_progress = s.progress;
             } else if (s.progress > e.best_progress) {
-                const double gain = kWProgress * (s.progress - e.best_progress) / kSmbUnit;
+                const double gain = kWProgress * (s.progress - e.best_progress) / G.progress_unit;
                 r += gain;
                 o.part[0] += gain;
                 e.best_progress = s.progress;
@@ -206,7 +208,7 @@ __device__ inline Out smb_update(const Rl10Signals& s, int frames, Rl10State& e)
     }
     bool death = false;
     if (had) {
-        death = s.dying && !p.dying;
+        death = G.death_from_lives ? s.has_lives && p.has_lives && s.lives < p.lives : s.dying && !p.dying;
         if (death && (s.in_play || p.in_play)) {
             r += kWDeath;
             o.part[2] += kWDeath;
@@ -214,8 +216,13 @@ __device__ inline Out smb_update(const Rl10Signals& s, int frames, Rl10State& e)
             evs |= EV_DEATH;
             fresh = true;
         }
-        if (s.in_play && p.in_play && s.score > p.score) {
-            double sr = kWScore * (double)(s.score - p.score) / kSmbScoreUnit;
+        if (s.in_play && p.in_play && s.has_health && p.has_health && s.health < p.health) {
+            const double rd = kWDamage * (p.health - s.health);
+            r += rd;
+            o.part[3] += rd;
+        }
+        if (s.in_play && p.in_play && s.has_score && p.has_score && s.score > p.score) {
+            double sr = kWScore * (double)(s.score - p.score) / G.score_unit;
             if (kScoreCap < sr) sr = kScoreCap;
             const double left = kScoreBudget - e.score_used;
             if (left < sr) sr = left;
@@ -228,14 +235,14 @@ __device__ inline Out smb_update(const Rl10Signals& s, int frames, Rl10State& e)
     }
     if (had && !e.done && !death && !s.dying && !p.dying && !s.won && !s.game_over && s.in_play && p.in_play &&
         s.progress_valid && p.progress_valid && s.level == p.level && s.level == e.best_level &&
-        p.progress - s.progress >= kRollbackDrop * kSmbUnit) {
+        p.progress - s.progress >= kRollbackDrop * G.progress_unit) {
         r += kWRollback;
         o.part[6] += kWRollback;
         evs |= EV_ROLLBACK;
     }
     if (!fresh && !e.done && had && s.in_play && p.in_play && s.progress_valid && p.progress_valid &&
         s.progress <= p.progress) {
-        const double idle = kSmbIdle * frames;
+        const double idle = G.idle_per_frame * frames;
         r += idle;
         o.part[6] += idle;
     }
@@ -250,7 +257,7 @@ __device__ inline Out smb_update(const Rl10Signals& s, int frames, Rl10State& e)
         evs |= EV_GAMEOVER;
         e.done = 1;
         e.end_reason = 1;
-    } else if (!e.done && (double)e.idle_frames >= kSmbStall) {
+    } else if (!e.done && G.stall_frames >= 0.0 && (double)e.idle_frames >= G.stall_frames) {
         r += kWStall;
         o.part[6] += kWStall;
         evs |= EV_STALL;
@@ -268,6 +275,23 @@ __device__ __forceinline__ void smb_gather(const uint8_t* ram, uint8_t* b) {
     b[0] = ram[0x0E]; b[1] = ram[0x6D]; b[2] = ram[0x86]; b[3] = ram[0xB5];
     b[4] = ram[0x75A]; b[5] = ram[0x75C]; b[6] = ram[0x75F]; b[7] = ram[0x770]; b[8] = ram[0x772];
     for (int i = 0; i < 6; ++i) b[9 + i] = ram[0x7DD + i];
+}
+
+// The game's reader on one env's 2 KB RAM (rl/csrc/reward10.cuh:546-548), then the tracker. rd and keys (cap
+// entries) are the env's reader state and key set; SMB keeps neither. The game id is uniform over a launch.
+__device__ inline Out observe_update(int game, const uint8_t* ram, int frames, Rl10State& st, Rl10Reader* rd,
+                                     uint32_t* keys, uint32_t cap) {
+    Rl10Signals sig;
+    if (game == RL10_SMB) {
+        uint8_t b15[15];
+        smb_gather(ram, b15);
+        sig = smb_signals(b15);
+    } else {
+        Rl10Reader r = *rd;
+        sig = rl10_observe(game, ram, &st, &r, keys, cap);
+        *rd = r;
+    }
+    return update(sig, frames, st, rl10_game(game));
 }
 
 }  // namespace ev

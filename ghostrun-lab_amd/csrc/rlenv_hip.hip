@@ -41,6 +41,7 @@ thread_local std::string g_error;
 // ============================================================================================ kernels
 struct EnvArrays {
     Rl10State* st;
+    Rl10Reader* rd;        // [N] reader state of the game's reader (unused by SMB)
     Dropout* drop;
     uint64_t *target, *sticky_seed, *sticky_ctr;
     uint32_t *ep_frame, *episode, *fault;
@@ -73,6 +74,8 @@ struct LevelK {
     int cap, levels;                 // cap 0: off
     NesRec* rec;                     // [cap]
     Rl10State* st;                   // [cap]
+    Rl10Reader* rd;                  // [cap]
+    uint32_t* keys;                  // [cap * kcap]
     uint64_t* target;                // [cap]
     uint32_t* frame;                 // [cap]
     int32_t* deaths;                 // [cap], -1 = nothing saved
@@ -86,7 +89,9 @@ struct GameK {
     NesRec* recs;          // n + 1 records, slot n = boot snapshot
     const NesRec* idle;    // idle templates
     Cart cart;
-    int n, offset, start_ok, select_ok;
+    int n, offset, start_ok, select_ok, game;
+    uint32_t kcap;         // key-set entries per env (rl10_keyset_capacity; 0 for most games)
+    uint32_t* keys;        // [n * kcap] per-env key sets
     uint64_t tmpl_target;
     int32_t* list;         // restart list (env index within the game)
     uint32_t* list_count;
@@ -494,11 +499,13 @@ __device__ __forceinline__ void reset_rl(const GameK& g, const EnvArrays& e, con
         e.target[ge] = L.target[lv];
         e.ep_frame[ge] = L.frame[lv];
         e.st[ge] = L.st[lv];
+        e.rd[ge] = L.rd[lv];
     } else {
         const int k = idle <= s.idle_tmpl ? idle : 0;
         e.target[ge] = g.tmpl_target + (uint64_t)k * NES_FRAME_DOTS;
         e.ep_frame[ge] = (uint32_t)k;
         e.st[ge] = Rl10State{};
+        e.rd[ge] = Rl10Reader{};   // the reader and its key set restart too (rl/csrc/reward10.cuh:531-532)
     }
     if (e.ep_start) e.ep_start[ge] = lv;
     e.fault[ge] = 0;
@@ -531,11 +538,9 @@ __global__ __launch_bounds__(256) void k_finish(FinishArgs a) {
     if (valid) {
         const NesRec* rec = &a.g.recs[e];
         if (a.o.ram_hash) a.o.ram_hash[ge] = ram_hash(rec->ram);
-        uint8_t b15[15];
-        ev::smb_gather(rec->ram, b15);
-        const Rl10Signals sig = ev::smb_signals(b15);
         Rl10State st = a.e.st[ge];
-        const ev::Out u = ev::smb_update(sig, RLE_FRAMES, st);
+        const ev::Out u = ev::observe_update(a.g.game, rec->ram, RLE_FRAMES, st, &a.e.rd[ge],
+                                             a.g.keys + (size_t)e * a.g.kcap, a.g.kcap);
         a.e.st[ge] = st;
         const bool faulted = a.e.fault[ge] != 0;
         const bool level_clear = !u.done && !faulted && a.s.episode_level_end >= 0 && (u.events & ev::EV_LEVEL) &&
@@ -568,7 +573,7 @@ __global__ __launch_bounds__(256) void k_finish(FinishArgs a) {
         }
         if (a.o.level_out) a.o.level_out[ge] = st.has_best_level ? st.best_level : -1;
         if (a.o.progress_out)
-            a.o.progress_out[ge] = st.has_prev && st.prev.progress_valid ? (float)(st.prev.progress / ev::kSmbUnit)
+            a.o.progress_out[ge] = st.has_prev && st.prev.progress_valid ? (float)(st.prev.progress / rl10_game(a.g.game).progress_unit)
                                                                           : __builtin_nanf("");
         if (done) {
             if (a.o.start_out) a.o.start_out[ge] = a.e.ep_start ? a.e.ep_start[ge] : -1;
@@ -610,6 +615,10 @@ __global__ __launch_bounds__(256) void k_reset_copy(FinishArgs a) {
                                                           : t == 0 ? &a.g.recs[a.g.n] : &a.g.idle[t - 1]);
         uint4* dst = reinterpret_cast<uint4*>(&a.g.recs[e]);
         for (uint32_t i = threadIdx.x; i < NES_REC_BYTES / 16u; i += blockDim.x) dst[i] = src[i];
+        // the env's key set: the level slot's, or empty
+        uint32_t* kd = a.g.keys + (size_t)e * a.g.kcap;
+        const uint32_t* ks = lv >= 0 ? a.g.lv.keys + (size_t)lv * a.g.kcap : nullptr;
+        for (uint32_t i = threadIdx.x; i < a.g.kcap; i += blockDim.x) kd[i] = ks ? ks[i] : 0u;
     }
 }
 
@@ -620,10 +629,9 @@ __global__ __launch_bounds__(256) void k_reset_finish(FinishArgs a) {
     if (k < a.e1 - a.e0) {
         const int e = a.e0 + k, ge = a.g.offset + e;
         if (a.e.resetting[ge]) {
-            uint8_t b15[15];
-            ev::smb_gather(a.g.recs[e].ram, b15);
             Rl10State st = a.e.st[ge];
-            (void)ev::smb_update(ev::smb_signals(b15), a.e.ep_idle[ge] + RLE_FRAMES, st);
+            (void)ev::observe_update(a.g.game, a.g.recs[e].ram, a.e.ep_idle[ge] + RLE_FRAMES, st, &a.e.rd[ge],
+                                     a.g.keys + (size_t)e * a.g.kcap, a.g.kcap);
             a.e.st[ge] = st;
             a.e.ep_ret[ge] = 0.0f;
             a.e.ep_len[ge] = 0;
@@ -673,12 +681,16 @@ __global__ __launch_bounds__(256) void k_archive(FinishArgs a) {
         const uint4* src = reinterpret_cast<const uint4*>(&a.g.recs[e]);
         uint4* dst = reinterpret_cast<uint4*>(&L.rec[q]);
         for (uint32_t i = threadIdx.x; i < NES_REC_BYTES / 16u; i += blockDim.x) dst[i] = src[i];
+        const uint32_t* ks = a.g.keys + (size_t)e * a.g.kcap;
+        uint32_t* kd = L.keys + (size_t)q * a.g.kcap;
+        for (uint32_t i = threadIdx.x; i < a.g.kcap; i += blockDim.x) kd[i] = ks[i];
     }
     __syncthreads();
     if (threadIdx.x == 0) {
         if (take) {
             const int ge = a.g.offset + e;
             L.st[q] = a.e.st[ge];
+            L.rd[q] = a.e.rd[ge];
             L.target[q] = a.e.target[ge];
             L.frame[q] = a.e.ep_frame[ge];
             L.deaths[q] = (int32_t)(cl >> 32);
@@ -696,12 +708,16 @@ __global__ __launch_bounds__(256) void k_place_save(FinishArgs a, const int32_t*
     const uint4* src = reinterpret_cast<const uint4*>(&a.g.recs[e]);
     uint4* dst = reinterpret_cast<uint4*>(&L.rec[q]);
     for (uint32_t i = threadIdx.x; i < NES_REC_BYTES / 16u; i += blockDim.x) dst[i] = src[i];
+    const uint32_t* ks = a.g.keys + (size_t)e * a.g.kcap;
+    uint32_t* kd = L.keys + (size_t)q * a.g.kcap;
+    for (uint32_t i = threadIdx.x; i < a.g.kcap; i += blockDim.x) kd[i] = ks[i];
     __syncthreads();
     if (threadIdx.x == 0) {
         const int ge = a.g.offset + e;
         Rl10State st = a.e.st[ge];
         st.idle_frames = 0;
         L.st[q] = st;
+        L.rd[q] = a.e.rd[ge];
         L.target[q] = a.e.target[ge];
         L.frame[q] = a.e.ep_frame[ge];
         L.deaths[q] = 0;
@@ -779,11 +795,43 @@ __global__ __launch_bounds__(256) void k_rl10_smb(const uint8_t* __restrict__ ra
         const uint4 q = reinterpret_cast<const uint4*>(ram15)[(size_t)t * N + e];
         uint8_t b[16];
         memcpy(b, &q, 16);
-        const ev::Out u = ev::smb_update(ev::smb_signals(b), frames, st);
+        const ev::Out u = ev::update(ev::smb_signals(b), frames, st, rl10_game(RL10_SMB));
         reward[(size_t)t * N + e] = (float)u.reward;
         done[(size_t)t * N + e] = u.done ? 1 : 0;
     }
     state[e] = st;
+}
+
+// Standalone reward10 tracker of any game: one env per thread, T steps over the 2 KB RAM of each env-step.
+struct Rl10RunArgs {
+    const uint8_t* ram;
+    const int32_t* frames;
+    Rl10State* state;
+    Rl10Reader* reader;
+    uint32_t* keys;
+    double* reward;
+    uint8_t *done, *end_reason;
+    uint32_t* events;
+    int32_t *event_level, *deaths;
+    int game, T, N;
+    uint32_t cap;
+};
+__global__ __launch_bounds__(256) void k_rl10_run(Rl10RunArgs a) {
+    const int e = (int)(blockIdx.x * blockDim.x + threadIdx.x);
+    if (e >= a.N) return;
+    Rl10State st = a.state[e];
+    uint32_t* keys = a.keys ? a.keys + (size_t)e * a.cap : nullptr;
+    for (int t = 0; t < a.T; ++t) {
+        const size_t i = (size_t)t * a.N + e;
+        const ev::Out u = ev::observe_update(a.game, a.ram + i * 2048u, a.frames[i], st, &a.reader[e], keys, a.cap);
+        if (a.reward) a.reward[i] = u.reward;
+        if (a.done) a.done[i] = u.done ? 1 : 0;
+        if (a.events) a.events[i] = u.events;
+        if (a.event_level) a.event_level[i] = u.event_level;
+        if (a.deaths) a.deaths[i] = st.deaths;
+        if (a.end_reason) a.end_reason[i] = st.end_reason;
+    }
+    a.state[e] = st;
 }
 
 // ============================================================================================== host
@@ -1079,9 +1127,13 @@ void boot_game(Env& env, GameH& gh, const uint8_t* pads, size_t npads) {
 
 template <class F>
 void for_each_state(Env& env, F&& f) {
-    for (auto& gh : env.games) f(gh.k.recs, sizeof(NesRec) * ((size_t)gh.k.n + 1));
+    for (auto& gh : env.games) {
+        f(gh.k.recs, sizeof(NesRec) * ((size_t)gh.k.n + 1));
+        f(gh.k.keys, (size_t)gh.k.n * gh.k.kcap * 4u);
+    }
     const size_t N = (size_t)env.total;
     f(env.e.st, N * sizeof(Rl10State));
+    f(env.e.rd, N * sizeof(Rl10Reader));
     f(env.e.drop, N * sizeof(Dropout));
     f(env.e.target, N * 8); f(env.e.ep_frame, N * 4); f(env.e.prev_applied, N * 2); f(env.e.sticky_seed, N * 8);
     f(env.e.sticky_ctr, N * 8); f(env.e.episode, N * 4); f(env.e.ep_ret, N * 4); f(env.e.ep_len, N * 4);
@@ -1094,6 +1146,8 @@ void for_each_state(Env& env, F&& f) {
             const size_t C = (size_t)L.cap;
             f(L.rec, C * sizeof(NesRec));
             f(L.st, C * sizeof(Rl10State));
+            f(L.rd, C * sizeof(Rl10Reader));
+            f(L.keys, C * gh.k.kcap * 4u);
             f(L.target, C * 8); f(L.frame, C * 4); f(L.deaths, C * 4);
         }
     }
@@ -1133,6 +1187,7 @@ void* rlenv_create(int ngames, const int* game_ids, const uint8_t* const* roms, 
         const size_t N = (size_t)env->total;
         EnvArrays& e = env->e;
         e.st = env->mem.zeros<Rl10State>(N);
+        e.rd = env->mem.zeros<Rl10Reader>(N);
         e.drop = env->mem.zeros<Dropout>(N);
         e.target = env->mem.zeros<uint64_t>(N);
         e.sticky_seed = env->mem.zeros<uint64_t>(N);
@@ -1152,9 +1207,9 @@ void* rlenv_create(int ngames, const int* game_ids, const uint8_t* const* roms, 
         e.resetting = env->mem.zeros<uint8_t>(N);
         int offset = 0;
         for (int i = 0; i < ngames; ++i) {
-            if (game_ids[i] != 0)
-                throw std::runtime_error("game id " + std::to_string(game_ids[i]) +
-                                         ": only the smb reward reader (0) is built");
+            if (game_ids[i] < 0 || game_ids[i] >= RL10_NUM_GAMES)
+                throw std::runtime_error("game id " + std::to_string(game_ids[i]) + ": the reward10 games are 0.." +
+                                         std::to_string(RL10_NUM_GAMES - 1));
             const Parsed p = parse_ines(roms[i], rom_sizes[i]);
             GameH gh{};
             gh.game = game_ids[i];
@@ -1162,8 +1217,11 @@ void* rlenv_create(int ngames, const int* game_ids, const uint8_t* const* roms, 
             g.n = n_envs[i];
             g.offset = offset;
             offset += g.n;
-            g.start_ok = 0;   // smb: Start/Select not allowed (rl/csrc/reward10_consts.h:28)
-            g.select_ok = 0;
+            g.game = game_ids[i];
+            g.kcap = rl10_keyset_capacity(g.game);
+            g.keys = env->mem.zeros<uint32_t>((size_t)g.n * g.kcap + 1u);
+            g.start_ok = rl10_game(g.game).start_ok;   // rl/csrc/reward10_consts.h:25-37
+            g.select_ok = rl10_game(g.game).select_ok;
             // widened PRG: word i = bytes i, i+1, i+2 (the instruction window at i); a fixed NROM or CNROM image is
             // widened to 32 KB (a 16 KB one mirrored, as the CPU sees it), so that the fast path (the NROM one for
             // both: CNROM switches only CHR) indexes it by address & $7FFF
@@ -1329,6 +1387,8 @@ int rlenv_enable_places(void* h, int cap, int levels) {
             L.levels = levels;
             L.rec = env.mem.zeros<NesRec>((size_t)cap);
             L.st = env.mem.zeros<Rl10State>((size_t)cap);
+            L.rd = env.mem.zeros<Rl10Reader>((size_t)cap);
+            L.keys = env.mem.zeros<uint32_t>((size_t)cap * gh.k.kcap + 1u);
             L.target = env.mem.zeros<uint64_t>((size_t)cap);
             L.frame = env.mem.zeros<uint32_t>((size_t)cap);
             L.deaths = env.mem.zeros<int32_t>((size_t)cap);
@@ -1389,7 +1449,8 @@ int rlenv_place_save(void* h, int gi, const int32_t* env_idx, const int32_t* slo
 int rlenv_place_copy(void* h, int gi, const int32_t* src, const int32_t* dst, int count, void* stream) {
     Env& env = *static_cast<Env*>(h);
     if (gi < 0 || gi >= (int)env.games.size()) { g_error = "place_copy: bad game"; return 1; }
-    const LevelK& L = env.games[gi].k.lv;
+    const GameK& g = env.games[gi].k;
+    const LevelK& L = g.lv;
     const hipStream_t s = static_cast<hipStream_t>(stream);
     int bad = 0;
     for (int i = 0; i < count; ++i) {
@@ -1403,6 +1464,8 @@ int rlenv_place_copy(void* h, int gi, const int32_t* src, const int32_t* dst, in
         };
         d2d(L.rec + b, L.rec + a, sizeof(NesRec));
         d2d(L.st + b, L.st + a, sizeof(Rl10State));
+        d2d(L.rd + b, L.rd + a, sizeof(Rl10Reader));
+        if (g.kcap) d2d(L.keys + b * g.kcap, L.keys + a * g.kcap, (size_t)g.kcap * 4u);
         d2d(L.target + b, L.target + a, 8);
         d2d(L.frame + b, L.frame + a, 4);
         d2d(L.deaths + b, L.deaths + a, 4);
@@ -1415,7 +1478,7 @@ void rlenv_level_layout(void* h, int gi, uint32_t* out) {
     const Env& env = *static_cast<Env*>(h);
     const LevelK& L = env.games[gi].k.lv;
     out[0] = (uint32_t)sizeof(NesRec);
-    out[1] = 0;   // key words per env: the SMB reader keeps none
+    out[1] = env.games[gi].k.kcap;   // key words per env (the game's key set)
     out[2] = (uint32_t)sizeof(Rl10State);
     out[3] = (uint32_t)L.cap;
     out[4] = (uint32_t)L.levels;
@@ -1504,6 +1567,23 @@ int rl10_smb_run(const uint8_t* ram15, int T, int N, int frames, void* state, fl
         hipLaunchKernelGGL(k_rl10_smb, dim3((N + 255) / 256), dim3(256), 0, static_cast<hipStream_t>(stream), ram15, T, N,
                            frames, static_cast<Rl10State*>(state), reward, done);
     return check("rl10_smb_run");
+}
+
+int rl10_run(int game, const uint8_t* ram, int T, int N, const int32_t* frames, void* state, void* reader,
+             uint32_t* keys, double* reward, uint8_t* done, uint32_t* events, int32_t* event_level, int32_t* deaths,
+             uint8_t* end_reason, void* stream) {
+    if (game < 0 || game >= RL10_NUM_GAMES || T < 0 || N < 0 || (N > 0 && T > 0 && (!ram || !frames || !state ||
+        !reader || (rl10_keyset_capacity(game) > 0 && !keys)))) {
+        g_error = "rl10_run: bad game id, size or buffer";
+        return 1;
+    }
+    if (N > 0 && T > 0) {
+        const Rl10RunArgs a{ram, frames, static_cast<Rl10State*>(state), static_cast<Rl10Reader*>(reader), keys,
+                            reward, done, end_reason, events, event_level, deaths, game, T, N,
+                            rl10_keyset_capacity(game)};
+        hipLaunchKernelGGL(k_rl10_run, dim3((N + 255) / 256), dim3(256), 0, static_cast<hipStream_t>(stream), a);
+    }
+    return check("rl10_run");
 }
 
 }  // extern "C"

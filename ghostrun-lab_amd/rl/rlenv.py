@@ -40,6 +40,7 @@ PART_NAMES = ('progress', 'level', 'death', 'damage', 'score', 'win', 'stall')  
 NUM_PARTS = len(PART_NAMES)
 END_NAMES = {0: 'none', 1: 'game_over', 2: 'won', 3: 'skip', 4: 'stall', 5: 'fault', 6: 'level_clear', 7: 'synthetic'}
 NES_REC_BYTES = 23552   # include/nesrec.h
+READER_BYTES = 120      # sizeof(Rl10Reader), include/rlenv_state.h
 
 
 def _load(path: Path):
@@ -78,6 +79,7 @@ def _load(path: Path):
     lib.rl_pack6.argtypes = [P, P, SZ, P]
     lib.rl_unpack6.argtypes = [P, P, SZ, P]
     lib.rl10_smb_run.argtypes = [P, I, I, I, P, P, P, P]
+    lib.rl10_run.argtypes = [I, P, I, I] + [P] * 11
     if hasattr(lib, 'rl_gather_rows'):  # GPU build only
         lib.rl_host_alloc.restype = P
         lib.rl_host_alloc.argtypes = [SZ]
@@ -242,11 +244,12 @@ class RlEnv:
 
     def _archive_sizes(self, cap):
         """Byte sizes of the level-start tail of the state blob per game for `cap` slots: saved consoles, trackers,
-        key words, targets, frames, deaths (the order the library saves them in)."""
+        reader states, key words, targets, frames, deaths (the order the library saves them in)."""
         out = []
         for gi in range(len(self.games)):
             lay = self.level_layout(gi)
-            out.append([cap * lay['stride'], cap * lay['st'], cap * lay['key_cap'] * 4, cap * 8, cap * 4, cap * 4])
+            out.append([cap * lay['stride'], cap * lay['st'], cap * READER_BYTES, cap * lay['key_cap'] * 4, cap * 8,
+                        cap * 4, cap * 4])
         return out
 
     def _grow_archive(self, buf, old_cap, need):
@@ -261,7 +264,7 @@ class RlEnv:
             for k, (a, b) in enumerate(zip(so, sn)):
                 parts.append(buf[o:o + a])
                 o += a
-                parts.append(np.full(b - a, 0xFF if k == 5 else 0, np.uint8))   # deaths -1 = empty
+                parts.append(np.full(b - a, 0xFF if k == 6 else 0, np.uint8))   # deaths -1 = empty
         return np.concatenate(parts)
 
     def _sync(self):

@@ -12,6 +12,8 @@ cartridges generated here from a seed:
 * ``smb_like_cart(seed)`` - NROM-128 that writes the RAM bytes the SMB reward reader reads (position, level,
   lives, score, dying, mode) from the pad, idling in a JMP-to-self loop with its logic in the NMI as SMB does,
   so rewards, deaths, level changes, game over and the idle fast-forward all run.
+* ``spec_cart(spec, seed)`` - NROM-128 that writes the RAM bytes a game's reward reader reads, from a spec of
+  value lists and pad-driven walks, in its NMI (any of the twelve reward10 games).
 * ``smb_ram15(seed, n_envs, steps)`` - per env-step the 15 RAM bytes the SMB reward reader reads (x position as a
   +-1..4 px random walk with 5% rollback jumps, world/level advancing with p 1e-3, lives lost with p 5e-4, BCD-like
   score digits), packed as ``rl10_smb_run`` takes them.
@@ -649,6 +651,102 @@ def smb_like_cart(seed: int = 0) -> bytes:
     for name, t in (('t_pal', pal), ('t_nt', nt), ('t_oam', oam), ('t_mix', mix)):
         a.label(name)
         a.data(bytes(int(v) for v in t))
+    code = a.assemble()
+    prg = bytearray(16384)
+    prg[:len(code)] = code
+    vec = (a.labels['nmi'], a.labels['reset'], a.labels['irq'])
+    prg[0x3FFA:0x4000] = bytes(sum(((v & 0xFF, v >> 8) for v in vec), ()))
+    chr_ = rng.integers(0, 256, 8192, dtype=np.uint8).tobytes()
+    return ines(bytes(prg), chr_, 0, vertical=True)
+
+
+SPEC_PAD, SPEC_PTR, SPEC_RNG = 0xE0, 0xE2, 0xE4   # zero page of spec_cart (no reward reader reads $E0-$E7)
+
+
+def spec_cart(spec: dict, seed: int = 0) -> bytes:
+    """NROM-128 cartridge that drives a reward reader's RAM bytes from the pad, so a game's reader (any of the
+    reward10 games) sees play, deaths, level changes and game overs inside the env. spec: RAM address -> list of
+    values, or ('walk', lo, hi, step). The main loop idles; each NMI does OAM DMA, reads the pad into $E0 and
+    visits the spec entries in order: a list entry takes a value drawn from its list with p ~1/32 per frame (a
+    16-bit xorshift at $E4/$E5, its low byte mixed with the pad each frame, draws); a walk moves by its step
+    towards hi while Right is held, towards lo while Left is held, else one random step with p 1/8, clamped to
+    [lo, hi]."""
+    rng = np.random.default_rng([0x53504543, seed])
+    pal, nt, oam, _ = _tables(rng)
+    entries = sorted(spec.items())
+    assert 0 < len(entries) <= 255 and all(not (0xE0 <= a <= 0xE7) and a < 0x800 for a, _ in entries)
+    lo_t, hi_t, kind_t, ta, tb, tc, pool = [], [], [], [], [], [], []
+    for addr, c in entries:
+        lo_t.append(addr & 0xFF)
+        hi_t.append(addr >> 8)
+        if isinstance(c, list):
+            assert 0 < len(c) <= 16
+            kind_t.append(0); ta.append(len(c)); tb.append(len(pool)); tc.append(0)
+            pool += c
+        else:
+            _, lo, hi, step = c
+            kind_t.append(1); ta.append(lo); tb.append(hi); tc.append(step)
+    assert len(pool) + 16 <= 256
+    a = Asm(0xC000)
+    a.label('reset')
+    _reset_common(a, 0x90, dict(pal='t_pal', nt='t_nt', oam='t_oam'))
+    a.op('LDA', 'imm', 0x5A); a.op('STA', 'zp', SPEC_RNG); a.op('LDA', 'imm', 0xC3); a.op('STA', 'zp', SPEC_RNG + 1)
+    for addr, c in entries:
+        a.op('LDA', 'imm', c[0] if isinstance(c, list) else (c[1] + c[2]) // 2); a.op('STA', 'abs', addr)
+    a.label('idle')
+    a.op('JMP', 'abs', 'idle')
+    a.label('rng')   # 16-bit xorshift (7, 9, 8) at $E4/$E5; A = the high byte
+    a.op('LDA', 'zp', SPEC_RNG + 1); a.op('LSR', 'acc'); a.op('LDA', 'zp', SPEC_RNG); a.op('ROR', 'acc')
+    a.op('EOR', 'zp', SPEC_RNG + 1); a.op('STA', 'zp', SPEC_RNG + 1); a.op('ROR', 'acc'); a.op('EOR', 'zp', SPEC_RNG)
+    a.op('STA', 'zp', SPEC_RNG); a.op('EOR', 'zp', SPEC_RNG + 1); a.op('STA', 'zp', SPEC_RNG + 1); a.op('RTS')
+    a.label('nmi')
+    a.op('PHA'); a.op('TXA'); a.op('PHA'); a.op('TYA'); a.op('PHA')
+    a.op('LDA', 'imm', 0); a.op('STA', 'abs', 0x2003); a.op('LDA', 'imm', OAM_PAGE >> 8); a.op('STA', 'abs', 0x4014)
+    a.op('LDA', 'imm', 1); a.op('STA', 'abs', 0x4016); a.op('LDA', 'imm', 0); a.op('STA', 'abs', 0x4016)
+    a.op('LDX', 'imm', 8)
+    a.label('sprd')
+    a.op('LDA', 'abs', 0x4016); a.op('LSR', 'acc'); a.op('ROR', 'zp', SPEC_PAD); a.op('DEX'); a.op('BNE', 'rel', 'sprd')
+    a.op('LDA', 'zp', SPEC_RNG); a.op('EOR', 'zp', SPEC_PAD); a.op('STA', 'zp', SPEC_RNG); a.op('ORA', 'zp', SPEC_RNG + 1)
+    a.op('BNE', 'rel', 'seed_ok'); a.op('INC', 'zp', SPEC_RNG)   # the all-zero state would stay zero
+    a.label('seed_ok')
+    a.op('LDX', 'imm', 0)
+    a.label('ent')
+    a.op('LDA', 'abx', 't_lo'); a.op('STA', 'zp', SPEC_PTR); a.op('LDA', 'abx', 't_hi'); a.op('STA', 'zp', SPEC_PTR + 1)
+    a.op('LDA', 'abx', 't_kind'); a.op('BNE', 'rel', 'walk')
+    # list: p 1/32, then an index below the list length (drawn in 0..15, out of range = no change)
+    a.op('JSR', 'abs', 'rng'); a.op('AND', 'imm', 31); a.op('BNE', 'rel', 'next_n')
+    a.op('JSR', 'abs', 'rng'); a.op('AND', 'imm', 15); a.op('CMP', 'abx', 't_a'); a.op('BCS', 'rel', 'next_n')
+    a.op('CLC'); a.op('ADC', 'abx', 't_b'); a.op('TAY'); a.op('LDA', 'aby', 't_pool'); a.op('JMP', 'abs', 'store')
+    a.label('next_n')
+    a.op('JMP', 'abs', 'next')
+    a.label('walk')
+    a.op('LDY', 'imm', 0)
+    a.op('LDA', 'zp', SPEC_PAD); a.op('AND', 'imm', 0x80); a.op('BNE', 'rel', 'up')
+    a.op('LDA', 'zp', SPEC_PAD); a.op('AND', 'imm', 0x40); a.op('BNE', 'rel', 'down')
+    a.op('JSR', 'abs', 'rng'); a.op('AND', 'imm', 7); a.op('BNE', 'rel', 'next_n')
+    a.op('JSR', 'abs', 'rng'); a.op('AND', 'imm', 1); a.op('BEQ', 'rel', 'down')
+    a.label('up')
+    a.op('LDY', 'imm', 0); a.op('LDA', 'izy', SPEC_PTR); a.op('CLC'); a.op('ADC', 'abx', 't_c'); a.op('BCS', 'rel', 'to_hi')
+    a.op('CMP', 'abx', 't_b'); a.op('BCC', 'rel', 'store'); a.op('BEQ', 'rel', 'store')
+    a.label('to_hi')
+    a.op('LDA', 'abx', 't_b'); a.op('JMP', 'abs', 'store')
+    a.label('down')
+    a.op('LDY', 'imm', 0); a.op('LDA', 'izy', SPEC_PTR); a.op('SEC'); a.op('SBC', 'abx', 't_c'); a.op('BCC', 'rel', 'to_lo')
+    a.op('CMP', 'abx', 't_a'); a.op('BCS', 'rel', 'store')
+    a.label('to_lo')
+    a.op('LDA', 'abx', 't_a')
+    a.label('store')
+    a.op('LDY', 'imm', 0); a.op('STA', 'izy', SPEC_PTR)
+    a.label('next')
+    a.op('INX'); a.op('CPX', 'imm', len(entries)); a.op('BEQ', 'rel', 'out'); a.op('JMP', 'abs', 'ent')
+    a.label('out')
+    _nmi_end(a)
+    a.label('irq')
+    a.op('RTI')
+    for name, t in (('t_pal', pal), ('t_nt', nt), ('t_oam', oam), ('t_lo', lo_t), ('t_hi', hi_t),
+                    ('t_kind', kind_t), ('t_a', ta), ('t_b', tb), ('t_c', tc), ('t_pool', pool + [0] * 16)):
+        a.label(name)
+        a.data(bytes(int(v) & 0xFF for v in t))
     code = a.assemble()
     prg = bytearray(16384)
     prg[:len(code)] = code

@@ -110,6 +110,17 @@ int rlenv_kernel_times(void* h, double* ms, int64_t* count, int n);
 int rl10_smb_run(const uint8_t* ram15, int T, int N, int frames, void* state, float* reward, uint8_t* done,
                  void* stream);
 
+/* The reward10 tracker of any game (ids as in rlenv_create) on device RAM: T steps of N envs, one env per thread.
+ * ram: u8 [T, N, 2048] device, the 2 KB RAM of each env-step; frames: i32 [T, N] emulated frames per step;
+ * state: Rl10State [N], reader: Rl10Reader [N] (include/rlenv_state.h) and keys: u32 [N * cap], cap =
+ * rl10_keyset_capacity(game) (include/rl10_games.h; keys may be null when it is 0), all zeroed for a fresh env and
+ * updated in place; a key set that fills sets state.overflow, as rl10_replay's nonzero return.
+ * Outputs [T, N]: reward f64, done u8, events u32, event_level i32, deaths i32 and end_reason u8 (the tracker's
+ * after each step; any output may be null). Follows rl/csrc/host_api.cpp:13-31 (rl10_replay) for N envs at once. */
+int rl10_run(int game, const uint8_t* ram, int T, int N, const int32_t* frames, void* state, void* reader,
+             uint32_t* keys, double* reward, uint8_t* done, uint32_t* events, int32_t* event_level, int32_t* deaths,
+             uint8_t* end_reason, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -1016,6 +1016,35 @@ int rl10_smb_run(const uint8_t* ram15, int T, int N, int frames, void* state, fl
     return 0;
 }
 
+/* The tracker of any game over T steps of N envs (include/rlenv_api.h rl10_run), host buffers. */
+int rl10_run(int game, const uint8_t* ram, int T, int N, const int32_t* frames, void* state, void* reader,
+             uint32_t* keys, double* reward, uint8_t* done, uint32_t* events, int32_t* event_level, int32_t* deaths,
+             uint8_t* end_reason, void* stream) {
+    (void)stream;
+    const uint32_t cap = game >= 0 && game < RL10_NUM_GAMES ? rl10_keyset_capacity(game) : 0u;
+    if (game < 0 || game >= RL10_NUM_GAMES || T < 0 || N < 0 ||
+        (N > 0 && T > 0 && (!ram || !frames || !state || !reader || (cap > 0 && !keys)))) {
+        snprintf(g_err, sizeof(g_err), "rl10_run: bad game id, size or buffer");
+        return 1;
+    }
+    Rl10State* st = (Rl10State*)state;
+    Rl10Reader* rd = (Rl10Reader*)reader;
+#pragma omp parallel for schedule(static)
+    for (int e = 0; e < N; ++e)
+        for (int t = 0; t < T; ++t) {
+            const size_t i = (size_t)t * N + e;
+            const Rl10Update u = rl10_update_game(game, ram + i * 2048u, frames[i], &st[e], &rd[e],
+                                                  keys ? keys + (size_t)e * cap : NULL, cap);
+            if (reward) reward[i] = u.reward;
+            if (done) done[i] = (uint8_t)u.done;
+            if (events) events[i] = u.events;
+            if (event_level) event_level[i] = u.event_level;
+            if (deaths) deaths[i] = st[e].deaths;
+            if (end_reason) end_reason[i] = st[e].end_reason;
+        }
+    return 0;
+}
+
 /* Test hooks with the signatures of the reference's rl/csrc/host_api.cpp:13-66. */
 int orc_rl10_replay(int game, const uint8_t* ram, int n, const int* frames, double* reward, uint8_t* done,
                     uint32_t* events, int* event_level, int* deaths, uint8_t* end_reason) {

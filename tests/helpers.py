@@ -60,6 +60,7 @@ def oracle():
         lib.rl_pack6.argtypes = [P, P, ctypes.c_size_t, P]
         lib.rl_unpack6.argtypes = [P, P, ctypes.c_size_t, P]
         lib.rl10_smb_run.argtypes = [P, I, I, I, P, P, P, P]
+        lib.rl10_run.argtypes = [I, P, I, I] + [P] * 11
         _oracle = lib
     return _oracle
 

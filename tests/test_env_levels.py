@@ -18,7 +18,7 @@ import torch
 
 from helpers import ORACLE_LIB, Console, ptr
 from rl import synth
-from rl.rlenv import RlEnv
+from rl.rlenv import READER_BYTES, RlEnv
 
 RIGHT, LEFT, DOWN, A = 128, 64, 32, 1
 REC = 23552
@@ -34,10 +34,12 @@ def env(n, **kw):
 
 def archive(e, gi=0):
     """The level-start tail of the state blob: (records [cap, REC], tracker bytes [cap, 80], targets, frames,
-    deaths), parsed with the library's own layout (rl/csrc/rlenv_build.hpp:269-279 order)."""
+    deaths), parsed with the library's own layout (rl/csrc/rlenv_build.hpp:269-279 order, with the reader states
+    after the trackers)."""
     lay = e.level_layout(gi)
     cap = lay['cap']
-    sizes = [cap * lay['stride'], cap * lay['st'], cap * lay['key_cap'] * 4, cap * 8, cap * 4, cap * 4]
+    sizes = [cap * lay['stride'], cap * lay['st'], cap * READER_BYTES, cap * lay['key_cap'] * 4, cap * 8, cap * 4,
+             cap * 4]
     blob = e.state_dict()['env']
     tail = blob[len(blob) - sum(sizes):]
     parts, o = [], 0
@@ -45,7 +47,7 @@ def archive(e, gi=0):
         parts.append(tail[o:o + s])
         o += s
     return (parts[0].reshape(cap, lay['stride']), parts[1].reshape(cap, lay['st']),
-            parts[3].view(np.uint64), parts[4].view(np.uint32), parts[5].view(np.int32))
+            parts[4].view(np.uint64), parts[5].view(np.uint32), parts[6].view(np.int32))
 
 
 def drive(e, pads_of, steps):

@@ -51,3 +51,64 @@ def test_fixtures_exercise_the_readers():
         assert (r > 0).any() and (r < 0).any(), game
         assert (ev & 4).any(), f'{game}: no death event'        # kEvDeath
         assert len(set(end[:, -1].tolist())) >= 2, f'{game}: one end kind only'
+
+
+STATE_BYTES, READER_BYTES = 80, 120   # sizeof(Rl10State), sizeof(Rl10Reader) (include/rlenv_state.h)
+
+
+def batch(game):
+    """The fixture's episodes of `game` as one batch: RAM [T, N, 2048], frames [T, N]."""
+    E, T = int(FIX['episodes']), int(FIX['steps'])
+    tr = [trajectory(game, ep, T) for ep in range(E)]
+    return (np.ascontiguousarray(np.stack([r for r, _ in tr], 1)),
+            np.ascontiguousarray(np.stack([f for _, f in tr], 1).astype(np.int32)))
+
+
+def run_batched(lib, gi, ram, frames, cap):
+    """rl10_run over [T, N] of host arrays; outputs transposed to [N, T] like the fixtures."""
+    T, N = frames.shape
+    st = np.zeros(N * STATE_BYTES, np.uint8)
+    rd = np.zeros(N * READER_BYTES, np.uint8)
+    keys = np.zeros(N * cap + 1, np.uint32)
+    out = dict(reward=np.zeros((T, N), np.float64), done=np.zeros((T, N), np.uint8),
+               events=np.zeros((T, N), np.uint32), level=np.zeros((T, N), np.int32),
+               deaths=np.zeros((T, N), np.int32), end=np.zeros((T, N), np.uint8))
+    assert lib.rl10_run(gi, p(ram), T, N, p(frames), p(st), p(rd), p(keys), p(out['reward']), p(out['done']),
+                        p(out['events']), p(out['level']), p(out['deaths']), p(out['end']), None) == 0
+    return {k: v.T for k, v in out.items()}
+
+
+KEY_CAP = {'castlevania': 4096, 'zelda': 16384}   # rl10_keyset_capacity (reward10.cuh:527-529)
+
+
+def test_batched_run_matches_reference_replay():
+    """rl10_run (one env per episode, all episodes of a game in one call) equals the reference's per-episode
+    rl10_replay outputs for every game, and rejects a bad game id and a missing key buffer."""
+    lib = oracle()
+    lib.rl10_run.argtypes = [ctypes.c_int, ctypes.c_void_p, ctypes.c_int, ctypes.c_int] + [ctypes.c_void_p] * 11
+    for game in GAMES[1:]:
+        gi = GAMES.index(game)
+        ram, frames = batch(game)
+        out = run_batched(lib, gi, ram, frames, KEY_CAP.get(game, 0))
+        for k in out:
+            np.testing.assert_array_equal(out[k], FIX[f'{game}_{k}'], err_msg=f'{game}: {k}')
+    ram, frames = batch('pacman')
+    z = np.zeros(4096, np.uint8)
+    assert lib.rl10_run(12, p(ram), 1, 1, p(frames), p(z), p(z), None, None, None, None, None, None, None, None) != 0
+    assert lib.rl10_run(GAMES.index('zelda'), p(ram), 1, 1, p(frames), p(z), p(z), None, None, None, None, None, None,
+                        None, None) != 0
+
+
+def test_batched_run_smb_matches_reference_fixture():
+    """SMB through rl10_run on the full 2 KB RAM equals the reference's SMB replay fixture."""
+    from rl import synth
+    lib = oracle()
+    lib.rl10_run.argtypes = [ctypes.c_int, ctypes.c_void_p, ctypes.c_int, ctypes.c_int] + [ctypes.c_void_p] * 11
+    gold = np.load(GOLDEN / 'reward10_smb.npz')
+    ram = np.ascontiguousarray(synth.expand_ram(gold['traj']))            # [T, N, 2048]
+    T, N = ram.shape[:2]
+    frames = np.ascontiguousarray(np.repeat(gold['frames'][:, None], N, 1).astype(np.int32))
+    out = run_batched(lib, 0, ram, frames, 0)
+    for k, g in (('reward', 'reward'), ('done', 'done'), ('events', 'events'), ('level', 'level'),
+                 ('deaths', 'deaths'), ('end', 'end')):
+        np.testing.assert_array_equal(out[k].T, gold[g], err_msg=k)
