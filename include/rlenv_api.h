@@ -20,8 +20,10 @@ extern "C" {
 
 /* Builds every game's boot snapshot (power-on, RAM 0xFF, the boot pad bytes frame by frame) and idle
  * templates, and allocates n+1 console records per game (slot n = boot snapshot).
- * Replaces rl/csrc/rlenv_api.h:10-12 (rlenv.cu:188-217). game_ids: reward10 game ids (0 = smb; the only
- * reward reader built). roms: iNES images (mappers 0-4). device: HIP device index. */
+ * Replaces rl/csrc/rlenv_api.h:10-12 (rlenv.cu:188-217). game_ids: reward10 game ids 0..11 (smb, pacman,
+ * excitebike, contra, castlevania, gradius, zelda, tetris, tecmobowl, kage, finalmission, punchout; the order of
+ * rl/games_manifest.json), each choosing the reward reader and the Start/Select legality. roms: iNES images
+ * (mappers 0-4). device: HIP device index. */
 void* rlenv_create(int ngames, const int* game_ids, const uint8_t* const* roms, const size_t* rom_sizes,
                    const uint8_t* const* boot_pads, const size_t* boot_sizes, const int* n_envs, uint64_t run_seed,
                    int sticky, int idle_max, int dropout, int device);
