@@ -12,6 +12,8 @@ cartridges generated here from a seed:
 * ``smb_like_cart(seed)`` - NROM-128 that writes the RAM bytes the SMB reward reader reads (position, level,
   lives, score, dying, mode) from the pad, idling in a JMP-to-self loop with its logic in the NMI as SMB does,
   so rewards, deaths, level changes, game over and the idle fast-forward all run.
+* ``mmc2_cart(seed)`` - MMC2 (mapper 9): 128 KB PRG in 8 KB banks, 128 KB CHR ROM, nametables and sprites rich in
+  the latch tiles $FD/$FE, CHR bank and mirroring rewrites, CPU-driven latch flips through $2006/$2007.
 * ``spec_cart(spec, seed)`` - NROM-128 that writes the RAM bytes a game's reward reader reads, from a spec of
   value lists and pad-driven walks, in its NMI (any of the twelve reward10 games).
 * ``smb_ram15(seed, n_envs, steps)`` - per env-step the 15 RAM bytes the SMB reward reader reads (x position as a
@@ -578,6 +580,77 @@ def mmc1_cart(seed: int = 0, blocks: int = 16, sub_blocks: int = 16) -> bytes:
     vec = (a.labels['nmi'], a.labels['reset'], a.labels['irq'])
     fixed[0x3FFA:0x4000] = bytes(sum(((v & 0xFF, v >> 8) for v in vec), ()))
     return ines(b''.join(banks) + bytes(fixed), b'', 1, vertical=True)
+
+
+def mmc2_cart(seed: int = 0, blocks: int = 12, sub_blocks: int = 12) -> bytes:
+    """MMC2 (mapper 9) cartridge: 128 KB PRG in 8 KB banks (0-12 switched in at $8000, the last three fixed at
+    $A000-$FFFF), 128 KB CHR ROM in 4 KB banks. The nametables and sprites use tiles $FD and $FE often, so the
+    renderer's fetches flip the latches of both pattern halves mid-line; the main loop calls a subroutine in the
+    $8000 bank, rewrites the four CHR bank registers and the mirroring now and then, swaps the background and
+    sprite pattern halves, and reads $0FD8/$0FE8/$1FD8/$1FE8 through $2006/$2007 (CPU-driven latch flips)."""
+    rng = np.random.default_rng([0x4D4D4332, seed])
+    pal, nt, oam, mix = _tables(rng)
+    trig = rng.random(256) < 0.12
+    nt[trig] = rng.choice(np.array([0xFD, 0xFE]), int(trig.sum()))
+    tiles = oam[1::4]
+    st = rng.random(64) < 0.3
+    tiles[st] = rng.choice(np.array([0xFD, 0xFE]), int(st.sum()))
+    oam[1::4] = tiles
+    banks = []
+    for b in range(13):   # switchable: a subroutine at $8000, a table at $9F00
+        sub = Asm(0x8000)
+        _filler(sub, rng, sub_blocks, f'b{b}', 0x9F00)
+        sub.op('RTS')
+        body = sub.assemble()
+        assert len(body) <= 0x1F00, len(body)
+        page = bytearray(8192)
+        page[:len(body)] = body
+        page[0x1F00:0x2000] = rng.integers(0, 256, 256, dtype=np.uint8).tobytes()
+        banks.append(bytes(page))
+    a = Asm(0xC000)
+    tables = dict(pal='t_pal', nt='t_nt', oam='t_oam')
+    a.label('reset')
+    _reset_common(a, 0x90, tables)                                        # NMI on, BG at $1000, sprites at $0000
+    a.label('main')
+    _read_pad(a, 'm')
+    _pad_moves(a, 't_mix')
+    a.op('LDA', 'zp', CNT_LO); a.op('EOR', 'zp', PAD); a.op('AND', 'imm', 0x07); a.op('STA', 'zp', BANK)
+    a.op('STA', 'abs', 0xA000); a.op('JSR', 'abs', 0x8000)
+    _filler(a, rng, blocks, 'f', 't_mix')
+    a.op('LDA', 'zp', CNT_LO); a.op('AND', 'imm', 0x0F); a.op('BNE', 'rel', 'no_chr')
+    a.op('LDA', 'zp', CNT_HI); a.op('EOR', 'zp', PX)
+    for k, reg in enumerate((0xB000, 0xC000, 0xD000, 0xE000)):
+        a.op('STA', 'abs', reg); a.op('CLC'); a.op('ADC', 'imm', 7 + 2 * k)
+    a.label('no_chr')
+    a.op('LDA', 'zp', CNT_LO); a.op('AND', 'imm', 0x1F); a.op('CMP', 'imm', 5); a.op('BNE', 'rel', 'no_mir')
+    a.op('LDA', 'zp', CNT_HI); a.op('STA', 'abs', 0xF000)
+    a.label('no_mir')
+    a.op('LDA', 'zp', CNT_LO); a.op('AND', 'imm', 0x3F); a.op('CMP', 'imm', 9); a.op('BNE', 'rel', 'no_swap')
+    a.op('LDA', 'zp', CTRL_SHADOW); a.op('EOR', 'imm', 0x18); a.op('STA', 'zp', CTRL_SHADOW)   # swap the halves
+    a.label('no_swap')
+    a.op('LDA', 'zp', CNT_LO); a.op('AND', 'imm', 0x0F); a.op('CMP', 'imm', 3); a.op('BNE', 'rel', 'no_cpu')
+    a.op('LDA', 'abs', 0x2002)                                            # CPU-driven latch flips
+    a.op('LDA', 'zp', CNT_HI); a.op('AND', 'imm', 0x10); a.op('ORA', 'imm', 0x0F); a.op('STA', 'abs', 0x2006)
+    a.op('LDA', 'zp', PX); a.op('AND', 'imm', 0x10); a.op('ORA', 'imm', 0xD8); a.op('STA', 'abs', 0x2006)
+    a.op('LDA', 'abs', 0x2007); a.op('LDA', 'abs', 0x2007)
+    a.label('no_cpu')
+    a.op('JMP', 'abs', 'main')
+    a.label('nmi')
+    _nmi_common(a)
+    _nmi_end(a)
+    a.label('irq')
+    a.op('RTI')
+    for name, t in (('t_pal', pal), ('t_nt', nt), ('t_oam', oam), ('t_mix', mix)):
+        a.label(name)
+        a.data(bytes(int(v) for v in t))
+    code = a.assemble()
+    assert len(code) <= 0x3FFA, len(code)
+    fixed = bytearray(24576)                                              # banks 13-15 at $A000-$FFFF
+    fixed[0x2000:0x2000 + len(code)] = code
+    vec = (a.labels['nmi'], a.labels['reset'], a.labels['irq'])
+    fixed[0x5FFA:0x6000] = bytes(sum(((v & 0xFF, v >> 8) for v in vec), ()))
+    chr_ = rng.integers(0, 256, 131072, dtype=np.uint8).tobytes()
+    return ines(b''.join(banks) + bytes(fixed), chr_, 9, vertical=True)
 
 
 DCNT, DYCNT = 0x44, 0x45                  # frames Down has been held, frames spent dying

@@ -39,6 +39,8 @@
 #define NES_BOARD_UXROM 2u                    /* 16 KB PRG bank at $8000, the last 16 KB fixed at $C000 */
 #define NES_BOARD_CNROM 3u                    /* 32 KB PRG fixed, 8 KB CHR bank latch (patch:3418) */
 #define NES_BOARD_MMC3 4u
+#define NES_BOARD_MMC2 5u                     /* mapper 9: 8 KB PRG bank at $8000, 4 KB CHR halves picked by the
+                                                 $FD/$FE latches (patch:3027-3035, 3147-3156) */
 
 /* Frame-log event kinds (word 0 bits 24..31). Word 0 bits 0..23: event time + NES_LOG_TIME_BIAS, where the
  * event time is in dots from the start of line 0 of the logged frame (pre-render line: negative).
@@ -52,9 +54,11 @@
 #define NES_EV_PAL 6u     /* $2007 palette write: value, aux = palette index (after mirroring) */
 #define NES_EV_CHR 7u     /* CHR 1 KB page change: value = page, aux = slot 0..7 */
 #define NES_EV_MIRROR 8u  /* nametable map change: value = nt_map packed 4 x 2 bits */
+#define NES_EV_MMC2 9u    /* MMC2 register change: value, aux = register (0-3 CHR banks, 6-7 latches) */
 
 /* Log header words: 0 count | overflow << 31, 1 ctrl | mask << 8 | fine x << 16, 2 v | t << 16,
- * 3-4 CHR 1 KB page of each slot (8 bits each), 5 nt_map packed, 6-13 palette RAM, 14-15 zero. */
+ * 3-4 CHR 1 KB page of each slot (8 bits each), 5 nt_map packed, 6-13 palette RAM, 14 MMC2 CHR registers
+ * (8 bits each), 15 MMC2 latch 0 | latch 1 << 8 (zero on other boards). */
 #define NES_LOG_OVERFLOW 0x80000000u
 
 typedef struct NesRec {

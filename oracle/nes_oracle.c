@@ -50,8 +50,13 @@ int orc_parse_ines(const uint8_t* rom, uint32_t size, uint8_t* prg_buf, uint32_t
         snprintf(err, err_len, "four-screen nametables are not supported");
         return -1;
     }
-    if (mapper > 4u) {
-        snprintf(err, err_len, "unsupported mapper %u (supported: 0 NROM, 1 MMC1, 2 UxROM, 3 CNROM, 4 MMC3)", mapper);
+    if (mapper > 4u && mapper != 9u) {
+        snprintf(err, err_len, "unsupported mapper %u (supported: 0 NROM, 1 MMC1, 2 UxROM, 3 CNROM, 4 MMC3, 9 MMC2)",
+                 mapper);
+        return -1;
+    }
+    if (mapper == 9u && chr == 0) {
+        snprintf(err, err_len, "MMC2 needs CHR ROM");
         return -1;
     }
     if (prg == 0 || 16u + trainer + prg + chr > size) {
@@ -73,7 +78,7 @@ int orc_parse_ines(const uint8_t* rom, uint32_t size, uint8_t* prg_buf, uint32_t
     cart->prg_size = padded;
     cart->chr = chr ? rom + 16 + trainer + prg : NULL;
     cart->chr_size = chr ? chr : NES_CHRRAM_BYTES;
-    cart->board = (uint8_t)mapper;
+    cart->board = (uint8_t)(mapper == 9u ? NES_BOARD_MMC2 : mapper);
     cart->mirroring = (uint8_t)(rom[6] & 1u);
     /* UxROM / CNROM bus conflicts only when the header declares them: NES 2.0 (byte 7 bits 2-3 = 2), submapper 2
      * (patch:4008, layout.bus_conflicts = mapper 3 && declared) */
@@ -101,7 +106,9 @@ static void set_chr1(NesRec* r, const NesCart* c, int slot, uint32_t page) {
 /* MMC1 registers: 0 control, 1 CHR0, 2 CHR1, 3 PRG, 4 shift, 5 shift count.
  * UxROM register: 0 the 16 KB PRG bank at $8000. CNROM register: 0 the 8 KB CHR bank.
  * MMC3 registers: 0-7 R0-R7, 8 bank select, 9 mirroring, 10 PRG RAM protect, 11 IRQ latch, 12 IRQ counter,
- * 13 IRQ enabled, 14 IRQ reload. (patch:2917-2919, 2991-3063) */
+ * 13 IRQ enabled, 14 IRQ reload. (patch:2917-2919, 2991-3063)
+ * MMC2 registers: 0-3 the CHR banks ($FD/$0000, $FE/$0000, $FD/$1000, $FE/$1000), 4 PRG, 5 mirroring (1 vertical),
+ * 6-7 the latches of the two halves (0 = $FD bank, 1 = $FE bank) (patch:2916, 3027-3035). */
 static void mapper_sync(NesRec* r, const NesCart* c) {
     const uint8_t* m = r->mreg;
     if (c->board == NES_BOARD_MMC1) {
@@ -149,6 +156,16 @@ static void mapper_sync(NesRec* r, const NesCart* c) {
         set_chr1(r, c, 6 ^ f, m[4]);
         set_chr1(r, c, 7 ^ f, m[5]);
         set_nt_map(r, (m[9] & 1u) ? 0u : 1u);
+    } else if (c->board == NES_BOARD_MMC2) { /* the 8 KB bank at $8000, the last three fixed */
+        set_prg8(r, c, 0, m[4]);
+        set_prg8(r, c, 1, ~2u);
+        set_prg8(r, c, 2, ~1u);
+        set_prg8(r, c, 3, ~0u);
+        for (int i = 0; i < 4; ++i) {
+            set_chr1(r, c, i, m[m[6] & 1u] * 4u + (uint32_t)i);
+            set_chr1(r, c, 4 + i, m[2u + (m[7] & 1u)] * 4u + (uint32_t)i);
+        }
+        set_nt_map(r, m[5] ? 1u : 0u);
     } else if (c->board == NES_BOARD_UXROM) { /* the 16 KB bank in register 0, the last one fixed at $C000 */
         const uint32_t last = c->prg_size / 16384u - 1u;
         set_prg8(r, c, 0, m[0] * 2u);
@@ -172,6 +189,9 @@ static void mapper_power_on(NesRec* r, const NesCart* c) {
     } else if (c->board == NES_BOARD_MMC3) {
         r->mreg[1] = 2; r->mreg[2] = 4; r->mreg[3] = 5; r->mreg[4] = 6; r->mreg[5] = 7; r->mreg[7] = 1;
         r->mreg[9] = c->mirroring ? 0 : 1;
+    } else if (c->board == NES_BOARD_MMC2) {
+        r->mreg[6] = 1;   /* both latches on the $FE bank (patch:3080-3083) */
+        r->mreg[7] = 1;
     }
     mapper_sync(r, c);
 }
@@ -204,6 +224,17 @@ static void mapper_write(NesRec* r, const NesCart* c, uint16_t addr, uint8_t v) 
             default: m[13] = 1; return;
         }
         mapper_sync(r, c);
+    } else if (c->board == NES_BOARD_MMC2) {
+        switch (addr & 0xF000u) {
+            case 0xA000u: m[4] = v & 0x0Fu; break;
+            case 0xB000u: m[0] = v & 0x1Fu; break;
+            case 0xC000u: m[1] = v & 0x1Fu; break;
+            case 0xD000u: m[2] = v & 0x1Fu; break;
+            case 0xE000u: m[3] = v & 0x1Fu; break;
+            case 0xF000u: m[5] = (v & 1u) ^ 1u; break;
+            default: return;   /* $8000-$9FFF: no register */
+        }
+        mapper_sync(r, c);
     } else if (c->board == NES_BOARD_CNROM || c->board == NES_BOARD_UXROM) {
         /* the bank latch, ANDed with the ROM byte under a bus conflict (patch:3124-3127, 3281-3283) */
         const uint8_t rom = c->prg[r->prg_off[(addr >> 13) & 3u] + (addr & 0x1FFFu)];
@@ -221,6 +252,14 @@ static void mmc3_clock(NesRec* r) { /* revision B counter (patch:3182-3193) */
         --m[12];
     }
     if (m[12] == 0 && m[13] != 0) r->irq_line = 1;
+}
+
+/* MMC2: a pattern fetch or CPU-driven VRAM address in $0FD0-$0FEF / $1FD0-$1FEF flips the latch of its half
+ * (FCEUmm's PPU_hook ranges, patch:3196-3220, 1390-1402). 0 = none, else the latch value + 1 | half << 2. */
+static uint32_t mmc2_trigger(uint32_t a) {
+    const uint32_t high = (a >> 8) & 0x3Fu, low = a & 0xF0u;
+    if (high >= 0x20u || (high & 0x0Fu) != 0x0Fu || (low != 0xD0u && low != 0xE0u)) return 0;
+    return (low == 0xE0u ? 2u : 1u) | (high < 0x10u ? 0u : 4u);
 }
 
 static int prg_ram_enabled(const NesRec* r, const NesCart* c) {
@@ -332,6 +371,10 @@ static void log_capture(NesRec* r) {
     h[2] = r->v | ((uint32_t)r->t << 16);
     for (int i = 0; i < 8; ++i) h[3 + (i >> 2)] |= ((r->chr_off[i] >> 10) & 0xFFu) << ((i & 3) * 8);
     h[5] = nt_map_packed(r);
+    if (r->board == NES_BOARD_MMC2) {
+        h[14] = r->mreg[0] | ((uint32_t)r->mreg[1] << 8) | ((uint32_t)r->mreg[2] << 16) | ((uint32_t)r->mreg[3] << 24);
+        h[15] = r->mreg[6] | ((uint32_t)r->mreg[7] << 8);
+    }
     for (int i = 0; i < 8; ++i)
         h[6 + i] = r->pal[4 * i] | ((uint32_t)r->pal[4 * i + 1] << 8) | ((uint32_t)r->pal[4 * i + 2] << 16) |
                    ((uint32_t)r->pal[4 * i + 3] << 24);
@@ -348,7 +391,21 @@ typedef struct Replay {
     uint8_t nt_map[4];
     uint32_t ev, count;
     const uint32_t* events;
+    int mmc2;                        /* MMC2: the CHR halves follow creg and the latches */
+    uint32_t creg[4], latch[2], chr_pages;
 } Replay;
+
+static void replay_mmc2_select(Replay* s, uint32_t half) { /* patch:1385-1388 */
+    const uint32_t bank = s->creg[2u * half + s->latch[half]];
+    for (uint32_t i = 0; i < 4u; ++i) s->chr_off[4u * half + i] = ((bank * 4u + i) & (s->chr_pages - 1u)) * 1024u;
+}
+
+static void replay_hook(Replay* s, uint32_t a) { /* a pattern fetch at a (patch:1390-1402) */
+    const uint32_t t = s->mmc2 ? mmc2_trigger(a) : 0u;
+    if (t == 0) return;
+    s->latch[t >> 2] = (t & 3u) - 1u;
+    replay_mmc2_select(s, t >> 2);
+}
 
 static int32_t ev_time(const Replay* s, uint32_t i) {
     return (int32_t)(s->events[2 * i] & 0xFFFFFFu) - NES_LOG_TIME_BIAS;
@@ -385,6 +442,15 @@ static void replay_apply(Replay* s, uint32_t i) {
         case NES_EV_CHR: s->chr_off[aux & 7u] = val * 1024u; break;
         case NES_EV_MIRROR:
             for (int k = 0; k < 4; ++k) s->nt_map[k] = (uint8_t)((val >> (2 * k)) & 3u);
+            break;
+        case NES_EV_MMC2: /* patch:1471-1478 */
+            if (aux < 4u) {
+                s->creg[aux] = val;
+                replay_mmc2_select(s, aux >> 1);
+            } else if (aux == 6u || aux == 7u) {
+                s->latch[aux - 6u] = val & 1u;
+                replay_mmc2_select(s, aux - 6u);
+            }
             break;
         default: break;
     }
@@ -430,8 +496,13 @@ static void replay_line_end(Replay* s, int l) {
     replay_until(s, base + 320);
 }
 
-static void replay_begin(Replay* s, const NesRec* r) {
+static void replay_begin(Replay* s, const NesRec* r, const NesCart* c) {
     const uint32_t* h = r->log;
+    s->mmc2 = c->board == NES_BOARD_MMC2;
+    s->chr_pages = c->chr_size / 1024u;
+    for (int i = 0; i < 4; ++i) s->creg[i] = (h[14] >> (8 * i)) & 0xFFu;
+    s->latch[0] = h[15] & 1u;
+    s->latch[1] = (h[15] >> 8) & 1u;
     s->ctrl = h[1] & 0xFFu;
     s->mask = (h[1] >> 8) & 0xFFu;
     s->fx = (h[1] >> 16) & 7u;
@@ -451,8 +522,63 @@ static uint8_t nt_read(const NesRec* r, const Replay* s, uint32_t addr) { /* add
     return r->nt[(s->nt_map[n] & 1u) * 1024u + (addr & 0x3FFu)];
 }
 
-/* Background pixel x (0..255) of a line drawn with state s: 2-bit value and palette select. */
-static uint32_t bg_pixel(const NesRec* r, const NesCart* c, const Replay* s, uint32_t x, uint32_t* attr_out) {
+/* Pattern address (low plane) of background tile slot `slot` (0..33) of the line drawn with state s. */
+static uint32_t bg_slot_pa(const NesRec* r, const Replay* s, uint32_t slot) {
+    uint32_t cx = (s->v & 31u) + slot, nth = (s->v >> 10) & 1u;
+    if (cx >= 32u) {
+        cx -= 32u;
+        nth ^= 1u;
+    }
+    const uint32_t cy = (s->v >> 5) & 31u, fy = (s->v >> 12) & 7u, ntv = (s->v >> 11) & 1u;
+    const uint32_t base = 0x2000u | ((nth | (ntv << 1)) << 10);
+    return ((s->ctrl & 0x10u) << 8) + nt_read(r, s, base | (cy << 5) | cx) * 16u + fy;
+}
+
+/* Pattern address (low plane) of a sprite's row `row` (0..h-1, before the vertical flip). */
+static uint32_t sprite_row_pa(uint32_t ctrl, uint32_t tile, uint32_t attr, uint32_t row) {
+    const uint32_t h = (ctrl & 0x20u) ? 16u : 8u;
+    if (attr & 0x80u) row = h - 1u - row;
+    if (h == 8u) return ((ctrl & 0x08u) << 9) + tile * 16u + row;
+    return ((tile & 1u) << 12) + (tile & 0xFEu) * 16u + (row & 7u) + ((row & 8u) << 1);
+}
+
+/* MMC2: the pattern fetches of line l in order, each through the bank of the moment and then the latch hook
+ * (patch:1496-1560, 1660-1700): the sprites of line l, fetched at the end of line l - 1 (l >= 1), then, unless
+ * sprites_only, the line's 34 background tile slots. sp_chr[k] / bg_chr[t] receive the CHR offset of the 4 KB
+ * half each fetch read (slot 0 of the half); either may be NULL. Fetches happen only while rendering is on. */
+static void mmc2_line_fetches(Replay* s, const NesRec* r, int l, int sprites_only, uint32_t* sp_chr,
+                              uint32_t* bg_chr) {
+    if (!s->mmc2 || (s->mask & 0x18u) == 0) return;
+    if (l >= 1) {
+        const int h = (s->ctrl & 0x20u) ? 16 : 8;
+        uint32_t n = 0;
+        for (uint32_t i = 0; i < 64u && n < 8u; ++i) {
+            const uint8_t* o = r->oam + 4u * i;
+            const int row = l - (int)o[0] - 1;
+            if (row < 0 || row >= h) continue;
+            const uint32_t pa = sprite_row_pa(s->ctrl, o[1], o[2], (uint32_t)row);
+            if (sp_chr) sp_chr[n] = s->chr_off[4u * (pa >> 12)];
+            replay_hook(s, pa);
+            ++n;
+        }
+    }
+    if (sprites_only) return;
+    for (uint32_t t = 0; t < 34u; ++t) {
+        const uint32_t pa = bg_slot_pa(r, s, t);
+        if (bg_chr) bg_chr[t] = s->chr_off[4u * (pa >> 12)];
+        replay_hook(s, pa);
+    }
+}
+
+/* A pattern byte through the 1 KB slot table, or (base4 != ~0) from the 4 KB CHR half at byte offset base4. */
+static uint32_t pat_read(const NesRec* r, const NesCart* c, const Replay* s, uint32_t base4, uint32_t a) {
+    return base4 != ~0u ? c->chr[base4 + (a & 0xFFFu)] : chr_read(r, c, s->chr_off, a);
+}
+
+/* Background pixel x (0..255) of a line drawn with state s: 2-bit value and palette select. bg_chr: the MMC2
+ * fetch banks of the line's tile slots, or NULL. */
+static uint32_t bg_pixel(const NesRec* r, const NesCart* c, const Replay* s, uint32_t x, uint32_t* attr_out,
+                         const uint32_t* bg_chr) {
     const uint32_t pos = x + s->fx, slot = pos >> 3, bit = pos & 7u;
     uint32_t cx = (s->v & 31u) + slot, nth = (s->v >> 10) & 1u;
     if (cx >= 32u) {
@@ -465,26 +591,24 @@ static uint32_t bg_pixel(const NesRec* r, const NesCart* c, const Replay* s, uin
     const uint32_t at = nt_read(r, s, base | 0x3C0u | ((cy >> 2) << 3) | (cx >> 2));
     *attr_out = (at >> (((cy & 2u) << 1) | (cx & 2u))) & 3u;
     const uint32_t pa = ((s->ctrl & 0x10u) << 8) + tile * 16u + fy;
-    const uint32_t lo = chr_read(r, c, s->chr_off, pa), hi = chr_read(r, c, s->chr_off, pa + 8u);
+    const uint32_t b4 = bg_chr ? bg_chr[slot] : ~0u;
+    const uint32_t lo = pat_read(r, c, s, b4, pa), hi = pat_read(r, c, s, b4, pa + 8u);
     return ((lo >> (7u - bit)) & 1u) | (((hi >> (7u - bit)) & 1u) << 1);
 }
 
-/* Pixel of sprite i at screen x on line l (0 transparent / outside), `row` = l - y - 1. */
+/* Pixel of sprite i at screen x on line l (0 transparent / outside), `row` = l - y - 1. base4: the MMC2 fetch
+ * bank of the sprite's row (~0 = the slot table). */
 static uint32_t sprite_pixel(const NesRec* r, const NesCart* c, const Replay* s, uint32_t i, uint32_t row,
-                             uint32_t col) {
+                             uint32_t col, uint32_t base4) {
     const uint8_t* o = r->oam + 4u * i;
-    const uint32_t h = (s->ctrl & 0x20u) ? 16u : 8u;
-    const uint32_t attr = o[2], tile = o[1];
-    if (attr & 0x40u) col = 7u - col;
-    if (attr & 0x80u) row = h - 1u - row;
-    uint32_t pa;
-    if (h == 8u) pa = ((s->ctrl & 0x08u) << 9) + tile * 16u + row;
-    else pa = ((tile & 1u) << 12) + (tile & 0xFEu) * 16u + (row & 7u) + ((row & 8u) << 1);
-    const uint32_t lo = chr_read(r, c, s->chr_off, pa), hi = chr_read(r, c, s->chr_off, pa + 8u);
+    if (o[2] & 0x40u) col = 7u - col;
+    const uint32_t pa = sprite_row_pa(s->ctrl, o[1], o[2], row);
+    const uint32_t lo = pat_read(r, c, s, base4, pa), hi = pat_read(r, c, s, base4, pa + 8u);
     return ((lo >> (7u - col)) & 1u) | (((hi >> (7u - col)) & 1u) << 1);
 }
 
-static void render_line(const NesRec* r, const NesCart* c, const Replay* s, int l, uint8_t* px) {
+static void render_line(const NesRec* r, const NesCart* c, const Replay* s, int l, uint8_t* px,
+                        const uint32_t* bg_chr, const uint32_t* sp_chr) {
     const int bg_on = (s->mask & 0x08u) != 0, sp_on = (s->mask & 0x10u) != 0;
     const uint32_t h = (s->ctrl & 0x20u) ? 16u : 8u;
     uint32_t sel[8], nsel = 0;
@@ -496,14 +620,15 @@ static void render_line(const NesRec* r, const NesCart* c, const Replay* s, int 
     }
     for (uint32_t x = 0; x < 256u; ++x) {
         uint32_t bg = 0, bga = 0;
-        if (bg_on && (x >= 8u || (s->mask & 0x02u))) bg = bg_pixel(r, c, s, x, &bga);
+        if (bg_on && (x >= 8u || (s->mask & 0x02u))) bg = bg_pixel(r, c, s, x, &bga, bg_chr);
         uint32_t sp = 0, spa = 0, behind = 0;
         if (x >= 8u || (s->mask & 0x04u)) {
             for (uint32_t k = 0; k < nsel; ++k) {
                 const uint8_t* o = r->oam + 4u * sel[k];
                 const uint32_t col = x - o[3];
                 if (x < o[3] || col >= 8u) continue;
-                const uint32_t p = sprite_pixel(r, c, s, sel[k], (uint32_t)(l - o[0] - 1), col);
+                const uint32_t p = sprite_pixel(r, c, s, sel[k], (uint32_t)(l - o[0] - 1), col,
+                                                sp_chr ? sp_chr[k] : ~0u);
                 if (p) {
                     sp = p;
                     spa = o[2] & 3u;
@@ -524,9 +649,11 @@ static void render_line(const NesRec* r, const NesCart* c, const Replay* s, int 
 
 void orc_render_full(const NesRec* r, const NesCart* c, uint8_t* pix, uint8_t* emph) {
     Replay s;
-    replay_begin(&s, r);
+    replay_begin(&s, r, c);
     for (int l = 0; l < 240; ++l) {
-        render_line(r, c, &s, l, pix + l * 256);
+        uint32_t bgc[34], spc[8];
+        mmc2_line_fetches(&s, r, l, 0, spc, bgc);
+        render_line(r, c, &s, l, pix + l * 256, s.mmc2 ? bgc : NULL, s.mmc2 ? spc : NULL);
         emph[l] = (uint8_t)((s.mask >> 5) & 7u);
         replay_line_end(&s, l);
     }
@@ -535,10 +662,12 @@ void orc_render_full(const NesRec* r, const NesCart* c, uint8_t* pix, uint8_t* e
 void orc_render_obs(const NesRec* r, const NesCart* c, uint8_t* obs, uint8_t* emph) {
     Replay s;
     uint8_t line[256];
-    replay_begin(&s, r);
+    replay_begin(&s, r, c);
     for (int l = 0; l < 232; ++l) {
+        uint32_t bgc[34], spc[8];
+        mmc2_line_fetches(&s, r, l, 0, spc, bgc);
         if (l >= 8) {
-            render_line(r, c, &s, l, line);
+            render_line(r, c, &s, l, line, s.mmc2 ? bgc : NULL, s.mmc2 ? spc : NULL);
             memcpy(obs + (l - 8) * 240, line + 8, 240);
             emph[l - 8] = (uint8_t)((s.mask >> 5) & 7u);
         }
@@ -552,8 +681,11 @@ int32_t orc_sprite0_scan(const NesRec* r, const NesCart* c) {
     Replay s;
     const int y0 = r->oam[0], x0 = r->oam[3];
     if (y0 >= 239) return NES_NO_HIT;
-    replay_begin(&s, r);
+    replay_begin(&s, r, c);
     for (int l = 0; l < 240; ++l) {
+        uint32_t bgc[34], spc[8];
+        mmc2_line_fetches(&s, r, l, 0, spc, bgc);
+        const uint32_t* bg_chr = s.mmc2 ? bgc : NULL;
         const uint32_t h = (s.ctrl & 0x20u) ? 16u : 8u;
         const int row = l - y0 - 1;
         if ((s.mask & 0x18u) == 0x18u && row >= 0 && row < (int)h) {
@@ -562,7 +694,8 @@ int32_t orc_sprite0_scan(const NesRec* r, const NesCart* c) {
                 if (x >= 255) break;
                 if (x < 8 && (s.mask & 0x06u) != 0x06u) continue;
                 uint32_t a;
-                if (sprite_pixel(r, c, &s, 0, (uint32_t)row, (uint32_t)col) && bg_pixel(r, c, &s, (uint32_t)x, &a))
+                if (sprite_pixel(r, c, &s, 0, (uint32_t)row, (uint32_t)col, s.mmc2 ? spc[0] : ~0u) &&
+                    bg_pixel(r, c, &s, (uint32_t)x, &a, bg_chr))
                     return l * 341 + x + 1;
             }
         }
@@ -611,6 +744,24 @@ static uint32_t dots_to_event(NesRec* r, const NesCart* c) {
     return best;
 }
 
+/* MMC2 at vblank: the latches this frame's own fetches leave, from a latches-only replay of its log over the
+ * nametables and OAM as they are now (NeSLE's frame_resolve_mmc2, patch:1790-1812; rl/csrc/nes_machine.cuh:110-131
+ * runs the same replay after the vblank stop, before any further instruction). */
+static void mmc2_resolve(NesRec* r, const NesCart* c) {
+    if (r->frame != r->log_frame) return;   /* no log of this frame (the first one after power-on) */
+    Replay s;
+    replay_begin(&s, r, c);
+    for (int l = 0; l < 240; ++l) {
+        mmc2_line_fetches(&s, r, l, 0, NULL, NULL);
+        replay_line_end(&s, l);
+    }
+    mmc2_line_fetches(&s, r, 240, 1, NULL, NULL);
+    replay_until(&s, INT32_MAX);
+    r->mreg[6] = (uint8_t)s.latch[0];
+    r->mreg[7] = (uint8_t)s.latch[1];
+    mapper_sync(r, c);
+}
+
 static void process_events(NesRec* r, const NesCart* c) {
     const uint32_t d = r->frame_dot;
     if (d == NES_FRAME_DOTS) {
@@ -621,6 +772,7 @@ static void process_events(NesRec* r, const NesCart* c) {
     if (d == NES_VBLANK_DOT) {
         r->status |= 0x80u;
         if (r->ctrl & 0x80u) r->nmi_pending = 1;
+        if (c->board == NES_BOARD_MMC2) mmc2_resolve(r, c);
     }
     if (d == NES_PRERENDER_DOT) {
         r->status &= 0x1Fu;
@@ -708,6 +860,19 @@ static void ppu_mem_write(Bus* b, uint32_t a, uint8_t v) {
     }
 }
 
+/* MMC2: the VRAM address the CPU drives through $2006/$2007 flips a latch; a change is logged for the renderer
+ * (patch:615-636, 3196-3220). */
+static void mmc2_ppu_address(Bus* b, uint32_t a) {
+    NesRec* r = b->r;
+    const uint32_t t = b->c->board == NES_BOARD_MMC2 ? mmc2_trigger(a) : 0u;
+    if (t == 0) return;
+    const uint32_t half = t >> 2, latch = (t & 3u) - 1u;
+    if (r->mreg[6 + half] == latch) return;
+    r->mreg[6 + half] = (uint8_t)latch;
+    mapper_sync(r, b->c);
+    log_event(b, NES_EV_MMC2, latch, 6 + half);
+}
+
 static uint8_t ppu_reg_read(Bus* b, uint32_t reg) {
     NesRec* r = b->r;
     uint8_t v;
@@ -722,13 +887,16 @@ static uint8_t ppu_reg_read(Bus* b, uint32_t reg) {
             const uint32_t a = r->v & 0x3FFFu;
             if (a < 0x3F00u) {
                 v = r->read_buf;
+                mmc2_ppu_address(b, a);
                 r->read_buf = ppu_mem_read(r, b->c, a);
             } else {
                 v = ppu_mem_read(r, b->c, a);
                 r->read_buf = ppu_mem_read(r, b->c, a - 0x1000u);
+                mmc2_ppu_address(b, a);
             }
             r->v = (uint16_t)((r->v + ((r->ctrl & 4u) ? 32u : 1u)) & 0x7FFFu);
             log_event(b, NES_EV_DATA, 0, 1);
+            mmc2_ppu_address(b, r->v & 0x3FFFu);
             break;
         }
         default: return r->open_bus;
@@ -776,11 +944,13 @@ static void ppu_reg_write(Bus* b, uint32_t reg, uint8_t v) {
                 r->t = (uint16_t)((r->t & 0xFF00u) | v);
                 r->v = r->t;
                 r->w = 0;
+                mmc2_ppu_address(b, r->v);
             }
             break;
         case 7:
             ppu_mem_write(b, r->v, v);
             r->v = (uint16_t)((r->v + ((r->ctrl & 4u) ? 32u : 1u)) & 0x7FFFu);
+            mmc2_ppu_address(b, r->v & 0x3FFFu);
             break;
         default: break;
     }
@@ -823,13 +993,17 @@ static void bus_write(Bus* b, uint16_t a, uint8_t v) {
         dmc_write(r, a, v);
     } else if (a >= 0x8000u) {
         uint32_t before[8];
-        uint8_t map_before[4];
+        uint8_t map_before[4], creg_before[4];
         memcpy(before, r->chr_off, sizeof(before));
         memcpy(map_before, r->nt_map, 4);
+        memcpy(creg_before, r->mreg, 4);
         mapper_write(r, b->c, a, v);
         for (uint32_t i = 0; i < 8u; ++i)
             if (r->chr_off[i] != before[i]) log_event(b, NES_EV_CHR, r->chr_off[i] >> 10, i);
         if (memcmp(map_before, r->nt_map, 4) != 0) log_event(b, NES_EV_MIRROR, nt_map_packed(r), 0);
+        if (b->c->board == NES_BOARD_MMC2)   /* patch:661-664 */
+            for (uint32_t i = 0; i < 4u; ++i)
+                if (r->mreg[i] != creg_before[i]) log_event(b, NES_EV_MMC2, r->mreg[i], i);
     } else if (a >= 0x6000u) {
         if (prg_ram_enabled(r, b->c)) r->prg_ram[a - 0x6000u] = v;
     }

@@ -1,4 +1,4 @@
-"""Known-answer tests of the oracle's cartridge boards (NROM, UxROM, CNROM, MMC1, MMC3) and its DMC.
+"""Known-answer tests of the oracle's cartridge boards (NROM, UxROM, CNROM, MMC1, MMC3, MMC2) and its DMC.
 
 MMC3: restates the reference's register case third_party/nesle-extensions.patch:4638-4673 (R0-R7 = 00 3A 4A 5D 6E 61
 0A 04, bank select $46, $A000 = 1 on 128 KB PRG / 128 KB CHR) by writing the registers through the CPU bus, plus
@@ -7,6 +7,8 @@ MMC1: the serial port and the bank modes written from the board's documented reg
 4 KB CHR banks), not from the oracle's page arithmetic.
 UxROM / CNROM: the bank latch and its declared AND-type bus conflicts from the board's behaviour as the reference states it
 (patch:2982-2990, 3124-3127, 4008), checked on a cart whose PRG pages are tagged with their numbers.
+MMC2: the registers, the CPU-driven latch flips and the renderer's fetch-then-flip order along a line as the reference
+states them (patch:3027-3035, 3147-3156, 3196-3220, 1385-1402, 1548-1551).
 DMC: restates the sample-channel cases of patch:4105-4205 (status bit 4, 4-cycle fetch steals, loop, rate change,
 no steal in the idle fast-forward) with the same 4-cycle instruction driver as the reference test.
 """
@@ -373,3 +375,94 @@ def test_dmc_fast_forward_steals_nothing():
     assert m.service(start, 0) == 0
     assert m.service(start + 10 * KBYTE, 0) == 0 and m.status() == 0x10
     assert m.service(start + 17 * KBYTE, 0) == 0 and m.status() == 0x00
+
+
+# ----------------------------------------------------------------------------------------------- MMC2
+
+def mmc2_con(chr_bytes=None):
+    chr_ = bytes(32 * KB) if chr_bytes is None else bytes(chr_bytes)
+    rom = bytearray(cart(9, 128, 32))
+    rom[16 + 128 * KB:] = chr_
+    return Console(bytes(rom))
+
+
+def test_mmc2_registers_prg_and_chr_halves():
+    """Power-on: both latches on the $FE bank; $A000 picks the 8 KB bank at $8000, the last three fixed; $B000-$E000
+    the four 4 KB CHR banks, each half showing its latch's bank; $F000 bit 0: 0 vertical, 1 horizontal."""
+    con = mmc2_con()
+    assert list(con.mem('mreg', 8)[6:8]) == [1, 1]
+    prg, _, _ = pages(con)
+    assert prg[1:] == [13, 14, 15]
+    for addr, v in ((0xA000, 5), (0xB000, 2), (0xC000, 3), (0xD000, 4), (0xE000, 6), (0xF000, 0)):
+        con.write(addr, v)
+    prg, chr_, nt = pages(con)
+    assert prg == [5, 13, 14, 15]
+    assert chr_ == [12, 13, 14, 15, 24, 25, 26, 27]            # latch 1 -> $FE banks 3 and 6 (4 KB -> 1 KB pages)
+    assert nt == [0, 1, 0, 1]
+    con.write(0xF000, 1)
+    assert pages(con)[2] == [0, 0, 1, 1]
+    con.write(0x9000, 7)                                        # $8000-$9FFF: no register
+    assert pages(con)[0] == [5, 13, 14, 15]
+
+
+def test_mmc2_cpu_driven_latch_flips():
+    """$2006 and the $2007 address increments put VRAM addresses on the bus: $0FD0-$0FDF / $0FE0-$0FEF set latch 0
+    to $FD / $FE, $1FD0-$1FEF latch 1 (patch:3196-3220)."""
+    con = mmc2_con()
+    for addr, v in ((0xB000, 2), (0xC000, 3), (0xD000, 4), (0xE000, 6)):
+        con.write(addr, v)
+    con.write(0x2006, 0x0F)
+    con.write(0x2006, 0xD8)
+    assert list(con.mem('mreg', 8)[6:8]) == [0, 1] and pages(con)[1][:4] == [8, 9, 10, 11]
+    con.write(0x2006, 0x1F)
+    con.write(0x2006, 0xCF)                                     # $1FCF: no flip
+    assert list(con.mem('mreg', 8)[6:8]) == [0, 1]
+    con.read(0x2007)                                            # the increment to $1FD0 flips latch 1 to $FD
+    assert list(con.mem('mreg', 8)[6:8]) == [0, 0] and pages(con)[1][4:] == [16, 17, 18, 19]
+    con.write(0x2006, 0x0F)
+    con.write(0x2006, 0xE0)
+    assert list(con.mem('mreg', 8)[6:8]) == [1, 0]
+
+
+def test_mmc2_renderer_fetch_then_flip_along_the_line():
+    """Background through half 0, latch 0 on $FE at the frame start. Bank $FD (2) holds opaque tiles, bank $FE (3)
+    transparent ones. Nametable row 0 has tile $FD at slot 10 and $FE at slot 20: each fetch reads through the bank
+    of the moment and then flips the latch (patch:1548-1551), so slots 11-20 are drawn from the $FD bank and every
+    other slot, the two latch tiles' own left neighbours included, from the $FE bank; the latch carries over to the
+    next line, which therefore looks the same."""
+    chr_ = bytearray(32 * KB)
+    for t in range(256):
+        chr_[2 * 4 * KB + 16 * t: 2 * 4 * KB + 16 * t + 8] = b'\xff' * 8
+    con = mmc2_con(chr_)
+    for addr, v in ((0xB000, 2), (0xC000, 3), (0xD000, 4), (0xE000, 5)):
+        con.write(addr, v)
+    h = con.words('log', 16 + 512)
+    h[:] = 0
+    h[1] = 0x0A << 8                                            # background on, no left clip, pattern half 0
+    h[3], h[4] = 0x0F0E0D0C, 0x17161514                         # the slot pages with both latches on $FE
+    h[5] = 0b01000100
+    h[6] = 0x0F | (0x21 << 8)                                   # backdrop $0F, colour 1 = $21
+    h[14] = 2 | (3 << 8) | (4 << 16) | (5 << 24)
+    h[15] = 1 | (1 << 8)
+    con.set('log_n', 0, 'H')
+    nt = con.mem('nt', 2048)
+    nt[:] = 0
+    nt[10], nt[20] = 0xFD, 0xFE
+    con.mem('oam', 256)[:] = 0xFF
+    pix = con.render_full()[0]
+    want = np.full(256, 0x0F, np.uint8)
+    want[88:168] = 0x21
+    for y in (0, 1, 7):
+        assert np.array_equal(pix[y], want), y
+
+
+def test_mmc2_synthetic_cart_flips_latches_while_rendering():
+    """The seed-generated MMC2 cart's frames leave both latches changing from frame to frame (the vblank resolve)."""
+    con = Console(synth.mmc2_cart(1))
+    seen = set()
+    target = 0
+    for f in range(40):
+        target += 89342
+        con.run_until(target)
+        seen.add(tuple(int(x) for x in con.mem('mreg', 8)[6:8]))
+    assert len(seen) >= 3, seen
