@@ -149,7 +149,16 @@ __device__ inline void map_set_nt(Con& c, const Mem& m, uint32_t kind) {
     for (uint32_t k = 0; k < 4; ++k) m.rec->nt_map[k] = (uint8_t)((c.nt_map >> (2 * k)) & 3u);
 }
 
-// Page tables from the board registers (MMC1: control, CHR0, CHR1, PRG; MMC3: R0-R7, select, mirroring, ...).
+// MMC2: an address in $0FD0-$0FEF / $1FD0-$1FEF flips the latch of its half (FCEUmm's PPU_hook ranges,
+// patch:3196-3220, 1390-1402). 0 = none, else the latch value + 1 | half << 2.
+__device__ __forceinline__ uint32_t mmc2_trigger(uint32_t a) {
+    const uint32_t high = (a >> 8) & 0x3Fu, low = a & 0xF0u;
+    if (high >= 0x20u || (high & 0x0Fu) != 0x0Fu || (low != 0xD0u && low != 0xE0u)) return 0;
+    return (low == 0xE0u ? 2u : 1u) | (high < 0x10u ? 0u : 4u);
+}
+
+// Page tables from the board registers (MMC1: control, CHR0, CHR1, PRG; MMC3: R0-R7, select, mirroring, ...;
+// MMC2: CHR $FD/$0000, $FE/$0000, $FD/$1000, $FE/$1000, PRG, mirroring, latch 0, latch 1).
 __device__ inline void map_sync(Con& c, const Mem& m) {
     const uint8_t* r = m.rec->mreg;
     if (m.cart.board == NES_BOARD_MMC1) {
@@ -183,6 +192,16 @@ __device__ inline void map_sync(Con& c, const Mem& m) {
         map_set_chr(m, 3u ^ f, r[1] | 1u);
         for (uint32_t i = 0; i < 4; ++i) map_set_chr(m, (4u + i) ^ f, r[2 + i]);
         map_set_nt(c, m, (r[9] & 1u) ? 0u : 1u);
+    } else if (m.cart.board == NES_BOARD_MMC2) {   // the 8 KB bank at $8000, the last three fixed (patch:3027-3035)
+        map_set_prg(c, m, 0, r[4]);
+        map_set_prg(c, m, 1, ~2u);
+        map_set_prg(c, m, 2, ~1u);
+        map_set_prg(c, m, 3, ~0u);
+        for (uint32_t i = 0; i < 4; ++i) {
+            map_set_chr(m, i, 4u * r[r[6] & 1u] + i);
+            map_set_chr(m, 4u + i, 4u * r[2u + (r[7] & 1u)] + i);
+        }
+        map_set_nt(c, m, r[5] ? 1u : 0u);
     } else if (m.cart.board == NES_BOARD_UXROM) {   // the 16 KB bank in register 0, the last one fixed at $C000
         const uint32_t last = m.cart.prg_pages8 / 2u - 1u;
         map_set_prg(c, m, 0, r[0] * 2u);
@@ -231,6 +250,13 @@ __device__ inline void map_write(Con& c, const Mem& m, uint32_t addr, uint32_t v
             else r[13] = 1;
             return;
         }
+        map_sync(c, m);
+    } else if (m.cart.board == NES_BOARD_MMC2) {   // patch:3147-3156
+        const uint32_t k = addr & 0xF000u;
+        if (k == 0xA000u) r[4] = (uint8_t)(v & 0x0Fu);
+        else if (k >= 0xB000u && k <= 0xE000u) r[(k >> 12) - 0xBu] = (uint8_t)(v & 0x1Fu);
+        else if (k == 0xF000u) r[5] = (uint8_t)((v & 1u) ^ 1u);
+        else return;   // $8000-$9FFF: no register
         map_sync(c, m);
     } else if (m.cart.board == NES_BOARD_CNROM || m.cart.board == NES_BOARD_UXROM) {
         // the bank latch, ANDed with the ROM byte under a bus conflict
@@ -314,10 +340,30 @@ struct Replay {
     uint32_t v, t, fx, ctrl, mask;
     uint32_t chr_lo, chr_hi;   // 1 KB CHR page of slots 0-3 / 4-7, 8 bits each
     uint32_t nt_map;
+    uint32_t creg, latch;      // MMC2: the 4 CHR registers (8 bits each), latch 0 | latch 1 << 8
+    uint32_t mmc2_pages;       // MMC2: the cart's 1 KB CHR pages; 0 on other boards
     uint32_t ev, count;
     int32_t next;              // time of event ev (INT32_MAX when none is left)
     const uint32_t* events;
 };
+
+// MMC2: half `half`'s slots from its register and latch (patch:1385-1388)
+__device__ __forceinline__ void rp_mmc2_select(Replay& s, uint32_t half) {
+    const uint32_t reg = 2u * half + ((s.latch >> (8u * half)) & 1u);
+    const uint32_t bank = (s.creg >> (8u * reg)) & 0xFFu;
+    uint32_t pk = 0;
+    for (uint32_t i = 0; i < 4u; ++i) pk |= ((bank * 4u + i) & (s.mmc2_pages - 1u)) << (8u * i);
+    if (half) s.chr_hi = pk;
+    else s.chr_lo = pk;
+}
+// MMC2: the latch hook of a pattern fetch at a (patch:1390-1402)
+__device__ __forceinline__ void rp_hook(Replay& s, uint32_t a) {
+    const uint32_t t = mmc2_trigger(a);
+    if (t == 0) return;
+    const uint32_t half = t >> 2;
+    s.latch = (s.latch & ~(0xFFu << (8u * half))) | (((t & 3u) - 1u) << (8u * half));
+    rp_mmc2_select(s, half);
+}
 
 __device__ __forceinline__ int32_t rp_time(const Replay& s, uint32_t i) {
     return (int32_t)(s.events[2u * i] & 0xFFFFFFu) - NES_LOG_TIME_BIAS;
@@ -358,6 +404,15 @@ __device__ inline void rp_apply(Replay& s, uint32_t i, uint8_t* pal) {
         else s.chr_lo = (s.chr_lo & keep) | (val << sh);
     } else if (kind == NES_EV_MIRROR) {
         s.nt_map = val;
+    } else if (kind == NES_EV_MMC2) {   // patch:1471-1478
+        if (aux < 4u) {
+            s.creg = (s.creg & ~(0xFFu << (8u * aux))) | (val << (8u * aux));
+            rp_mmc2_select(s, aux >> 1);
+        } else if (aux == 6u || aux == 7u) {
+            const uint32_t h = aux - 6u;
+            s.latch = (s.latch & ~(0xFFu << (8u * h))) | ((val & 1u) << (8u * h));
+            rp_mmc2_select(s, h);
+        }
     }
 }
 
@@ -408,9 +463,14 @@ __device__ inline void rp_line_end(Replay& s, int l, uint8_t* pal) {
     rp_until(s, base + 320, pal);
 }
 
-// events: the log's event words (from `log` + NES_LOG_HDR_WORDS on), in place or a copy of them.
-__device__ inline void rp_begin(Replay& s, const uint32_t* log, uint32_t log_n, uint8_t* pal, const uint32_t* events) {
+// events: the log's event words (from `log` + NES_LOG_HDR_WORDS on), in place or a copy of them. mmc2_pages: the
+// cart's 1 KB CHR pages on MMC2, else 0.
+__device__ inline void rp_begin(Replay& s, const uint32_t* log, uint32_t log_n, uint8_t* pal, const uint32_t* events,
+                                uint32_t mmc2_pages) {
     const uint32_t h1 = log[1], h2 = log[2], h3 = log[3], h4 = log[4];
+    s.creg = log[14];
+    s.latch = log[15];
+    s.mmc2_pages = mmc2_pages;
     s.ctrl = h1 & 0xFFu;
     s.mask = (h1 >> 8) & 0xFFu;
     s.fx = (h1 >> 16) & 7u;
@@ -432,8 +492,10 @@ __device__ inline void rp_begin(Replay& s, const uint32_t* log, uint32_t log_n, 
     rp_line_end(s, -1, pal);
 }
 
-// Background 2-bit value at pixel x of a line drawn with state s (nametables/CHR read through the record).
-__device__ inline uint32_t rp_bg(const Replay& s, const Mem& m, uint32_t x, uint32_t* pal_sel) {
+// Background 2-bit value at pixel x of a line drawn with state s (nametables/CHR read through the record), the
+// pattern bytes through the slot pages lo/hi.
+__device__ inline uint32_t rp_bg(const Replay& s, const Mem& m, uint32_t x, uint32_t* pal_sel, uint32_t lo_pk,
+                                 uint32_t hi_pk) {
     const uint32_t pos = x + s.fx, bit = pos & 7u;
     uint32_t cx = (s.v & 31u) + (pos >> 3), nth = (s.v >> 10) & 1u;
     if (cx >= 32u) {
@@ -446,7 +508,7 @@ __device__ inline uint32_t rp_bg(const Replay& s, const Mem& m, uint32_t x, uint
     const uint32_t at = m.nt[nt_index(s.nt_map, base | 0x3C0u | ((cy >> 2) << 3) | (cx >> 2))];
     *pal_sel = (at >> (((cy & 2u) << 1) | (cx & 2u))) & 3u;
     const uint32_t pa = ((s.ctrl & 0x10u) << 8) + tile * 16u + fy;
-    const uint32_t lo = chr_byte_pk(m, s.chr_lo, s.chr_hi, pa), hi = chr_byte_pk(m, s.chr_lo, s.chr_hi, pa + 8u);
+    const uint32_t lo = chr_byte_pk(m, lo_pk, hi_pk, pa), hi = chr_byte_pk(m, lo_pk, hi_pk, pa + 8u);
     return ((lo >> (7u - bit)) & 1u) | (((hi >> (7u - bit)) & 1u) << 1);
 }
 
@@ -457,14 +519,86 @@ __device__ inline uint32_t sprite_row_addr(uint32_t ctrl, uint32_t tile, uint32_
     return ((tile & 1u) << 12) + (tile & 0xFEu) * 16u + (row & 7u) + ((row & 8u) << 1);
 }
 
-// First sprite-0 hit of the logged frame from the events logged so far (frame dot), kNoHit if none.
-__device__ __forceinline__ int32_t sprite0_scan(const Mem m, uint32_t log_n) {
+// MMC2: the pattern fetches of line l in order, each through the slot pages of the moment and then the latch hook
+// (patch:1496-1560, 1660-1700): the sprites of line l, fetched at the end of line l - 1 (l >= 1), then, unless
+// sprites_only, the line's 34 background tile slots. sink(kind, index, chr_lo, chr_hi, pa) gets the pages each
+// fetch read through and its pattern address (kind 0: sprite rank, 1: tile slot). Fetches happen only while
+// rendering is on. Wave-uniform.
+template <class Sink>
+__device__ __forceinline__ void rp_mmc2_line(Replay& s, const uint8_t* nt, const uint8_t* oam, int l, bool sprites_only,
+                                    Sink&& sink) {
+    if (s.mmc2_pages == 0 || (s.mask & 0x18u) == 0) return;
+    if (l >= 1) {
+        const int h = (s.ctrl & 0x20u) ? 16 : 8;
+        uint32_t n = 0;
+        for (uint32_t i = 0; i < 64u && n < 8u; ++i) {
+            const int row = l - (int)oam[4u * i] - 1;
+            if (row < 0 || row >= h) continue;
+            const uint32_t pa = sprite_row_addr(s.ctrl, oam[4u * i + 1u], oam[4u * i + 2u], (uint32_t)row);
+            sink(0u, n, s.chr_lo, s.chr_hi, pa);
+            rp_hook(s, pa);
+            ++n;
+        }
+    }
+    if (sprites_only) return;
+    const uint32_t cy = (s.v >> 5) & 31u, fy = (s.v >> 12) & 7u, ntv = (s.v >> 11) & 1u;
+    for (uint32_t t = 0; t < 34u; ++t) {   // one tile right per slot, the nametable switching at each wrap
+        const uint32_t cc = (s.v & 31u) + t, nth = ((s.v >> 10) & 1u) ^ ((cc >> 5) & 1u);
+        const uint32_t base = 0x2000u | ((nth | (ntv << 1)) << 10);
+        const uint32_t pa = ((s.ctrl & 0x10u) << 8) + nt[nt_index(s.nt_map, base | (cy << 5) | (cc & 31u))] * 16u + fy;
+        sink(1u, t, s.chr_lo, s.chr_hi, pa);
+        rp_hook(s, pa);
+    }
+}
+
+// First sprite-0 hit of the logged frame on MMC2 (the scan below, with each line's fetches moving the latches):
+// sprite 0 and the two tile slots under it read through the pages of their own fetches.
+__device__ inline int32_t sprite0_scan_mmc2(const Mem m, uint32_t log_n) {
     const uint8_t* oam = m.oam;
     const int y0 = oam[0], x0 = oam[3];
     if (y0 >= 239) return (int32_t)kNoHit;
     const uint32_t tile = oam[1], attr = oam[2];
     Replay s;
-    rp_begin(s, m.rec->log, log_n, nullptr, m.rec->log + NES_LOG_HDR_WORDS);
+    rp_begin(s, m.rec->log, log_n, nullptr, m.rec->log + NES_LOG_HDR_WORDS, m.cart.chr_pages1);
+    for (int l = 0; l < 240; ++l) {
+        const uint32_t slot_a = ((uint32_t)x0 + s.fx) >> 3;
+        uint32_t s0lo = s.chr_lo, s0hi = s.chr_hi, alo = s.chr_lo, ahi = s.chr_hi, blo = s.chr_lo, bhi = s.chr_hi;
+        rp_mmc2_line(s, m.nt, oam, l, false, [&](uint32_t kind, uint32_t i, uint32_t lo, uint32_t hi, uint32_t) {
+            if (kind == 0u && i == 0u) { s0lo = lo; s0hi = hi; }
+            if (kind == 1u && i == slot_a) { alo = lo; ahi = hi; }
+            if (kind == 1u && i == slot_a + 1u) { blo = lo; bhi = hi; }
+        });
+        const int h = (s.ctrl & 0x20u) ? 16 : 8;
+        const int row = l - y0 - 1;
+        if ((s.mask & 0x18u) == 0x18u && row >= 0 && row < h) {
+            const uint32_t pa = sprite_row_addr(s.ctrl, tile, attr, (uint32_t)row);
+            const uint32_t lo = chr_byte_pk(m, s0lo, s0hi, pa), hi = chr_byte_pk(m, s0lo, s0hi, pa + 8u);
+            for (int col = 0; col < 8; ++col) {
+                const int x = x0 + col;
+                if (x >= 255) break;
+                if (x < 8 && (s.mask & 0x06u) != 0x06u) continue;
+                const uint32_t b = (attr & 0x40u) ? (uint32_t)col : 7u - (uint32_t)col;
+                if ((((lo >> b) & 1u) | ((hi >> b) & 1u)) == 0) continue;
+                uint32_t ps;
+                const bool in_a = (((uint32_t)x + s.fx) >> 3) == slot_a;
+                if (rp_bg(s, m, (uint32_t)x, &ps, in_a ? alo : blo, in_a ? ahi : bhi)) return l * 341 + x + 1;
+            }
+        }
+        if (l >= y0 + 16) break;
+        rp_line_end(s, l, nullptr);
+    }
+    return (int32_t)kNoHit;
+}
+
+// First sprite-0 hit of the logged frame from the events logged so far (frame dot), kNoHit if none.
+__device__ __forceinline__ int32_t sprite0_scan(const Mem m, uint32_t log_n) {
+    if (m.cart.board == NES_BOARD_MMC2) return sprite0_scan_mmc2(m, log_n);
+    const uint8_t* oam = m.oam;
+    const int y0 = oam[0], x0 = oam[3];
+    if (y0 >= 239) return (int32_t)kNoHit;
+    const uint32_t tile = oam[1], attr = oam[2];
+    Replay s;
+    rp_begin(s, m.rec->log, log_n, nullptr, m.rec->log + NES_LOG_HDR_WORDS, 0u);
     for (int l = 0; l < 240; ++l) {
         const int h = (s.ctrl & 0x20u) ? 16 : 8;
         const int row = l - y0 - 1;
@@ -478,7 +612,7 @@ __device__ __forceinline__ int32_t sprite0_scan(const Mem m, uint32_t log_n) {
                 const uint32_t b = (attr & 0x40u) ? (uint32_t)col : 7u - (uint32_t)col;
                 if ((((lo >> b) & 1u) | ((hi >> b) & 1u)) == 0) continue;
                 uint32_t ps;
-                if (rp_bg(s, m, (uint32_t)x, &ps)) return l * 341 + x + 1;
+                if (rp_bg(s, m, (uint32_t)x, &ps, s.chr_lo, s.chr_hi)) return l * 341 + x + 1;
             }
         }
         if (l >= y0 + 16) break;
@@ -542,12 +676,38 @@ __device__ inline void log_capture(Con& c, const Mem& m) {
     h[4] = p1;
     h[5] = c.nt_map;
     for (uint32_t i = 0; i < 8; ++i) h[6 + i] = pal[i];
-    h[14] = 0;
-    h[15] = 0;
+    const uint8_t* r = m.rec->mreg;
+    const bool mmc2 = m.cart.board == NES_BOARD_MMC2;
+    h[14] = mmc2 ? (r[0] | ((uint32_t)r[1] << 8) | ((uint32_t)r[2] << 16) | ((uint32_t)r[3] << 24)) : 0u;
+    h[15] = mmc2 ? (r[6] | ((uint32_t)r[7] << 8)) : 0u;
     c.log_n = 0;
     c.log_frame = c.frame + 1u;
     c.s0_valid = 0;
     c.s0_dot = (int32_t)kNoHit;
+}
+
+// MMC2 at vblank: the latches this frame's own fetches leave, from a latches-only replay of its log over the
+// nametables and OAM as they are now (NeSLE's frame_resolve_mmc2, patch:1790-1812; rl/csrc/nes_machine.cuh:110-131
+// runs the same replay after the vblank stop, before any further instruction). Every frame the kernels run ends at
+// the vblank dot, so they call it at each frame's stop (the vblank just processed, no instruction after it).
+__device__ inline void mmc2_resolve(NesRec* rec, const uint8_t* nt, const uint8_t* oam, uint32_t log_n,
+                                    uint32_t chr_pages) {
+    Replay s;
+    rp_begin(s, rec->log, log_n, nullptr, rec->log + NES_LOG_HDR_WORDS, chr_pages);
+    const auto none = [](uint32_t, uint32_t, uint32_t, uint32_t, uint32_t) {};
+    for (int l = 0; l < 240; ++l) {
+        rp_mmc2_line(s, nt, oam, l, false, none);
+        rp_line_end(s, l, nullptr);
+    }
+    rp_mmc2_line(s, nt, oam, 240, true, none);
+    rp_until(s, INT32_MAX, nullptr);
+    const uint32_t l0 = s.latch & 1u, l1 = (s.latch >> 8) & 1u;
+    rec->mreg[6] = (uint8_t)l0;
+    rec->mreg[7] = (uint8_t)l1;
+    for (uint32_t i = 0; i < 4; ++i) {   // the halves' pages, as the board's page sync sets them
+        rec->chr_off[i] = ((4u * rec->mreg[l0] + i) & (chr_pages - 1u)) * 1024u;
+        rec->chr_off[4u + i] = ((4u * rec->mreg[2u + l1] + i) & (chr_pages - 1u)) * 1024u;
+    }
 }
 
 __device__ inline void process_events(Con& c, const Mem& m) {
@@ -627,6 +787,19 @@ __device__ inline uint32_t ppu_mem_read(const Con& c, const Mem& m, uint32_t a) 
 
 __device__ __forceinline__ uint32_t vinc(const Con& c) { return (c.ctrl & 4u) ? 32u : 1u; }
 
+// MMC2: the VRAM address the CPU drives through $2006/$2007 flips a latch; a change is logged for the renderer
+// (patch:615-636, 3196-3220).
+__device__ inline void mmc2_ppu_address(Con& c, const Mem& m, const Access& ac, uint32_t a) {
+    const uint32_t t = m.cart.board == NES_BOARD_MMC2 ? mmc2_trigger(a) : 0u;
+    if (t == 0) return;
+    const uint32_t half = t >> 2, latch = (t & 3u) - 1u;
+    uint8_t* r = m.rec->mreg;
+    if (r[6 + half] == latch) return;
+    r[6 + half] = (uint8_t)latch;
+    for (uint32_t i = 0; i < 4; ++i) map_set_chr(m, 4u * half + i, 4u * r[2u * half + latch] + i);   // the half's pages
+    log_event(c, m, ac, NES_EV_MMC2, latch, 6 + half);
+}
+
 __device__ inline uint32_t io_read(Con& c, const Mem& m, const Access& ac, uint32_t a) {
     if (a < 0x4000u) {
         const uint32_t reg = a & 7u;
@@ -641,13 +814,16 @@ __device__ inline uint32_t io_read(Con& c, const Mem& m, const Access& ac, uint3
             const uint32_t pa = c.v & 0x3FFFu;
             if (pa < 0x3F00u) {
                 v = c.read_buf;
+                mmc2_ppu_address(c, m, ac, pa);
                 c.read_buf = ppu_mem_read(c, m, pa);
             } else {
                 v = ppu_mem_read(c, m, pa);
                 c.read_buf = ppu_mem_read(c, m, pa - 0x1000u);
+                mmc2_ppu_address(c, m, ac, pa);
             }
             c.v = (c.v + vinc(c)) & 0x7FFFu;
             log_event(c, m, ac, NES_EV_DATA, 0, 1);
+            mmc2_ppu_address(c, m, ac, c.v & 0x3FFFu);
         } else {
             return c.open_bus;
         }
@@ -717,6 +893,7 @@ __device__ inline void ppu_reg_write(Con& c, const Mem& m, const Access& ac, uin
             c.t = (c.t & 0xFF00u) | v;
             c.v = c.t;
             c.w = 0;
+            mmc2_ppu_address(c, m, ac, c.v);
         }
     } else if (reg == 7) {
         const uint32_t pa = c.v & 0x3FFFu;
@@ -736,6 +913,7 @@ __device__ inline void ppu_reg_write(Con& c, const Mem& m, const Access& ac, uin
             log_event(c, m, ac, NES_EV_PAL, v & 0x3Fu, i);
         }
         c.v = (c.v + vinc(c)) & 0x7FFFu;
+        mmc2_ppu_address(c, m, ac, c.v & 0x3FFFu);
     }
 }
 
@@ -768,10 +946,16 @@ __device__ inline void io_write(Con& c, const Mem& m, Access& ac, uint32_t a, ui
         const uint32_t* co = m.rec->chr_off;
         for (uint32_t i = 0; i < 8; ++i) before[i] = co[i];
         const uint32_t map_before = c.nt_map;
+        const uint32_t creg_before = *reinterpret_cast<const uint32_t*>(m.rec->mreg);
         map_write(c, m, a, v);
         for (uint32_t i = 0; i < 8; ++i)
             if (co[i] != before[i]) log_event(c, m, ac, NES_EV_CHR, co[i] >> 10, i);
         if (c.nt_map != map_before) log_event(c, m, ac, NES_EV_MIRROR, c.nt_map, 0);
+        if (m.cart.board == NES_BOARD_MMC2)   // patch:661-664
+            for (uint32_t i = 0; i < 4; ++i) {
+                const uint32_t now = m.rec->mreg[i];
+                if (now != ((creg_before >> (8u * i)) & 0xFFu)) log_event(c, m, ac, NES_EV_MMC2, now, i);
+            }
     } else if (a >= 0x6000u) {
         if (prg_ram_on(m)) m.rec->prg_ram[a - 0x6000u] = (uint8_t)v;
     }
@@ -1062,6 +1246,9 @@ __device__ inline void power_on(NesRec* rec, const Cart& cart) {
     } else if (cart.board == NES_BOARD_MMC3) {
         r[1] = 2; r[2] = 4; r[3] = 5; r[4] = 6; r[5] = 7; r[7] = 1;
         r[9] = cart.mirroring ? 0 : 1;
+    } else if (cart.board == NES_BOARD_MMC2) {
+        r[6] = 1;   // both latches on the $FE bank (patch:3080-3083)
+        r[7] = 1;
     }
     map_sync(c, m);
     for (uint32_t i = 0; i < NES_RAM_BYTES; ++i) rec->ram[i] = 0xFF;

@@ -188,6 +188,8 @@ __global__ __launch_bounds__(64) void k_emu(EmuArgs a) {
                 if (f != 0) {
                     if (a.mode == EMU_BOOT) atomicOr(a.boot_fault, 1u);
                     else a.e.fault[ge] = f;
+                } else if (a.g.cart.board == NES_BOARD_MMC2 && c.frame == c.log_frame) {   // the vblank stop
+                    mmc2_resolve(rec, m.nt, m.oam, c.log_n, a.g.cart.chr_pages1);
                 }
             }
             con_store(c, rec);
@@ -276,6 +278,9 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(8, 8))) void
                     if (a.mode == EMU_BOOT) atomicOr(a.boot_fault, 1u);
                     else a.e.fault[ge] = f;
                     fault = f;
+                } else if constexpr (B != NES_BOARD_NROM) {   // MMC2 at the vblank stop (no log: first frame)
+                    if (a.g.cart.board == NES_BOARD_MMC2 && cs.frame == cs.log_frame)
+                        mmc2_resolve(rec, L.nt, L.oam, cs.log_n, a.g.cart.chr_pages1);
                 }
             }
             target += NES_FRAME_DOTS;
@@ -319,15 +324,27 @@ __device__ __forceinline__ uint32_t nibbles8(uint32_t b) {
 // one ballot over the 64 OAM entries, and lines 8..231, columns 8..247 go out as one 240-byte row store each
 // (rl/csrc/nes_machine.cuh:133-155). nt/oam: the console's nametables and OAM as of the frame's vblank (LDS);
 // pal: 32 bytes of LDS for the replayed palette; ev_s: the log's events, copied to LDS.
+template <bool kMmc2>
 __device__ __forceinline__ void render_wave(const NesRec* rec, uint32_t log_n, const uint8_t* nt_s, const uint8_t* oam_s,
                                             uint8_t* pal_s, const uint32_t* ev_s, uint32_t* spr_s, uint32_t* slot_s,
-                                            uint32_t* tile_s, const Cart& cart, uint8_t* obs, uint8_t* emph, int lane) {
+                                            uint32_t* tile_s, uint32_t* mk_s, const Cart& cart, uint8_t* obs,
+                                            uint8_t* emph, int lane) {
     Replay s;   // wave-uniform: every lane replays the same log (and stores the same palette bytes)
-    rp_begin(s, rec->log, log_n, pal_s, ev_s);
+    rp_begin(s, rec->log, log_n, pal_s, ev_s, kMmc2 ? cart.chr_pages1 : 0u);
+    constexpr bool mmc2 = kMmc2;
     __syncthreads();
     const Mem m = mem_of(const_cast<NesRec*>(rec), nullptr, cart);
     const uint32_t my_sy = oam_s[4 * lane];
     for (int l = 0; l < 232; ++l) {
+        const uint32_t line_lo = s.chr_lo, line_hi = s.chr_hi;
+        if constexpr (mmc2) {
+            // the line's fetches in order, each through the pages of the moment: mk_s[k] (sprite rank k) and
+            // mk_s[8 + t] (tile slot t) hold the 4 slot pages of the half the fetch's address is in
+            rp_mmc2_line(s, nt_s, oam_s, l, false, [&](uint32_t kind, uint32_t i, uint32_t lo, uint32_t hi, uint32_t pa) {
+                if (lane == 0) mk_s[kind ? 8u + i : i] = (pa & 0x1000u) ? hi : lo;
+            });
+            __syncthreads();
+        }
         if (l >= 8) {
             const uint32_t mask = s.mask, ctrl = s.ctrl;
             const bool bg_on = (mask & 0x08u) != 0, sp_on = (mask & 0x10u) != 0;
@@ -350,8 +367,10 @@ __device__ __forceinline__ void render_wave(const NesRec* rec, uint32_t log_n, c
                     const uint32_t at = nt_s[nt_index(s.nt_map, base | 0x3C0u | ((cy >> 2) << 3) | ((cx & 31u) >> 2))];
                     const uint32_t ps = (at >> (((cy & 2u) << 1) | (cx & 2u))) & 3u;
                     const uint32_t pa = ((ctrl & 0x10u) << 8) + tile * 16u + fy;
-                    const uint32_t lo = chr_byte_pk(m, s.chr_lo, s.chr_hi, pa);
-                    const uint32_t hi = chr_byte_pk(m, s.chr_lo, s.chr_hi, pa + 8u);
+                    const uint32_t plo = mmc2 ? mk_s[8 + lane] : line_lo;   // the fetch reads only its own half
+                    const uint32_t phi = mmc2 ? mk_s[8 + lane] : line_hi;
+                    const uint32_t lo = chr_byte_pk(m, plo, phi, pa);
+                    const uint32_t hi = chr_byte_pk(m, plo, phi, pa + 8u);
                     tile_s[lane] = nibbles8(lo) | (nibbles8(hi) << 1) | (ps * 0x44444444u);
                 }
                 __syncthreads();
@@ -382,8 +401,10 @@ __device__ __forceinline__ void render_wave(const NesRec* rec, uint32_t log_n, c
                     const uint32_t e = reinterpret_cast<const uint32_t*>(oam_s)[i];
                     const uint32_t sy = e & 0xFFu, tile = (e >> 8) & 0xFFu, attr = (e >> 16) & 0xFFu, sx = e >> 24;
                     const uint32_t pa = sprite_row_addr(ctrl, tile, attr, (uint32_t)(l - (int)sy - 1));
-                    const uint32_t plo = chr_byte_pk(m, s.chr_lo, s.chr_hi, pa);
-                    const uint32_t phi = chr_byte_pk(m, s.chr_lo, s.chr_hi, pa + 8u);
+                    const uint32_t kp = mmc2 ? mk_s[k] : 0u;   // the fetch reads only its own half
+                    const uint32_t klo = mmc2 ? kp : line_lo, khi = mmc2 ? kp : line_hi;
+                    const uint32_t plo = chr_byte_pk(m, klo, khi, pa);
+                    const uint32_t phi = chr_byte_pk(m, klo, khi, pa + 8u);
                     const uint32_t b = (attr & 0x40u) ? px : 7u - px;
                     const uint32_t v = ((plo >> b) & 1u) | (((phi >> b) & 1u) << 1);
                     const uint32_t x = sx + px;
@@ -419,6 +440,7 @@ __device__ __forceinline__ void render_wave(const NesRec* rec, uint32_t log_n, c
 }
 
 // One console-frame per wavefront (blockDim 64).
+template <bool kMmc2>
 __global__ __launch_bounds__(64) void k_render(RenderArgs a) {
     __shared__ __align__(16) uint8_t nt_s[2048];
     __shared__ __align__(16) uint8_t oam_s[256];
@@ -426,7 +448,10 @@ __global__ __launch_bounds__(64) void k_render(RenderArgs a) {
     __shared__ __align__(16) uint32_t ev_s[2 * NES_LOG_EVENTS];
     __shared__ __align__(16) uint32_t spr_s[256];   // the line's sprite pixels (0 = none)
     __shared__ uint32_t slot_s[8];
-    __shared__ uint32_t tile_s[34];                 // the line's background tile slots
+    // MMC2: the pages of the line's sprite fetches (0-7) and tile fetches (8-41); the line's background tile slots
+    // (tile_s) take the place of the tile fetches' pages, each lane reading its slot's pages before it writes it
+    __shared__ uint32_t mk_s[8 + 34];
+    uint32_t* tile_s = mk_s + 8;
     const int count = slot_count(a.g, a.use_list, a.e0, a.e1);
     const int k = (int)blockIdx.x;
     if (k >= count) return;
@@ -444,7 +469,7 @@ __global__ __launch_bounds__(64) void k_render(RenderArgs a) {
     __syncthreads();
     uint8_t* obs = a.o.obs + ((size_t)ge * RLE_FRAMES + a.f) * RLE_OBS_PIXELS;
     uint8_t* emph = a.o.emph + ((size_t)ge * RLE_FRAMES + a.f) * RLE_OBS_H;
-    render_wave(rec, log_n, nt_s, oam_s, pal_s, ev_s, spr_s, slot_s, tile_s, a.g.cart, obs, emph, lane);
+    render_wave<kMmc2>(rec, log_n, nt_s, oam_s, pal_s, ev_s, spr_s, slot_s, tile_s, mk_s, a.g.cart, obs, emph, lane);
 }
 
 // ----------------------------------------------------------------------------------------- finish
@@ -947,9 +972,10 @@ Parsed parse_ines(const uint8_t* rom, size_t size) {
     const uint32_t mapper = (rom[6] >> 4) | (rom[7] & 0xF0u);
     const size_t skip = 16u + ((rom[6] & 4u) ? 512u : 0u);
     if (rom[6] & 8u) throw std::runtime_error("four-screen nametables are not supported");
-    if (mapper > 4u)
+    if (mapper > 4u && mapper != 9u)
         throw std::runtime_error("unsupported mapper " + std::to_string(mapper) +
-                                 " (supported: 0 NROM, 1 MMC1, 2 UxROM, 3 CNROM, 4 MMC3)");
+                                 " (supported: 0 NROM, 1 MMC1, 2 UxROM, 3 CNROM, 4 MMC3, 9 MMC2)");
+    if (mapper == 9u && chr == 0) throw std::runtime_error("MMC2 needs CHR ROM");
     if (prg == 0 || skip + prg + chr > size) throw std::runtime_error("truncated iNES image");
     Parsed p;
     size_t padded = 8192;
@@ -957,7 +983,7 @@ Parsed parse_ines(const uint8_t* rom, size_t size) {
     p.prg.resize(padded);
     for (size_t o = 0; o < padded; o += prg) std::memcpy(p.prg.data() + o, rom + skip, std::min(prg, padded - o));
     p.chr.assign(rom + skip + prg, rom + skip + prg + chr);
-    p.board = mapper;
+    p.board = mapper == 9u ? NES_BOARD_MMC2 : mapper;
     p.mirroring = rom[6] & 1u;
     // UxROM / CNROM bus conflicts only when the header declares them: NES 2.0, submapper 2 (patch:4008)
     p.bus_conflicts = (mapper == 2u || mapper == 3u) && (rom[7] & 0x0Cu) == 0x08u && (rom[8] >> 4) == 2u;
@@ -1022,7 +1048,10 @@ void launch_render(const Env& env, const GameK& g, const Outs& o, int f, bool us
     const int n = use_list ? g.n : e1 - e0;
     if (n > 0)
         env.clock.run(restart ? KC_RENDER_RESTART : KC_RENDER, st,
-                      [&] { hipLaunchKernelGGL(k_render, dim3(n), dim3(64), 0, st, a); });
+                      [&] {
+                          if (g.cart.board == NES_BOARD_MMC2) hipLaunchKernelGGL(k_render<true>, dim3(n), dim3(64), 0, st, a);
+                          else hipLaunchKernelGGL(k_render<false>, dim3(n), dim3(64), 0, st, a);
+                      });
     trace(restart ? "render_restart" : "render", st);
 }
 

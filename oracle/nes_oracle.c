@@ -524,11 +524,9 @@ static uint8_t nt_read(const NesRec* r, const Replay* s, uint32_t addr) { /* add
 
 /* Pattern address (low plane) of background tile slot `slot` (0..33) of the line drawn with state s. */
 static uint32_t bg_slot_pa(const NesRec* r, const Replay* s, uint32_t slot) {
-    uint32_t cx = (s->v & 31u) + slot, nth = (s->v >> 10) & 1u;
-    if (cx >= 32u) {
-        cx -= 32u;
-        nth ^= 1u;
-    }
+    /* the fetch address moves right one tile per slot, switching nametables at each wrap (twice for slot 33
+     * from column 31) */
+    const uint32_t cc = (s->v & 31u) + slot, cx = cc & 31u, nth = ((s->v >> 10) & 1u) ^ ((cc >> 5) & 1u);
     const uint32_t cy = (s->v >> 5) & 31u, fy = (s->v >> 12) & 7u, ntv = (s->v >> 11) & 1u;
     const uint32_t base = 0x2000u | ((nth | (ntv << 1)) << 10);
     return ((s->ctrl & 0x10u) << 8) + nt_read(r, s, base | (cy << 5) | cx) * 16u + fy;

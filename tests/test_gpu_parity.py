@@ -102,3 +102,12 @@ def test_mmc1_from_power_on():
           flush=True)
     cpu, gpu = pair(8, synth.mmc1_cart(3), seed=18, sticky=False, idle_max=0, dropout=False, pad_mode=True)
     run(cpu, gpu, 12, 4, True)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize('seed', [1, 2])
+def test_mmc2_latches_follow_the_fetches(seed):
+    print(f'case: MMC2 seed {seed}, 16 consoles, raw pads, $FD/$FE tiles in nametables and sprites, CHR bank and '
+          'mirroring rewrites, CPU-driven latch flips, 16 decisions', flush=True)
+    cpu, gpu = pair(16, synth.mmc2_cart(seed), seed=20 + seed, sticky=True, idle_max=2, dropout=False, pad_mode=True)
+    run(cpu, gpu, 16, 7 + seed, True)
