@@ -23,7 +23,7 @@ extern "C" {
  * Replaces rl/csrc/rlenv_api.h:10-12 (rlenv.cu:188-217). game_ids: reward10 game ids 0..11 (smb, pacman,
  * excitebike, contra, castlevania, gradius, zelda, tetris, tecmobowl, kage, finalmission, punchout; the order of
  * rl/games_manifest.json), each choosing the reward reader and the Start/Select legality. roms: iNES images
- * (mappers 0-4). device: HIP device index. */
+ * (mappers 0-4 and 9). device: HIP device index. */
 void* rlenv_create(int ngames, const int* game_ids, const uint8_t* const* roms, const size_t* rom_sizes,
                    const uint8_t* const* boot_pads, const size_t* boot_sizes, const int* n_envs, uint64_t run_seed,
                    int sticky, int idle_max, int dropout, int device);
