@@ -2,7 +2,7 @@
  *
  * Scalar CPU restatement of one NES console on the env's hot path: 6502 (official opcodes; any other
  * opcode is a fault), bus, PPU timing with the frame log, the line-replay renderer, sprite-0 hit,
- * NROM/MMC1/MMC3, DMC, controller port. It exists to check the HIP library bit for bit; nothing in the
+ * NROM/MMC1/UxROM/CNROM/MMC3/MMC2, DMC, controller port. It exists to check the HIP library bit for bit; nothing in the
  * product links it. Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg may load it.
  *
  * Reference behaviour followed (file:line in kdcyberdude/ghostrun-lab):
@@ -16,10 +16,16 @@
  *   PPU events ............ patch:1822-2240 (vblank 82182, pre-render 89002 + log capture, MMC3 clocks at
  *                           dot 266 on lines 0-239 and dot 256 on the pre-render line, sprite-0 event)
  *   frame log ............. patch:894-1185 (header at pre-render, dot-stamped PPU-visible writes)
- *   mappers ............... patch:2841-3367 (MMC1 serial port/modes, MMC3 R0-R7/modes/IRQ rev B, WRAM enable)
+ *   mappers ............... patch:2841-3367 (MMC1 serial port/modes, MMC3 R0-R7/modes/IRQ rev B, WRAM enable,
+ *                           CNROM/UxROM latches, MMC2 registers)
+ *   MMC2 latches .......... patch:615-664, 3196-3220 (CPU-driven flips), 1385-1402, 1496-1560, 1660-1700 (the
+ *                           hook after each replayed pattern fetch), 1790-1812 (the vblank resolve)
  *   obs crop .............. rl/csrc/nes_machine.cuh:133-155 (lines 8..231, x 8..247, & 0x3F, emph = mask>>5&7)
  * The 6502 core itself is upstream NeSLE (not in the reference tree): parity with it is unpinned; the
  * oracle is pinned by datasheet known-answer tests instead (tests/test_oracle_cpu6502.py).
+ * MMC2: registers, CPU-driven flips and the fetch-then-flip order along a line are pinned by known-answer tests
+ * (tests/test_oracle_mappers.py); the vblank resolve and the order of hblank-time MMC2 events against the next
+ * line's sprite fetch are parity unpinned (no golden vector of the reference covers them).
  */
 #ifndef NES_ORACLE_H
 #define NES_ORACLE_H
