@@ -42,23 +42,45 @@
 #define NES_BOARD_MMC2 5u                     /* mapper 9: 8 KB PRG bank at $8000, 4 KB CHR halves picked by the
                                                  $FD/$FE latches (patch:3027-3035, 3147-3156) */
 
-/* Frame-log event kinds (word 0 bits 24..31). Word 0 bits 0..23: event time + NES_LOG_TIME_BIAS, where the
- * event time is in dots from the start of line 0 of the logged frame (pre-render line: negative).
- * Word 1: value | aux << 8. */
-#define NES_LOG_TIME_BIAS 1024
+/* Frame timing of the renderer's line grid (FCEUmm's, which the reference replays the log on,
+ * third_party/nesle-extensions.patch:940-965). A log event is stamped with the NeSLE frame dot at which its
+ * instruction starts and the instruction's cycles; on the replay grid it sits NES_FCEU_LAG dots later, and the
+ * pre-render line's writes are counted back from line 0 (one dot more on a "kook" frame, whose pre-render line is a
+ * dot short). Line l of the replay starts NES_LINE_LEAD dots before the line's dot 0. */
+#define NES_FCEU_LAG 11
+#define NES_LINE_LEAD 16
+#define NES_VFLAG_DOT (NES_VBLANK_DOT - 12u)      /* 82170: $2002 bit 7 set (patch:1940-1945) */
+#define NES_SCLR_DOT (NES_PRERENDER_DOT - 12u)    /* 88990: $2002 bits 5-7 cleared */
+
+/* Frame-log events: two words each. Word 0: kind (bits 0-3) | instruction cycles, at most 15 (bits 4-7) |
+ * NeSLE frame dot of the instruction's start (bits 8-24). Word 1: value | aux << 8. */
 #define NES_EV_CTRL 1u    /* $2000 */
 #define NES_EV_MASK 2u    /* $2001 */
 #define NES_EV_SCROLL 3u  /* $2005, aux = write toggle before the write */
 #define NES_EV_ADDR 4u    /* $2006, aux = write toggle before the write */
-#define NES_EV_DATA 5u    /* $2007 access below the palette: address increments, aux = count */
-#define NES_EV_PAL 6u     /* $2007 palette write: value, aux = palette index (after mirroring) */
+#define NES_EV_DATA 5u    /* $2007 write below the palette: address increment; aux = further writes merged into it */
+#define NES_EV_PAL 6u     /* $2007 palette write: value, aux = palette index (after mirroring); address increment */
 #define NES_EV_CHR 7u     /* CHR 1 KB page change: value = page, aux = slot 0..7 */
 #define NES_EV_MIRROR 8u  /* nametable map change: value = nt_map packed 4 x 2 bits */
 #define NES_EV_MMC2 9u    /* MMC2 register change: value, aux = register (0-3 CHR banks, 6-7 latches) */
+#define NES_EV_DREAD 10u  /* $2007 read: address increment (a vertical step while a line is drawn) */
+#define NES_EV_WORD0(kind, dot) ((uint32_t)(kind) | ((uint32_t)(dot) << 8))
 
 /* Log header words: 0 count | overflow << 31, 1 ctrl | mask << 8 | fine x << 16, 2 v | t << 16,
- * 3-4 CHR 1 KB page of each slot (8 bits each), 5 nt_map packed, 6-13 palette RAM, 14 MMC2 CHR registers
- * (8 bits each), 15 MMC2 latch 0 | latch 1 << 8 (zero on other boards). */
+ * 3-4 CHR 1 KB page of each slot (8 bits each), 5 nt_map packed | kook frame << 8, 6-13 palette RAM,
+ * 14 MMC2 CHR registers (8 bits each), 15 MMC2 latch 0 | latch 1 << 8 (zero on other boards). */
+#define NES_LOG_KOOK 0x100u
+
+/* s0_sched: the frame dot of the next sprite-0 check (bits 0-16), 0 = none this frame; once a check has run and
+ * left a later dot: the answer it found (NES_S0_KNOWN, NES_S0_HIT) and the log length it saw (bits 20-28). */
+#define NES_S0_DOT 0x1FFFFu
+#define NES_S0_HIT 0x20000000u
+#define NES_S0_KNOWN 0x40000000u
+
+/* log_flags */
+#define NES_LOG_NEXT_KOOK 1u   /* the next frame captured is a kook frame */
+#define NES_LOG_SHORT 2u       /* this frame's pre-render line is a dot short (from its capture to the wrap) */
+
 #define NES_LOG_OVERFLOW 0x80000000u
 
 typedef struct NesRec {
@@ -78,10 +100,10 @@ typedef struct NesRec {
     uint16_t v, t;
     uint8_t ctrl, mask, status, oam_addr;
     uint8_t fx, w, read_buf, open_bus;
-    int32_t s0_dot;       /* frame dot of this frame's sprite-0 hit, NES_NO_HIT = none */
+    uint32_t s0_sched;    /* next sprite-0 check (NES_S0_*) */
     uint32_t log_frame;   /* frame whose lines the log describes */
     uint16_t log_n;
-    uint8_t s0_valid;     /* 1: s0_dot is computed for the events logged so far */
+    uint8_t log_flags;    /* NES_LOG_NEXT_KOOK, NES_LOG_SHORT */
     uint8_t board;
     uint64_t _ppu_res;
     /* ---- DMC (0x40) ---- */

@@ -14,8 +14,6 @@
 #define FL_V 0x40u
 #define FL_N 0x80u
 
-#define PRE_LINE_START (-341)
-#define LOG_WINDOW_START (-340) /* pre-render dot 1 */
 
 uint64_t orc_splitmix64(uint64_t x) {
     x += 0x9E3779B97F4A7C15ull;
@@ -340,6 +338,9 @@ static void dmc_write(NesRec* r, uint16_t addr, uint8_t v) {
 
 /* ------------------------------------------------------------------------------------------- power-on */
 
+static void log_header(NesRec* r, int kook);
+
+
 void orc_power_on(NesRec* r, const NesCart* c) {
     memset(r, 0, sizeof(*r));
     r->board = c->board;
@@ -350,50 +351,94 @@ void orc_power_on(NesRec* r, const NesCart* c) {
     const uint32_t lo = c->prg[r->prg_off[3] + 0x1FFCu], hi = c->prg[r->prg_off[3] + 0x1FFDu];
     r->pc = (uint16_t)(lo | (hi << 8));
     r->cycles = 7;
-    r->s0_dot = NES_NO_HIT;
-    r->s0_valid = 0;
     orc_dmc_reset(r, r->cycles);
-    /* the log of frame 0 starts from the power-on PPU state */
-    uint32_t* h = r->log;
-    h[1] = 0;
-    h[2] = 0;
-    for (int i = 0; i < 8; ++i) h[3 + (i >> 2)] |= ((r->chr_off[i] >> 10) & 0xFFu) << ((i & 3) * 8);
-    h[5] = nt_map_packed(r);
-    r->log_frame = 0;
+    log_header(r, 0);   /* frame 0 is logged from the power-on state (patch:1160-1166) */
 }
 
 /* ------------------------------------------------------------------------------------- frame log + replay */
 
-static void log_capture(NesRec* r) {
+/* The frame log's header from the live PPU and board state (patch:1073-1105): taken at the pre-render line, and
+ * at power-on for the first frame. */
+static void log_header(NesRec* r, int kook) {
     uint32_t* h = r->log;
     memset(h, 0, NES_LOG_HDR_WORDS * 4u);
     h[1] = r->ctrl | ((uint32_t)r->mask << 8) | ((uint32_t)r->fx << 16);
     h[2] = r->v | ((uint32_t)r->t << 16);
     for (int i = 0; i < 8; ++i) h[3 + (i >> 2)] |= ((r->chr_off[i] >> 10) & 0xFFu) << ((i & 3) * 8);
-    h[5] = nt_map_packed(r);
+    h[5] = nt_map_packed(r) | (kook ? NES_LOG_KOOK : 0u);
+    for (int i = 0; i < 8; ++i)
+        h[6 + i] = r->pal[4 * i] | ((uint32_t)r->pal[4 * i + 1] << 8) | ((uint32_t)r->pal[4 * i + 2] << 16) |
+                   ((uint32_t)r->pal[4 * i + 3] << 24);
     if (r->board == NES_BOARD_MMC2) {
         h[14] = r->mreg[0] | ((uint32_t)r->mreg[1] << 8) | ((uint32_t)r->mreg[2] << 16) | ((uint32_t)r->mreg[3] << 24);
         h[15] = r->mreg[6] | ((uint32_t)r->mreg[7] << 8);
     }
-    for (int i = 0; i < 8; ++i)
-        h[6 + i] = r->pal[4 * i] | ((uint32_t)r->pal[4 * i + 1] << 8) | ((uint32_t)r->pal[4 * i + 2] << 16) |
-                   ((uint32_t)r->pal[4 * i + 3] << 24);
-    r->log_n = 0;
-    r->log_frame = r->frame + 1u;
-    r->s0_valid = 0;
-    r->s0_dot = NES_NO_HIT;
 }
 
+/* Pre-render line: the log starts over for the next frame; every other frame is a kook frame, whose pre-render
+ * line is a dot short (patch:1111-1122). */
+static void log_capture(NesRec* r) {
+    const int kook = (r->log_flags & NES_LOG_NEXT_KOOK) != 0;
+    log_header(r, kook);
+    r->log_n = 0;
+    r->log_frame = r->frame + 1u;
+    r->log_flags = (uint8_t)(((r->log_flags ^ NES_LOG_NEXT_KOOK) & ~NES_LOG_SHORT) | (kook ? NES_LOG_SHORT : 0u));
+}
+
+/* Replay time of NeSLE frame dot `dot`: line 0 dot 0 is 0, the pre-render line negative (patch:950-956). */
+static int32_t fceu_time(uint32_t dot, int kook) {
+    return dot >= NES_PRERENDER_DOT ? (int32_t)dot - (int32_t)NES_FRAME_DOTS + NES_FCEU_LAG + kook
+                                    : (int32_t)dot + NES_FCEU_LAG;
+}
+
+/* Up to eight sprites of one line: pattern bytes, attributes and x (FCEUmm's sprite line buffer). */
+typedef struct SprLine {
+    uint32_t n;
+    uint8_t lo[8], hi[8], attr[8], x[8];
+} SprLine;
+
+/* The renderer's state between lines (patch:1289-1313): the PPU registers it has replayed, the board's CHR and
+ * nametable wiring, the background shift registers, the sprite line fetched for the next line and the one it
+ * draws, and the sprite-0 check. */
 typedef struct Replay {
+    const NesRec* r;
+    const NesCart* c;
+    const uint32_t* ev;
+    uint32_t count, cur;
+    int kook;
     uint32_t v, t, fx, ctrl, mask;
-    uint8_t pal[32];
     uint32_t chr_off[8];
     uint8_t nt_map[4];
-    uint32_t ev, count;
-    const uint32_t* events;
-    int mmc2;                        /* MMC2: the CHR halves follow creg and the latches */
+    int mmc2;
     uint32_t creg[4], latch[2], chr_pages;
+    uint8_t pal[32];
+    uint32_t sh_lo, sh_hi, at;       /* pattern shift registers (last two tiles fetched), attribute latch */
+    SprLine fetched, drawn;
+    uint8_t spal[16];
+    int blurp;                       /* sprite 0 is in the fetched line */
+    int spork;                       /* a sprite line waits to be drawn */
+    int hit, hit_x;                  /* $2002 bit 6 of the replay and the pixel where it was found */
+    int sphitx;                      /* x of sprite 0 on this line, NO_CHECK = no check */
+    uint32_t sphit_bits;             /* its opaque pixels, leftmost in bit 7 */
 } Replay;
+#define NO_CHECK 0x100
+
+/* One line's pixels: the palette value, 0x40 | backdrop where the background is transparent, 0xFF not drawn yet;
+ * the next tile slot, the output position and whether the line's vertical step is still due. */
+typedef struct Line {
+    uint8_t px[256];
+    int tile, out, fix;
+} Line;
+
+static uint32_t ev_kind(const Replay* s, uint32_t i) { return s->ev[2u * i] & 15u; }
+static int32_t ev_start(const Replay* s, uint32_t i) {
+    return fceu_time((s->ev[2u * i] >> 8) & 0x1FFFFu, s->kook);
+}
+/* The end of the event's instruction: its accesses are stamped there (patch:1336-1338). */
+static int32_t ev_end(const Replay* s, uint32_t i) { return ev_start(s, i) + 3 * (int32_t)((s->ev[2u * i] >> 4) & 15u); }
+
+static int rendering(const Replay* s) { return (s->mask & 0x18u) != 0; }
+static uint32_t inc_of(const Replay* s) { return (s->ctrl & 4u) ? 32u : 1u; }
 
 static void replay_mmc2_select(Replay* s, uint32_t half) { /* patch:1385-1388 */
     const uint32_t bank = s->creg[2u * half + s->latch[half]];
@@ -407,15 +452,30 @@ static void replay_hook(Replay* s, uint32_t a) { /* a pattern fetch at a (patch:
     replay_mmc2_select(s, t >> 2);
 }
 
-static int32_t ev_time(const Replay* s, uint32_t i) {
-    return (int32_t)(s->events[2 * i] & 0xFFFFFFu) - NES_LOG_TIME_BIAS;
+static uint8_t rp_chr(const Replay* s, uint32_t a) { return chr_read(s->r, s->c, s->chr_off, a & 0x1FFFu); }
+static uint8_t rp_nt(const Replay* s, uint32_t a) {
+    return s->r->nt[(s->nt_map[(a >> 10) & 3u] & 1u) * 1024u + (a & 0x3FFu)];
 }
 
-static void replay_apply(Replay* s, uint32_t i) {
-    const uint32_t kind = s->events[2 * i] >> 24, w1 = s->events[2 * i + 1];
-    const uint32_t val = w1 & 0xFFu, aux = (w1 >> 8) & 0xFFu;
-    const uint32_t inc = (s->ctrl & 4u) ? 32u : 1u;
-    switch (kind) {
+/* v one row down (FCEUmm's Fixit1, and a $2007 read while a line is drawn; patch:1410-1422). */
+static void y_step(Replay* s) {
+    uint32_t v = s->v;
+    if ((v & 0x7000u) != 0x7000u) {
+        v += 0x1000u;
+    } else {
+        v &= ~0x7000u;
+        const uint32_t row = (v >> 5) & 31u;
+        if (row == 29u) v = (v & ~0x03E0u) ^ 0x0800u;
+        else if (row == 31u) v &= ~0x03E0u;
+        else v += 0x20u;
+    }
+    s->v = v & 0x7FFFu;
+}
+
+/* Event i on the replay state (patch:1424-1481). `drawing`: a line is being drawn. */
+static void replay_apply(Replay* s, uint32_t i, int drawing) {
+    const uint32_t w1 = s->ev[2u * i + 1u], val = w1 & 0xFFu, aux = (w1 >> 8) & 0xFFu;
+    switch (ev_kind(s, i)) {
         case NES_EV_CTRL: s->ctrl = val; s->t = (s->t & 0xF3FFu) | ((val & 3u) << 10); break;
         case NES_EV_MASK: s->mask = val; break;
         case NES_EV_SCROLL:
@@ -434,16 +494,20 @@ static void replay_apply(Replay* s, uint32_t i) {
                 s->v = s->t;
             }
             break;
-        case NES_EV_DATA: s->v = (s->v + aux * inc) & 0x7FFFu; break;
+        case NES_EV_DATA: s->v = (s->v + (aux + 1u) * inc_of(s)) & 0x7FFFu; break;
+        case NES_EV_DREAD:
+            if (drawing && rendering(s)) y_step(s);
+            else s->v = (s->v + inc_of(s)) & 0x7FFFu;
+            break;
         case NES_EV_PAL:
             s->pal[aux & 31u] = (uint8_t)val;
-            s->v = (s->v + inc) & 0x7FFFu;
+            s->v = (s->v + inc_of(s)) & 0x7FFFu;
             break;
         case NES_EV_CHR: s->chr_off[aux & 7u] = val * 1024u; break;
         case NES_EV_MIRROR:
             for (int k = 0; k < 4; ++k) s->nt_map[k] = (uint8_t)((val >> (2 * k)) & 3u);
             break;
-        case NES_EV_MMC2: /* patch:1471-1478 */
+        case NES_EV_MMC2:
             if (aux < 4u) {
                 s->creg[aux] = val;
                 replay_mmc2_select(s, aux >> 1);
@@ -456,344 +520,404 @@ static void replay_apply(Replay* s, uint32_t i) {
     }
 }
 
-static void replay_until(Replay* s, int32_t time) { /* events strictly before `time` */
-    while (s->ev < s->count && ev_time(s, s->ev) < time) replay_apply(s, s->ev++);
-}
-
-static int rendering(const Replay* s) { return (s->mask & 0x18u) != 0; }
-
-static void y_increment(Replay* s) {
-    if ((s->v & 0x7000u) != 0x7000u) {
-        s->v += 0x1000u;
-    } else {
-        s->v &= ~0x7000u;
-        uint32_t y = (s->v >> 5) & 31u;
-        if (y == 29u) {
-            y = 0;
-            s->v ^= 0x0800u;
-        } else if (y == 31u) {
-            y = 0;
-        } else {
-            ++y;
-        }
-        s->v = (s->v & ~0x03E0u) | (y << 5);
-    }
-}
-
-/* Line l's internal operations after its pixels: Y increment at dot 256, horizontal copy at 257; on the
- * pre-render line (l = -1) also the vertical copy (taken at dot 304); then the state at dot 320 is the one
- * line l + 1 is drawn with. */
-static void replay_line_end(Replay* s, int l) {
-    const int32_t base = l * 341;
-    replay_until(s, base + 256);
-    if (rendering(s)) y_increment(s);
-    replay_until(s, base + 257);
-    if (rendering(s)) s->v = (s->v & ~0x041Fu) | (s->t & 0x041Fu);
-    if (l < 0) {
-        replay_until(s, base + 304);
-        if (rendering(s)) s->v = (s->v & ~0x7BE0u) | (s->t & 0x7BE0u);
-    }
-    replay_until(s, base + 320);
-}
-
-static void replay_begin(Replay* s, const NesRec* r, const NesCart* c) {
+/* The replay of the console's logged frame, from its header (patch:1361-1383), over the console's nametables and
+ * OAM as they are now; `n` events of the log. */
+static void replay_load(Replay* s, const NesRec* r, const NesCart* c, uint32_t n) {
+    memset(s, 0, sizeof(*s));
     const uint32_t* h = r->log;
+    s->r = r;
+    s->c = c;
+    s->ev = h + NES_LOG_HDR_WORDS;
+    s->count = n < NES_LOG_EVENTS ? n : NES_LOG_EVENTS;
+    s->kook = (h[5] & NES_LOG_KOOK) != 0;
+    s->ctrl = h[1] & 0xFFu;
+    s->mask = (h[1] >> 8) & 0xFFu;
+    s->fx = (h[1] >> 16) & 7u;
+    s->v = h[2] & 0x7FFFu;
+    s->t = (h[2] >> 16) & 0x7FFFu;
+    for (int i = 0; i < 8; ++i) s->chr_off[i] = ((h[3 + (i >> 2)] >> ((i & 3) * 8)) & 0xFFu) * 1024u;
+    for (int k = 0; k < 4; ++k) s->nt_map[k] = (uint8_t)((h[5] >> (2 * k)) & 3u);
+    for (int i = 0; i < 32; ++i) s->pal[i] = (uint8_t)(h[6 + (i >> 2)] >> ((i & 3) * 8));
     s->mmc2 = c->board == NES_BOARD_MMC2;
     s->chr_pages = c->chr_size / 1024u;
     for (int i = 0; i < 4; ++i) s->creg[i] = (h[14] >> (8 * i)) & 0xFFu;
     s->latch[0] = h[15] & 1u;
     s->latch[1] = (h[15] >> 8) & 1u;
-    s->ctrl = h[1] & 0xFFu;
-    s->mask = (h[1] >> 8) & 0xFFu;
-    s->fx = (h[1] >> 16) & 7u;
-    s->v = h[2] & 0xFFFFu;
-    s->t = h[2] >> 16;
-    for (int i = 0; i < 8; ++i) s->chr_off[i] = ((h[3 + (i >> 2)] >> ((i & 3) * 8)) & 0xFFu) * 1024u;
-    for (int k = 0; k < 4; ++k) s->nt_map[k] = (uint8_t)((h[5] >> (2 * k)) & 3u);
-    for (int i = 0; i < 32; ++i) s->pal[i] = (uint8_t)(h[6 + (i >> 2)] >> ((i & 3) * 8));
-    s->events = h + NES_LOG_HDR_WORDS;
-    s->count = r->log_n < NES_LOG_EVENTS ? r->log_n : NES_LOG_EVENTS;
-    s->ev = 0;
-    replay_line_end(s, -1);
+    s->sphitx = NO_CHECK;
+    s->hit_x = -1;
 }
 
-static uint8_t nt_read(const NesRec* r, const Replay* s, uint32_t addr) { /* addr in $2000-$2FFF */
-    const uint32_t n = (addr >> 10) & 3u;
-    return r->nt[(s->nt_map[n] & 1u) * 1024u + (addr & 0x3FFu)];
+/* The pre-render line: the writes before line 0's lead-in, then v = t while rendering (patch:1483-1490). */
+static void replay_begin_frame(Replay* s) {
+    while (s->cur < s->count && ev_start(s, s->cur) < -NES_LINE_LEAD) replay_apply(s, s->cur++, 0);
+    if (rendering(s)) s->v = s->t;
 }
 
-/* Pattern address (low plane) of background tile slot `slot` (0..33) of the line drawn with state s. */
-static uint32_t bg_slot_pa(const NesRec* r, const Replay* s, uint32_t slot) {
-    /* the fetch address moves right one tile per slot, switching nametables at each wrap (twice for slot 33
-     * from column 31) */
-    const uint32_t cc = (s->v & 31u) + slot, cx = cc & 31u, nth = ((s->v >> 10) & 1u) ^ ((cc >> 5) & 1u);
-    const uint32_t cy = (s->v >> 5) & 31u, fy = (s->v >> 12) & 7u, ntv = (s->v >> 11) & 1u;
-    const uint32_t base = 0x2000u | ((nth | (ntv << 1)) << 10);
-    return ((s->ctrl & 0x10u) << 8) + nt_read(r, s, base | (cy << 5) | cx) * 16u + fy;
-}
-
-/* Pattern address (low plane) of a sprite's row `row` (0..h-1, before the vertical flip). */
-static uint32_t sprite_row_pa(uint32_t ctrl, uint32_t tile, uint32_t attr, uint32_t row) {
-    const uint32_t h = (ctrl & 0x20u) ? 16u : 8u;
-    if (attr & 0x80u) row = h - 1u - row;
-    if (h == 8u) return ((ctrl & 0x08u) << 9) + tile * 16u + row;
-    return ((tile & 1u) << 12) + (tile & 0xFEu) * 16u + (row & 7u) + ((row & 8u) << 1);
-}
-
-/* MMC2: the pattern fetches of line l in order, each through the bank of the moment and then the latch hook
- * (patch:1496-1560, 1660-1700): the sprites of line l, fetched at the end of line l - 1 (l >= 1), then, unless
- * sprites_only, the line's 34 background tile slots. sp_chr[k] / bg_chr[t] receive the CHR offset of the 4 KB
- * half each fetch read (slot 0 of the half); either may be NULL. Fetches happen only while rendering is on. */
-static void mmc2_line_fetches(Replay* s, const NesRec* r, int l, int sprites_only, uint32_t* sp_chr,
-                              uint32_t* bg_chr) {
-    if (!s->mmc2 || (s->mask & 0x18u) == 0) return;
-    if (l >= 1) {
-        const int h = (s->ctrl & 0x20u) ? 16 : 8;
-        uint32_t n = 0;
-        for (uint32_t i = 0; i < 64u && n < 8u; ++i) {
-            const uint8_t* o = r->oam + 4u * i;
-            const int row = l - (int)o[0] - 1;
-            if (row < 0 || row >= h) continue;
-            const uint32_t pa = sprite_row_pa(s->ctrl, o[1], o[2], (uint32_t)row);
-            if (sp_chr) sp_chr[n] = s->chr_off[4u * (pa >> 12)];
-            replay_hook(s, pa);
-            ++n;
-        }
+/* Tile slots [ln->tile, last) of the current line (FCEUmm's tile loop, patch:1496-1577). Slot k >= 2 first
+ * shifts out 8 pixels of the two tiles fetched before it at the output position, then slot k's tile is fetched at
+ * v and v steps one tile right. With rendering off the slots draw the backdrop and still move the output position,
+ * the two prefetch slots included. The oracle fetches every slot also without pixels: only the last two fetches of
+ * a run and the MMC2 latches outlast it, and both come out the same. */
+static void replay_tiles(Replay* s, Line* ln, int last, int pixels) {
+    const int first = ln->tile;
+    const uint8_t back = (uint8_t)((s->pal[0] & 0x3Fu) | 0x40u);
+    if (!rendering(s)) {
+        if (pixels)
+            for (int p = ln->out; p < ln->out + 8 * (last - first) && p < 256; ++p) ln->px[p] = back;
+        ln->out += 8 * (last - first);
+        ln->tile = last;
+        return;
     }
-    if (sprites_only) return;
-    for (uint32_t t = 0; t < 34u; ++t) {
-        const uint32_t pa = bg_slot_pa(r, s, t);
-        if (bg_chr) bg_chr[t] = s->chr_off[4u * (pa >> 12)];
-        replay_hook(s, pa);
-    }
-}
-
-/* A pattern byte through the 1 KB slot table, or (base4 != ~0) from the 4 KB CHR half at byte offset base4. */
-static uint32_t pat_read(const NesRec* r, const NesCart* c, const Replay* s, uint32_t base4, uint32_t a) {
-    return base4 != ~0u ? c->chr[base4 + (a & 0xFFFu)] : chr_read(r, c, s->chr_off, a);
-}
-
-/* Background pixel x (0..255) of a line drawn with state s: 2-bit value and palette select. bg_chr: the MMC2
- * fetch banks of the line's tile slots, or NULL. */
-static uint32_t bg_pixel(const NesRec* r, const NesCart* c, const Replay* s, uint32_t x, uint32_t* attr_out,
-                         const uint32_t* bg_chr) {
-    const uint32_t pos = x + s->fx, slot = pos >> 3, bit = pos & 7u;
-    uint32_t cx = (s->v & 31u) + slot, nth = (s->v >> 10) & 1u;
-    if (cx >= 32u) {
-        cx -= 32u;
-        nth ^= 1u;
-    }
-    const uint32_t cy = (s->v >> 5) & 31u, fy = (s->v >> 12) & 7u, ntv = (s->v >> 11) & 1u;
-    const uint32_t base = 0x2000u | ((nth | (ntv << 1)) << 10);
-    const uint32_t tile = nt_read(r, s, base | (cy << 5) | cx);
-    const uint32_t at = nt_read(r, s, base | 0x3C0u | ((cy >> 2) << 3) | (cx >> 2));
-    *attr_out = (at >> (((cy & 2u) << 1) | (cx & 2u))) & 3u;
-    const uint32_t pa = ((s->ctrl & 0x10u) << 8) + tile * 16u + fy;
-    const uint32_t b4 = bg_chr ? bg_chr[slot] : ~0u;
-    const uint32_t lo = pat_read(r, c, s, b4, pa), hi = pat_read(r, c, s, b4, pa + 8u);
-    return ((lo >> (7u - bit)) & 1u) | (((hi >> (7u - bit)) & 1u) << 1);
-}
-
-/* Pixel of sprite i at screen x on line l (0 transparent / outside), `row` = l - y - 1. base4: the MMC2 fetch
- * bank of the sprite's row (~0 = the slot table). */
-static uint32_t sprite_pixel(const NesRec* r, const NesCart* c, const Replay* s, uint32_t i, uint32_t row,
-                             uint32_t col, uint32_t base4) {
-    const uint8_t* o = r->oam + 4u * i;
-    if (o[2] & 0x40u) col = 7u - col;
-    const uint32_t pa = sprite_row_pa(s->ctrl, o[1], o[2], row);
-    const uint32_t lo = pat_read(r, c, s, base4, pa), hi = pat_read(r, c, s, base4, pa + 8u);
-    return ((lo >> (7u - col)) & 1u) | (((hi >> (7u - col)) & 1u) << 1);
-}
-
-static void render_line(const NesRec* r, const NesCart* c, const Replay* s, int l, uint8_t* px,
-                        const uint32_t* bg_chr, const uint32_t* sp_chr) {
-    const int bg_on = (s->mask & 0x08u) != 0, sp_on = (s->mask & 0x10u) != 0;
-    const uint32_t h = (s->ctrl & 0x20u) ? 16u : 8u;
-    uint32_t sel[8], nsel = 0;
-    if (sp_on) {
-        for (uint32_t i = 0; i < 64u && nsel < 8u; ++i) {
-            const int row = l - (int)r->oam[4 * i] - 1;
-            if (row >= 0 && row < (int)h) sel[nsel++] = i;
-        }
-    }
-    for (uint32_t x = 0; x < 256u; ++x) {
-        uint32_t bg = 0, bga = 0;
-        if (bg_on && (x >= 8u || (s->mask & 0x02u))) bg = bg_pixel(r, c, s, x, &bga, bg_chr);
-        uint32_t sp = 0, spa = 0, behind = 0;
-        if (x >= 8u || (s->mask & 0x04u)) {
-            for (uint32_t k = 0; k < nsel; ++k) {
-                const uint8_t* o = r->oam + 4u * sel[k];
-                const uint32_t col = x - o[3];
-                if (x < o[3] || col >= 8u) continue;
-                const uint32_t p = sprite_pixel(r, c, s, sel[k], (uint32_t)(l - o[0] - 1), col,
-                                                sp_chr ? sp_chr[k] : ~0u);
-                if (p) {
-                    sp = p;
-                    spa = o[2] & 3u;
-                    behind = (o[2] >> 5) & 1u;
-                    break;
+    for (int k = first; k < last; ++k) {
+        if (k >= 2) {
+            if (pixels && ln->out < 256) {
+                const uint32_t lo = (s->sh_lo >> (8u - s->fx)) & 0xFFu, hi = (s->sh_hi >> (8u - s->fx)) & 0xFFu;
+                for (uint32_t q = 0; q < 8u; ++q) {
+                    const uint32_t val = ((lo >> (7u - q)) & 1u) | (((hi >> (7u - q)) & 1u) << 1);
+                    const uint32_t sel = q + s->fx < 8u ? (s->at & 3u) : ((s->at >> 2) & 3u);
+                    ln->px[ln->out + (int)q] = val ? (uint8_t)(s->pal[sel * 4u + val] & 0x3Fu) : back;
                 }
             }
+            ln->out += 8;
         }
-        uint32_t colour;
-        if (bg && (!sp || behind)) colour = s->pal[bga * 4u + bg];
-        else if (sp) colour = s->pal[16u + spa * 4u + sp];
-        else colour = s->pal[0];
-        colour &= 0x3Fu;
-        if (s->mask & 1u) colour &= 0x30u;
-        px[x] = (uint8_t)colour;
+        const uint32_t v = s->v, base = 0x2000u | (v & 0x0C00u);
+        const uint32_t tile = rp_nt(s, base | (v & 0x3FFu));
+        const uint32_t col = v & 0x1Fu;
+        const uint32_t attr = rp_nt(s, base | 0x3C0u | (col >> 2) | ((v & 0x380u) >> 4));
+        const uint32_t sel = (attr >> ((col & 2u) | ((v & 0x40u) >> 4))) & 3u;
+        const uint32_t pa = tile * 16u + ((s->ctrl & 0x10u) << 8) + ((v >> 12) & 7u);
+        const uint32_t p0 = rp_chr(s, pa), p1 = rp_chr(s, pa + 8u);   /* both through the bank before the hook */
+        replay_hook(s, pa);
+        s->at = (s->at >> 2) | (sel << 2);
+        s->sh_lo = (s->sh_lo << 8) | p0;
+        s->sh_hi = (s->sh_hi << 8) | p1;
+        s->v = col == 0x1Fu ? (v ^ 0x41Fu) : (v + 1u);
+    }
+    if (pixels) {
+        if (first <= 2 && last > 2 && !(s->mask & 0x02u))   /* left column of the background hidden */
+            for (int p = 0; p < 8; ++p) ln->px[p] = back;
+        if (!(s->mask & 0x08u)) {                            /* background off (sprites on) */
+            int from = first - 2, n = last - first;
+            if (from < 0) {
+                n += from;
+                from = 0;
+            }
+            for (int p = 8 * from; p < 8 * (from + n) && p < 256; ++p) ln->px[p] = back;
+        }
+    }
+    ln->tile = last;
+}
+
+/* The sprite-0 check against the background drawn left of line position p - 16 (patch:1583-1594). */
+static void replay_check_hit(Replay* s, const Line* ln, int p) {
+    if (s->sphitx == NO_CHECK) return;
+    for (int x = s->sphitx; x < s->sphitx + 8 && x < p - 16 && x < 255; ++x) {
+        if ((s->sphit_bits & (0x80u >> (x - s->sphitx))) && !(ln->px[x] & 0x40u)) {
+            s->hit = 1;
+            s->hit_x = x;
+            s->sphitx = NO_CHECK;
+            return;
+        }
+    }
+}
+
+/* The line drawn up to position p (FCEUmm's RefreshLine for an access at p, patch:1596-1613): the tile slots up
+ * to p / 8, one more while the sprite-0 check waits on the slot being drawn, the line's vertical step once p
+ * reaches 268, then the check. */
+static void replay_update(Replay* s, Line* ln, int p, int pixels) {
+    int last = p >> 3;
+    if (pixels && s->sphitx != NO_CHECK && s->sphitx < p - 16 && s->sphitx >= (last - 2) * 8) ++last;
+    if (last > 34) last = 34;
+    if (last <= ln->tile) return;
+    replay_tiles(s, ln, last, pixels);
+    if (p >= 268 && ln->fix) {
+        if (rendering(s)) y_step(s);
+        ln->fix = 0;
+    }
+    if (pixels) replay_check_hit(s, ln, p);
+}
+
+/* Line l: its pixels with every write that lands while it is drawn, each at the end of its instruction; $2007
+ * writes draw nothing first (patch:1617-1634). */
+static void replay_line(Replay* s, Line* ln, int l, int pixels) {
+    const int start = l * 341 - NES_LINE_LEAD;
+    ln->tile = 0;
+    ln->out = 0;
+    ln->fix = 1;
+    if (pixels) memset(ln->px, 0xFF, sizeof(ln->px));
+    while (s->cur < s->count && ev_start(s, s->cur) < start + 272) {
+        const uint32_t kind = ev_kind(s, s->cur);
+        if (kind != NES_EV_DATA && kind != NES_EV_PAL) replay_update(s, ln, ev_end(s, s->cur) - start, pixels);
+        replay_apply(s, s->cur++, 1);
+    }
+    replay_update(s, ln, 272, pixels);
+    if (ln->fix) {
+        if (rendering(s)) y_step(s);
+        ln->fix = 0;
+    }
+    if (pixels) replay_check_hit(s, ln, 272);
+}
+
+/* The sprites of the line (if sprites are on at its end), then greyscale; returns the line's emphasis bits
+ * (patch:1637-1661). Each pixel takes the lowest-numbered opaque sprite on it, drawn over a transparent background
+ * or when in front. */
+static uint32_t replay_compose(Replay* s, Line* ln) {
+    if ((s->mask & 0x10u) && s->spork) {
+        s->spork = 0;
+        const SprLine* d = &s->drawn;
+        for (uint32_t x = (s->mask & 0x04u) ? 0u : 8u; x < 256u; ++x) {
+            for (uint32_t n = 0; n < d->n; ++n) {
+                const uint32_t col = x - d->x[n];
+                if (col >= 8u) continue;
+                const uint32_t b = (d->attr[n] & 0x40u) ? col : 7u - col;
+                const uint32_t val = ((d->lo[n] >> b) & 1u) | (((d->hi[n] >> b) & 1u) << 1);
+                if (val == 0) continue;
+                if (!(d->attr[n] & 0x20u) || (ln->px[x] & 0x40u)) ln->px[x] = s->spal[(d->attr[n] & 3u) * 4u + val];
+                break;
+            }
+        }
+    }
+    const uint8_t keep = (s->mask & 0x01u) && rendering(s) ? 0x30u : 0x3Fu;
+    for (int x = 0; x < 256; ++x) ln->px[x] &= keep;
+    return s->mask >> 5;
+}
+
+/* After line l's pixels (patch:1666-1730): the sprites of line l + 1 fetched with the state of that moment (up to
+ * eight, OAM order), the writes up to dot 262 of the line grid, the horizontal copy from t, the writes up to its end,
+ * and, with sprites on, the fetched line becomes the one drawn next, with its palette and sprite-0 check. `sprites`
+ * 0 skips the fetch where no later line can need it (not on MMC2, whose latches every fetch moves). */
+static void replay_end_of_line(Replay* s, int l, int sprites) {
+    const int start = l * 341 - NES_LINE_LEAD;
+    s->sphitx = NO_CHECK;
+    if (rendering(s) && (sprites || s->mmc2)) {
+        const uint32_t ctrl = s->ctrl, h = (ctrl & 0x20u) ? 16u : 8u;
+        const uint32_t table8 = (ctrl & 0x08u) && !(ctrl & 0x20u) ? 0x1000u : 0u;
+        SprLine* f = &s->fetched;
+        f->n = 0;
+        s->blurp = 0;
+        for (uint32_t i = 0; i < 64u; ++i) {
+            const uint8_t* o = s->r->oam + 4u * i;
+            const uint32_t row = (uint32_t)(l - (int)o[0]);
+            if (row >= h) continue;
+            if (f->n >= 8u) break;
+            if (i == 0) s->blurp = 1;
+            uint32_t pa = h == 16u ? ((o[1] & 1u) << 12) + ((o[1] & 0xFEu) << 4) : ((uint32_t)o[1] << 4) + table8;
+            if (o[2] & 0x80u) pa += 7u - row + ((ctrl & 0x20u) >> 1) - (row & 8u);   /* vertical flip */
+            else pa += row + (row & 8u);
+            pa &= 0x1FFFu;
+            f->lo[f->n] = rp_chr(s, pa);
+            f->hi[f->n] = rp_chr(s, pa + 8u);
+            replay_hook(s, pa);
+            f->attr[f->n] = o[2];
+            f->x[f->n] = o[3];
+            ++f->n;
+        }
+    }
+    while (s->cur < s->count && ev_start(s, s->cur) < start + 278) replay_apply(s, s->cur++, 1);
+    if (rendering(s)) s->v = (s->v & 0xFBE0u) | (s->t & 0x041Fu);
+    while (s->cur < s->count && ev_start(s, s->cur) < start + 341) replay_apply(s, s->cur++, 1);
+    if (s->mask & 0x10u) {
+        s->spork = 0;
+        if (s->fetched.n != 0) {
+            s->drawn = s->fetched;
+            for (int i = 0; i < 16; ++i) s->spal[i] = (uint8_t)(s->pal[16 + i] & 0x3Fu);
+            const uint32_t bits = s->drawn.lo[0] | s->drawn.hi[0];
+            if (s->blurp && !s->hit && bits) {
+                uint32_t b = bits;
+                if (s->drawn.attr[0] & 0x40u) {   /* flipped: mirror the byte */
+                    b = 0;
+                    for (int k = 0; k < 8; ++k) b |= ((bits >> k) & 1u) << (7 - k);
+                }
+                s->sphitx = s->drawn.x[0];
+                s->sphit_bits = b;
+            }
+            s->spork = 1;
+        }
     }
 }
 
 void orc_render_full(const NesRec* r, const NesCart* c, uint8_t* pix, uint8_t* emph) {
     Replay s;
-    replay_begin(&s, r, c);
+    Line ln;
+    replay_load(&s, r, c, r->log_n);
+    replay_begin_frame(&s);
     for (int l = 0; l < 240; ++l) {
-        uint32_t bgc[34], spc[8];
-        mmc2_line_fetches(&s, r, l, 0, spc, bgc);
-        render_line(r, c, &s, l, pix + l * 256, s.mmc2 ? bgc : NULL, s.mmc2 ? spc : NULL);
-        emph[l] = (uint8_t)((s.mask >> 5) & 7u);
-        replay_line_end(&s, l);
+        replay_line(&s, &ln, l, 1);
+        emph[l] = (uint8_t)(replay_compose(&s, &ln) & 7u);
+        memcpy(pix + 256 * l, ln.px, 256);
+        replay_end_of_line(&s, l, 1);
     }
 }
 
+/* The env's picture (rl/csrc/nes_machine.cuh:133-155): lines 8..231, x 8..247. */
 void orc_render_obs(const NesRec* r, const NesCart* c, uint8_t* obs, uint8_t* emph) {
     Replay s;
-    uint8_t line[256];
-    replay_begin(&s, r, c);
+    Line ln;
+    replay_load(&s, r, c, r->log_n);
+    replay_begin_frame(&s);
     for (int l = 0; l < 232; ++l) {
-        uint32_t bgc[34], spc[8];
-        mmc2_line_fetches(&s, r, l, 0, spc, bgc);
+        replay_line(&s, &ln, l, 1);
+        const uint32_t e = replay_compose(&s, &ln);
         if (l >= 8) {
-            render_line(r, c, &s, l, line, s.mmc2 ? bgc : NULL, s.mmc2 ? spc : NULL);
-            memcpy(obs + (l - 8) * 240, line + 8, 240);
-            emph[l - 8] = (uint8_t)((s.mask >> 5) & 7u);
+            for (int x = 0; x < 240; ++x) obs[(l - 8) * 240 + x] = ln.px[8 + x] & 0x3Fu;
+            emph[l - 8] = (uint8_t)(e & 7u);
         }
-        replay_line_end(&s, l);
+        replay_end_of_line(&s, l, 1);
     }
 }
 
-/* First sprite-0 hit of the logged frame (frame dot), from the log so far: sprite 0's opaque pixels against
- * opaque background pixels, both layers on, not at x = 255, not in a clipped left column. */
-int32_t orc_sprite0_scan(const NesRec* r, const NesCart* c) {
-    Replay s;
-    const int y0 = r->oam[0], x0 = r->oam[3];
-    if (y0 >= 239) return NES_NO_HIT;
-    replay_begin(&s, r, c);
-    for (int l = 0; l < 240; ++l) {
-        uint32_t bgc[34], spc[8];
-        mmc2_line_fetches(&s, r, l, 0, spc, bgc);
-        const uint32_t* bg_chr = s.mmc2 ? bgc : NULL;
-        const uint32_t h = (s.ctrl & 0x20u) ? 16u : 8u;
-        const int row = l - y0 - 1;
-        if ((s.mask & 0x18u) == 0x18u && row >= 0 && row < (int)h) {
-            for (int col = 0; col < 8; ++col) {
-                const int x = x0 + col;
-                if (x >= 255) break;
-                if (x < 8 && (s.mask & 0x06u) != 0x06u) continue;
-                uint32_t a;
-                if (sprite_pixel(r, c, &s, 0, (uint32_t)row, (uint32_t)col, s.mmc2 ? spc[0] : ~0u) &&
-                    bg_pixel(r, c, &s, (uint32_t)x, &a, bg_chr))
-                    return l * 341 + x + 1;
-            }
-        }
-        if (l >= y0 + 16) break; /* past sprite 0 at any size: no later hit possible */
-        replay_line_end(&s, l);
+/* The first line position >= x + 17 whose RefreshLine has drawn pixel x (patch:1743-1750): the position from which
+ * an access sees a hit found at x. */
+static int first_seen(int x, int sphitx) {
+    for (int p = x + 17;; ++p) {
+        int last = p >> 3;
+        if (sphitx < p - 16 && sphitx >= (last - 2) * 8) ++last;
+        if (last > 34) last = 34;
+        if (x < (last - 2) * 8) return p;
     }
-    return NES_NO_HIT;
+}
+
+/* The frame's sprite-0 hit from the log so far (patch:1752-1788): replays up to sprite 0's last line (pixels from
+ * its first) and returns the NeSLE frame dot from which an instruction sees the flag, *hit = 1. An access is stamped
+ * with its instruction's end, so a 4-cycle $2002 read that starts 12 dots earlier sees it. With no hit: the dot
+ * after which no write can add one (the end of sprite 0's lines), or 0 when sprite 0 is below the picture. */
+uint32_t orc_sprite0_hit(const NesRec* r, const NesCart* c, int* hit) {
+    *hit = 0;
+    const int first = (int)r->oam[0] + 1;
+    if (first >= 240) return 0;
+    Replay s;
+    Line ln;
+    replay_load(&s, r, c, r->log_n);
+    replay_begin_frame(&s);
+    const int last = first + 15 < 239 ? first + 15 : 239;
+    for (int l = 0; l <= last; ++l) {
+        const int sphitx = s.sphitx;
+        replay_line(&s, &ln, l, l >= first);
+        if (s.hit) {
+            *hit = 1;
+            return (uint32_t)(l * 341 - NES_LINE_LEAD + first_seen(s.hit_x, sphitx) - 12 - NES_FCEU_LAG);
+        }
+        s.spork = 0;
+        replay_end_of_line(&s, l, l >= first - 1);
+    }
+    return (uint32_t)(last * 341 + 256 - NES_FCEU_LAG);
+}
+
+/* MMC2 at vblank: the latches this frame's own pattern fetches leave (NeSLE's frame_resolve_mmc2, patch:1790-1812,
+ * which the reference env runs right after the vblank stop, rl/csrc/nes_machine.cuh:110-131). */
+static void mmc2_resolve(NesRec* r, const NesCart* c) {
+    Replay s;
+    Line ln;
+    replay_load(&s, r, c, r->log_n);
+    replay_begin_frame(&s);
+    for (int l = 0; l < 240; ++l) {
+        replay_line(&s, &ln, l, 0);
+        replay_end_of_line(&s, l, 1);
+    }
+    while (s.cur < s.count) replay_apply(&s, s.cur++, 0);
+    r->mreg[6] = (uint8_t)s.latch[0];
+    r->mreg[7] = (uint8_t)s.latch[1];
+    mapper_sync(r, c);
 }
 
 /* ------------------------------------------------------------------------------------------ PPU events */
 
 static uint64_t abs_dot(const NesRec* r) { return (uint64_t)r->frame * NES_FRAME_DOTS + r->frame_dot; }
 
-static void s0_update(NesRec* r, const NesCart* c) {
-    if (r->s0_valid || r->frame != r->log_frame) return;
-    r->s0_valid = 1;
-    r->s0_dot = NES_NO_HIT;
-    if ((r->status & 0x40u) || r->frame_dot >= 240u * 341u) return;
-    int32_t hit = orc_sprite0_scan(r, c);
-    if (hit != NES_NO_HIT && hit <= (int32_t)r->frame_dot) hit = (int32_t)r->frame_dot + 1;
-    r->s0_dot = hit;
+/* Dots from the current frame dot to the next MMC3 counter clock (dot 266 of lines 0-239, dot 256 of the
+ * pre-render line), strictly after it (patch:1881-1903). */
+static uint32_t dots_to_mmc3_clock(uint32_t cur) {
+    const uint32_t line = cur / 341u, d = cur % 341u;
+    if (line < 240u) {
+        if (d < 266u) return 266u - d;
+        if (line + 1u < 240u) return 341u - d + 266u;
+        return (261u - line) * 341u + 256u - d;
+    }
+    if (line < 261u) return (261u - line) * 341u + 256u - d;
+    if (d < 256u) return 256u - d;
+    return 341u - d + 266u;
 }
 
-static int is_mmc3_clock_dot(uint32_t d) {
-    if (d == 261u * 341u + 256u) return 1;
-    return d < 240u * 341u && d % 341u == 266u;
-}
-
-static uint32_t dots_to_event(NesRec* r, const NesCart* c) {
-    const uint32_t fd = r->frame_dot;
-    uint32_t best = NES_FRAME_DOTS - fd;
-    if (fd < NES_VBLANK_DOT && NES_VBLANK_DOT - fd < best) best = NES_VBLANK_DOT - fd;
-    if (fd < NES_PRERENDER_DOT && NES_PRERENDER_DOT - fd < best) best = NES_PRERENDER_DOT - fd;
+/* Dots to the next PPU event (patch:2001-2037): the frame wrap, vblank, pre-render, the $2002 flag set and clear
+ * dots, the scheduled sprite-0 check and the MMC3 clocks. A short frame ends a dot early. */
+static uint32_t dots_to_event(const NesRec* r, const NesCart* c) {
+    const uint32_t cur = r->frame_dot, skip = (r->log_flags & NES_LOG_SHORT) ? 1u : 0u;
+    const uint32_t frame = NES_FRAME_DOTS - skip;
+#define DIST(e) ((e) > cur ? (e) - cur : frame - cur + (e))
+    uint32_t next = frame - cur, d;
+    if ((d = DIST(NES_VBLANK_DOT)) < next) next = d;
+    if ((d = DIST(NES_PRERENDER_DOT)) < next) next = d;
+    if ((d = DIST(NES_VFLAG_DOT)) < next) next = d;
+    if ((d = DIST(NES_SCLR_DOT)) < next) next = d;
+    const uint32_t s0 = r->s0_sched & NES_S0_DOT;
+    if (s0 != 0 && (d = DIST(s0)) < next) next = d;
+#undef DIST
     if (c->board == NES_BOARD_MMC3) {
-        const uint32_t line = fd / 341u, d = fd % 341u;
-        uint32_t next;
-        if (line < 240u) next = d < 266u ? line * 341u + 266u : (line < 239u ? (line + 1u) * 341u + 266u : 261u * 341u + 256u);
-        else if (line < 261u) next = 261u * 341u + 256u;
-        else next = d < 256u ? 261u * 341u + 256u : 0xFFFFFFFFu;
-        if (next != 0xFFFFFFFFu && next - fd < best) best = next - fd;
+        uint32_t clk = dots_to_mmc3_clock(cur);
+        if (cur + clk >= NES_FRAME_DOTS) clk -= skip;
+        if (clk < next) next = clk;
     }
-    s0_update(r, c);
-    if (r->frame == r->log_frame && r->s0_dot != NES_NO_HIT && (uint32_t)r->s0_dot > fd &&
-        (uint32_t)r->s0_dot - fd < best)
-        best = (uint32_t)r->s0_dot - fd;
-    return best;
+    return next;
 }
 
-/* MMC2 at vblank: the latches this frame's own fetches leave, from a latches-only replay of its log over the
- * nametables and OAM as they are now (NeSLE's frame_resolve_mmc2, patch:1790-1812; rl/csrc/nes_machine.cuh:110-131
- * runs the same replay after the vblank stop, before any further instruction). */
-static void mmc2_resolve(NesRec* r, const NesCart* c) {
-    if (r->frame != r->log_frame) return;   /* no log of this frame (the first one after power-on) */
-    Replay s;
-    replay_begin(&s, r, c);
-    for (int l = 0; l < 240; ++l) {
-        mmc2_line_fetches(&s, r, l, 0, NULL, NULL);
-        replay_line_end(&s, l);
-    }
-    mmc2_line_fetches(&s, r, 240, 1, NULL, NULL);
-    replay_until(&s, INT32_MAX);
-    r->mreg[6] = (uint8_t)s.latch[0];
-    r->mreg[7] = (uint8_t)s.latch[1];
-    mapper_sync(r, c);
-}
-
-static void process_events(NesRec* r, const NesCart* c) {
-    const uint32_t d = r->frame_dot;
-    if (d == NES_FRAME_DOTS) {
-        r->frame_dot = 0;
-        ++r->frame;
-        return;
-    }
-    if (d == NES_VBLANK_DOT) {
-        r->status |= 0x80u;
-        if (r->ctrl & 0x80u) r->nmi_pending = 1;
-        if (c->board == NES_BOARD_MMC2) mmc2_resolve(r, c);
-    }
-    if (d == NES_PRERENDER_DOT) {
-        r->status &= 0x1Fu;
-        log_capture(r);
-    }
-    if (c->board == NES_BOARD_MMC3 && is_mmc3_clock_dot(d) && (r->mask & 0x18u)) mmc3_clock(r);
-    if (r->frame == r->log_frame && r->s0_dot != NES_NO_HIT && d == (uint32_t)r->s0_dot) {
-        r->status |= 0x40u;
-        r->s0_dot = NES_NO_HIT;
-    }
-}
-
-static void ppu_advance(NesRec* r, const NesCart* c, uint32_t dots) {
-    while (dots > 0) {
-        const uint32_t to = dots_to_event(r, c);
-        if (dots < to) {
-            r->frame_dot += dots;
-            return;
+/* The PPU over `dots` dots from the current frame dot (NeSLE's settle, patch:2040-2156): every event in the span,
+ * per frame in this order: the sprite-0 check, the $2002 vblank flag, vblank (NMI; MMC2's latch resolve), the $2002
+ * clear, the pre-render line (log capture, the frame's sprite-0 check scheduled at sprite 0's first line); then the
+ * span's MMC3 clocks. */
+static void ppu_step(NesRec* r, const NesCart* c, uint32_t dots) {
+    const uint32_t start = r->frame_dot;
+    uint32_t end = start + dots;
+    if ((r->log_flags & NES_LOG_SHORT) && end >= NES_FRAME_DOTS - 1u) end += 1u;   /* the skipped last dot */
+    const uint32_t frames = end / NES_FRAME_DOTS;
+    for (uint32_t f = 0; f <= frames; ++f) {
+        const uint32_t base = f * NES_FRAME_DOTS;
+#define CROSSED(e) (base + (e) > start && base + (e) <= end)
+        const uint32_t sched = r->s0_sched, s0 = sched & NES_S0_DOT;
+        if (s0 != 0 && CROSSED(s0)) {
+            /* worked out again with the writes logged so far, unless nothing was logged since the last answer */
+            int hit;
+            uint32_t dot;
+            if ((sched & NES_S0_KNOWN) && ((sched >> 20) & 0x1FFu) == r->log_n) {
+                dot = s0;
+                hit = (sched & NES_S0_HIT) != 0;
+            } else {
+                dot = orc_sprite0_hit(r, c, &hit);
+            }
+            const int reached = base + dot <= end;
+            if (hit && reached) r->status |= 0x40u;
+            r->s0_sched = dot != 0 && !reached
+                              ? dot | NES_S0_KNOWN | (hit ? NES_S0_HIT : 0u) | ((uint32_t)r->log_n << 20)
+                              : 0u;
         }
-        r->frame_dot += to;
-        dots -= to;
-        process_events(r, c);
+        if (CROSSED(NES_VFLAG_DOT)) r->status |= 0x80u;
+        if (CROSSED(NES_VBLANK_DOT)) {   /* NMI 12 dots after the flag, whether or not a read took it */
+            if (r->ctrl & 0x80u) r->nmi_pending = 1;
+            if (c->board == NES_BOARD_MMC2) mmc2_resolve(r, c);
+        }
+        if (CROSSED(NES_SCLR_DOT)) r->status &= 0x1Fu;
+        if (CROSSED(NES_PRERENDER_DOT)) {
+            r->status &= 0x1Fu;
+            log_capture(r);
+            const uint32_t y = r->oam[0];
+            r->s0_sched = y < 239u ? (y + 1u) * 341u - 20u - NES_FCEU_LAG : 0u;
+        }
+#undef CROSSED
     }
+    if (c->board == NES_BOARD_MMC3 && (r->mask & 0x18u) && (r->ctrl & 0x38u) != 0x18u) {
+        /* FCEUmm clocks the counter while rendering, unless both pattern tables are at $1000 with 8x8 sprites */
+        for (uint32_t la = start / 341u; la <= end / 341u; ++la) {
+            const uint32_t line = la % 262u;
+            uint32_t at;
+            if (line < 240u) at = 266u;
+            else if (line == 261u) at = 256u;
+            else continue;
+            const uint32_t d = la * 341u + at;
+            if (d > start && d <= end) mmc3_clock(r);
+        }
+    }
+    r->frame_dot = end % NES_FRAME_DOTS;
+    r->frame += frames;
+    if (frames) r->log_flags &= (uint8_t)~NES_LOG_SHORT;
 }
 
 /* ------------------------------------------------------------------------------------------------- bus */
@@ -801,20 +925,19 @@ static void ppu_advance(NesRec* r, const NesCart* c, uint32_t dots) {
 typedef struct Bus {
     NesRec* r;
     const NesCart* c;
-    int32_t ev_time; /* log time of this instruction's accesses (its end) */
-    int log_on;      /* the instruction started inside the log window */
+    uint32_t now;    /* NeSLE frame dot at which this instruction starts (its log stamp) */
+    int log_on;      /* the instruction starts while a frame is logged: before vblank or from the pre-render line */
     int dma;         /* a $4014 write happened */
 } Bus;
 
 static void log_event(Bus* b, uint32_t kind, uint32_t value, uint32_t aux) {
     NesRec* r = b->r;
-    if (kind != NES_EV_PAL) r->s0_valid = 0;
     if (!b->log_on) return;
     uint32_t* h = r->log;
     uint32_t* ev = h + NES_LOG_HDR_WORDS;
     if (kind == NES_EV_DATA && (r->mask & 0x18u) == 0 && r->log_n > 0) {
         uint32_t* last = ev + 2u * (r->log_n - 1u);
-        if ((last[0] >> 24) == NES_EV_DATA && (last[1] >> 8) < 0xFFu) {
+        if ((last[0] & 15u) == NES_EV_DATA && (last[1] >> 8) < 0xFFu) {
             last[1] += 0x100u;
             return;
         }
@@ -823,7 +946,7 @@ static void log_event(Bus* b, uint32_t kind, uint32_t value, uint32_t aux) {
         h[0] |= NES_LOG_OVERFLOW;
         return;
     }
-    ev[2u * r->log_n] = ((uint32_t)(b->ev_time + NES_LOG_TIME_BIAS) & 0xFFFFFFu) | (kind << 24);
+    ev[2u * r->log_n] = NES_EV_WORD0(kind, b->now & 0x1FFFFu);
     ev[2u * r->log_n + 1u] = (value & 0xFFu) | ((aux & 0xFFu) << 8);
     ++r->log_n;
     h[0] = (h[0] & NES_LOG_OVERFLOW) | r->log_n;
@@ -844,12 +967,11 @@ static void ppu_mem_write(Bus* b, uint32_t a, uint8_t v) {
     if (a < 0x2000u) {
         if (!b->c->chr) {
             r->chr_ram[(r->chr_off[(a >> 10) & 7u] + (a & 0x3FFu)) & (NES_CHRRAM_BYTES - 1u)] = v;
-            r->s0_valid = 0;
         }
-        log_event(b, NES_EV_DATA, 0, 1);
+        log_event(b, NES_EV_DATA, 0, 0);
     } else if (a < 0x3F00u) {
         r->nt[(r->nt_map[(a >> 10) & 3u] & 1u) * 1024u + (a & 0x3FFu)] = v;
-        log_event(b, NES_EV_DATA, 0, 1);
+        log_event(b, NES_EV_DATA, 0, 0);
     } else {
         uint32_t i = a & 0x1Fu;
         if ((i & 0x13u) == 0x10u) i &= 0x0Fu;
@@ -893,7 +1015,7 @@ static uint8_t ppu_reg_read(Bus* b, uint32_t reg) {
                 mmc2_ppu_address(b, a);
             }
             r->v = (uint16_t)((r->v + ((r->ctrl & 4u) ? 32u : 1u)) & 0x7FFFu);
-            log_event(b, NES_EV_DATA, 0, 1);
+            log_event(b, NES_EV_DREAD, 0, 0);
             mmc2_ppu_address(b, r->v & 0x3FFFu);
             break;
         }
@@ -920,7 +1042,6 @@ static void ppu_reg_write(Bus* b, uint32_t reg, uint8_t v) {
         case 3: r->oam_addr = v; break;
         case 4:
             r->oam[r->oam_addr++] = v;
-            r->s0_valid = 0;
             break;
         case 5:
             log_event(b, NES_EV_SCROLL, v, r->w);
@@ -982,7 +1103,6 @@ static void bus_write(Bus* b, uint16_t a, uint8_t v) {
         ppu_reg_write(b, a & 7u, v);
     } else if (a == 0x4014u) {
         for (uint32_t i = 0; i < 256u; ++i) r->oam[(r->oam_addr + i) & 0xFFu] = bus_read(b, (uint16_t)((v << 8) | i));
-        r->s0_valid = 0;
         b->dma = 1;
     } else if (a == 0x4016u) {
         r->strobe = v & 1u;
@@ -1146,7 +1266,7 @@ static uint16_t ea_rmw(Cpu* k, uint8_t op, uint16_t* len) {
 
 /* Executes instruction `op` at pc. Returns 0 on an unimplemented opcode. Data accesses that the frame log
  * may record are stamped with the instruction's end: every penalty cycle is known before them. */
-static int execute(Cpu* k, uint8_t op, int32_t abs_start_rel, int log_on) {
+static int execute(Cpu* k, uint8_t op) {
     NesRec* r = k->r;
     Bus* b = k->b;
     const uint32_t base = kCycles[op];
@@ -1154,8 +1274,6 @@ static int execute(Cpu* k, uint8_t op, int32_t abs_start_rel, int log_on) {
     k->cycles = base;
     uint16_t len = 1, a;
     uint8_t m;
-    b->log_on = log_on;
-    b->ev_time = abs_start_rel + 3 * (int32_t)base;
     switch (op) {
         /* ---- group 1: ORA AND EOR ADC LDA CMP SBC (STA below) ---- */
         case 0x01: case 0x05: case 0x09: case 0x0D: case 0x11: case 0x15: case 0x19: case 0x1D:
@@ -1170,10 +1288,10 @@ static int execute(Cpu* k, uint8_t op, int32_t abs_start_rel, int log_on) {
                 case 1: m = rd(k, ea_zp(k)); len = 2; break;
                 case 2: m = k->lo; len = 2; break;
                 case 3: m = rd(k, ea_abs(k)); len = 3; break;
-                case 4: a = ea_izy(k, 1); b->ev_time = abs_start_rel + 3 * (int32_t)k->cycles; m = rd(k, a); len = 2; break;
+                case 4: a = ea_izy(k, 1); m = rd(k, a); len = 2; break;
                 case 5: m = rd(k, ea_zpx(k)); len = 2; break;
-                case 6: a = ea_abi(k, r->y, 1); b->ev_time = abs_start_rel + 3 * (int32_t)k->cycles; m = rd(k, a); len = 3; break;
-                default: a = ea_abi(k, r->x, 1); b->ev_time = abs_start_rel + 3 * (int32_t)k->cycles; m = rd(k, a); len = 3; break;
+                case 6: a = ea_abi(k, r->y, 1); m = rd(k, a); len = 3; break;
+                default: a = ea_abi(k, r->x, 1); m = rd(k, a); len = 3; break;
             }
             switch (op >> 5) {
                 case 0: r->a |= m; nz(r, r->a); break;
@@ -1211,8 +1329,8 @@ static int execute(Cpu* k, uint8_t op, int32_t abs_start_rel, int log_on) {
                 case 0xAE: case 0xAC: case 0xEC: case 0xCC: case 0x2C: m = rd(k, ea_abs(k)); len = 3; break;
                 case 0xB6: m = rd(k, ea_zpy(k)); len = 2; break;
                 case 0xB4: m = rd(k, ea_zpx(k)); len = 2; break;
-                case 0xBE: a = ea_abi(k, r->y, 1); b->ev_time = abs_start_rel + 3 * (int32_t)k->cycles; m = rd(k, a); len = 3; break;
-                default: a = ea_abi(k, r->x, 1); b->ev_time = abs_start_rel + 3 * (int32_t)k->cycles; m = rd(k, a); len = 3; break;
+                case 0xBE: a = ea_abi(k, r->y, 1); m = rd(k, a); len = 3; break;
+                default: a = ea_abi(k, r->x, 1); m = rd(k, a); len = 3; break;
             }
             switch (op) {
                 case 0xA2: case 0xA6: case 0xAE: case 0xB6: case 0xBE: r->x = m; nz(r, m); break;
@@ -1314,7 +1432,9 @@ static int execute(Cpu* k, uint8_t op, int32_t abs_start_rel, int log_on) {
 }
 
 /* One step: pending NMI (or an asserted cartridge IRQ with I clear), then one instruction, then the OAM-DMA
- * stall and the DMC service (patch:823-862). `pending` = dots not yet settled. */
+ * stall and the DMC service (patch:823-862). `pending` = dots not yet settled. The frame-log events the
+ * instruction makes are stamped with its start dot, and with its cycles once it has run (patch:829-836,
+ * 1166-1185). */
 static uint32_t step(NesRec* r, const NesCart* c, uint32_t pending, uint32_t* fault, uint8_t* op_out,
                      uint16_t* pc_out) {
     Bus b = {r, c, 0, 0, 0};
@@ -1328,16 +1448,19 @@ static uint32_t step(NesRec* r, const NesCart* c, uint32_t pending, uint32_t* fa
         interrupt(&k, 0xFFFE);
         cyc = 7;
     }
-    const int64_t start = (int64_t)abs_dot(r) + pending + 3 * cyc - (int64_t)r->log_frame * NES_FRAME_DOTS;
-    const int log_on = start >= LOG_WINDOW_START && start < (int64_t)NES_VBLANK_DOT;
+    b.now = r->frame_dot + pending + 3u * cyc;
+    b.log_on = b.now < NES_VBLANK_DOT || b.now >= NES_PRERENDER_DOT;
+    const uint32_t logged = r->log_n;
     *pc_out = r->pc;
     *op_out = fetch(r, c, r->pc);
     k.lo = fetch(r, c, (uint16_t)(r->pc + 1));
     k.hi = fetch(r, c, (uint16_t)(r->pc + 2));
-    if (!execute(&k, *op_out, (int32_t)start, log_on)) {
+    if (!execute(&k, *op_out)) {
         *fault = ((uint32_t)r->pc << 8) | *op_out;
         return 0;
     }
+    for (uint32_t i = logged; i < r->log_n && i < NES_LOG_EVENTS; ++i)
+        r->log[NES_LOG_HDR_WORDS + 2u * i] |= (k.cycles > 15u ? 15u : k.cycles) << 4;
     cyc += k.cycles;
     r->cycles += cyc;
     if (b.dma) {
@@ -1357,34 +1480,36 @@ uint32_t orc_step(NesRec* r, const NesCart* c, uint32_t* fault) {
     uint8_t op;
     uint16_t pc;
     *fault = 0;
-    (void)dots_to_event(r, c);
     const uint32_t cyc = step(r, c, 0, fault, &op, &pc);
     if (*fault) return 0;
-    ppu_advance(r, c, 3u * cyc);
+    ppu_step(r, c, 3u * cyc);
     return cyc;
 }
 
-/* The JMP-to-self idle loop: skip whole 3-cycle jumps up to the next PPU event (patch:866-893). Not while an
- * interrupt waits to be taken. */
+/* The JMP-to-self idle loop: skip whole 3-cycle jumps up to the next PPU event (patch:866-893); not with an NMI
+ * raised by the settle before it. */
 static void fast_forward(NesRec* r, const NesCart* c) {
-    if (r->nmi_pending || (r->irq_line && !(r->p & FL_I))) return;
+    if (r->nmi_pending) return;
     const uint32_t to = dots_to_event(r, c);
     const uint32_t jumps = (to + 8u) / 9u;
     if (jumps == 0) return;
     r->cycles += 3u * jumps;
     if (r->cycles >= r->dmc_event) (void)orc_dmc_service(r, r->cycles, 0);
-    ppu_advance(r, c, 9u * jumps);
+    ppu_step(r, c, 9u * jumps);
 }
 
-uint32_t orc_run_until(NesRec* r, const NesCart* c, uint64_t target) {
+/* rl/csrc/nes_machine.cuh:67-103: instructions until a settle reaches absolute dot `target`, with the PPU settled
+ * lazily at its event horizon and after an idle jump. */
+uint32_t orc_run_until_budget(NesRec* r, const NesCart* c, uint64_t target, uint32_t budget) {
     uint32_t instructions = 0, fault = 0, pending = 0;
     uint32_t to_event = dots_to_event(r, c);
-    while (instructions < NES_BUDGET) {
+    int done = 0;
+    while (instructions < budget && !done) {
         if (pending >= to_event) {
-            ppu_advance(r, c, pending);
+            ppu_step(r, c, pending);
             pending = 0;
-            if (abs_dot(r) >= target) break;
             to_event = dots_to_event(r, c);
+            if (abs_dot(r) >= target) break;
         }
         uint8_t op;
         uint16_t pc0;
@@ -1393,16 +1518,19 @@ uint32_t orc_run_until(NesRec* r, const NesCart* c, uint64_t target) {
         pending += 3u * cyc;
         ++instructions;
         ++r->instr_lo;
-        if (!r->s0_valid) to_event = dots_to_event(r, c);
         if (op == 0x4C && r->pc == pc0) {
-            ppu_advance(r, c, pending);
+            ppu_step(r, c, pending);
             pending = 0;
             if (abs_dot(r) >= target) break;
             fast_forward(r, c);
             to_event = dots_to_event(r, c);
-            if (abs_dot(r) >= target) break;
+            done = abs_dot(r) >= target;
         }
     }
-    if (pending) ppu_advance(r, c, pending);
+    if (pending) ppu_step(r, c, pending);
     return fault;
+}
+
+uint32_t orc_run_until(NesRec* r, const NesCart* c, uint64_t target) {
+    return orc_run_until_budget(r, c, target, NES_BUDGET);
 }

@@ -16,8 +16,8 @@ REC_BYTES = 23552
 # NesRec field offsets (include/nesrec.h)
 OFF = dict(pc=0x00, a=0x02, x=0x03, y=0x04, sp=0x05, p=0x06, irq_line=0x07, cycles=0x08, nmi_pending=0x10, pad=0x11,
            shift=0x12, strobe=0x13, instr=0x14, frame_dot=0x18, frame=0x1C, v=0x20, t=0x22, ctrl=0x24, mask=0x25,
-           status=0x26, oam_addr=0x27, fx=0x28, w=0x29, read_buf=0x2A, open_bus=0x2B, s0_dot=0x2C, log_frame=0x30,
-           log_n=0x34, s0_valid=0x36, dmc_byte_end=0x40, dmc_event=0x48, dmc_left=0x50, ram=0x100, nt=0x900,
+           status=0x26, oam_addr=0x27, fx=0x28, w=0x29, read_buf=0x2A, open_bus=0x2B, s0_sched=0x2C, log_frame=0x30,
+           log_n=0x34, log_flags=0x36, dmc_byte_end=0x40, dmc_event=0x48, dmc_left=0x50, ram=0x100, nt=0x900,
            oam=0x1100, pal=0x1200, log=0x1300, prg_ram=0x1C00, chr_ram=0x3C00, mreg=0x58, prg_off=0x68, chr_off=0x78,
            nt_map=0x98)
 
@@ -51,8 +51,10 @@ def oracle():
         lib.orc_dmc_service.argtypes = [P, U64, I]
         lib.orc_dmc_service.restype = U32
         lib.orc_dmc_reset.argtypes = [P, U64]
-        lib.orc_sprite0_scan.argtypes = [P, P]
-        lib.orc_sprite0_scan.restype = ctypes.c_int32
+        lib.orc_sprite0_hit.argtypes = [P, P, P]
+        lib.orc_sprite0_hit.restype = U32
+        lib.orc_run_until_budget.argtypes = [P, P, U64, U32]
+        lib.orc_run_until_budget.restype = U32
         lib.orc_ram_hash.argtypes = [P]
         lib.orc_ram_hash.restype = U64
         lib.orc_parse_ines.argtypes = [P, U32, P, U32, P, ctypes.c_char_p, I]

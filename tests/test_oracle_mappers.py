@@ -100,7 +100,7 @@ def test_cnrom_synthetic_cart_switches_chr(conflicts):
         banks.add(pages(con)[1][0] // 8)
         n = con.u('log_n', 'H')
         log = con.words('log', 16 + 2 * 256)
-        events += sum(1 for i in range(min(n, 256)) if (int(log[16 + 2 * i]) >> 24) == 7)   # NES_EV_CHR
+        events += sum(1 for i in range(min(n, 256)) if (int(log[16 + 2 * i]) & 15) == 7)   # NES_EV_CHR
     assert banks == {0, 1, 2, 3} and events > 0
 
 

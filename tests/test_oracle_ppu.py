@@ -5,6 +5,8 @@ env is built on (rl/csrc/nes_machine.cuh:28-29: vblank at 241 * 341 + 1, 262 x 3
 of the reference's own PPU tests: the renderer pixel cases of third_party/nesle-extensions.patch:4413-4521 and the
 SMB NMI frame-header case of patch:4249-4268 (the frame captured at the pre-render line starts from t).
 """
+import ctypes
+
 import numpy as np
 import pytest
 
@@ -14,8 +16,6 @@ from rl import synth
 VBLANK = 241 * 341 + 1
 PRERENDER = 261 * 341 + 1
 FRAME = 341 * 262
-EV_SCROLL = 3
-BIAS = 1024
 
 
 def nrom(chr_bytes=None, vertical=True):
@@ -124,32 +124,65 @@ def test_oam_dma_copies_a_page_and_stalls(con):
 
 # ----------------------------------------------------------------------------------------------- timing
 
-def test_vblank_flag_and_nmi_timing(con):
-    """Stepping the NOP loop instruction by instruction: the vblank flag is up exactly from dot 241 * 341 + 1, the
-    NMI is taken by the next step, and the flags drop at the pre-render dot 261 * 341 + 1."""
+VFLAG = VBLANK - 12                                      # the replay's $2002 flag: 12 dots before NMI (patch:1940-1945)
+SCLR = PRERENDER - 12
+
+
+def test_vblank_flag_nmi_and_status_clear_timing(con):
+    """Stepping the NOP loop instruction by instruction: $2002 bit 7 is up from 241 * 341 + 1 - 12, the NMI is
+    raised at 241 * 341 + 1 and taken by the next step, and the flags drop at the pre-render dot - 12."""
     con.write(0x2000, 0x80)                              # NMI on vblank
     con.set('p', 0x24)
     seen = False
     while con.u('frame_dot', 'I') < VBLANK + 30:
-        before = con.u('frame_dot', 'I')
         cyc, fault = con.step()
         assert fault == 0
         dot = con.u('frame_dot', 'I')
-        assert bool(con.u('status') & 0x80) == (dot >= VBLANK), (before, dot)
+        assert bool(con.u('status') & 0x80) == (dot >= VFLAG), dot
+        assert bool(con.u('nmi_pending')) == (dot >= VBLANK and not seen), dot
         if dot >= VBLANK and not seen:
             seen = True
-            assert con.u('nmi_pending') == 1
             cyc, fault = con.step()                      # NMI entry (7) + NOP (2)
             assert cyc == 9 and con.u('nmi_pending') == 0 and con.u('sp') == 0xFD - 3
     while con.u('frame_dot', 'I') < PRERENDER + 30:
         dot0 = con.u('frame_dot', 'I')
         con.step()
         dot = con.u('frame_dot', 'I')
-        if dot0 < PRERENDER <= dot:
+        if dot >= SCLR:
             assert con.u('status') & 0xE0 == 0
-        elif dot < PRERENDER:
+        else:
             assert con.u('status') & 0x80
     assert con.run_until(FRAME) == 0 and con.u('frame', 'I') == 1
+
+
+def test_nmi_fires_even_when_a_read_took_the_flag(con):
+    """A $2002 read between the flag (dot 82170) and NMI (82182) clears bit 7, and the NMI still comes."""
+    con.write(0x2000, 0x80)
+    con.set('p', 0x24)
+    while con.u('frame_dot', 'I') < VFLAG:
+        con.step()
+    assert con.u('frame_dot', 'I') < VBLANK and con.read(0x2002) & 0x80 and con.u('status') & 0x80 == 0
+    while con.u('frame_dot', 'I') < VBLANK:
+        con.step()
+    assert con.u('nmi_pending') == 1
+
+
+def test_kook_frames_alternate_and_drop_the_last_pre_render_dot(con):
+    """Every other frame's pre-render line is a dot short: the header of every second frame captured carries the
+    kook bit, and a step across that frame's wrap lands one dot further."""
+    kooks = []
+    for f in range(1, 6):
+        assert con.run_until(f * FRAME) == 0
+        kooks.append((int(con.words('log', 16)[5]) >> 8) & 1)
+    assert kooks == [0, 1, 0, 1, 0]
+    for short in (0, 1):
+        c2 = Console(nrom())
+        c2.set('frame_dot', FRAME - 4, 'I')
+        c2.set('log_flags', 2 * short)
+        c2.set('pc', 0xC000, 'H')
+        cyc, fault = c2.step()                           # NOP: 2 cycles, 6 dots, across the wrap
+        assert cyc == 2 and c2.u('frame', 'I') == 1 and c2.u('frame_dot', 'I') == 2 + short
+        assert c2.u('log_flags') & 2 == 0                # the short frame has ended
 
 
 def test_run_until_stops_at_the_first_event_at_or_after_the_target(con):
@@ -182,6 +215,14 @@ def test_frame_header_starts_from_t_not_ppuctrl(con):
 
 
 # --------------------------------------------------------------------------------------------- renderer
+#
+# The replay grid (third_party/nesle-extensions.patch:900-1830): a write by an instruction that starts at NeSLE frame
+# dot d with c cycles lands at position p = d + 11 + 3c - (l * 341 - 16) of line l; the line's tile slots are drawn
+# in steps of 8 positions up to p / 8 before it (slot k's tile is fetched there and shows 16 pixels later, at pixels
+# 8(k - 2)..8(k - 2) + 7), a $2007 write draws nothing first, and what is left of the line is drawn at position 272.
+
+EV = dict(ctrl=1, mask=2, scroll=3, addr=4, data=5, pal=6, chr=7, mirror=8, mmc2=9, dread=10)
+
 
 class Picture:
     """A console whose logged frame is set by hand: header, nametables, OAM, CHR."""
@@ -205,9 +246,11 @@ class Picture:
         w = self.h[6 + i // 4]
         self.h[6 + i // 4] = (int(w) & ~(0xFF << (8 * (i % 4)))) | (v << (8 * (i % 4)))
 
-    def event(self, time, kind, value, aux=0):
+    def event(self, line, dot, kind, value, aux=0, cycles=4):
+        """A write by a `cycles`-cycle instruction that starts at dot `dot` of line `line` (NeSLE's grid)."""
         n = self.con.u('log_n', 'H')
-        self.h[16 + 2 * n] = ((time + BIAS) & 0xFFFFFF) | (kind << 24)
+        d = line * 341 + dot if line >= 0 else PRERENDER - 1 + dot
+        self.h[16 + 2 * n] = EV[kind] | (cycles << 4) | (d << 8)
         self.h[17 + 2 * n] = value | (aux << 8)
         self.con.set('log_n', n + 1, 'H')
         self.h[0] = n + 1
@@ -215,6 +258,23 @@ class Picture:
     def render(self):
         pix, emph = self.con.render_full()
         return pix
+
+    def opaque_tile(self, tile=1, planes=(0,)):
+        for row in range(8):
+            for pl in planes:
+                self.chr_view[16 * tile + 8 * pl + row] = 0xFF
+
+
+def stripes(p):
+    """Tile 1 (opaque colour 1) in the even columns of both nametables, tile 0 (transparent) in the odd ones,
+    palette 1 = $21, backdrop $0F."""
+    p.opaque_tile(1)
+    for col in range(0, 32, 2):
+        for tile_row in range(30):
+            p.nt[tile_row * 32 + col] = 0x01
+            p.nt[1024 + tile_row * 32 + col] = 0x01
+    p.palette(0, 0x0F)
+    p.palette(1, 0x21)
 
 
 def test_background_tile_top_left_and_left_clip():
@@ -237,20 +297,136 @@ def test_sprite_at_oam_y_is_drawn_from_the_next_line():
     assert pix[10, 12] == 0x16 and pix[9, 12] == 0x00 and pix[10, 13] == 0x00
 
 
-def test_mid_frame_scroll_write_from_the_log():
+def test_scroll_written_in_hblank_takes_effect_on_the_next_line():
+    """$2005 = 8 by a 4-cycle store from dot 240 of line 100: position 240 + 39 = 279 is past the line's pixels
+    (272), so line 100 keeps the old scroll and the horizontal copy at its end brings coarse x 1 to line 101."""
     p = Picture(mask=0x0A)
-    for row in range(8):
-        p.chr_view[0x0010 + row] = 0xFF                  # tile 1: every pixel colour 1
-    for col in range(0, 32, 2):
-        for tile_row in range(30):
-            p.nt[tile_row * 32 + col] = 0x01
-    p.palette(1, 0x21)
-    p.event(100 * 341 + 240 + 3 * 4, EV_SCROLL, 8, 0)    # $2005 = 8 by a 4-cycle store from dot 240 of line 100
+    stripes(p)
+    p.event(100, 240, 'scroll', 8, 0)
     pix = p.render()
-    assert pix[50, 0] == 0x21 and pix[50, 8] == 0x00
-    assert pix[100, 0] == 0x21 and pix[100, 8] == 0x00
-    assert pix[101, 0] == 0x00 and pix[101, 8] == 0x21
-    assert pix[200, 0] == 0x00 and pix[200, 8] == 0x21
+    for y in (50, 100):
+        assert pix[y, 0] == 0x21 and pix[y, 8] == 0x0F
+    for y in (101, 200):
+        assert pix[y, 0] == 0x0F and pix[y, 8] == 0x21
+
+
+def test_mask_write_mid_line_cuts_to_the_backdrop_at_its_tile():
+    """$2001 = 0 by a 4-cycle store from dot 100 of line 50 lands at position 100 + 39 = 139: slots 0..16 are drawn
+    before it (pixels 0..119 from the background), the rest of the line and every later line is the backdrop."""
+    p = Picture(mask=0x0A)
+    p.opaque_tile(1)
+    p.nt[:960] = 0x01
+    p.palette(0, 0x0F)
+    p.palette(1, 0x21)
+    p.event(50, 100, 'mask', 0x00)
+    pix = p.render()
+    assert (pix[49] == 0x21).all()
+    assert (pix[50, :120] == 0x21).all() and (pix[50, 120:] == 0x0F).all()
+    assert (pix[51:] == 0x0F).all()
+
+
+def test_fine_x_written_mid_line_shifts_the_rest_of_it():
+    """A first $2005 write of 3 (coarse x 0, fine x 3) from dot 100 of line 60: slots 0..16 keep fine x 0; from
+    pixel 120 on each pixel x shows background column x + 3; line 61 takes coarse x 0 from t and keeps fine x 3."""
+    p = Picture(mask=0x0A)
+    stripes(p)
+    p.event(60, 100, 'scroll', 0x03, 0)
+    pix = p.render()
+    col = np.arange(256)
+    want = lambda shift: np.where(((col + shift) // 8) % 2 == 0, 0x21, 0x0F)
+    assert np.array_equal(pix[59], want(0))
+    assert np.array_equal(pix[60, :120], want(0)[:120]) and np.array_equal(pix[60, 120:], want(3)[120:])
+    assert np.array_equal(pix[61], want(3))
+
+
+def test_address_written_mid_line_moves_the_fetches_at_once():
+    """Rows 0-14 of the nametable opaque, rows 15-29 transparent. $2006 = $21 from dot 90 and $E0 from dot 102 of
+    line 40 (4-cycle stores, positions 129 and 141): the second write sets v = $21E0 (row 15, fine y 2) after slot
+    16, so background columns 0..16 (pixels 0..135) come from row 5 and the rest from row 15; line 41 stays in
+    row 15."""
+    p = Picture(mask=0x0A)
+    p.opaque_tile(1)
+    p.nt[:15 * 32] = 0x01
+    p.palette(0, 0x0F)
+    p.palette(1, 0x21)
+    p.event(40, 90, 'addr', 0x21, 0)
+    p.event(40, 102, 'addr', 0xE0, 1)
+    pix = p.render()
+    assert (pix[39] == 0x21).all()
+    assert (pix[40, :136] == 0x21).all() and (pix[40, 136:] == 0x0F).all()
+    assert (pix[41] == 0x0F).all()
+
+
+def test_palette_write_draws_nothing_first():
+    """A $2007 palette write (colour 1 = $16) from dot 100 of line 70 triggers no drawing: the whole line is drawn
+    at its end with the new colour. On line 75 a $2000 write from dot 50 (position 89) first draws slots 0..10, so
+    pixels 0..71 keep the old colour."""
+    p = Picture(mask=0x0A)
+    p.opaque_tile(1)
+    p.nt[:960] = 0x01
+    p.nt[1024:1024 + 960] = 0x01                         # (the write's own address increment moves the fetches)
+    p.palette(1, 0x21)
+    p.event(70, 100, 'pal', 0x16, 1)
+    p.event(72, 100, 'pal', 0x21, 1)
+    p.event(75, 50, 'ctrl', 0x00)
+    p.event(75, 100, 'pal', 0x16, 1)
+    pix = p.render()
+    assert (pix[69] == 0x21).all() and (pix[70] == 0x16).all() and (pix[72] == 0x21).all()
+    assert (pix[75, :72] == 0x21).all() and (pix[75, 72:] == 0x16).all()
+    assert (pix[76] == 0x16).all()
+
+
+def test_greyscale_applies_only_while_rendering():
+    """Greyscale keeps bits 4-5 of each colour while the background or sprites are on; with both off the backdrop
+    keeps all six bits ($2D stays $2D)."""
+    p = Picture(mask=0x0A | 0x01 | 0xE0)
+    p.chr_view[0x0010] = 0x80
+    p.nt[0] = 0x01
+    p.palette(1, 0x2D)
+    pix, emph = p.con.render_full()
+    assert pix[0, 0] == 0x2D & 0x30 and (emph == 7).all()
+    q = Picture(mask=0x01)
+    q.palette(0, 0x2D)
+    assert (q.render() == 0x2D).all()
+
+
+def test_emphasis_is_the_mask_at_the_end_of_the_line():
+    """Emphasis bits from $2001 written from dot 100 of line 90 (during its pixels) show on line 90 itself; written
+    from dot 300 of line 80 (after position 272) they start on line 81."""
+    p = Picture(mask=0x0A)
+    p.event(80, 300, 'mask', 0x2A)
+    p.event(90, 100, 'mask', 0x4A)
+    pix, emph = p.con.render_full()
+    assert emph[80] == 0 and emph[81] == 1 and emph[89] == 1 and emph[90] == 2
+
+
+def test_sprite_line_latched_while_sprites_were_on_is_drawn_when_they_come_back():
+    """Sprite 1 covers lines 100-107. Sprites are on at the end of line 99 (its line is latched) and turned off by
+    a write from dot 10 of line 100, so line 100 draws no sprite and keeps the latched line pending; turned on again
+    from dot 10 of line 120, line 120 draws that stale line (x 40) and line 121 nothing."""
+    p = Picture(mask=0x1E)
+    p.opaque_tile(2)
+    p.palette(0x11, 0x16)
+    p.oam[4:8] = (99, 2, 0, 40)
+    p.event(100, 10, 'mask', 0x0E)
+    p.event(120, 10, 'mask', 0x1E)
+    pix = p.render()
+    assert pix[99, 40] == 0x00 and pix[100, 40] == 0x00 and pix[110, 40] == 0x00
+    assert (pix[120, 40:48] == 0x16).all() and pix[120, 39] == 0x00 and pix[121, 40] == 0x00
+
+
+def test_rendering_turned_on_during_the_prefetch_shifts_the_line():
+    """Background turned on by a 2-cycle write from dot 326 of the pre-render line (replay time -4, inside line 0's
+    lead-in, position 18): v = t is not done (rendering was off), slots 0-1 are drawn with rendering off and still
+    advance the output position by 16, and the shift registers start empty, so line 0 shows background column j at
+    pixel 32 + 8j."""
+    p = Picture(mask=0x00)
+    stripes(p)
+    p.event(-1, 326, 'mask', 0x0A, cycles=2)
+    pix = p.render()
+    col = np.arange(256)
+    want = np.where(col < 32, 0x0F, np.where(((col - 32) // 8) % 2 == 0, 0x21, 0x0F))
+    assert np.array_equal(pix[0], want)
 
 
 def test_sprite_priority_and_eight_per_line():
@@ -273,24 +449,66 @@ def test_sprite_priority_and_eight_per_line():
     assert all(pix[80, 8 + 16 * i] == 0x33 for i in range(8)) and pix[80, 8 + 16 * 8] == 0x01
 
 
-def test_greyscale_and_emphasis():
-    p = Picture(mask=0x0A | 0x01 | 0xE0)
-    p.chr_view[0x0010] = 0x80
-    p.nt[0] = 0x01
-    p.palette(1, 0x2D)
-    pix, emph = p.con.render_full()
-    assert pix[0, 0] == 0x2D & 0x30 and (emph == 7).all()
+# ------------------------------------------------------------------------------------------- sprite 0
+
+def sprite0(p):
+    hit = ctypes.c_int(0)
+    dot = p.con.lib.orc_sprite0_hit(p.con.rec.ctypes.data, p.con.cart_ptr(), ctypes.byref(hit))
+    return dot, hit.value
 
 
 def test_sprite0_hit_dot():
+    """Sprite 0 from line 31 at x 40 over opaque background: pixel 40 is drawn (with the slot the pending check
+    adds) and left of p - 16 from line position 57, so a 4-cycle $2002 read that ends there, i.e. starts at NeSLE
+    dot 31 * 341 - 16 + 57 - 12 - 11, sees the flag. x 255 never hits: the answer is then the end of sprite 0's
+    lines (line 46, position 256); sprite 0 below the picture gives no check at all."""
     p = Picture(mask=0x1E)
-    for row in range(8):
-        p.chr_view[0x0010 + row] = 0xFF
+    p.opaque_tile(1)
     p.nt[:960] = 0x01
-    p.oam[0:4] = (30, 1, 0, 40)                          # sprite 0 from line 31, x 40, over opaque background
-    assert p.con.lib.orc_sprite0_scan(p.con.rec.ctypes.data, p.con.cart_ptr()) == 31 * 341 + 40 + 1
-    p.oam[3] = 255                                       # x = 255 never hits
-    assert p.con.lib.orc_sprite0_scan(p.con.rec.ctypes.data, p.con.cart_ptr()) == 0x7FFFFFFF
-    p.oam[3] = 2                                         # left 8 pixels clipped for sprites: first hit at x 8
-    p.h[1] = 0x18 << 8
-    assert p.con.lib.orc_sprite0_scan(p.con.rec.ctypes.data, p.con.cart_ptr()) == 31 * 341 + 8 + 1
+    p.oam[0:4] = (30, 1, 0, 40)
+    assert sprite0(p) == (31 * 341 - 16 + 57 - 23, 1)
+    p.oam[3] = 255
+    assert sprite0(p) == (46 * 341 + 256 - 11, 0)
+    p.oam[0] = 239
+    assert sprite0(p) == (0, 0)
+
+
+def test_sprite0_hit_left_column_follows_the_background_clip_only():
+    """Sprite 0 at x 2. With the background's left column hidden the first opaque background pixel under it is 8,
+    seen from position 32 (slot 4 drawn, 8 < 32 - 16); with it shown the hit is at x 2 from position 19 even though
+    the sprites' own left column is hidden (FCEUmm's check looks at the background only)."""
+    p = Picture(mask=0x18)
+    p.opaque_tile(1)
+    p.nt[:960] = 0x01
+    p.oam[0:4] = (30, 1, 0, 2)
+    assert sprite0(p) == (31 * 341 - 16 + 32 - 23, 1)
+    p.h[1] = 0x1A << 8
+    assert sprite0(p) == (31 * 341 - 16 + 19 - 23, 1)
+
+
+def test_bit_2002_polling_sees_the_hit_at_its_dot():
+    """A BIT $2002 / BVC loop (7 cycles) spinning on bit 6 with sprite 0 at line 31, x 40: the first BIT that reads
+    the flag is the first one that starts at or after the hit dot (31 * 341 + 18), and none before it does."""
+    prg = bytearray(16384)
+    prg[0:5] = bytes((0x2C, 0x02, 0x20, 0x50, 0xFB))     # $C000: BIT $2002; BVC $C000
+    prg[5:8] = bytes((0x4C, 0x05, 0xC0))                 # $C005: JMP $C005
+    prg[0x3FFA:0x4000] = bytes((0x00, 0xC0, 0x00, 0xC0, 0x00, 0xC0))
+    chr_ = bytearray(8192)
+    for row in range(8):
+        chr_[0x10 + row] = 0xFF
+    con = Console(synth.ines(bytes(prg), bytes(chr_), 0, vertical=True))
+    con.set('p', 0x24)
+    con.write(0x2001, 0x1E)
+    con.mem('nt', 2048)[:960] = 0x01
+    oam = con.mem('oam', 256)
+    oam[:] = 0xFF
+    oam[0:4] = (30, 1, 0, 40)
+    assert con.run_until(FRAME) == 0                     # through a pre-render line: the frame's check is scheduled
+    hit_dot = 31 * 341 + 18
+    starts = []
+    while con.u('pc', 'H') != 0xC005:
+        if con.u('pc', 'H') == 0xC000:
+            starts.append(con.u('frame_dot', 'I'))
+        cyc, fault = con.step()
+        assert fault == 0 and con.u('frame', 'I') == 1
+    assert starts[-1] >= hit_dot and starts[-2] < hit_dot
