@@ -88,9 +88,6 @@ def parse():
     ap.add_argument('--cart-seed', type=int, default=1)
     ap.add_argument('--seed', type=int, default=1)
     ap.add_argument('--host-slots', type=int, default=4, help='pinned host ring slots of rollout-pack6')
-    ap.add_argument('--emu', choices=('lane', 'wave'), default=None,
-                    help='emulation kernel: one console per wavefront (k_emu_w, default) or per lane (k_emu)')
-    ap.add_argument('--cpw', type=int, default=0, help='consoles per wavefront of k_emu (0 = library default)')
     ap.add_argument('--cpu-seconds', type=float, default=10.0)
     ap.add_argument('--cpu-consoles', type=int, default=64)
     ap.add_argument('--no-cpu', action='store_true', help='skip the parity check and the CPU baseline')
@@ -108,10 +105,6 @@ def main():
         sys.exit(2)
     if args.steps < 1 or args.warmup < 1:
         sys.exit('need --steps >= 1 and --warmup >= 1')
-    if args.cpw:
-        os.environ['RLENV_CPW'] = str(args.cpw)
-    if args.emu:
-        os.environ['RLENV_EMU'] = args.emu
     import torch
     if not torch.cuda.is_available():
         sys.exit('bench.py needs a HIP device')

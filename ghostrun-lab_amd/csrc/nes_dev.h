@@ -17,11 +17,10 @@
 #include <stdint.h>
 
 #include "nesrec.h"
+#include "replay_dev.h"
 
 namespace nd {
 
-constexpr uint32_t kRamStride = 2052;   // LDS bytes per console: 513 words, so equal offsets of 64 consoles hit 64 banks
-constexpr uint32_t kNoHit = 0x7FFFFFFFu;
 constexpr uint64_t kDmcIdle = ~0ull;
 constexpr uint32_t FL_C = 1, FL_Z = 2, FL_I = 4, FL_D = 8, FL_B = 16, FL_U = 32, FL_V = 64, FL_N = 128;
 
@@ -48,8 +47,8 @@ struct Con {
     uint32_t pad, shift, strobe, instr;
     uint32_t frame_dot, frame;
     uint32_t v, t, ctrl, mask, status, oam_addr, fx, w, read_buf, open_bus;
-    int32_t s0_dot;
-    uint32_t log_frame, log_n, s0_valid;
+    uint32_t s0_sched;
+    uint32_t log_frame, log_n, log_flags;
     uint64_t dmc_event;
     uint32_t prg0, prg1, prg2, prg3;   // PRG byte offsets of $8000/$A000/$C000/$E000
     uint32_t nt_map;                   // 4 x 2 bits
@@ -98,11 +97,12 @@ struct Mem {
     uint8_t* oam;
     uint8_t* pal;
     Cart cart;
+    uint32_t* scratch;      // 34 words of LDS for the sprite-0 check's MMC2 pages
 };
 
 // The memories of a console record, with the CPU RAM at `ram`.
 __device__ __forceinline__ Mem mem_of(NesRec* rec, uint8_t* ram, const Cart& cart) {
-    return Mem{rec, ram, rec->nt, rec->oam, rec->pal, cart};
+    return Mem{rec, ram, rec->nt, rec->oam, rec->pal, cart, nullptr};
 }
 
 __device__ __forceinline__ uint32_t sel4(uint32_t i, uint32_t a, uint32_t b, uint32_t c, uint32_t d) {
@@ -147,14 +147,6 @@ __device__ inline uint32_t nt_map_of(uint32_t kind) {   // 0 horizontal, 1 verti
 __device__ inline void map_set_nt(Con& c, const Mem& m, uint32_t kind) {
     c.nt_map = nt_map_of(kind);
     for (uint32_t k = 0; k < 4; ++k) m.rec->nt_map[k] = (uint8_t)((c.nt_map >> (2 * k)) & 3u);
-}
-
-// MMC2: an address in $0FD0-$0FEF / $1FD0-$1FEF flips the latch of its half (FCEUmm's PPU_hook ranges,
-// patch:3196-3220, 1390-1402). 0 = none, else the latch value + 1 | half << 2.
-__device__ __forceinline__ uint32_t mmc2_trigger(uint32_t a) {
-    const uint32_t high = (a >> 8) & 0x3Fu, low = a & 0xF0u;
-    if (high >= 0x20u || (high & 0x0Fu) != 0x0Fu || (low != 0xD0u && low != 0xE0u)) return 0;
-    return (low == 0xE0u ? 2u : 1u) | (high < 0x10u ? 0u : 4u);
 }
 
 // Page tables from the board registers (MMC1: control, CHR0, CHR1, PRG; MMC3: R0-R7, select, mirroring, ...;
@@ -334,333 +326,53 @@ __device__ __forceinline__ uint32_t dmc_service(NesRec* r, uint64_t now, int ste
     return stolen;
 }
 
-// ------------------------------------------------------------------------------- line replay (frame log)
-// Renderer state of one line: the PPU state at dot 320 of the line before (the first tile prefetch).
-struct Replay {
-    uint32_t v, t, fx, ctrl, mask;
-    uint32_t chr_lo, chr_hi;   // 1 KB CHR page of slots 0-3 / 4-7, 8 bits each
-    uint32_t nt_map;
-    uint32_t creg, latch;      // MMC2: the 4 CHR registers (8 bits each), latch 0 | latch 1 << 8
-    uint32_t mmc2_pages;       // MMC2: the cart's 1 KB CHR pages; 0 on other boards
-    uint32_t ev, count;
-    int32_t next;              // time of event ev (INT32_MAX when none is left)
-    const uint32_t* events;
-};
-
-// MMC2: half `half`'s slots from its register and latch (patch:1385-1388)
-__device__ __forceinline__ void rp_mmc2_select(Replay& s, uint32_t half) {
-    const uint32_t reg = 2u * half + ((s.latch >> (8u * half)) & 1u);
-    const uint32_t bank = (s.creg >> (8u * reg)) & 0xFFu;
-    uint32_t pk = 0;
-    for (uint32_t i = 0; i < 4u; ++i) pk |= ((bank * 4u + i) & (s.mmc2_pages - 1u)) << (8u * i);
-    if (half) s.chr_hi = pk;
-    else s.chr_lo = pk;
-}
-// MMC2: the latch hook of a pattern fetch at a (patch:1390-1402)
-__device__ __forceinline__ void rp_hook(Replay& s, uint32_t a) {
-    const uint32_t t = mmc2_trigger(a);
-    if (t == 0) return;
-    const uint32_t half = t >> 2;
-    s.latch = (s.latch & ~(0xFFu << (8u * half))) | (((t & 3u) - 1u) << (8u * half));
-    rp_mmc2_select(s, half);
-}
-
-__device__ __forceinline__ int32_t rp_time(const Replay& s, uint32_t i) {
-    return (int32_t)(s.events[2u * i] & 0xFFFFFFu) - NES_LOG_TIME_BIAS;
-}
-
-// Applies event i. Palette writes go to `pal` (nullptr: ignored, as in the sprite-0 scan).
-__device__ inline void rp_apply(Replay& s, uint32_t i, uint8_t* pal) {
-    const uint32_t w0 = s.events[2u * i], w1 = s.events[2u * i + 1u];
-    const uint32_t kind = w0 >> 24, val = w1 & 0xFFu, aux = (w1 >> 8) & 0xFFu;
-    const uint32_t step = (s.ctrl & 4u) ? 32u : 1u;
-    if (kind == NES_EV_CTRL) {
-        s.ctrl = val;
-        s.t = (s.t & 0xF3FFu) | ((val & 3u) << 10);
-    } else if (kind == NES_EV_MASK) {
-        s.mask = val;
-    } else if (kind == NES_EV_SCROLL) {
-        if (aux == 0) {
-            s.t = (s.t & 0xFFE0u) | (val >> 3);
-            s.fx = val & 7u;
-        } else {
-            s.t = (s.t & 0x0C1Fu) | ((val & 7u) << 12) | ((val & 0xF8u) << 2);
-        }
-    } else if (kind == NES_EV_ADDR) {
-        if (aux == 0) {
-            s.t = (s.t & 0x00FFu) | ((val & 0x3Fu) << 8);
-        } else {
-            s.t = (s.t & 0xFF00u) | val;
-            s.v = s.t;
-        }
-    } else if (kind == NES_EV_DATA) {
-        s.v = (s.v + aux * step) & 0x7FFFu;
-    } else if (kind == NES_EV_PAL) {
-        if (pal) pal[aux & 31u] = (uint8_t)val;
-        s.v = (s.v + step) & 0x7FFFu;
-    } else if (kind == NES_EV_CHR) {
-        const uint32_t sh = (aux & 3u) * 8u, keep = ~(0xFFu << sh);
-        if (aux & 4u) s.chr_hi = (s.chr_hi & keep) | (val << sh);
-        else s.chr_lo = (s.chr_lo & keep) | (val << sh);
-    } else if (kind == NES_EV_MIRROR) {
-        s.nt_map = val;
-    } else if (kind == NES_EV_MMC2) {   // patch:1471-1478
-        if (aux < 4u) {
-            s.creg = (s.creg & ~(0xFFu << (8u * aux))) | (val << (8u * aux));
-            rp_mmc2_select(s, aux >> 1);
-        } else if (aux == 6u || aux == 7u) {
-            const uint32_t h = aux - 6u;
-            s.latch = (s.latch & ~(0xFFu << (8u * h))) | ((val & 1u) << (8u * h));
-            rp_mmc2_select(s, h);
-        }
-    }
-}
-
-__device__ __forceinline__ void rp_next(Replay& s) {
-    s.next = s.ev < s.count ? rp_time(s, s.ev) : INT32_MAX;
-}
-
-// Applies the events before `time`; the time of the next one is kept in a register, so a check with nothing to apply
-// reads no memory.
-__device__ inline void rp_until(Replay& s, int32_t time, uint8_t* pal) {
-    while (s.next < time) {
-        rp_apply(s, s.ev, pal);
-        ++s.ev;
-        rp_next(s);
-    }
-}
-
-__device__ inline void rp_yinc(Replay& s) {
-    if ((s.v & 0x7000u) != 0x7000u) {
-        s.v += 0x1000u;
-        return;
-    }
-    s.v &= ~0x7000u;
-    uint32_t cy = (s.v >> 5) & 31u;
-    if (cy == 29u) {
-        cy = 0;
-        s.v ^= 0x0800u;
-    } else if (cy == 31u) {
-        cy = 0;
-    } else {
-        ++cy;
-    }
-    s.v = (s.v & ~0x03E0u) | (cy << 5);
-}
-
-// After line l's pixels: Y increment (dot 256), horizontal copy (257), on the pre-render line (l = -1) the vertical
-// copy (304); the state at dot 320 is the next line's.
-__device__ inline void rp_line_end(Replay& s, int l, uint8_t* pal) {
-    const int32_t base = l * 341;
-    rp_until(s, base + 256, pal);
-    if (s.mask & 0x18u) rp_yinc(s);
-    rp_until(s, base + 257, pal);
-    if (s.mask & 0x18u) s.v = (s.v & ~0x041Fu) | (s.t & 0x041Fu);
-    if (l < 0) {
-        rp_until(s, base + 304, pal);
-        if (s.mask & 0x18u) s.v = (s.v & ~0x7BE0u) | (s.t & 0x7BE0u);
-    }
-    rp_until(s, base + 320, pal);
-}
-
-// events: the log's event words (from `log` + NES_LOG_HDR_WORDS on), in place or a copy of them. mmc2_pages: the
-// cart's 1 KB CHR pages on MMC2, else 0.
-__device__ inline void rp_begin(Replay& s, const uint32_t* log, uint32_t log_n, uint8_t* pal, const uint32_t* events,
-                                uint32_t mmc2_pages) {
-    const uint32_t h1 = log[1], h2 = log[2], h3 = log[3], h4 = log[4];
-    s.creg = log[14];
-    s.latch = log[15];
-    s.mmc2_pages = mmc2_pages;
-    s.ctrl = h1 & 0xFFu;
-    s.mask = (h1 >> 8) & 0xFFu;
-    s.fx = (h1 >> 16) & 7u;
-    s.v = h2 & 0xFFFFu;
-    s.t = h2 >> 16;
-    s.chr_lo = h3;
-    s.chr_hi = h4;
-    s.nt_map = log[5] & 0xFFu;
-    if (pal)
-        for (uint32_t i = 0; i < 8; ++i) {
-            const uint32_t w = log[6 + i];
-            pal[4 * i] = (uint8_t)w; pal[4 * i + 1] = (uint8_t)(w >> 8);
-            pal[4 * i + 2] = (uint8_t)(w >> 16); pal[4 * i + 3] = (uint8_t)(w >> 24);
-        }
-    s.events = events;
-    s.count = log_n < NES_LOG_EVENTS ? log_n : NES_LOG_EVENTS;
-    s.ev = 0;
-    rp_next(s);
-    rp_line_end(s, -1, pal);
-}
-
-// Background 2-bit value at pixel x of a line drawn with state s (nametables/CHR read through the record), the
-// pattern bytes through the slot pages lo/hi.
-__device__ inline uint32_t rp_bg(const Replay& s, const Mem& m, uint32_t x, uint32_t* pal_sel, uint32_t lo_pk,
-                                 uint32_t hi_pk) {
-    const uint32_t pos = x + s.fx, bit = pos & 7u;
-    uint32_t cx = (s.v & 31u) + (pos >> 3), nth = (s.v >> 10) & 1u;
-    if (cx >= 32u) {
-        cx -= 32u;
-        nth ^= 1u;
-    }
-    const uint32_t cy = (s.v >> 5) & 31u, fy = (s.v >> 12) & 7u;
-    const uint32_t base = 0x2000u | ((nth | (((s.v >> 11) & 1u) << 1)) << 10);
-    const uint32_t tile = m.nt[nt_index(s.nt_map, base | (cy << 5) | cx)];
-    const uint32_t at = m.nt[nt_index(s.nt_map, base | 0x3C0u | ((cy >> 2) << 3) | (cx >> 2))];
-    *pal_sel = (at >> (((cy & 2u) << 1) | (cx & 2u))) & 3u;
-    const uint32_t pa = ((s.ctrl & 0x10u) << 8) + tile * 16u + fy;
-    const uint32_t lo = chr_byte_pk(m, lo_pk, hi_pk, pa), hi = chr_byte_pk(m, lo_pk, hi_pk, pa + 8u);
-    return ((lo >> (7u - bit)) & 1u) | (((hi >> (7u - bit)) & 1u) << 1);
-}
-
-__device__ inline uint32_t sprite_row_addr(uint32_t ctrl, uint32_t tile, uint32_t attr, uint32_t row) {
-    const uint32_t h = (ctrl & 0x20u) ? 16u : 8u;
-    if (attr & 0x80u) row = h - 1u - row;
-    if (h == 8u) return ((ctrl & 0x08u) << 9) + tile * 16u + row;
-    return ((tile & 1u) << 12) + (tile & 0xFEu) * 16u + (row & 7u) + ((row & 8u) << 1);
-}
-
-// MMC2: the pattern fetches of line l in order, each through the slot pages of the moment and then the latch hook
-// (patch:1496-1560, 1660-1700): the sprites of line l, fetched at the end of line l - 1 (l >= 1), then, unless
-// sprites_only, the line's 34 background tile slots. sink(kind, index, chr_lo, chr_hi, pa) gets the pages each
-// fetch read through and its pattern address (kind 0: sprite rank, 1: tile slot). Fetches happen only while
-// rendering is on. Wave-uniform.
-template <class Sink>
-__device__ __forceinline__ void rp_mmc2_line(Replay& s, const uint8_t* nt, const uint8_t* oam, int l, bool sprites_only,
-                                    Sink&& sink) {
-    if (s.mmc2_pages == 0 || (s.mask & 0x18u) == 0) return;
-    if (l >= 1) {
-        const int h = (s.ctrl & 0x20u) ? 16 : 8;
-        uint32_t n = 0;
-        for (uint32_t i = 0; i < 64u && n < 8u; ++i) {
-            const int row = l - (int)oam[4u * i] - 1;
-            if (row < 0 || row >= h) continue;
-            const uint32_t pa = sprite_row_addr(s.ctrl, oam[4u * i + 1u], oam[4u * i + 2u], (uint32_t)row);
-            sink(0u, n, s.chr_lo, s.chr_hi, pa);
-            rp_hook(s, pa);
-            ++n;
-        }
-    }
-    if (sprites_only) return;
-    const uint32_t cy = (s.v >> 5) & 31u, fy = (s.v >> 12) & 7u, ntv = (s.v >> 11) & 1u;
-    for (uint32_t t = 0; t < 34u; ++t) {   // one tile right per slot, the nametable switching at each wrap
-        const uint32_t cc = (s.v & 31u) + t, nth = ((s.v >> 10) & 1u) ^ ((cc >> 5) & 1u);
-        const uint32_t base = 0x2000u | ((nth | (ntv << 1)) << 10);
-        const uint32_t pa = ((s.ctrl & 0x10u) << 8) + nt[nt_index(s.nt_map, base | (cy << 5) | (cc & 31u))] * 16u + fy;
-        sink(1u, t, s.chr_lo, s.chr_hi, pa);
-        rp_hook(s, pa);
-    }
-}
-
-// First sprite-0 hit of the logged frame on MMC2 (the scan below, with each line's fetches moving the latches):
-// sprite 0 and the two tile slots under it read through the pages of their own fetches.
-__device__ inline int32_t sprite0_scan_mmc2(const Mem m, uint32_t log_n) {
-    const uint8_t* oam = m.oam;
-    const int y0 = oam[0], x0 = oam[3];
-    if (y0 >= 239) return (int32_t)kNoHit;
-    const uint32_t tile = oam[1], attr = oam[2];
-    Replay s;
-    rp_begin(s, m.rec->log, log_n, nullptr, m.rec->log + NES_LOG_HDR_WORDS, m.cart.chr_pages1);
-    for (int l = 0; l < 240; ++l) {
-        const uint32_t slot_a = ((uint32_t)x0 + s.fx) >> 3;
-        uint32_t s0lo = s.chr_lo, s0hi = s.chr_hi, alo = s.chr_lo, ahi = s.chr_hi, blo = s.chr_lo, bhi = s.chr_hi;
-        rp_mmc2_line(s, m.nt, oam, l, false, [&](uint32_t kind, uint32_t i, uint32_t lo, uint32_t hi, uint32_t) {
-            if (kind == 0u && i == 0u) { s0lo = lo; s0hi = hi; }
-            if (kind == 1u && i == slot_a) { alo = lo; ahi = hi; }
-            if (kind == 1u && i == slot_a + 1u) { blo = lo; bhi = hi; }
-        });
-        const int h = (s.ctrl & 0x20u) ? 16 : 8;
-        const int row = l - y0 - 1;
-        if ((s.mask & 0x18u) == 0x18u && row >= 0 && row < h) {
-            const uint32_t pa = sprite_row_addr(s.ctrl, tile, attr, (uint32_t)row);
-            const uint32_t lo = chr_byte_pk(m, s0lo, s0hi, pa), hi = chr_byte_pk(m, s0lo, s0hi, pa + 8u);
-            for (int col = 0; col < 8; ++col) {
-                const int x = x0 + col;
-                if (x >= 255) break;
-                if (x < 8 && (s.mask & 0x06u) != 0x06u) continue;
-                const uint32_t b = (attr & 0x40u) ? (uint32_t)col : 7u - (uint32_t)col;
-                if ((((lo >> b) & 1u) | ((hi >> b) & 1u)) == 0) continue;
-                uint32_t ps;
-                const bool in_a = (((uint32_t)x + s.fx) >> 3) == slot_a;
-                if (rp_bg(s, m, (uint32_t)x, &ps, in_a ? alo : blo, in_a ? ahi : bhi)) return l * 341 + x + 1;
-            }
-        }
-        if (l >= y0 + 16) break;
-        rp_line_end(s, l, nullptr);
-    }
-    return (int32_t)kNoHit;
-}
-
-// First sprite-0 hit of the logged frame from the events logged so far (frame dot), kNoHit if none.
-__device__ __forceinline__ int32_t sprite0_scan(const Mem m, uint32_t log_n) {
-    if (m.cart.board == NES_BOARD_MMC2) return sprite0_scan_mmc2(m, log_n);
-    const uint8_t* oam = m.oam;
-    const int y0 = oam[0], x0 = oam[3];
-    if (y0 >= 239) return (int32_t)kNoHit;
-    const uint32_t tile = oam[1], attr = oam[2];
-    Replay s;
-    rp_begin(s, m.rec->log, log_n, nullptr, m.rec->log + NES_LOG_HDR_WORDS, 0u);
-    for (int l = 0; l < 240; ++l) {
-        const int h = (s.ctrl & 0x20u) ? 16 : 8;
-        const int row = l - y0 - 1;
-        if ((s.mask & 0x18u) == 0x18u && row >= 0 && row < h) {
-            const uint32_t pa = sprite_row_addr(s.ctrl, tile, attr, (uint32_t)row);
-            const uint32_t lo = chr_byte_pk(m, s.chr_lo, s.chr_hi, pa), hi = chr_byte_pk(m, s.chr_lo, s.chr_hi, pa + 8u);
-            for (int col = 0; col < 8; ++col) {
-                const int x = x0 + col;
-                if (x >= 255) break;
-                if (x < 8 && (s.mask & 0x06u) != 0x06u) continue;
-                const uint32_t b = (attr & 0x40u) ? (uint32_t)col : 7u - (uint32_t)col;
-                if ((((lo >> b) & 1u) | ((hi >> b) & 1u)) == 0) continue;
-                uint32_t ps;
-                if (rp_bg(s, m, (uint32_t)x, &ps, s.chr_lo, s.chr_hi)) return l * 341 + x + 1;
-            }
-        }
-        if (l >= y0 + 16) break;
-        rp_line_end(s, l, nullptr);
-    }
-    return (int32_t)kNoHit;
-}
-
 // ------------------------------------------------------------------------------------- PPU timing events
-__device__ __forceinline__ uint64_t abs_dot(const Con& c) { return (uint64_t)c.frame * NES_FRAME_DOTS + c.frame_dot; }
-
-__device__ inline void s0_refresh(Con& c, const Mem& m) {
-    if (c.s0_valid || c.frame != c.log_frame) return;
-    c.s0_valid = 1;
-    c.s0_dot = (int32_t)kNoHit;
-    if ((c.status & 0x40u) || c.frame_dot >= 240u * 341u) return;
-    int32_t hit = sprite0_scan(m, c.log_n);
-    if (hit != (int32_t)kNoHit && hit <= (int32_t)c.frame_dot) hit = (int32_t)c.frame_dot + 1;
-    c.s0_dot = hit;
+__device__ __forceinline__ uint64_t abs_dot(const Con& c) {
+    return (uint64_t)uni(c.frame) * NES_FRAME_DOTS + uni(c.frame_dot);
 }
 
-// Dots from the current frame dot to the next PPU event. Written as a search for the nearest absolute event dot
-// (every candidate is compared, never subtracted, before the one final difference): the min-of-differences form
-// `if (fd < E) best = min(best, E - fd)` is folded by the gfx950 compiler into an unguarded min, which returns 0 when
-// fd == E and stalls ppu_advance.
-__device__ inline uint32_t dots_to_event(Con& c, const Mem& m) {
-    const uint32_t fd = c.frame_dot;
-    uint32_t next = NES_FRAME_DOTS;
-    if (fd < NES_PRERENDER_DOT) next = NES_PRERENDER_DOT;
-    if (fd < NES_VBLANK_DOT) next = NES_VBLANK_DOT;
+// Dots from frame dot `cur` to the next MMC3 counter clock (dot 266 of lines 0-239, dot 256 of the pre-render line),
+// strictly after it (patch:1881-1903).
+__device__ __forceinline__ uint32_t dots_to_mmc3_clock(uint32_t cur) {
+    const uint32_t line = cur / 341u, d = cur - line * 341u;
+    if (line < 240u) {
+        if (d < 266u) return 266u - d;
+        if (line + 1u < 240u) return 341u - d + 266u;
+        return (261u - line) * 341u + 256u - d;
+    }
+    if (line < 261u) return (261u - line) * 341u + 256u - d;
+    if (d < 256u) return 256u - d;
+    return 341u - d + 266u;
+}
+
+// Dots from the current frame dot to the next PPU event (patch:2001-2037): the frame wrap, vblank, the pre-render
+// line, the $2002 flag set and clear dots, the scheduled sprite-0 check and, on MMC3, the counter clocks. A short
+// frame ends a dot early. Written as a search for the nearest event at an absolute dot (events at or before the
+// current dot count from the next frame), then one difference.
+__device__ inline uint32_t dots_to_event(const Con& c, const Mem& m) {
+    const uint32_t cur = uni(c.frame_dot), skip = (uni(c.log_flags) & NES_LOG_SHORT) ? 1u : 0u;
+    const uint32_t frame = NES_FRAME_DOTS - skip;
+    uint32_t next = frame;
+    auto cand = [&](uint32_t e) {
+        const uint32_t at = e > cur ? e : frame + e;
+        if (at < next) next = at;
+    };
+    cand(NES_VFLAG_DOT);
+    cand(NES_VBLANK_DOT);
+    cand(NES_SCLR_DOT);
+    cand(NES_PRERENDER_DOT);
+    const uint32_t s0 = uni(c.s0_sched) & NES_S0_DOT;
+    if (s0 != 0) cand(s0);
     if (m.cart.board == NES_BOARD_MMC3) {
-        // clocks: dot 266 of lines 0..239, dot 256 of the pre-render line
-        const uint32_t line = fd / 341u, d = fd - line * 341u;
-        uint32_t clk = next;
-        if (line < 239u) clk = d < 266u ? line * 341u + 266u : line * 341u + 341u + 266u;
-        else if (line == 239u) clk = d < 266u ? line * 341u + 266u : 261u * 341u + 256u;
-        else if (line < 261u || d < 256u) clk = 261u * 341u + 256u;
-        if (clk > fd && clk < next) next = clk;
+        uint32_t at = cur + dots_to_mmc3_clock(cur);
+        if (at >= NES_FRAME_DOTS) at -= skip;
+        if (at < next) next = at;
     }
-    s0_refresh(c, m);
-    if (c.frame == c.log_frame && c.s0_dot != (int32_t)kNoHit) {
-        const uint32_t s0 = (uint32_t)c.s0_dot;
-        if (s0 > fd && s0 < next) next = s0;
-    }
-    return next - fd;
+    return next - cur;
 }
 
-__device__ inline void log_capture(Con& c, const Mem& m) {
+// The frame log's header from the live state (patch:1073-1105): taken at the pre-render line, and at power-on.
+__device__ inline void log_header(const Con& c, const Mem& m, uint32_t kook) {
     uint32_t* h = m.rec->log;
     const uint32_t* co = m.rec->chr_off;
     uint32_t p0 = 0, p1 = 0;
@@ -674,94 +386,115 @@ __device__ inline void log_capture(Con& c, const Mem& m) {
     h[2] = c.v | (c.t << 16);
     h[3] = p0;
     h[4] = p1;
-    h[5] = c.nt_map;
+    h[5] = c.nt_map | (kook ? NES_LOG_KOOK : 0u);
     for (uint32_t i = 0; i < 8; ++i) h[6 + i] = pal[i];
     const uint8_t* r = m.rec->mreg;
     const bool mmc2 = m.cart.board == NES_BOARD_MMC2;
     h[14] = mmc2 ? (r[0] | ((uint32_t)r[1] << 8) | ((uint32_t)r[2] << 16) | ((uint32_t)r[3] << 24)) : 0u;
     h[15] = mmc2 ? (r[6] | ((uint32_t)r[7] << 8)) : 0u;
-    c.log_n = 0;
-    c.log_frame = c.frame + 1u;
-    c.s0_valid = 0;
-    c.s0_dot = (int32_t)kNoHit;
 }
 
-// MMC2 at vblank: the latches this frame's own fetches leave, from a latches-only replay of its log over the
-// nametables and OAM as they are now (NeSLE's frame_resolve_mmc2, patch:1790-1812; rl/csrc/nes_machine.cuh:110-131
-// runs the same replay after the vblank stop, before any further instruction). Every frame the kernels run ends at
-// the vblank dot, so they call it at each frame's stop (the vblank just processed, no instruction after it).
-__device__ inline void mmc2_resolve(NesRec* rec, const uint8_t* nt, const uint8_t* oam, uint32_t log_n,
-                                    uint32_t chr_pages) {
-    Replay s;
-    rp_begin(s, rec->log, log_n, nullptr, rec->log + NES_LOG_HDR_WORDS, chr_pages);
-    const auto none = [](uint32_t, uint32_t, uint32_t, uint32_t, uint32_t) {};
-    for (int l = 0; l < 240; ++l) {
-        rp_mmc2_line(s, nt, oam, l, false, none);
-        rp_line_end(s, l, nullptr);
-    }
-    rp_mmc2_line(s, nt, oam, 240, true, none);
-    rp_until(s, INT32_MAX, nullptr);
-    const uint32_t l0 = s.latch & 1u, l1 = (s.latch >> 8) & 1u;
+// The pre-render line: the log starts over for the next frame; every other frame is a kook frame, whose pre-render
+// line is a dot short (patch:1111-1122).
+__device__ inline void log_capture(Con& c, const Mem& m) {
+    const uint32_t flags = uni(c.log_flags), kook = flags & NES_LOG_NEXT_KOOK;
+    log_header(c, m, kook);
+    c.log_n = 0;
+    c.log_frame = uni(c.frame) + 1u;
+    c.log_flags = ((flags ^ NES_LOG_NEXT_KOOK) & ~NES_LOG_SHORT) | (kook ? NES_LOG_SHORT : 0u);
+}
+
+// MMC2 at vblank: the latches the frame's own pattern fetches leave, and the halves' pages they select.
+__device__ inline void mmc2_resolve(Con& c, const Mem& m) {
+    const uint32_t lat = mmc2_latches(m.rec->log, uni(c.log_n), m.nt, m.oam, m.cart.chr_pages1);
+    NesRec* rec = m.rec;
+    const uint32_t l0 = lat & 1u, l1 = (lat >> 8) & 1u;
     rec->mreg[6] = (uint8_t)l0;
     rec->mreg[7] = (uint8_t)l1;
+    const uint32_t b0 = rec->mreg[l0], b1 = rec->mreg[2u + l1];
     for (uint32_t i = 0; i < 4; ++i) {   // the halves' pages, as the board's page sync sets them
-        rec->chr_off[i] = ((4u * rec->mreg[l0] + i) & (chr_pages - 1u)) * 1024u;
-        rec->chr_off[4u + i] = ((4u * rec->mreg[2u + l1] + i) & (chr_pages - 1u)) * 1024u;
+        map_set_chr(m, i, 4u * b0 + i);
+        map_set_chr(m, 4u + i, 4u * b1 + i);
     }
 }
 
-__device__ inline void process_events(Con& c, const Mem& m) {
-    const uint32_t d = c.frame_dot;
-    if (d == NES_FRAME_DOTS) {
-        c.frame_dot = 0;
-        ++c.frame;
-        return;
-    }
-    if (d == NES_VBLANK_DOT) {
-        c.status |= 0x80u;
-        if (c.ctrl & 0x80u) c.nmi_pending = 1;
-    }
-    if (d == NES_PRERENDER_DOT) {
-        c.status &= 0x1Fu;
-        log_capture(c, m);
-    }
-    if (m.cart.board == NES_BOARD_MMC3 && (c.mask & 0x18u) &&
-        ((d < 240u * 341u && d % 341u == 266u) || d == 261u * 341u + 256u))
-        mmc3_clock(c, m);
-    if (c.frame == c.log_frame && c.s0_dot != (int32_t)kNoHit && d == (uint32_t)c.s0_dot) {
-        c.status |= 0x40u;
-        c.s0_dot = (int32_t)kNoHit;
-    }
-}
-
-__device__ inline void ppu_advance(Con& c, const Mem& m, uint32_t dots) {
-    while (dots > 0) {
-        const uint32_t to = dots_to_event(c, m);
-        if (dots < to) {
-            c.frame_dot += dots;
-            return;
+// The PPU over `dots` dots from the current frame dot (NeSLE's settle, patch:2040-2156): every event in the span,
+// per frame in this order - the sprite-0 check, the $2002 vblank flag, vblank (NMI 12 dots after the flag, whether
+// or not a read took it; MMC2's latch resolve), the $2002 clear, the pre-render line (log capture, this frame's
+// sprite-0 check scheduled for sprite 0's first line) - then the span's MMC3 clocks. B: the emulator's board class
+// (the fixed-PRG instantiation has neither MMC2 nor MMC3).
+template <uint32_t B>
+__device__ inline void ppu_step(Con& c, const Mem& m, uint32_t dots) {
+    const uint32_t start = uni(c.frame_dot);
+    uint32_t end = start + dots;
+    if ((uni(c.log_flags) & NES_LOG_SHORT) && end >= NES_FRAME_DOTS - 1u) end += 1u;   // the skipped last dot
+    const uint32_t frames = end / NES_FRAME_DOTS;
+    for (uint32_t f = 0; f <= frames; ++f) {
+        const uint32_t base = f * NES_FRAME_DOTS;
+        auto crossed = [&](uint32_t e) { return base + e > start && base + e <= end; };
+        const uint32_t sched = uni(c.s0_sched), s0 = sched & NES_S0_DOT;
+        if (s0 != 0 && crossed(s0)) {
+            // worked out again with the writes logged so far, unless nothing was logged since the last answer
+            const uint32_t log_n = uni(c.log_n);
+            uint32_t hit, dot;
+            if ((sched & NES_S0_KNOWN) && ((sched >> 20) & 0x1FFu) == log_n) {
+                dot = s0;
+                hit = (sched & NES_S0_HIT) ? 1u : 0u;
+            } else {
+                dot = sprite0_hit(m.rec->log, log_n, m.nt, m.oam, m.cart.chr, m.rec->chr_ram,
+                                  m.cart.board == NES_BOARD_MMC2 ? m.cart.chr_pages1 : 0u, m.scratch, &hit);
+                dot = uni(dot);
+                hit = uni(hit);
+            }
+            const bool reached = base + dot <= end;
+            if (hit && reached) c.status = uni(c.status) | 0x40u;
+            c.s0_sched = dot != 0 && !reached ? dot | NES_S0_KNOWN | (hit ? NES_S0_HIT : 0u) | (log_n << 20) : 0u;
         }
-        c.frame_dot += to;
-        dots -= to;
-        process_events(c, m);
+        if (crossed(NES_VFLAG_DOT)) c.status = uni(c.status) | 0x80u;
+        if (crossed(NES_VBLANK_DOT)) {
+            if (uni(c.ctrl) & 0x80u) c.nmi_pending = 1;
+            if constexpr (B != NES_BOARD_NROM)
+                if (m.cart.board == NES_BOARD_MMC2) mmc2_resolve(c, m);
+        }
+        if (crossed(NES_SCLR_DOT)) c.status = uni(c.status) & 0x1Fu;
+        if (crossed(NES_PRERENDER_DOT)) {
+            c.status = uni(c.status) & 0x1Fu;
+            log_capture(c, m);
+            const uint32_t y = uni(m.oam[0]);
+            c.s0_sched = y < 239u ? (y + 1u) * 341u - 20u - NES_FCEU_LAG : 0u;
+        }
     }
+    if constexpr (B != NES_BOARD_NROM) {
+        // FCEUmm clocks the counter while rendering, unless both pattern tables are at $1000 with 8x8 sprites
+        if (m.cart.board == NES_BOARD_MMC3 && (uni(c.mask) & 0x18u) && (uni(c.ctrl) & 0x38u) != 0x18u) {
+            for (uint32_t la = start / 341u; la <= end / 341u; ++la) {
+                const uint32_t line = la % 262u;
+                const uint32_t at = line < 240u ? 266u : 256u;
+                if (line >= 240u && line != 261u) continue;
+                const uint32_t d = la * 341u + at;
+                if (d > start && d <= end) mmc3_clock(c, m);
+            }
+        }
+    }
+    c.frame_dot = end % NES_FRAME_DOTS;
+    c.frame = uni(c.frame) + frames;
+    if (frames) c.log_flags = uni(c.log_flags) & ~NES_LOG_SHORT;
 }
 
 // ------------------------------------------------------------------------------------------------ bus
 struct Access {
-    int32_t ev_time;   // log time of this instruction's PPU accesses (its last cycle)
-    bool log_on;       // the instruction started inside the log window
+    uint32_t now;      // NeSLE frame dot at which the instruction starts: the stamp of its log events
+    bool log_on;       // the instruction starts while a frame is logged (before vblank or from the pre-render line)
     bool dma;          // a $4014 write happened
 };
 
 __device__ inline void log_event(Con& c, const Mem& m, const Access& ac, uint32_t kind, uint32_t value, uint32_t aux) {
-    if (kind != NES_EV_PAL) c.s0_valid = 0;
     if (!ac.log_on) return;
     uint32_t* h = m.rec->log;
     uint32_t* ev = h + NES_LOG_HDR_WORDS;
     if (kind == NES_EV_DATA && (c.mask & 0x18u) == 0 && c.log_n > 0) {
         uint32_t* last = ev + 2u * (c.log_n - 1u);
-        if ((last[0] >> 24) == NES_EV_DATA && (last[1] >> 8) < 0xFFu) {
+        if ((last[0] & 15u) == NES_EV_DATA && (last[1] >> 8) < 0xFFu) {
             last[1] += 0x100u;
             return;
         }
@@ -770,7 +503,7 @@ __device__ inline void log_event(Con& c, const Mem& m, const Access& ac, uint32_
         h[0] |= NES_LOG_OVERFLOW;
         return;
     }
-    ev[2u * c.log_n] = ((uint32_t)(ac.ev_time + NES_LOG_TIME_BIAS) & 0xFFFFFFu) | (kind << 24);
+    ev[2u * c.log_n] = NES_EV_WORD0(kind, ac.now & 0x1FFFFu);
     ev[2u * c.log_n + 1u] = (value & 0xFFu) | ((aux & 0xFFu) << 8);
     ++c.log_n;
     h[0] = (h[0] & NES_LOG_OVERFLOW) | c.log_n;
@@ -822,7 +555,7 @@ __device__ inline uint32_t io_read(Con& c, const Mem& m, const Access& ac, uint3
                 mmc2_ppu_address(c, m, ac, pa);
             }
             c.v = (c.v + vinc(c)) & 0x7FFFu;
-            log_event(c, m, ac, NES_EV_DATA, 0, 1);
+            log_event(c, m, ac, NES_EV_DREAD, 0, 0);
             mmc2_ppu_address(c, m, ac, c.v & 0x3FFFu);
         } else {
             return c.open_bus;
@@ -873,7 +606,6 @@ __device__ inline void ppu_reg_write(Con& c, const Mem& m, const Access& ac, uin
     } else if (reg == 4) {
         m.oam[c.oam_addr] = (uint8_t)v;
         c.oam_addr = (c.oam_addr + 1u) & 0xFFu;
-        c.s0_valid = 0;
     } else if (reg == 5) {
         log_event(c, m, ac, NES_EV_SCROLL, v, c.w);
         if (c.w == 0) {
@@ -900,12 +632,11 @@ __device__ inline void ppu_reg_write(Con& c, const Mem& m, const Access& ac, uin
         if (pa < 0x2000u) {
             if (!m.cart.chr) {
                 m.rec->chr_ram[(m.rec->chr_off[(pa >> 10) & 7u] + (pa & 0x3FFu)) & (NES_CHRRAM_BYTES - 1u)] = (uint8_t)v;
-                c.s0_valid = 0;
             }
-            log_event(c, m, ac, NES_EV_DATA, 0, 1);
+            log_event(c, m, ac, NES_EV_DATA, 0, 0);
         } else if (pa < 0x3F00u) {
             m.nt[nt_index(c.nt_map, pa)] = (uint8_t)v;
-            log_event(c, m, ac, NES_EV_DATA, 0, 1);
+            log_event(c, m, ac, NES_EV_DATA, 0, 0);
         } else {
             uint32_t i = pa & 0x1Fu;
             if ((i & 0x13u) == 0x10u) i &= 0x0Fu;
@@ -928,7 +659,6 @@ __device__ inline void io_write(Con& c, const Mem& m, Access& ac, uint32_t a, ui
             const uint32_t b = src < 0x2000u ? m.ram[src & 0x7FFu] : bus_read(c, m, ac, src);
             oam[(c.oam_addr + i) & 0xFFu] = (uint8_t)b;
         }
-        c.s0_valid = 0;
         ac.dma = true;
     } else if (a == 0x4016u) {
         c.strobe = v & 1u;
@@ -1001,8 +731,10 @@ __device__ inline void interrupt(Con& c, const Mem& m, uint32_t vector) {
 }
 
 // One step: a pending NMI (or the asserted cartridge IRQ with I clear), then one instruction, the OAM-DMA stall and
-// the DMC service. `start_rel` = log time of the step's first dot. Returns the CPU cycles, 0 with *fault set.
-__device__ inline uint32_t cpu_step(Con& c, const Mem& m, const uint32_t* optab, int32_t start_rel, uint32_t* fault,
+// the DMC service. `now0` = the frame dot of the step's first dot (the settled frame dot plus the dots not settled
+// yet): the instruction's log events are stamped with its start, and with its cycles once it has run (patch:829-836,
+// 1166-1185). Returns the CPU cycles, 0 with *fault set.
+__device__ inline uint32_t cpu_step(Con& c, const Mem& m, const uint32_t* optab, uint32_t now0, uint32_t* fault,
                                     uint32_t* op_out, uint32_t* pc_out) {
     uint32_t cyc = 0;
     if (c.nmi_pending) {
@@ -1013,10 +745,11 @@ __device__ inline uint32_t cpu_step(Con& c, const Mem& m, const uint32_t* optab,
         interrupt(c, m, 0xFFFEu);
         cyc = 7;
     }
-    const int32_t rel = start_rel + 3 * (int32_t)cyc;
     Access ac;
-    ac.log_on = rel >= -340 && rel < (int32_t)NES_VBLANK_DOT;
+    ac.now = now0 + 3u * cyc;
+    ac.log_on = ac.now < NES_VBLANK_DOT || ac.now >= NES_PRERENDER_DOT;
     ac.dma = false;
+    const uint32_t logged = c.log_n;
     // fetch opcode + operands
     const uint32_t pc = c.pc;
     uint32_t word;
@@ -1052,7 +785,6 @@ __device__ inline uint32_t cpu_step(Con& c, const Mem& m, const uint32_t* optab,
         ea = (base + idx) & 0xFFFFu;
         if ((d & D_PEN) && ((base ^ ea) & 0xFF00u)) ++icyc;
     }
-    ac.ev_time = rel + 3 * (int32_t)icyc;
     uint32_t opd = lo;
     if (d & D_READ) opd = bus_read(c, m, ac, ea);
     uint32_t res = 0, npc = (pc + (mode == M_IMP ? 1u : (mode >= M_ABS && mode <= M_ABY) || mode == M_IND ? 3u : 2u)) & 0xFFFFu;
@@ -1168,6 +900,8 @@ __device__ inline uint32_t cpu_step(Con& c, const Mem& m, const uint32_t* optab,
     }
     if (d & D_WRITE) bus_write(c, m, ac, ea, res);
     c.pc = npc;
+    for (uint32_t i = logged; i < c.log_n && i < NES_LOG_EVENTS; ++i)
+        m.rec->log[NES_LOG_HDR_WORDS + 2u * i] |= (icyc > 15u ? 15u : icyc) << 4;
     cyc += icyc;
     c.cycles += cyc;
     if (ac.dma) {
@@ -1182,54 +916,6 @@ __device__ inline uint32_t cpu_step(Con& c, const Mem& m, const uint32_t* optab,
         cyc += s;
     }
     return cyc;
-}
-
-// Skip whole 3-cycle jumps of a JMP-to-self idle loop up to the next PPU event; not while an interrupt waits.
-__device__ inline void fast_forward(Con& c, const Mem& m) {
-    if (c.nmi_pending || (c.irq_line && !(c.p & FL_I))) return;
-    const uint32_t to = dots_to_event(c, m);
-    const uint32_t jumps = (to + 8u) / 9u;
-    if (jumps == 0) return;
-    c.cycles += 3u * jumps;
-    if (c.cycles >= c.dmc_event) {
-        (void)dmc_service(m.rec, c.cycles, 0);
-        c.dmc_event = m.rec->dmc_event;
-    }
-    ppu_advance(c, m, 9u * jumps);
-}
-
-// Runs the console until the PPU reaches absolute dot `target` (rl/csrc/nes_machine.cuh:67-103). Returns the fault.
-__device__ inline uint32_t run_until(Con& c, const Mem& m, const uint32_t* optab, uint64_t target,
-                                     uint32_t budget = NES_BUDGET) {
-    uint32_t instructions = 0, fault = 0, pending = 0;
-    uint32_t to_event = dots_to_event(c, m);
-    while (instructions < budget) {
-        if (pending >= to_event) {
-            ppu_advance(c, m, pending);
-            pending = 0;
-            if (abs_dot(c) >= target) break;
-            to_event = dots_to_event(c, m);
-        }
-        const int32_t start_rel =
-            (int32_t)((int64_t)abs_dot(c) + pending - (int64_t)c.log_frame * NES_FRAME_DOTS);
-        uint32_t op, pc0;
-        const uint32_t cyc = cpu_step(c, m, optab, start_rel, &fault, &op, &pc0);
-        if (fault) break;
-        pending += 3u * cyc;
-        ++instructions;
-        ++c.instr;
-        if (!c.s0_valid) to_event = dots_to_event(c, m);
-        if (op == 0x4Cu && c.pc == pc0) {
-            ppu_advance(c, m, pending);
-            pending = 0;
-            if (abs_dot(c) >= target) break;
-            fast_forward(c, m);
-            to_event = dots_to_event(c, m);
-            if (abs_dot(c) >= target) break;
-        }
-    }
-    if (pending) ppu_advance(c, m, pending);
-    return fault;
 }
 
 // Power-on of one console record: cold reset, RAM 0xFF, frame 0's log from the power-on PPU state.
@@ -1257,17 +943,10 @@ __device__ inline void power_on(NesRec* rec, const Cart& cart) {
     const uint32_t vec = rec->prg_off[3] + 0x1FFCu;
     rec->pc = (uint16_t)((cart.prgw[vec] & 0xFFu) | ((cart.prgw[vec + 1] & 0xFFu) << 8));
     rec->cycles = 7;
-    rec->s0_dot = (int32_t)kNoHit;
-    rec->s0_valid = 0;
     rec->dmc_byte_end = 7u + 1u + 7u * 428u;
     rec->dmc_event = kDmcIdle;
-    uint32_t* h = rec->log;
-    for (uint32_t i = 0; i < 4; ++i) {
-        h[3] |= ((rec->chr_off[i] >> 10) & 0xFFu) << (8 * i);
-        h[4] |= ((rec->chr_off[4 + i] >> 10) & 0xFFu) << (8 * i);
-    }
-    h[5] = c.nt_map;
-    rec->log_frame = 0;
+    c.ctrl = c.mask = c.fx = c.v = c.t = 0;
+    log_header(c, m, 0);   // frame 0 is logged from the power-on state (patch:1160-1166)
 }
 
 // ------------------------------------------------------------------------------------ record <-> lane
@@ -1278,7 +957,7 @@ __device__ inline void con_load(Con& c, const NesRec* r) {
     c.frame_dot = r->frame_dot; c.frame = r->frame;
     c.v = r->v; c.t = r->t; c.ctrl = r->ctrl; c.mask = r->mask; c.status = r->status; c.oam_addr = r->oam_addr;
     c.fx = r->fx; c.w = r->w; c.read_buf = r->read_buf; c.open_bus = r->open_bus;
-    c.s0_dot = r->s0_dot; c.log_frame = r->log_frame; c.log_n = r->log_n; c.s0_valid = r->s0_valid;
+    c.s0_sched = r->s0_sched; c.log_frame = r->log_frame; c.log_n = r->log_n; c.log_flags = r->log_flags;
     c.dmc_event = r->dmc_event;
     c.prg0 = r->prg_off[0]; c.prg1 = r->prg_off[1]; c.prg2 = r->prg_off[2]; c.prg3 = r->prg_off[3];
     c.nt_map = r->nt_map[0] | (r->nt_map[1] << 2) | (r->nt_map[2] << 4) | ((uint32_t)r->nt_map[3] << 6);
@@ -1292,7 +971,8 @@ __device__ inline void con_store(const Con& c, NesRec* r) {
     r->v = (uint16_t)c.v; r->t = (uint16_t)c.t; r->ctrl = (uint8_t)c.ctrl; r->mask = (uint8_t)c.mask;
     r->status = (uint8_t)c.status; r->oam_addr = (uint8_t)c.oam_addr; r->fx = (uint8_t)c.fx; r->w = (uint8_t)c.w;
     r->read_buf = (uint8_t)c.read_buf; r->open_bus = (uint8_t)c.open_bus;
-    r->s0_dot = c.s0_dot; r->log_frame = c.log_frame; r->log_n = (uint16_t)c.log_n; r->s0_valid = (uint8_t)c.s0_valid;
+    r->s0_sched = c.s0_sched; r->log_frame = c.log_frame; r->log_n = (uint16_t)c.log_n;
+    r->log_flags = (uint8_t)c.log_flags;
     r->dmc_event = c.dmc_event;
     // prg_off and nt_map are written through to the record whenever they change (map_set_*)
 }

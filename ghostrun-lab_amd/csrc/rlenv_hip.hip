@@ -2,19 +2,20 @@
 //
 // One decision of one game is this launch sequence on the caller's stream (the reference's phase order,
 // rl/csrc/rlenv_core.cuh:389-414 and rl/csrc/rlenv.cu:145-170):
-//   4 x (k_emu: one emulated frame of every console, k_render: its picture into obs slot f)
+//   4 x (k_emu_w: one emulated frame of every console, k_render: its picture into obs slot f)
 //   k_finish: reward10 update, outputs, dropout advance; finished episodes reset their RL state and join the
 //             restart list (wave ballot + one atomic per wave)
 //   k_reset_copy: boot snapshot (or idle template) -> console record, one workgroup per listed console
-//   4 x (k_emu, k_render) over the restart list only (neutral frames of the new episode)
+//   4 x (k_emu_w, k_render) over the restart list only (neutral frames of the new episode)
 //   k_reset_finish: first tracker update of new episodes; masks and dropout timeline of every env
 //
 // k_emu_w (the default) gives each console a whole wavefront: the console index comes from blockIdx, so its state
 // is wave-uniform and the 6502 runs on the scalar unit (uniform branches, SGPRs) with a per-opcode fast path
 // (wave_dev.h); the console's RAM, nametables, OAM, palette and cold state live in LDS for the launch. 8192 consoles
-// are 8192 waves, 8 per SIMD. k_emu (RLENV_EMU=lane) runs one console per lane, `cpw` consoles per wavefront.
-// k_render draws one console-frame per wavefront: the line replay is wave-uniform, each lane composes 4 pixels,
-// sprites are selected with one ballot per line, and each output row is one coalesced 240-byte store.
+// are 8192 waves, 8 per SIMD.
+// k_render draws one console-frame per wavefront: the log is replayed through FCEUmm's line renderer (replay_dev.h),
+// its scalar walk wave-uniform, each run of tile slots fetched and shifted out by the lanes into a line buffer in LDS,
+// sprites selected with one ballot per line, and each output row is one coalesced 240-byte store.
 #include <hip/hip_runtime.h>
 
 #include <cstdio>
@@ -106,7 +107,7 @@ struct EmuArgs {
     Outs o;
     Settings s;
     const uint32_t* optab;
-    int mode, f, cpw, use_list, e0, e1;
+    int mode, f, use_list, e0, e1;
     uint32_t boot_pad;
     uint64_t boot_target;
     uint32_t* boot_fault;
@@ -145,69 +146,6 @@ __device__ __forceinline__ uint32_t decision_pad(const Args& a, int ge, int f) {
     return pad;
 }
 
-__global__ __launch_bounds__(64) void k_emu(EmuArgs a) {
-    extern __shared__ __align__(16) uint8_t smem[];
-    const int count = a.mode == EMU_BOOT ? 1 : slot_count(a.g, a.use_list, a.e0, a.e1);
-    const int first = (int)blockIdx.x * a.cpw;
-    if (first >= count) return;
-    const int lane = (int)threadIdx.x;
-    uint32_t* optab = reinterpret_cast<uint32_t*>(smem);
-    uint8_t* rams = smem + 1024;
-    for (int i = lane; i < 256; i += 64) optab[i] = a.optab[i];
-    const int nslot = min(a.cpw, count - first);
-    for (int j = 0; j < nslot; ++j) {
-        const int e = a.mode == EMU_BOOT ? a.e0 : slot_env(a.g, a.use_list, a.e0, first + j);
-        const uint32_t* src = reinterpret_cast<const uint32_t*>(a.g.recs[e].ram);
-        uint32_t* dst = reinterpret_cast<uint32_t*>(rams + j * kRamStride);
-        for (int w = lane; w < 512; w += 64) dst[w] = src[w];
-    }
-    __syncthreads();
-    if (lane < nslot) {
-        const int e = a.mode == EMU_BOOT ? a.e0 : slot_env(a.g, a.use_list, a.e0, first + lane);
-        NesRec* rec = &a.g.recs[e];
-        const Mem m = mem_of(rec, rams + lane * kRamStride, a.g.cart);
-        const int ge = a.g.offset + e;
-        uint32_t pad = 0, fault = 0;
-        uint64_t target;
-        bool run = true;
-        if (a.mode == EMU_BOOT) {
-            pad = a.boot_pad;
-            target = a.boot_target;
-        } else {
-            if (a.mode == EMU_RESTART && a.e.resetting[ge] == 0) run = false;
-            if (a.mode == EMU_DECISION) pad = decision_pad(a, ge, a.f);
-            target = a.e.target[ge];
-            fault = a.e.fault[ge];
-        }
-        if (run) {
-            Con c;
-            con_load(c, rec);
-            c.pad = pad;
-            if (fault == 0) {
-                const uint32_t f = run_until(c, m, optab, target, a.budget);
-                if (f != 0) {
-                    if (a.mode == EMU_BOOT) atomicOr(a.boot_fault, 1u);
-                    else a.e.fault[ge] = f;
-                } else if (a.g.cart.board == NES_BOARD_MMC2 && c.frame == c.log_frame) {   // the vblank stop
-                    mmc2_resolve(rec, m.nt, m.oam, c.log_n, a.g.cart.chr_pages1);
-                }
-            }
-            con_store(c, rec);
-            if (a.mode != EMU_BOOT) {
-                a.e.target[ge] = target + NES_FRAME_DOTS;
-                a.e.ep_frame[ge] += 1u;
-            }
-        }
-    }
-    __syncthreads();
-    for (int j = 0; j < nslot; ++j) {
-        const int e = a.mode == EMU_BOOT ? a.e0 : slot_env(a.g, a.use_list, a.e0, first + j);
-        uint32_t* dst = reinterpret_cast<uint32_t*>(a.g.recs[e].ram);
-        const uint32_t* src = reinterpret_cast<const uint32_t*>(rams + j * kRamStride);
-        for (int w = lane; w < 512; w += 64) dst[w] = src[w];
-    }
-}
-
 // The opcode descriptors in constant memory: the wave-uniform generic step reads them through the scalar cache.
 __constant__ Optab c_optab = kOptab;
 
@@ -225,6 +163,7 @@ struct WaveLds {
     uint8_t oam[NES_OAM_BYTES];
     uint8_t pal[NES_PAL_BYTES];
     Con cs;
+    uint32_t scratch[34];   // the sprite-0 check's MMC2 pages
 };
 
 // One console per wavefront (blockDim 64): the console index comes from blockIdx only, so every emulator value is
@@ -269,7 +208,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(8, 8))) void
         }
         Con& cs = L.cs;
         con_load(cs, rec);
-        const Mem m{rec, L.ram, L.nt, L.oam, L.pal, a.g.cart};
+        const Mem m{rec, L.ram, L.nt, L.oam, L.pal, a.g.cart, L.scratch};
         for (int i = 0; i < frames; ++i) {   // a faulted console stays put; its target and frame still advance
             cs.pad = pad;
             if (fault == 0) {
@@ -278,9 +217,6 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(8, 8))) void
                     if (a.mode == EMU_BOOT) atomicOr(a.boot_fault, 1u);
                     else a.e.fault[ge] = f;
                     fault = f;
-                } else if constexpr (B != NES_BOARD_NROM) {   // MMC2 at the vblank stop (no log: first frame)
-                    if (a.g.cart.board == NES_BOARD_MMC2 && cs.frame == cs.log_frame)
-                        mmc2_resolve(rec, L.nt, L.oam, cs.log_n, a.g.cart.chr_pages1);
                 }
             }
             target += NES_FRAME_DOTS;
@@ -312,146 +248,215 @@ struct RenderArgs {
     int f, use_list, restart_pass, e0, e1;
 };
 
-// Bit i of byte b at bit 4i (the 8 bits of a pattern byte spread to the low bits of 8 nibbles).
-__device__ __forceinline__ uint32_t nibbles8(uint32_t b) {
-    b = (b | (b << 12)) & 0x000F000Fu;
-    b = (b | (b << 6)) & 0x03030303u;
-    return (b | (b << 3)) & 0x11111111u;
-}
+// The renderer's side of the line replay (replay_dev.h): the walker runs wave-uniform on every lane and hands each run
+// of tile slots here, where the 64 lanes work on it in LDS:
+//   - fetch: lane j fetches slot j's tile (nametable tile and attribute, both pattern bytes) into F[j + 2];
+//   - output: lane k >= 2 shifts out slot k's 8 pixels - the two fetches before it, fine x, the palette of the moment -
+//     into the line buffer at the run's output position (F[0], F[1] carry the line's first fetches' predecessors);
+//   - the run's hidden left column and background-off range, then the sprite-0 check over 8 lanes.
+// Sprite lines are fetched with one ballot over the 64 OAM entries (lane = sprite) into one of two buffers; the one
+// RefreshSprites latched is the one composed.
+struct RenderLds {
+    uint8_t nt[NES_NT_BYTES];
+    uint8_t oam[NES_OAM_BYTES];
+    uint32_t ev[2 * NES_LOG_EVENTS];
+    uint32_t px[64];          // the line: palette value, 0x40 | backdrop where the background is transparent
+    uint32_t f[36];           // fetches: lo | hi << 8 | attribute << 16; 0-1 carried, 2 + j slot j
+    uint32_t spr[2][8];       // sprite lines: lo | hi << 8 | attr << 16 | x << 24
+    uint32_t pages[34 + 8];   // MMC2: the pages of each slot's fetch, then of each sprite's
+    uint8_t pal[32];
+    uint8_t spal[16];
+};
 
-// The picture of the frame a console has logged, drawn by one wavefront: the frame log is replayed line by line
-// (wave-uniform state), each lane composes 4 pixels of the 256-pixel line, the sprites of a line are picked with
-// one ballot over the 64 OAM entries, and lines 8..231, columns 8..247 go out as one 240-byte row store each
-// (rl/csrc/nes_machine.cuh:133-155). nt/oam: the console's nametables and OAM as of the frame's vblank (LDS);
-// pal: 32 bytes of LDS for the replayed palette; ev_s: the log's events, copied to LDS.
-template <bool kMmc2>
-__device__ __forceinline__ void render_wave(const NesRec* rec, uint32_t log_n, const uint8_t* nt_s, const uint8_t* oam_s,
-                                            uint8_t* pal_s, const uint32_t* ev_s, uint32_t* spr_s, uint32_t* slot_s,
-                                            uint32_t* tile_s, uint32_t* mk_s, const Cart& cart, uint8_t* obs,
-                                            uint8_t* emph, int lane) {
-    Replay s;   // wave-uniform: every lane replays the same log (and stores the same palette bytes)
-    rp_begin(s, rec->log, log_n, pal_s, ev_s, kMmc2 ? cart.chr_pages1 : 0u);
-    constexpr bool mmc2 = kMmc2;
-    __syncthreads();
-    const Mem m = mem_of(const_cast<NesRec*>(rec), nullptr, cart);
-    const uint32_t my_sy = oam_s[4 * lane];
-    for (int l = 0; l < 232; ++l) {
-        const uint32_t line_lo = s.chr_lo, line_hi = s.chr_hi;
-        if constexpr (mmc2) {
-            // the line's fetches in order, each through the pages of the moment: mk_s[k] (sprite rank k) and
-            // mk_s[8 + t] (tile slot t) hold the 4 slot pages of the half the fetch's address is in
-            rp_mmc2_line(s, nt_s, oam_s, l, false, [&](uint32_t kind, uint32_t i, uint32_t lo, uint32_t hi, uint32_t pa) {
-                if (lane == 0) mk_s[kind ? 8u + i : i] = (pa & 0x1000u) ? hi : lo;
-            });
-            __syncthreads();
-        }
-        if (l >= 8) {
-            const uint32_t mask = s.mask, ctrl = s.ctrl;
-            const bool bg_on = (mask & 0x08u) != 0, sp_on = (mask & 0x10u) != 0;
-            const int h = (ctrl & 0x20u) ? 16 : 8;
-            const int row_me = l - (int)my_sy - 1;
-            const uint64_t sel = __ballot(sp_on && row_me >= 0 && row_me < h);
-            // background: lane t < 34 fetches tile slot t of the line (its nametable tile, attribute and two pattern
-            // bytes) into tile_s[t] as 8 nibbles palette << 2 | value, leftmost pixel in the top nibble; then each
-            // lane takes its pixels x0..x0+3, which lie in slots A = (x0 + fx) / 8 and A + 1, out of the two words
-            uint32_t bgv[4] = {0, 0, 0, 0}, bga[4] = {0, 0, 0, 0};
-            const uint32_t x0 = 4u * (uint32_t)lane;
-            if (bg_on) {
-                const uint32_t cy = (s.v >> 5) & 31u, fy = (s.v >> 12) & 7u, ntv = (s.v >> 11) & 1u;
-                if (lane < 34) {
-                    const uint32_t c = (s.v & 31u) + (uint32_t)lane;   // < 64; slot 33 is read, never used
-                    const uint32_t wrap = c >= 32u ? 1u : 0u;
-                    const uint32_t cx = c - 32u * wrap, nth = ((s.v >> 10) & 1u) ^ wrap;
-                    const uint32_t base = 0x2000u | ((nth | (ntv << 1)) << 10);
-                    const uint32_t tile = nt_s[nt_index(s.nt_map, base | (cy << 5) | (cx & 31u))];
-                    const uint32_t at = nt_s[nt_index(s.nt_map, base | 0x3C0u | ((cy >> 2) << 3) | ((cx & 31u) >> 2))];
-                    const uint32_t ps = (at >> (((cy & 2u) << 1) | (cx & 2u))) & 3u;
-                    const uint32_t pa = ((ctrl & 0x10u) << 8) + tile * 16u + fy;
-                    const uint32_t plo = mmc2 ? mk_s[8 + lane] : line_lo;   // the fetch reads only its own half
-                    const uint32_t phi = mmc2 ? mk_s[8 + lane] : line_hi;
-                    const uint32_t lo = chr_byte_pk(m, plo, phi, pa);
-                    const uint32_t hi = chr_byte_pk(m, plo, phi, pa + 8u);
-                    tile_s[lane] = nibbles8(lo) | (nibbles8(hi) << 1) | (ps * 0x44444444u);
-                }
-                __syncthreads();
-                const uint32_t pos0 = x0 + s.fx, slot_a = pos0 >> 3;
-                const uint64_t w = (((uint64_t)tile_s[slot_a] << 32) | tile_s[slot_a + 1u]) << (4u * (pos0 & 7u));
-                const uint32_t top = (uint32_t)(w >> 32);   // the lane's 4 pixels in the top 16 bits
-                for (int q = 0; q < 4; ++q) {
-                    const uint32_t nib = (top >> (28u - 4u * (uint32_t)q)) & 15u;
-                    const bool clip = x0 + (uint32_t)q < 8u && !(mask & 0x02u);
-                    bgv[q] = clip ? 0u : nib & 3u;
-                    bga[q] = nib >> 2;
-                }
-            }
-            // sprites: the first 8 in OAM order that cover this line; per pixel the first opaque one wins. One pass
-            // for all of them: lane j draws pixel j & 7 of the line's sprite j >> 3 into the line buffer spr_s with
-            // an LDS max over (7 - sprite rank) << 5 | behind << 4 | palette << 2 | value, so the lowest-ranked
-            // opaque sprite wins each pixel; slot_s maps rank -> OAM index.
-            uint32_t spv[4] = {0, 0, 0, 0}, spa[4] = {0, 0, 0, 0}, spb[4] = {0, 0, 0, 0};
-            if (sel != 0) {
-                const uint32_t below = __builtin_amdgcn_mbcnt_hi((uint32_t)(sel >> 32),
-                                                                 __builtin_amdgcn_mbcnt_lo((uint32_t)sel, 0u));
-                if (((sel >> lane) & 1u) && below < 8u) slot_s[below] = (uint32_t)lane;
-                const uint32_t count = min((uint32_t)__builtin_popcountll(sel), 8u);
-                __syncthreads();
-                const uint32_t k = (uint32_t)lane >> 3, px = (uint32_t)lane & 7u;
-                if (k < count) {
-                    const uint32_t i = slot_s[k];
-                    const uint32_t e = reinterpret_cast<const uint32_t*>(oam_s)[i];
-                    const uint32_t sy = e & 0xFFu, tile = (e >> 8) & 0xFFu, attr = (e >> 16) & 0xFFu, sx = e >> 24;
-                    const uint32_t pa = sprite_row_addr(ctrl, tile, attr, (uint32_t)(l - (int)sy - 1));
-                    const uint32_t kp = mmc2 ? mk_s[k] : 0u;   // the fetch reads only its own half
-                    const uint32_t klo = mmc2 ? kp : line_lo, khi = mmc2 ? kp : line_hi;
-                    const uint32_t plo = chr_byte_pk(m, klo, khi, pa);
-                    const uint32_t phi = chr_byte_pk(m, klo, khi, pa + 8u);
-                    const uint32_t b = (attr & 0x40u) ? px : 7u - px;
-                    const uint32_t v = ((plo >> b) & 1u) | (((phi >> b) & 1u) << 1);
-                    const uint32_t x = sx + px;
-                    if (v != 0u && x < 256u && !(x < 8u && !(mask & 0x04u)))
-                        atomicMax(&spr_s[x], ((7u - k) << 5) | (((attr >> 5) & 1u) << 4) | ((attr & 3u) << 2) | v);
-                }
-                __syncthreads();
-                const uint4 got = reinterpret_cast<uint4*>(spr_s)[lane];
-                reinterpret_cast<uint4*>(spr_s)[lane] = make_uint4(0u, 0u, 0u, 0u);
-                const uint32_t g[4] = {got.x, got.y, got.z, got.w};
-                for (int q = 0; q < 4; ++q) {
-                    spv[q] = g[q] & 3u;
-                    spa[q] = (g[q] >> 2) & 3u;
-                    spb[q] = (g[q] >> 4) & 1u;
-                }
-            }
-            uint32_t word = 0;
-            for (int q = 0; q < 4; ++q) {   // palette entry: background over a sprite behind it, else the sprite
-                const uint32_t sp_idx = spv[q] ? 16u + spa[q] * 4u + spv[q] : 0u;
-                const uint32_t idx = (bgv[q] && (!spv[q] || spb[q])) ? bga[q] * 4u + bgv[q] : sp_idx;
-                uint32_t colour = pal_s[idx] & 0x3Fu;
-                if (mask & 1u) colour &= 0x30u;
-                word |= colour << (8 * q);
-            }
-            const int y = l - 8;
-            if (lane >= 2 && lane < 62) reinterpret_cast<uint32_t*>(obs + y * RLE_OBS_W)[lane - 2] = word;
-            if (lane == 0) emph[y] = (uint8_t)((mask >> 5) & 7u);
-        }
-        __syncthreads();   // palette writes of the replay below vs. reads above
-        rp_line_end(s, l, pal_s);
+struct RenderSink {
+    RenderLds* L;
+    const uint8_t *chr_rom, *chr_ram;
+    int lane;
+    bool mmc2;
+    uint32_t ha, hb;          // F indices of the last two fetches
+    uint32_t fetched, drawn, drawn_n;
+
+    __device__ uint32_t nt(uint32_t i) { return uni(L->nt[i]); }
+    __device__ uint32_t oam(uint32_t i) { return uni(L->oam[i]); }
+    __device__ uint8_t* px8() { return reinterpret_cast<uint8_t*>(L->px); }
+    __device__ uint32_t back4() { return (((uint32_t)L->pal[0] & 0x3Fu) | 0x40u) * 0x01010101u; }
+    __device__ void palette(uint32_t i, uint32_t v) {
+        if (lane == 0) L->pal[i] = (uint8_t)v;
         __syncthreads();
     }
-}
+    __device__ void slot_pages(int32_t j, uint32_t pk) {
+        if (lane == 0) L->pages[j] = pk;
+    }
+    __device__ void sprite_pages(uint32_t n, uint32_t pk) {
+        if (lane == 0) L->pages[34 + n] = pk;
+    }
+    // A new line: the last two fetches move to F[0], F[1]; nothing drawn yet (0xFF reads as transparent).
+    __device__ void line_begin(const Rs&, bool) {
+        const uint32_t carry = lane < 2 ? L->f[lane ? hb : ha] : 0u;
+        __syncthreads();
+        if (lane < 2) L->f[lane] = carry;
+        L->px[lane] = 0xFFFFFFFFu;
+        ha = 0;
+        hb = 1;
+        __syncthreads();
+    }
+    // Pixels [o, o + n) the backdrop (o and n multiples of 8).
+    __device__ void fill(int32_t o, int32_t n) {
+        const int32_t x = 4 * lane;
+        if (x >= o && x < o + n) L->px[lane] = back4();
+    }
+    __device__ void off_run(int32_t out, int32_t n, bool) {
+        fill(out, n);
+        __syncthreads();
+    }
+    __device__ void on_run(const Rs& s, int32_t first, int32_t last, int32_t out, bool pixels) {
+        __syncthreads();   // the walker's page and palette writes
+        if (lane >= first && lane < last) {
+            const uint32_t v = v_steps(s.v, (uint32_t)(lane - first));
+            const uint32_t ntb = 0x2000u | (v & 0x0C00u), col = v & 31u;
+            const uint32_t tile = L->nt[nt_slot(s.nt_map, ntb | (v & 0x3FFu))];
+            const uint32_t at = L->nt[nt_slot(s.nt_map, ntb | 0x3C0u | (col >> 2) | ((v & 0x380u) >> 4))];
+            const uint32_t sel = (at >> ((col & 2u) | ((v & 0x40u) >> 4))) & 3u;
+            const uint32_t pa = tile * 16u + ((s.ctrl & 0x10u) << 8) + ((v >> 12) & 7u);
+            const uint32_t pk = mmc2 ? L->pages[lane] : 0u;
+            const uint32_t lo = mmc2 ? pk : s.chr_lo, hi = mmc2 ? pk : s.chr_hi;
+            L->f[lane + 2] = chr_pk(chr_rom, chr_ram, lo, hi, pa) | (chr_pk(chr_rom, chr_ram, lo, hi, pa + 8u) << 8) |
+                             (sel << 16);
+        }
+        __syncthreads();
+        const int32_t from = first > 2 ? first : 2;
+        if (pixels) {
+            const int32_t o = out + 8 * (lane - from);
+            if (lane >= from && lane < last && o < 256) {
+                const int32_t j = lane - first;
+                const uint32_t p1 = L->f[j >= 1 ? (uint32_t)lane + 1u : hb];
+                const uint32_t p2 = L->f[j >= 2 ? (uint32_t)lane : (j == 1 ? hb : ha)];
+                const uint32_t lo16 = ((p2 & 0xFFu) << 8) | (p1 & 0xFFu), hi16 = (p2 & 0xFF00u) | ((p1 >> 8) & 0xFFu);
+                const uint32_t c2 = (p2 >> 16) & 3u, c1 = (p1 >> 16) & 3u;
+                const uint32_t back = (L->pal[0] & 0x3Fu) | 0x40u;
+                uint32_t w[2] = {0u, 0u};
+                for (uint32_t q = 0; q < 8u; ++q) {
+                    const uint32_t bit = 15u - s.fx - q;
+                    const uint32_t val = ((lo16 >> bit) & 1u) | (((hi16 >> bit) & 1u) << 1);
+                    const uint32_t pal_sel = q + s.fx < 8u ? c2 : c1;
+                    const uint32_t c = val ? (L->pal[pal_sel * 4u + val] & 0x3Fu) : back;
+                    w[q >> 2] |= c << (8u * (q & 3u));
+                }
+                L->px[o >> 2] = w[0];
+                L->px[(o >> 2) + 1] = w[1];
+            }
+            const bool clip = first <= 2 && last > 2 && !(s.mask & 0x02u), bg_off = !(s.mask & 0x08u);
+            if (clip || bg_off) {
+                __syncthreads();
+                if (clip) fill(0, 8);
+                if (bg_off) {
+                    int32_t f = first - 2, n = last - first;
+                    if (f < 0) {
+                        n += f;
+                        f = 0;
+                    }
+                    fill(8 * f, 8 * n);
+                }
+            }
+        }
+        if (last - first >= 2) {
+            ha = (uint32_t)last;
+            hb = (uint32_t)last + 1u;
+        } else {
+            ha = hb;
+            hb = (uint32_t)first + 2u;
+        }
+        __syncthreads();
+    }
+    __device__ int32_t find_hit(int32_t x, uint32_t bits, int32_t end) {
+        const int32_t xi = x + lane;
+        const bool hit = lane < 8 && xi < end && ((bits >> (7 - lane)) & 1u) && !(px8()[xi] & 0x40u);
+        const uint64_t b = __ballot(hit);
+        return b ? x + (int32_t)__builtin_ctzll(b) : -1;
+    }
+    // FetchSpriteData for line l + 1: the first eight OAM entries on it, each row through the pages of the moment
+    // (MMC2: of its own fetch), into the buffer not latched.
+    __device__ void fetch_sprites(Rs& s, int32_t l) {
+        const uint32_t ctrl = s.ctrl, h = (ctrl & 0x20u) ? 16u : 8u;
+        const uint32_t e = reinterpret_cast<const uint32_t*>(L->oam)[lane];
+        const uint32_t row = (uint32_t)(l - (int32_t)(e & 0xFFu));
+        const uint64_t sel = __ballot(row < h);
+        const uint32_t rank = __builtin_amdgcn_mbcnt_hi((uint32_t)(sel >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)sel, 0u));
+        const uint32_t target = fetched == drawn ? drawn ^ 1u : fetched;
+        if (row < h && rank < 8u) {
+            const uint32_t tile = (e >> 8) & 0xFFu, attr = (e >> 16) & 0xFFu;
+            const uint32_t table8 = (ctrl & 0x08u) && !(ctrl & 0x20u) ? 0x1000u : 0u;
+            uint32_t pa = h == 16u ? ((tile & 1u) << 12) + ((tile & 0xFEu) << 4) : (tile << 4) + table8;
+            if (attr & 0x80u) pa += 7u - row + ((ctrl & 0x20u) >> 1) - (row & 8u);
+            else pa += row + (row & 8u);
+            pa &= 0x1FFFu;
+            const uint32_t pk = mmc2 ? L->pages[34 + rank] : 0u;
+            const uint32_t lo = mmc2 ? pk : s.chr_lo, hi = mmc2 ? pk : s.chr_hi;
+            L->spr[target][rank] = chr_pk(chr_rom, chr_ram, lo, hi, pa) |
+                                   (chr_pk(chr_rom, chr_ram, lo, hi, pa + 8u) << 8) | (e & 0xFFFF0000u);
+        }
+        fetched = target;
+        const uint32_t n = (uint32_t)__builtin_popcountll(sel);
+        s.f_n = n < 8u ? n : 8u;
+        s.f_blurp = (uint32_t)(sel & 1u);
+        __syncthreads();
+        if (s.f_n) {
+            const uint32_t e0 = uni(L->spr[target][0]);
+            s.f_bits = (e0 & 0xFFu) | ((e0 >> 8) & 0xFFu);
+            s.f_attr = (e0 >> 16) & 0xFFu;
+            s.f_x = e0 >> 24;
+        }
+    }
+    // RefreshSprites: the fetched line is the one drawn next, with the sprite palette of the moment.
+    __device__ void latch_sprites(const Rs& s) {
+        drawn = fetched;
+        drawn_n = s.f_n;
+        if (lane < 16) L->spal[lane] = (uint8_t)(L->pal[16 + lane] & 0x3Fu);
+        __syncthreads();
+    }
+    // CopySprites (with sprites on at the line's end and a latched line waiting), greyscale while rendering, and the
+    // observation row (rl/csrc/nes_machine.cuh:133-155: lines 8..231, x 8..247); returns the emphasis bits
+    // (patch:1637-1661).
+    __device__ void compose(Rs& s, int32_t l, uint8_t* obs, uint8_t* emph) {
+        const bool sprites = (s.mask & 0x10u) && s.spork;
+        if (sprites) s.spork = 0;
+        const uint32_t keep = (s.mask & 0x01u) && rs_rendering(s) ? 0x30u : 0x3Fu;
+        if (l < 8) return;
+        uint32_t w = L->px[lane];
+        if (sprites) {
+            const uint32_t xstart = (s.mask & 0x04u) ? 0u : 8u;
+            uint32_t out = 0;
+            for (uint32_t q = 0; q < 4u; ++q) {
+                const uint32_t x = 4u * (uint32_t)lane + q;
+                uint32_t c = (w >> (8u * q)) & 0xFFu;
+                if (x >= xstart) {
+                    for (uint32_t n = 0; n < drawn_n; ++n) {
+                        const uint32_t e = L->spr[drawn][n];
+                        const uint32_t col = x - (e >> 24);
+                        if (col >= 8u) continue;
+                        const uint32_t attr = (e >> 16) & 0xFFu;
+                        const uint32_t b = (attr & 0x40u) ? col : 7u - col;
+                        const uint32_t val = ((e >> b) & 1u) | (((e >> (8u + b)) & 1u) << 1);
+                        if (val == 0) continue;
+                        if (!(attr & 0x20u) || (c & 0x40u)) c = L->spal[(attr & 3u) * 4u + val];
+                        break;
+                    }
+                }
+                out |= c << (8u * q);
+            }
+            w = out;
+        }
+        w &= keep * 0x01010101u;
+        const int32_t y = l - 8;
+        if (lane >= 2 && lane < 62) reinterpret_cast<uint32_t*>(obs + y * RLE_OBS_W)[lane - 2] = w;
+        if (lane == 0) emph[y] = (uint8_t)((s.mask >> 5) & 7u);
+    }
+};
 
-// One console-frame per wavefront (blockDim 64).
-template <bool kMmc2>
+// One console-frame per wavefront (blockDim 64): the picture of the frame the console has logged, drawn from its
+// nametables and OAM as of the frame's vblank stop.
 __global__ __launch_bounds__(64) void k_render(RenderArgs a) {
-    __shared__ __align__(16) uint8_t nt_s[2048];
-    __shared__ __align__(16) uint8_t oam_s[256];
-    __shared__ __align__(16) uint8_t pal_s[32];
-    __shared__ __align__(16) uint32_t ev_s[2 * NES_LOG_EVENTS];
-    __shared__ __align__(16) uint32_t spr_s[256];   // the line's sprite pixels (0 = none)
-    __shared__ uint32_t slot_s[8];
-    // MMC2: the pages of the line's sprite fetches (0-7) and tile fetches (8-41); the line's background tile slots
-    // (tile_s) take the place of the tile fetches' pages, each lane reading its slot's pages before it writes it
-    __shared__ uint32_t mk_s[8 + 34];
-    uint32_t* tile_s = mk_s + 8;
+    __shared__ __align__(16) RenderLds L;
     const int count = slot_count(a.g, a.use_list, a.e0, a.e1);
     const int k = (int)blockIdx.x;
     if (k >= count) return;
@@ -461,15 +466,26 @@ __global__ __launch_bounds__(64) void k_render(RenderArgs a) {
     if (a.s.no_render) return;
     const int lane = (int)threadIdx.x;
     const NesRec* rec = &a.g.recs[e];
-    for (int w = lane; w < 512; w += 64) reinterpret_cast<uint32_t*>(nt_s)[w] = reinterpret_cast<const uint32_t*>(rec->nt)[w];
-    reinterpret_cast<uint32_t*>(oam_s)[lane] = reinterpret_cast<const uint32_t*>(rec->oam)[lane];
+    wave_copy16(L.nt, rec->nt, NES_NT_BYTES, lane);
+    wave_copy16(L.oam, rec->oam, NES_OAM_BYTES, lane);
     const uint32_t log_n = rec->log_n, ev_words = 2u * (log_n < NES_LOG_EVENTS ? log_n : NES_LOG_EVENTS);
-    for (uint32_t w = (uint32_t)lane; w < ev_words; w += 64u) ev_s[w] = rec->log[NES_LOG_HDR_WORDS + w];
-    reinterpret_cast<uint4*>(spr_s)[lane] = make_uint4(0u, 0u, 0u, 0u);
+    for (uint32_t w = (uint32_t)lane; w < ev_words; w += 64u) L.ev[w] = rec->log[NES_LOG_HDR_WORDS + w];
+    if (lane < 8) reinterpret_cast<uint32_t*>(L.pal)[lane] = rec->log[6 + lane];
+    if (lane < 2) L.f[lane] = 0;
+    if (lane < 16) L.spr[lane >> 3][lane & 7] = 0;
     __syncthreads();
+    const bool mmc2 = a.g.cart.board == NES_BOARD_MMC2;
+    Rs s;
+    rs_load(s, rec->log, L.ev, log_n, mmc2 ? a.g.cart.chr_pages1 : 0u);
+    RenderSink sink{&L, a.g.cart.chr, rec->chr_ram, lane, mmc2, 0u, 1u, 0u, 0u, 0u};
+    rs_begin_frame(s, sink);
     uint8_t* obs = a.o.obs + ((size_t)ge * RLE_FRAMES + a.f) * RLE_OBS_PIXELS;
     uint8_t* emph = a.o.emph + ((size_t)ge * RLE_FRAMES + a.f) * RLE_OBS_H;
-    render_wave<kMmc2>(rec, log_n, nt_s, oam_s, pal_s, ev_s, spr_s, slot_s, tile_s, mk_s, a.g.cart, obs, emph, lane);
+    for (int32_t l = 0; l < 232; ++l) {
+        rs_line(s, sink, l, true);
+        sink.compose(s, l, obs, emph);
+        rs_end_of_line(s, sink, l, true);
+    }
 }
 
 // ----------------------------------------------------------------------------------------- finish
@@ -953,8 +969,6 @@ struct Env {
     Outs o{};
     Settings s{};
     uint32_t* optab = nullptr;
-    int cpw = 16;
-    bool emu_wave = true;    // k_emu_w (one console per wavefront); RLENV_EMU=lane selects k_emu
     uint32_t budget = NES_BUDGET;
     int lv_cap = 0;          // level starts / places per game (0 = off)
     mutable KernelClock clock;
@@ -1022,22 +1036,16 @@ FinishArgs finish_args(const Env& env, const GameK& g, int e0, int e1, const Out
 
 void launch_emu(const Env& env, const GameK& g, const Outs& o, int mode, int f, bool use_list, int e0, int e1,
                 hipStream_t st) {
-    EmuArgs a{g, env.e, o, env.s, env.optab, mode, f, env.cpw, use_list ? 1 : 0, e0, e1, 0, 0, nullptr, env.budget};
-    const int n = use_list ? g.n : e1 - e0;
-    const bool wave = env.emu_wave || mode == EMU_IDLE;   // the idle-frame pass exists in the wave kernel only
-    const int blocks = wave ? n : (n + env.cpw - 1) / env.cpw;
-    const size_t lds = 1024u + (size_t)env.cpw * kRamStride;
+    EmuArgs a{g, env.e, o, env.s, env.optab, mode, f, use_list ? 1 : 0, e0, e1, 0, 0, nullptr, env.budget};
+    const int blocks = use_list ? g.n : e1 - e0;
     const int cls = mode == EMU_DECISION ? KC_EMU : mode == EMU_IDLE ? KC_EMU_IDLE : KC_EMU_RESTART;
     if (blocks > 0)
         env.clock.run(cls, st, [&] {
-            if (wave) {
-                // the fast path knows two kinds of board: fixed 32 KB PRG (NROM, CNROM) and banked PRG (the rest)
-                if (g.cart.board == NES_BOARD_NROM || g.cart.board == NES_BOARD_CNROM)
-                    hipLaunchKernelGGL(k_emu_w<NES_BOARD_NROM>, dim3(blocks), dim3(64), 0, st, a);
-                else
-                    hipLaunchKernelGGL(k_emu_w<NES_BOARD_MMC3>, dim3(blocks), dim3(64), 0, st, a);
-            }
-            else hipLaunchKernelGGL(k_emu, dim3(blocks), dim3(64), lds, st, a);
+            // the fast path knows two kinds of board: fixed 32 KB PRG (NROM, CNROM) and banked PRG (the rest)
+            if (g.cart.board == NES_BOARD_NROM || g.cart.board == NES_BOARD_CNROM)
+                hipLaunchKernelGGL(k_emu_w<NES_BOARD_NROM>, dim3(blocks), dim3(64), 0, st, a);
+            else
+                hipLaunchKernelGGL(k_emu_w<NES_BOARD_MMC3>, dim3(blocks), dim3(64), 0, st, a);
         });
     trace(mode == EMU_DECISION ? "emu" : mode == EMU_IDLE ? "emu_idle" : "emu_restart", st);
 }
@@ -1049,8 +1057,7 @@ void launch_render(const Env& env, const GameK& g, const Outs& o, int f, bool us
     if (n > 0)
         env.clock.run(restart ? KC_RENDER_RESTART : KC_RENDER, st,
                       [&] {
-                          if (g.cart.board == NES_BOARD_MMC2) hipLaunchKernelGGL(k_render<true>, dim3(n), dim3(64), 0, st, a);
-                          else hipLaunchKernelGGL(k_render<false>, dim3(n), dim3(64), 0, st, a);
+                          hipLaunchKernelGGL(k_render, dim3(n), dim3(64), 0, st, a);
                       });
     trace(restart ? "render_restart" : "render", st);
 }
@@ -1134,9 +1141,12 @@ void boot_game(Env& env, GameH& gh, const uint8_t* pads, size_t npads) {
     auto frame = [&](NesRec* base, int index, uint32_t pad) {
         GameK one = g;
         one.recs = base;
-        EmuArgs a{one, env.e, env.o, env.s, env.optab, EMU_BOOT, 0, 1, 0, index, index + 1, pad, target, fault,
+        EmuArgs a{one, env.e, env.o, env.s, env.optab, EMU_BOOT, 0, 0, index, index + 1, pad, target, fault,
                   env.budget};
-        hipLaunchKernelGGL(k_emu, dim3(1), dim3(64), 1024u + kRamStride, 0, a);
+        if (g.cart.board == NES_BOARD_NROM || g.cart.board == NES_BOARD_CNROM)
+            hipLaunchKernelGGL(k_emu_w<NES_BOARD_NROM>, dim3(1), dim3(64), 0, 0, a);
+        else
+            hipLaunchKernelGGL(k_emu_w<NES_BOARD_MMC3>, dim3(1), dim3(64), 0, 0, a);
         target += NES_FRAME_DOTS;
     };
     for (size_t i = 0; i < npads; ++i) frame(g.recs, g.n, pads[i]);
@@ -1195,12 +1205,7 @@ void* rlenv_create(int ngames, const int* game_ids, const uint8_t* const* roms, 
         if (hipSetDevice(device) != hipSuccess) throw std::runtime_error("hipSetDevice failed");
         env = new Env();
         env->device = device;
-        if (const char* v = std::getenv("RLENV_CPW")) env->cpw = std::max(1, std::min(64, std::atoi(v)));
-        if (const char* v = std::getenv("RLENV_EMU")) env->emu_wave = std::strcmp(v, "lane") != 0;
         if (const char* v = std::getenv("RLENV_BUDGET")) env->budget = (uint32_t)std::max(1, std::min((int)NES_BUDGET, std::atoi(v)));
-        if (hipFuncSetAttribute(reinterpret_cast<const void*>(k_emu), hipFuncAttributeMaxDynamicSharedMemorySize,
-                                (int)(1024u + 64u * kRamStride)) != hipSuccess)
-            throw std::runtime_error("hipFuncSetAttribute(k_emu) failed");
         env->s.run_seed = run_seed;
         env->s.sticky = sticky;
         env->s.idle_max = idle_max;

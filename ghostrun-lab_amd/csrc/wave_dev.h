@@ -36,12 +36,8 @@ struct Hot {
 };
 constexpr uint32_t pc_shift(uint32_t board) { return board == NES_BOARD_NROM ? 3u : 0u; }
 
-// A wave-uniform value read from LDS, as a scalar (an LDS load lands in a VGPR; without this the compiler moves every
-// use of it to the vector unit, with lane-mask compares instead of SCC branches).
-__device__ __forceinline__ uint32_t uni(uint32_t v) { return (uint32_t)__builtin_amdgcn_readfirstlane((int)v); }
-__device__ __forceinline__ uint64_t uni64(uint64_t v) {
-    return (uint64_t)uni((uint32_t)v) | ((uint64_t)uni((uint32_t)(v >> 32)) << 32);
-}
+// (uni(): a wave-uniform value read from LDS, as a scalar - replay_dev.h. An LDS load lands in a VGPR; without it the
+// compiler moves every use of the value to the vector unit, with lane-mask compares instead of SCC branches.)
 
 // The lazy N and Z of a status byte p: bit 8 = N, and a low byte that is 0 exactly when Z is set.
 __device__ __forceinline__ uint32_t nz_of_p(uint32_t p) {
@@ -381,11 +377,13 @@ __device__ __forceinline__ uint32_t dmc_distance(uint64_t now, uint64_t event) {
     return d > 0xFFFFFFFFull ? 0xFFFFFFFFu : (uint32_t)d;
 }
 
-// run_until (nes_dev.h) with the fast path first, for a console whose state `cs` lives in LDS: the same PPU
-// settling, event horizon, idle-loop fast-forward, budget and fault handling, so the console ends in exactly the
-// state run_until leaves. The fast loop keeps only Hot and a few scalars live and counts CPU cycles in 32 bits since
-// the last flush into h.cycles (a frame is ~30k cycles); the generic step, the settle and the fast-forward work on
-// `cs` (registers written back before and reloaded after each of them).
+// The frame loop (rl/csrc/nes_machine.cuh:67-103) for a console whose state `cs` lives in LDS: instructions until a
+// settle reaches absolute dot `target`, the PPU settled lazily when the unsettled dots reach the event horizon and
+// after an idle jump (then fast-forwarded), within the instruction budget, stopping on a fault. Fast instructions run
+// in bursts that keep only Hot and a few scalars live, counting CPU cycles in 32 bits since the last flush into
+// h.cycles (a frame is ~30k cycles); the generic step and the settle work on `cs` (registers written back before and
+// reloaded after the generic step; the settle touches no CPU register). Every settle goes through the one call of
+// ppu_step at the top of the loop, so its replays are inlined once.
 template <uint32_t B>
 __device__ __forceinline__ uint32_t run_until_wave(Con& cs, const Mem& m, const uint32_t* optab, uint64_t target,
                                                    uint32_t budget = NES_BUDGET) {
@@ -396,7 +394,9 @@ __device__ __forceinline__ uint32_t run_until_wave(Con& cs, const Mem& m, const 
     uint64_t dmc_event = uni64(cs.dmc_event);
     uint32_t ecyc = 0;                                     // cycles not yet added to h.cycles
     uint32_t dmc_in = dmc_distance(h.cycles, dmc_event);   // from h.cycles to the DMC event; ecyc <= dmc_in here
-    uint32_t nmi = uni(cs.nmi_pending), irq = uni(cs.irq_line), s0v = uni(cs.s0_valid);
+    uint32_t nmi = uni(cs.nmi_pending), irq = uni(cs.irq_line);
+    // why a settle is due besides the horizon: 1 after an idle jump (then the fast-forward), 2 before leaving
+    uint32_t why = 0;
     // The last fast instruction took the cycle count to the DMC event: service it, then count the instruction with
     // the stolen cycles (cpu_step's order).
     auto dmc_due = [&](uint32_t cyc) {
@@ -409,29 +409,51 @@ __device__ __forceinline__ uint32_t run_until_wave(Con& cs, const Mem& m, const 
         pending += 3u * (cyc + s);
         ++instructions;
     };
-    while (instructions < budget) {
-        if (pending >= to_event) {
-            ppu_advance(cs, m, pending);   // touches no CPU register
+    for (;;) {
+        if (why == 0 && instructions >= budget) why = 2;
+        if (why != 0 || pending >= to_event) {
+            ppu_step<B>(cs, m, pending);   // touches no CPU register
             pending = 0;
             nmi = uni(cs.nmi_pending);
             irq = uni(cs.irq_line);
-            if (abs_dot(cs) >= target) break;
+            if (why == 2) break;
+            if (why == 1) {
+                why = 0;
+                if (abs_dot(cs) >= target) break;
+                // The idle JMP-to-self loop (patch:866-893): whole 3-cycle jumps up to the next PPU event, settled at
+                // once; not with an NMI raised by the settle before it. (h is current: the generic step stored it.)
+                if (!nmi) {
+                    const uint32_t jumps = (uni(dots_to_event(cs, m)) + 8u) / 9u;
+                    if (jumps) {
+                        h.cycles += 3u * jumps;
+                        if (h.cycles >= dmc_event) {
+                            (void)dmc_service(m.rec, h.cycles, 0);
+                            dmc_event = uni64(m.rec->dmc_event);
+                        }
+                        dmc_in = dmc_distance(h.cycles, dmc_event);
+                        pending = 9u * jumps;
+                        to_event = 0;
+                        continue;
+                    }
+                }
+                to_event = uni(dots_to_event(cs, m));
+                continue;
+            }
             to_event = uni(dots_to_event(cs, m));
-            s0v = uni(cs.s0_valid);
+            if (abs_dot(cs) >= target) break;
         }
         uint32_t op = 0, pc0 = 0, cyc = 0;
         if (((nmi | (irq & ~(h.p >> 2))) & 1u) == 0u) {   // no NMI, and no IRQ unless the I flag masks it
-            // Fast instructions. With the sprite-0 horizon current and no IRQ asserted (a masked one is taken as soon
-            // as CLI, PLP or RTI clears the I flag) this is a burst: they run back to back until one
-            // needs the generic step (cyc = 0, nothing changed) or the cycles used reach `room`, the nearest of the
-            // DMC event, the PPU event horizon (3 dots a cycle) and the instruction budget (every instruction takes
-            // at least 2 cycles, so a burst never passes it). Otherwise one instruction runs and the horizon is
-            // refreshed after it. lm1 = room - 1 (< 2^15: the horizon is less than a frame, 89342 dots, away).
-            // One register counts both: v = lm1 << 14 | instructions run (< 2^14: half the room at most), and each
-            // instruction takes (cyc << 14) - 1 off it (a constant for most handlers). v < take exactly when
-            // cyc > lm1, "cyc == 0 or cyc >= room" (kGeneric stands for a cyc of 0).
+            // Fast instructions. With no IRQ asserted (a masked one is taken as soon as CLI, PLP or RTI clears the I
+            // flag) this is a burst: they run back to back until one needs the generic step (cyc = 0, nothing
+            // changed) or the cycles used reach `room`, the nearest of the DMC event, the PPU event horizon (3 dots a
+            // cycle) and the instruction budget (every instruction takes at least 2 cycles, so a burst never passes
+            // it). Otherwise one instruction runs. lm1 = room - 1 (< 2^15: the horizon is less than a frame, 89342
+            // dots, away). One register counts both: v = lm1 << 14 | instructions run (< 2^14: half the room at
+            // most), and each instruction takes (cyc << 14) - 1 off it (a constant for most handlers). v < take
+            // exactly when cyc > lm1, "cyc == 0 or cyc >= room" (kGeneric stands for a cyc of 0).
             uint32_t lm1 = 0;
-            if ((s0v & ~irq) & 1u)
+            if ((irq & 1u) == 0u)
                 lm1 = uni(max(min(min(dmc_in - ecyc, (to_event - pending + 2u) / 3u), 2u * (budget - instructions)),
                               1u) - 1u);
             const uint32_t lm1_0 = lm1;
@@ -455,10 +477,6 @@ __device__ __forceinline__ uint32_t run_until_wave(Con& cs, const Mem& m, const 
                     pending += 3u * used;
                     instructions += n;
                 }
-                if (!s0v) {
-                    to_event = uni(dots_to_event(cs, m));
-                    s0v = uni(cs.s0_valid);
-                }
                 continue;
             }
             pending += 3u * used;       // the last one needs the generic step
@@ -469,45 +487,24 @@ __device__ __forceinline__ uint32_t run_until_wave(Con& cs, const Mem& m, const 
         ecyc = 0;
         hot_store<B>(h, cs);
         cs.dmc_event = dmc_event;
-        const int32_t start_rel = (int32_t)((int64_t)abs_dot(cs) + pending - (int64_t)cs.log_frame * NES_FRAME_DOTS);
-        cyc = cpu_step(cs, m, optab, start_rel, &fault, &op, &pc0);
+        cyc = cpu_step(cs, m, optab, uni(cs.frame_dot) + pending, &fault, &op, &pc0);
         hot_load<B>(h, cs);
         dmc_event = uni64(cs.dmc_event);
         dmc_in = dmc_distance(h.cycles, dmc_event);
         nmi = uni(cs.nmi_pending);
         irq = uni(cs.irq_line);
-        s0v = uni(cs.s0_valid);
-        if (fault) break;
+        if (fault) {
+            why = 2;
+            continue;
+        }
         pending += 3u * cyc;
         ++instructions;
-        if (!s0v) {
-            to_event = uni(dots_to_event(cs, m));
-            s0v = uni(cs.s0_valid);
-        }
-        if (op == 0x4Cu && h.pc == pc0 << pc_shift(B)) {
-            hot_store<B>(h, cs);
-            cs.dmc_event = dmc_event;
-            ppu_advance(cs, m, pending);
-            pending = 0;
-            nmi = uni(cs.nmi_pending);
-            irq = uni(cs.irq_line);
-            if (abs_dot(cs) >= target) break;
-            fast_forward(cs, m);
-            h.cycles = uni64(cs.cycles);
-            dmc_event = uni64(cs.dmc_event);
-            dmc_in = dmc_distance(h.cycles, dmc_event);
-            nmi = uni(cs.nmi_pending);
-            irq = uni(cs.irq_line);
-            to_event = uni(dots_to_event(cs, m));
-            s0v = uni(cs.s0_valid);
-            if (abs_dot(cs) >= target) break;
-        }
+        if (op == 0x4Cu && h.pc == pc0 << pc_shift(B)) why = 1;
     }
     h.cycles += ecyc;
     hot_store<B>(h, cs);
     cs.dmc_event = dmc_event;
     cs.instr += instructions;
-    if (pending) ppu_advance(cs, m, pending);
     return fault;
 }
 

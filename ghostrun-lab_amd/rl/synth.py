@@ -665,9 +665,11 @@ def smb_like_cart(seed: int = 0) -> bytes:
     forward, Left 1 px back, A adds 10 points (score digits $07E1-$07E2), holding Down for 24 frames starts dying
     (routine 6); page 3 is the next level ($075C, then world $075F), world 8 wins (mode 2, world 7). Dying lasts 30
     frames, then a life ($075A) is lost and play resumes at the level start; losing a life at 0 is game over
-    (mode 3)."""
+    (mode 3). Like SMB, the NMI ends with the status-bar split: it waits for the sprite-0 hit (sprite 0 at line
+    24) and then writes the horizontal scroll, mid-line."""
     rng = np.random.default_rng([0x534D424C, seed])
     pal, nt, oam, mix = _tables(rng)
+    oam[0:4] = (23, int(oam[1]), 0x00, 88)                    # sprite 0 at the bottom of a status bar, as in SMB
     a = Asm(0xC000)
     tables = dict(pal='t_pal', nt='t_nt', oam='t_oam')
     a.label('reset')
@@ -718,6 +720,18 @@ def smb_like_cart(seed: int = 0) -> bytes:
     a.op('DEC', 'abs', 0x075A); a.op('BPL', 'rel', 'done')
     a.op('LDA', 'imm', 3); a.op('STA', 'abs', 0x0770)
     a.label('done')
+    # SMB's status-bar split: wait for the sprite-0 flag to drop (pre-render line), then for the hit, a short delay
+    # into the line, then the playfield's horizontal scroll (each wait bounded)
+    a.op('LDX', 'imm', 0)
+    a.label('s0c'); a.op('BIT', 'abs', 0x2002); a.op('BVC', 'rel', 's0c_ok'); a.op('DEX'); a.op('BNE', 'rel', 's0c')
+    a.label('s0c_ok')
+    a.op('LDY', 'imm', 4)
+    a.label('s0w'); a.op('BIT', 'abs', 0x2002); a.op('BVS', 'rel', 's0h'); a.op('DEX'); a.op('BNE', 'rel', 's0w')
+    a.op('DEY'); a.op('BNE', 'rel', 's0w')
+    a.label('s0h')
+    a.op('LDY', 'imm', 5)
+    a.label('s0d'); a.op('DEY'); a.op('BNE', 'rel', 's0d')
+    a.op('LDA', 'zp', 0x86); a.op('STA', 'abs', 0x2005); a.op('LDA', 'imm', 0); a.op('STA', 'abs', 0x2005)
     _nmi_end(a)
     a.label('irq')
     a.op('RTI')

@@ -512,3 +512,42 @@ def test_bit_2002_polling_sees_the_hit_at_its_dot():
         cyc, fault = con.step()
         assert fault == 0 and con.u('frame', 'I') == 1
     assert starts[-1] >= hit_dot and starts[-2] < hit_dot
+
+
+# --------------------------------------------------------------------------- what the parity carts exercise
+
+def line_landings(con):
+    """(line, position) of every logged write of the console's frame that lands while a visible line is drawn:
+    position = the instruction's end on the replay grid minus the line's start (16 dots before its dot 0)."""
+    h = con.words('log', 16 + 512)
+    n = min(con.u('log_n', 'H'), 256)
+    kook = (int(h[5]) >> 8) & 1
+    out = []
+    for i in range(n):
+        w0 = int(h[16 + 2 * i])
+        kind, cyc, dot = w0 & 15, (w0 >> 4) & 15, (w0 >> 8) & 0x1FFFF
+        if kind in (EV['data'], EV['pal']):
+            continue
+        t = dot - FRAME + 11 + kook if dot >= PRERENDER else dot + 11
+        end = t + 3 * cyc
+        line = (t + 16) // 341
+        pos = end - (line * 341 - 16)
+        if 0 <= line < 240 and 17 <= pos < 272:
+            out.append((line, pos))
+    return out
+
+
+@pytest.mark.parametrize('make', [lambda: synth.mmc3_cart(1), lambda: synth.smb_like_cart(1)], ids=['mmc3', 'smb'])
+def test_parity_carts_split_lines_mid_line_and_hit_sprite0(make):
+    """The seed-generated carts of the GPU parity tests draw frames the textbook line-start model would get wrong:
+    writes that land while a visible line is being drawn, and sprite-0 hits the CPU waits on."""
+    con = Console(make())
+    mid, hits = 0, 0
+    for f in range(1, 41):
+        con.set('pad', [0x81, 0x40, 0x02, 0xC0, 0x10][f % 5])
+        assert con.run_until(f * FRAME + VBLANK) == 0
+        mid += len(line_landings(con))
+        hit = ctypes.c_int(0)
+        con.lib.orc_sprite0_hit(con.rec.ctypes.data, con.cart_ptr(), ctypes.byref(hit))
+        hits += hit.value
+    assert mid >= 10 and hits >= 10, (mid, hits)
