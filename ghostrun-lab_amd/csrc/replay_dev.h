@@ -469,8 +469,9 @@ struct S0Sink {
             d1hi = mmc2 ? page(first) : s.chr_hi;
         }
     }
+    // (bits: sprite 0's opaque pixels, leftmost in bit 7; opq: leftmost in bit 0)
     __device__ int32_t find_hit(int32_t x, uint32_t bits, int32_t end) {
-        const uint32_t m = opq & bits & ((1u << (end - x)) - 1u);
+        const uint32_t m = opq & (__builtin_bitreverse32(bits) >> 24) & ((1u << (end - x)) - 1u);
         return m ? x + (int32_t)__builtin_ctz(m) : -1;
     }
     // Sprite 0's row when it is in the line (the sprite-0 setup needs only that: a fetched line without sprite 0

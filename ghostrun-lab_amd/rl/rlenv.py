@@ -87,6 +87,7 @@ def _load(path: Path):
         lib.rl_memcpy_async.argtypes = [P, P, SZ, P]
         lib.rl_gather_rows.argtypes = [P, P, P, I, SZ, P]
         lib.rl_gather_envs.argtypes = [P, P, P, I, I, I, SZ, P]
+    if hasattr(lib, 'rlenv_step_range'):
         lib.rlenv_step_game.argtypes = [P, I, P, P, P]
         lib.rlenv_step_range.argtypes = [P, I, I, I, P, P, P]
     return lib

@@ -12,6 +12,8 @@ cartridges generated here from a seed:
 * ``smb_like_cart(seed)`` - NROM-128 that writes the RAM bytes the SMB reward reader reads (position, level,
   lives, score, dying, mode) from the pad, idling in a JMP-to-self loop with its logic in the NMI as SMB does,
   so rewards, deaths, level changes, game over and the idle fast-forward all run.
+* ``dmc_cart(seed)`` - NROM-128 playing DMC samples (rate and loop changes, starts, stops, status polls).
+* ``fault_cart(nmis)`` - NROM-128 that hits an unofficial opcode after `nmis` frames (the emulator-fault end).
 * ``mmc2_cart(seed)`` - MMC2 (mapper 9): 128 KB PRG in 8 KB banks, 128 KB CHR ROM, nametables and sprites rich in
   the latch tiles $FD/$FE, CHR bank and mirroring rewrites, CPU-driven latch flips through $2006/$2007.
 * ``spec_cart(spec, seed)`` - NROM-128 that writes the RAM bytes a game's reward reader reads, from a spec of
@@ -293,6 +295,75 @@ def nrom_cart(seed: int = 0, blocks: int = 24) -> bytes:
     prg[0x3FFA:0x4000] = bytes(sum(((v & 0xFF, v >> 8) for v in vec), ()))
     chr_ = rng.integers(0, 256, 8192, dtype=np.uint8).tobytes()
     return ines(bytes(prg), chr_, 0, vertical=True)
+
+
+DMC_CNT = 0x25                            # the DMC cart's count of status polls that saw a sample playing
+
+
+def dmc_cart(seed: int = 0, blocks: int = 16) -> bytes:
+    """NROM-128 cartridge that plays DMC samples: every pass of its main loop writes a rate ($4010 bits 0-3, changed
+    while a sample plays) and the loop flag (bit 6) from its counters, a length ($4013) from the pad, starts a sample
+    ($4015 = $10) every 32 passes and stops it ($4015 = 0) every 64, and polls $4015 bit 4 (bytes left) up to 8 times.
+    Each sample byte fetched steals 4 CPU cycles, so the console's timing, and with it every later frame, depends on
+    the channel."""
+    rng = np.random.default_rng([0x444D4320, seed])
+    pal, nt, oam, mix = _tables(rng)
+    a = Asm(0xC000)
+    tables = dict(pal='t_pal', nt='t_nt', oam='t_oam')
+    a.label('reset')
+    _reset_common(a, 0x90, tables)
+    a.label('main')
+    _read_pad(a, 'm')
+    _pad_moves(a, 't_mix')
+    a.op('LDA', 'zp', CNT_LO); a.op('EOR', 'zp', PAD); a.op('AND', 'imm', 0x4F); a.op('STA', 'abs', 0x4010)
+    a.op('LDA', 'zp', PAD); a.op('AND', 'imm', 0x07); a.op('STA', 'abs', 0x4013)
+    a.op('LDA', 'zp', CNT_LO); a.op('AND', 'imm', 0x1F); a.op('BNE', 'rel', 'd_nostart')
+    a.op('LDA', 'imm', 0x10); a.op('STA', 'abs', 0x4015)
+    a.label('d_nostart')
+    a.op('LDA', 'zp', CNT_LO); a.op('AND', 'imm', 0x3F); a.op('CMP', 'imm', 0x30); a.op('BNE', 'rel', 'd_nostop')
+    a.op('LDA', 'imm', 0x00); a.op('STA', 'abs', 0x4015)
+    a.label('d_nostop')
+    a.op('LDX', 'imm', 8)
+    a.label('d_poll'); a.op('LDA', 'abs', 0x4015); a.op('AND', 'imm', 0x10); a.op('BEQ', 'rel', 'd_done')
+    a.op('INC', 'zp', DMC_CNT); a.op('DEX'); a.op('BNE', 'rel', 'd_poll')
+    a.label('d_done')
+    _filler(a, rng, blocks, 'f', 't_mix')
+    a.op('JMP', 'abs', 'main')
+    a.label('nmi')
+    _nmi_common(a)
+    _nmi_end(a)
+    a.label('irq')
+    a.op('RTI')
+    for name, t in (('t_pal', pal), ('t_nt', nt), ('t_oam', oam), ('t_mix', mix)):
+        a.label(name)
+        a.data(bytes(int(v) for v in t))
+    code = a.assemble()
+    assert len(code) <= 0x3FFA, len(code)
+    prg = bytearray(16384)
+    prg[:len(code)] = code
+    vec = (a.labels['nmi'], a.labels['reset'], a.labels['irq'])
+    prg[0x3FFA:0x4000] = bytes(sum(((v & 0xFF, v >> 8) for v in vec), ()))
+    chr_ = rng.integers(0, 256, 8192, dtype=np.uint8).tobytes()
+    return ines(bytes(prg), chr_, 0, vertical=True)
+
+
+def fault_cart(nmis: int = 3) -> bytes:
+    """NROM-128 cartridge that runs into an unofficial opcode ($02) once its NMI has counted `nmis` frames: an
+    emulator fault, which ends the episode (end reason 5, reward 0; rl/csrc/rlenv_core.cuh:273-301)."""
+    a = Asm(0xC000)
+    a.label('reset')
+    a.op('SEI'); a.op('LDA', 'imm', 0); a.op('STA', 'zp', 0x10); a.op('LDA', 'imm', 0x80); a.op('STA', 'abs', 0x2000)
+    a.op('LDA', 'imm', 0x1E); a.op('STA', 'abs', 0x2001)
+    a.label('loop')
+    a.op('LDA', 'zp', 0x10); a.op('CMP', 'imm', nmis); a.op('BCC', 'rel', 'loop')
+    a.byte(0x02)
+    a.label('nmi')
+    a.op('INC', 'zp', 0x10); a.op('RTI')
+    code = a.assemble()
+    prg = bytearray(16384)
+    prg[:len(code)] = code
+    prg[0x3FFA:0x4000] = bytes((a.labels['nmi'] & 0xFF, a.labels['nmi'] >> 8, 0, 0xC0, 0, 0xC0))
+    return ines(bytes(prg), bytes(range(256)) * 32, 0)
 
 
 def cnrom_cart(seed: int = 0, blocks: int = 24, conflicts: bool = False) -> bytes:

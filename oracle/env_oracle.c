@@ -415,13 +415,14 @@ typedef struct Env {
     uint64_t run_seed;
     int sticky, idle_max, dropout, no_render, episode_level_end, pad_mode;
     uint32_t end_p32, gap_p32;
+    uint32_t budget;          /* instructions per frame: NES_BUDGET, or RLENV_BUDGET (diagnostics of the budget exit) */
 } Env;
 
 static void emu_frame(Env* E, Game* g, int e, int ge, uint8_t pad) {
     NesRec* r = &g->recs[e];
     r->pad = pad;
     if (E->fault[ge] == 0) {
-        const uint32_t f = orc_run_until(r, &g->cart, E->target[ge]);
+        const uint32_t f = orc_run_until_budget(r, &g->cart, E->target[ge], E->budget);
         if (f) E->fault[ge] = f;
     }
     E->target[ge] += NES_FRAME_DOTS;
@@ -668,6 +669,14 @@ void* rlenv_create(int ngames, const int* game_ids, const uint8_t* const* roms, 
     E->idle_tmpl = idle_max > 0 ? idle_max : 0;
     E->episode_level_end = -1;
     E->gap_p32 = RLC_GAP_P32;
+    E->budget = NES_BUDGET;
+    {   /* the HIP library's diagnostic knob, read the same way */
+        const char* v = getenv("RLENV_BUDGET");
+        if (v) {
+            const int b = atoi(v);
+            E->budget = (uint32_t)(b < 1 ? 1 : b > (int)NES_BUDGET ? (int)NES_BUDGET : b);
+        }
+    }
     for (int i = 0; i < ngames; ++i) {
         Game* g = &E->games[i];
         if (game_ids[i] < 0 || game_ids[i] >= RL10_NUM_GAMES) {
@@ -696,7 +705,7 @@ void* rlenv_create(int ngames, const int* game_ids, const uint8_t* const* roms, 
         uint64_t target = NES_VBLANK_DOT;
         for (size_t f = 0; f < boot_sizes[i]; ++f) {
             boot->pad = boot_pads[i][f];
-            if (orc_run_until(boot, &g->cart, target) != 0) {
+            if (orc_run_until_budget(boot, &g->cart, target, E->budget) != 0) {
                 snprintf(g_err, sizeof(g_err), "emulator fault during boot of game %d", g->game);
                 env_free(E);
                 return NULL;
@@ -707,7 +716,7 @@ void* rlenv_create(int ngames, const int* game_ids, const uint8_t* const* roms, 
         NesRec tmp = *boot;
         for (int k = 1; k <= E->idle_tmpl; ++k) {
             tmp.pad = 0;
-            if (orc_run_until(&tmp, &g->cart, target) != 0) {
+            if (orc_run_until_budget(&tmp, &g->cart, target, E->budget) != 0) {
                 snprintf(g_err, sizeof(g_err), "emulator fault in idle frames of game %d", g->game);
                 env_free(E);
                 return NULL;
@@ -772,6 +781,26 @@ int rlenv_start(void* h, void* stream) {
     return 0;
 }
 
+/* Level-start saves of game g after its envs' finish (rlenv_core.cuh:343-387, rl/csrc/rlenv_cpu.cpp:108-117). */
+static void level_saves(Env* E, Game* g) {
+    for (int s = 0; s < g->lv_levels; ++s) {
+        const uint64_t cl = g->lv_claim[s];
+        if (cl == ~0ull) continue;
+        const int take = g->lv_deaths[s] < 0 || (int32_t)(cl >> 32) <= g->lv_deaths[s];
+        if (take) {
+            const int e = (int)(cl & 0xFFFFFFFFull), ge = g->offset + e;
+            g->lv_rec[s] = g->recs[e];
+            g->lv_st[s] = E->st[ge];
+            g->lv_rd[s] = E->rd[ge];
+            memcpy(g->lv_keys + (size_t)s * g->kcap, g->keys + (size_t)e * g->kcap, (size_t)g->kcap * 4u);
+            g->lv_target[s] = E->target[ge];
+            g->lv_frame[s] = E->ep_frame[ge];
+            g->lv_deaths[s] = (int32_t)(cl >> 32);
+        }
+        g->lv_claim[s] = ~0ull;
+    }
+}
+
 int rlenv_step(void* h, void* stream) {
     (void)stream;
     Env* E = (Env*)h;
@@ -783,26 +812,43 @@ int rlenv_step(void* h, void* stream) {
     }
     /* level-start saves after every env's finish; restarts read the saves only in reset_state, so doing them after
      * the whole step equals the GPU's order (rlenv_core.cuh:343-387, rl/csrc/rlenv_cpu.cpp:108-117) */
-    for (int i = 0; i < E->ngames; ++i) {
-        Game* g = &E->games[i];
-        for (int s = 0; s < g->lv_levels; ++s) {
-            const uint64_t cl = g->lv_claim[s];
-            if (cl == ~0ull) continue;
-            const int take = g->lv_deaths[s] < 0 || (int32_t)(cl >> 32) <= g->lv_deaths[s];
-            if (take) {
-                const int e = (int)(cl & 0xFFFFFFFFull), ge = g->offset + e;
-                g->lv_rec[s] = g->recs[e];
-                g->lv_st[s] = E->st[ge];
-                g->lv_rd[s] = E->rd[ge];
-                memcpy(g->lv_keys + (size_t)s * g->kcap, g->keys + (size_t)e * g->kcap, (size_t)g->kcap * 4u);
-                g->lv_target[s] = E->target[ge];
-                g->lv_frame[s] = E->ep_frame[ge];
-                g->lv_deaths[s] = (int32_t)(cl >> 32);
-            }
-            g->lv_claim[s] = ~0ull;
-        }
-    }
+    for (int i = 0; i < E->ngames; ++i) level_saves(E, &E->games[i]);
     return 0;
+}
+
+/* One decision of envs [start, start + count) of game gi, their pictures into obs / emph (whole-batch buffers; these
+ * envs write only their own rows): the GPU extras rlenv_step_game / rlenv_step_range of rl/csrc/rlenv.cu:247-268,
+ * for the checker. */
+int rlenv_step_range(void* h, int gi, int start, int count, uint8_t* obs, uint8_t* emph, void* stream) {
+    (void)stream;
+    Env* E = (Env*)h;
+    if (gi < 0 || gi >= E->ngames) {
+        snprintf(g_err, sizeof(g_err), "step_range: bad game");
+        return 1;
+    }
+    Game* g = &E->games[gi];
+    if (start < 0 || count <= 0 || start + count > g->n) {
+        snprintf(g_err, sizeof(g_err), "step_range: bad range");
+        return 1;
+    }
+    uint8_t *obs0 = E->obs, *emph0 = E->emph;
+    E->obs = obs;
+    E->emph = emph;
+#pragma omp parallel for schedule(dynamic, 1)
+    for (int e = start; e < start + count; ++e) env_step_one(E, g, e);
+    level_saves(E, g);
+    E->obs = obs0;
+    E->emph = emph0;
+    return 0;
+}
+
+int rlenv_step_game(void* h, int gi, uint8_t* obs, uint8_t* emph, void* stream) {
+    Env* E = (Env*)h;
+    if (gi < 0 || gi >= E->ngames) {
+        snprintf(g_err, sizeof(g_err), "step_game: bad game");
+        return 1;
+    }
+    return rlenv_step_range(h, gi, 0, E->games[gi].n, obs, emph, stream);
 }
 
 /* ---------------------------------------------------------------------------- level starts / places
