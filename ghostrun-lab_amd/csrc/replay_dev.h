@@ -100,14 +100,14 @@ struct Rs {
     uint32_t spork, hit;
     int32_t sphitx, hit_x;
     uint32_t sphit_bits;
-    const uint32_t* ev;
 };
 
 __device__ __forceinline__ bool rs_rendering(const Rs& s) { return (s.mask & 0x18u) != 0; }
 __device__ __forceinline__ uint32_t rs_inc(const Rs& s) { return (s.ctrl & 4u) ? 32u : 1u; }
 
-__device__ __forceinline__ void rs_next(Rs& s) {
-    s.next = s.cur < s.count ? fceu_time((uni(s.ev[2u * s.cur]) >> 8) & 0x1FFFFu, s.kook) : kNoEvent;
+template <class K>
+__device__ __forceinline__ void rs_next(Rs& s, K& k) {
+    s.next = s.cur < s.count ? fceu_time((k.ev(2u * s.cur) >> 8) & 0x1FFFFu, s.kook) : kNoEvent;
 }
 
 // MMC2: half `half`'s slots from its register and latch (patch:1385-1388).
@@ -128,9 +128,10 @@ __device__ __forceinline__ void rs_hook(Rs& s, uint32_t a) {
     rs_mmc2_select(s, half);
 }
 
-// The replay from the log header (patch:1361-1383): `log` = header + events (global memory), `ev` = the events to
-// read (the log's own, or a copy of them), `n` events.
-__device__ inline void rs_load(Rs& s, const uint32_t* log, const uint32_t* ev, uint32_t n, uint32_t mmc2_pages) {
+// The replay from the log header (patch:1361-1383): `log` = header + events (global memory), `n` events (read through
+// the sink).
+template <class K>
+__device__ inline void rs_load(Rs& s, K& k, const uint32_t* log, uint32_t n, uint32_t mmc2_pages) {
     const uint32_t h1 = uni(log[1]), h2 = uni(log[2]), h5 = uni(log[5]);
     s.ctrl = h1 & 0xFFu;
     s.mask = (h1 >> 8) & 0xFFu;
@@ -144,7 +145,6 @@ __device__ inline void rs_load(Rs& s, const uint32_t* log, const uint32_t* ev, u
     s.creg = uni(log[14]);
     s.latch = uni(log[15]);
     s.mmc2_pages = mmc2_pages;
-    s.ev = ev;
     s.count = n < NES_LOG_EVENTS ? n : NES_LOG_EVENTS;
     s.cur = 0;
     s.f_n = s.f_blurp = s.f_bits = s.f_attr = s.f_x = 0;
@@ -152,16 +152,16 @@ __device__ inline void rs_load(Rs& s, const uint32_t* log, const uint32_t* ev, u
     s.sphitx = kNoCheck;
     s.hit_x = -1;
     s.sphit_bits = 0;
-    rs_next(s);
+    rs_next(s, k);
 }
 
 // Event cur applied to the replay (patch:1424-1481); palette writes go to the sink. `drawing`: a line is drawn.
 template <class K>
 __device__ inline void rs_apply(Rs& s, K& k, bool drawing) {
-    const uint32_t w0 = uni(s.ev[2u * s.cur]), w1 = uni(s.ev[2u * s.cur + 1u]);
+    const uint32_t w0 = k.ev(2u * s.cur), w1 = k.ev(2u * s.cur + 1u);
     const uint32_t kind = w0 & 15u, val = w1 & 0xFFu, aux = (w1 >> 8) & 0xFFu;
     ++s.cur;
-    rs_next(s);
+    rs_next(s, k);
     if (kind == NES_EV_CTRL) {
         s.ctrl = val;
         s.t = (s.t & 0xF3FFu) | ((val & 3u) << 10);
@@ -295,7 +295,7 @@ __device__ inline void rs_line(Rs& s, K& k, int32_t l, bool pixels) {
     Ln ln{0, 0, true};
     k.line_begin(s, pixels);
     while (s.next < start + 272) {
-        const uint32_t w0 = uni(s.ev[2u * s.cur]), kind = w0 & 15u;
+        const uint32_t w0 = k.ev(2u * s.cur), kind = w0 & 15u;
         if (kind != NES_EV_DATA && kind != NES_EV_PAL) rs_update(s, k, ln, s.next + 3 * (int32_t)((w0 >> 4) & 15u) - start, pixels);
         rs_apply(s, k, true);
     }
@@ -368,6 +368,7 @@ __device__ __forceinline__ uint32_t chr_pk(const uint8_t* chr_rom, const uint8_t
 // fetch is kept as a descriptor (v | pattern table << 15 | nametable map << 16, and the slot pages) and fetched only
 // when its pixels fall under sprite 0.
 struct S0Sink {
+    const uint32_t* ev_mem;      // the log's events (global memory, written by this kernel)
     const uint8_t* nt_mem;       // the console's nametables and OAM as they are now (LDS)
     const uint8_t* oam_mem;
     const uint8_t *chr_rom, *chr_ram;
@@ -377,6 +378,7 @@ struct S0Sink {
     uint32_t opq;                // sprite 0's 8 pixels on this line: bit i set = pixel sphitx + i opaque background
     int32_t x0;                  // sphitx of this line (kNoCheck: no check, nothing to track)
 
+    __device__ uint32_t ev(uint32_t i) { return uni(ev_mem[i]); }
     __device__ uint32_t nt(uint32_t i) { return uni(nt_mem[i]); }
     __device__ uint32_t oam(uint32_t i) { return uni(oam_mem[i]); }
     __device__ void palette(uint32_t, uint32_t) {}
@@ -507,8 +509,9 @@ __device__ __forceinline__ uint32_t sprite0_hit(const uint32_t* log, uint32_t lo
     const int32_t first = (int32_t)uni(oam[0]) + 1;
     if (first >= 240) return 0;
     Rs s;
-    rs_load(s, log, log + NES_LOG_HDR_WORDS, log_n, mmc2_pages);
     S0Sink k;
+    k.ev_mem = log + NES_LOG_HDR_WORDS;
+    rs_load(s, k, log, log_n, mmc2_pages);
     k.nt_mem = nt;
     k.oam_mem = oam;
     k.chr_rom = chr_rom;
@@ -564,8 +567,10 @@ __device__ __forceinline__ uint32_t sprite0_hit(const uint32_t* log, uint32_t lo
 // ------------------------------------------------------------------------------------------- MMC2
 // The latches-only replay: every pattern fetch's hook runs in the walker, nothing is drawn.
 struct LatchSink {
+    const uint32_t* ev_mem;
     const uint8_t* nt_mem;
     const uint8_t* oam_mem;
+    __device__ uint32_t ev(uint32_t i) { return uni(ev_mem[i]); }
     __device__ uint32_t nt(uint32_t i) { return uni(nt_mem[i]); }
     __device__ uint32_t oam(uint32_t i) { return uni(oam_mem[i]); }
     __device__ void palette(uint32_t, uint32_t) {}
@@ -585,8 +590,8 @@ struct LatchSink {
 __device__ __forceinline__ uint32_t mmc2_latches(const uint32_t* log, uint32_t log_n, const uint8_t* nt, const uint8_t* oam,
                                               uint32_t chr_pages) {
     Rs s;
-    rs_load(s, log, log + NES_LOG_HDR_WORDS, log_n, chr_pages);
-    LatchSink k{nt, oam};
+    LatchSink k{log + NES_LOG_HDR_WORDS, nt, oam};
+    rs_load(s, k, log, log_n, chr_pages);
     rs_begin_frame(s, k);
     for (int32_t l = 0; l < 240; ++l) {
         rs_line(s, k, l, false);

@@ -255,12 +255,15 @@ struct RenderArgs {
 //     into the line buffer at the run's output position (F[0], F[1] carry the line's first fetches' predecessors);
 //   - the run's hidden left column and background-off range, then the sprite-0 check over 8 lanes.
 // Sprite lines are fetched with one ballot over the 64 OAM entries (lane = sprite) into one of two buffers; the one
-// RefreshSprites latched is the one composed.
+// RefreshSprites latched is expanded at the start of the line it is drawn on (lane 8k + p = pixel p of sprite k) into
+// a sprite line with one LDS max per pixel, which picks the lowest-numbered opaque sprite.
+// A line with no write and no sprite-0 check (most of them) takes fast_line: one fetch phase, one sync, and each lane
+// composes its 4 pixels in registers.
 struct RenderLds {
     uint8_t nt[NES_NT_BYTES];
     uint8_t oam[NES_OAM_BYTES];
-    uint32_t ev[2 * NES_LOG_EVENTS];
     uint32_t px[64];          // the line: palette value, 0x40 | backdrop where the background is transparent
+    uint32_t sp[256];         // the sprite line: (7 - rank) << 8 | behind << 7 | palette << 2 | value, 0 = none
     uint32_t f[36];           // fetches: lo | hi << 8 | attribute << 16; 0-1 carried, 2 + j slot j
     uint32_t spr[2][8];       // sprite lines: lo | hi << 8 | attr << 16 | x << 24
     uint32_t pages[34 + 8];   // MMC2: the pages of each slot's fetch, then of each sprite's
@@ -268,18 +271,21 @@ struct RenderLds {
     uint8_t spal[16];
 };
 
+typedef __attribute__((address_space(4))) const uint32_t KU32;
+
 struct RenderSink {
     RenderLds* L;
+    const uint32_t* log;      // the console's frame log (read-only in this kernel: scalar loads)
     const uint8_t *chr_rom, *chr_ram;
     int lane;
     bool mmc2;
     uint32_t ha, hb;          // F indices of the last two fetches
     uint32_t fetched, drawn, drawn_n;
 
+    __device__ uint32_t ev(uint32_t i) { return ((KU32*)(log + NES_LOG_HDR_WORDS))[i]; }
     __device__ uint32_t nt(uint32_t i) { return uni(L->nt[i]); }
     __device__ uint32_t oam(uint32_t i) { return uni(L->oam[i]); }
-    __device__ uint8_t* px8() { return reinterpret_cast<uint8_t*>(L->px); }
-    __device__ uint32_t back4() { return (((uint32_t)L->pal[0] & 0x3Fu) | 0x40u) * 0x01010101u; }
+    __device__ uint32_t back() { return ((uint32_t)L->pal[0] & 0x3Fu) | 0x40u; }
     __device__ void palette(uint32_t i, uint32_t v) {
         if (lane == 0) L->pal[i] = (uint8_t)v;
         __syncthreads();
@@ -290,60 +296,81 @@ struct RenderSink {
     __device__ void sprite_pages(uint32_t n, uint32_t pk) {
         if (lane == 0) L->pages[34 + n] = pk;
     }
-    // A new line: the last two fetches move to F[0], F[1]; nothing drawn yet (0xFF reads as transparent).
-    __device__ void line_begin(const Rs&, bool) {
+    // The latched sprite line expanded into L->sp (before the line's first sync; the compose reads and clears it).
+    __device__ void expand_sprites(const Rs& s) {
+        if (!s.spork) return;
+        const uint32_t k = (uint32_t)lane >> 3, p = (uint32_t)lane & 7u;
+        if (k < drawn_n) {
+            const uint32_t e = L->spr[drawn][k];
+            const uint32_t attr = (e >> 16) & 0xFFu, b = (attr & 0x40u) ? p : 7u - p;
+            const uint32_t val = ((e >> b) & 1u) | (((e >> (8u + b)) & 1u) << 1);
+            const uint32_t x = (e >> 24) + p;
+            if (val && x < 256u)
+                atomicMax(&L->sp[x], ((7u - k) << 8) | ((attr & 0x20u) << 2) | ((attr & 3u) << 2) | val);
+        }
+    }
+    // A new line (general path): the last two fetches move to F[0], F[1]; nothing drawn yet (0xFF reads as
+    // transparent); the sprite line expanded.
+    __device__ void line_begin(const Rs& s, bool) {
         const uint32_t carry = lane < 2 ? L->f[lane ? hb : ha] : 0u;
         __syncthreads();
         if (lane < 2) L->f[lane] = carry;
         L->px[lane] = 0xFFFFFFFFu;
         ha = 0;
         hb = 1;
+        expand_sprites(s);
         __syncthreads();
     }
     // Pixels [o, o + n) the backdrop (o and n multiples of 8).
     __device__ void fill(int32_t o, int32_t n) {
         const int32_t x = 4 * lane;
-        if (x >= o && x < o + n) L->px[lane] = back4();
+        if (x >= o && x < o + n) L->px[lane] = back() * 0x01010101u;
     }
     __device__ void off_run(int32_t out, int32_t n, bool) {
         fill(out, n);
         __syncthreads();
     }
+    // Slot j's tile (nametable tile and attribute, both pattern bytes) fetched at v into F[j + 2].
+    __device__ void fetch_slot(const Rs& s, uint32_t v, uint32_t j, uint32_t lo, uint32_t hi) {
+        const uint32_t ntb = 0x2000u | (v & 0x0C00u), col = v & 31u;
+        const uint32_t tile = L->nt[nt_slot(s.nt_map, ntb | (v & 0x3FFu))];
+        const uint32_t at = L->nt[nt_slot(s.nt_map, ntb | 0x3C0u | (col >> 2) | ((v & 0x380u) >> 4))];
+        const uint32_t sel = (at >> ((col & 2u) | ((v & 0x40u) >> 4))) & 3u;
+        const uint32_t pa = tile * 16u + ((s.ctrl & 0x10u) << 8) + ((v >> 12) & 7u);
+        L->f[j + 2u] = chr_pk(chr_rom, chr_ram, lo, hi, pa) | (chr_pk(chr_rom, chr_ram, lo, hi, pa + 8u) << 8) |
+                       (sel << 16);
+    }
+    // 4 background pixels, leftmost in the low byte: kk0..kk0 + 3 of the 8 a slot shifts out from fetches p2 (older),
+    // p1 with fine x fx.
+    __device__ uint32_t shift4(uint32_t p2, uint32_t p1, uint32_t kk0, uint32_t fx, uint32_t back) {
+        const uint32_t lo16 = ((p2 & 0xFFu) << 8) | (p1 & 0xFFu), hi16 = (p2 & 0xFF00u) | ((p1 >> 8) & 0xFFu);
+        const uint32_t c2 = (p2 >> 16) & 3u, c1 = (p1 >> 16) & 3u;
+        uint32_t w = 0;
+        for (uint32_t q = 0; q < 4u; ++q) {
+            const uint32_t kk = kk0 + q, bit = 15u - fx - kk;
+            const uint32_t val = ((lo16 >> bit) & 1u) | (((hi16 >> bit) & 1u) << 1);
+            const uint32_t c = val ? (L->pal[(kk + fx < 8u ? c2 : c1) * 4u + val] & 0x3Fu) : back;
+            w |= c << (8u * q);
+        }
+        return w;
+    }
     __device__ void on_run(const Rs& s, int32_t first, int32_t last, int32_t out, bool pixels) {
         __syncthreads();   // the walker's page and palette writes
         if (lane >= first && lane < last) {
-            const uint32_t v = v_steps(s.v, (uint32_t)(lane - first));
-            const uint32_t ntb = 0x2000u | (v & 0x0C00u), col = v & 31u;
-            const uint32_t tile = L->nt[nt_slot(s.nt_map, ntb | (v & 0x3FFu))];
-            const uint32_t at = L->nt[nt_slot(s.nt_map, ntb | 0x3C0u | (col >> 2) | ((v & 0x380u) >> 4))];
-            const uint32_t sel = (at >> ((col & 2u) | ((v & 0x40u) >> 4))) & 3u;
-            const uint32_t pa = tile * 16u + ((s.ctrl & 0x10u) << 8) + ((v >> 12) & 7u);
             const uint32_t pk = mmc2 ? L->pages[lane] : 0u;
-            const uint32_t lo = mmc2 ? pk : s.chr_lo, hi = mmc2 ? pk : s.chr_hi;
-            L->f[lane + 2] = chr_pk(chr_rom, chr_ram, lo, hi, pa) | (chr_pk(chr_rom, chr_ram, lo, hi, pa + 8u) << 8) |
-                             (sel << 16);
+            fetch_slot(s, v_steps(s.v, (uint32_t)(lane - first)), (uint32_t)lane, mmc2 ? pk : s.chr_lo,
+                       mmc2 ? pk : s.chr_hi);
         }
         __syncthreads();
-        const int32_t from = first > 2 ? first : 2;
         if (pixels) {
-            const int32_t o = out + 8 * (lane - from);
-            if (lane >= from && lane < last && o < 256) {
-                const int32_t j = lane - first;
-                const uint32_t p1 = L->f[j >= 1 ? (uint32_t)lane + 1u : hb];
-                const uint32_t p2 = L->f[j >= 2 ? (uint32_t)lane : (j == 1 ? hb : ha)];
-                const uint32_t lo16 = ((p2 & 0xFFu) << 8) | (p1 & 0xFFu), hi16 = (p2 & 0xFF00u) | ((p1 >> 8) & 0xFFu);
-                const uint32_t c2 = (p2 >> 16) & 3u, c1 = (p1 >> 16) & 3u;
-                const uint32_t back = (L->pal[0] & 0x3Fu) | 0x40u;
-                uint32_t w[2] = {0u, 0u};
-                for (uint32_t q = 0; q < 8u; ++q) {
-                    const uint32_t bit = 15u - s.fx - q;
-                    const uint32_t val = ((lo16 >> bit) & 1u) | (((hi16 >> bit) & 1u) << 1);
-                    const uint32_t pal_sel = q + s.fx < 8u ? c2 : c1;
-                    const uint32_t c = val ? (L->pal[pal_sel * 4u + val] & 0x3Fu) : back;
-                    w[q >> 2] |= c << (8u * (q & 3u));
-                }
-                L->px[o >> 2] = w[0];
-                L->px[(o >> 2) + 1] = w[1];
+            // lane j writes pixels 4j..4j+3 where they fall in the run's output, [out, out + 8 (last - from))
+            const int32_t from = first > 2 ? first : 2, x = 4 * lane;
+            if (last > from && x >= out && x < out + 8 * (last - from)) {
+                const int32_t k = from + (x - out) / 8;   // the slot that shifts out pixel x
+                const int32_t j = k - first;
+                const uint32_t p1 = L->f[j >= 1 ? (uint32_t)k + 1u : hb];
+                const uint32_t p2 = L->f[j >= 2 ? (uint32_t)k : (j == 1 ? hb : ha)];
+                L->px[lane] = shift4(p2, p1, (uint32_t)((x - out) & 7), s.fx, back());
             }
             const bool clip = first <= 2 && last > 2 && !(s.mask & 0x02u), bg_off = !(s.mask & 0x08u);
             if (clip || bg_off) {
@@ -370,13 +397,14 @@ struct RenderSink {
     }
     __device__ int32_t find_hit(int32_t x, uint32_t bits, int32_t end) {
         const int32_t xi = x + lane;
-        const bool hit = lane < 8 && xi < end && ((bits >> (7 - lane)) & 1u) && !(px8()[xi] & 0x40u);
+        const bool hit = lane < 8 && xi < end && ((bits >> (7 - lane)) & 1u) &&
+                         !(reinterpret_cast<const uint8_t*>(L->px)[xi] & 0x40u);
         const uint64_t b = __ballot(hit);
         return b ? x + (int32_t)__builtin_ctzll(b) : -1;
     }
-    // FetchSpriteData for line l + 1: the first eight OAM entries on it, each row through the pages of the moment
-    // (MMC2: of its own fetch), into the buffer not latched.
-    __device__ void fetch_sprites(Rs& s, int32_t l) {
+    // The lanes' part of FetchSpriteData: lane i is OAM entry i; the first eight on line l + 1 are fetched into the
+    // buffer not latched. Returns the ballot of the entries on the line (read the fetch after a sync).
+    __device__ uint64_t sprite_fetch_lanes(const Rs& s, int32_t l) {
         const uint32_t ctrl = s.ctrl, h = (ctrl & 0x20u) ? 16u : 8u;
         const uint32_t e = reinterpret_cast<const uint32_t*>(L->oam)[lane];
         const uint32_t row = (uint32_t)(l - (int32_t)(e & 0xFFu));
@@ -396,66 +424,110 @@ struct RenderSink {
                                    (chr_pk(chr_rom, chr_ram, lo, hi, pa + 8u) << 8) | (e & 0xFFFF0000u);
         }
         fetched = target;
+        return sel;
+    }
+    // What RefreshSprites needs of the fetch (after the sync).
+    __device__ void sprite_fetch_done(Rs& s, uint64_t sel) {
         const uint32_t n = (uint32_t)__builtin_popcountll(sel);
         s.f_n = n < 8u ? n : 8u;
         s.f_blurp = (uint32_t)(sel & 1u);
-        __syncthreads();
         if (s.f_n) {
-            const uint32_t e0 = uni(L->spr[target][0]);
+            const uint32_t e0 = uni(L->spr[fetched][0]);
             s.f_bits = (e0 & 0xFFu) | ((e0 >> 8) & 0xFFu);
             s.f_attr = (e0 >> 16) & 0xFFu;
             s.f_x = e0 >> 24;
         }
     }
-    // RefreshSprites: the fetched line is the one drawn next, with the sprite palette of the moment.
+    __device__ void fetch_sprites(Rs& s, int32_t l) {
+        if (mmc2) __syncthreads();   // the walker's page writes
+        const uint64_t sel = sprite_fetch_lanes(s, l);
+        __syncthreads();
+        sprite_fetch_done(s, sel);
+    }
+    // RefreshSprites: the fetched line is the one drawn next, with the sprite palette of the moment (read by the next
+    // line's compose, after its syncs).
     __device__ void latch_sprites(const Rs& s) {
         drawn = fetched;
         drawn_n = s.f_n;
         if (lane < 16) L->spal[lane] = (uint8_t)(L->pal[16 + lane] & 0x3Fu);
-        __syncthreads();
     }
-    // CopySprites (with sprites on at the line's end and a latched line waiting), greyscale while rendering, and the
-    // observation row (rl/csrc/nes_machine.cuh:133-155: lines 8..231, x 8..247); returns the emphasis bits
-    // (patch:1637-1661).
-    __device__ void compose(Rs& s, int32_t l, uint8_t* obs, uint8_t* emph) {
-        const bool sprites = (s.mask & 0x10u) && s.spork;
+    // CopySprites (with sprites on at the line's end and a latched line waiting) over the background pixels w of
+    // this lane, greyscale while rendering, and the observation row (rl/csrc/nes_machine.cuh:133-155: lines 8..231,
+    // x 8..247) with the line's emphasis (patch:1637-1661). Clears the lane's part of the sprite line.
+    __device__ void compose(Rs& s, int32_t l, uint32_t w, uint8_t* obs, uint8_t* emph) {
+        const bool expanded = s.spork != 0, sprites = (s.mask & 0x10u) && expanded;
         if (sprites) s.spork = 0;
         const uint32_t keep = (s.mask & 0x01u) && rs_rendering(s) ? 0x30u : 0x3Fu;
-        if (l < 8) return;
-        uint32_t w = L->px[lane];
-        if (sprites) {
-            const uint32_t xstart = (s.mask & 0x04u) ? 0u : 8u;
-            uint32_t out = 0;
-            for (uint32_t q = 0; q < 4u; ++q) {
-                const uint32_t x = 4u * (uint32_t)lane + q;
-                uint32_t c = (w >> (8u * q)) & 0xFFu;
-                if (x >= xstart) {
-                    for (uint32_t n = 0; n < drawn_n; ++n) {
-                        const uint32_t e = L->spr[drawn][n];
-                        const uint32_t col = x - (e >> 24);
-                        if (col >= 8u) continue;
-                        const uint32_t attr = (e >> 16) & 0xFFu;
-                        const uint32_t b = (attr & 0x40u) ? col : 7u - col;
-                        const uint32_t val = ((e >> b) & 1u) | (((e >> (8u + b)) & 1u) << 1);
-                        if (val == 0) continue;
-                        if (!(attr & 0x20u) || (c & 0x40u)) c = L->spal[(attr & 3u) * 4u + val];
-                        break;
-                    }
+        if (expanded) {
+            const uint4 sp = reinterpret_cast<const uint4*>(L->sp)[lane];
+            reinterpret_cast<uint4*>(L->sp)[lane] = make_uint4(0u, 0u, 0u, 0u);
+            if (sprites) {
+                const uint32_t g[4] = {sp.x, sp.y, sp.z, sp.w};
+                const uint32_t xstart = (s.mask & 0x04u) ? 0u : 8u;
+                uint32_t out = 0;
+                for (uint32_t q = 0; q < 4u; ++q) {
+                    uint32_t c = (w >> (8u * q)) & 0xFFu;
+                    const uint32_t e = g[q];
+                    const bool show = e != 0u && 4u * (uint32_t)lane + q >= xstart && (!(e & 0x80u) || (c & 0x40u));
+                    c = show ? L->spal[e & 0x0Fu] : c;
+                    out |= c << (8u * q);
                 }
-                out |= c << (8u * q);
+                w = out;
             }
-            w = out;
         }
+        if (l < 8) return;
         w &= keep * 0x01010101u;
         const int32_t y = l - 8;
         if (lane >= 2 && lane < 62) reinterpret_cast<uint32_t*>(obs + y * RLE_OBS_W)[lane - 2] = w;
         if (lane == 0) emph[y] = (uint8_t)((s.mask >> 5) & 7u);
     }
+    // A line with no write from its lead-in to its end, no sprite-0 check and no MMC2 latches: one run of the 34 slots
+    // with the state as it is, FetchSpriteData, Fixit1/Fixit2 and RefreshSprites in closed form. The lanes fetch the
+    // line's tiles and the next line's sprites and expand this line's sprites together, sync once, and each composes
+    // its 4 pixels in registers (pixel x from slot x / 8 + 2, i.e. the fetches F[x / 8 + 2] and F[x / 8 + 3]).
+    __device__ void fast_line(Rs& s, int32_t l, uint8_t* obs, uint8_t* emph) {
+        const bool rend = rs_rendering(s);
+        uint64_t sel = 0;
+        if (rend) {
+            if (lane < 34) fetch_slot(s, v_steps(s.v, (uint32_t)lane), (uint32_t)lane, s.chr_lo, s.chr_hi);
+            sel = sprite_fetch_lanes(s, l);
+        }
+        expand_sprites(s);
+        __syncthreads();
+        const uint32_t back = this->back();
+        uint32_t w = back * 0x01010101u;
+        if (rend && (s.mask & 0x08u) && (lane >= 2 || (s.mask & 0x02u))) {
+            const uint32_t k = (uint32_t)lane / 2u + 2u;
+            w = shift4(L->f[k], L->f[k + 1u], ((uint32_t)lane & 1u) * 4u, s.fx, back);
+        }
+        compose(s, l, w, obs, emph);
+        // the end of the line: Fixit1 and Fixit2 (v from t horizontally), the next line's sprites, RefreshSprites
+        s.sphitx = kNoCheck;
+        if (rend) {
+            s.v = (y_step(s.v) & 0x7BE0u) | (s.t & 0x041Fu);
+            ha = 34u;
+            hb = 35u;
+            sprite_fetch_done(s, sel);
+        }
+        if (s.mask & 0x10u) {
+            s.spork = 0;
+            if (s.f_n != 0) {
+                latch_sprites(s);
+                if (s.f_blurp && !s.hit && s.f_bits) {
+                    uint32_t b = s.f_bits;
+                    if (s.f_attr & 0x40u) b = __builtin_bitreverse32(b) >> 24;
+                    s.sphitx = (int32_t)s.f_x;
+                    s.sphit_bits = b;
+                }
+                s.spork = 1;
+            }
+        }
+    }
 };
 
 // One console-frame per wavefront (blockDim 64): the picture of the frame the console has logged, drawn from its
 // nametables and OAM as of the frame's vblank stop.
-__global__ __launch_bounds__(64) void k_render(RenderArgs a) {
+__global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(8, 8))) void k_render(RenderArgs a) {
     __shared__ __align__(16) RenderLds L;
     const int count = slot_count(a.g, a.use_list, a.e0, a.e1);
     const int k = (int)blockIdx.x;
@@ -468,22 +540,25 @@ __global__ __launch_bounds__(64) void k_render(RenderArgs a) {
     const NesRec* rec = &a.g.recs[e];
     wave_copy16(L.nt, rec->nt, NES_NT_BYTES, lane);
     wave_copy16(L.oam, rec->oam, NES_OAM_BYTES, lane);
-    const uint32_t log_n = rec->log_n, ev_words = 2u * (log_n < NES_LOG_EVENTS ? log_n : NES_LOG_EVENTS);
-    for (uint32_t w = (uint32_t)lane; w < ev_words; w += 64u) L.ev[w] = rec->log[NES_LOG_HDR_WORDS + w];
     if (lane < 8) reinterpret_cast<uint32_t*>(L.pal)[lane] = rec->log[6 + lane];
     if (lane < 2) L.f[lane] = 0;
     if (lane < 16) L.spr[lane >> 3][lane & 7] = 0;
+    reinterpret_cast<uint4*>(L.sp)[lane] = make_uint4(0u, 0u, 0u, 0u);
     __syncthreads();
     const bool mmc2 = a.g.cart.board == NES_BOARD_MMC2;
+    RenderSink sink{&L, rec->log, a.g.cart.chr, rec->chr_ram, lane, mmc2, 0u, 1u, 0u, 0u, 0u};
     Rs s;
-    rs_load(s, rec->log, L.ev, log_n, mmc2 ? a.g.cart.chr_pages1 : 0u);
-    RenderSink sink{&L, a.g.cart.chr, rec->chr_ram, lane, mmc2, 0u, 1u, 0u, 0u, 0u};
+    rs_load(s, sink, rec->log, rec->log_n, mmc2 ? a.g.cart.chr_pages1 : 0u);
     rs_begin_frame(s, sink);
     uint8_t* obs = a.o.obs + ((size_t)ge * RLE_FRAMES + a.f) * RLE_OBS_PIXELS;
     uint8_t* emph = a.o.emph + ((size_t)ge * RLE_FRAMES + a.f) * RLE_OBS_H;
     for (int32_t l = 0; l < 232; ++l) {
+        if (!mmc2 && s.next >= (l + 1) * 341 - NES_LINE_LEAD && s.sphitx == kNoCheck) {
+            sink.fast_line(s, l, obs, emph);
+            continue;
+        }
         rs_line(s, sink, l, true);
-        sink.compose(s, l, obs, emph);
+        sink.compose(s, l, L.px[lane], obs, emph);
         rs_end_of_line(s, sink, l, true);
     }
 }
