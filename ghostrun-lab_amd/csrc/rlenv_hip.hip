@@ -22,6 +22,7 @@
 #include <cstdlib>
 #include <ctime>
 #include <cstring>
+#include <mutex>
 #include <stdexcept>
 #include <string>
 #include <vector>
@@ -950,6 +951,12 @@ __global__ __launch_bounds__(256) void k_rl10_run(Rl10RunArgs a) {
     a.state[e] = st;
 }
 
+// rlenv_step_static's restart queues, per GPU: the counts of up to kStaticGames games, then the queued env indices
+// of up to kStaticEnvs envs in all (each game's at its env offset). In host code the name stands for no device address:
+// the library takes the address once per device at rlenv_create (hipGetSymbolAddress) and uses only that.
+constexpr uint32_t kStaticGames = 64u, kStaticEnvs = 1u << 18;
+static __device__ __align__(256) uint32_t scratch[kStaticGames + kStaticEnvs];
+
 // ============================================================================================== host
 struct DevMem {
     std::vector<void*> blocks;
@@ -1046,8 +1053,24 @@ struct Env {
     uint32_t* optab = nullptr;
     uint32_t budget = NES_BUDGET;
     int lv_cap = 0;          // level starts / places per game (0 = off)
+    uint32_t* scratch = nullptr;   // this device's static restart-queue scratch (rlenv_step_static)
     mutable KernelClock clock;
 };
+
+// The address of `scratch` on each device, taken once with that device current.
+uint32_t* scratch_of(int device) {
+    static std::mutex lock;
+    static uint32_t* ptr[64] = {};
+    if (device < 0 || device >= 64) throw std::runtime_error("device index out of range");
+    std::lock_guard<std::mutex> hold(lock);
+    if (!ptr[device]) {
+        void* p = nullptr;
+        if (hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)) != hipSuccess || !p)
+            throw std::runtime_error("hipGetSymbolAddress(scratch) failed");
+        ptr[device] = static_cast<uint32_t*>(p);
+    }
+    return ptr[device];
+}
 
 // iNES -> cart description; the PRG is padded to a power of two by repeating a short image (NROM-128).
 struct Parsed {
@@ -1280,6 +1303,7 @@ void* rlenv_create(int ngames, const int* game_ids, const uint8_t* const* roms, 
         if (hipSetDevice(device) != hipSuccess) throw std::runtime_error("hipSetDevice failed");
         env = new Env();
         env->device = device;
+        env->scratch = scratch_of(device);
         if (const char* v = std::getenv("RLENV_BUDGET")) env->budget = (uint32_t)std::max(1, std::min((int)NES_BUDGET, std::atoi(v)));
         env->s.run_seed = run_seed;
         env->s.sticky = sticky;
@@ -1428,6 +1452,24 @@ int rlenv_step(void* h, void* stream) {
     const hipStream_t st = static_cast<hipStream_t>(stream);
     for (auto& gh : env.games) decision_phases(env, gh.k, env.o, 0, gh.k.n, st);
     return check("step");
+}
+
+int rlenv_step_static(void* h, void* stream) {
+    Env& env = *static_cast<Env*>(h);
+    if (env.games.size() > kStaticGames || (uint32_t)env.total > kStaticEnvs) {
+        g_error = "step_static: at most " + std::to_string(kStaticGames) + " games and " + std::to_string(kStaticEnvs) +
+                  " envs";
+        return 1;
+    }
+    const hipStream_t st = static_cast<hipStream_t>(stream);
+    for (size_t gi = 0; gi < env.games.size(); ++gi) {
+        GameK g = env.games[gi].k;
+        g.list = reinterpret_cast<int32_t*>(env.scratch + kStaticGames + g.offset);
+        g.list_count = env.scratch + gi;
+        hipLaunchKernelGGL(k_list_clear, dim3(1), dim3(1), 0, st, g.list_count);   // the last call's count
+        decision_phases(env, g, env.o, 0, g.n, st);
+    }
+    return check("step_static");
 }
 
 int rlenv_step_game(void* h, int gi, uint8_t* obs, uint8_t* emph, void* stream) {

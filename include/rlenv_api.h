@@ -123,6 +123,14 @@ int rl10_run(int game, const uint8_t* ram, int T, int N, const int32_t* frames, 
              uint32_t* keys, double* reward, uint8_t* done, uint32_t* events, int32_t* event_level, int32_t* deaths,
              uint8_t* end_reason, void* stream);
 
+/* rlenv_step with every game's restart queue (the indices of the envs whose episode ended this decision, and their
+ * count) in the library's static device scratch instead of the buffers rlenv_create allocated for it: the call
+ * allocates nothing (no hipMalloc, hipFree or allocating library routine). No counterpart in the reference: it is
+ * for callers that cannot allocate (code under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc). Limits: at most 64 games and 262,144 envs per env (larger envs are refused with an error). Every
+ * call on one GPU shares that GPU's scratch, so calls that overlap on one GPU (two streams, two envs) race. */
+int rlenv_step_static(void* h, void* stream);
+
 #ifdef __cplusplus
 }
 #endif
