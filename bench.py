@@ -139,9 +139,9 @@ def env_kwargs(w, args, cart):
 
 class Pack6Sink:
     """Where each decision's pictures go. 'device': packed 6 bits per pixel on the device (3/4 of the bytes) into a
-    staging buffer. 'host': the trainer's pinned-host store (rl.hostobs.HostObs, rl/train.py:174-294): the env draws
-    into two alternating device slots, each packed and copied into a ring of pinned host rows on a side stream while
-    the next decision runs."""
+    staging buffer. 'host': the pinned-host rollout store (rl.hostobs.RolloutStore; the trainer's store of
+    rl/train.py:174-294): the env draws into a ring of two device slots, each packed and copied into a ring of pinned
+    host rows on a copy stream while the next decision runs."""
 
     def __init__(self, env, mode, slots):
         import torch
@@ -149,25 +149,23 @@ class Pack6Sink:
         self.lib = env.lib
         self.t = 0
         if mode == 'host':
-            from rl.hostobs import HostObs
-            self.store = HostObs(env.lib, slots, env.n, env.device, 1, regions=1, nslots=2, pack6=True)
+            from rl.hostobs import RolloutStore
+            self.rows = slots
+            self.store = RolloutStore(env.lib, slots - 1, env.n, env.device, 1, regions=1, ring=2, pack6=True)
             self.emph = env.emph
         else:
             self.px = env.n * 4 * 224 * 240
-            self.lib.rl_pack6.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p]
             self.staging = torch.empty(self.px // 4 * 3, dtype=torch.uint8, device=env.device)
 
     def before(self):
         """Ahead of a decision: point the env's pictures at the ring slot it draws into."""
         if self.mode == 'host':
-            tt = self.t % self.store.T
-            self.store.before_write(tt - 1)
-            self.env.bind_obs(self.store.slot(0, tt), self.emph)
+            self.env.bind_obs(self.store.target(self.t), self.emph)
 
     def after(self):
         import torch
         if self.mode == 'host':
-            self.store.saved(0, self.t % self.store.T)
+            self.store.commit(0, self.t % self.rows)
         else:
             st = ctypes.c_void_p(torch.cuda.current_stream(self.env.device).cuda_stream)
             if self.lib.rl_pack6(ctypes.c_void_p(self.env.obs.data_ptr()), ctypes.c_void_p(self.staging.data_ptr()),
@@ -177,7 +175,7 @@ class Pack6Sink:
 
     def obs(self):
         """The pictures of the last decision."""
-        return self.store.slot(0, (self.t - 1) % self.store.T) if self.mode == 'host' else self.env.obs
+        return self.store.ring[(self.t - 1) % 2] if self.mode == 'host' else self.env.obs
 
     def close(self):
         if self.mode == 'host':

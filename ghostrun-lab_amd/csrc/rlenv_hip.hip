@@ -75,8 +75,7 @@ struct Settings {
 struct LevelK {
     int cap, levels;                 // cap 0: off
     NesRec* rec;                     // [cap]
-    Rl10State* st;                   // [cap]
-    Rl10Reader* rd;                  // [cap]
+    Rl10Saved* st;                   // [cap] tracker + reader per slot
     uint32_t* keys;                  // [cap * kcap]
     uint64_t* target;                // [cap]
     uint32_t* frame;                 // [cap]
@@ -615,8 +614,8 @@ __device__ __forceinline__ void reset_rl(const GameK& g, const EnvArrays& e, con
     if (lv >= 0) {
         e.target[ge] = L.target[lv];
         e.ep_frame[ge] = L.frame[lv];
-        e.st[ge] = L.st[lv];
-        e.rd[ge] = L.rd[lv];
+        e.st[ge] = L.st[lv].st;
+        e.rd[ge] = L.st[lv].rd;
     } else {
         const int k = idle <= s.idle_tmpl ? idle : 0;
         e.target[ge] = g.tmpl_target + (uint64_t)k * NES_FRAME_DOTS;
@@ -806,8 +805,8 @@ __global__ __launch_bounds__(256) void k_archive(FinishArgs a) {
     if (threadIdx.x == 0) {
         if (take) {
             const int ge = a.g.offset + e;
-            L.st[q] = a.e.st[ge];
-            L.rd[q] = a.e.rd[ge];
+            L.st[q].st = a.e.st[ge];
+            L.st[q].rd = a.e.rd[ge];
             L.target[q] = a.e.target[ge];
             L.frame[q] = a.e.ep_frame[ge];
             L.deaths[q] = (int32_t)(cl >> 32);
@@ -833,8 +832,8 @@ __global__ __launch_bounds__(256) void k_place_save(FinishArgs a, const int32_t*
         const int ge = a.g.offset + e;
         Rl10State st = a.e.st[ge];
         st.idle_frames = 0;
-        L.st[q] = st;
-        L.rd[q] = a.e.rd[ge];
+        L.st[q].st = st;
+        L.st[q].rd = a.e.rd[ge];
         L.target[q] = a.e.target[ge];
         L.frame[q] = a.e.ep_frame[ge];
         L.deaths[q] = 0;
@@ -1282,8 +1281,7 @@ void for_each_state(Env& env, F&& f) {
             const LevelK& L = gh.k.lv;
             const size_t C = (size_t)L.cap;
             f(L.rec, C * sizeof(NesRec));
-            f(L.st, C * sizeof(Rl10State));
-            f(L.rd, C * sizeof(Rl10Reader));
+            f(L.st, C * sizeof(Rl10Saved));
             f(L.keys, C * gh.k.kcap * 4u);
             f(L.target, C * 8); f(L.frame, C * 4); f(L.deaths, C * 4);
         }
@@ -1537,8 +1535,7 @@ int rlenv_enable_places(void* h, int cap, int levels) {
             L.cap = cap;
             L.levels = levels;
             L.rec = env.mem.zeros<NesRec>((size_t)cap);
-            L.st = env.mem.zeros<Rl10State>((size_t)cap);
-            L.rd = env.mem.zeros<Rl10Reader>((size_t)cap);
+            L.st = env.mem.zeros<Rl10Saved>((size_t)cap);
             L.keys = env.mem.zeros<uint32_t>((size_t)cap * gh.k.kcap + 1u);
             L.target = env.mem.zeros<uint64_t>((size_t)cap);
             L.frame = env.mem.zeros<uint32_t>((size_t)cap);
@@ -1614,8 +1611,7 @@ int rlenv_place_copy(void* h, int gi, const int32_t* src, const int32_t* dst, in
             bad |= hipMemcpyAsync(to, from, n, hipMemcpyDeviceToDevice, s) != hipSuccess;
         };
         d2d(L.rec + b, L.rec + a, sizeof(NesRec));
-        d2d(L.st + b, L.st + a, sizeof(Rl10State));
-        d2d(L.rd + b, L.rd + a, sizeof(Rl10Reader));
+        d2d(L.st + b, L.st + a, sizeof(Rl10Saved));
         if (g.kcap) d2d(L.keys + b * g.kcap, L.keys + a * g.kcap, (size_t)g.kcap * 4u);
         d2d(L.target + b, L.target + a, 8);
         d2d(L.frame + b, L.frame + a, 4);
@@ -1630,7 +1626,7 @@ void rlenv_level_layout(void* h, int gi, uint32_t* out) {
     const LevelK& L = env.games[gi].k.lv;
     out[0] = (uint32_t)sizeof(NesRec);
     out[1] = env.games[gi].k.kcap;   // key words per env (the game's key set)
-    out[2] = (uint32_t)sizeof(Rl10State);
+    out[2] = (uint32_t)sizeof(Rl10Saved);   // tracker + reader per slot
     out[3] = (uint32_t)L.cap;
     out[4] = (uint32_t)L.levels;
 }

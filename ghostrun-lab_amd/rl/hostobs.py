@@ -1,19 +1,25 @@
-"""Rollout pictures in pinned host memory: the consumer of the environment's pictures in the reference trainer
-(rl/train.py:174-294, class HostObs), over this library's entry points.
+"""`RolloutStore`: a rollout's pictures in pinned host memory, the consumer of the env's pictures in a training loop
+(the role of the reference trainer's host store, rl/train.py:174-294), over this library's pack6 / memcpy / gather
+entry points (include/rlenv_api.h).
 
-A rollout of T decisions of N envs does not fit next to the learner in HBM at the reference's sizes, so the pictures
-go to pinned host memory and come back per minibatch:
+At the reference's sizes the pictures of a T-decision rollout of N envs do not fit beside a learner in HBM, so they
+live in host memory and come back one minibatch at a time. The design:
 
-  * the env draws decision t into device slot t % nslots (`slot`, bound with RlEnv.bind_obs);
-  * `saved(r, t)` packs the slot 6 bits per pixel on the device (pack6, 3/4 of the bytes) and copies it into row t of
-    host region r on a side stream, so the copy overlaps the next decision;
-  * `before_write(t)` makes the env wait until the slot it draws next has been copied out;
-  * `epoch(r, perm, mb)` / `batch(i)` / `done_with(i)` hand the learner whole T-row sequences of mb envs: a 2-D copy per
-    env (rl_gather_envs, the copy engines) into one of two device buffers, unpacked (rl_unpack6) on a gather stream,
-    one minibatch ahead of the learner.
+  * Host memory: `regions` blocks of (T + 1) rows x N envs x row_bytes (row 0 of a region is the observation the
+    rollout starts from). With pack6 a row is 6 bits per pixel (3/4 of the bytes).
+  * Device ring: `ring` picture tensors that the env draws into in turn (decision t into `target(t)`), each with its
+    own packed staging buffer and a `drained` event: the ring slot is free again once its copy to the host is done.
+    `target(t)` makes torch's current stream wait for that before it hands the slot out, so the env never
+    overwrites pictures that are still being copied, and the host never blocks.
+  * `commit(region, t)` packs the slot on the current stream (right behind the env's decision), then copies it to
+    host row t of the region on a copy stream, so the copy overlaps the next decision.
+  * `minibatches(region, perm, mb)` yields the learner [T * mb, 4, 224, 240] device tensors (row t * mb + j =
+    decision t of env perm[i * mb + j]): a strided host-to-device copy per env (rl_gather_envs) into one of two
+    device buffers, unpacked there, on a gather stream that runs one minibatch ahead; a buffer is reused once the
+    caller has asked for the minibatch after the one it held. The gather stream first waits for the copy stream, so
+    the rollout's copies are complete without a host synchronisation.
 
-Streams are torch streams at the default priority; ordering is by torch events only (no host synchronisation
-except where the docstrings say so). Region r holds T + 1 rows: row 0 is the observation the rollout starts from.
+Every stream is a torch stream at the default priority; ordering is by torch events only.
 """
 from __future__ import annotations
 
@@ -23,137 +29,118 @@ import numpy as np
 import torch
 
 FRAME_BYTES = 4 * 224 * 240
+PACKED_BYTES = FRAME_BYTES * 3 // 4
 
 
-class HostObs:
-    def __init__(self, lib, T, N, dev, mb, regions, nslots=2, pack6=False):
-        if nslots not in (1, 2) or T % nslots:
-            raise ValueError('nslots must be 1 or 2 and divide T (the next rollout starts in slot 0)')
-        self.lib, self.T, self.N, self.dev, self.nslots = lib, int(T), int(N), torch.device(dev), int(nslots)
+def _vp(x):
+    return ctypes.c_void_p(x if isinstance(x, int) else x.data_ptr())
+
+
+class RolloutStore:
+    def __init__(self, lib, decisions, envs, device, minibatch_envs, regions=1, ring=2, pack6=True):
+        """lib: the env's library (RlEnv.lib). decisions: T, rows per region after the start row. envs: N.
+        minibatch_envs: the largest minibatch `minibatches` will be asked for."""
+        self.lib, self.T, self.N = lib, int(decisions), int(envs)
+        self.dev = torch.device(device)
         self.pack6 = bool(pack6)
-        self.row_bytes = FRAME_BYTES * 3 // 4 if self.pack6 else FRAME_BYTES
+        self.row_bytes = PACKED_BYTES if self.pack6 else FRAME_BYTES
         self.region_bytes = (self.T + 1) * self.N * self.row_bytes
-        self.ptr = lib.rl_host_alloc(self.region_bytes * int(regions))
-        if not self.ptr:
-            raise RuntimeError(f'pinned host allocation of {self.region_bytes * regions / 2 ** 30:.2f} GiB failed: '
-                               f'{lib.rlenv_error().decode()}')
-        self.slots = [torch.zeros(N, 4, 224, 240, dtype=torch.uint8, device=self.dev) for _ in range(self.nslots)]
-        self.packed = torch.empty(N, self.row_bytes, dtype=torch.uint8, device=self.dev) if self.pack6 else None
-        self.d2h = torch.cuda.Stream(self.dev)
-        self.gather = torch.cuda.Stream(self.dev)
-        self.copied = [torch.cuda.Event() for _ in range(2)]     # slot k's last copy-out has finished
-        self.mbuf = [torch.empty(self.T * mb, 4, 224, 240, dtype=torch.uint8, device=self.dev) for _ in range(2)]
-        self.pmbuf = ([torch.empty(self.T * mb, self.row_bytes, dtype=torch.uint8, device=self.dev) for _ in range(2)]
-                      if self.pack6 else self.mbuf)
-        self.mb_cap = int(mb)
-        self.fetched = [torch.cuda.Event() for _ in range(2)]    # minibatch buffer k is filled
-        self.used = [torch.cuda.Event() for _ in range(2)]       # the learner is done with minibatch buffer k
-        self.d2h_g, self.copied_g = [], []
-
-    def close(self):
-        if getattr(self, 'ptr', None):
-            torch.cuda.synchronize(self.dev)
-            self.lib.rl_host_free(ctypes.c_void_p(self.ptr))
-            self.ptr = None
-
-    def __del__(self):
-        self.close()
+        self.regions = int(regions)
+        self.base = lib.rl_host_alloc(self.region_bytes * self.regions)
+        if not self.base:
+            raise RuntimeError(f'pinned host allocation of {self.region_bytes * self.regions / 2 ** 30:.2f} GiB '
+                               f'failed: {lib.rlenv_error().decode()}')
+        new = lambda *shape: torch.empty(shape, dtype=torch.uint8, device=self.dev)  # noqa: E731
+        self.ring = [new(self.N, 4, 224, 240).zero_() for _ in range(int(ring))]
+        self.staging = [new(self.N, self.row_bytes) for _ in self.ring] if self.pack6 else None
+        self.drained = [torch.cuda.Event() for _ in self.ring]
+        self.copy_stream = torch.cuda.Stream(self.dev)
+        self.gather_stream = torch.cuda.Stream(self.dev)
+        self.mb_cap = int(minibatch_envs)
+        self.batches = [new(self.T * self.mb_cap, 4, 224, 240) for _ in range(2)]
+        self.packed_batches = [new(self.T * self.mb_cap, self.row_bytes) for _ in range(2)] if self.pack6 else None
+        self.ready = [torch.cuda.Event() for _ in range(2)]
+        self.released = [torch.cuda.Event() for _ in range(2)]
 
     def _check(self, rc):
         if rc != 0:
             raise RuntimeError(self.lib.rlenv_error().decode())
 
-    def host_row(self, r, t):
-        """Address of row t of region r (N rows of row_bytes)."""
-        return self.ptr + r * self.region_bytes + t * self.N * self.row_bytes
+    def row_address(self, region, t):
+        """Host address of row t of a region (N consecutive env rows of row_bytes)."""
+        if not (0 <= region < self.regions and 0 <= t <= self.T):
+            raise IndexError(f'row {t} of region {region}')
+        return self.base + region * self.region_bytes + t * self.N * self.row_bytes
 
-    def slot(self, r, t):
-        return self.slots[t % self.nslots]
+    # ----------------------------------------------------------------- rollout side
+    def target(self, t):
+        """The ring slot decision t is drawn into (bind it with RlEnv.bind_obs), free once torch's current stream
+        reaches this point: the stream waits for the slot's last copy to the host."""
+        k = t % len(self.ring)
+        torch.cuda.current_stream(self.dev).wait_event(self.drained[k])
+        return self.ring[k]
 
-    def before_write(self, t):
-        """The env is about to draw decision t + 1 into its slot: that slot's previous copy-out must have finished."""
-        torch.cuda.current_stream(self.dev).wait_event(self.copied[(t + 1) % self.nslots])
-
-    def _copy_out(self, src, dst, nbytes, stream, done_event):
+    def commit(self, region, t, rows=None):
+        """Decision t is in its ring slot: pack it (pack6) on the current stream and copy it, or the env rows
+        `rows` (a slice) of it, to host row t of the region on the copy stream."""
+        k = t % len(self.ring)
+        rows = rows or slice(0, self.N)
         current = torch.cuda.current_stream(self.dev)
-        stream.wait_stream(current)
-        self._check(self.lib.rl_memcpy_async(ctypes.c_void_p(dst), ctypes.c_void_p(src.data_ptr()), nbytes,
-                                             ctypes.c_void_p(stream.cuda_stream)))
-        done_event.record(stream)
-
-    def saved(self, r, t):
-        """Slot t % nslots holds decision t: copy it (packed when pack6) into row t of region r."""
-        current = torch.cuda.current_stream(self.dev)
-        src = self.slots[t % self.nslots]
+        src = self.ring[k][rows]
         if self.pack6:
-            current.wait_event(self.copied[(t - 1) % self.nslots])   # one packed staging row: its last copy is out
-            self._check(self.lib.rl_pack6(ctypes.c_void_p(src.data_ptr()), ctypes.c_void_p(self.packed.data_ptr()),
-                                          self.N * FRAME_BYTES, ctypes.c_void_p(current.cuda_stream)))
-            src = self.packed
-        self._copy_out(src, self.host_row(r, t), self.N * self.row_bytes, self.d2h, self.copied[t % self.nslots])
+            dst = self.staging[k][rows]
+            self._check(self.lib.rl_pack6(_vp(src), _vp(dst), src.numel(), _vp(current.cuda_stream)))
+            src = dst
+        self.copy_stream.wait_stream(current)
+        self._check(self.lib.rl_memcpy_async(_vp(self.row_address(region, t) + rows.start * self.row_bytes),
+                                             _vp(src), src.numel(),
+                                             _vp(self.copy_stream.cuda_stream)))
+        self.drained[k].record(self.copy_stream)
 
-    def handoff(self, src, dst):
-        """Decision T sits in device slot T % nslots == 0, where the next rollout starts: nothing to move."""
+    # ----------------------------------------------------------------- learner side
+    def minibatches(self, region, perm, mb):
+        """Iterate over the region's decisions 0..T-1 in minibatches of mb envs taken in the order of perm (env
+        indices); each item is ready on torch's current stream when it is returned."""
+        envs = np.ascontiguousarray(torch.as_tensor(perm).cpu().numpy(), dtype=np.int64)
+        if envs.size and (envs.min() < 0 or envs.max() >= self.N):
+            raise ValueError('minibatches: env index out of range')
+        if not 0 < mb <= self.mb_cap:
+            raise ValueError(f'minibatches: {mb} envs per minibatch, the buffers hold {self.mb_cap}')
+        count = len(envs) // mb
+        src = self.row_address(region, 0)
+        self.gather_stream.wait_stream(self.copy_stream)
+        self.gather_stream.wait_stream(torch.cuda.current_stream(self.dev))
 
-    def _game_streams(self, gi):
-        while len(self.d2h_g) <= gi:
-            self.d2h_g.append(torch.cuda.Stream(self.dev))
-            self.copied_g.append([torch.cuda.Event(), torch.cuda.Event()])
-        return self.d2h_g[gi], self.copied_g[gi]
+        def fetch(i):
+            k = i % 2
+            self.gather_stream.wait_event(self.released[k])
+            chunk = envs[i * mb:(i + 1) * mb]
+            staged = self.packed_batches[k] if self.pack6 else self.batches[k]
+            self._check(self.lib.rl_gather_envs(_vp(staged), _vp(src), chunk.ctypes.data_as(ctypes.c_void_p), mb,
+                                                self.T, self.N, self.row_bytes, _vp(self.gather_stream.cuda_stream)))
+            if self.pack6:
+                self._check(self.lib.rl_unpack6(_vp(staged), _vp(self.batches[k]), self.T * mb * FRAME_BYTES,
+                                                _vp(self.gather_stream.cuda_stream)))
+            self.ready[k].record(self.gather_stream)
 
-    def before_write_game(self, gi, t):
-        torch.cuda.current_stream(self.dev).wait_event(self._game_streams(gi)[1][(t + 1) % self.nslots])
+        return self._iterate(count, mb, fetch)
 
-    def saved_game(self, r, t, gi, rows):
-        """Like saved, for the env rows `rows` (a slice) of game gi, on that game's own copy stream."""
-        stream, events = self._game_streams(gi)
-        current = torch.cuda.current_stream(self.dev)
-        src = self.slots[t % self.nslots][rows]
-        if self.pack6:
-            current.wait_event(events[(t - 1) % self.nslots])
-            packed = self.packed[rows]
-            self._check(self.lib.rl_pack6(ctypes.c_void_p(src.data_ptr()), ctypes.c_void_p(packed.data_ptr()),
-                                          src.numel(), ctypes.c_void_p(current.cuda_stream)))
-            src = packed
-        self._copy_out(src, self.host_row(r, t) + rows.start * self.row_bytes, (rows.stop - rows.start) * self.row_bytes,
-                       stream, events[t % self.nslots])
+    def _iterate(self, count, mb, fetch):
+        if count:
+            fetch(0)
+        for i in range(count):
+            if i + 1 < count:
+                fetch(i + 1)
+            current = torch.cuda.current_stream(self.dev)
+            current.wait_event(self.ready[i % 2])
+            yield self.batches[i % 2][:self.T * mb]
+            self.released[i % 2].record(torch.cuda.current_stream(self.dev))
 
-    def epoch(self, r, perm, mb):
-        """This epoch's minibatches: whole T-row sequences of mb envs of region r, in the order of perm (env
-        indices); starts fetching the first. Every copy-out of region r must have finished (the caller synchronises
-        between rollout and learning)."""
-        self.base = self.host_row(r, 0)
-        self.perm_host = np.ascontiguousarray(torch.as_tensor(perm).cpu().numpy().astype(np.int64))
-        if self.perm_host.size and (self.perm_host.min() < 0 or self.perm_host.max() >= self.N):
-            raise ValueError('epoch: env index out of range')
-        self.mb = int(mb)
-        if not 0 < self.mb <= self.mb_cap:
-            raise ValueError(f'epoch: minibatch of {mb} envs, the buffers hold {self.mb_cap}')
-        self.nmb = len(self.perm_host) // self.mb
-        self.gather.wait_stream(torch.cuda.current_stream(self.dev))
-        if self.nmb:
-            self._fetch(0)
+    def close(self):
+        if getattr(self, 'base', None):
+            torch.cuda.synchronize(self.dev)
+            self.lib.rl_host_free(ctypes.c_void_p(self.base))
+            self.base = None
 
-    def _fetch(self, i):
-        k = i % 2
-        self.gather.wait_event(self.used[k])
-        envs = self.perm_host[i * self.mb:(i + 1) * self.mb]
-        self._check(self.lib.rl_gather_envs(ctypes.c_void_p(self.pmbuf[k].data_ptr()), ctypes.c_void_p(self.base),
-                                            envs.ctypes.data_as(ctypes.c_void_p), self.mb, self.T, self.N,
-                                            self.row_bytes, ctypes.c_void_p(self.gather.cuda_stream)))
-        if self.pack6:
-            self._check(self.lib.rl_unpack6(ctypes.c_void_p(self.pmbuf[k].data_ptr()),
-                                            ctypes.c_void_p(self.mbuf[k].data_ptr()), self.T * self.mb * FRAME_BYTES,
-                                            ctypes.c_void_p(self.gather.cuda_stream)))
-        self.fetched[k].record(self.gather)
-
-    def batch(self, i):
-        """Minibatch i as [T * mb, 4, 224, 240] uint8 (row t * mb + j = decision t of env perm[i * mb + j]), ready on
-        the current stream; the next one is fetched meanwhile."""
-        if i + 1 < self.nmb:
-            self._fetch(i + 1)
-        torch.cuda.current_stream(self.dev).wait_event(self.fetched[i % 2])
-        return self.mbuf[i % 2]
-
-    def done_with(self, i):
-        self.used[i % 2].record(torch.cuda.current_stream(self.dev))
+    def __del__(self):
+        self.close()

@@ -36,6 +36,14 @@ typedef struct Rl10Reader {
     double key_d, dist, best_arc, drive_start, drive_best;
 } Rl10Reader;                     /* 120 bytes */
 
+/* One archive slot's tracker state: the tracker and its game reader, saved, restored and copied together. It is the
+ * per-slot block whose size rlenv_level_layout reports (the sizeof(rl10::EnvState) of rl/csrc/rlenv_build.hpp:275),
+ * so a state blob's archive tail has the reference's six parts per game. */
+typedef struct Rl10Saved {
+    Rl10State st;
+    Rl10Reader rd;
+} Rl10Saved;                      /* 200 bytes */
+
 #define RLC_RING 64
 typedef struct Dropout {
     uint64_t seed, counter;       /* the schedule's own generator */

@@ -375,8 +375,7 @@ typedef struct Game {
      * the level event; slots lv_levels..lv_cap-1 are places, saved on request. One saved console is a whole record. */
     int lv_cap, lv_levels;
     NesRec* lv_rec;           /* [lv_cap] */
-    Rl10State* lv_st;         /* [lv_cap] */
-    Rl10Reader* lv_rd;        /* [lv_cap] */
+    Rl10Saved* lv_st;         /* [lv_cap] tracker + reader per slot */
     uint32_t* lv_keys;        /* [lv_cap * kcap] */
     uint64_t* lv_target;      /* [lv_cap] */
     uint32_t* lv_frame;       /* [lv_cap] */
@@ -487,8 +486,8 @@ static void reset_state(Env* E, Game* g, int e) {
     if (lv >= 0) {
         E->target[ge] = g->lv_target[lv];
         E->ep_frame[ge] = g->lv_frame[lv];
-        E->st[ge] = g->lv_st[lv];
-        E->rd[ge] = g->lv_rd[lv];
+        E->st[ge] = g->lv_st[lv].st;
+        E->rd[ge] = g->lv_st[lv].rd;
         memcpy(keys, g->lv_keys + (size_t)lv * g->kcap, (size_t)g->kcap * 4u);
     } else {
         E->target[ge] = g->tmpl_target + (uint64_t)k * NES_FRAME_DOTS;
@@ -646,7 +645,7 @@ static void env_free(Env* E) {
         free(E->games[i].idle);
         free(E->games[i].lv_rec); free(E->games[i].lv_st); free(E->games[i].lv_target); free(E->games[i].lv_frame);
         free(E->games[i].lv_deaths); free(E->games[i].lv_claim); free(E->games[i].lv_cdf);
-        free(E->games[i].lv_rd); free(E->games[i].lv_keys); free(E->games[i].keys);
+        free(E->games[i].lv_keys); free(E->games[i].keys);
     }
     free(E->games);
     free(E->st); free(E->rd); free(E->drop); free(E->target); free(E->sticky_seed); free(E->sticky_ctr);
@@ -790,8 +789,8 @@ static void level_saves(Env* E, Game* g) {
         if (take) {
             const int e = (int)(cl & 0xFFFFFFFFull), ge = g->offset + e;
             g->lv_rec[s] = g->recs[e];
-            g->lv_st[s] = E->st[ge];
-            g->lv_rd[s] = E->rd[ge];
+            g->lv_st[s].st = E->st[ge];
+            g->lv_st[s].rd = E->rd[ge];
             memcpy(g->lv_keys + (size_t)s * g->kcap, g->keys + (size_t)e * g->kcap, (size_t)g->kcap * 4u);
             g->lv_target[s] = E->target[ge];
             g->lv_frame[s] = E->ep_frame[ge];
@@ -864,8 +863,7 @@ int rlenv_enable_places(void* h, int cap, int levels) {
         g->lv_cap = cap;
         g->lv_levels = levels;
         g->lv_rec = (NesRec*)xcalloc((size_t)cap, sizeof(NesRec));
-        g->lv_st = (Rl10State*)xcalloc((size_t)cap, sizeof(Rl10State));
-        g->lv_rd = (Rl10Reader*)xcalloc((size_t)cap, sizeof(Rl10Reader));
+        g->lv_st = (Rl10Saved*)xcalloc((size_t)cap, sizeof(Rl10Saved));
         g->lv_keys = (uint32_t*)xcalloc((size_t)cap * g->kcap + 1u, 4);
         g->lv_target = (uint64_t*)xcalloc((size_t)cap, 8);
         g->lv_frame = (uint32_t*)xcalloc((size_t)cap, 4);
@@ -909,9 +907,9 @@ int rlenv_place_save(void* h, int gi, const int32_t* env_idx, const int32_t* slo
         if (s < g->lv_levels || s >= g->lv_cap || e < 0 || e >= g->n) continue;
         const int ge = g->offset + e;
         g->lv_rec[s] = g->recs[e];
-        g->lv_st[s] = E->st[ge];
-        g->lv_st[s].idle_frames = 0;   /* the no-progress clock restarts at a place (rlenv_core.cuh:366-375) */
-        g->lv_rd[s] = E->rd[ge];
+        g->lv_st[s].st = E->st[ge];
+        g->lv_st[s].st.idle_frames = 0;   /* the no-progress clock restarts at a place (rlenv_core.cuh:366-375) */
+        g->lv_st[s].rd = E->rd[ge];
         memcpy(g->lv_keys + (size_t)s * g->kcap, g->keys + (size_t)e * g->kcap, (size_t)g->kcap * 4u);
         g->lv_target[s] = E->target[ge];
         g->lv_frame[s] = E->ep_frame[ge];
@@ -930,7 +928,6 @@ int rlenv_place_copy(void* h, int gi, const int32_t* src, const int32_t* dst, in
         const int a = src[j], b = dst[j];
         g->lv_rec[b] = g->lv_rec[a];
         g->lv_st[b] = g->lv_st[a];
-        g->lv_rd[b] = g->lv_rd[a];
         memmove(g->lv_keys + (size_t)b * g->kcap, g->lv_keys + (size_t)a * g->kcap, (size_t)g->kcap * 4u);
         g->lv_target[b] = g->lv_target[a];
         g->lv_frame[b] = g->lv_frame[a];
@@ -943,7 +940,7 @@ void rlenv_level_layout(void* h, int gi, uint32_t* out) {
     const Game* g = &((Env*)h)->games[gi];
     out[0] = (uint32_t)sizeof(NesRec);
     out[1] = g->kcap;
-    out[2] = (uint32_t)sizeof(Rl10State);
+    out[2] = (uint32_t)sizeof(Rl10Saved);   /* tracker + reader per slot */
     out[3] = (uint32_t)g->lv_cap;
     out[4] = (uint32_t)g->lv_levels;
 }
@@ -971,8 +968,7 @@ static void for_each_state(Env* E, visit_fn f, void* ctx) {
             Game* g = &E->games[i];
             const size_t L = (size_t)g->lv_cap;
             f(g->lv_rec, L * sizeof(NesRec), ctx);
-            f(g->lv_st, L * sizeof(Rl10State), ctx);
-            f(g->lv_rd, L * sizeof(Rl10Reader), ctx);
+            f(g->lv_st, L * sizeof(Rl10Saved), ctx);
             f(g->lv_keys, L * g->kcap * 4u, ctx);
             f(g->lv_target, L * 8, ctx); f(g->lv_frame, L * 4, ctx); f(g->lv_deaths, L * 4, ctx);
         }

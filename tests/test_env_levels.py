@@ -18,7 +18,7 @@ import torch
 
 from helpers import ORACLE_LIB, Console, ptr
 from rl import synth
-from rl.rlenv import READER_BYTES, RlEnv
+from rl.rlenv import RlEnv
 
 RIGHT, LEFT, DOWN, A = 128, 64, 32, 1
 REC = 23552
@@ -32,22 +32,27 @@ def env(n, **kw):
                  sticky=False, idle_max=0, dropout=False, pad_mode=True, **kw)
 
 
+def tail_sizes(lay, cap):
+    """The reference's six archive parts of one game for `cap` slots (rl/rlenv.py:293-310 _grow_archive,
+    rl/csrc/rlenv_build.hpp:274-278): consoles, tracker blocks, key words, targets, frames, deaths."""
+    return [cap * lay['stride'], cap * lay['st'], cap * lay['key_cap'] * 4, cap * 8, cap * 4, cap * 4]
+
+
 def archive(e, gi=0):
-    """The level-start tail of the state blob: (records [cap, REC], tracker bytes [cap, 80], targets, frames,
-    deaths), parsed with the library's own layout (rl/csrc/rlenv_build.hpp:269-279 order, with the reader states
-    after the trackers)."""
-    lay = e.level_layout(gi)
-    cap = lay['cap']
-    sizes = [cap * lay['stride'], cap * lay['st'], cap * READER_BYTES, cap * lay['key_cap'] * 4, cap * 8, cap * 4,
-             cap * 4]
+    """Game gi's part of the level-start tail of the state blob: (records [cap, REC], tracker blocks [cap, st] =
+    Rl10State then Rl10Reader, targets, frames, deaths), parsed with the reference's six-part layout."""
+    lays = [e.level_layout(g) for g in range(len(e.games))]
     blob = e.state_dict()['env']
-    tail = blob[len(blob) - sum(sizes):]
-    parts, o = [], 0
-    for s in sizes:
-        parts.append(tail[o:o + s])
-        o += s
+    o = len(blob) - sum(sum(tail_sizes(l, l['cap'])) for l in lays)
+    for g in range(gi):
+        o += sum(tail_sizes(lays[g], lays[g]['cap']))
+    lay, cap = lays[gi], lays[gi]['cap']
+    parts = []
+    for s_ in tail_sizes(lay, cap):
+        parts.append(blob[o:o + s_])
+        o += s_
     return (parts[0].reshape(cap, lay['stride']), parts[1].reshape(cap, lay['st']),
-            parts[4].view(np.uint64), parts[5].view(np.uint32), parts[6].view(np.int32))
+            parts[3].view(np.uint64), parts[4].view(np.uint32), parts[5].view(np.int32))
 
 
 def drive(e, pads_of, steps):
@@ -63,7 +68,7 @@ def force_end(e, on=True):
 
 def test_layout_enable_errors_and_empty_archive():
     e = env(4, level_cap=6, level_slots=2)
-    assert e.level_layout(0) == dict(stride=REC, key_cap=0, st=80, cap=6, levels=2)
+    assert e.level_layout(0) == dict(stride=REC, key_cap=0, st=80 + 120, cap=6, levels=2)   # tracker + reader
     assert e.saved_levels() == {'smb': {}}
     assert e.lib.rlenv_enable_places(e.h, 4, 4) != 0 and b'once' in e.lib.rlenv_error()
     f = RlEnv({'smb': 2}, device='cpu', lib_path=ORACLE_LIB, roms={'smb': synth.smb_like_cart(1)})
@@ -243,3 +248,50 @@ def test_archive_resumes_exactly_and_grows():
     d = env(3)
     d.load_state_dict(d0.state_dict())
     assert (archive(d)[4] == -1).all()
+
+
+def reference_grow(buf, lays, old_cap, new_cap):
+    """The reference's archive growth (rl/rlenv.py:293-310), restated: the blob's prefix, then per game each of the
+    six parts with its old slots followed by the new empty ones (zeros; deaths 0xFF bytes = -1)."""
+    old_tail = sum(sum(tail_sizes(l, old_cap)) for l in lays)
+    out, o = [buf[:len(buf) - old_tail]], len(buf) - old_tail
+    for l in lays:
+        for k, (a, b) in enumerate(zip(tail_sizes(l, old_cap), tail_sizes(l, new_cap))):
+            out += [buf[o:o + a], np.full(b - a, 0xFF if k == 5 else 0, np.uint8)]
+            o += a
+    return np.concatenate(out)
+
+
+def test_reference_formula_grows_a_two_game_archive():
+    """A blob saved with 2 slots per game, on an SMB env and a Castlevania env (a 4,096-word key set per env and
+    slot), grown to 4 slots by the reference's own six-part formula: RlEnv's growth gives the same bytes, the
+    grown blob loads, the saved slots keep their contents, and the resumed env steps exactly as the saved one."""
+    roms = {'smb': synth.smb_like_cart(1), 'castlevania': synth.nrom_cart(2)}
+    mk = lambda cap: RlEnv({'smb': 2, 'castlevania': 2}, device='cpu', lib_path=ORACLE_LIB, roms=roms, seed=5,  # noqa
+                           sticky=False, idle_max=0, dropout=False, pad_mode=True, level_cap=cap)
+    a = mk(2)
+    a.start()
+    drive(a, lambda t: [RIGHT, RIGHT | A, RIGHT, 0], 95)
+    assert 1 in a.saved_levels()['smb']
+    sd = a.state_dict()
+    lays = [a.level_layout(g) for g in range(2)]
+    assert lays[1]['key_cap'] == 4096 and lays[0]['st'] == lays[1]['st'] == 200
+    grown = reference_grow(sd['env'], lays, 2, 4)
+    b = mk(4)
+    assert len(grown) == b.lib.rlenv_state_bytes(b.h)
+    assert np.array_equal(b._grow_archive(sd['env'], 2, len(grown)), grown)
+    b.load_state_dict(sd)
+    assert np.array_equal(b.state_dict()['env'], grown)
+    for gi in range(2):
+        ra, rb = archive(a, gi), archive(b, gi)
+        for x, y in zip(ra, rb):
+            assert np.array_equal(y[:2], x)
+        assert list(rb[4][2:]) == [-1, -1] and not rb[0][2:].any()
+    g = torch.Generator().manual_seed(4)
+    for t in range(10):
+        act = torch.randint(0, 256, (4,), generator=g, dtype=torch.int16)
+        for x in (a, b):
+            x.actions.copy_(act)
+            x.step()
+        for k in ('obs', 'reward', 'done', 'masks', 'level_now'):
+            assert torch.equal(getattr(a, k), getattr(b, k)), (t, k)

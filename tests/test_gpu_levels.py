@@ -105,3 +105,44 @@ def test_places_weighted_plan():
     run_pair(cpu, gpu, 22, 24, g)
     assert set(cpu.start_level.numpy()[cpu.done.numpy() == 1]) <= {-1, 2, 3, 4}
     assert np.array_equal(cpu.state_dict()['env'], gpu.state_dict()['env'])
+
+
+@pytest.mark.gpu
+def test_grown_archive_resumes_on_both_builds():
+    """A HIP blob saved with 2 archive slots per game (SMB-like and a Castlevania env with its key sets), grown to 4
+    by the reference's six-part formula (rl/rlenv.py:293-310), loads into a HIP env and an oracle env of 4 slots;
+    both then step bit-exactly alike, with level starts drawn from the grown archive."""
+    from test_env_levels import reference_grow
+    print('case: smb 3 + castlevania 2 envs, archive 2 -> 4 slots, 95 + 12 decisions', flush=True)
+    roms = {'smb': synth.smb_like_cart(1), 'castlevania': synth.nrom_cart(2)}
+    kw = dict(roms=roms, seed=6, sticky=False, idle_max=0, dropout=False, pad_mode=True, ram_hash=True)
+    a = RlEnv({'smb': 3, 'castlevania': 2}, device='cuda', lib_path=HIP_LIB, level_cap=2, **kw)
+    a.start()
+    for t in range(95):
+        a.actions.copy_(torch.tensor([RIGHT, RIGHT | A, RIGHT, 0, RIGHT], dtype=torch.int16, device='cuda'))
+        a.step()
+    assert 1 in a.saved_levels()['smb']
+    sd = a.state_dict()
+    lays = [a.level_layout(g) for g in range(2)]
+    cpu = RlEnv({'smb': 3, 'castlevania': 2}, device='cpu', lib_path=ORACLE_LIB, level_cap=4, **kw)
+    gpu = RlEnv({'smb': 3, 'castlevania': 2}, device='cuda', lib_path=HIP_LIB, level_cap=4, **kw)
+    grown = reference_grow(sd['env'], lays, 2, 4)
+    for x in (cpu, gpu):
+        x.load_state_dict(dict(sd, env=grown, level_cap=4))
+        x.set_level_prob(0.5)
+        set_end(x, 1 / 3)
+    assert np.array_equal(cpu.state_dict()['env'], gpu.state_dict()['env'])
+    g = torch.Generator().manual_seed(7)
+    starts = 0
+    for t in range(12):
+        act = torch.randint(0, 256, (5,), generator=g, dtype=torch.int16)
+        cpu.actions.copy_(act)
+        gpu.actions.copy_(act.cuda())
+        cpu.step()
+        gpu.step()
+        torch.cuda.synchronize()
+        for k in OUTS + ('start_level', 'level_now'):
+            assert np.array_equal(getattr(cpu, k).numpy(), getattr(gpu, k).cpu().numpy()), (t, k)
+        starts += int(((cpu.start_level >= 0) & (cpu.done > 0)).sum())
+    assert starts > 0
+    assert np.array_equal(cpu.state_dict()['env'], gpu.state_dict()['env'])

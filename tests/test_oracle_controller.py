@@ -150,3 +150,37 @@ def test_seeds_and_disable():
     assert np.array_equal(a, b) and not np.array_equal(a, c)
     off, tl = schedule(99, 500, enabled=False, with_timeline=True)
     assert (off == -1).all() and tl.sum() == 0
+
+
+def test_move_id_codec_and_random_legal():
+    """rl/actions.py's mixed-radix move ids (d-pad 9, A 3, B 3, Start 2, Select 2, least significant first): every
+    one of the 324 ids round-trips, the place values are the running products of the radices, the mask columns are
+    the parts side by side, and random_legal draws only legal choices, every legal choice of a part with about
+    equal frequency."""
+    import torch
+    from rl import actions
+    ids = torch.arange(324, dtype=torch.int16)
+    parts = actions.unpack(ids)
+    assert [int(p.max()) + 1 for p in parts] == [9, 3, 3, 2, 2]
+    assert torch.equal(actions.pack(parts), ids)
+    assert actions.MULT == [1, 9, 27, 81, 162] and actions.NUM_MOVES == 324
+    assert actions.PARTS == [(0, 9), (9, 12), (12, 15), (15, 17), (17, 19)]
+    # brute force: the id of (d, a, b, s, t) is d + 9a + 27b + 81s + 162t
+    want = [d + 9 * a + 27 * b + 81 * s + 162 * t for t in range(2) for s in range(2) for b in range(3)
+            for a in range(3) for d in range(9)]
+    assert want == list(range(324))
+    g = torch.Generator().manual_seed(3)
+    masks = torch.zeros(4000, 19, dtype=torch.uint8)
+    masks[:, [0, 4, 8]] = 1            # d-pad: none, left-ish, right-ish only
+    masks[:, 9] = 1                    # A: only "off"
+    masks[:, 12:15] = 1                # B: all three
+    masks[:2000, 15] = 1               # Start: off for half the envs, on for the other half
+    masks[2000:, 16] = 1
+    masks[:, 17:19] = 1
+    got = actions.unpack(actions.random_legal(masks, g))
+    for k, (a, b) in enumerate(actions.PARTS):
+        assert bool(masks[torch.arange(4000), a + got[k]].all())
+    counts = torch.bincount(got[0], minlength=9)
+    assert set(torch.nonzero(counts).flatten().tolist()) == {0, 4, 8}
+    assert all(abs(int(counts[c]) - 4000 / 3) < 200 for c in (0, 4, 8))
+    assert (got[3][:2000] == 0).all() and (got[3][2000:] == 1).all()
