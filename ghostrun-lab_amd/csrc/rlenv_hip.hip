@@ -89,6 +89,13 @@ struct LevelK {
 struct GameK {
     NesRec* recs;          // n + 1 records, slot n = boot snapshot
     const NesRec* idle;    // idle templates
+    // Restart templates, one per idle count k = 0..idle_tmpl: the record after a restart's 4 neutral frames from
+    // the boot snapshot (k = 0) or idle template k, those frames' pictures and emphasis, and the fault code they
+    // leave (0 = none). A restart from the boot snapshot copies one instead of emulating the frames.
+    const NesRec* rst;
+    const uint8_t* rst_obs;     // [idle_tmpl + 1][RLE_FRAMES][RLE_OBS_PIXELS]
+    const uint8_t* rst_emph;    // [idle_tmpl + 1][RLE_FRAMES][RLE_OBS_H]
+    const uint32_t* rst_fault;  // [idle_tmpl + 1]
     Cart cart;
     int n, offset, start_ok, select_ok, game;
     uint32_t kcap;         // key-set entries per env (rl10_keyset_capacity; 0 for most games)
@@ -99,7 +106,9 @@ struct GameK {
     LevelK lv;
 };
 
-enum : int { EMU_DECISION = 0, EMU_RESTART = 1, EMU_BOOT = 2, EMU_IDLE = 3 };
+// EMU_TEMPLATE: one frame of every restart template (block k = template k, pad 0, target boot_target + k frames,
+// fault word boot_fault[k]); the GameK's recs point at the templates.
+enum : int { EMU_DECISION = 0, EMU_RESTART = 1, EMU_BOOT = 2, EMU_IDLE = 3, EMU_TEMPLATE = 4 };
 
 struct EmuArgs {
     GameK g;
@@ -180,7 +189,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(8, 8))) void
     const int lane = (int)threadIdx.x;
     const int e = a.mode == EMU_BOOT ? a.e0 : slot_env(a.g, a.use_list, a.e0, k);
     const int ge = a.g.offset + e;
-    if (a.mode == EMU_RESTART && a.e.resetting[ge] == 0) return;
+    if (a.mode == EMU_RESTART && a.e.resetting[ge] != 1) return;   // 2: copied from a restart template
     // EMU_IDLE: a restart from a saved level start emulates all of its idle frames (pad 0) in this one launch; a
     // restart from the boot snapshot copied a template that holds them (rl/csrc/rlenv_core.cuh:312-318)
     int frames = 1;
@@ -201,6 +210,9 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(8, 8))) void
         if (a.mode == EMU_BOOT) {
             pad = a.boot_pad;
             target = a.boot_target;
+        } else if (a.mode == EMU_TEMPLATE) {
+            target = a.boot_target + (uint64_t)e * NES_FRAME_DOTS;
+            fault = a.boot_fault[e];
         } else {
             if (a.mode == EMU_DECISION) pad = decision_pad(a, ge, a.f);
             target = a.e.target[ge];
@@ -215,6 +227,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(8, 8))) void
                 const uint32_t f = run_until_wave<B>(cs, m, c_optab.t, target, a.budget);
                 if (f != 0) {
                     if (a.mode == EMU_BOOT) atomicOr(a.boot_fault, 1u);
+                    else if (a.mode == EMU_TEMPLATE) a.boot_fault[e] = f;
                     else a.e.fault[ge] = f;
                     fault = f;
                 }
@@ -222,7 +235,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(8, 8))) void
             target += NES_FRAME_DOTS;
         }
         con_store(cs, rec);
-        if (a.mode != EMU_BOOT) {
+        if (a.mode != EMU_BOOT && a.mode != EMU_TEMPLATE) {
             a.e.target[ge] = target;
             a.e.ep_frame[ge] += (uint32_t)frames;
         }
@@ -534,7 +547,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(8, 8))) void
     if (k >= count) return;
     const int e = slot_env(a.g, a.use_list, a.e0, k);
     const int ge = a.g.offset + e;
-    if (a.restart_pass && a.e.resetting[ge] == 0) return;
+    if (a.restart_pass && a.e.resetting[ge] != 1) return;   // 2: copied from a restart template
     if (a.s.no_render) return;
     const int lane = (int)threadIdx.x;
     const NesRec* rec = &a.g.recs[e];
@@ -719,22 +732,39 @@ __global__ __launch_bounds__(256) void k_start(FinishArgs a) {
     list_append(a.g, valid, e);
 }
 
-// Boot snapshot (slot n) or idle template k-1 -> the listed console's record; one workgroup per entry.
+// A listed restart, one workgroup per entry. From a saved level start: the slot's record and key set (its idle and
+// restart frames are emulated next). From the boot snapshot: restart template k (k = the idle count) - the record
+// after the 4 neutral frames, their pictures, emphasis and fault - with the target and frame counter moved past
+// those frames; the env is marked 2 (copied) so that the restart passes leave it alone. Empty key set.
 __global__ __launch_bounds__(256) void k_reset_copy(FinishArgs a) {
     const uint32_t count = *a.g.list_count;
     for (uint32_t k = blockIdx.x; k < count; k += gridDim.x) {
-        const int e = a.g.list[k];
-        const int idle = a.e.ep_idle[a.g.offset + e];
-        const int lv = a.e.ep_start ? a.e.ep_start[a.g.offset + e] : -1;
+        const int e = a.g.list[k], ge = a.g.offset + e;
+        const int idle = a.e.ep_idle[ge];
+        const int lv = a.e.ep_start ? a.e.ep_start[ge] : -1;
         const int t = idle <= a.s.idle_tmpl ? idle : 0;
-        const uint4* src = reinterpret_cast<const uint4*>(lv >= 0 ? &a.g.lv.rec[lv]
-                                                          : t == 0 ? &a.g.recs[a.g.n] : &a.g.idle[t - 1]);
+        const uint4* src = reinterpret_cast<const uint4*>(lv >= 0 ? &a.g.lv.rec[lv] : &a.g.rst[t]);
         uint4* dst = reinterpret_cast<uint4*>(&a.g.recs[e]);
         for (uint32_t i = threadIdx.x; i < NES_REC_BYTES / 16u; i += blockDim.x) dst[i] = src[i];
-        // the env's key set: the level slot's, or empty
         uint32_t* kd = a.g.keys + (size_t)e * a.g.kcap;
         const uint32_t* ks = lv >= 0 ? a.g.lv.keys + (size_t)lv * a.g.kcap : nullptr;
         for (uint32_t i = threadIdx.x; i < a.g.kcap; i += blockDim.x) kd[i] = ks ? ks[i] : 0u;
+        if (lv >= 0) continue;
+        if (!a.s.no_render) {
+            constexpr uint32_t kObs = RLE_FRAMES * RLE_OBS_PIXELS / 16u, kEmph = RLE_FRAMES * RLE_OBS_H / 16u;
+            const uint4* so = reinterpret_cast<const uint4*>(a.g.rst_obs + (size_t)t * RLE_FRAMES * RLE_OBS_PIXELS);
+            uint4* d = reinterpret_cast<uint4*>(a.o.obs + (size_t)ge * RLE_FRAMES * RLE_OBS_PIXELS);
+            for (uint32_t i = threadIdx.x; i < kObs; i += blockDim.x) d[i] = so[i];
+            const uint4* se = reinterpret_cast<const uint4*>(a.g.rst_emph + (size_t)t * RLE_FRAMES * RLE_OBS_H);
+            uint4* de = reinterpret_cast<uint4*>(a.o.emph + (size_t)ge * RLE_FRAMES * RLE_OBS_H);
+            for (uint32_t i = threadIdx.x; i < kEmph; i += blockDim.x) de[i] = se[i];
+        }
+        if (threadIdx.x == 0) {
+            a.e.fault[ge] = a.g.rst_fault[t];
+            a.e.target[ge] += (uint64_t)RLE_FRAMES * NES_FRAME_DOTS;
+            a.e.ep_frame[ge] += RLE_FRAMES;
+            a.e.resetting[ge] = 2;
+        }
     }
 }
 
@@ -1169,10 +1199,13 @@ void restart_phases(const Env& env, const GameK& g, const Outs& o, int e0, int e
     trace("reset_copy", st);
     // Idle frames: a restart from the boot snapshot copied the template that holds them (the template count equals
     // idle_max); one from a saved level start emulates them here.
-    if (g.lv.cap > 0 && env.s.idle_max > 0) launch_emu(env, g, o, EMU_IDLE, 0, true, e0, e1, st);
-    for (int f = 0; f < RLE_FRAMES; ++f) {
-        launch_emu(env, g, o, EMU_RESTART, f, true, e0, e1, st);
-        launch_render(env, g, o, f, true, true, e0, e1, st);
+    // Only a restart from a saved level start emulates; one from the boot snapshot was a copy.
+    if (g.lv.cap > 0) {
+        if (env.s.idle_max > 0) launch_emu(env, g, o, EMU_IDLE, 0, true, e0, e1, st);
+        for (int f = 0; f < RLE_FRAMES; ++f) {
+            launch_emu(env, g, o, EMU_RESTART, f, true, e0, e1, st);
+            launch_render(env, g, o, f, true, true, e0, e1, st);
+        }
     }
     env.clock.run(KC_RESET_FINISH, st,
                   [&] { hipLaunchKernelGGL(k_reset_finish, dim3((n + 255) / 256), dim3(256), 0, st, fa); });
@@ -1229,6 +1262,38 @@ void fetch_entry(uint32_t* e, uint32_t a, uint32_t op, uint32_t b1, uint32_t b2,
     e[1] = base;
 }
 
+// The restart templates of a game (GameK::rst): the snapshot and every idle template, each run through a restart's
+// 4 neutral frames (rl/csrc/rlenv_core.cuh:320-326, ph_reset_frame, and the restart pass of ph_render) - one
+// launch per frame over all templates, each drawn into its own pictures. A fault in those frames is recorded, not an
+// error: the episode that copies the template ends with it at its first decision, as one that emulated them would.
+void build_restart_templates(Env& env, GameK& g) {
+    const int count = env.s.idle_tmpl + 1;
+    NesRec* rst = const_cast<NesRec*>(g.rst);
+    if (hipMemcpy(&rst[0], &g.recs[g.n], sizeof(NesRec), hipMemcpyDeviceToDevice) != hipSuccess ||
+        (count > 1 && hipMemcpy(&rst[1], g.idle, sizeof(NesRec) * (size_t)(count - 1), hipMemcpyDeviceToDevice) !=
+                          hipSuccess))
+        throw std::runtime_error("restart template copy failed");
+    GameK t = g;
+    t.recs = rst;
+    t.offset = 0;
+    Outs o = env.o;
+    o.obs = const_cast<uint8_t*>(g.rst_obs);
+    o.emph = const_cast<uint8_t*>(g.rst_emph);
+    Settings s = env.s;
+    s.no_render = 0;
+    for (int f = 0; f < RLE_FRAMES; ++f) {
+        const EmuArgs a{t, env.e, o, s, env.optab, EMU_TEMPLATE, f, 0, 0, count, 0,
+                        g.tmpl_target + (uint64_t)f * NES_FRAME_DOTS, const_cast<uint32_t*>(g.rst_fault), env.budget};
+        if (g.cart.board == NES_BOARD_NROM || g.cart.board == NES_BOARD_CNROM)
+            hipLaunchKernelGGL(k_emu_w<NES_BOARD_NROM>, dim3(count), dim3(64), 0, 0, a);
+        else
+            hipLaunchKernelGGL(k_emu_w<NES_BOARD_MMC3>, dim3(count), dim3(64), 0, 0, a);
+        const RenderArgs r{t, env.e, o, s, f, 0, 0, 0, count};
+        hipLaunchKernelGGL(k_render, dim3(count), dim3(64), 0, 0, r);
+    }
+    if (hipDeviceSynchronize() != hipSuccess || check("restart templates")) throw std::runtime_error(g_error);
+}
+
 void boot_game(Env& env, GameH& gh, const uint8_t* pads, size_t npads) {
     GameK& g = gh.k;
     hipLaunchKernelGGL(k_power_on, dim3(1), dim3(1), 0, 0, &g.recs[g.n], g.cart);
@@ -1259,6 +1324,7 @@ void boot_game(Env& env, GameH& gh, const uint8_t* pads, size_t npads) {
     if (hipMemcpy(&host_fault, fault, 4, hipMemcpyDeviceToHost) != hipSuccess) throw std::runtime_error("boot sync failed");
     if (check("boot")) throw std::runtime_error(g_error);
     if (host_fault) throw std::runtime_error("emulator fault during boot of game " + std::to_string(gh.game));
+    build_restart_templates(env, g);
 }
 
 template <class F>
@@ -1397,6 +1463,11 @@ void* rlenv_create(int ngames, const int* game_ids, const uint8_t* const* roms, 
                           p.bus_conflicts};
             g.recs = env->mem.zeros<NesRec>((size_t)g.n + 1);
             g.idle = env->mem.zeros<NesRec>((size_t)std::max(env->s.idle_tmpl, 1));
+            const size_t tmpl = (size_t)env->s.idle_tmpl + 1;
+            g.rst = env->mem.zeros<NesRec>(tmpl);
+            g.rst_obs = env->mem.zeros<uint8_t>(tmpl * RLE_FRAMES * RLE_OBS_PIXELS);
+            g.rst_emph = env->mem.zeros<uint8_t>(tmpl * RLE_FRAMES * RLE_OBS_H);
+            g.rst_fault = env->mem.zeros<uint32_t>(tmpl);
             g.list = env->mem.zeros<int32_t>((size_t)std::max(g.n, 1));
             g.list_count = env->mem.zeros<uint32_t>(1);
             env->games.push_back(gh);
