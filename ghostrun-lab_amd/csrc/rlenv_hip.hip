@@ -638,9 +638,7 @@ __device__ __forceinline__ void reset_rl(const GameK& g, const EnvArrays& e, con
     }
     if (e.ep_start) e.ep_start[ge] = lv;
     e.fault[ge] = 0;
-    Dropout d;
-    ev::drop_reset(d, seed, s.dropout != 0, s.gap_p32);
-    e.drop[ge] = d;
+    ev::drop_reset(e.drop[ge], seed, s.dropout != 0, s.gap_p32);   // in place: a local copy of the ring spills
     e.prev_applied[ge] = 0;
     e.ep_idle[ge] = idle;
     e.resetting[ge] = 1;
@@ -692,9 +690,7 @@ __global__ __launch_bounds__(256) void k_finish(FinishArgs a) {
         const int32_t len = a.e.ep_len[ge] + 1;
         a.e.ep_len[ge] = len;
         if (u.event_level > a.e.ep_maxlvl[ge]) a.e.ep_maxlvl[ge] = u.event_level;
-        Dropout d = a.e.drop[ge];
-        ev::drop_advance(d, a.s.dropout != 0, a.s.gap_p32);
-        a.e.drop[ge] = d;
+        ev::drop_advance(a.e.drop[ge], a.s.dropout != 0, a.s.gap_p32);   // in place (no local copy of the ring)
         // level-start claim: the arrival with the fewest deaths, then the lowest env index (rlenv_core.cuh:288-291)
         if (a.g.lv.cap > 0 && !done && (u.events & ev::EV_LEVEL) && u.event_level >= 0 && u.event_level < a.g.lv.levels) {
             const unsigned long long dd = (unsigned long long)(uint32_t)(st.deaths < 0 ? 0 : st.deaths);
