@@ -1,34 +1,40 @@
 #!/usr/bin/env python3
 """Throughput of the batched NES environment step on one MI355X (emulated frames/s and decisions/s).
 
-    python bench.py [--steps K] [--warmup W] [--workload NAME] [--no-cpu]
+    python bench.py [--steps K] [--warmup W] [--workload NAME] [--only] [--no-cpu]
 
 A step is one decision of every console: 4 emulated frames each (6502 + PPU + mapper), each frame's 224x240
 colour-index picture and emphasis written to HBM, then the reward10 tracker, the outputs and the restart pass
 (rl/csrc/rlenv.cu:145-170 is the reference's launch order for one decision).
 
 Workloads (synthetic data; the reference ships no ROMs):
-  nrom128-raw-frames (default, the headline): 8192 consoles of the seed-generated NROM-128 cartridge
+  nrom128-raw-frames (the headline line): 8192 consoles of the seed-generated NROM-128 cartridge
       (rl.synth.nrom_cart: 16 KB PRG of generated 6502 code, 8 KB random CHR), per console and decision a pad byte
       uniform over 0..255, sticky repeat p = 0.25 per frame, no dropout, no idle frames, raw uint8 frames
       [N, 4, 224, 240] + emphasis + a 2 KB RAM hash per console to HBM. The SMB reward reader sees RAM bytes the
-      cart never writes, so no episode ends within 1800 decisions: the restart kernels find nothing to restart.
+      cart never writes, so no episode ends: the restart kernels find nothing to restart.
   rollout-pack6: 8192 NROM consoles, episode ends drawn with p = 1/2000 per decision, finished consoles restored
       from the boot snapshot, 20 % of decisions with a dropped input, and every decision's frames 6-bit packed on
       the device and copied into a ring of pinned host slots on a second stream (the trainer's obs-pack6 store).
   mmc3-stress: 16384 consoles of the seed-generated MMC3 cartridge (256 KB PRG, 128 KB CHR, bank switches,
       scanline IRQ at a varying line, sprite-0 split), independent random pads, frames 6-bit packed on the device.
+  twelve-games: the twelve reward10 games, 3072 consoles each (36,864), each on its own seed-generated cartridge
+      (the SMB-like cart for smb; NROM, MMC1, UxROM, CNROM, MMC3 and MMC2 carts for the others), raw pads with
+      sticky repeat, raw frames; the games step concurrently, one stream each.
   reward10: the SMB reward tracker alone, 8192 envs x 1024 steps of seed-generated SMB RAM trajectories
       (rl.synth.smb_ram15); value in env-steps/s.
+
+One invocation measures the chosen workload (the headline by default) with its parity check and CPU baseline, then,
+unless --only, every other workload with a parity check, each under "workloads" in the same JSON line.
 
 Timing: W untimed decisions, then K decisions between device synchronisations; value = consoles * K / seconds.
 Inputs (pad bytes) are resident in HBM before the timed region. The library's per-kernel clock brackets every
 launch with HIP events on the stream it runs on, which gives each kernel's average duration over the same timed
-region; the roofline is computed for the kernel that takes the most time.
+region; the roofline is computed for the kernel that takes the most time, and for the whole step.
 
 Parity: after the warmup the first 64 consoles' outputs are compared with the CPU oracle run on the same seeds and
-pad bytes; the oracle then continues as the timed CPU baseline (a bounded sample of the same workload on the
-host's cores, plus a 1-thread sample).
+pad bytes; for the chosen workload the oracle then continues as the timed CPU baseline (a bounded sample of the same
+workload on the host's cores, plus a 1-thread sample).
 """
 from __future__ import annotations
 
@@ -49,14 +55,21 @@ METRIC = 'emulated NES frames/sec and decisions/sec at 8192 consoles, 1 MI355X'
 ORACLE_LIB = ROOT / 'oracle' / '_build' / 'liboracle_rlenv.so'
 COUNTERS = ROOT / 'profiles' / 'counters.json'
 HBM_PEAK_GBPS = 8000.0
-SALU_PEAK = 256 * 2.4e9                    # one scalar ALU per CU (256 CUs) at the 2.4 GHz peak engine clock
+CLOCK_HZ = 2.4e9                           # MI355X peak engine clock
+CUS = 256
+SALU_PEAK = CUS * CLOCK_HZ                 # one scalar instruction per CU per clock
+VALU_PEAK = CUS * CLOCK_HZ                 # one wave64 vector instruction per CU per clock (4 SIMDs x 1/4)
 KERNELS = ('k_emu', 'k_render', 'k_finish', 'k_reset_copy', 'k_emu_restart', 'k_render_restart', 'k_reset_finish',
            'k_emu_idle', 'k_archive')
 
 # Algorithmic bytes per console per launch (outputs written + inputs read by the path, not state traffic).
 PICTURE_BYTES = 224 * 240 + 224            # one frame's colour indices + emphasis
+DECISION_BYTES = 4 * (PICTURE_BYTES + 1) + 2 + 4 + 1 + 4 + 28 + 19 + 360   # 216,358 B per console per decision
+FRAME_UNIT_BYTES = DECISION_BYTES / 4      # 54,089.5 B: the algorithmic bytes of one emulated frame
+PACK6_BYTES = 4 * 224 * 240 * 3 // 4 + 896 + 420                       # 162,596 B per console per decision
+RL10_STEP_BYTES = 20                                                      # 15 RAM bytes read + f32 reward + done
 ALG_BYTES = {
-    'k_emu': 2 + 1,                         # the action (int16) read, the frame's pad byte written
+    'k_emu': FRAME_UNIT_BYTES,              # the frame unit: one launch emulates one frame of every console
     'k_render': PICTURE_BYTES,
     'k_finish': 4 + 1 + 4 + 28 + 8,         # reward, done, events, parts, RAM hash
     'k_reset_copy': 0,
@@ -66,16 +79,16 @@ ALG_BYTES = {
     'k_emu_idle': 0,
     'k_archive': 0,
 }
-DECISION_BYTES = 4 * (PICTURE_BYTES + 1) + 2 + 4 + 1 + 4 + 28 + 19 + 360   # 216,358 B per console per decision
-PACK6_BYTES = 4 * 224 * 240 * 3 // 4 + 896 + 420                       # 162,596 B per console per decision
-RL10_STEP_BYTES = 20                                                      # 15 RAM bytes read + f32 reward + done
 
 WORKLOADS = {
     'nrom128-raw-frames': dict(consoles=8192, cart='nrom', sticky=True, dropout=False, end_prob=0.0, pack6=None),
     'rollout-pack6': dict(consoles=8192, cart='nrom', sticky=True, dropout=True, end_prob=1 / 2000, pack6='host'),
     'mmc3-stress': dict(consoles=16384, cart='mmc3', sticky=False, dropout=False, end_prob=0.0, pack6='device'),
+    'twelve-games': dict(consoles=12 * 3072, cart='twelve', sticky=True, dropout=False, end_prob=0.0, pack6=None),
     'reward10': dict(consoles=8192),
 }
+HEADLINE = 'nrom128-raw-frames'
+EXTRA_STEPS = 16                            # timed decisions of each additional workload
 
 
 def parse():
@@ -83,14 +96,14 @@ def parse():
     ap.add_argument('--gpus', type=int, default=1)
     ap.add_argument('--steps', type=int, default=64)
     ap.add_argument('--warmup', type=int, default=8)
-    ap.add_argument('--workload', choices=sorted(WORKLOADS), default='nrom128-raw-frames')
+    ap.add_argument('--workload', choices=sorted(WORKLOADS), default=HEADLINE)
+    ap.add_argument('--only', action='store_true', help='measure the chosen workload only')
     ap.add_argument('--consoles', type=int, default=0, help='override the workload console count')
     ap.add_argument('--cart-seed', type=int, default=1)
     ap.add_argument('--seed', type=int, default=1)
     ap.add_argument('--host-slots', type=int, default=4, help='pinned host ring slots of rollout-pack6')
     ap.add_argument('--cpu-seconds', type=float, default=10.0)
-    ap.add_argument('--cpu-consoles', type=int, default=64)
-    ap.add_argument('--no-cpu', action='store_true', help='skip the parity check and the CPU baseline')
+    ap.add_argument('--no-cpu', action='store_true', help='skip the parity checks and the CPU baseline')
     ap.add_argument('--no-kernel-clock', action='store_true')
     return ap.parse_args()
 
@@ -108,18 +121,48 @@ def main():
     import torch
     if not torch.cuda.is_available():
         sys.exit('bench.py needs a HIP device')
-    out = bench_reward10(args) if args.workload == 'reward10' else bench_env(args)
+    out = run_workload(args, args.workload, args.steps, args.warmup, baseline=True)
+    if not args.only:
+        out['workloads'] = {}
+        for name in WORKLOADS:
+            if name == args.workload:
+                continue
+            res = run_workload(args, name, min(args.steps, EXTRA_STEPS), min(args.warmup, 6), baseline=False)
+            out['workloads'][name] = {k: res[k] for k in ('metric', 'value', 'unit', 'ms_per_step', 'steps', 'warmup',
+                                                          'dtype', 'config', 'roofline', 'parity', 'kernels',
+                                                          'frames_per_s', 'emulated_instructions_per_s',
+                                                          'step_output_gbps') if k in res}
+            torch.cuda.empty_cache()
     print(json.dumps(out), flush=True)
-    if 'parity' in out and not out['parity']['bit_exact']:
+    bad = [n for n, r in [(args.workload, out)] + list(out.get('workloads', {}).items())
+           if 'parity' in r and not r['parity']['bit_exact']]
+    if bad:
+        print(f'[bench] parity FAILED for {bad}', file=sys.stderr, flush=True)
         sys.exit(3)
+
+
+def run_workload(args, name, steps, warmup, baseline):
+    if name == 'reward10':
+        return bench_reward10(args, steps, warmup, baseline)
+    return bench_env(args, name, steps, warmup, baseline)
 
 
 # ------------------------------------------------------------------------------------------------ env
 
 
-def cart_of(w, seed):
+# The twelve-games batch: a cart per game, in GAMES order (the SMB-like cart for smb, the boards in turn after it).
+TWELVE_BOARDS = ('smb_like', 'nrom', 'mmc1', 'uxrom', 'cnrom', 'mmc3', 'mmc2', 'nrom', 'mmc1', 'uxrom', 'cnrom', 'mmc3')
+
+
+def carts_of(w, seed):
+    """game slug -> cart bytes of a workload."""
     from rl import synth
-    return synth.nrom_cart(seed) if w['cart'] == 'nrom' else synth.mmc3_cart(seed)
+    from rl.rlenv import GAMES
+    if w['cart'] != 'twelve':
+        return {'smb': synth.nrom_cart(seed) if w['cart'] == 'nrom' else synth.mmc3_cart(seed)}
+    make = dict(smb_like=synth.smb_like_cart, nrom=synth.nrom_cart, mmc1=synth.mmc1_cart, uxrom=synth.uxrom_cart,
+                cnrom=synth.cnrom_cart, mmc3=synth.mmc3_cart, mmc2=synth.mmc2_cart)
+    return {g: make[b](seed + i) for i, (g, b) in enumerate(zip(GAMES, TWELVE_BOARDS))}
 
 
 # Boot: the reference records each game's boot pad bytes from power-on through its boot sequence and takes the
@@ -129,9 +172,9 @@ def cart_of(w, seed):
 BOOT_FRAMES = 4
 
 
-def env_kwargs(w, args, cart):
+def env_kwargs(w, args, carts):
     kw = dict(seed=args.seed, sticky=w['sticky'], idle_max=0, dropout=w['dropout'], pad_mode=True, ram_hash=True,
-              roms={'smb': cart}, end_prob=w['end_prob'], boot={'smb': bytes(BOOT_FRAMES)})
+              roms=carts, end_prob=w['end_prob'], boot={g: bytes(BOOT_FRAMES) for g in carts})
     if w['dropout']:
         kw['dropout_gap'] = 1 / 60   # mean gap 60 decisions, mean run 15: 20 % of decisions with a dropped input
     return kw
@@ -182,22 +225,22 @@ class Pack6Sink:
             self.store.close()
 
 
-def bench_env(args):
+def bench_env(args, name, K, W, baseline):
     import torch
-    from rl.rlenv import RlEnv
-    w = WORKLOADS[args.workload]
+    from rl.rlenv import GAMES, RlEnv
+    w = WORKLOADS[name]
     dev = torch.device('cuda:0')
-    N = args.consoles or w['consoles']
-    W, K = args.warmup, args.steps
-    cart = cart_of(w, args.cart_seed)
-    kw = env_kwargs(w, args, cart)
+    N = (args.consoles if name == args.workload else 0) or w['consoles']
+    carts = carts_of(w, args.cart_seed)
+    counts = {g: N // len(carts) for g in carts}
+    N = sum(counts.values())
+    kw = env_kwargs(w, args, carts)
     gen = torch.Generator().manual_seed(args.seed)
     pads_host = torch.randint(0, 256, (W + K, N), generator=gen, dtype=torch.int16)
     pads = pads_host.to(dev)
 
-    print(f'[bench] workload {args.workload}: {N} consoles, warmup {W}, timed {K} decisions', file=sys.stderr,
-          flush=True)
-    env = RlEnv({'smb': N}, device=dev, **kw)
+    print(f'[bench] workload {name}: {N} consoles, warmup {W}, timed {K} decisions', file=sys.stderr, flush=True)
+    env = RlEnv(counts, device=dev, **kw)
     sink = Pack6Sink(env, w['pack6'], args.host_slots) if w['pack6'] else None
     env.start()
     for t in range(W):
@@ -208,7 +251,8 @@ def bench_env(args):
         if sink:
             sink.after()
     torch.cuda.synchronize()
-    ncmp = min(args.cpu_consoles, N)
+    first = env.games[0]
+    ncmp = min(64, counts[first])
     snap = {k: getattr(env, k)[:ncmp].cpu().numpy() for k in ('emph', 'reward', 'done', 'ram_hash')}
     snap['obs'] = (sink.obs() if sink else env.obs)[:ncmp].cpu().numpy()
     instr0 = _instructions(env)
@@ -242,8 +286,10 @@ def bench_env(args):
 
     decisions = N * K / dt
     out_bytes = PACK6_BYTES if w['pack6'] else DECISION_BYTES
-    cfg = dict(workload=args.workload, consoles=N, frames_per_decision=4,
-               cart=f'rl.synth.{w["cart"]}_cart({args.cart_seed})',
+    cart = (f'rl.synth.{w["cart"]}_cart({args.cart_seed})' if w['cart'] != 'twelve' else
+            'per game: ' + ', '.join(f'{g}={b}({args.cart_seed + i})' for i, (g, b) in enumerate(zip(GAMES,
+                                                                                                    TWELVE_BOARDS))))
+    cfg = dict(workload=name, consoles=N, games=len(counts), frames_per_decision=4, cart=cart,
                pads='uniform 0..255' + (', sticky p=0.25' if w['sticky'] else ''), dropout=w['dropout'],
                end_prob=w['end_prob'], idle_max=0,
                outputs=('raw u8 frames [N,4,224,240]' if not w['pack6'] else
@@ -254,21 +300,22 @@ def bench_env(args):
     out = dict(metric=METRIC, value=round(decisions, 1), unit='decisions/s', frames_per_s=round(4 * decisions, 1),
                n_gpus=1, steps=K, warmup=W, ms_per_step=round(dt * 1e3 / K, 3), higher_is_better=True,
                scaling='weak', vs_baseline=None, dtype='u8',
-               data='synthetic: seed-generated cartridge (rl.synth), uniform random pad bytes', config=cfg,
+               data='synthetic: seed-generated cartridges (rl.synth), uniform random pad bytes', config=cfg,
                emulated_instructions_per_s=round(float(instr1 - instr0) / dt, 1),
                step_output_gbps=round(out_bytes * N * K / dt / 1e9, 3))
     if kern:
-        out['roofline'] = _roofline(kern, N)
-        iss = _issue_roofline(args.workload, kern, K, dt, out['emulated_instructions_per_s'])
-        if iss:
-            out['issue_roofline'] = iss
+        out['roofline'] = _roofline(name, kern, N, K, dt, out_bytes, out['emulated_instructions_per_s'])
         out['kernels'] = kern
-        counters = _counters(args.workload)
+        counters = _counters(name)
         if counters:
             out['counters'] = counters
     if not args.no_cpu:
-        out['parity'], out['cpu_baseline'], out['cpu_baseline_1thread'] = _cpu_env(args, w, kw, pads_host, snap,
-                                                                                 ncmp)
+        cpu_kw = dict(kw, roms={first: carts[first]}, boot={first: bytes(BOOT_FRAMES)})
+        parity, base, one = _cpu_env(args, w, first, cpu_kw, pads_host, snap, ncmp, W, baseline)
+        out['parity'] = parity
+        if baseline:
+            out['cpu_baseline'], out['cpu_baseline_1thread'] = base, one
+    del env
     return out
 
 
@@ -278,49 +325,47 @@ def _kernel_times(env, N, K, dt):
     if env.lib.rlenv_kernel_times(env.h, ms.ctypes.data, cnt.ctypes.data, len(KERNELS)) != 0:
         raise RuntimeError(env.lib.rlenv_error().decode())
     env.lib.rlenv_set_kernel_timing(env.h, 0)
+    games = len(env.games)
     kern = {}
     for name, m, c in zip(KERNELS, ms, cnt):
         if c == 0:
             continue
         per = m / c
-        alg = ALG_BYTES[name] * N
+        alg = ALG_BYTES[name] * N / games   # a launch covers one game's consoles
         kern[name] = dict(ms_per_launch=round(per, 4), launches_per_step=round(c / K, 3), ms_per_step=round(m / K, 3),
-                          share=round(m / (dt * 1e3), 4), alg_bytes_per_launch=alg,
+                          share=round(m / (dt * 1e3), 4), alg_bytes_per_launch=round(alg),
                           achieved_gbps=round(alg / (per * 1e-3) / 1e9, 3))
     return kern
 
 
-def _roofline(kern, n):
+def _roofline(name, kern, n, K, dt, out_bytes, ips):
+    """The dominant kernel against HBM (its algorithmic bytes per launch over its average launch time), the whole
+    step against HBM (the decision's algorithmic bytes over the measured step time), and the emulator kernel's
+    scalar and vector issue against one instruction per CU per clock each (instructions per emulated instruction from
+    the committed counter run of the same workload, emulated instructions and kernel time from this run)."""
     dom = max(kern, key=lambda k: kern[k]['ms_per_step'])
     d = kern[dom]
+    step_gbps = out_bytes * n * K / dt / 1e9
     r = dict(kernel=dom, bound='hbm', achieved=d['achieved_gbps'], peak=HBM_PEAK_GBPS, unit='GB/s',
-             frac=round(d['achieved_gbps'] / HBM_PEAK_GBPS, 6), traffic=_traffic(dom, n))
-    if dom in ('k_emu', 'k_emu_restart'):
-        r['note'] = ('the 6502 interpreter: one console per wavefront on the scalar unit, bound by scalar issue '
-                     '(issue_roofline), not by HBM; its algorithmic bytes are the action read and the pad byte written')
+             frac=round(d['achieved_gbps'] / HBM_PEAK_GBPS, 6), traffic=_traffic(dom, n),
+             step_achieved_gbps=round(step_gbps, 3), step_frac=round(step_gbps / HBM_PEAK_GBPS, 6))
+    c = (_counters(name) or {}).get('k_emu')
+    emu = kern.get('k_emu')
+    restart = kern.get('k_emu_restart', {}).get('ms_per_step', 0.0) + kern.get('k_emu_idle', {}).get('ms_per_step', 0.0)
+    if c and emu and restart <= 0.05 * emu['ms_per_step']:
+        per = c['per_emulated_instruction']
+        emu_s = emu['ms_per_step'] * K / 1e3
+        ips_kernel = ips * dt / emu_s              # emulated instructions per second of k_emu time
+        r['emu_issue'] = dict(kernel='k_emu', salu_per_instruction=per['salu'], valu_per_instruction=per['valu'],
+                              salu_frac=round(ips_kernel * per['salu'] / SALU_PEAK, 4),
+                              valu_frac=round(ips_kernel * per['valu'] / VALU_PEAK, 4),
+                              counter_SALUBusy_pct=c.get('SALUBusy_pct'), counter_VALUBusy_pct=c.get('VALUBusy_pct'),
+                              counter_VALUUtilization_pct=c.get('VALUUtilization_pct'),
+                              note='one console per wavefront, the 6502 on the scalar unit: bound by scalar issue')
+    if name == 'rollout-pack6':
+        r['host_link_gbps'] = round(PACK6_BYTES * n * K / dt / 1e9, 3)
+        r['note'] = 'every decision\'s packed frames cross the host link (PCIe 5 x16, about 63 GB/s each way)'
     return r
-
-
-def _issue_roofline(workload, kern, K, dt, ips):
-    """Scalar-issue roofline of the emulator kernel: SALU instructions per second against one scalar ALU per CU at
-    the peak engine clock. SALU instructions per emulated instruction come from the committed counter run of the same
-    workload (SQ_INSTS_SALU); the emulated instructions and the kernel's time are measured in this run. VALU
-    utilisation of the two frame kernels is reported beside it from the same counter run."""
-    c = _counters(workload) or {}
-    e = c.get('k_emu')
-    if not e or 'k_emu' not in kern:
-        return None
-    restart = kern.get('k_emu_restart', {}).get('ms_per_step', 0.0)
-    if restart > 0.05 * kern['k_emu']['ms_per_step']:
-        return None                          # restart frames would count in the instructions but not in k_emu time
-    salu = e['per_emulated_instruction']['salu']
-    emu_s = kern['k_emu']['ms_per_step'] * K / 1e3
-    achieved = ips * dt / emu_s * salu
-    out = dict(kernel='k_emu', bound='salu', unit='SALU instr/s', achieved=round(achieved / 1e9, 1) * 1e9,
-               peak=SALU_PEAK, frac=round(achieved / SALU_PEAK, 4), salu_per_emulated_instruction=salu,
-               counter_SALUBusy_pct=e.get('SALUBusy_pct'))
-    out['valu_busy_pct'] = {k: v.get('VALUBusy_pct') for k, v in c.items() if isinstance(v, dict)}
-    return out
 
 
 def _summary():
@@ -346,8 +391,11 @@ def _instructions(env) -> int:
     """Emulated 6502 instructions of every console so far (record field instr_lo, u32 at 0x14)."""
     import torch
     torch.cuda.synchronize()
-    rec = env.consoles(0)
-    return int(np.frombuffer(np.ascontiguousarray(rec[:, 0x14:0x18]).tobytes(), np.uint32).astype(np.int64).sum())
+    total = 0
+    for gi in range(len(env.games)):
+        rec = env.consoles(gi)
+        total += int(np.frombuffer(np.ascontiguousarray(rec[:, 0x14:0x18]).tobytes(), np.uint32).astype(np.int64).sum())
+    return total
 
 
 def _oracle():
@@ -356,37 +404,63 @@ def _oracle():
     return lib
 
 
-def _threads():
-    return int(os.environ.get('OMP_NUM_THREADS', '0')) or min(os.cpu_count() or 1, 16)
+def _host_cpus():
+    """Threads the CPU baseline uses (OMP_NUM_THREADS, else the CPUs this process may run on, at most 16: the GPU
+    box's CPU share), and the host's logical and physical core counts."""
+    try:
+        allowed = len(os.sched_getaffinity(0))
+    except AttributeError:
+        allowed = os.cpu_count() or 1
+    phys = set()
+    try:
+        cur = {}
+        for line in Path('/proc/cpuinfo').read_text().splitlines() + ['']:
+            if not line.strip():
+                if 'core id' in cur:
+                    phys.add((cur.get('physical id'), cur['core id']))
+                cur = {}
+            elif ':' in line:
+                k, v = line.split(':', 1)
+                cur[k.strip()] = v.strip()
+    except OSError:
+        pass
+    threads = int(os.environ.get('OMP_NUM_THREADS', '0')) or min(allowed, 16)
+    return threads, dict(nproc=os.cpu_count(), affinity=allowed, physical_cores=len(phys) or None)
 
 
-def _cpu_env(args, w, kw, pads_host, snap, ncmp):
-    """Parity of the first ncmp consoles after the warmup, then the CPU baseline (oracle) on the same workload."""
+def _cpu_env(args, w, game, kw, pads_host, snap, ncmp, W, baseline):
+    """Parity of the first ncmp consoles after the warmup; with `baseline`, the CPU baseline (oracle) on the same
+    workload: max(64, 4 x threads) consoles on the baseline threads, then 64 consoles on 1 thread."""
     import torch
     from rl.rlenv import RlEnv
     lib = _oracle()
     lib.rl_pack6.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p]
-    W = args.warmup
+    threads, host = _host_cpus()
+    lib.orc_set_threads(threads)
+    cpu = RlEnv({game: ncmp}, device='cpu', lib_path=ORACLE_LIB, **kw)
+    cpu.start()
+    for t in range(W):
+        cpu.actions.copy_(pads_host[t, :ncmp])
+        cpu.step()
+    bad = [k for k in snap if not np.array_equal(snap[k], getattr(cpu, k).numpy())]
+    parity = dict(consoles=ncmp, decisions=W, bit_exact=not bad, differs=bad, outputs=sorted(snap))
+    print(f'[bench] parity vs oracle on {ncmp} consoles x {W} decisions: '
+          f'{"bit-exact" if not bad else "DIFFERS in " + ",".join(bad)}', file=sys.stderr, flush=True)
+    del cpu
+    if not baseline:
+        return parity, None, None
     res = {}
-    parity = None
-    for label, nthr, budget in (('all', _threads(), args.cpu_seconds), ('one', 1, max(2.0, args.cpu_seconds / 3))):
+    for label, nthr, n, budget in (('all', threads, max(64, 4 * threads), args.cpu_seconds),
+                                   ('one', 1, 64, max(2.0, args.cpu_seconds / 3))):
         lib.orc_set_threads(nthr)
-        cpu = RlEnv({'smb': ncmp}, device='cpu', lib_path=ORACLE_LIB, **kw)
-        packed = np.empty(ncmp * 4 * 224 * 240 // 4 * 3, np.uint8)
+        cpu = RlEnv({game: n}, device='cpu', lib_path=ORACLE_LIB, **kw)
+        packed = np.empty(n * 4 * 224 * 240 // 4 * 3, np.uint8)
         cpu.start()
-        for t in range(W):
-            cpu.actions.copy_(pads_host[t, :ncmp])
-            cpu.step()
-        if label == 'all':
-            bad = [k for k in snap if not np.array_equal(snap[k], getattr(cpu, k).numpy())]
-            parity = dict(consoles=ncmp, decisions=W, bit_exact=not bad, differs=bad, outputs=sorted(snap))
-            print(f'[bench] parity vs oracle on {ncmp} consoles x {W} decisions: '
-                  f'{"bit-exact" if not bad else "DIFFERS in " + ",".join(bad)}', file=sys.stderr, flush=True)
         gen = np.random.default_rng(args.seed + 7)
         t0 = time.perf_counter()
         d = 0
         while True:
-            cpu.actions.copy_(torch.from_numpy(gen.integers(0, 256, ncmp).astype(np.int16)))
+            cpu.actions.copy_(torch.from_numpy(gen.integers(0, 256, n).astype(np.int16)))
             cpu.step()
             if w['pack6']:
                 obs = cpu.obs.numpy()
@@ -395,8 +469,8 @@ def _cpu_env(args, w, kw, pads_host, snap, ncmp):
             el = time.perf_counter() - t0
             if el >= budget and d >= 2:
                 break
-        res[label] = dict(value=round(ncmp * d / el, 2), unit='decisions/s', cores=nthr, kind='port',
-                          sample=f'CPU oracle (oracle/, C, OpenMP over consoles) on {ncmp} consoles of the same '
+        res[label] = dict(value=round(n * d / el, 2), unit='decisions/s', cores=nthr, kind='port', **host,
+                          sample=f'CPU oracle (oracle/, C, OpenMP over consoles) on {n} consoles of the same '
                                  f'cartridge, settings and pad distribution{" with pack6" if w["pack6"] else ""}, '
                                  f'{d} decisions x 4 frames in {el:.1f} s, {nthr} thread(s)')
         del cpu
@@ -406,15 +480,14 @@ def _cpu_env(args, w, kw, pads_host, snap, ncmp):
 # ------------------------------------------------------------------------------------------- reward10
 
 
-def bench_reward10(args):
+def bench_reward10(args, K, W, baseline):
     """The SMB reward tracker alone (rl10_smb_run): T steps of N envs over seed-generated RAM trajectories, one
     env per lane; value in env-steps/s."""
     import torch
     from rl import synth
     from rl.rlenv import hip_library
-    N = args.consoles or WORKLOADS['reward10']['consoles']
+    N = (args.consoles if args.workload == 'reward10' else 0) or WORKLOADS['reward10']['consoles']
     T = 1024
-    K, W = args.steps, args.warmup
     print(f'[bench] workload reward10: {N} envs x {T} steps, warmup {W}, timed {K} runs', file=sys.stderr,
           flush=True)
     ram = synth.smb_ram15(args.seed, N, T)                   # [T, N, 16]
@@ -474,21 +547,23 @@ def bench_reward10(args):
         lib_o.rl10_smb_run(sub.ctypes.data, T, ncmp, 4, st0.ctypes.data, want_r.ctypes.data, want_d.ctypes.data, None)
         ok = np.array_equal(got_r[:, :ncmp], want_r) and np.array_equal(got_d[:, :ncmp], want_d)
         out['parity'] = dict(envs=ncmp, steps=T, bit_exact=bool(ok), outputs=['reward', 'done'])
-        res = {}
-        for label, nthr in (('all', _threads()), ('one', 1)):
-            lib_o.orc_set_threads(nthr)
-            n = N if nthr > 1 else N // 8
-            sub = np.ascontiguousarray(ram[:, :n])
-            r = np.zeros((T, n), np.float32)
-            dd = np.zeros((T, n), np.uint8)
-            s = np.zeros(n * 80, np.uint8)
-            t0 = time.perf_counter()
-            lib_o.rl10_smb_run(sub.ctypes.data, T, n, 4, s.ctypes.data, r.ctypes.data, dd.ctypes.data, None)
-            el = time.perf_counter() - t0
-            res[label] = dict(value=round(n * T / el, 1), unit='env-steps/s', cores=nthr, kind='port',
-                              sample=f'CPU oracle rl10_smb_run (C, OpenMP over envs) on {n} envs x {T} steps of '
-                                     f'the same trajectories, {el:.2f} s, {nthr} thread(s)')
-        out['cpu_baseline'], out['cpu_baseline_1thread'] = res['all'], res['one']
+        if baseline:
+            threads, host = _host_cpus()
+            res = {}
+            for label, nthr in (('all', threads), ('one', 1)):
+                lib_o.orc_set_threads(nthr)
+                n = N if nthr > 1 else N // 8
+                sub = np.ascontiguousarray(ram[:, :n])
+                r = np.zeros((T, n), np.float32)
+                dd = np.zeros((T, n), np.uint8)
+                s = np.zeros(n * 80, np.uint8)
+                t0 = time.perf_counter()
+                lib_o.rl10_smb_run(sub.ctypes.data, T, n, 4, s.ctypes.data, r.ctypes.data, dd.ctypes.data, None)
+                el = time.perf_counter() - t0
+                res[label] = dict(value=round(n * T / el, 1), unit='env-steps/s', cores=nthr, kind='port', **host,
+                                  sample=f'CPU oracle rl10_smb_run (C, OpenMP over envs) on {n} envs x {T} steps of '
+                                         f'the same trajectories, {el:.2f} s, {nthr} thread(s)')
+            out['cpu_baseline'], out['cpu_baseline_1thread'] = res['all'], res['one']
     return out
 
 

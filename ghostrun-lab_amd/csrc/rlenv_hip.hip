@@ -926,21 +926,43 @@ __global__ void k_gather_rows(uint4* __restrict__ dst, const uint4* __restrict__
     for (size_t i = blockIdx.y * blockDim.x + threadIdx.x; i < row_vecs; i += (size_t)gridDim.y * blockDim.x) d[i] = s[i];
 }
 
-// Standalone reward10 SMB tracker: one env per lane, T steps; per step one 16-byte load and a 5-byte result.
-__global__ __launch_bounds__(256) void k_rl10_smb(const uint8_t* __restrict__ ram15, int T, int N, int frames,
-                                                  Rl10State* __restrict__ state, float* __restrict__ reward,
-                                                  uint8_t* __restrict__ done) {
+// Standalone reward10 SMB tracker: one env per lane, T steps; per step one 16-byte load and a 5-byte result. The loads
+// do not depend on the tracker, so they run ahead: two register buffers of kAhead steps each, one filled while the
+// other is consumed (a register move out of a buffer would wait for its load). 64-lane blocks spread the waves over
+// as many CUs as there are waves (8192 envs: 128 waves).
+constexpr int kAhead = 4;
+__device__ __forceinline__ void smb_step(const uint4& q, int frames, Rl10State& st, float* __restrict__ reward,
+                                         uint8_t* __restrict__ done, size_t at) {
+    uint8_t b[16];
+    memcpy(b, &q, 16);
+    const ev::Out u = ev::update(ev::smb_signals(b), frames, st, rl10_game(RL10_SMB));
+    reward[at] = (float)u.reward;
+    done[at] = u.done ? 1 : 0;
+}
+__global__ __launch_bounds__(64) void k_rl10_smb(const uint8_t* __restrict__ ram15, int T, int N, int frames,
+                                                 Rl10State* __restrict__ state, float* __restrict__ reward,
+                                                 uint8_t* __restrict__ done) {
     const int e = (int)(blockIdx.x * blockDim.x + threadIdx.x);
     if (e >= N) return;
+    const uint4* src = reinterpret_cast<const uint4*>(ram15);
+    // step t's 16 bytes (a step past the end reads the last one again, unused)
+    auto load = [&](int t) { return src[(size_t)min(t, T - 1) * N + e]; };
     Rl10State st = state[e];
-    for (int t = 0; t < T; ++t) {
-        const uint4 q = reinterpret_cast<const uint4*>(ram15)[(size_t)t * N + e];
-        uint8_t b[16];
-        memcpy(b, &q, 16);
-        const ev::Out u = ev::update(ev::smb_signals(b), frames, st, rl10_game(RL10_SMB));
-        reward[(size_t)t * N + e] = (float)u.reward;
-        done[(size_t)t * N + e] = u.done ? 1 : 0;
+    uint4 a[kAhead], b[kAhead];
+#pragma unroll
+    for (int j = 0; j < kAhead; ++j) a[j] = load(j);
+    int t = 0;
+    for (; t + 2 * kAhead <= T; t += 2 * kAhead) {
+#pragma unroll
+        for (int j = 0; j < kAhead; ++j) b[j] = load(t + kAhead + j);
+#pragma unroll
+        for (int j = 0; j < kAhead; ++j) smb_step(a[j], frames, st, reward, done, (size_t)(t + j) * N + e);
+#pragma unroll
+        for (int j = 0; j < kAhead; ++j) a[j] = load(t + 2 * kAhead + j);
+#pragma unroll
+        for (int j = 0; j < kAhead; ++j) smb_step(b[j], frames, st, reward, done, (size_t)(t + kAhead + j) * N + e);
     }
+    for (; t < T; ++t) smb_step(load(t), frames, st, reward, done, (size_t)t * N + e);   // the last T % 8 steps
     state[e] = st;
 }
 
@@ -1067,8 +1089,37 @@ struct KernelClock {
     }
 };
 
+// One stream per game (default priority) and the events that fork a call's work from the caller's stream onto them
+// and join it back (rl/csrc/rlenv.cu:38-40, 173-182): the games of a multi-game env step concurrently, so a batch of
+// many small games fills the GPU as one large game does. Created with the env (a call allocates nothing).
+struct GameStreams {
+    std::vector<hipStream_t> s;
+    std::vector<hipEvent_t> done;
+    hipEvent_t fork = nullptr;
+    void create(size_t n) {
+        if (hipEventCreateWithFlags(&fork, hipEventDisableTiming) != hipSuccess)
+            throw std::runtime_error("hipEventCreate failed");
+        for (size_t i = 0; i < n; ++i) {
+            hipStream_t st = nullptr;
+            hipEvent_t ev = nullptr;
+            if (hipStreamCreateWithFlags(&st, hipStreamNonBlocking) != hipSuccess)
+                throw std::runtime_error("hipStreamCreate failed");
+            s.push_back(st);
+            if (hipEventCreateWithFlags(&ev, hipEventDisableTiming) != hipSuccess)
+                throw std::runtime_error("hipEventCreate failed");
+            done.push_back(ev);
+        }
+    }
+    ~GameStreams() {
+        for (hipEvent_t ev : done) (void)hipEventDestroy(ev);
+        for (hipStream_t st : s) (void)hipStreamDestroy(st);
+        if (fork) (void)hipEventDestroy(fork);
+    }
+};
+
 struct Env {
     DevMem mem;
+    GameStreams gs;          // per-game streams when there is more than one game
     int device = 0;
     int total = 0;
     std::vector<GameH> games;
@@ -1095,6 +1146,27 @@ uint32_t* scratch_of(int device) {
         ptr[device] = static_cast<uint32_t*>(p);
     }
     return ptr[device];
+}
+
+// Runs f(game index, stream) for every game: on the caller's stream for a one-game env; otherwise each game on its
+// own stream, forked from and joined back to the caller's stream. Returns 0, or 1 with g_error set.
+template <class F>
+int for_games(Env& env, hipStream_t st, F&& f) {
+    const size_t n = env.games.size();
+    if (n == 1) {
+        f(0, st);
+        return 0;
+    }
+    bool bad = hipEventRecord(env.gs.fork, st) != hipSuccess;
+    for (size_t gi = 0; gi < n; ++gi) {
+        const hipStream_t gst = env.gs.s[gi];
+        bad |= hipStreamWaitEvent(gst, env.gs.fork, 0) != hipSuccess;
+        f(gi, gst);
+        bad |= hipEventRecord(env.gs.done[gi], gst) != hipSuccess;
+        bad |= hipStreamWaitEvent(st, env.gs.done[gi], 0) != hipSuccess;
+    }
+    if (bad) g_error = "fork/join of the game streams failed";
+    return bad ? 1 : 0;
 }
 
 // iNES -> cart description; the PRG is padded to a power of two by repeating a short image (NROM-128).
@@ -1469,6 +1541,7 @@ void* rlenv_create(int ngames, const int* game_ids, const uint8_t* const* roms, 
             env->games.push_back(gh);
             boot_game(*env, env->games.back(), boot_pads[i], boot_sizes[i]);
         }
+        if (env->games.size() > 1) env->gs.create(env->games.size());
         if (hipDeviceSynchronize() != hipSuccess || check("create")) throw std::runtime_error(g_error);
         return env;
     } catch (const std::exception& ex) {
@@ -1502,21 +1575,22 @@ void rlenv_bind_obs(void* h, uint8_t* obs, uint8_t* emph) {
 
 int rlenv_start(void* h, void* stream) {
     Env& env = *static_cast<Env*>(h);
-    const hipStream_t st = static_cast<hipStream_t>(stream);
-    for (auto& gh : env.games) {
-        const FinishArgs fa = finish_args(env, gh.k, 0, gh.k.n, env.o);
-        hipLaunchKernelGGL(k_start, dim3((gh.k.n + 255) / 256), dim3(256), 0, st, fa);
+    const int bad = for_games(env, static_cast<hipStream_t>(stream), [&](size_t gi, hipStream_t st) {
+        const GameK& g = env.games[gi].k;
+        const FinishArgs fa = finish_args(env, g, 0, g.n, env.o);
+        hipLaunchKernelGGL(k_start, dim3((g.n + 255) / 256), dim3(256), 0, st, fa);
         trace("start", st);
-        restart_phases(env, gh.k, env.o, 0, gh.k.n, st);
-    }
-    return check("start");
+        restart_phases(env, g, env.o, 0, g.n, st);
+    });
+    return bad ? 1 : check("start");
 }
 
 int rlenv_step(void* h, void* stream) {
     Env& env = *static_cast<Env*>(h);
-    const hipStream_t st = static_cast<hipStream_t>(stream);
-    for (auto& gh : env.games) decision_phases(env, gh.k, env.o, 0, gh.k.n, st);
-    return check("step");
+    const int bad = for_games(env, static_cast<hipStream_t>(stream), [&](size_t gi, hipStream_t st) {
+        decision_phases(env, env.games[gi].k, env.o, 0, env.games[gi].k.n, st);
+    });
+    return bad ? 1 : check("step");
 }
 
 int rlenv_step_static(void* h, void* stream) {
@@ -1526,15 +1600,14 @@ int rlenv_step_static(void* h, void* stream) {
                   " envs";
         return 1;
     }
-    const hipStream_t st = static_cast<hipStream_t>(stream);
-    for (size_t gi = 0; gi < env.games.size(); ++gi) {
+    const int bad = for_games(env, static_cast<hipStream_t>(stream), [&](size_t gi, hipStream_t st) {
         GameK g = env.games[gi].k;
         g.list = reinterpret_cast<int32_t*>(env.scratch + kStaticGames + g.offset);
         g.list_count = env.scratch + gi;
         hipLaunchKernelGGL(k_list_clear, dim3(1), dim3(1), 0, st, g.list_count);   // the last call's count
         decision_phases(env, g, env.o, 0, g.n, st);
-    }
-    return check("step_static");
+    });
+    return bad ? 1 : check("step_static");
 }
 
 int rlenv_step_game(void* h, int gi, uint8_t* obs, uint8_t* emph, void* stream) {
@@ -1778,7 +1851,7 @@ int rl_gather_envs(void* dst, const void* src, const int64_t* envs, int n, int T
 int rl10_smb_run(const uint8_t* ram15, int T, int N, int frames, void* state, float* reward, uint8_t* done,
                  void* stream) {
     if (N > 0)
-        hipLaunchKernelGGL(k_rl10_smb, dim3((N + 255) / 256), dim3(256), 0, static_cast<hipStream_t>(stream), ram15, T, N,
+        hipLaunchKernelGGL(k_rl10_smb, dim3((N + 63) / 64), dim3(64), 0, static_cast<hipStream_t>(stream), ram15, T, N,
                            frames, static_cast<Rl10State*>(state), reward, done);
     return check("rl10_smb_run");
 }
