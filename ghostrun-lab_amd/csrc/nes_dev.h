@@ -63,6 +63,9 @@ struct Cart {
     uint32_t board;
     uint32_t mirroring;     // header: 0 horizontal, 1 vertical
     uint32_t bus_conflicts; // UxROM / CNROM declared with AND-type bus conflicts (NES 2.0 submapper 2)
+    // CHR ROM again with each tile row's two plane bytes side by side (16-bit word page * 512 + (a & $3F0) / 2 +
+    // (a & 7) holds the bytes at a and a + 8), for the renderer's one-load pattern fetch; nullptr = CHR RAM
+    const uint16_t* chr_pairs;
 };
 
 // Instruction-fetch table (fast path): entry = {dispatch key, operand word}, two dwords: the opcode, or its hot key

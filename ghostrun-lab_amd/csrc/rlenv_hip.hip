@@ -280,8 +280,8 @@ struct RenderLds {
     uint32_t f[36];           // fetches: lo | hi << 8 | attribute << 16; 0-1 carried, 2 + j slot j
     uint32_t spr[2][8];       // sprite lines: lo | hi << 8 | attr << 16 | x << 24
     uint32_t pages[34 + 8];   // MMC2: the pages of each slot's fetch, then of each sprite's
-    uint8_t pal[32];
-    uint8_t spal[16];
+    alignas(4) uint8_t pal[32];
+    alignas(4) uint8_t spal[16];
 };
 
 typedef __attribute__((address_space(4))) const uint32_t KU32;
@@ -290,6 +290,7 @@ struct RenderSink {
     RenderLds* L;
     const uint32_t* log;      // the console's frame log (read-only in this kernel: scalar loads)
     const uint8_t *chr_rom, *chr_ram;
+    const uint16_t* chr_pairs;   // CHR ROM by tile row (both planes in one word), nullptr with CHR RAM
     int lane;
     bool mmc2;
     uint32_t ha, hb;          // F indices of the last two fetches
@@ -343,6 +344,14 @@ struct RenderSink {
         fill(out, n);
         __syncthreads();
     }
+    // The two plane bytes of pattern address pa (a row of plane 0; pa + 8 is plane 1) through the packed pages,
+    // plane 0 in the low byte: one 16-bit load with CHR ROM, two byte loads with CHR RAM.
+    __device__ uint32_t pattern(uint32_t lo, uint32_t hi, uint32_t pa) {
+        if (!chr_pairs) return chr_pk(chr_rom, chr_ram, lo, hi, pa) | (chr_pk(chr_rom, chr_ram, lo, hi, pa + 8u) << 8);
+        const uint32_t slot = (pa >> 10) & 7u;
+        const uint32_t page = ((slot & 4u ? hi : lo) >> ((slot & 3u) * 8u)) & 0xFFu;
+        return chr_pairs[page * 512u + ((pa & 0x3F0u) >> 1) + (pa & 7u)];
+    }
     // Slot j's tile (nametable tile and attribute, both pattern bytes) fetched at v into F[j + 2].
     __device__ void fetch_slot(const Rs& s, uint32_t v, uint32_t j, uint32_t lo, uint32_t hi) {
         const uint32_t ntb = 0x2000u | (v & 0x0C00u), col = v & 31u;
@@ -350,22 +359,33 @@ struct RenderSink {
         const uint32_t at = L->nt[nt_slot(s.nt_map, ntb | 0x3C0u | (col >> 2) | ((v & 0x380u) >> 4))];
         const uint32_t sel = (at >> ((col & 2u) | ((v & 0x40u) >> 4))) & 3u;
         const uint32_t pa = tile * 16u + ((s.ctrl & 0x10u) << 8) + ((v >> 12) & 7u);
-        L->f[j + 2u] = chr_pk(chr_rom, chr_ram, lo, hi, pa) | (chr_pk(chr_rom, chr_ram, lo, hi, pa + 8u) << 8) |
-                       (sel << 16);
+        L->f[j + 2u] = pattern(lo, hi, pa) | (sel << 16);
+    }
+    // The background palette as 16 bytes in four words, entry 4a + v: palette a's colour v, and for v = 0 the
+    // backdrop with bit 6 set (the transparency mark the sprite priority test reads). Wave-uniform.
+    __device__ void bg_table(uint32_t t[4]) {
+        const uint32_t b = back();
+        for (int i = 0; i < 4; ++i) t[i] = (uni(reinterpret_cast<const uint32_t*>(L->pal)[i]) & 0x3F3F3F00u) | b;
     }
     // 4 background pixels, leftmost in the low byte: kk0..kk0 + 3 of the 8 a slot shifts out from fetches p2 (older),
-    // p1 with fine x fx.
-    __device__ uint32_t shift4(uint32_t p2, uint32_t p1, uint32_t kk0, uint32_t fx, uint32_t back) {
+    // p1 with fine x fx; pixel q is bit 15 - fx - kk0 - q of the two 16-bit plane pairs, with p2's attribute while
+    // fx + kk0 + q < 8, else p1's. All four at once: the planes' 4 bits bit-reversed into place and spread one to a
+    // byte, the attribute chosen per byte by a mask, and the colours looked up 4 at a time by byte permutes of the
+    // palette table.
+    __device__ uint32_t shift4(uint32_t p2, uint32_t p1, uint32_t kk0, uint32_t fx, const uint32_t t[4]) {
+        const uint32_t sh = fx + kk0;   // 0..11
         const uint32_t lo16 = ((p2 & 0xFFu) << 8) | (p1 & 0xFFu), hi16 = (p2 & 0xFF00u) | ((p1 >> 8) & 0xFFu);
-        const uint32_t c2 = (p2 >> 16) & 3u, c1 = (p1 >> 16) & 3u;
-        uint32_t w = 0;
-        for (uint32_t q = 0; q < 4u; ++q) {
-            const uint32_t kk = kk0 + q, bit = 15u - fx - kk;
-            const uint32_t val = ((lo16 >> bit) & 1u) | (((hi16 >> bit) & 1u) << 1);
-            const uint32_t c = val ? (L->pal[(kk + fx < 8u ? c2 : c1) * 4u + val] & 0x3Fu) : back;
-            w |= c << (8u * q);
-        }
-        return w;
+        const uint32_t lo4 = __builtin_bitreverse32(lo16 << (16u + sh)) & 0xFu;   // pixel q at bit q
+        const uint32_t hi4 = __builtin_bitreverse32(hi16 << (16u + sh)) & 0xFu;
+        const uint32_t val = ((lo4 * 0x00204081u) & 0x01010101u) | (((hi4 * 0x00204081u) & 0x01010101u) << 1);
+        const int32_t b = 8 - (int32_t)sh;   // pixels q < b take p2's attribute
+        const uint32_t m = b >= 4 ? 0xFFFFFFFFu : b <= 0 ? 0u : (1u << (8 * b)) - 1u;
+        const uint32_t attr = ((((p2 >> 16) & 3u) * 0x01010101u) & m) | ((((p1 >> 16) & 3u) * 0x01010101u) & ~m);
+        const uint32_t idx = (attr << 2) | val;   // palette entry per byte, 0..15
+        const uint32_t sel = idx & 0x07070707u;
+        const uint32_t lo = __builtin_amdgcn_perm(t[1], t[0], sel), hi = __builtin_amdgcn_perm(t[3], t[2], sel);
+        const uint32_t mh = ((idx >> 3) & 0x01010101u) * 0xFFu;
+        return (lo & ~mh) | (hi & mh);
     }
     __device__ void on_run(const Rs& s, int32_t first, int32_t last, int32_t out, bool pixels) {
         __syncthreads();   // the walker's page and palette writes
@@ -383,7 +403,9 @@ struct RenderSink {
                 const int32_t j = k - first;
                 const uint32_t p1 = L->f[j >= 1 ? (uint32_t)k + 1u : hb];
                 const uint32_t p2 = L->f[j >= 2 ? (uint32_t)k : (j == 1 ? hb : ha)];
-                L->px[lane] = shift4(p2, p1, (uint32_t)((x - out) & 7), s.fx, back());
+                uint32_t t[4];
+                bg_table(t);
+                L->px[lane] = shift4(p2, p1, (uint32_t)((x - out) & 7), s.fx, t);
             }
             const bool clip = first <= 2 && last > 2 && !(s.mask & 0x02u), bg_off = !(s.mask & 0x08u);
             if (clip || bg_off) {
@@ -433,8 +455,7 @@ struct RenderSink {
             pa &= 0x1FFFu;
             const uint32_t pk = mmc2 ? L->pages[34 + rank] : 0u;
             const uint32_t lo = mmc2 ? pk : s.chr_lo, hi = mmc2 ? pk : s.chr_hi;
-            L->spr[target][rank] = chr_pk(chr_rom, chr_ram, lo, hi, pa) |
-                                   (chr_pk(chr_rom, chr_ram, lo, hi, pa + 8u) << 8) | (e & 0xFFFF0000u);
+            L->spr[target][rank] = pattern(lo, hi, pa) | (e & 0xFFFF0000u);
         }
         fetched = target;
         return sel;
@@ -475,17 +496,20 @@ struct RenderSink {
             const uint4 sp = reinterpret_cast<const uint4*>(L->sp)[lane];
             reinterpret_cast<uint4*>(L->sp)[lane] = make_uint4(0u, 0u, 0u, 0u);
             if (sprites) {
-                const uint32_t g[4] = {sp.x, sp.y, sp.z, sp.w};
-                const uint32_t xstart = (s.mask & 0x04u) ? 0u : 8u;
-                uint32_t out = 0;
-                for (uint32_t q = 0; q < 4u; ++q) {
-                    uint32_t c = (w >> (8u * q)) & 0xFFu;
-                    const uint32_t e = g[q];
-                    const bool show = e != 0u && 4u * (uint32_t)lane + q >= xstart && (!(e & 0x80u) || (c & 0x40u));
-                    c = show ? L->spal[e & 0x0Fu] : c;
-                    out |= c << (8u * q);
-                }
-                w = out;
+                // the four pixels at once, one per byte: a sprite pixel (value != 0) shows in front, or behind a
+                // transparent background pixel (bit 6, the backdrop mark), except in the left 8 with sprite
+                // clipping; its colour from the latched sprite palette by byte permutes (entry = palette << 2 | value)
+                const uint32_t eb = (sp.x & 0xFFu) | ((sp.y & 0xFFu) << 8) | ((sp.z & 0xFFu) << 16) | (sp.w << 24);
+                const uint32_t opaque = (eb | (eb >> 1)) & 0x01010101u;
+                const uint32_t front = ~(eb >> 7) & 0x01010101u, clear_bg = (w >> 6) & 0x01010101u;
+                const bool clipped = !(s.mask & 0x04u) && lane < 2;
+                const uint32_t show = clipped ? 0u : (opaque & (front | clear_bg)) * 0xFFu;
+                uint32_t t[4];
+                for (int i = 0; i < 4; ++i) t[i] = uni(reinterpret_cast<const uint32_t*>(L->spal)[i]);
+                const uint32_t sel = eb & 0x07070707u;
+                const uint32_t lo = __builtin_amdgcn_perm(t[1], t[0], sel), hi = __builtin_amdgcn_perm(t[3], t[2], sel);
+                const uint32_t hm = ((eb >> 3) & 0x01010101u) * 0xFFu;
+                w = (w & ~show) | (((lo & ~hm) | (hi & hm)) & show);
             }
         }
         if (l < 8) return;
@@ -507,11 +531,12 @@ struct RenderSink {
         }
         expand_sprites(s);
         __syncthreads();
-        const uint32_t back = this->back();
-        uint32_t w = back * 0x01010101u;
+        uint32_t t[4];
+        bg_table(t);
+        uint32_t w = (t[0] & 0xFFu) * 0x01010101u;   // the backdrop
         if (rend && (s.mask & 0x08u) && (lane >= 2 || (s.mask & 0x02u))) {
             const uint32_t k = (uint32_t)lane / 2u + 2u;
-            w = shift4(L->f[k], L->f[k + 1u], ((uint32_t)lane & 1u) * 4u, s.fx, back);
+            w = shift4(L->f[k], L->f[k + 1u], ((uint32_t)lane & 1u) * 4u, s.fx, t);
         }
         compose(s, l, w, obs, emph);
         // the end of the line: Fixit1 and Fixit2 (v from t horizontally), the next line's sprites, RefreshSprites
@@ -559,7 +584,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(8, 8))) void
     reinterpret_cast<uint4*>(L.sp)[lane] = make_uint4(0u, 0u, 0u, 0u);
     __syncthreads();
     const bool mmc2 = a.g.cart.board == NES_BOARD_MMC2;
-    RenderSink sink{&L, rec->log, a.g.cart.chr, rec->chr_ram, lane, mmc2, 0u, 1u, 0u, 0u, 0u};
+    RenderSink sink{&L, rec->log, a.g.cart.chr, rec->chr_ram, a.g.cart.chr_pairs, lane, mmc2, 0u, 1u, 0u, 0u, 0u};
     Rs s;
     rs_load(s, sink, rec->log, rec->log_n, mmc2 ? a.g.cart.chr_pages1 : 0u);
     rs_begin_frame(s, sink);
@@ -1504,9 +1529,16 @@ void* rlenv_create(int ngames, const int* game_ids, const uint8_t* const* roms, 
             uint32_t* prgw = static_cast<uint32_t*>(env->mem.alloc(wide.size() * 4));
             env->mem.upload(prgw, wide.data(), wide.size() * 4);
             uint8_t* chr = nullptr;
+            uint16_t* chr_pairs = nullptr;
             if (!p.chr.empty()) {
                 chr = static_cast<uint8_t*>(env->mem.alloc(p.chr.size()));
                 env->mem.upload(chr, p.chr.data(), p.chr.size());
+                std::vector<uint16_t> pairs(p.chr.size() / 2);   // per 16-byte tile: row r = plane 0 | plane 1 << 8
+                for (size_t t = 0; t < p.chr.size(); t += 16)
+                    for (size_t r = 0; r < 8; ++r)
+                        pairs[t / 2 + r] = (uint16_t)(p.chr[t + r] | (p.chr[t + 8 + r] << 8));
+                chr_pairs = static_cast<uint16_t*>(env->mem.alloc(p.chr.size()));
+                env->mem.upload(chr_pairs, pairs.data(), p.chr.size());
             }
             uint32_t chr_pages = p.chr.empty() ? 8u : (uint32_t)(p.chr.size() / 1024u);
             if (chr_pages & (chr_pages - 1u)) throw std::runtime_error("CHR size must be a power of two");
@@ -1528,7 +1560,7 @@ void* rlenv_create(int ngames, const int* game_ids, const uint8_t* const* roms, 
             uint32_t* fetchw = static_cast<uint32_t*>(env->mem.alloc(f.size() * 4));
             env->mem.upload(fetchw, f.data(), f.size() * 4);
             g.cart = Cart{prgw, fetchw, chr, (uint32_t)(p.prg.size() / 8192u), chr_pages, p.board, p.mirroring,
-                          p.bus_conflicts};
+                          p.bus_conflicts, chr_pairs};
             g.recs = env->mem.zeros<NesRec>((size_t)g.n + 1);
             g.idle = env->mem.zeros<NesRec>((size_t)std::max(env->s.idle_tmpl, 1));
             const size_t tmpl = (size_t)env->s.idle_tmpl + 1;
