@@ -347,7 +347,7 @@ def _roofline(name, kern, n, K, dt, out_bytes, ips):
     d = kern[dom]
     step_gbps = out_bytes * n * K / dt / 1e9
     r = dict(kernel=dom, bound='hbm', achieved=d['achieved_gbps'], peak=HBM_PEAK_GBPS, unit='GB/s',
-             frac=round(d['achieved_gbps'] / HBM_PEAK_GBPS, 6), traffic=_traffic(dom, n),
+             frac=round(d['achieved_gbps'] / HBM_PEAK_GBPS, 6), traffic=_traffic(dom, n) if name == HEADLINE else None,
              step_achieved_gbps=round(step_gbps, 3), step_frac=round(step_gbps / HBM_PEAK_GBPS, 6))
     c = (_counters(name) or {}).get('k_emu')
     emu = kern.get('k_emu')
