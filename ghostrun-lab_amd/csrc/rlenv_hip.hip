@@ -86,6 +86,18 @@ struct LevelK {
     int weighted;                    // 1: pick by cdf, 0: uniform over the saved slots
 };
 
+// What the renderer needs of one console-frame, copied out of the record by the emulator kernel at the frame's vblank
+// stop: the frame log and its event count, the nametables and the OAM (CHR RAM, on carts that have it, in a parallel
+// array). One bank per frame of a decision, so that frame f is drawn from its bank while the frames after it are
+// emulated.
+struct FrameBank {
+    uint32_t log[NES_LOG_WORDS];
+    uint32_t log_n, unused[3];
+    uint8_t nt[NES_NT_BYTES];
+    uint8_t oam[NES_OAM_BYTES];
+};
+static_assert(sizeof(FrameBank) % 16 == 0 && (NES_LOG_WORDS * 4) % 16 == 0, "16-byte copies");
+
 struct GameK {
     NesRec* recs;          // n + 1 records, slot n = boot snapshot
     const NesRec* idle;    // idle templates
@@ -104,6 +116,8 @@ struct GameK {
     int32_t* list;         // restart list (env index within the game)
     uint32_t* list_count;
     LevelK lv;
+    FrameBank* bank[RLE_FRAMES];     // [n] per frame of a decision
+    uint8_t* bank_chr[RLE_FRAMES];   // [n][NES_CHRRAM_BYTES] per frame, CHR RAM carts only (else nullptr)
 };
 
 // EMU_TEMPLATE: one frame of every restart template (block k = template k, pad 0, target boot_target + k frames,
@@ -121,6 +135,8 @@ struct EmuArgs {
     uint64_t boot_target;
     uint32_t* boot_fault;
     uint32_t budget;       // instructions per frame (NES_BUDGET; smaller only for diagnostics)
+    FrameBank* bank;       // decision frames drawn from a bank: the bank this frame's render state goes to
+    uint8_t* bank_chr;
 };
 
 __device__ __forceinline__ int slot_count(const GameK& g, int use_list, int e0, int e1) {
@@ -180,7 +196,8 @@ struct WaveLds {
 // LDS, the 64 lanes copy them in and out. Eight waves per SIMD: 8192 consoles fill 256 CUs x 4 SIMDs x 8 in one
 // round (left to itself the compiler takes 71 VGPRs, 7 waves, and the eighth wave of every SIMD runs after the
 // others).
-template <uint32_t B>
+// kBank: a decision frame whose picture is drawn from a frame bank (its render state is copied there at the end).
+template <uint32_t B, bool kBank>
 __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(8, 8))) void k_emu_w(EmuArgs a) {
     __shared__ __align__(16) WaveLds L;
     const int count = a.mode == EMU_BOOT ? 1 : slot_count(a.g, a.use_list, a.e0, a.e1);
@@ -245,6 +262,14 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(8, 8))) void
     wave_copy16(rec->nt, L.nt, NES_NT_BYTES, lane);
     wave_copy16(rec->oam, L.oam, NES_OAM_BYTES, lane);
     wave_copy16(rec->pal, L.pal, NES_PAL_BYTES, lane);
+    if constexpr (kBank) {   // the frame's render state (the log lane 0 wrote before the sync above)
+        FrameBank* b = &a.bank[e];
+        wave_copy16(b->log, rec->log, NES_LOG_WORDS * 4u, lane);
+        wave_copy16(b->nt, L.nt, NES_NT_BYTES, lane);
+        wave_copy16(b->oam, L.oam, NES_OAM_BYTES, lane);
+        if (lane == 0) b->log_n = L.cs.log_n;
+        if (a.bank_chr) wave_copy16(a.bank_chr + (size_t)e * NES_CHRRAM_BYTES, rec->chr_ram, NES_CHRRAM_BYTES, lane);
+    }
 }
 
 // Power-on of one console record.
@@ -259,6 +284,8 @@ struct RenderArgs {
     Outs o;
     Settings s;
     int f, use_list, restart_pass, e0, e1;
+    const FrameBank* bank;       // draw from this bank (nullptr: from the record)
+    const uint8_t* bank_chr;
 };
 
 // The renderer's side of the line replay (replay_dev.h): the walker runs wave-uniform on every lane and hands each run
@@ -565,6 +592,7 @@ struct RenderSink {
 
 // One console-frame per wavefront (blockDim 64): the picture of the frame the console has logged, drawn from its
 // nametables and OAM as of the frame's vblank stop.
+template <bool kBank>
 __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(8, 8))) void k_render(RenderArgs a) {
     __shared__ __align__(16) RenderLds L;
     const int count = slot_count(a.g, a.use_list, a.e0, a.e1);
@@ -576,17 +604,21 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(8, 8))) void
     if (a.s.no_render) return;
     const int lane = (int)threadIdx.x;
     const NesRec* rec = &a.g.recs[e];
-    wave_copy16(L.nt, rec->nt, NES_NT_BYTES, lane);
-    wave_copy16(L.oam, rec->oam, NES_OAM_BYTES, lane);
-    if (lane < 8) reinterpret_cast<uint32_t*>(L.pal)[lane] = rec->log[6 + lane];
+    const FrameBank* bk = kBank ? &a.bank[e] : nullptr;
+    const uint32_t* log = kBank ? bk->log : rec->log;
+    const uint32_t log_n = kBank ? bk->log_n : rec->log_n;
+    const uint8_t* chr_ram = kBank && a.bank_chr ? a.bank_chr + (size_t)e * NES_CHRRAM_BYTES : rec->chr_ram;
+    wave_copy16(L.nt, kBank ? bk->nt : rec->nt, NES_NT_BYTES, lane);
+    wave_copy16(L.oam, kBank ? bk->oam : rec->oam, NES_OAM_BYTES, lane);
+    if (lane < 8) reinterpret_cast<uint32_t*>(L.pal)[lane] = log[6 + lane];
     if (lane < 2) L.f[lane] = 0;
     if (lane < 16) L.spr[lane >> 3][lane & 7] = 0;
     reinterpret_cast<uint4*>(L.sp)[lane] = make_uint4(0u, 0u, 0u, 0u);
     __syncthreads();
     const bool mmc2 = a.g.cart.board == NES_BOARD_MMC2;
-    RenderSink sink{&L, rec->log, a.g.cart.chr, rec->chr_ram, a.g.cart.chr_pairs, lane, mmc2, 0u, 1u, 0u, 0u, 0u};
+    RenderSink sink{&L, log, a.g.cart.chr, chr_ram, a.g.cart.chr_pairs, lane, mmc2, 0u, 1u, 0u, 0u, 0u};
     Rs s;
-    rs_load(s, sink, rec->log, rec->log_n, mmc2 ? a.g.cart.chr_pages1 : 0u);
+    rs_load(s, sink, log, uni(log_n), mmc2 ? a.g.cart.chr_pages1 : 0u);
     rs_begin_frame(s, sink);
     uint8_t* obs = a.o.obs + ((size_t)ge * RLE_FRAMES + a.f) * RLE_OBS_PIXELS;
     uint8_t* emph = a.o.emph + ((size_t)ge * RLE_FRAMES + a.f) * RLE_OBS_H;
@@ -1114,37 +1146,62 @@ struct KernelClock {
     }
 };
 
-// One stream per game (default priority) and the events that fork a call's work from the caller's stream onto them
-// and join it back (rl/csrc/rlenv.cu:38-40, 173-182): the games of a multi-game env step concurrently, so a batch of
-// many small games fills the GPU as one large game does. Created with the env (a call allocates nothing).
+// Streams and events, all at the default priority and created with the env (a call allocates nothing):
+// * with more than one game, one stream per game and the events that fork a call's work from the caller's stream
+//   onto them and join it back (rl/csrc/rlenv.cu:38-40, 173-182): the games step concurrently, so a batch of many
+//   small games fills the GPU as one large game does;
+// * with one game, a render stream, per decision frame f an "emulated" event and one "drawn" event: frame f is drawn
+//   on the render stream from its frame bank while the frames after it are emulated on the caller's stream.
+struct RenderPipe {
+    hipStream_t stream = nullptr;
+    hipEvent_t emulated[RLE_FRAMES] = {}, drawn = nullptr;
+};
 struct GameStreams {
     std::vector<hipStream_t> s;
     std::vector<hipEvent_t> done;
+    std::vector<RenderPipe> render;
     hipEvent_t fork = nullptr;
+    static hipEvent_t event() {
+        hipEvent_t ev = nullptr;
+        if (hipEventCreateWithFlags(&ev, hipEventDisableTiming) != hipSuccess) throw std::runtime_error("hipEventCreate failed");
+        return ev;
+    }
+    static hipStream_t stream() {
+        hipStream_t st = nullptr;
+        if (hipStreamCreateWithFlags(&st, hipStreamNonBlocking) != hipSuccess) throw std::runtime_error("hipStreamCreate failed");
+        return st;
+    }
     void create(size_t n) {
-        if (hipEventCreateWithFlags(&fork, hipEventDisableTiming) != hipSuccess)
-            throw std::runtime_error("hipEventCreate failed");
+        render.resize(n);
+        if (n == 1) {
+            render[0].stream = stream();
+            for (int f = 0; f < RLE_FRAMES; ++f) render[0].emulated[f] = event();
+            render[0].drawn = event();
+            return;
+        }
+        fork = event();
         for (size_t i = 0; i < n; ++i) {
-            hipStream_t st = nullptr;
-            hipEvent_t ev = nullptr;
-            if (hipStreamCreateWithFlags(&st, hipStreamNonBlocking) != hipSuccess)
-                throw std::runtime_error("hipStreamCreate failed");
-            s.push_back(st);
-            if (hipEventCreateWithFlags(&ev, hipEventDisableTiming) != hipSuccess)
-                throw std::runtime_error("hipEventCreate failed");
-            done.push_back(ev);
+            s.push_back(stream());
+            done.push_back(event());
         }
     }
     ~GameStreams() {
         for (hipEvent_t ev : done) (void)hipEventDestroy(ev);
         for (hipStream_t st : s) (void)hipStreamDestroy(st);
+        for (RenderPipe& p : render) {
+            for (int f = 0; f < RLE_FRAMES; ++f)
+                if (p.emulated[f]) (void)hipEventDestroy(p.emulated[f]);
+            if (p.drawn) (void)hipEventDestroy(p.drawn);
+            if (p.stream) (void)hipStreamDestroy(p.stream);
+        }
         if (fork) (void)hipEventDestroy(fork);
     }
 };
 
 struct Env {
     DevMem mem;
-    GameStreams gs;          // per-game streams when there is more than one game
+    GameStreams gs;          // per-game streams (with more than one game) and render pipes
+    int one_round = 8192;    // one-console waves the GPU holds at once: CUs x 4 SIMDs x 8 waves
     int device = 0;
     int total = 0;
     std::vector<GameH> games;
@@ -1255,29 +1312,36 @@ FinishArgs finish_args(const Env& env, const GameK& g, int e0, int e1, const Out
 }
 
 void launch_emu(const Env& env, const GameK& g, const Outs& o, int mode, int f, bool use_list, int e0, int e1,
-                hipStream_t st) {
-    EmuArgs a{g, env.e, o, env.s, env.optab, mode, f, use_list ? 1 : 0, e0, e1, 0, 0, nullptr, env.budget};
+                hipStream_t st, int bank = -1) {
+    EmuArgs a{g, env.e, o, env.s, env.optab, mode, f, use_list ? 1 : 0, e0, e1, 0, 0, nullptr, env.budget,
+              bank >= 0 ? g.bank[bank] : nullptr, bank >= 0 ? g.bank_chr[bank] : nullptr};
     const int blocks = use_list ? g.n : e1 - e0;
     const int cls = mode == EMU_DECISION ? KC_EMU : mode == EMU_IDLE ? KC_EMU_IDLE : KC_EMU_RESTART;
     if (blocks > 0)
         env.clock.run(cls, st, [&] {
             // the fast path knows two kinds of board: fixed 32 KB PRG (NROM, CNROM) and banked PRG (the rest)
-            if (g.cart.board == NES_BOARD_NROM || g.cart.board == NES_BOARD_CNROM)
-                hipLaunchKernelGGL(k_emu_w<NES_BOARD_NROM>, dim3(blocks), dim3(64), 0, st, a);
-            else
-                hipLaunchKernelGGL(k_emu_w<NES_BOARD_MMC3>, dim3(blocks), dim3(64), 0, st, a);
+            const bool nrom = g.cart.board == NES_BOARD_NROM || g.cart.board == NES_BOARD_CNROM;
+            if (a.bank) {
+                if (nrom) hipLaunchKernelGGL((k_emu_w<NES_BOARD_NROM, true>), dim3(blocks), dim3(64), 0, st, a);
+                else hipLaunchKernelGGL((k_emu_w<NES_BOARD_MMC3, true>), dim3(blocks), dim3(64), 0, st, a);
+            } else {
+                if (nrom) hipLaunchKernelGGL((k_emu_w<NES_BOARD_NROM, false>), dim3(blocks), dim3(64), 0, st, a);
+                else hipLaunchKernelGGL((k_emu_w<NES_BOARD_MMC3, false>), dim3(blocks), dim3(64), 0, st, a);
+            }
         });
     trace(mode == EMU_DECISION ? "emu" : mode == EMU_IDLE ? "emu_idle" : "emu_restart", st);
 }
 
 void launch_render(const Env& env, const GameK& g, const Outs& o, int f, bool use_list, bool restart, int e0, int e1,
-                   hipStream_t st) {
-    RenderArgs a{g, env.e, o, env.s, f, use_list ? 1 : 0, restart ? 1 : 0, e0, e1};
+                   hipStream_t st, int bank = -1) {
+    RenderArgs a{g, env.e, o, env.s, f, use_list ? 1 : 0, restart ? 1 : 0, e0, e1,
+                 bank >= 0 ? g.bank[bank] : nullptr, bank >= 0 ? g.bank_chr[bank] : nullptr};
     const int n = use_list ? g.n : e1 - e0;
     if (n > 0)
         env.clock.run(restart ? KC_RENDER_RESTART : KC_RENDER, st,
                       [&] {
-                          hipLaunchKernelGGL(k_render, dim3(n), dim3(64), 0, st, a);
+                          if (a.bank) hipLaunchKernelGGL(k_render<true>, dim3(n), dim3(64), 0, st, a);
+                          else hipLaunchKernelGGL(k_render<false>, dim3(n), dim3(64), 0, st, a);
                       });
     trace(restart ? "render_restart" : "render", st);
 }
@@ -1307,13 +1371,31 @@ void restart_phases(const Env& env, const GameK& g, const Outs& o, int e0, int e
 }
 
 
-void decision_phases(const Env& env, const GameK& g, const Outs& o, int e0, int e1, hipStream_t st) {
+// A decision of envs [e0, e1) of game g: 4 frames, then the finish, the level saves and the restart pass.
+// Pipelined (a one-game env whose frame launch fits in one round of waves, so that waves retiring from the
+// emulator leave CU slots idle): frame f is drawn on the game's render stream from frame bank f while the frames
+// after it are emulated on `st`, and the restart pass, which writes the pictures of restarted envs, waits until
+// every frame is drawn (so does the next decision, which refills the banks, through it). Otherwise each frame is
+// drawn on `st` after it is emulated: with several rounds of waves, or with other games' streams, the CUs are
+// already kept busy.
+void decision_phases(const Env& env, const GameK& g, const RenderPipe& p, const Outs& o, int e0, int e1,
+                     hipStream_t st) {
     const int n = e1 - e0;
     if (n <= 0) return;
+    const bool draw = !env.s.no_render;
+    const bool pipelined = draw && env.games.size() == 1 && n <= env.one_round;
     for (int f = 0; f < RLE_FRAMES; ++f) {
-        launch_emu(env, g, o, EMU_DECISION, f, false, e0, e1, st);
-        launch_render(env, g, o, f, false, false, e0, e1, st);
+        if (!pipelined) {
+            launch_emu(env, g, o, EMU_DECISION, f, false, e0, e1, st);
+            launch_render(env, g, o, f, false, false, e0, e1, st);
+            continue;
+        }
+        launch_emu(env, g, o, EMU_DECISION, f, false, e0, e1, st, f);
+        (void)hipEventRecord(p.emulated[f], st);
+        (void)hipStreamWaitEvent(p.stream, p.emulated[f], 0);
+        launch_render(env, g, o, f, false, false, e0, e1, p.stream, f);
     }
+    if (pipelined) (void)hipEventRecord(p.drawn, p.stream);
     const FinishArgs fa = finish_args(env, g, e0, e1, o);
     env.clock.run(KC_FINISH, st, [&] { hipLaunchKernelGGL(k_finish, dim3((n + 255) / 256), dim3(256), 0, st, fa); });
     trace("finish", st);
@@ -1322,6 +1404,7 @@ void decision_phases(const Env& env, const GameK& g, const Outs& o, int e0, int 
                       [&] { hipLaunchKernelGGL(k_archive, dim3(g.lv.levels), dim3(256), 0, st, fa); });
         trace("archive", st);
     }
+    if (pipelined) (void)hipStreamWaitEvent(st, p.drawn, 0);
     restart_phases(env, g, o, e0, e1, st);
 }
 
@@ -1378,11 +1461,11 @@ void build_restart_templates(Env& env, GameK& g) {
         const EmuArgs a{t, env.e, o, s, env.optab, EMU_TEMPLATE, f, 0, 0, count, 0,
                         g.tmpl_target + (uint64_t)f * NES_FRAME_DOTS, const_cast<uint32_t*>(g.rst_fault), env.budget};
         if (g.cart.board == NES_BOARD_NROM || g.cart.board == NES_BOARD_CNROM)
-            hipLaunchKernelGGL(k_emu_w<NES_BOARD_NROM>, dim3(count), dim3(64), 0, 0, a);
+            hipLaunchKernelGGL((k_emu_w<NES_BOARD_NROM, false>), dim3(count), dim3(64), 0, 0, a);
         else
-            hipLaunchKernelGGL(k_emu_w<NES_BOARD_MMC3>, dim3(count), dim3(64), 0, 0, a);
+            hipLaunchKernelGGL((k_emu_w<NES_BOARD_MMC3, false>), dim3(count), dim3(64), 0, 0, a);
         const RenderArgs r{t, env.e, o, s, f, 0, 0, 0, count};
-        hipLaunchKernelGGL(k_render, dim3(count), dim3(64), 0, 0, r);
+        hipLaunchKernelGGL(k_render<false>, dim3(count), dim3(64), 0, 0, r);
     }
     if (hipDeviceSynchronize() != hipSuccess || check("restart templates")) throw std::runtime_error(g_error);
 }
@@ -1399,9 +1482,9 @@ void boot_game(Env& env, GameH& gh, const uint8_t* pads, size_t npads) {
         EmuArgs a{one, env.e, env.o, env.s, env.optab, EMU_BOOT, 0, 0, index, index + 1, pad, target, fault,
                   env.budget};
         if (g.cart.board == NES_BOARD_NROM || g.cart.board == NES_BOARD_CNROM)
-            hipLaunchKernelGGL(k_emu_w<NES_BOARD_NROM>, dim3(1), dim3(64), 0, 0, a);
+            hipLaunchKernelGGL((k_emu_w<NES_BOARD_NROM, false>), dim3(1), dim3(64), 0, 0, a);
         else
-            hipLaunchKernelGGL(k_emu_w<NES_BOARD_MMC3>, dim3(1), dim3(64), 0, 0, a);
+            hipLaunchKernelGGL((k_emu_w<NES_BOARD_MMC3, false>), dim3(1), dim3(64), 0, 0, a);
         target += NES_FRAME_DOTS;
     };
     for (size_t i = 0; i < npads; ++i) frame(g.recs, g.n, pads[i]);
@@ -1461,6 +1544,9 @@ void* rlenv_create(int ngames, const int* game_ids, const uint8_t* const* roms, 
         env = new Env();
         env->device = device;
         env->scratch = scratch_of(device);
+        int cus = 0;
+        if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device) == hipSuccess && cus > 0)
+            env->one_round = cus * 32;
         if (const char* v = std::getenv("RLENV_BUDGET")) env->budget = (uint32_t)std::max(1, std::min((int)NES_BUDGET, std::atoi(v)));
         env->s.run_seed = run_seed;
         env->s.sticky = sticky;
@@ -1568,12 +1654,16 @@ void* rlenv_create(int ngames, const int* game_ids, const uint8_t* const* roms, 
             g.rst_obs = env->mem.zeros<uint8_t>(tmpl * RLE_FRAMES * RLE_OBS_PIXELS);
             g.rst_emph = env->mem.zeros<uint8_t>(tmpl * RLE_FRAMES * RLE_OBS_H);
             g.rst_fault = env->mem.zeros<uint32_t>(tmpl);
+            for (int b = 0; b < RLE_FRAMES; ++b) {
+                g.bank[b] = env->mem.zeros<FrameBank>((size_t)std::max(g.n, 1));
+                g.bank_chr[b] = g.cart.chr ? nullptr : env->mem.zeros<uint8_t>((size_t)g.n * NES_CHRRAM_BYTES);
+            }
             g.list = env->mem.zeros<int32_t>((size_t)std::max(g.n, 1));
             g.list_count = env->mem.zeros<uint32_t>(1);
             env->games.push_back(gh);
             boot_game(*env, env->games.back(), boot_pads[i], boot_sizes[i]);
         }
-        if (env->games.size() > 1) env->gs.create(env->games.size());
+        env->gs.create(env->games.size());
         if (hipDeviceSynchronize() != hipSuccess || check("create")) throw std::runtime_error(g_error);
         return env;
     } catch (const std::exception& ex) {
@@ -1620,7 +1710,7 @@ int rlenv_start(void* h, void* stream) {
 int rlenv_step(void* h, void* stream) {
     Env& env = *static_cast<Env*>(h);
     const int bad = for_games(env, static_cast<hipStream_t>(stream), [&](size_t gi, hipStream_t st) {
-        decision_phases(env, env.games[gi].k, env.o, 0, env.games[gi].k.n, st);
+        decision_phases(env, env.games[gi].k, env.gs.render[gi], env.o, 0, env.games[gi].k.n, st);
     });
     return bad ? 1 : check("step");
 }
@@ -1637,7 +1727,7 @@ int rlenv_step_static(void* h, void* stream) {
         g.list = reinterpret_cast<int32_t*>(env.scratch + kStaticGames + g.offset);
         g.list_count = env.scratch + gi;
         hipLaunchKernelGGL(k_list_clear, dim3(1), dim3(1), 0, st, g.list_count);   // the last call's count
-        decision_phases(env, g, env.o, 0, g.n, st);
+        decision_phases(env, g, env.gs.render[gi], env.o, 0, g.n, st);
     });
     return bad ? 1 : check("step_static");
 }
@@ -1648,7 +1738,7 @@ int rlenv_step_game(void* h, int gi, uint8_t* obs, uint8_t* emph, void* stream) 
     Outs o = env.o;
     o.obs = obs;
     o.emph = emph;
-    decision_phases(env, env.games[gi].k, o, 0, env.games[gi].k.n, static_cast<hipStream_t>(stream));
+    decision_phases(env, env.games[gi].k, env.gs.render[gi], o, 0, env.games[gi].k.n, static_cast<hipStream_t>(stream));
     return check("step_game");
 }
 
@@ -1660,7 +1750,7 @@ int rlenv_step_range(void* h, int gi, int start, int count, uint8_t* obs, uint8_
     Outs o = env.o;
     o.obs = obs;
     o.emph = emph;
-    decision_phases(env, g, o, start, start + count, static_cast<hipStream_t>(stream));
+    decision_phases(env, g, env.gs.render[gi], o, start, start + count, static_cast<hipStream_t>(stream));
     return check("step_range");
 }
 
