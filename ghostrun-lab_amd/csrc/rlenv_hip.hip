@@ -308,7 +308,6 @@ struct RenderLds {
     uint32_t spr[2][8];       // sprite lines: lo | hi << 8 | attr << 16 | x << 24
     uint32_t pages[34 + 8];   // MMC2: the pages of each slot's fetch, then of each sprite's
     alignas(4) uint8_t pal[32];
-    alignas(4) uint8_t spal[16];
 };
 
 typedef __attribute__((address_space(4))) const uint32_t KU32;
@@ -322,6 +321,10 @@ struct RenderSink {
     bool mmc2;
     uint32_t ha, hb;          // F indices of the last two fetches
     uint32_t fetched, drawn, drawn_n;
+    // the background palette table (bg_table) and the latched sprite palette (latch_sprites), wave-uniform, rebuilt
+    // only after a palette write
+    uint32_t bgt[4], spt[4];
+    bool bg_stale, sp_stale;
 
     __device__ uint32_t ev(uint32_t i) { return ((KU32*)(log + NES_LOG_HDR_WORDS))[i]; }
     __device__ uint32_t nt(uint32_t i) { return uni(L->nt[i]); }
@@ -330,6 +333,7 @@ struct RenderSink {
     __device__ void palette(uint32_t i, uint32_t v) {
         if (lane == 0) L->pal[i] = (uint8_t)v;
         __syncthreads();
+        bg_stale = sp_stale = true;
     }
     __device__ void slot_pages(int32_t j, uint32_t pk) {
         if (lane == 0) L->pages[j] = pk;
@@ -391,8 +395,12 @@ struct RenderSink {
     // The background palette as 16 bytes in four words, entry 4a + v: palette a's colour v, and for v = 0 the
     // backdrop with bit 6 set (the transparency mark the sprite priority test reads). Wave-uniform.
     __device__ void bg_table(uint32_t t[4]) {
-        const uint32_t b = back();
-        for (int i = 0; i < 4; ++i) t[i] = (uni(reinterpret_cast<const uint32_t*>(L->pal)[i]) & 0x3F3F3F00u) | b;
+        if (bg_stale) {
+            const uint32_t b = back();
+            for (int i = 0; i < 4; ++i) bgt[i] = (uni(reinterpret_cast<const uint32_t*>(L->pal)[i]) & 0x3F3F3F00u) | b;
+            bg_stale = false;
+        }
+        for (int i = 0; i < 4; ++i) t[i] = bgt[i];
     }
     // 4 background pixels, leftmost in the low byte: kk0..kk0 + 3 of the 8 a slot shifts out from fetches p2 (older),
     // p1 with fine x fx; pixel q is bit 15 - fx - kk0 - q of the two 16-bit plane pairs, with p2's attribute while
@@ -510,7 +518,10 @@ struct RenderSink {
     __device__ void latch_sprites(const Rs& s) {
         drawn = fetched;
         drawn_n = s.f_n;
-        if (lane < 16) L->spal[lane] = (uint8_t)(L->pal[16 + lane] & 0x3Fu);
+        if (sp_stale) {
+            for (int i = 0; i < 4; ++i) spt[i] = uni(reinterpret_cast<const uint32_t*>(L->pal)[4 + i]) & 0x3F3F3F3Fu;
+            sp_stale = false;
+        }
     }
     // CopySprites (with sprites on at the line's end and a latched line waiting) over the background pixels w of
     // this lane, greyscale while rendering, and the observation row (rl/csrc/nes_machine.cuh:133-155: lines 8..231,
@@ -531,10 +542,8 @@ struct RenderSink {
                 const uint32_t front = ~(eb >> 7) & 0x01010101u, clear_bg = (w >> 6) & 0x01010101u;
                 const bool clipped = !(s.mask & 0x04u) && lane < 2;
                 const uint32_t show = clipped ? 0u : (opaque & (front | clear_bg)) * 0xFFu;
-                uint32_t t[4];
-                for (int i = 0; i < 4; ++i) t[i] = uni(reinterpret_cast<const uint32_t*>(L->spal)[i]);
                 const uint32_t sel = eb & 0x07070707u;
-                const uint32_t lo = __builtin_amdgcn_perm(t[1], t[0], sel), hi = __builtin_amdgcn_perm(t[3], t[2], sel);
+                const uint32_t lo = __builtin_amdgcn_perm(spt[1], spt[0], sel), hi = __builtin_amdgcn_perm(spt[3], spt[2], sel);
                 const uint32_t hm = ((eb >> 3) & 0x01010101u) * 0xFFu;
                 w = (w & ~show) | (((lo & ~hm) | (hi & hm)) & show);
             }
@@ -616,7 +625,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(8, 8))) void
     reinterpret_cast<uint4*>(L.sp)[lane] = make_uint4(0u, 0u, 0u, 0u);
     __syncthreads();
     const bool mmc2 = a.g.cart.board == NES_BOARD_MMC2;
-    RenderSink sink{&L, log, a.g.cart.chr, chr_ram, a.g.cart.chr_pairs, lane, mmc2, 0u, 1u, 0u, 0u, 0u};
+    RenderSink sink{&L, log, a.g.cart.chr, chr_ram, a.g.cart.chr_pairs, lane, mmc2, 0u, 1u, 0u, 0u, 0u, {}, {}, true, true};
     Rs s;
     rs_load(s, sink, log, uni(log_n), mmc2 ? a.g.cart.chr_pages1 : 0u);
     rs_begin_frame(s, sink);
