@@ -71,9 +71,15 @@ struct Cart {
 // Instruction-fetch table (fast path): entry = {dispatch key, operand word}, two dwords: the opcode, or its hot key
 // for the opcodes of kHotOps, and the decoded operand. NROM and CNROM (fixed PRG): entry a for CPU address a, for
 // $8000 <= a <= $FFFD; every other entry (RAM, I/O, the last two bytes, and a pc just past $FFFF) holds opcode $02,
-// which no fast-path handler runs, so the generic step fetches it. Banked boards: one entry per PRG byte offset (the
-// last two of each 8 KB page hold $02: an instruction there runs into the next CPU page).
+// which no fast-path handler runs, so the generic step fetches it. Banked boards: one entry per PRG byte offset, $02
+// where the instruction would end on the last byte of its 8 KB page or beyond it, so that every instruction the
+// fast path runs leaves the next pc on the same page (the next CPU page may map another bank).
 constexpr uint32_t kFetchWords = 0x10100u;
+
+// Bytes of an instruction of addressing mode `mode`.
+constexpr uint32_t instr_len(uint32_t mode) {
+    return mode == M_IMP ? 1u : ((mode >= M_ABS && mode <= M_ABY) || mode == M_IND) ? 3u : 2u;
+}
 
 // Opcodes the NROM fetch table stores as hot keys $100 + i (i = index here) instead of the opcode: the interpreter
 // dispatches a hot key through a switch of 32 cases (5 compares) after one range check, and every other opcode
@@ -790,7 +796,7 @@ __device__ inline uint32_t cpu_step(Con& c, const Mem& m, const uint32_t* optab,
     }
     uint32_t opd = lo;
     if (d & D_READ) opd = bus_read(c, m, ac, ea);
-    uint32_t res = 0, npc = (pc + (mode == M_IMP ? 1u : (mode >= M_ABS && mode <= M_ABY) || mode == M_IND ? 3u : 2u)) & 0xFFFFu;
+    uint32_t res = 0, npc = (pc + instr_len(mode)) & 0xFFFFu;
     switch (grp) {
         case G_LD: {   // LDA LDX LDY, TAX TAY TXA TYA TSX TXS
             res = reg_get(c, src, opd);

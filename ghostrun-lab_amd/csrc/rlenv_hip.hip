@@ -1437,7 +1437,7 @@ void fetch_entry(uint32_t* e, uint32_t a, uint32_t op, uint32_t b1, uint32_t b2,
     } else if (mode == M_REL) {
         const uint32_t off = (uint32_t)(int32_t)(int8_t)b1, tgt = a + 2u + off;
         cross = ((a + 2u) ^ tgt) & 0xFF00u;   // the page of pc + 2 and of the target (low bits of a suffice)
-        base = nrom ? tgt << 3 : off;
+        base = nrom ? tgt << 3 : off << 3;
     } else if (nrom && (op == 0x4Cu || op == 0x20u)) {
         base <<= 3;
     }
@@ -1645,11 +1645,13 @@ void* rlenv_create(int ngames, const int* game_ids, const uint8_t* const* roms, 
                 for (uint32_t a = 0x8000u; a <= 0xFFFDu; ++a)
                     fetch_entry(&f[2u * a], a, p.prg[a & mask], p.prg[(a + 1u) & mask], p.prg[(a + 2u) & mask],
                                 true);
-            } else {                            // by PRG offset; the last two bytes of each 8 KB page hold $02
+            } else {   // by PRG offset; $02 where an instruction would end on the last byte of its 8 KB page
                 f.assign(2u * p.prg.size(), 0u);
+                const auto at = [&](uint32_t k) { return k < p.prg.size() ? (uint32_t)p.prg[k] : 0u; };
                 for (uint32_t o = 0; o < p.prg.size(); ++o) {
-                    if ((o & 0x1FFFu) > 0x1FFDu) f[2u * o] = 0x02u;
-                    else fetch_entry(&f[2u * o], o, p.prg[o], p.prg[o + 1u], p.prg[o + 2u], false);
+                    const uint32_t op = p.prg[o];
+                    if ((o & 0x1FFFu) + instr_len(kOptab.t[op] & 15u) >= 0x2000u) f[2u * o] = 0x02u;
+                    else fetch_entry(&f[2u * o], o, op, at(o + 1u), at(o + 2u), false);
                 }
             }
             uint32_t* fetchw = static_cast<uint32_t*>(env->mem.alloc(f.size() * 4));

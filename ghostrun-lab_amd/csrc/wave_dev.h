@@ -25,16 +25,25 @@ typedef __attribute__((address_space(4))) const uint8_t ConstU8;
 // step, the PPU settle and the idle fast-forward touch it, so the loop's live set is small enough to stay in SGPRs.
 // N and Z are kept lazily in one value nz: N = (nz >= $80), Z = (low byte of nz == 0). An instruction that sets both
 // from a result r stores r itself; BIT, whose N comes from the operand, adds the operand's bit 7 as bit 8. The N and
-// Z bits of p are stale in between and are rebuilt when p is stored or pushed. pc is held shifted left by
-// pc_shift(board): on NROM times 8, the byte offset of its fetch-table entry, so the fetch needs no address
-// arithmetic. It may run one past $FFFF after the last instruction of the address space and is wrapped when stored
-// (the fast path sends such a pc to the generic step).
+// Z bits of p are stale in between and are rebuilt when p is stored or pushed.
+// pc is held as pcs, the byte offset of its fetch-table entry (8 bytes an entry), so the fetch needs no address
+// arithmetic. On NROM the table is by CPU address and pcs = pc * 8; it may run one past $FFFF after the last
+// instruction of the address space and is wrapped when stored (the fast path sends such a pc to the generic step).
+// On the banked boards the table is by PRG offset, pcs = (PRG offset of pc) * 8 and pd = that offset - pc (mod 2^32),
+// so pc = pcs / 8 - pd. Within an 8 KB page the offset moves with pc: the table sends every instruction that ends on
+// the last byte of its page to the generic step, so sequential flow never leaves a page in the fast path, a branch to
+// another page goes to the generic step, and every jump, call and return maps its target again (hot_pcs), as does
+// the reload after the generic step, which is the only place the PRG mapping changes.
 struct Hot {
     uint32_t pc, a, x, y, sp, p, nz;
     uint64_t cycles;
     uint32_t prg0, prg1, prg2, prg3;
+    uint32_t pd;
 };
-constexpr uint32_t pc_shift(uint32_t board) { return board == NES_BOARD_NROM ? 3u : 0u; }
+constexpr uint32_t kPcShift = 3u;
+// The banked boards' stand-in for a pc outside PRG ($0000-$7FFF, or one past $FFFF): the entry of the last byte of
+// PRG page 0, which holds the generic step's key (no instruction that starts there ends inside the page).
+constexpr uint32_t kOffPrg = 0x1FFFu;
 
 // (uni(): a wave-uniform value read from LDS, as a scalar - replay_dev.h. An LDS load lands in a VGPR; without it the
 // compiler moves every use of the value to the vector unit, with lane-mask compares instead of SCC branches.)
@@ -49,17 +58,41 @@ __device__ __forceinline__ uint32_t hflags(const Hot& h) {
     return (h.p & ~(FL_N | FL_Z)) | (h.nz >= 0x80u ? FL_N : 0u) | ((h.nz & 0xFFu) ? 0u : FL_Z);
 }
 
+// pcs of CPU address `pc` (on the banked boards also pd, from the PRG offsets in h).
+template <uint32_t B>
+__device__ __forceinline__ uint32_t hot_pcs(Hot& h, uint32_t pc) {
+    if constexpr (B == NES_BOARD_NROM) {
+        return pc << kPcShift;
+    } else {
+        if (pc - 0x8000u >= 0x8000u) {
+            h.pd = kOffPrg - pc;
+            return kOffPrg << kPcShift;
+        }
+        const uint32_t page = sel4((pc >> 13) & 3u, h.prg0, h.prg1, h.prg2, h.prg3);
+        h.pd = page - (pc & 0xE000u);
+        return (page + (pc & 0x1FFFu)) << kPcShift;
+    }
+}
+// The CPU address of pcs (not wrapped).
+template <uint32_t B>
+__device__ __forceinline__ uint32_t hot_cpu(const Hot& h, uint32_t pcs) {
+    if constexpr (B == NES_BOARD_NROM) return pcs >> kPcShift;
+    else return (pcs >> kPcShift) - h.pd;
+}
+
 template <uint32_t B>
 __device__ __forceinline__ void hot_load(Hot& h, const Con& c) {
-    h.pc = uni(c.pc) << pc_shift(B); h.a = uni(c.a); h.x = uni(c.x); h.y = uni(c.y); h.sp = uni(c.sp); h.p = uni(c.p);
+    h.a = uni(c.a); h.x = uni(c.x); h.y = uni(c.y); h.sp = uni(c.sp); h.p = uni(c.p);
     h.nz = nz_of_p(h.p);
     h.cycles = uni64(c.cycles);
     h.prg0 = uni(c.prg0); h.prg1 = uni(c.prg1); h.prg2 = uni(c.prg2); h.prg3 = uni(c.prg3);
+    h.pd = 0;
+    h.pc = hot_pcs<B>(h, uni(c.pc));
 }
 // (the PRG offsets change only in the generic step, which writes them to the console state itself)
 template <uint32_t B>
 __device__ __forceinline__ void hot_store(const Hot& h, Con& c) {
-    c.pc = (h.pc >> pc_shift(B)) & 0xFFFFu; c.a = h.a; c.x = h.x; c.y = h.y; c.sp = h.sp; c.p = hflags(h);
+    c.pc = hot_cpu<B>(h, h.pc) & 0xFFFFu; c.a = h.a; c.x = h.x; c.y = h.y; c.sp = h.sp; c.p = hflags(h);
     c.cycles = h.cycles;
 }
 
@@ -136,14 +169,15 @@ __device__ __forceinline__ uint32_t prg_wide(const Mem& m, uint32_t idx) {
 // (cycles << 14) - 1 it stands for 0 cycles.
 constexpr uint32_t kGeneric = 0xFFFFFFFFu;
 
-// One instruction of opcode descriptor D at pcs = pc << pc_shift(B) (operand bytes lo, hi). Returns what it takes
+// One instruction of opcode descriptor D at pcs (operand bytes lo, hi). Returns what it takes
 // off the burst counter, (CPU cycles << 14) - 1, or kGeneric with nothing changed when the generic step must run it.
 // The operand word comes decoded from the fetch table (kFetchWords): the operand byte of a two-byte instruction; a
-// branch's target times 8 (NROM) or its sign-extended offset (banked boards); JMP's and JSR's target (times 8 on NROM);
+// branch's target times 8 (NROM) or its sign-extended offset times 8 (banked boards); JMP's and JSR's target (times 8
+// on NROM);
 // else lo | hi << 8. HOT: a hot key (a branch that stays on its page).
 template <uint32_t B, uint32_t D, bool HOT = false>
 __device__ __forceinline__ uint32_t fx(Hot& h, const Mem& m, Con& cs, uint32_t pcs, uint32_t base) {
-    constexpr uint32_t PS = pc_shift(B);
+    constexpr uint32_t PS = kPcShift;
     constexpr bool nrom = B == NES_BOARD_NROM;
     constexpr uint32_t mode = D & 15u, grp = (D >> 8) & 15u, sub = (D >> 12) & 15u;
     constexpr uint32_t src = (D >> 16) & 7u, dst = (D >> 19) & 7u;
@@ -202,7 +236,7 @@ __device__ __forceinline__ uint32_t fx(Hot& h, const Mem& m, Con& cs, uint32_t p
                 else return kGeneric;
             }
         }
-        constexpr uint32_t len = mode == M_IMP ? 1u : ((mode >= M_ABS && mode <= M_ABY) || mode == M_IND) ? 3u : 2u;
+        constexpr uint32_t len = instr_len(mode);
         uint32_t npc = pcs + (len << PS), res = 0;   // pc <= $FFFD here; $10000 is wrapped when stored
         if constexpr (grp == G_LD) {
             res = hget(h, src, opd);
@@ -251,6 +285,9 @@ __device__ __forceinline__ uint32_t fx(Hot& h, const Mem& m, Con& cs, uint32_t p
             else set = ((h.p >> bit) & 1u) != 0;
             if (set == ((sub & 8u) != 0)) {
                 const uint32_t tgt = nrom ? base : npc + base;   // wrapped when stored
+                if constexpr (!nrom && !HOT) {
+                    if ((npc ^ tgt) >> 16) return kGeneric;   // to another 8 KB page: bits 13+ of the PRG offset
+                }
                 if constexpr (HOT) cyc += 1u;
                 else cyc += ((npc ^ tgt) & (0xFF00u << PS)) ? 2u : 1u;
                 npc = tgt;
@@ -277,24 +314,30 @@ __device__ __forceinline__ uint32_t fx(Hot& h, const Mem& m, Con& cs, uint32_t p
                                                    : (prg_wide(m, prg_index<B>(h, m, base)) & 0xFFu);
                 const uint32_t h8 = a1 < 0x2000u ? rd8(m, a1 & 0x7FFu)
                                                  : (prg_wide(m, prg_index<B>(h, m, a1)) & 0xFFu);
-                npc = (l8 | (h8 << 8)) << PS;
+                npc = hot_pcs<B>(h, l8 | (h8 << 8));
             } else {
-                npc = base;
-                if (npc == pcs) return kGeneric;   // the idle loop: the generic step runs it, then the fast-forward
+                // the idle loop (a jump to itself): the generic step runs it, then the fast-forward
+                if constexpr (nrom) {
+                    npc = base;
+                    if (npc == pcs) return kGeneric;
+                } else {
+                    if (base == hot_cpu<B>(h, pcs)) return kGeneric;
+                    npc = hot_pcs<B>(h, base);
+                }
             }
         } else if constexpr (grp == G_JSR) {
-            const uint32_t ret = (pcs >> PS) + 2u;   // <= $FFFF
+            const uint32_t ret = hot_cpu<B>(h, pcs) + 2u;   // <= $FFFF
             hpush(h, m, ret >> 8);
             hpush(h, m, ret & 0xFFu);
-            npc = base;
+            npc = nrom ? base : hot_pcs<B>(h, base);
         } else if constexpr (grp == G_RTS) {
             const uint32_t l8 = hpull(h, m), h8 = hpull(h, m);
-            npc = (((h8 << 8) | l8) + 1u) << PS;
+            npc = hot_pcs<B>(h, ((h8 << 8) | l8) + 1u);
         } else if constexpr (grp == G_RTI) {
             h.p = (hpull(h, m) & ~FL_B) | FL_U;
             h.nz = nz_of_p(h.p);
             const uint32_t l8 = hpull(h, m), h8 = hpull(h, m);
-            npc = ((h8 << 8) | l8) << PS;
+            npc = hot_pcs<B>(h, (h8 << 8) | l8);
         }
         if constexpr (wr) {
             if constexpr (mode == M_ZP) m.ram[ea] = (uint8_t)res;
@@ -344,20 +387,16 @@ __device__ __forceinline__ uint32_t fx_hot(Hot& h, const Mem& m, Con& cs, uint32
 }
 
 // The fast path for the instruction at h.pc: (its cycles << 14) - 1, or kGeneric (nothing changed) for the generic
-// step. The instruction comes decoded from the fetch table: on NROM at byte offset pcs = pc * 8 (pc <= $1007E, a
-// branch just past $FFFF; $02 outside PRG), a scalar load with an SGPR offset; on the banked boards at the PRG offset
-// of pc ($02 in the last two bytes of a page), for pc in PRG.
+// step. The instruction comes decoded from the fetch table at byte offset pcs, a scalar load with an SGPR offset: on
+// NROM pcs = pc * 8 (pc <= $1007E, a branch just past $FFFF; $02 outside PRG), on the banked boards the PRG offset
+// of pc times 8 ($02 where an instruction would end on the last byte of its 8 KB page, and kOffPrg for a pc outside
+// PRG).
 template <uint32_t B>
 __device__ __forceinline__ uint32_t fast_step(Hot& h, const Mem& m, Con& cs, uint32_t* op_out) {
     const uint32_t pcs = h.pc;
-    uint32_t off = pcs;
-    if constexpr (B != NES_BOARD_NROM) {
-        if (pcs - 0x8000u >= 0x8000u) return kGeneric;   // pc outside $8000-$FFFF (one past $FFFF included)
-        off = prg_index<B>(h, m, pcs) << 3;
-    }
     // (two 32-bit loads, which the compiler pairs into one 64-bit load: read as the halves of a 64-bit value,
     // base's compares would become 64-bit ones, which the scalar unit has only for equality)
-    ConstU32* e = (ConstU32*)((ConstU8*)m.cart.fetchw + off);
+    ConstU32* e = (ConstU32*)((ConstU8*)m.cart.fetchw + pcs);
     const uint32_t op = e[0], base = e[1];
     *op_out = op;
     if (__builtin_expect(op >= kHotKey, 1)) return fx_hot<B>(h, m, cs, pcs, op, base);
@@ -499,7 +538,7 @@ __device__ __forceinline__ uint32_t run_until_wave(Con& cs, const Mem& m, const 
         }
         pending += 3u * cyc;
         ++instructions;
-        if (op == 0x4Cu && h.pc == pc0 << pc_shift(B)) why = 1;
+        if (op == 0x4Cu && hot_cpu<B>(h, h.pc) == pc0) why = 1;
     }
     h.cycles += ecyc;
     hot_store<B>(h, cs);

@@ -653,6 +653,154 @@ def mmc1_cart(seed: int = 0, blocks: int = 16, sub_blocks: int = 16) -> bytes:
     return ines(b''.join(banks) + bytes(fixed), b'', 1, vertical=True)
 
 
+SEAM_LOOPS, SEAM_JMP, SEAM_HEADS, SEAM_RAM, SEAM_TAILS, SEAM_BANK2, SEAM_MODE = 0x70, 0x71, 0x72, 0x73, 0x74, 0x75, 0x76
+SEAM_VEC = 0x04FF                         # JMP ($04FF): the 6502 takes the high byte from $0400
+SEAM_RAM_CODE = 0x0500                    # the routine copied to CPU RAM
+
+
+def _seam_run(a: Asm, rng: np.random.Generator, last: int, strip: int):
+    """Instructions filling a.pc .. a.pc + 15 exactly, the last one `last` bytes long: the bytes that run off the end
+    of an 8 KB window into the next one. A two-byte slot may be a branch into the next window's landing strip."""
+    end = a.pc + 16
+    while a.pc < end:
+        room = end - a.pc
+        n = last if room == last else int(rng.integers(1, min(3, room - last) + 1)) if room > last else room
+        if n == 1:
+            a.op(('NOP', 'INX', 'DEY', 'CLC', 'SEC')[int(rng.integers(5))])
+        elif n == 2:
+            k = int(rng.integers(5))
+            if k == 4:
+                a.op('BCC', 'rel', strip + int(rng.integers(8)))
+            else:
+                a.op(*(('LDA', 'zp'), ('ADC', 'imm'), ('STA', 'zp'), ('EOR', 'imm'))[k],
+                     int(rng.choice(SCRATCH_ZP)) if k in (0, 2) else int(rng.integers(256)))
+        else:
+            k = int(rng.integers(4))
+            a.op(('LDA', 'STA', 'INC', 'ADC')[k], 'abs', WORK_PAGE + int(rng.integers(256)) if k < 3 else 0xE300
+                 + int(rng.integers(256)))
+
+
+def seam_cart(seed: int = 0, blocks: int = 8, sub_blocks: int = 6) -> bytes:
+    """MMC3 cartridge whose code crosses its 8 KB PRG windows in every way a program can: 128 KB PRG (16 x 8 KB;
+    banks 0-14 share one layout, bank 15 is fixed at $E000 with the main loop, the tables and the vectors), 128 KB
+    random CHR. Each of banks 0-14 starts with a head (a 16-NOP landing strip at offset 0, then code that loops back
+    into the previous window and returns) and ends with a tail (offset $1F80: an entry that may branch forward into
+    the next window's strip, seeded work, a 16-NOP strip at $1FE0, then 16 bytes of 1-, 2- and 3-byte instructions
+    ending exactly on the window's last byte, the last one's length differing between banks, which run into the next
+    window). The main loop maps two banks (R6, R7, possibly the same one) in PRG mode 0 or 1, so a tail at $8000 or
+    $A000 runs into a head at $A000 or $C000 of another bank (bank 14 in the fixed slot included); it enters the tail
+    by JSR or by JMP ($04FF) (the vector's high byte from $0400, the 6502's page wrap), loops through the seam 1-4
+    times, and calls a routine copied to CPU RAM at $0500 that calls back into PRG. Every pass counts itself in zero
+    page (heads $72, RAM routine $73, tails $74)."""
+    rng = np.random.default_rng([0x5345414D, seed])
+    pal, nt, oam, mix = _tables(rng)
+    # fixed bank 15 at $E000: tables, main loop, NMI, helper; the RAM routine's image at $FF00
+    a = Asm(0xE000)
+    for name, t in (('t_pal', pal), ('t_nt', nt), ('t_oam', oam), ('t_mix', mix)):
+        a.label(name)
+        a.data(bytes(int(v) for v in t))
+    assert a.labels['t_mix'] == 0xE220
+    a.data(rng.integers(0, 256, 256, dtype=np.uint8).tobytes())        # $E300: a table the seam runs read
+    tables = dict(pal='t_pal', nt='t_nt', oam='t_oam')
+    a.label('reset')
+    a.op('LDA', 'imm', 0x80); a.op('STA', 'abs', 0xA001)               # PRG RAM on
+    a.op('LDA', 'imm', 0); a.op('STA', 'abs', 0xA000)                  # vertical mirroring
+    _reset_common(a, 0x88, tables)
+    a.op('LDX', 'imm', 0)
+    a.label('cp'); a.op('LDA', 'abx', 0xFF00); a.op('STA', 'abx', SEAM_RAM_CODE); a.op('INX'); a.op('CPX', 'imm', 32)
+    a.op('BNE', 'rel', 'cp')
+    a.label('main')
+    _read_pad(a, 'm')
+    _pad_moves(a, 't_mix')
+    for var, shift, lab in ((BANK, 0, 'b6'), (SEAM_BANK2, 3, 'b7')):   # two banks of 0-14
+        a.op('LDA', 'zp', CNT_LO)
+        for _ in range(shift):
+            a.op('LSR', 'acc')
+        a.op('EOR', 'zp', PAD); a.op('AND', 'imm', 0x0F); a.op('CMP', 'imm', 15); a.op('BCC', 'rel', lab)
+        a.op('LDA', 'zp', FRAMES); a.op('AND', 'imm', 7)
+        a.label(lab); a.op('STA', 'zp', var)
+    a.op('LDA', 'zp', CNT_LO); a.op('EOR', 'zp', FRAMES); a.op('AND', 'imm', 0x10); a.op('ASL', 'acc'); a.op('ASL', 'acc')
+    a.op('STA', 'zp', SEAM_MODE)                                        # PRG mode bit 6
+    a.op('ORA', 'imm', 6); a.op('STA', 'abs', 0x8000); a.op('LDA', 'zp', BANK); a.op('STA', 'abs', 0x8001)
+    a.op('LDA', 'zp', SEAM_MODE); a.op('ORA', 'imm', 7); a.op('STA', 'abs', 0x8000)
+    a.op('LDA', 'zp', SEAM_BANK2); a.op('STA', 'abs', 0x8001)
+    a.op('LDA', 'zp', PAD); a.op('AND', 'imm', 3); a.op('CLC'); a.op('ADC', 'imm', 1); a.op('STA', 'zp', SEAM_LOOPS)
+    a.op('LDA', 'imm', 0x80); a.op('STA', 'abs', SEAM_VEC)               # the tail entry of window $8000 or $A000
+    a.op('LDA', 'zp', CNT_LO); a.op('AND', 'imm', 0x40); a.op('BEQ', 'rel', 'w8')
+    a.op('LDA', 'imm', 0xBF); a.op('BNE', 'rel', 'wset')
+    a.label('w8'); a.op('LDA', 'imm', 0x9F)
+    a.label('wset'); a.op('STA', 'abs', SEAM_VEC + 1 - 0x100)
+    a.op('LDA', 'zp', CNT_LO); a.op('EOR', 'zp', PAD); a.op('AND', 'imm', 0x20); a.op('BEQ', 'rel', 'by_jsr')
+    a.op('LDA', 'imm', 1); a.op('STA', 'zp', SEAM_JMP); a.op('JMP', 'ind', SEAM_VEC)
+    a.label('by_jsr')
+    a.op('LDA', 'imm', 0); a.op('STA', 'zp', SEAM_JMP)
+    a.op('LDA', 'zp', CNT_LO); a.op('AND', 'imm', 0x40); a.op('BEQ', 'rel', 'j8')
+    a.op('JSR', 'abs', 0xBF80); a.op('JMP', 'abs', 'main_ret')
+    a.label('j8'); a.op('JSR', 'abs', 0x9F80)
+    a.label('main_ret')
+    a.op('JSR', 'abs', SEAM_RAM_CODE)
+    _filler(a, rng, blocks, 'f', 't_mix', with_prg_ram=True)
+    a.op('JMP', 'abs', 'main')
+    a.label('nmi')
+    _nmi_common(a)
+    _nmi_end(a)
+    a.label('irq')
+    a.op('RTI')
+    a.label('helper')
+    a.op('LDA', 'zp', 0x58); a.op('CLC'); a.op('ADC', 'imm', 0x11); a.op('STA', 'zp', 0x58); a.op('RTS')
+    code_e = a.assemble()
+    assert len(code_e) <= 0x1F00, len(code_e)
+    r = Asm(SEAM_RAM_CODE)                                              # runs from CPU RAM
+    r.op('INC', 'zp', SEAM_RAM); r.op('LDA', 'zp', SEAM_RAM); r.op('EOR', 'zp', PAD); r.op('STA', 'zp', 0x5E)
+    r.op('JSR', 'abs', a.labels['helper']); r.op('AND', 'imm', 7); r.op('BNE', 'rel', 'r_out'); r.op('INC', 'zp', 0x5D)
+    r.label('r_out'); r.op('RTS')
+    ram_code = r.assemble()
+    assert len(ram_code) <= 32
+    fixed = bytearray(8192)
+    fixed[:len(code_e)] = code_e
+    fixed[0x1F00:0x1F00 + len(ram_code)] = ram_code
+    vec = (a.labels['nmi'], a.labels['reset'], a.labels['irq'])
+    fixed[0x1FFA:0x2000] = bytes(sum(((v & 0xFF, v >> 8) for v in vec), ()))
+    banks = []
+    for b in range(15):
+        page = bytearray(8192)
+        h = Asm(0xA000)                                                 # head (position independent)
+        for _ in range(16):
+            h.op('NOP')
+        h.op('DEC', 'zp', SEAM_LOOPS); h.op('BEQ', 'rel', 'h_done'); h.op('LDA', 'zp', SEAM_LOOPS)
+        h.op('BNE', 'rel', 0x9FE0 + int(rng.integers(16)))              # back into the previous window's strip
+        h.label('h_done')
+        h.op('INC', 'zp', SEAM_HEADS); h.op('JSR', 'abs', a.labels['helper'])
+        _filler(h, rng, sub_blocks, f'h{b}', 0xE300, with_prg_ram=True)
+        h.op('LDA', 'zp', SEAM_JMP); h.op('BNE', 'rel', 'hx'); h.op('RTS')
+        h.label('hx'); h.op('JMP', 'abs', a.labels['main_ret'])
+        head = h.assemble()
+        page[:len(head)] = head
+        t = Asm(0x9F80)                                                 # tail (position independent)
+        t.op('INC', 'zp', SEAM_TAILS); t.op('LDA', 'zp', PAD); t.op('AND', 'imm', 1 << int(rng.integers(8)))
+        t.op('BNE', 'rel', 0xA000 + int(rng.integers(8)))               # forward into the next window's strip
+        while True:                                                     # seeded work up to the strip at $1FE0
+            w = Asm(t.pc)
+            _filler(w, rng, 1, f't{b}_{t.pc:x}', 0xE300, with_prg_ram=True)
+            if w.pc > 0x9FE0:
+                break
+            t.items += w.items
+            t.labels.update(w.labels)
+            t.pc = w.pc
+        while t.pc < 0x9FE0:
+            t.op('NOP')
+        for _ in range(16):
+            t.op('NOP')
+        _seam_run(t, rng, b % 3 + 1, 0xA000)
+        assert t.pc == 0xA000
+        tail = t.assemble()
+        page[0x1F80:] = tail
+        assert len(head) <= 0x1F00
+        banks.append(bytes(page))
+    chr_ = rng.integers(0, 256, 128 * 1024, dtype=np.uint8).tobytes()
+    return ines(b''.join(banks) + bytes(fixed), chr_, 4, vertical=True)
+
+
 def mmc2_cart(seed: int = 0, blocks: int = 12, sub_blocks: int = 12) -> bytes:
     """MMC2 (mapper 9) cartridge: 128 KB PRG in 8 KB banks (0-12 switched in at $8000, the last three fixed at
     $A000-$FFFF), 128 KB CHR ROM in 4 KB banks. The nametables and sprites use tiles $FD and $FE often, so the

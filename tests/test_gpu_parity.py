@@ -111,3 +111,12 @@ def test_mmc2_latches_follow_the_fetches(seed):
           'mirroring rewrites, CPU-driven latch flips, 16 decisions', flush=True)
     cpu, gpu = pair(16, synth.mmc2_cart(seed), seed=20 + seed, sticky=True, idle_max=2, dropout=False, pad_mode=True)
     run(cpu, gpu, 16, 7 + seed, True)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize('seed', [0, 1])
+def test_mmc3_code_across_prg_windows(seed):
+    print(f'case: seam cart seed {seed} (MMC3), 16 consoles, raw pads, sticky, code running off 8 KB windows, '
+          'branches across them, JMP ($04FF), code in RAM, 16 decisions', flush=True)
+    cpu, gpu = pair(16, synth.seam_cart(seed), seed=30 + seed, sticky=True, idle_max=1, dropout=False, pad_mode=True)
+    run(cpu, gpu, 16, 11 + seed, True)
