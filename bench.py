@@ -241,6 +241,16 @@ def bench_env(args, name, K, W, baseline):
 
     print(f'[bench] workload {name}: {N} consoles, warmup {W}, timed {K} decisions', file=sys.stderr, flush=True)
     env = RlEnv(counts, device=dev, **kw)
+    # the translated kernels of the fixed-PRG carts (compiled on threads of their own while the env is created):
+    # warmup, parity and the timed region all run them
+    t_jit = time.perf_counter()
+    env.jit_wait()
+    translated = [dict(game=g, **env.jit_status(gi)) for gi, g in enumerate(counts)]
+    translated = [t for t in translated if t['state'] != 'none']
+    if translated:
+        print(f'[bench] translated kernels ready after {time.perf_counter() - t_jit:.1f} s: ' +
+              ', '.join(f'{t["game"]} {t["blocks"]} blocks / {t["instructions"]} instructions' for t in translated),
+              file=sys.stderr, flush=True)
     sink = Pack6Sink(env, w['pack6'], args.host_slots) if w['pack6'] else None
     env.start()
     for t in range(W):
@@ -303,6 +313,8 @@ def bench_env(args, name, K, W, baseline):
                data='synthetic: seed-generated cartridges (rl.synth), uniform random pad bytes', config=cfg,
                emulated_instructions_per_s=round(float(instr1 - instr0) / dt, 1),
                step_output_gbps=round(out_bytes * N * K / dt / 1e9, 3))
+    if translated:   # fixed-PRG games whose decision frames ran their translated kernel
+        out['translated'] = translated
     if kern:
         out['roofline'] = _roofline(name, kern, N, K, dt, out_bytes, out['emulated_instructions_per_s'])
         out['kernels'] = kern

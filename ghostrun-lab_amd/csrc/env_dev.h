@@ -5,9 +5,13 @@
 // reference is, double in Python's evaluation order for the reward (built with -ffp-contract=off).
 #pragma once
 #ifndef ND_HOST_BUILD
+#ifndef __HIPCC_RTC__   // (built in where hiprtc compiles this at run time)
 #include <hip/hip_runtime.h>
 #endif
+#endif
+#ifndef __HIPCC_RTC__   // (built in where hiprtc compiles this at run time)
 #include <stdint.h>
+#endif
 
 #include "rlenv_state.h"
 #include "rl10_games.h"

@@ -11,10 +11,12 @@
 // rl/csrc/nes_machine.cuh:67-103, instruction step third_party/nesle-extensions.patch:823-862, bus side effects
 // patch:570-779, PPU events patch:1822-2240, frame log patch:894-1185, mappers patch:2841-3367, DMC patch:430-565.
 #pragma once
+#ifndef __HIPCC_RTC__   // (built in where hiprtc compiles this at run time)
 #ifndef ND_HOST_BUILD
 #include <hip/hip_runtime.h>
 #endif
 #include <stdint.h>
+#endif
 
 #include "nesrec.h"
 #include "replay_dev.h"
@@ -93,6 +95,7 @@ constexpr uint32_t kHotOps[32] = {
     0xE8u, 0xCAu, 0xC8u, 0x88u,                                      // INX DEX INY DEY
     0xC9u, 0x29u, 0x18u, 0x69u, 0x4Au, 0x0Au, 0xAAu};                // CMP # AND # CLC ADC # LSR A ASL A TAX
 constexpr uint32_t kHotKey = 0x100u;
+constexpr uint32_t kBlockKey = 0x200u;   // translated blocks (jit.h): keys kBlockKey + block index
 constexpr bool is_hot(uint32_t op) {
     for (uint32_t i = 0; i < 32u; ++i)
         if (kHotOps[i] == op) return true;

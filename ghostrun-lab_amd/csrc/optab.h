@@ -1,7 +1,9 @@
 // Host-side construction of the 6502 opcode descriptors the device interpreter reads (nes_dev.h): the 151 official
 // opcodes, derived from the 6502's operation classes and addressing modes; every other byte is a fault.
 #pragma once
+#ifndef __HIPCC_RTC__   // (built in where hiprtc compiles this at run time)
 #include <stdint.h>
+#endif
 
 #include "nes_dev.h"
 

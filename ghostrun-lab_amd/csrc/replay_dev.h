@@ -19,7 +19,9 @@
 // MMC2's latch hook after every pattern fetch is run by the walker itself, slot by slot, so the sinks only receive the
 // CHR pages each fetch read through.
 #pragma once
+#ifndef __HIPCC_RTC__   // (built in where hiprtc compiles this at run time)
 #include <stdint.h>
+#endif
 
 #include "nesrec.h"
 

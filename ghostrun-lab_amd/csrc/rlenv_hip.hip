@@ -17,22 +17,30 @@
 // its scalar walk wave-uniform, each run of tile slots fetched and shifted out by the lanes into a line buffer in LDS,
 // sprites selected with one ballot per line, and each output row is one coalesced 240-byte store.
 #include <hip/hip_runtime.h>
+#include <hip/hiprtc.h>
 
+#include <atomic>
+#include <chrono>
 #include <cstdio>
 #include <cstdlib>
 #include <ctime>
 #include <cstring>
+#include <map>
+#include <memory>
 #include <mutex>
 #include <stdexcept>
 #include <string>
+#include <thread>
 #include <vector>
 
+#include "emu_kernel.h"
 #include "env_dev.h"
+#include "jit.h"
 #include "nes_dev.h"
 #include "optab.h"
 #include "rlenv_api.h"
-#include "wave_dev.h"
 #include "rlenv_state.h"
+#include "wave_dev.h"
 
 using namespace nd;
 
@@ -41,235 +49,10 @@ namespace {
 thread_local std::string g_error;
 
 // ============================================================================================ kernels
-struct EnvArrays {
-    Rl10State* st;
-    Rl10Reader* rd;        // [N] reader state of the game's reader (unused by SMB)
-    Dropout* drop;
-    uint64_t *target, *sticky_seed, *sticky_ctr;
-    uint32_t *ep_frame, *episode, *fault;
-    int16_t* prev_applied;
-    float* ep_ret;
-    int32_t *ep_len, *ep_maxlvl, *ep_idle;
-    uint8_t* resetting;
-    int32_t* ep_start;     // [N] slot the episode started from, -1 = boot snapshot; nullptr without level starts
-};
-
-struct Outs {
-    const int16_t* actions;
-    uint8_t *obs, *emph, *done, *masks, *tl, *pads;
-    float *reward, *info, *parts;
-    uint32_t* events;
-    uint64_t* ram_hash;
-    int32_t *start_out, *level_out;   // level starts: start slot of a finished episode, level after the decision
-    float* progress_out;              // within-level progress / progress unit, NaN = not valid
-};
-
-struct Settings {
-    uint64_t run_seed;
-    int sticky, idle_max, idle_tmpl, dropout, no_render, episode_level_end, pad_mode;
-    uint32_t end_p32, gap_p32;
-};
-
-// Saved level starts and places of one game (rl/csrc/rlenv_core.cuh:60-74): slot s < levels is level s, saved on the
-// tracker's level event; slots levels..cap-1 are places, saved on request. A saved console is a whole record.
-struct LevelK {
-    int cap, levels;                 // cap 0: off
-    NesRec* rec;                     // [cap]
-    Rl10Saved* st;                   // [cap] tracker + reader per slot
-    uint32_t* keys;                  // [cap * kcap]
-    uint64_t* target;                // [cap]
-    uint32_t* frame;                 // [cap]
-    int32_t* deaths;                 // [cap], -1 = nothing saved
-    unsigned long long* claim;       // [cap] (deaths << 32 | env) of this decision's best arrival, ~0 = none
-    uint32_t* cdf;                   // [cap] cumulative slot weights * 2^32
-    uint32_t thresh;                 // P(a new episode starts from a saved slot) * 2^32
-    int weighted;                    // 1: pick by cdf, 0: uniform over the saved slots
-};
-
-// What the renderer needs of one console-frame, copied out of the record by the emulator kernel at the frame's vblank
-// stop: the frame log and its event count, the nametables and the OAM (CHR RAM, on carts that have it, in a parallel
-// array). One bank per frame of a decision, so that frame f is drawn from its bank while the frames after it are
-// emulated.
-struct FrameBank {
-    uint32_t log[NES_LOG_WORDS];
-    uint32_t log_n, unused[3];
-    uint8_t nt[NES_NT_BYTES];
-    uint8_t oam[NES_OAM_BYTES];
-};
-static_assert(sizeof(FrameBank) % 16 == 0 && (NES_LOG_WORDS * 4) % 16 == 0, "16-byte copies");
-
-struct GameK {
-    NesRec* recs;          // n + 1 records, slot n = boot snapshot
-    const NesRec* idle;    // idle templates
-    // Restart templates, one per idle count k = 0..idle_tmpl: the record after a restart's 4 neutral frames from
-    // the boot snapshot (k = 0) or idle template k, those frames' pictures and emphasis, and the fault code they
-    // leave (0 = none). A restart from the boot snapshot copies one instead of emulating the frames.
-    const NesRec* rst;
-    const uint8_t* rst_obs;     // [idle_tmpl + 1][RLE_FRAMES][RLE_OBS_PIXELS]
-    const uint8_t* rst_emph;    // [idle_tmpl + 1][RLE_FRAMES][RLE_OBS_H]
-    const uint32_t* rst_fault;  // [idle_tmpl + 1]
-    Cart cart;
-    int n, offset, start_ok, select_ok, game;
-    uint32_t kcap;         // key-set entries per env (rl10_keyset_capacity; 0 for most games)
-    uint32_t* keys;        // [n * kcap] per-env key sets
-    uint64_t tmpl_target;
-    int32_t* list;         // restart list (env index within the game)
-    uint32_t* list_count;
-    LevelK lv;
-    FrameBank* bank[RLE_FRAMES];     // [n] per frame of a decision
-    uint8_t* bank_chr[RLE_FRAMES];   // [n][NES_CHRRAM_BYTES] per frame, CHR RAM carts only (else nullptr)
-};
-
-// EMU_TEMPLATE: one frame of every restart template (block k = template k, pad 0, target boot_target + k frames,
-// fault word boot_fault[k]); the GameK's recs point at the templates.
-enum : int { EMU_DECISION = 0, EMU_RESTART = 1, EMU_BOOT = 2, EMU_IDLE = 3, EMU_TEMPLATE = 4 };
-
-struct EmuArgs {
-    GameK g;
-    EnvArrays e;
-    Outs o;
-    Settings s;
-    const uint32_t* optab;
-    int mode, f, use_list, e0, e1;
-    uint32_t boot_pad;
-    uint64_t boot_target;
-    uint32_t* boot_fault;
-    uint32_t budget;       // instructions per frame (NES_BUDGET; smaller only for diagnostics)
-    FrameBank* bank;       // decision frames drawn from a bank: the bank this frame's render state goes to
-    uint8_t* bank_chr;
-};
-
-__device__ __forceinline__ int slot_count(const GameK& g, int use_list, int e0, int e1) {
-    return use_list ? (int)*g.list_count : e1 - e0;
-}
-__device__ __forceinline__ int slot_env(const GameK& g, int use_list, int e0, int k) {
-    return use_list ? g.list[k] : e0 + k;
-}
-
-// Per-frame pad byte of a decision frame (rl/csrc/rlenv_core.cuh:181-191): sticky repeat, dropout, turbo phase.
-template <class Args>
-__device__ __forceinline__ uint32_t decision_pad(const Args& a, int ge, int f) {
-    const int d = ev::dropped_now(&a.e.drop[ge]);
-    uint64_t ctr = a.e.sticky_ctr[ge];
-    const uint64_t seed = a.e.sticky_seed[ge];
-    uint32_t pad;
-    if (a.s.pad_mode) {
-        uint32_t p = (uint16_t)a.o.actions[ge] & 0xFFu;
-        if (a.s.sticky && ev::rnd32(seed, ctr) < RLC_STICKY_P32) p = (uint16_t)a.e.prev_applied[ge] & 0xFFu;
-        pad = ev::restrict_pad(p, d);
-        a.e.prev_applied[ge] = (int16_t)pad;
-    } else {
-        ev::Move mv = ev::unpack((uint32_t)(int32_t)a.o.actions[ge]);
-        if (a.s.sticky && ev::rnd32(seed, ctr) < RLC_STICKY_P32)
-            mv = ev::restrict_move(ev::unpack((uint32_t)(int32_t)a.e.prev_applied[ge]), d, a.g.start_ok != 0,
-                                   a.g.select_ok != 0);
-        a.e.prev_applied[ge] = (int16_t)ev::pack(mv);
-        pad = ev::pad_of(mv, a.e.ep_frame[ge]);
-    }
-    a.e.sticky_ctr[ge] = ctr;
-    a.o.pads[(size_t)ge * RLE_FRAMES + f] = (uint8_t)pad;
-    return pad;
-}
-
-// The opcode descriptors in constant memory: the wave-uniform generic step reads them through the scalar cache.
-__constant__ Optab c_optab = kOptab;
-
-// Copies n bytes (a multiple of 16, 16-byte aligned) with the 64 lanes of the wavefront.
-__device__ __forceinline__ void wave_copy16(void* dst, const void* src, uint32_t n, int lane) {
-    uint4* d = static_cast<uint4*>(dst);
-    const uint4* s = static_cast<const uint4*>(src);
-    for (uint32_t i = (uint32_t)lane; i < n / 16u; i += 64u) d[i] = s[i];
-}
-
-// Per-wavefront LDS of one console: CPU RAM, nametables, OAM, palette and the console state.
-struct WaveLds {
-    uint8_t ram[NES_RAM_BYTES];
-    uint8_t nt[NES_NT_BYTES];
-    uint8_t oam[NES_OAM_BYTES];
-    uint8_t pal[NES_PAL_BYTES];
-    Con cs;
-    uint32_t scratch[34];   // the sprite-0 check's MMC2 pages
-};
-
-// One console per wavefront (blockDim 64): the console index comes from blockIdx only, so every emulator value is
-// wave-uniform; lane 0 runs the 6502 on the scalar unit (SGPRs, uniform branches) with the console's memories in
-// LDS, the 64 lanes copy them in and out. Eight waves per SIMD: 8192 consoles fill 256 CUs x 4 SIMDs x 8 in one
-// round (left to itself the compiler takes 71 VGPRs, 7 waves, and the eighth wave of every SIMD runs after the
-// others).
-// kBank: a decision frame whose picture is drawn from a frame bank (its render state is copied there at the end).
+// (the console-frame kernel's arguments and body: emu_kernel.h, shared with the translated kernels of jit.h)
 template <uint32_t B, bool kBank>
 __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(8, 8))) void k_emu_w(EmuArgs a) {
-    __shared__ __align__(16) WaveLds L;
-    const int count = a.mode == EMU_BOOT ? 1 : slot_count(a.g, a.use_list, a.e0, a.e1);
-    const int k = (int)blockIdx.x;
-    if (k >= count) return;
-    const int lane = (int)threadIdx.x;
-    const int e = a.mode == EMU_BOOT ? a.e0 : slot_env(a.g, a.use_list, a.e0, k);
-    const int ge = a.g.offset + e;
-    if (a.mode == EMU_RESTART && a.e.resetting[ge] != 1) return;   // 2: copied from a restart template
-    // EMU_IDLE: a restart from a saved level start emulates all of its idle frames (pad 0) in this one launch; a
-    // restart from the boot snapshot copied a template that holds them (rl/csrc/rlenv_core.cuh:312-318)
-    int frames = 1;
-    if (a.mode == EMU_IDLE) {
-        if (a.e.resetting[ge] == 0 || a.e.ep_start == nullptr || a.e.ep_start[ge] < 0) return;
-        frames = a.e.ep_idle[ge];
-        if (frames <= 0) return;
-    }
-    NesRec* rec = &a.g.recs[e];
-    wave_copy16(L.ram, rec->ram, NES_RAM_BYTES, lane);
-    wave_copy16(L.nt, rec->nt, NES_NT_BYTES, lane);
-    wave_copy16(L.oam, rec->oam, NES_OAM_BYTES, lane);
-    wave_copy16(L.pal, rec->pal, NES_PAL_BYTES, lane);
-    __syncthreads();
-    if (lane == 0) {
-        uint32_t pad = 0, fault = 0;
-        uint64_t target;
-        if (a.mode == EMU_BOOT) {
-            pad = a.boot_pad;
-            target = a.boot_target;
-        } else if (a.mode == EMU_TEMPLATE) {
-            target = a.boot_target + (uint64_t)e * NES_FRAME_DOTS;
-            fault = a.boot_fault[e];
-        } else {
-            if (a.mode == EMU_DECISION) pad = decision_pad(a, ge, a.f);
-            target = a.e.target[ge];
-            fault = a.e.fault[ge];
-        }
-        Con& cs = L.cs;
-        con_load(cs, rec);
-        const Mem m{rec, L.ram, L.nt, L.oam, L.pal, a.g.cart, L.scratch};
-        for (int i = 0; i < frames; ++i) {   // a faulted console stays put; its target and frame still advance
-            cs.pad = pad;
-            if (fault == 0) {
-                const uint32_t f = run_until_wave<B>(cs, m, c_optab.t, target, a.budget);
-                if (f != 0) {
-                    if (a.mode == EMU_BOOT) atomicOr(a.boot_fault, 1u);
-                    else if (a.mode == EMU_TEMPLATE) a.boot_fault[e] = f;
-                    else a.e.fault[ge] = f;
-                    fault = f;
-                }
-            }
-            target += NES_FRAME_DOTS;
-        }
-        con_store(cs, rec);
-        if (a.mode != EMU_BOOT && a.mode != EMU_TEMPLATE) {
-            a.e.target[ge] = target;
-            a.e.ep_frame[ge] += (uint32_t)frames;
-        }
-    }
-    __syncthreads();
-    wave_copy16(rec->ram, L.ram, NES_RAM_BYTES, lane);
-    wave_copy16(rec->nt, L.nt, NES_NT_BYTES, lane);
-    wave_copy16(rec->oam, L.oam, NES_OAM_BYTES, lane);
-    wave_copy16(rec->pal, L.pal, NES_PAL_BYTES, lane);
-    if constexpr (kBank) {   // the frame's render state (the log lane 0 wrote before the sync above)
-        FrameBank* b = &a.bank[e];
-        wave_copy16(b->log, rec->log, NES_LOG_WORDS * 4u, lane);
-        wave_copy16(b->nt, L.nt, NES_NT_BYTES, lane);
-        wave_copy16(b->oam, L.oam, NES_OAM_BYTES, lane);
-        if (lane == 0) b->log_n = L.cs.log_n;
-        if (a.bank_chr) wave_copy16(a.bank_chr + (size_t)e * NES_CHRRAM_BYTES, rec->chr_ram, NES_CHRRAM_BYTES, lane);
-    }
+    emu_body<B, kBank>(a);
 }
 
 // Power-on of one console record.
@@ -1092,9 +875,130 @@ struct DevMem {
     }
 };
 
+// ------------------------------------------------------------------------------- translated kernels (jit.h)
+// The device headers the translated kernels are compiled from, embedded by the Makefile.
+struct JitHeader { const char* name; const char* text; };
+const JitHeader kJitHeaders[] = {
+#include "jit_headers.inc"
+};
+// hiprtc options: the Makefile's device flags.
+const char* const kJitOptions[] = {"--offload-arch=gfx950", "-O3", "-std=c++17", "-ffp-contract=off", "-fno-fast-math",
+                                   "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops", "-mllvm",
+                                   "-structurizecfg-skip-uniform-regions=true"};
+
+// One translation compiled for gfx950, shared by every env of the process whose translation has the same text; with
+// RLENV_JIT_CACHE=<directory> the code object is also kept there, named by a hash of everything it is built from.
+struct JitJob {
+    std::string blocks, source;
+    std::atomic<int> state{0};   // 0 compiling, 1 compiled, 2 failed
+    std::vector<char> code;
+    std::string error;
+    double seconds = 0;
+};
+
+// A game's translated kernel: its job, the fetch table with the blocks' keys, the variant it was built for (decision
+// frames drawn from frame banks or not), and its module once loaded on the env's device.
+struct JitSlot {
+    std::shared_ptr<JitJob> job;
+    const uint32_t* fetchw = nullptr;
+    bool bank = false;
+    uint32_t blocks = 0, instructions = 0;
+    hipModule_t mod = nullptr;
+    hipFunction_t fn = nullptr;
+    bool failed = false;
+};
+
+uint64_t fnv1a(const char* p, size_t n, uint64_t h = 0xcbf29ce484222325ull) {
+    for (size_t i = 0; i < n; ++i) h = (h ^ (uint8_t)p[i]) * 0x100000001b3ull;
+    return h;
+}
+
+void jit_compile(JitJob& job) {
+    const auto t0 = std::chrono::steady_clock::now();
+    std::string path;
+    if (const char* dir = std::getenv("RLENV_JIT_CACHE"); dir && *dir) {
+        uint64_t h = fnv1a(job.source.data(), job.source.size());
+        h = fnv1a(job.blocks.data(), job.blocks.size(), h);
+        for (const JitHeader& hd : kJitHeaders) h = fnv1a(hd.text, strlen(hd.text), h);
+        for (const char* o : kJitOptions) h = fnv1a(o, strlen(o), h);
+        char name[48];
+        snprintf(name, sizeof name, "/rlenv_jit_%016llx.hsaco", (unsigned long long)h);
+        path = std::string(dir) + name;
+        if (FILE* f = fopen(path.c_str(), "rb")) {
+            char buf[65536];
+            size_t n;
+            while ((n = fread(buf, 1, sizeof buf, f)) > 0) job.code.insert(job.code.end(), buf, buf + n);
+            fclose(f);
+            if (!job.code.empty()) {
+                job.seconds = std::chrono::duration<double>(std::chrono::steady_clock::now() - t0).count();
+                job.state.store(1, std::memory_order_release);
+                return;
+            }
+        }
+    }
+    std::vector<const char*> texts, names;
+    for (const JitHeader& hd : kJitHeaders) {
+        texts.push_back(hd.text);
+        names.push_back(hd.name);
+    }
+    texts.push_back(job.blocks.c_str());
+    names.push_back("jit_blocks.inc");
+    hiprtcProgram prog = nullptr;
+    hiprtcResult r = hiprtcCreateProgram(&prog, job.source.c_str(), "rlenv_jit.hip", (int)texts.size(), texts.data(),
+                                         names.data());
+    if (r == HIPRTC_SUCCESS)
+        r = hiprtcCompileProgram(prog, (int)(sizeof kJitOptions / sizeof kJitOptions[0]), kJitOptions);
+    bool ok = r == HIPRTC_SUCCESS;
+    if (ok) {
+        size_t n = 0;
+        ok = hiprtcGetCodeSize(prog, &n) == HIPRTC_SUCCESS && n > 0;
+        job.code.resize(n);
+        ok = ok && hiprtcGetCode(prog, job.code.data()) == HIPRTC_SUCCESS;
+    }
+    if (!ok) {
+        job.error = std::string("hiprtc: ") + hiprtcGetErrorString(r);
+        size_t n = 0;
+        if (prog && hiprtcGetProgramLogSize(prog, &n) == HIPRTC_SUCCESS && n > 1) {
+            std::string log(n, '\0');
+            if (hiprtcGetProgramLog(prog, &log[0]) == HIPRTC_SUCCESS) job.error += "\n" + log.substr(0, 4000);
+        }
+    }
+    if (prog) hiprtcDestroyProgram(&prog);
+    if (ok && !path.empty()) {   // written aside, then renamed: a reader never sees half a file
+        const std::string tmp = path + ".tmp" + std::to_string((unsigned long long)std::hash<std::thread::id>{}(
+                                                    std::this_thread::get_id()));
+        if (FILE* f = fopen(tmp.c_str(), "wb")) {
+            const bool written = fwrite(job.code.data(), 1, job.code.size(), f) == job.code.size();
+            fclose(f);
+            if (!written || rename(tmp.c_str(), path.c_str()) != 0) remove(tmp.c_str());
+        }
+    }
+    job.seconds = std::chrono::duration<double>(std::chrono::steady_clock::now() - t0).count();
+    job.state.store(ok ? 1 : 2, std::memory_order_release);
+}
+
+// The job of (blocks, source): this process's existing one (fresh = false), or a new one the caller compiles.
+constexpr int kJitMinEnvs = 1024;   // games of fewer envs run the library's kernel unless RLENV_JIT=sync
+
+std::shared_ptr<JitJob> jit_job(std::string blocks, std::string source, bool& fresh) {
+    static std::mutex lock;
+    static std::map<std::string, std::shared_ptr<JitJob>> jobs;
+    std::lock_guard<std::mutex> hold(lock);
+    std::string key = source + blocks;
+    auto it = jobs.find(key);
+    fresh = it == jobs.end();
+    if (!fresh) return it->second;
+    auto job = std::make_shared<JitJob>();
+    job->blocks = std::move(blocks);
+    job->source = std::move(source);
+    jobs.emplace(std::move(key), job);
+    return job;
+}
+
 struct GameH {
     GameK k;
     int game;
+    std::shared_ptr<JitSlot> jit;   // fixed-PRG carts: the translated kernel (nullptr: none)
 };
 
 // Kernel classes of a decision, for the per-kernel clock (rlenv_kernel_times).
@@ -1222,7 +1126,51 @@ struct Env {
     int lv_cap = 0;          // level starts / places per game (0 = off)
     uint32_t* scratch = nullptr;   // this device's static restart-queue scratch (rlenv_step_static)
     mutable KernelClock clock;
+    ~Env() {
+        bool loaded = false;
+        for (const GameH& gh : games) loaded = loaded || (gh.jit && gh.jit->mod);
+        if (loaded) {   // no launch of a translated kernel may be left in flight when its module goes
+            (void)hipSetDevice(device);
+            (void)hipDeviceSynchronize();
+            for (const GameH& gh : games)
+                if (gh.jit && gh.jit->mod) (void)hipModuleUnload(gh.jit->mod);
+        }
+    }
 };
+
+// The translated kernel of the game whose device arguments are g (found by its first env, which copies keep).
+JitSlot* jit_slot(const Env& env, const GameK& g) {
+    for (const GameH& gh : env.games)
+        if (gh.jit && gh.k.offset == g.offset && gh.k.n == g.n) return gh.jit.get();
+    return nullptr;
+}
+
+// Whether the translated kernel can be launched: loads its module on the env's device the first time its job has
+// compiled. A failed compile or load leaves the game on the library's own kernel (the results are the same).
+bool jit_ready(const Env& env, JitSlot& j) {
+    if (j.fn) return true;
+    if (j.failed || !j.job) return false;
+    const int st = j.job->state.load(std::memory_order_acquire);
+    if (st == 0) return false;
+    if (st == 2) {
+        j.failed = true;
+        return false;
+    }
+    int cur = -1;
+    (void)hipGetDevice(&cur);
+    if (cur != env.device) (void)hipSetDevice(env.device);
+    const bool ok = hipModuleLoadData(&j.mod, j.job->code.data()) == hipSuccess &&
+                    hipModuleGetFunction(&j.fn, j.mod, "k_emu_jit") == hipSuccess;
+    if (!ok) {
+        (void)hipGetLastError();
+        if (j.mod) (void)hipModuleUnload(j.mod);
+        j.mod = nullptr;
+        j.fn = nullptr;
+        j.failed = true;
+    }
+    if (cur >= 0 && cur != env.device) (void)hipSetDevice(cur);
+    return ok;
+}
 
 // The address of `scratch` on each device, taken once with that device current.
 uint32_t* scratch_of(int device) {
@@ -1326,6 +1274,18 @@ void launch_emu(const Env& env, const GameK& g, const Outs& o, int mode, int f, 
               bank >= 0 ? g.bank[bank] : nullptr, bank >= 0 ? g.bank_chr[bank] : nullptr};
     const int blocks = use_list ? g.n : e1 - e0;
     const int cls = mode == EMU_DECISION ? KC_EMU : mode == EMU_IDLE ? KC_EMU_IDLE : KC_EMU_RESTART;
+    // decision frames of a fixed-PRG cart run its translated kernel once that is compiled and loaded, when it was
+    // built for the way this launch's frame is drawn
+    JitSlot* js = mode == EMU_DECISION && blocks > 0 ? jit_slot(env, g) : nullptr;
+    if (js && js->bank == (a.bank != nullptr) && jit_ready(env, *js)) {
+        a.g.cart.fetchw = js->fetchw;
+        void* args[] = {&a};
+        env.clock.run(cls, st, [&] {
+            (void)hipModuleLaunchKernel(js->fn, (unsigned)blocks, 1, 1, 64, 1, 1, 0, st, args, nullptr);
+        });
+        trace("emu_jit", st);
+        return;
+    }
     if (blocks > 0)
         env.clock.run(cls, st, [&] {
             // the fast path knows two kinds of board: fixed 32 KB PRG (NROM, CNROM) and banked PRG (the rest)
@@ -1590,6 +1550,11 @@ void* rlenv_create(int ngames, const int* game_ids, const uint8_t* const* roms, 
         e.ep_maxlvl = env->mem.zeros<int32_t>(N);
         e.ep_idle = env->mem.zeros<int32_t>(N);
         e.resetting = env->mem.zeros<uint8_t>(N);
+        // translated kernels of fixed-PRG carts: RLENV_JIT=0 (or off) none; sync for every such game; otherwise
+        // for games of at least kJitMinEnvs envs (a smaller one gains less than the compile takes)
+        const char* jv = std::getenv("RLENV_JIT");
+        const int jit_mode = jv && (!strcmp(jv, "0") || !strcmp(jv, "off")) ? 0 : jv && !strcmp(jv, "sync") ? 2 : 1;
+        std::vector<std::string> jit_cases((size_t)ngames);
         int offset = 0;
         for (int i = 0; i < ngames; ++i) {
             if (game_ids[i] < 0 || game_ids[i] >= RL10_NUM_GAMES)
@@ -1645,6 +1610,23 @@ void* rlenv_create(int ngames, const int* game_ids, const uint8_t* const* roms, 
                 for (uint32_t a = 0x8000u; a <= 0xFFFDu; ++a)
                     fetch_entry(&f[2u * a], a, p.prg[a & mask], p.prg[(a + 1u) & mask], p.prg[(a + 2u) & mask],
                                 true);
+                // the translation, and a fetch table with its blocks' keys
+                if (jit_mode == 2 || (jit_mode == 1 && g.n >= kJitMinEnvs)) {
+                    JitProgram jp = jit_translate_fixed(img);
+                    if (!jp.leader_addr.empty()) {
+                        std::vector<uint32_t> fj(f);
+                        for (size_t b = 0; b < jp.leader_addr.size(); ++b)
+                            fj[2u * jp.leader_addr[b]] = kBlockKey + (uint32_t)b;
+                        auto js = std::make_shared<JitSlot>();
+                        uint32_t* fjw = static_cast<uint32_t*>(env->mem.alloc(fj.size() * 4));
+                        env->mem.upload(fjw, fj.data(), fj.size() * 4);
+                        js->fetchw = fjw;
+                        js->blocks = (uint32_t)jp.leader_addr.size();
+                        js->instructions = jp.instructions;
+                        gh.jit = js;
+                        jit_cases[i] = std::move(jp.cases);
+                    }
+                }
             } else {   // by PRG offset; $02 where an instruction would end on the last byte of its 8 KB page
                 f.assign(2u * p.prg.size(), 0u);
                 const auto at = [&](uint32_t k) { return k < p.prg.size() ? (uint32_t)p.prg[k] : 0u; };
@@ -1676,6 +1658,28 @@ void* rlenv_create(int ngames, const int* game_ids, const uint8_t* const* roms, 
         }
         env->gs.create(env->games.size());
         if (hipDeviceSynchronize() != hipSuccess || check("create")) throw std::runtime_error(g_error);
+        // the translations' kernels, compiled in parallel (one thread per new translation) before the env is returned
+        std::vector<std::shared_ptr<JitJob>> fresh;
+        for (size_t i = 0; i < env->games.size(); ++i) {
+            GameH& gh = env->games[i];
+            if (!gh.jit) continue;
+            // the variant the decision frames use: drawn from frame banks in a one-game env of one round of waves
+            gh.jit->bank = env->games.size() == 1 && gh.k.n <= env->one_round;
+            bool is_new = false;
+            gh.jit->job = jit_job(std::move(jit_cases[i]), jit_module_source(gh.jit->bank), is_new);
+            if (is_new) fresh.push_back(gh.jit->job);
+        }
+        {
+            std::vector<std::thread> workers;
+            for (const auto& job : fresh) workers.emplace_back([job] { jit_compile(*job); });
+            for (std::thread& t : workers) t.join();
+        }
+        for (GameH& gh : env->games)
+            if (gh.jit) {
+                while (gh.jit->job->state.load(std::memory_order_acquire) == 0)   // another env's compile of it
+                    std::this_thread::sleep_for(std::chrono::milliseconds(5));
+                (void)jit_ready(*env, *gh.jit);
+            }
         return env;
     } catch (const std::exception& ex) {
         g_error = ex.what();
@@ -1921,6 +1925,76 @@ int rlenv_read_consoles(void* h, int gi, int first, int count, uint8_t* out, voi
 }
 
 void rlenv_set_kernel_timing(void* h, int on) { static_cast<Env*>(h)->clock.on = on != 0; }
+
+int rlenv_jit_wait(void* h) {
+    Env& env = *static_cast<Env*>(h);
+    std::string err;
+    for (size_t gi = 0; gi < env.games.size(); ++gi) {
+        JitSlot* j = env.games[gi].jit.get();
+        if (!j || !j->job) continue;
+        while (j->job->state.load(std::memory_order_acquire) == 0)
+            std::this_thread::sleep_for(std::chrono::milliseconds(5));
+        if (!jit_ready(env, *j))
+            err += "game " + std::to_string(gi) + ": " +
+                   (j->job->error.empty() ? std::string("loading the translated kernel failed") : j->job->error) + "\n";
+    }
+    if (!err.empty()) {
+        g_error = "jit: " + err;
+        return 1;
+    }
+    return 0;
+}
+
+int rlenv_jit_translate(const uint8_t* rom, size_t rom_size, int compile, int32_t* out, char* text, size_t text_cap) {
+    try {
+        const Parsed p = parse_ines(rom, rom_size);
+        if (p.board != NES_BOARD_NROM && p.board != NES_BOARD_CNROM) {
+            g_error = "jit_translate: only fixed-PRG boards (NROM, CNROM) are translated";
+            return 1;
+        }
+        std::vector<uint8_t> img(32768u);   // as the CPU sees it: a 16 KB image mirrored
+        for (size_t k = 0; k < img.size(); ++k) img[k] = p.prg[k % p.prg.size()];
+        JitProgram jp = jit_translate_fixed(img);
+        out[0] = (int32_t)jp.leader_addr.size();
+        out[1] = (int32_t)jp.instructions;
+        out[2] = -1;
+        out[3] = 0;
+        if (text && text_cap) {
+            const size_t n = std::min(text_cap - 1, jp.cases.size());
+            memcpy(text, jp.cases.data(), n);
+            text[n] = 0;
+        }
+        if (compile) {
+            JitJob job;
+            job.blocks = std::move(jp.cases);
+            job.source = jit_module_source(false);
+            jit_compile(job);
+            out[2] = (int32_t)(job.seconds * 1000.0);
+            out[3] = (int32_t)job.code.size();
+            if (job.state.load() != 1) {
+                g_error = job.error;
+                return 1;
+            }
+        }
+        return 0;
+    } catch (const std::exception& ex) {
+        g_error = ex.what();
+        return 1;
+    }
+}
+
+int rlenv_jit_status(void* h, int gi, int32_t* out) {
+    Env& env = *static_cast<Env*>(h);
+    if (gi < 0 || gi >= (int)env.games.size()) { g_error = "jit_status: bad game"; return 1; }
+    const JitSlot* j = env.games[gi].jit.get();
+    const int st = !j ? 0 : j->fn ? 2 : (j->failed || (j->job && j->job->state.load() == 2)) ? 3 : 1;
+    out[0] = st;
+    out[1] = j ? (int32_t)j->blocks : 0;
+    out[2] = j ? (int32_t)j->instructions : 0;
+    out[3] = j && j->job && j->job->state.load() != 0 ? (int32_t)(j->job->seconds * 1000.0) : -1;
+    out[4] = j && j->bank ? 1 : 0;
+    return 0;
+}
 
 int rlenv_kernel_times(void* h, double* ms, int64_t* count, int n) {
     if (n < KC_COUNT) { g_error = "kernel_times: need room for every kernel class (9)"; return 1; }

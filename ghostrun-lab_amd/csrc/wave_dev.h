@@ -392,17 +392,22 @@ __device__ __forceinline__ uint32_t fx_hot(Hot& h, const Mem& m, Con& cs, uint32
 // of pc times 8 ($02 where an instruction would end on the last byte of its 8 KB page, and kOffPrg for a pc outside
 // PRG).
 template <uint32_t B>
-__device__ __forceinline__ uint32_t fast_step(Hot& h, const Mem& m, Con& cs, uint32_t* op_out) {
+__device__ __forceinline__ uint32_t fast_step(Hot& h, const Mem& m, Con& cs, uint32_t op, uint32_t base) {
     const uint32_t pcs = h.pc;
-    // (two 32-bit loads, which the compiler pairs into one 64-bit load: read as the halves of a 64-bit value,
-    // base's compares would become 64-bit ones, which the scalar unit has only for equality)
-    ConstU32* e = (ConstU32*)((ConstU8*)m.cart.fetchw + pcs);
-    const uint32_t op = e[0], base = e[1];
-    *op_out = op;
     if (__builtin_expect(op >= kHotKey, 1)) return fx_hot<B>(h, m, cs, pcs, op, base);
     // (read back as an opaque scalar: with the range op < $100 known the compiler narrows the switch to 8 bits and
     // widens it again with two masks)
     return fx_all<B>(h, m, cs, pcs, uni(op), base);
+}
+// The same, fetching the entry itself.
+template <uint32_t B>
+__device__ __forceinline__ uint32_t fast_step(Hot& h, const Mem& m, Con& cs, uint32_t* op_out) {
+    // (two 32-bit loads, which the compiler pairs into one 64-bit load: read as the halves of a 64-bit value,
+    // base's compares would become 64-bit ones, which the scalar unit has only for equality)
+    ConstU32* e = (ConstU32*)((ConstU8*)m.cart.fetchw + h.pc);
+    const uint32_t op = e[0], base = e[1];
+    *op_out = op;
+    return fast_step<B>(h, m, cs, op, base);
 }
 #undef ND_FX16
 #undef ND_FX
@@ -415,6 +420,26 @@ __device__ __forceinline__ uint32_t dmc_distance(uint64_t now, uint64_t event) {
     const uint64_t d = event - now;
     return d > 0xFFFFFFFFull ? 0xFFFFFFFFu : (uint32_t)d;
 }
+
+#ifdef RLENV_JIT_INC
+// The most a translated block's instruction can take off the burst counter: its cycles with the page-crossing
+// penalty and a taken branch to another page.
+constexpr uint32_t jit_maxtake(uint32_t op) {
+    return ((((kOptab.t[op] >> 4) & 15u) + ((kOptab.t[op] & D_PEN) ? 1u : 0u) +
+             (((kOptab.t[op] >> 8) & 15u) == G_BR ? 2u : 0u)) << 14) - 1u;
+}
+// One instruction of a block (inside the block's room), and the block's first instruction alone (no room for the
+// block: the interpreter's own test ends the burst).
+#define JIT_STEP(op, pcs, base)                              \
+    t = fx<B, kOptab.t[op]>(h, m, cs, pcs, base);            \
+    if (t == kGeneric) { take = t; goto burst_end; }          \
+    v -= t;
+#define JIT_ONE(op, pcs, base)                               \
+    t = fx<B, kOptab.t[op]>(h, m, cs, pcs, base);            \
+    if (v < t) { take = t; goto burst_end; }                  \
+    v -= t;                                                   \
+    continue;
+#endif
 
 // The frame loop (rl/csrc/nes_machine.cuh:67-103) for a console whose state `cs` lives in LDS: instructions until a
 // settle reaches absolute dot `target`, the PPU settled lazily when the unsettled dots reach the event horizon and
@@ -498,10 +523,28 @@ __device__ __forceinline__ uint32_t run_until_wave(Con& cs, const Mem& m, const 
             const uint32_t lm1_0 = lm1;
             uint32_t v = lm1 << 14, take;
             for (;;) {
+#ifdef RLENV_JIT_INC
+                ConstU32* e = (ConstU32*)((ConstU8*)m.cart.fetchw + h.pc);
+                const uint32_t fop = e[0], fbase = e[1];
+                if constexpr (B == NES_BOARD_NROM) {   // a translated block starts here (jit.h)
+                    if (fop >= kBlockKey) {
+                        uint32_t t;
+                        switch (fop) {
+#include RLENV_JIT_INC
+                            default: __builtin_unreachable();
+                        }
+                    }
+                }
+                take = fast_step<B>(h, m, cs, fop, fbase);
+#else
                 take = fast_step<B>(h, m, cs, &op);
+#endif
                 if (v < take) break;
                 v -= take;
             }
+#ifdef RLENV_JIT_INC
+        burst_end:
+#endif
             cyc = (take + 1u) >> 14;               // 0 for kGeneric
             lm1 = v >> 14;
             const uint32_t n = (v & 0x3FFFu) + 1u;

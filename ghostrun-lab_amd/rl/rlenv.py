@@ -89,6 +89,9 @@ _ABI = {
     'rlenv_step_game': (_I, [_P, _I, _P, _P, _P], True),
     'rlenv_step_range': (_I, [_P, _I, _I, _I, _P, _P, _P], True),
     'rlenv_step_static': (_I, [_P, _P], True),
+    'rlenv_jit_wait': (_I, [_P], True),
+    'rlenv_jit_status': (_I, [_P, _I, _P], True),
+    'rlenv_jit_translate': (_I, [_P, _SZ, _I, _P, _P, _SZ], True),
     'rl_host_alloc': (_P, [_SZ], True),
     'rl_host_free': (_VOID, [_P], True),
     'rl_memcpy_async': (_I, [_P, _P, _SZ, _P], True),
@@ -255,6 +258,20 @@ class RlEnv:
     def step_range(self, gi, start, count, obs, emph):
         """step_game restricted to envs start..start+count-1 of game gi."""
         self._check(self.lib.rlenv_step_range(self.h, gi, start, count, _addr(obs), _addr(emph), self._stream()))
+
+    # ------------------------------------------------------------------ translated kernels
+    def jit_wait(self):
+        """Wait until the translated kernel of every fixed-PRG game (include/rlenv_api.h rlenv_jit_wait) is compiled
+        and loaded; an error if a compile failed."""
+        self._check(self.lib.rlenv_jit_wait(self.h))
+
+    def jit_status(self, gi=0) -> dict:
+        """State of game gi's translated kernel: state ('none', 'compiling', 'loaded', 'failed'), blocks,
+        instructions, compile_ms (-1 while compiling), bank (built for frames drawn from frame banks)."""
+        out = (ctypes.c_int32 * 5)()
+        self._check(self.lib.rlenv_jit_status(self.h, gi, out))
+        return dict(state=('none', 'compiling', 'loaded', 'failed')[out[0]], blocks=out[1], instructions=out[2],
+                    compile_ms=out[3], bank=bool(out[4]))
 
     def set_episode_level_end(self, level):
         """End episodes (reason level_clear) on reaching `level`; 0 = never."""

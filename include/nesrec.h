@@ -12,8 +12,10 @@
  */
 #ifndef NESREC_H
 #define NESREC_H
+#ifndef __HIPCC_RTC__   // (built in where hiprtc compiles this at run time)
 #include <stddef.h>
 #include <stdint.h>
+#endif
 
 #define NES_RAM_BYTES 2048u
 #define NES_NT_BYTES 2048u

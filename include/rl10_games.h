@@ -12,8 +12,10 @@
  */
 #ifndef RL10_GAMES_H
 #define RL10_GAMES_H
+#ifndef __HIPCC_RTC__   // (built in where hiprtc compiles this at run time)
 #include <math.h>
 #include <stdint.h>
+#endif
 
 #include "rlenv_state.h"
 

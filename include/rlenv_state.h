@@ -6,7 +6,9 @@
  */
 #ifndef RLENV_STATE_H
 #define RLENV_STATE_H
+#ifndef __HIPCC_RTC__   // (built in where hiprtc compiles this at run time)
 #include <stdint.h>
+#endif
 
 typedef struct Rl10Signals {      /* reward.Signals with explicit "has" flags for Python's None */
     uint8_t in_play, progress_valid, dying, has_lives, has_health, has_score, game_over, won;

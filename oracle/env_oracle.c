@@ -1165,3 +1165,10 @@ int rlenv_kernel_times(void* h, double* ms, int64_t* count, int n) {
     for (int i = 0; i < n; ++i) { ms[i] = 0.0; count[i] = 0; }
     return 0;
 }
+/* The oracle runs no translated kernels: nothing to wait for, no translation per game. */
+int rlenv_jit_wait(void* h) { (void)h; return 0; }
+int rlenv_jit_status(void* h, int gi, int32_t* out) {
+    (void)h; (void)gi;
+    out[0] = 0; out[1] = 0; out[2] = 0; out[3] = -1; out[4] = 0;
+    return 0;
+}

@@ -54,7 +54,8 @@ def test_product_device_code_has_no_packed_fp32_and_no_scratch(tmp_path):
     flags = makefile_flags()
     assert all(f in flags for f in NO_PACKED)
     remarks = []
-    asm = device_asm(CSRC / 'rlenv_hip.hip', tmp_path / 'rlenv.s', [f'-I{ROOT / "include"}', f'-I{CSRC}'] +
+    asm = device_asm(CSRC / 'rlenv_hip.hip', tmp_path / 'rlenv.s', [f'-I{ROOT / "include"}', f'-I{CSRC}',
+                                                                     f'-I{CSRC / "_build"}'] +
                      [f for f in flags if not f.startswith('--offload-arch') and f != '-O3' and f != '-std=c++17'],
                      remarks)
     assert '.amdgcn_target "amdgcn-amd-amdhsa--gfx950"' in asm
@@ -63,3 +64,33 @@ def test_product_device_code_has_no_packed_fp32_and_no_scratch(tmp_path):
     scratch = [int(x) for x in re.findall(r'ScratchSize \[bytes/lane\]: (\d+)', remarks[0])]
     assert len(names) == len(scratch) >= 15 and any('k_emu_w' in n for n in names)
     assert not [n for n, b in zip(names, scratch) if b], list(zip(names, scratch))
+
+
+@pytest.mark.skipif(not Path(HIPCC).exists(), reason='hipcc not installed')
+def test_translated_kernel_device_code_has_no_packed_fp32_and_no_scratch(tmp_path):
+    """The kernel the library compiles at run time from a cartridge's translated blocks (jit.h), here the blocks of
+    the benchmark cart (rl.synth.nrom_cart(1)) as rlenv_jit_translate writes them, built with the same flags."""
+    import ctypes
+    from rl import synth
+    from rl.rlenv import bind_library
+    from helpers import HIP_LIB
+    lib = bind_library(HIP_LIB)
+    rom = synth.nrom_cart(1)
+    out = (ctypes.c_int32 * 4)()
+    text = ctypes.create_string_buffer(1 << 20)
+    assert lib.rlenv_jit_translate(rom, len(rom), 0, out, text, len(text)) == 0
+    assert out[0] > 50 and out[1] > 200 and len(text.value) < len(text) - 1
+    (tmp_path / 'jit_blocks.inc').write_bytes(text.value)
+    src = tmp_path / 'jit.hip'
+    src.write_text('#define RLENV_JIT_INC "jit_blocks.inc"\n#include "emu_kernel.h"\n'
+                   'extern "C" __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(8, 8)))\n'
+                   'void k_emu_jit(nd::EmuArgs a) { nd::emu_body<NES_BOARD_NROM, true>(a); }\n')
+    flags = makefile_flags()
+    remarks = []
+    asm = device_asm(src, tmp_path / 'jit.s', [f'-I{ROOT / "include"}', f'-I{CSRC}', f'-I{tmp_path}'] +
+                     [f for f in flags if not f.startswith('--offload-arch') and f != '-O3' and f != '-std=c++17'],
+                     remarks)
+    assert 'k_emu_jit' in asm and not PACKED.search(asm)
+    scratch = [int(x) for x in re.findall(r'ScratchSize \[bytes/lane\]: (\d+)', remarks[0])]
+    occupancy = [int(x) for x in re.findall(r'Occupancy \[waves/SIMD\]: (\d+)', remarks[0])]
+    assert scratch == [0] and occupancy == [8], (scratch, occupancy)

@@ -1,0 +1,151 @@
+"""Translated kernels (ghostrun-lab_amd/csrc/jit.h) against the CPU oracle: the decision frames of a fixed-PRG cart
+run the kernel compiled from its translated blocks, and every output and every console record must still equal the
+oracle's, bit for bit (the reference's own check is rl/tests/gpu_check.py:28-53: every output every step). Each case
+forces the translation (RLENV_JIT=sync) on a small env and asserts that it was loaded; the carts cover what ends a
+block early or keeps an instruction out of one: the idle JMP-to-self loop and NMI-driven logic (SMB-like cart), DMC
+events inside bursts, an unofficial opcode (the fault end), writes to ROM (CNROM bank switches, with and without bus
+conflicts), instruction-budget stops, and the two variants (frames drawn from frame banks in a one-game env, from
+the records in a two-game env)."""
+import os
+
+import numpy as np
+import pytest
+import torch
+
+from helpers import HIP_LIB, ORACLE_LIB
+from rl import synth
+from rl.rlenv import RlEnv
+from test_gpu_parity import compare, pair, run
+
+
+def translated_pair(n, cart, **kw):
+    os.environ['RLENV_JIT'] = 'sync'
+    try:
+        cpu, gpu = pair(n, cart, **kw)
+    finally:
+        del os.environ['RLENV_JIT']
+    st = gpu.jit_status(0)
+    assert st['state'] == 'loaded' and st['blocks'] > 0 and st['instructions'] > 0, st
+    gpu.jit_wait()
+    return cpu, gpu, st
+
+
+@pytest.mark.gpu
+def test_translated_benchmark_cart():
+    print('case: translated NROM seed 1 (the benchmark cart), 16 consoles, raw pads, sticky, 24 decisions',
+          flush=True)
+    cpu, gpu, st = translated_pair(16, synth.nrom_cart(1), seed=5, sticky=True, idle_max=0, dropout=False,
+                                   pad_mode=True)
+    assert st['bank']   # one game, one round of waves: decision frames drawn from frame banks
+    run(cpu, gpu, 24, 0, True)
+
+
+@pytest.mark.gpu
+def test_translated_smb_like_idle_loop_and_ends():
+    print('case: translated SMB-like seed 2, 24 consoles, raw pads, level end 0, Geometric(1/16) ends, idle 0..3, '
+          '40 decisions', flush=True)
+    cpu, gpu, _ = translated_pair(24, synth.smb_like_cart(2), seed=12, sticky=True, idle_max=3, dropout=True,
+                                  pad_mode=True, end_prob=1 / 16, dropout_gap=0.05)
+    cpu.set_episode_level_end(0)
+    gpu.set_episode_level_end(0)
+    run(cpu, gpu, 40, 4, True)
+
+
+@pytest.mark.gpu
+def test_translated_dmc_cart():
+    print('case: translated DMC cart seed 1, 16 consoles, raw pads, sticky, 24 decisions', flush=True)
+    cpu, gpu, _ = translated_pair(16, synth.dmc_cart(1), seed=31, sticky=True, idle_max=2, dropout=False,
+                                  pad_mode=True)
+    run(cpu, gpu, 24, 31, True)
+
+
+@pytest.mark.gpu
+def test_translated_fault_cart():
+    print('case: translated fault cart, 8 consoles, 12 decisions (end reason 5 every episode)', flush=True)
+    cpu, gpu, _ = translated_pair(8, synth.fault_cart(3), seed=32, sticky=False, idle_max=0, dropout=False,
+                                  pad_mode=True)
+    run(cpu, gpu, 12, 32, True)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize('conflicts', [False, True])
+def test_translated_cnrom_bank_switches(conflicts):
+    print(f'case: translated CNROM seed 2, bus conflicts {conflicts}, 16 consoles, Geometric(1/8) ends, 16 decisions',
+          flush=True)
+    cpu, gpu, _ = translated_pair(16, synth.cnrom_cart(2, conflicts=conflicts), seed=19, sticky=True, idle_max=1,
+                                  dropout=True, pad_mode=True, end_prob=1 / 8)
+    run(cpu, gpu, 16, 5, True)
+
+
+@pytest.mark.gpu
+def test_translated_instruction_budget_exit():
+    print('case: translated NROM seed 3, RLENV_BUDGET 3000, 8 consoles, 10 decisions', flush=True)
+    os.environ['RLENV_BUDGET'] = '3000'
+    try:
+        cpu, gpu, _ = translated_pair(8, synth.nrom_cart(3), seed=33, sticky=True, idle_max=0, dropout=False,
+                                      pad_mode=True)
+    finally:
+        del os.environ['RLENV_BUDGET']
+    run(cpu, gpu, 10, 33, True)
+    fd = cpu.consoles(0)[:, 0x18:0x1C].copy().view(np.uint32)[:, 0]
+    assert (fd != 82182).any()   # some frames stopped short of vblank
+
+
+@pytest.mark.gpu
+def test_translated_two_games_from_the_records():
+    """Two games: each game's decision frames are drawn from the records (no frame banks), the other variant."""
+    print('case: translated tetris (NROM seed 6) + smb (SMB-like seed 5), 8 + 8 consoles, 16 decisions', flush=True)
+    roms = {'smb': synth.smb_like_cart(5), 'tetris': synth.nrom_cart(6)}
+    kw = dict(seed=35, sticky=True, idle_max=2, dropout=True, pad_mode=True, ram_hash=True, roms=roms)
+    os.environ['RLENV_JIT'] = 'sync'
+    try:
+        gpu = RlEnv({'smb': 8, 'tetris': 8}, device='cuda', lib_path=HIP_LIB, **kw)
+    finally:
+        del os.environ['RLENV_JIT']
+    cpu = RlEnv({'smb': 8, 'tetris': 8}, device='cpu', lib_path=ORACLE_LIB, **kw)
+    for gi in range(2):
+        st = gpu.jit_status(gi)
+        assert st['state'] == 'loaded' and not st['bank'], st
+    g = torch.Generator().manual_seed(35)
+    cpu.start()
+    gpu.start()
+    compare(cpu, gpu, 'start')
+    for t in range(16):
+        act = torch.randint(0, 256, (16,), generator=g, dtype=torch.int16)
+        cpu.actions.copy_(act)
+        gpu.actions.copy_(act.cuda())
+        cpu.step()
+        gpu.step()
+        compare(cpu, gpu, f'step {t}')
+    for gi in range(2):
+        assert np.array_equal(cpu.consoles(gi), gpu.consoles(gi)), gi
+
+
+@pytest.mark.gpu
+def test_translated_equals_interpreter_at_full_size():
+    """8192 consoles of the benchmark cart, sticky: the env that runs the translated kernel (a game this size is
+    translated by default) and one that does not (RLENV_JIT=0) give the same outputs and records, every decision."""
+    print('case: NROM seed 1, 8192 consoles, translated vs the library kernel, 12 decisions', flush=True)
+    kw = dict(seed=1, sticky=True, idle_max=0, dropout=False, pad_mode=True, ram_hash=True,
+              roms={'smb': synth.nrom_cart(1)})
+    fast = RlEnv({'smb': 8192}, device='cuda', lib_path=HIP_LIB, **kw)
+    assert fast.jit_status(0)['state'] == 'loaded'
+    os.environ['RLENV_JIT'] = '0'
+    try:
+        slow = RlEnv({'smb': 8192}, device='cuda', lib_path=HIP_LIB, **kw)
+    finally:
+        del os.environ['RLENV_JIT']
+    assert slow.jit_status(0)['state'] == 'none'
+    g = torch.Generator().manual_seed(41)
+    fast.start()
+    slow.start()
+    for t in range(12):
+        act = torch.randint(0, 256, (8192,), generator=g, dtype=torch.int16).cuda()
+        fast.actions.copy_(act)
+        slow.actions.copy_(act)
+        fast.step()
+        slow.step()
+        torch.cuda.synchronize()
+        for k in ('obs', 'emph', 'reward', 'done', 'ram_hash', 'pads'):
+            assert torch.equal(getattr(fast, k), getattr(slow, k)), (t, k)
+    assert np.array_equal(fast.consoles(0), slow.consoles(0))
