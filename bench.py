@@ -131,7 +131,7 @@ def main():
             out['workloads'][name] = {k: res[k] for k in ('metric', 'value', 'unit', 'ms_per_step', 'steps', 'warmup',
                                                           'dtype', 'config', 'roofline', 'parity', 'kernels',
                                                           'frames_per_s', 'emulated_instructions_per_s',
-                                                          'step_output_gbps') if k in res}
+                                                          'step_output_gbps', 'translated') if k in res}
             torch.cuda.empty_cache()
     print(json.dumps(out), flush=True)
     bad = [n for n, r in [(args.workload, out)] + list(out.get('workloads', {}).items())
