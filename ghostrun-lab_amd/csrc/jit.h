@@ -9,7 +9,7 @@
 // the generic step. Code is found by following those from the vectors (a recursive descent over CPU addresses
 // $8000-$FFFD); the byte sequence each leader starts is decoded on its own, so overlapping instruction streams are
 // fine. A block ends at a branch, a jump, a call or a return, before an instruction that always needs the generic
-// step (I/O other than $2002 reads and $4016, a jump to itself, an unofficial opcode), at the next leader, or after
+// step (I/O other than $2002 reads, $4016 and PRG RAM, a jump to itself, an unofficial opcode), at the next leader, or after
 // kJitMaxBlock instructions; blocks are made in address order until kJitMaxInstructions. A copy of the fetch table
 // marks each block's first entry with the key kBlockKey + block index; at any other address the interpreter runs as
 // before.
@@ -53,9 +53,10 @@ inline bool jit_always_generic(uint32_t a, uint32_t op, uint32_t b1, uint32_t b2
         return (ea >= 0x2000u && ea < 0x8000u) || (a1 >= 0x2000u && a1 < 0x8000u);
     }
     if (mode != M_ABS || grp == G_JSR) return false;
-    if (rd && wr) return ea >= 0x2000u;
-    if (wr) return ea >= 0x2000u && ea != 0x4016u;
-    if (rd) return !(ea < 0x2000u || ea >= 0x8000u || ea == 0x4016u || (ea & 0xE007u) == 0x2002u);
+    const bool prg_ram = ea >= 0x6000u && ea < 0x8000u;   // served by the fast path except on MMC1 (decided then)
+    if (rd && wr) return ea >= 0x2000u && !prg_ram;
+    if (wr) return ea >= 0x2000u && ea != 0x4016u && !prg_ram;
+    if (rd) return !(ea < 0x2000u || ea >= 0x8000u || ea == 0x4016u || (ea & 0xE007u) == 0x2002u || prg_ram);
     return false;
 }
 
@@ -186,10 +187,156 @@ inline JitProgram jit_translate_fixed(const std::vector<uint8_t>& prg) {
     return p;
 }
 
+// The blocks of a banked PRG image (MMC1, UxROM, MMC3, MMC2), by PRG offset: which bank a window holds is known only
+// at run time, so a block is a run of one 8 KB page, pcs its PRG offset x 8 (the fetch table's index on these
+// boards, wave_dev.h), and only branches inside the page and falls into the next leader of the page jump straight;
+// jumps, calls and returns map their target through the page table at run time and go back to the loop. Leaders:
+// the vectors' offsets in the last two pages (the banks fixed at $C000-$FFFF at power-on), then, for every JMP or JSR
+// target found, its offset within its 8 KB window in every page (any bank may be mapped there), and inside a page
+// the branch targets, return points and the instruction after an always-generic one. Blocks are kept in the order
+// they are found from the vectors first, within kJitMaxInstructions.
+inline JitProgram jit_translate_banked(const std::vector<uint8_t>& prg) {
+    const uint32_t size = (uint32_t)prg.size(), pages = size >> 13;
+    auto rd = [&](uint32_t o) { return o < size ? (uint32_t)prg[o] : 0u; };
+    auto rd16 = [&](uint32_t o) { return rd(o) | (rd(o + 1u) << 8); };
+    auto len_of = [&](uint32_t o) { return instr_len(kOptab.t[rd(o)] & 15u); };
+    auto grp_of = [&](uint32_t o) { return (kOptab.t[rd(o)] >> 8) & 15u; };
+    auto same_page = [](uint32_t a, uint32_t b) { return (a >> 13) == (b >> 13); };
+    // the table holds the generic step's key where an instruction would end on its page's last byte (rlenv_hip.hip);
+    // a jump to itself is found at run time (fx compares with the CPU address)
+    auto generic = [&](uint32_t o) {
+        return (o & 0x1FFFu) + len_of(o) >= 0x2000u || jit_always_generic(0xFFFFFFFFu, rd(o), rd(o + 1u), rd(o + 2u));
+    };
+    auto target_of = [&](uint32_t o) { return o + 2u + (uint32_t)(int32_t)(int8_t)rd(o + 1u); };
+    std::vector<int> order(size, -1);   // discovery rank of each leader
+    std::vector<uint32_t> leaders, work;
+    std::vector<char> seen(size, 0), window(0x2000, 0);
+    auto entry = [&](uint32_t o) {
+        if (o < size && order[o] < 0) {
+            order[o] = (int)leaders.size();
+            leaders.push_back(o);
+            work.push_back(o);
+        }
+    };
+    auto descend = [&]() {
+        while (!work.empty()) {
+            uint32_t o = work.back();
+            work.pop_back();
+            while (o < size && !seen[o]) {
+                seen[o] = 1;
+                const uint32_t grp = grp_of(o), mode = kOptab.t[rd(o)] & 15u, next = o + len_of(o);
+                if (generic(o)) {
+                    if (grp != G_ILL && grp != G_BRK && grp != G_JMP && same_page(o, next)) entry(next);
+                    break;
+                }
+                if (grp == G_BR) {
+                    if (same_page(o, target_of(o))) entry(target_of(o));
+                    entry(next);
+                    break;
+                }
+                if (grp == G_JMP || grp == G_JSR) {
+                    if (mode == M_ABS && rd16(o + 1u) >= 0x8000u) window[rd16(o + 1u) & 0x1FFFu] = 1;
+                    if (grp == G_JSR) entry(next);
+                    break;
+                }
+                if (grp == G_RTS || grp == G_RTI) break;
+                o = next;
+            }
+        }
+    };
+    for (uint32_t v = 0; v < 3; ++v) {
+        const uint32_t vec = rd(size - 6u + 2u * v) | (rd(size - 5u + 2u * v) << 8);
+        for (uint32_t pg = pages >= 2 ? pages - 2 : 0; pg < pages; ++pg)
+            if (((vec >> 13) & 3u) == (pg & 1u ? 3u : 2u) || pages < 2) entry((pg << 13) | (vec & 0x1FFFu));
+    }
+    descend();
+    std::vector<char> seeded(0x2000, 0);
+    for (bool grew = true; grew;) {   // window targets into every page, until no new one appears
+        grew = false;
+        for (uint32_t w = 0; w < 0x2000u; ++w)
+            if (window[w] && !seeded[w]) {
+                seeded[w] = 1;
+                grew = true;
+                for (uint32_t pg = 0; pg < pages; ++pg) entry((pg << 13) | w);
+            }
+        descend();
+    }
+
+    // blocks in discovery order within the cap; a block is a run of one page
+    std::vector<int> id_of(size, -1);
+    struct Block { uint32_t start; std::vector<uint32_t> ins; uint32_t stop; };
+    std::vector<Block> kept;
+    JitProgram p;
+    for (uint32_t start : leaders) {
+        Block b{start, {}, start};
+        uint32_t o = start;
+        for (;;) {
+            if (o >= size || !same_page(o, start) || (o != start && order[o] >= 0) || b.ins.size() == kJitMaxBlock ||
+                generic(o))
+                break;
+            b.ins.push_back(o);
+            const uint32_t grp = grp_of(o);
+            o += len_of(o);
+            if (grp == G_BR || grp == G_JMP || grp == G_JSR || grp == G_RTS || grp == G_RTI) break;
+        }
+        b.stop = o;
+        if (b.ins.empty()) continue;
+        if (p.instructions + b.ins.size() > kJitMaxInstructions) break;
+        id_of[start] = (int)kept.size();
+        p.leader_addr.push_back(start);
+        p.instructions += (uint32_t)b.ins.size();
+        kept.push_back(std::move(b));
+    }
+    auto go = [&](uint32_t from, uint32_t o) {
+        return o < size && same_page(from, o) && id_of[o] >= 0 && o >= from ? "goto JB_" + std::to_string(id_of[o]) + ";"
+                                                                           : std::string("continue;");
+    };
+    auto operand = [&](uint32_t x) {   // the fetch table's decoded operand word (rlenv_hip.hip fetch_entry, banked)
+        const uint32_t mode = kOptab.t[rd(x)] & 15u;
+        if (mode == M_IMM || mode == M_ZP || mode == M_ZPX || mode == M_ZPY || mode == M_IZX || mode == M_IZY)
+            return rd(x + 1u);
+        if (mode == M_REL) return (uint32_t)(int32_t)(int8_t)rd(x + 1u) << 3;
+        return rd16(x + 1u);
+    };
+    char buf[200];
+    for (size_t i = 0; i < kept.size(); ++i) {
+        const Block& b = kept[i];
+        const uint32_t last = b.ins.back(), grp = grp_of(last);
+        std::string end;
+        if (grp == G_BR) {
+            // (taken to another page, the branch leaves the block as needing the generic step)
+            const uint32_t tgt = target_of(last);
+            snprintf(buf, sizeof buf, "if (h.pc == 0x%Xu) ", (tgt << 3));
+            end = same_page(last, tgt) ? buf + go(b.start, tgt) + " " + go(b.start, b.stop) : go(b.start, b.stop);
+        } else if (grp == G_JMP || grp == G_JSR || grp == G_RTS || grp == G_RTI) {
+            end = "continue;";
+        } else {
+            end = go(b.start, b.stop);
+        }
+        snprintf(buf, sizeof buf, "case 0x%Xu: JB_%zu: {   // PRG $%05X, %zu instructions\n", kBlockKey + (uint32_t)i,
+                 i, b.start, b.ins.size());
+        p.cases += buf;
+        std::string mx;
+        for (uint32_t x : b.ins) {
+            snprintf(buf, sizeof buf, "%sjit_maxtake(0x%02Xu)", mx.empty() ? "" : " + ", rd(x));
+            mx += buf;
+        }
+        snprintf(buf, sizeof buf, ") { JIT_ONE(0x%02Xu, 0x%Xu, 0x%Xu) }\n", rd(b.start), b.start << 3,
+                 operand(b.start));
+        p.cases += "    if (v < " + mx + buf;
+        for (uint32_t x : b.ins) {
+            snprintf(buf, sizeof buf, "    JIT_STEP(0x%02Xu, 0x%Xu, 0x%Xu)\n", rd(x), x << 3, operand(x));
+            p.cases += buf;
+        }
+        p.cases += "    " + end + "\n}\n";
+    }
+    return p;
+}
+
 // The source of the kernel a translation is compiled into: the console-frame kernel (emu_kernel.h) of the fixed-PRG
 // boards with the blocks (the header "jit_blocks.inc") in its burst loop, launched as rlenv_hip.hip k_emu_w is.
 // hiprtc has the HIP runtime and the fixed-width integer types built in, the latter in a namespace of its own.
-inline std::string jit_module_source(bool bank) {
+inline std::string jit_module_source(bool bank, bool banked) {
     return std::string(
                "using __hip_internal::uint8_t;\nusing __hip_internal::uint16_t;\nusing __hip_internal::uint32_t;\n"
                "using __hip_internal::uint64_t;\nusing __hip_internal::int8_t;\nusing __hip_internal::int16_t;\n"
@@ -197,8 +344,8 @@ inline std::string jit_module_source(bool bank) {
                "#ifndef offsetof\n#define offsetof(t, m) __builtin_offsetof(t, m)\n#endif\n"
                "#define RLENV_JIT_INC \"jit_blocks.inc\"\n#include \"emu_kernel.h\"\n"
                "extern \"C\" __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(8, 8)))\n"
-               "void k_emu_jit(nd::EmuArgs a) { nd::emu_body<NES_BOARD_NROM, ") +
-           (bank ? "true" : "false") + ">(a); }\n";
+               "void k_emu_jit(nd::EmuArgs a) { nd::emu_body<") +
+           (banked ? "NES_BOARD_MMC3, " : "NES_BOARD_NROM, ") + (bank ? "true" : "false") + ">(a); }\n";
 }
 
 }  // namespace nd

@@ -901,7 +901,7 @@ struct JitJob {
 struct JitSlot {
     std::shared_ptr<JitJob> job;
     const uint32_t* fetchw = nullptr;
-    bool bank = false;
+    bool bank = false, banked = false;   // built for frames drawn from frame banks; for a banked-PRG board
     uint32_t blocks = 0, instructions = 0;
     hipModule_t mod = nullptr;
     hipFunction_t fn = nullptr;
@@ -1550,10 +1550,12 @@ void* rlenv_create(int ngames, const int* game_ids, const uint8_t* const* roms, 
         e.ep_maxlvl = env->mem.zeros<int32_t>(N);
         e.ep_idle = env->mem.zeros<int32_t>(N);
         e.resetting = env->mem.zeros<uint8_t>(N);
-        // translated kernels of fixed-PRG carts: RLENV_JIT=0 (or off) none; sync for every such game; otherwise
-        // for games of at least kJitMinEnvs envs (a smaller one gains less than the compile takes)
+        // translated kernels (jit.h): RLENV_JIT=0 (or off) none; by default the fixed-PRG games of at least
+        // kJitMinEnvs envs (a smaller one gains less than the compile takes); all: every game of that size, banked
+        // boards too (their translations are larger: tens of seconds of compile each); sync: every game
         const char* jv = std::getenv("RLENV_JIT");
-        const int jit_mode = jv && (!strcmp(jv, "0") || !strcmp(jv, "off")) ? 0 : jv && !strcmp(jv, "sync") ? 2 : 1;
+        const int jit_mode = !jv ? 1 : (!strcmp(jv, "0") || !strcmp(jv, "off")) ? 0 : !strcmp(jv, "sync") ? 3
+                             : !strcmp(jv, "all") ? 2 : 1;
         std::vector<std::string> jit_cases((size_t)ngames);
         int offset = 0;
         for (int i = 0; i < ngames; ++i) {
@@ -1610,23 +1612,6 @@ void* rlenv_create(int ngames, const int* game_ids, const uint8_t* const* roms, 
                 for (uint32_t a = 0x8000u; a <= 0xFFFDu; ++a)
                     fetch_entry(&f[2u * a], a, p.prg[a & mask], p.prg[(a + 1u) & mask], p.prg[(a + 2u) & mask],
                                 true);
-                // the translation, and a fetch table with its blocks' keys
-                if (jit_mode == 2 || (jit_mode == 1 && g.n >= kJitMinEnvs)) {
-                    JitProgram jp = jit_translate_fixed(img);
-                    if (!jp.leader_addr.empty()) {
-                        std::vector<uint32_t> fj(f);
-                        for (size_t b = 0; b < jp.leader_addr.size(); ++b)
-                            fj[2u * jp.leader_addr[b]] = kBlockKey + (uint32_t)b;
-                        auto js = std::make_shared<JitSlot>();
-                        uint32_t* fjw = static_cast<uint32_t*>(env->mem.alloc(fj.size() * 4));
-                        env->mem.upload(fjw, fj.data(), fj.size() * 4);
-                        js->fetchw = fjw;
-                        js->blocks = (uint32_t)jp.leader_addr.size();
-                        js->instructions = jp.instructions;
-                        gh.jit = js;
-                        jit_cases[i] = std::move(jp.cases);
-                    }
-                }
             } else {   // by PRG offset; $02 where an instruction would end on the last byte of its 8 KB page
                 f.assign(2u * p.prg.size(), 0u);
                 const auto at = [&](uint32_t k) { return k < p.prg.size() ? (uint32_t)p.prg[k] : 0u; };
@@ -1634,6 +1619,24 @@ void* rlenv_create(int ngames, const int* game_ids, const uint8_t* const* roms, 
                     const uint32_t op = p.prg[o];
                     if ((o & 0x1FFFu) + instr_len(kOptab.t[op] & 15u) >= 0x2000u) f[2u * o] = 0x02u;
                     else fetch_entry(&f[2u * o], o, op, at(o + 1u), at(o + 2u), false);
+                }
+            }
+            // the translation, and a fetch table with its blocks' keys (by CPU address, or by PRG offset)
+            if (jit_mode == 3 || (jit_mode >= 1 && g.n >= kJitMinEnvs && (fixed32 || jit_mode == 2))) {
+                JitProgram jp = fixed32 ? jit_translate_fixed(img) : jit_translate_banked(p.prg);
+                if (!jp.leader_addr.empty()) {
+                    std::vector<uint32_t> fj(f);
+                    for (size_t b = 0; b < jp.leader_addr.size(); ++b)
+                        fj[2u * jp.leader_addr[b]] = kBlockKey + (uint32_t)b;
+                    auto js = std::make_shared<JitSlot>();
+                    uint32_t* fjw = static_cast<uint32_t*>(env->mem.alloc(fj.size() * 4));
+                    env->mem.upload(fjw, fj.data(), fj.size() * 4);
+                    js->fetchw = fjw;
+                    js->banked = !fixed32;
+                    js->blocks = (uint32_t)jp.leader_addr.size();
+                    js->instructions = jp.instructions;
+                    gh.jit = js;
+                    jit_cases[i] = std::move(jp.cases);
                 }
             }
             uint32_t* fetchw = static_cast<uint32_t*>(env->mem.alloc(f.size() * 4));
@@ -1666,7 +1669,7 @@ void* rlenv_create(int ngames, const int* game_ids, const uint8_t* const* roms, 
             // the variant the decision frames use: drawn from frame banks in a one-game env of one round of waves
             gh.jit->bank = env->games.size() == 1 && gh.k.n <= env->one_round;
             bool is_new = false;
-            gh.jit->job = jit_job(std::move(jit_cases[i]), jit_module_source(gh.jit->bank), is_new);
+            gh.jit->job = jit_job(std::move(jit_cases[i]), jit_module_source(gh.jit->bank, gh.jit->banked), is_new);
             if (is_new) fresh.push_back(gh.jit->job);
         }
         {
@@ -1948,13 +1951,10 @@ int rlenv_jit_wait(void* h) {
 int rlenv_jit_translate(const uint8_t* rom, size_t rom_size, int compile, int32_t* out, char* text, size_t text_cap) {
     try {
         const Parsed p = parse_ines(rom, rom_size);
-        if (p.board != NES_BOARD_NROM && p.board != NES_BOARD_CNROM) {
-            g_error = "jit_translate: only fixed-PRG boards (NROM, CNROM) are translated";
-            return 1;
-        }
-        std::vector<uint8_t> img(32768u);   // as the CPU sees it: a 16 KB image mirrored
+        const bool fixed32 = p.board == NES_BOARD_NROM || p.board == NES_BOARD_CNROM;
+        std::vector<uint8_t> img(32768u);   // a fixed image as the CPU sees it: 16 KB mirrored
         for (size_t k = 0; k < img.size(); ++k) img[k] = p.prg[k % p.prg.size()];
-        JitProgram jp = jit_translate_fixed(img);
+        JitProgram jp = fixed32 ? jit_translate_fixed(img) : jit_translate_banked(p.prg);
         out[0] = (int32_t)jp.leader_addr.size();
         out[1] = (int32_t)jp.instructions;
         out[2] = -1;
@@ -1967,7 +1967,7 @@ int rlenv_jit_translate(const uint8_t* rom, size_t rom_size, int compile, int32_
         if (compile) {
             JitJob job;
             job.blocks = std::move(jp.cases);
-            job.source = jit_module_source(false);
+            job.source = jit_module_source(false, !fixed32);
             jit_compile(job);
             out[2] = (int32_t)(job.seconds * 1000.0);
             out[3] = (int32_t)job.code.size();

@@ -159,6 +159,12 @@ __device__ __forceinline__ uint32_t prg_index(const Hot& h, const Mem& m, uint32
     else return sel4((addr >> 13) & 3u, h.prg0, h.prg1, h.prg2, h.prg3) + (addr & 0x1FFFu);
 }
 
+// A PRG RAM byte ($6000-$7FFF, in the console record), as a scalar; the bus's read (nes_dev.h io_read) with the RAM
+// on, which it is on every board but MMC1 (the fast path leaves MMC1's to the generic step).
+__device__ __forceinline__ uint32_t prg_ram_read(const Mem& m, uint32_t a) {
+    return (uint32_t)__builtin_amdgcn_readfirstlane((int)m.rec->prg_ram[a - 0x6000u]);
+}
+
 // Widened PRG word at `idx` (bytes idx, idx+1, idx+2) through a scalar load: the image is read-only for the
 // whole kernel.
 __device__ __forceinline__ uint32_t prg_wide(const Mem& m, uint32_t idx) {
@@ -211,28 +217,40 @@ __device__ __forceinline__ uint32_t fx(Hot& h, const Mem& m, Con& cs, uint32_t p
             if constexpr (pen) cyc += ((b2 ^ ea) & 0xFF00u) ? 1u : 0u;
         }
         // Memory class, decided before any side effect (every check below comes before the first state change):
-        // RAM, PRG reads, the controller port and PPU status reads run here; any other I/O register, a
-        // read-modify-write outside RAM and any write at $8000+ (a mapper) go to the generic step. Written as
-        // chains of single compares: boolean combinations of uniform conditions become lane-mask arithmetic.
+        // RAM, PRG RAM ($6000-$7FFF; on MMC1, whose register can disable it, the generic step), PRG reads, the
+        // controller port and PPU status reads run here; any other I/O register, a read-modify-write elsewhere and
+        // any write at $8000+ (a mapper) go to the generic step. Written as chains of single compares: boolean
+        // combinations of uniform conditions become lane-mask arithmetic.
         if constexpr (!zpage && rd && wr) {
-            if (ea >= 0x2000u) return kGeneric;
+            if (ea >= 0x2000u) {
+                if (ea < 0x6000u) return kGeneric;
+                if (ea >= 0x8000u) return kGeneric;
+                if (m.cart.board == NES_BOARD_MMC1) return kGeneric;
+            }
         }
         if constexpr (!zpage && wr && !rd) {
             if (ea >= 0x2000u) {
-                if (ea != 0x4016u) return kGeneric;
+                if (ea != 0x4016u) {
+                    if (ea < 0x6000u) return kGeneric;
+                    if (ea >= 0x8000u) return kGeneric;
+                    if (m.cart.board == NES_BOARD_MMC1) return kGeneric;
+                }
             }
         }
         uint32_t opd = lo;
         if constexpr (rd) {
             if constexpr (mode == M_ZP) {
                 opd = rd8(m, ea);   // the fetch table's operand byte: < $100
-            } else if constexpr (zpage || wr) {
+            } else if constexpr (zpage) {
                 opd = rd8(m, ea & 0x7FFu);
+            } else if constexpr (wr) {
+                opd = ea < 0x2000u ? rd8(m, ea & 0x7FFu) : prg_ram_read(m, ea);
             } else {
                 if (ea < 0x2000u) opd = rd8(m, ea & 0x7FFu);
                 else if (ea >= 0x8000u) opd = prg_wide(m, prg_index<B>(h, m, ea)) & 0xFFu;
                 else if (ea == 0x4016u) opd = port_read(cs);
                 else if ((ea & 0xE007u) == 0x2002u) opd = status_read(cs);
+                else if (ea >= 0x6000u && m.cart.board != NES_BOARD_MMC1) opd = prg_ram_read(m, ea);
                 else return kGeneric;
             }
         }
@@ -341,8 +359,9 @@ __device__ __forceinline__ uint32_t fx(Hot& h, const Mem& m, Con& cs, uint32_t p
         }
         if constexpr (wr) {
             if constexpr (mode == M_ZP) m.ram[ea] = (uint8_t)res;
-            else if constexpr (zpage || rd) m.ram[ea & 0x7FFu] = (uint8_t)res;
+            else if constexpr (zpage) m.ram[ea & 0x7FFu] = (uint8_t)res;
             else if (ea < 0x2000u) m.ram[ea & 0x7FFu] = (uint8_t)res;
+            else if (ea >= 0x6000u) m.rec->prg_ram[ea - 0x6000u] = (uint8_t)res;   // (a read-modify-write: here)
             else port_write(cs, res);
         }
         h.pc = npc;
@@ -526,13 +545,11 @@ __device__ __forceinline__ uint32_t run_until_wave(Con& cs, const Mem& m, const 
 #ifdef RLENV_JIT_INC
                 ConstU32* e = (ConstU32*)((ConstU8*)m.cart.fetchw + h.pc);
                 const uint32_t fop = e[0], fbase = e[1];
-                if constexpr (B == NES_BOARD_NROM) {   // a translated block starts here (jit.h)
-                    if (fop >= kBlockKey) {
-                        uint32_t t;
-                        switch (fop) {
+                if (fop >= kBlockKey) {   // a translated block starts here (jit.h)
+                    uint32_t t;
+                    switch (fop) {
 #include RLENV_JIT_INC
-                            default: __builtin_unreachable();
-                        }
+                        default: __builtin_unreachable();
                     }
                 }
                 take = fast_step<B>(h, m, cs, fop, fbase);

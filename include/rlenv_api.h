@@ -104,21 +104,22 @@ int rlenv_read_consoles(void* h, int gi, int first, int count, uint8_t* host_out
 void rlenv_set_kernel_timing(void* h, int on);
 int rlenv_kernel_times(void* h, double* ms, int64_t* count, int n);
 /* Translated kernels (no reference counterpart: an acceleration inside this library). rlenv_create translates the
- * 6502 code of a fixed-PRG cart (NROM, CNROM) into blocks of the interpreter's per-opcode handlers with constant
- * operands and compiles them at run time (hiprtc; the games' compiles in parallel, each translation once per
- * process) into a copy of the console-frame kernel that the game's decision frames then use; a console's results
- * are the same on either kernel. Which games: those of at least 1024 envs; RLENV_JIT=sync: every fixed-PRG game;
- * RLENV_JIT=0 (or off): none. RLENV_JIT_CACHE=<directory>: compiled code objects are also kept there, for later
- * processes.
+ * cart's 6502 code into blocks of the interpreter's per-opcode handlers with constant operands (by CPU address on
+ * NROM and CNROM, by PRG offset on the banked boards) and compiles them at run time (hiprtc; the games' compiles in
+ * parallel, each translation once per process) into a copy of the console-frame kernel that the game's decision
+ * frames then use; a console's results are the same on either kernel. Which games: by default the fixed-PRG games
+ * of at least 1024 envs; RLENV_JIT=all: every game of at least 1024 envs (a banked cart's translation is larger,
+ * tens of seconds of compile); RLENV_JIT=sync: every game; RLENV_JIT=0 (or off): none. Compiles of one process run
+ * one at a time. RLENV_JIT_CACHE=<directory>: compiled code objects are also kept there, for later processes.
  *  jit_wait: 0 when every translated game runs translated decision frames (those drawn the way its translation was
  *    built for: from frame banks in a one-game env of one round of waves, from the records otherwise); non-zero,
  *    with the compile error in rlenv_error, when a compile or load failed (that game keeps the library's own
  *    kernel).
  *  jit_status: out[5] = state (0 no translation, 1 compiling, 2 loaded, 3 failed), blocks, instructions, compile
  *    milliseconds (-1 while compiling), 1 if built for frames drawn from frame banks.
- *  jit_translate: the translation of an iNES image (fixed-PRG boards only; needs no GPU): out[4] = blocks,
- *    instructions, compile milliseconds and code-object bytes (-1 and 0 without compile); text (if not null): the
- *    generated blocks, NUL-terminated, cut at text_cap. Non-zero for another board or a failed compile. */
+ *  jit_translate: the translation of an iNES image (needs no GPU): out[4] = blocks, instructions, compile
+ *    milliseconds and code-object bytes (-1 and 0 without compile); text (if not null): the generated blocks,
+ *    NUL-terminated, cut at text_cap. Non-zero for an image that does not parse or a failed compile. */
 int rlenv_jit_wait(void* h);
 int rlenv_jit_status(void* h, int gi, int32_t* out);
 int rlenv_jit_translate(const uint8_t* rom, size_t rom_size, int compile, int32_t* out, char* text, size_t text_cap);

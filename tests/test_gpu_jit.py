@@ -149,3 +149,23 @@ def test_translated_equals_interpreter_at_full_size():
         for k in ('obs', 'emph', 'reward', 'done', 'ram_hash', 'pads'):
             assert torch.equal(getattr(fast, k), getattr(slow, k)), (t, k)
     assert np.array_equal(fast.consoles(0), slow.consoles(0))
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize('board', ['seam', 'mmc3', 'mmc1', 'uxrom', 'mmc2'])
+def test_translated_banked_boards(board):
+    """Banked PRG (blocks by PRG offset, a run of one 8 KB page each; jumps, calls and returns mapped at run time):
+    the seam cart (code running off windows, branches across them, JMP ($04FF), code in RAM), MMC3 (scanline IRQ,
+    sprite-0 split, PRG RAM), MMC1 from power-on (serial writes, CHR RAM), UxROM with bus conflicts, MMC2 latches.
+    Smaller seed-generated carts than the benchmark's keep the compiles short."""
+    carts = {'seam': lambda: synth.seam_cart(1, blocks=4, sub_blocks=3),
+             'mmc3': lambda: synth.mmc3_cart(3, blocks=6, sub_blocks=4),
+             'mmc1': lambda: synth.mmc1_cart(3, blocks=6, sub_blocks=4),
+             'uxrom': lambda: synth.uxrom_cart(2, blocks=6, sub_blocks=4, conflicts=True),
+             'mmc2': lambda: synth.mmc2_cart(1, blocks=6, sub_blocks=4)}
+    print(f'case: translated {board} (small seed-generated cart), 16 consoles, raw pads, sticky, Geometric(1/8) '
+          'ends, 16 decisions', flush=True)
+    cpu, gpu, st = translated_pair(16, carts[board](), seed=50, sticky=True, idle_max=1, dropout=True, pad_mode=True,
+                                   end_prob=1 / 8)
+    print(f'  {st["blocks"]} blocks, {st["instructions"]} instructions, compiled in {st["compile_ms"]} ms', flush=True)
+    run(cpu, gpu, 16, 51, True)
