@@ -162,8 +162,8 @@ struct RenderSink {
     // plane 0 in the low byte: one 16-bit load with CHR ROM, two byte loads with CHR RAM.
     __device__ uint32_t pattern(uint32_t lo, uint32_t hi, uint32_t pa) {
         if (!chr_pairs) return chr_pk(chr_rom, chr_ram, lo, hi, pa) | (chr_pk(chr_rom, chr_ram, lo, hi, pa + 8u) << 8);
-        const uint32_t slot = (pa >> 10) & 7u;
-        const uint32_t page = ((slot & 4u ? hi : lo) >> ((slot & 3u) * 8u)) & 0xFFu;
+        // the 1 KB slot's page: byte (pa >> 10) & 7 of hi:lo, one byte permute
+        const uint32_t page = __builtin_amdgcn_perm(hi, lo, (pa >> 10) & 7u) & 0xFFu;
         return chr_pairs[page * 512u + ((pa & 0x3F0u) >> 1) + (pa & 7u)];
     }
     // Slot j's tile (nametable tile and attribute, both pattern bytes) fetched at v into F[j + 2].
@@ -265,12 +265,13 @@ struct RenderSink {
         const uint32_t rank = __builtin_amdgcn_mbcnt_hi((uint32_t)(sel >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)sel, 0u));
         const uint32_t target = fetched == drawn ? drawn ^ 1u : fetched;
         if (row < h && rank < 8u) {
-            const uint32_t tile = (e >> 8) & 0xFFu, attr = (e >> 16) & 0xFFu;
+            const uint32_t tile = (e >> 8) & 0xFFu;
             const uint32_t table8 = (ctrl & 0x08u) && !(ctrl & 0x20u) ? 0x1000u : 0u;
-            uint32_t pa = h == 16u ? ((tile & 1u) << 12) + ((tile & 0xFEu) << 4) : (tile << 4) + table8;
-            if (attr & 0x80u) pa += 7u - row + ((ctrl & 0x20u) >> 1) - (row & 8u);
-            else pa += row + (row & 8u);
-            pa &= 0x1FFFu;
+            const uint32_t base = h == 16u ? ((tile & 1u) << 12) + ((tile & 0xFEu) << 4) : (tile << 4) + table8;
+            // the row's offset, row + (row & 8), or with vertical flip (attribute bit 7) 7 (+ 16 for 8x16) minus it:
+            // flip = all ones negates it (x ^ flip) - flip and adds the 7 (+ 16)
+            const uint32_t r2 = row + (row & 8u), flip = (uint32_t)((int32_t)(e << 8) >> 31);
+            const uint32_t pa = (base + (flip & (7u + ((ctrl & 0x20u) >> 1))) + ((r2 ^ flip) - flip)) & 0x1FFFu;
             const uint32_t pk = mmc2 ? L->pages[34 + rank] : 0u;
             const uint32_t lo = mmc2 ? pk : s.chr_lo, hi = mmc2 ? pk : s.chr_hi;
             L->spr[target][rank] = pattern(lo, hi, pa) | (e & 0xFFFF0000u);
@@ -337,10 +338,31 @@ struct RenderSink {
         if (lane >= 2 && lane < 62) reinterpret_cast<uint32_t*>(obs + y * RLE_OBS_W)[lane - 2] = w;
         if (lane == 0) emph[y] = (uint8_t)((s.mask >> 5) & 7u);
     }
-    // A line with no write from its lead-in to its end, no sprite-0 check and no MMC2 latches: one run of the 34 slots
-    // with the state as it is, FetchSpriteData, Fixit1/Fixit2 and RefreshSprites in closed form. The lanes fetch the
-    // line's tiles and the next line's sprites and expand this line's sprites together, sync once, and each composes
-    // its 4 pixels in registers (pixel x from slot x / 8 + 2, i.e. the fetches F[x / 8 + 2] and F[x / 8 + 3]).
+    // The line's sprite-0 check (replay_dev.h rs_check at the line's end, where the whole line is drawn): the first
+    // pixel in [sphitx, min(sphitx + 8, 255)) where sprite 0's pixel is set and the background pixel is not
+    // transparent (bit 6, the backdrop mark), over the background pixels w the lanes hold (4 each).
+    __device__ void check_hit(Rs& s, uint32_t w) {
+        const int32_t x0 = s.sphitx, end = x0 + 8 < 255 ? x0 + 8 : 255;
+        uint32_t first = 4u;
+        for (uint32_t q = 0; q < 4u; ++q) {
+            const int32_t x = 4 * lane + (int32_t)q;
+            const bool in = x >= x0 && x < end;
+            const uint32_t bit = in ? (s.sphit_bits >> (uint32_t)(7 - (x - x0))) & 1u : 0u;
+            if (first == 4u && bit && !((w >> (8u * q)) & 0x40u)) first = q;
+        }
+        const uint64_t b = __ballot(first < 4u);
+        if (b) {
+            const int ln = (int)__builtin_ctzll(b);
+            s.hit = 1;
+            s.hit_x = 4 * ln + __builtin_amdgcn_readlane((int)first, ln);
+            s.sphitx = kNoCheck;
+        }
+    }
+    // A line with no write from its lead-in to its end and no MMC2 latches: one run of the 34 slots with the state as
+    // it is, the sprite-0 check (if one is due) against the drawn line, FetchSpriteData, Fixit1/Fixit2 and
+    // RefreshSprites in closed form. The lanes fetch the line's tiles and the next line's sprites and expand this
+    // line's sprites together, sync once, and each composes its 4 pixels in registers (pixel x from slot x / 8 + 2,
+    // i.e. the fetches F[x / 8 + 2] and F[x / 8 + 3]).
     __device__ void fast_line(Rs& s, int32_t l, uint8_t* obs, uint8_t* emph) {
         const bool rend = rs_rendering(s);
         uint64_t sel = 0;
@@ -357,6 +379,7 @@ struct RenderSink {
             const uint32_t k = (uint32_t)lane / 2u + 2u;
             w = shift4(L->f[k], L->f[k + 1u], ((uint32_t)lane & 1u) * 4u, s.fx, t);
         }
+        if (s.sphitx != kNoCheck) check_hit(s, w);
         compose(s, l, w, obs, emph);
         // the end of the line: Fixit1 and Fixit2 (v from t horizontally), the next line's sprites, RefreshSprites
         s.sphitx = kNoCheck;
@@ -415,7 +438,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(8, 8))) void
     uint8_t* obs = a.o.obs + ((size_t)ge * RLE_FRAMES + a.f) * RLE_OBS_PIXELS;
     uint8_t* emph = a.o.emph + ((size_t)ge * RLE_FRAMES + a.f) * RLE_OBS_H;
     for (int32_t l = 0; l < 232; ++l) {
-        if (!mmc2 && s.next >= (l + 1) * 341 - NES_LINE_LEAD && s.sphitx == kNoCheck) {
+        if (!mmc2 && s.next >= (l + 1) * 341 - NES_LINE_LEAD) {
             sink.fast_line(s, l, obs, emph);
             continue;
         }
