@@ -80,7 +80,7 @@ struct RenderArgs {
 // Sprite lines are fetched with one ballot over the 64 OAM entries (lane = sprite) into one of two buffers; the one
 // RefreshSprites latched is expanded at the start of the line it is drawn on (lane 8k + p = pixel p of sprite k) into
 // a sprite line with one LDS max per pixel, which picks the lowest-numbered opaque sprite.
-// A line with no write and no sprite-0 check (most of them) takes fast_line: one fetch phase, one sync, and each lane
+// A run of lines with no write (most of them) takes fast_run: per line one fetch phase, one sync, and each lane
 // composes its 4 pixels in registers.
 struct RenderLds {
     uint8_t nt[NES_NT_BYTES];
@@ -90,7 +90,8 @@ struct RenderLds {
     uint32_t f[36];           // fetches: lo | hi << 8 | attribute << 16; 0-1 carried, 2 + j slot j
     uint32_t spr[2][8];       // sprite lines: lo | hi << 8 | attr << 16 | x << 24
     uint32_t pages[34 + 8];   // MMC2: the pages of each slot's fetch, then of each sprite's
-    alignas(4) uint8_t pal[32];
+    uint4 tab[2];             // the background palette table (bg_table), the latched sprite palette (latch_sprites)
+    alignas(16) uint8_t pal[32];
 };
 
 typedef __attribute__((address_space(4))) const uint32_t KU32;
@@ -104,9 +105,7 @@ struct RenderSink {
     bool mmc2;
     uint32_t ha, hb;          // F indices of the last two fetches
     uint32_t fetched, drawn, drawn_n;
-    // the background palette table (bg_table) and the latched sprite palette (latch_sprites), wave-uniform, rebuilt
-    // only after a palette write
-    uint32_t bgt[4], spt[4];
+    // L->tab[0] and L->tab[1] are rebuilt only after a palette write
     bool bg_stale, sp_stale;
 
     __device__ uint32_t ev(uint32_t i) { return ((KU32*)(log + NES_LOG_HDR_WORDS))[i]; }
@@ -159,12 +158,19 @@ struct RenderSink {
         __syncthreads();
     }
     // The two plane bytes of pattern address pa (a row of plane 0; pa + 8 is plane 1) through the packed pages,
-    // plane 0 in the low byte: one 16-bit load with CHR ROM, two byte loads with CHR RAM.
+    // plane 0 in the low byte: one 16-bit load with CHR ROM (kPairs), two byte loads with CHR RAM.
+    template <bool kPairs>
+    __device__ uint32_t pattern_of(uint32_t lo, uint32_t hi, uint32_t pa) {
+        if constexpr (!kPairs) {
+            return chr_pk(chr_rom, chr_ram, lo, hi, pa) | (chr_pk(chr_rom, chr_ram, lo, hi, pa + 8u) << 8);
+        } else {
+            // the 1 KB slot's page: byte (pa >> 10) & 7 of hi:lo, one byte permute
+            const uint32_t page = __builtin_amdgcn_perm(hi, lo, (pa >> 10) & 7u) & 0xFFu;
+            return chr_pairs[page * 512u + ((pa & 0x3F0u) >> 1) + (pa & 7u)];
+        }
+    }
     __device__ uint32_t pattern(uint32_t lo, uint32_t hi, uint32_t pa) {
-        if (!chr_pairs) return chr_pk(chr_rom, chr_ram, lo, hi, pa) | (chr_pk(chr_rom, chr_ram, lo, hi, pa + 8u) << 8);
-        // the 1 KB slot's page: byte (pa >> 10) & 7 of hi:lo, one byte permute
-        const uint32_t page = __builtin_amdgcn_perm(hi, lo, (pa >> 10) & 7u) & 0xFFu;
-        return chr_pairs[page * 512u + ((pa & 0x3F0u) >> 1) + (pa & 7u)];
+        return chr_pairs ? pattern_of<true>(lo, hi, pa) : pattern_of<false>(lo, hi, pa);
     }
     // Slot j's tile (nametable tile and attribute, both pattern bytes) fetched at v into F[j + 2].
     __device__ void fetch_slot(const Rs& s, uint32_t v, uint32_t j, uint32_t lo, uint32_t hi) {
@@ -177,13 +183,20 @@ struct RenderSink {
     }
     // The background palette as 16 bytes in four words, entry 4a + v: palette a's colour v, and for v = 0 the
     // backdrop with bit 6 set (the transparency mark the sprite priority test reads). Wave-uniform.
+    // (The tables are written by every active lane, the same 16 bytes: callers may be in lane-divergent code.)
     __device__ void bg_table(uint32_t t[4]) {
         if (bg_stale) {
+            const uint4 p = reinterpret_cast<const uint4*>(L->pal)[0];
             const uint32_t b = back();
-            for (int i = 0; i < 4; ++i) bgt[i] = (uni(reinterpret_cast<const uint32_t*>(L->pal)[i]) & 0x3F3F3F00u) | b;
+            L->tab[0] = make_uint4((uni(p.x) & 0x3F3F3F00u) | b, (uni(p.y) & 0x3F3F3F00u) | b,
+                                   (uni(p.z) & 0x3F3F3F00u) | b, (uni(p.w) & 0x3F3F3F00u) | b);
             bg_stale = false;
         }
-        for (int i = 0; i < 4; ++i) t[i] = bgt[i];
+        const uint4 q = L->tab[0];
+        t[0] = uni(q.x);
+        t[1] = uni(q.y);
+        t[2] = uni(q.z);
+        t[3] = uni(q.w);
     }
     // 4 background pixels, leftmost in the low byte: kk0..kk0 + 3 of the 8 a slot shifts out from fetches p2 (older),
     // p1 with fine x fx; pixel q is bit 15 - fx - kk0 - q of the two 16-bit plane pairs, with p2's attribute while
@@ -297,20 +310,31 @@ struct RenderSink {
         __syncthreads();
         sprite_fetch_done(s, sel);
     }
+    __device__ void latch_table() {
+        const uint4 p = reinterpret_cast<const uint4*>(L->pal)[1];
+        L->tab[1] = make_uint4(uni(p.x) & 0x3F3F3F3Fu, uni(p.y) & 0x3F3F3F3Fu, uni(p.z) & 0x3F3F3F3Fu,
+                               uni(p.w) & 0x3F3F3F3Fu);
+        sp_stale = false;
+    }
     // RefreshSprites: the fetched line is the one drawn next, with the sprite palette of the moment (read by the next
     // line's compose, after its syncs).
     __device__ void latch_sprites(const Rs& s) {
         drawn = fetched;
         drawn_n = s.f_n;
-        if (sp_stale) {
-            for (int i = 0; i < 4; ++i) spt[i] = uni(reinterpret_cast<const uint32_t*>(L->pal)[4 + i]) & 0x3F3F3F3Fu;
-            sp_stale = false;
-        }
+        if (sp_stale) latch_table();
     }
     // CopySprites (with sprites on at the line's end and a latched line waiting) over the background pixels w of
     // this lane, greyscale while rendering, and the observation row (rl/csrc/nes_machine.cuh:133-155: lines 8..231,
     // x 8..247) with the line's emphasis (patch:1637-1661). Clears the lane's part of the sprite line.
-    __device__ void compose(Rs& s, int32_t l, uint32_t w, uint8_t* obs, uint8_t* emph) {
+    __device__ void sprite_table(uint32_t t[4]) {
+        const uint4 q = L->tab[1];
+        t[0] = uni(q.x);
+        t[1] = uni(q.y);
+        t[2] = uni(q.z);
+        t[3] = uni(q.w);
+    }
+    // spt: the latched sprite palette (sprite_table)
+    __device__ void compose(Rs& s, int32_t l, uint32_t w, uint8_t* obs, uint8_t* emph, const uint32_t spt[4]) {
         const bool expanded = s.spork != 0, sprites = (s.mask & 0x10u) && expanded;
         if (sprites) s.spork = 0;
         const uint32_t keep = (s.mask & 0x01u) && rs_rendering(s) ? 0x30u : 0x3Fu;
@@ -358,50 +382,103 @@ struct RenderSink {
             s.sphitx = kNoCheck;
         }
     }
-    // A line with no write from its lead-in to its end and no MMC2 latches: one run of the 34 slots with the state as
-    // it is, the sprite-0 check (if one is due) against the drawn line, FetchSpriteData, Fixit1/Fixit2 and
-    // RefreshSprites in closed form. The lanes fetch the line's tiles and the next line's sprites and expand this
-    // line's sprites together, sync once, and each composes its 4 pixels in registers (pixel x from slot x / 8 + 2,
-    // i.e. the fetches F[x / 8 + 2] and F[x / 8 + 3]).
-    __device__ void fast_line(Rs& s, int32_t l, uint8_t* obs, uint8_t* emph) {
-        const bool rend = rs_rendering(s);
-        uint64_t sel = 0;
-        if (rend) {
-            if (lane < 34) fetch_slot(s, v_steps(s.v, (uint32_t)lane), (uint32_t)lane, s.chr_lo, s.chr_hi);
-            sel = sprite_fetch_lanes(s, l);
-        }
-        expand_sprites(s);
-        __syncthreads();
+    // Lines l .. stop - 1, a run with no write from the first one's lead-in to the last one's end (and no MMC2
+    // latches): each line is one run of the 34 slots with the state as it is, the sprite-0 check (if one is due)
+    // against the drawn line, FetchSpriteData, Fixit1/Fixit2 and RefreshSprites in closed form. ctrl, mask, the
+    // palette, the CHR pages and the nametable map hold for the whole run, so what follows from them is set up once:
+    //   - background: lane j fetches tile slot (j + 1) / 2, so lanes 2i and 2i + 1 hold slots i and i + 1 between
+    //     them, the two fetches that lane 2i's pixels 8i..8i+3 and lane 2i + 1's 8i+4..8i+7 shift out (pixel x from
+    //     slots x / 8 and x / 8 + 1), and one swap within the lane pair (DPP) gives each lane both. The tile and
+    //     attribute are read again only when v's row of tiles changes (every 8 lines), the pattern row every line;
+    //   - sprites: lane i keeps OAM entry i and its pattern row base; FetchSpriteData is one ballot over the lanes;
+    //   - the lanes expand this line's sprites, sync once, and each composes its 4 pixels in registers.
+    // With rendering off the lines are the backdrop: nothing is fetched, v stays, no sprite is drawn and no sprite-0
+    // check can hit (the backdrop is transparent).
+    template <bool kPairs>
+    __device__ void fast_run(Rs& s, int32_t l, int32_t stop, uint8_t* obs, uint8_t* emph) {
         uint32_t t[4];
         bg_table(t);
-        uint32_t w = (t[0] & 0xFFu) * 0x01010101u;   // the backdrop
-        if (rend && (s.mask & 0x08u) && (lane >= 2 || (s.mask & 0x02u))) {
-            const uint32_t k = (uint32_t)lane / 2u + 2u;
-            w = shift4(L->f[k], L->f[k + 1u], ((uint32_t)lane & 1u) * 4u, s.fx, t);
+        const uint32_t back4 = (t[0] & 0xFFu) * 0x01010101u;
+        const uint32_t mask = s.mask;
+        if (!rs_rendering(s)) {
+            const uint32_t row4 = back4 & 0x3F3F3F3Fu, em = (mask >> 5) & 7u;
+            for (int32_t y = (l > 8 ? l : 8) - 8; y < stop - 8; ++y) {
+                if (lane >= 2 && lane < 62) reinterpret_cast<uint32_t*>(obs + y * RLE_OBS_W)[lane - 2] = row4;
+                if (lane == 0) emph[y] = (uint8_t)em;
+            }
+            s.sphitx = kNoCheck;
+            return;
         }
-        if (s.sphitx != kNoCheck) check_hit(s, w);
-        compose(s, l, w, obs, emph);
-        // the end of the line: Fixit1 and Fixit2 (v from t horizontally), the next line's sprites, RefreshSprites
-        s.sphitx = kNoCheck;
-        if (rend) {
-            s.v = (y_step(s.v) & 0x7BE0u) | (s.t & 0x041Fu);
-            ha = 34u;
-            hb = 35u;
+        const uint32_t ctrl = s.ctrl, h = (ctrl & 0x20u) ? 16u : 8u, ptab = (ctrl & 0x10u) << 8;
+        const bool bg_on = (mask & 0x08u) && (lane >= 2 || (mask & 0x02u)), spr_on = (mask & 0x10u) != 0;
+        // this lane's OAM entry: its pattern row is sb + row (+ 8 for the lower tile of 8x16), vertical flip negating
+        // the row (flip = all ones: (r ^ flip) - flip, and sb adds the 7 or 23)
+        const uint32_t e = reinterpret_cast<const uint32_t*>(L->oam)[lane];
+        const uint32_t st = (e >> 8) & 0xFFu, table8 = (ctrl & 0x08u) && !(ctrl & 0x20u) ? 0x1000u : 0u;
+        const uint32_t flip = (uint32_t)((int32_t)(e << 8) >> 31);
+        const uint32_t sb = (h == 16u ? ((st & 1u) << 12) + ((st & 0xFEu) << 4) : (st << 4) + table8) +
+                            (flip & (7u + ((ctrl & 0x20u) >> 1)));
+        const uint32_t slot = ((uint32_t)lane + 1u) >> 1, kk0 = ((uint32_t)lane & 1u) * 4u;
+        // the latched sprite palette. With sprites on, the line before the run ended with RefreshSprites: it latched
+        // the palette as it is now, or latched nothing (no sprite is drawn before a latch in the run, which takes this
+        // same palette), so the table can be brought up to date here. With sprites off nothing is latched or drawn in
+        // the run, and the table keeps the palette of the last latch for the lines after it.
+        if (spr_on && sp_stale) latch_table();
+        uint32_t spt[4];
+        sprite_table(spt);
+        uint32_t key = 0xFFFFFFFFu, tb = 0, tsel = 0, vl = s.v;
+        for (; l < stop; ++l) {
+            vl = s.v;
+            if ((vl & 0x0FFFu) != key) {   // a new row of tiles (or the run's first line)
+                key = vl & 0x0FFFu;
+                const uint32_t vs = v_steps(vl, slot);
+                const uint32_t ntb = 0x2000u | (vs & 0x0C00u), col = vs & 31u;
+                const uint32_t tile = L->nt[nt_slot(s.nt_map, ntb | (vs & 0x3FFu))];
+                const uint32_t at = L->nt[nt_slot(s.nt_map, ntb | 0x3C0u | (col >> 2) | ((vs & 0x380u) >> 4))];
+                tsel = ((at >> ((col & 2u) | ((vs & 0x40u) >> 4))) & 3u) << 16;
+                tb = tile * 16u + ptab;
+            }
+            const uint32_t mine = pattern_of<kPairs>(s.chr_lo, s.chr_hi, tb + ((vl >> 12) & 7u)) | tsel;
+            const uint32_t other = (uint32_t)__builtin_amdgcn_mov_dpp((int)mine, 0xB1, 0xF, 0xF, false);   // lane ^ 1
+            // FetchSpriteData for line l + 1 into the buffer not latched
+            const uint32_t row = (uint32_t)(l - (int32_t)(e & 0xFFu));
+            const uint64_t sel = __ballot(row < h);
+            const uint32_t rank = __builtin_amdgcn_mbcnt_hi((uint32_t)(sel >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)sel, 0u));
+            const uint32_t target = fetched == drawn ? drawn ^ 1u : fetched;
+            if (row < h && rank < 8u) {
+                const uint32_t r2 = row + (row & 8u);
+                L->spr[target][rank] = pattern_of<kPairs>(s.chr_lo, s.chr_hi, (sb + ((r2 ^ flip) - flip)) & 0x1FFFu) |
+                                       (e & 0xFFFF0000u);
+            }
+            fetched = target;
+            expand_sprites(s);
+            __syncthreads();
+            uint32_t w = back4;
+            if (bg_on) w = shift4(lane & 1 ? other : mine, lane & 1 ? mine : other, kk0, s.fx, t);
+            if (s.sphitx != kNoCheck) check_hit(s, w);
+            compose(s, l, w, obs, emph, spt);
+            // the end of the line: Fixit1 and Fixit2 (v from t horizontally), the next line's sprites, RefreshSprites
+            s.sphitx = kNoCheck;
+            s.v = (y_step(vl) & 0x7BE0u) | (s.t & 0x041Fu);
             sprite_fetch_done(s, sel);
-        }
-        if (s.mask & 0x10u) {
-            s.spork = 0;
-            if (s.f_n != 0) {
-                latch_sprites(s);
-                if (s.f_blurp && !s.hit && s.f_bits) {
-                    uint32_t b = s.f_bits;
-                    if (s.f_attr & 0x40u) b = __builtin_bitreverse32(b) >> 24;
-                    s.sphitx = (int32_t)s.f_x;
-                    s.sphit_bits = b;
+            if (spr_on) {
+                s.spork = 0;
+                if (s.f_n != 0) {
+                    latch_sprites(s);
+                    if (s.f_blurp && !s.hit && s.f_bits) {
+                        uint32_t b = s.f_bits;
+                        if (s.f_attr & 0x40u) b = __builtin_bitreverse32(b) >> 24;
+                        s.sphitx = (int32_t)s.f_x;
+                        s.sphit_bits = b;
+                    }
+                    s.spork = 1;
                 }
-                s.spork = 1;
             }
         }
+        // the last line's slots 32 and 33, where a line with writes after the run starts from (F[34], F[35])
+        if (lane < 2) fetch_slot(s, v_steps(vl, 32u + (uint32_t)lane), 32u + (uint32_t)lane, s.chr_lo, s.chr_hi);
+        ha = 34u;
+        hb = 35u;
     }
 };
 
@@ -431,7 +508,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(8, 8))) void
     reinterpret_cast<uint4*>(L.sp)[lane] = make_uint4(0u, 0u, 0u, 0u);
     __syncthreads();
     const bool mmc2 = a.g.cart.board == NES_BOARD_MMC2;
-    RenderSink sink{&L, log, a.g.cart.chr, chr_ram, a.g.cart.chr_pairs, lane, mmc2, 0u, 1u, 0u, 0u, 0u, {}, {}, true, true};
+    RenderSink sink{&L, log, a.g.cart.chr, chr_ram, a.g.cart.chr_pairs, lane, mmc2, 0u, 1u, 0u, 0u, 0u, true, true};
     Rs s;
     rs_load(s, sink, log, uni(log_n), mmc2 ? a.g.cart.chr_pages1 : 0u);
     rs_begin_frame(s, sink);
@@ -439,11 +516,17 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(8, 8))) void
     uint8_t* emph = a.o.emph + ((size_t)ge * RLE_FRAMES + a.f) * RLE_OBS_H;
     for (int32_t l = 0; l < 232; ++l) {
         if (!mmc2 && s.next >= (l + 1) * 341 - NES_LINE_LEAD) {
-            sink.fast_line(s, l, obs, emph);
+            // lines l .. stop - 1 end before the next write's line (its lead-in included)
+            const int32_t stop = s.next >= 232 * 341 - NES_LINE_LEAD ? 232 : (s.next + NES_LINE_LEAD) / 341;
+            if (sink.chr_pairs) sink.fast_run<true>(s, l, stop, obs, emph);
+            else sink.fast_run<false>(s, l, stop, obs, emph);
+            l = stop - 1;
             continue;
         }
         rs_line(s, sink, l, true);
-        sink.compose(s, l, L.px[lane], obs, emph);
+        uint32_t spt[4];
+        sink.sprite_table(spt);
+        sink.compose(s, l, L.px[lane], obs, emph, spt);
         rs_end_of_line(s, sink, l, true);
     }
 }
