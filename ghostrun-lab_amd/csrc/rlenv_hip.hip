@@ -333,8 +333,8 @@ struct RenderSink {
         t[2] = uni(q.z);
         t[3] = uni(q.w);
     }
-    // spt: the latched sprite palette (sprite_table)
-    __device__ void compose(Rs& s, int32_t l, uint32_t w, uint8_t* obs, uint8_t* emph, const uint32_t spt[4]) {
+    // spt: the latched sprite palette (sprite_table). The line's emphasis is the caller's (the mask at this point).
+    __device__ void compose(Rs& s, int32_t l, uint32_t w, uint8_t* obs, const uint32_t spt[4]) {
         const bool expanded = s.spork != 0, sprites = (s.mask & 0x10u) && expanded;
         if (sprites) s.spork = 0;
         const uint32_t keep = (s.mask & 0x01u) && rs_rendering(s) ? 0x30u : 0x3Fu;
@@ -360,7 +360,10 @@ struct RenderSink {
         w &= keep * 0x01010101u;
         const int32_t y = l - 8;
         if (lane >= 2 && lane < 62) reinterpret_cast<uint32_t*>(obs + y * RLE_OBS_W)[lane - 2] = w;
-        if (lane == 0) emph[y] = (uint8_t)((s.mask >> 5) & 7u);
+    }
+    // Emphasis of rows y0 .. y1 - 1 (the lines' mask bits 5-7).
+    __device__ void emphasis(uint8_t* emph, int32_t y0, int32_t y1, uint32_t mask) {
+        for (int32_t y = y0 + lane; y < y1; y += 64) emph[y] = (uint8_t)((mask >> 5) & 7u);
     }
     // The line's sprite-0 check (replay_dev.h rs_check at the line's end, where the whole line is drawn): the first
     // pixel in [sphitx, min(sphitx + 8, 255)) where sprite 0's pixel is set and the background pixel is not
@@ -401,11 +404,10 @@ struct RenderSink {
         const uint32_t back4 = (t[0] & 0xFFu) * 0x01010101u;
         const uint32_t mask = s.mask;
         if (!rs_rendering(s)) {
-            const uint32_t row4 = back4 & 0x3F3F3F3Fu, em = (mask >> 5) & 7u;
-            for (int32_t y = (l > 8 ? l : 8) - 8; y < stop - 8; ++y) {
+            const uint32_t row4 = back4 & 0x3F3F3F3Fu;
+            for (int32_t y = (l > 8 ? l : 8) - 8; y < stop - 8; ++y)
                 if (lane >= 2 && lane < 62) reinterpret_cast<uint32_t*>(obs + y * RLE_OBS_W)[lane - 2] = row4;
-                if (lane == 0) emph[y] = (uint8_t)em;
-            }
+            emphasis(emph, (l > 8 ? l : 8) - 8, stop - 8, mask);
             s.sphitx = kNoCheck;
             return;
         }
@@ -427,6 +429,7 @@ struct RenderSink {
         uint32_t spt[4];
         sprite_table(spt);
         uint32_t key = 0xFFFFFFFFu, tb = 0, tsel = 0, vl = s.v;
+        const int32_t l0 = l;
         for (; l < stop; ++l) {
             vl = s.v;
             if ((vl & 0x0FFFu) != key) {   // a new row of tiles (or the run's first line)
@@ -445,22 +448,32 @@ struct RenderSink {
             const uint64_t sel = __ballot(row < h);
             const uint32_t rank = __builtin_amdgcn_mbcnt_hi((uint32_t)(sel >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)sel, 0u));
             const uint32_t target = fetched == drawn ? drawn ^ 1u : fetched;
-            if (row < h && rank < 8u) {
-                const uint32_t r2 = row + (row & 8u);
-                L->spr[target][rank] = pattern_of<kPairs>(s.chr_lo, s.chr_hi, (sb + ((r2 ^ flip) - flip)) & 0x1FFFu) |
-                                       (e & 0xFFFF0000u);
-            }
+            // (every lane fetches its entry's row, only the first eight on the line keep it)
+            const uint32_t r2 = row + (row & 8u);
+            const uint32_t sp = pattern_of<kPairs>(s.chr_lo, s.chr_hi, (sb + ((r2 ^ flip) - flip)) & 0x1FFFu) |
+                                (e & 0xFFFF0000u);
+            if (row < h && rank < 8u) L->spr[target][rank] = sp;
             fetched = target;
             expand_sprites(s);
             __syncthreads();
             uint32_t w = back4;
             if (bg_on) w = shift4(lane & 1 ? other : mine, lane & 1 ? mine : other, kk0, s.fx, t);
             if (s.sphitx != kNoCheck) check_hit(s, w);
-            compose(s, l, w, obs, emph, spt);
+            compose(s, l, w, obs, spt);
             // the end of the line: Fixit1 and Fixit2 (v from t horizontally), the next line's sprites, RefreshSprites
             s.sphitx = kNoCheck;
             s.v = (y_step(vl) & 0x7BE0u) | (s.t & 0x041Fu);
-            sprite_fetch_done(s, sel);
+            // what RefreshSprites needs of the fetch (sprite_fetch_done): with sprite 0 on the line it is the first
+            // one fetched, lane 0's
+            const uint32_t n = (uint32_t)__builtin_popcountll(sel);
+            s.f_n = n < 8u ? n : 8u;
+            s.f_blurp = (uint32_t)(sel & 1u);
+            if (s.f_blurp) {
+                const uint32_t e0 = (uint32_t)__builtin_amdgcn_readlane((int)sp, 0);
+                s.f_bits = (e0 & 0xFFu) | ((e0 >> 8) & 0xFFu);
+                s.f_attr = (e0 >> 16) & 0xFFu;
+                s.f_x = e0 >> 24;
+            }
             if (spr_on) {
                 s.spork = 0;
                 if (s.f_n != 0) {
@@ -475,6 +488,7 @@ struct RenderSink {
                 }
             }
         }
+        emphasis(emph, (l0 > 8 ? l0 : 8) - 8, stop - 8, mask);
         // the last line's slots 32 and 33, where a line with writes after the run starts from (F[34], F[35])
         if (lane < 2) fetch_slot(s, v_steps(vl, 32u + (uint32_t)lane), 32u + (uint32_t)lane, s.chr_lo, s.chr_hi);
         ha = 34u;
@@ -526,7 +540,8 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(8, 8))) void
         rs_line(s, sink, l, true);
         uint32_t spt[4];
         sink.sprite_table(spt);
-        sink.compose(s, l, L.px[lane], obs, emph, spt);
+        sink.compose(s, l, L.px[lane], obs, spt);
+        if (l >= 8) sink.emphasis(emph, l - 8, l - 7, s.mask);
         rs_end_of_line(s, sink, l, true);
     }
 }
