@@ -11,6 +11,7 @@
 #include "env_dev.h"
 #include "nes_dev.h"
 #include "optab.h"
+#include "render_dev.h"
 #include "rlenv_state.h"
 #include "wave_dev.h"
 
@@ -165,6 +166,8 @@ struct WaveLds {
     Con cs;
     uint32_t scratch[34];   // the sprite-0 check's MMC2 pages
 };
+static_assert(sizeof(RenderScratch) <= NES_RAM_BYTES && offsetof(WaveLds, ram) % 16 == 0,
+              "the render's scratch fits over the CPU RAM");
 
 // One console per wavefront (blockDim 64): the console index comes from blockIdx only, so every emulator value is
 // wave-uniform; lane 0 runs the 6502 on the scalar unit (SGPRs, uniform branches) with the console's memories in
@@ -172,7 +175,9 @@ struct WaveLds {
 // round (left to itself the compiler takes 71 VGPRs, 7 waves, and the eighth wave of every SIMD runs after the
 // others).
 // kBank: a decision frame whose picture is drawn from a frame bank (its render state is copied there at the end).
-template <uint32_t B, bool kBank>
+// kDraw: a decision frame whose picture the same wave draws once the frame is emulated and the console copied out
+// (render_dev.h, the render's scratch laid over the CPU RAM in LDS, the nametables and OAM where the frame left them).
+template <uint32_t B, bool kBank, bool kDraw = false>
 __device__ __forceinline__ void emu_body(const EmuArgs& a) {
     __shared__ __align__(16) WaveLds L;
     const int count = a.mode == EMU_BOOT ? 1 : slot_count(a.g, a.use_list, a.e0, a.e1);
@@ -244,6 +249,18 @@ __device__ __forceinline__ void emu_body(const EmuArgs& a) {
         wave_copy16(b->oam, L.oam, NES_OAM_BYTES, lane);
         if (lane == 0) b->log_n = L.cs.log_n;
         if (a.bank_chr) wave_copy16(a.bank_chr + (size_t)e * NES_CHRRAM_BYTES, rec->chr_ram, NES_CHRRAM_BYTES, lane);
+    }
+    if constexpr (kDraw) {
+        if (a.mode == EMU_DECISION && !a.s.no_render) {
+            // the frame log and CHR RAM lane 0 wrote are read by vector loads after this sync, and the copy-out's
+            // reads of the RAM are done before the scratch overwrites it
+            const uint32_t log_n = uni(L.cs.log_n);
+            __syncthreads();
+            uint8_t* obs = a.o.obs + ((size_t)ge * RLE_FRAMES + a.f) * RLE_OBS_PIXELS;
+            uint8_t* emph = a.o.emph + ((size_t)ge * RLE_FRAMES + a.f) * RLE_OBS_H;
+            draw_frame<false>(reinterpret_cast<RenderScratch*>(L.ram), L.nt, L.oam, rec->log, log_n, a.g.cart,
+                              rec->chr_ram, obs, emph, lane);
+        }
     }
 }
 

@@ -333,19 +333,25 @@ inline JitProgram jit_translate_banked(const std::vector<uint8_t>& prg) {
     return p;
 }
 
-// The source of the kernel a translation is compiled into: the console-frame kernel (emu_kernel.h) of the fixed-PRG
-// boards with the blocks (the header "jit_blocks.inc") in its burst loop, launched as rlenv_hip.hip k_emu_w is.
+// The source of the kernels a translation is compiled into: the console-frame kernel (emu_kernel.h) with the blocks
+// (the header "jit_blocks.inc") in its burst loop, launched as rlenv_hip.hip k_emu_w is: k_emu_jit_draw for decision
+// frames the emulator's waves draw themselves, and in a bank translation also k_emu_jit for frames drawn from frame
+// banks.
 // hiprtc has the HIP runtime and the fixed-width integer types built in, the latter in a namespace of its own.
 inline std::string jit_module_source(bool bank, bool banked) {
+    const std::string board = banked ? "NES_BOARD_MMC3" : "NES_BOARD_NROM";
     return std::string(
                "using __hip_internal::uint8_t;\nusing __hip_internal::uint16_t;\nusing __hip_internal::uint32_t;\n"
                "using __hip_internal::uint64_t;\nusing __hip_internal::int8_t;\nusing __hip_internal::int16_t;\n"
                "using __hip_internal::int32_t;\nusing __hip_internal::int64_t;\n"
                "#ifndef offsetof\n#define offsetof(t, m) __builtin_offsetof(t, m)\n#endif\n"
-               "#define RLENV_JIT_INC \"jit_blocks.inc\"\n#include \"emu_kernel.h\"\n"
-               "extern \"C\" __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(8, 8)))\n"
-               "void k_emu_jit(nd::EmuArgs a) { nd::emu_body<") +
-           (banked ? "NES_BOARD_MMC3, " : "NES_BOARD_NROM, ") + (bank ? "true" : "false") + ">(a); }\n";
+               "#define RLENV_JIT_INC \"jit_blocks.inc\"\n#include \"emu_kernel.h\"\n") +
+           (bank ? std::string("extern \"C\" __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(8, 8)))\n"
+                               "void k_emu_jit(nd::EmuArgs a) { nd::emu_body<") +
+                       board + ", true, false>(a); }\n"
+                 : std::string()) +
+           "extern \"C\" __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(8, 8)))\n"
+           "void k_emu_jit_draw(nd::EmuArgs a) { nd::emu_body<" + board + ", false, true>(a); }\n";
 }
 
 }  // namespace nd

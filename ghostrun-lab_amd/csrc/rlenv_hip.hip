@@ -38,6 +38,7 @@
 #include "jit.h"
 #include "nes_dev.h"
 #include "optab.h"
+#include "render_dev.h"
 #include "rlenv_api.h"
 #include "rlenv_state.h"
 #include "wave_dev.h"
@@ -50,9 +51,9 @@ thread_local std::string g_error;
 
 // ============================================================================================ kernels
 // (the console-frame kernel's arguments and body: emu_kernel.h, shared with the translated kernels of jit.h)
-template <uint32_t B, bool kBank>
+template <uint32_t B, bool kBank, bool kDraw>
 __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(8, 8))) void k_emu_w(EmuArgs a) {
-    emu_body<B, kBank>(a);
+    emu_body<B, kBank, kDraw>(a);
 }
 
 // Power-on of one console record.
@@ -71,436 +72,15 @@ struct RenderArgs {
     const uint8_t* bank_chr;
 };
 
-// The renderer's side of the line replay (replay_dev.h): the walker runs wave-uniform on every lane and hands each run
-// of tile slots here, where the 64 lanes work on it in LDS:
-//   - fetch: lane j fetches slot j's tile (nametable tile and attribute, both pattern bytes) into F[j + 2];
-//   - output: lane k >= 2 shifts out slot k's 8 pixels - the two fetches before it, fine x, the palette of the moment -
-//     into the line buffer at the run's output position (F[0], F[1] carry the line's first fetches' predecessors);
-//   - the run's hidden left column and background-off range, then the sprite-0 check over 8 lanes.
-// Sprite lines are fetched with one ballot over the 64 OAM entries (lane = sprite) into one of two buffers; the one
-// RefreshSprites latched is expanded at the start of the line it is drawn on (lane 8k + p = pixel p of sprite k) into
-// a sprite line with one LDS max per pixel, which picks the lowest-numbered opaque sprite.
-// A run of lines with no write (most of them) takes fast_run: per line one fetch phase, one sync, and each lane
-// composes its 4 pixels in registers.
-struct RenderLds {
-    uint8_t nt[NES_NT_BYTES];
-    uint8_t oam[NES_OAM_BYTES];
-    uint32_t px[64];          // the line: palette value, 0x40 | backdrop where the background is transparent
-    uint32_t sp[256];         // the sprite line: (7 - rank) << 8 | behind << 7 | palette << 2 | value, 0 = none
-    uint32_t f[36];           // fetches: lo | hi << 8 | attribute << 16; 0-1 carried, 2 + j slot j
-    uint32_t spr[2][8];       // sprite lines: lo | hi << 8 | attr << 16 | x << 24
-    uint32_t pages[34 + 8];   // MMC2: the pages of each slot's fetch, then of each sprite's
-    uint4 tab[2];             // the background palette table (bg_table), the latched sprite palette (latch_sprites)
-    alignas(16) uint8_t pal[32];
-};
-
-typedef __attribute__((address_space(4))) const uint32_t KU32;
-
-struct RenderSink {
-    RenderLds* L;
-    const uint32_t* log;      // the console's frame log (read-only in this kernel: scalar loads)
-    const uint8_t *chr_rom, *chr_ram;
-    const uint16_t* chr_pairs;   // CHR ROM by tile row (both planes in one word), nullptr with CHR RAM
-    int lane;
-    bool mmc2;
-    uint32_t ha, hb;          // F indices of the last two fetches
-    uint32_t fetched, drawn, drawn_n;
-    // L->tab[0] and L->tab[1] are rebuilt only after a palette write
-    bool bg_stale, sp_stale;
-
-    __device__ uint32_t ev(uint32_t i) { return ((KU32*)(log + NES_LOG_HDR_WORDS))[i]; }
-    __device__ uint32_t nt(uint32_t i) { return uni(L->nt[i]); }
-    __device__ uint32_t oam(uint32_t i) { return uni(L->oam[i]); }
-    __device__ uint32_t back() { return ((uint32_t)L->pal[0] & 0x3Fu) | 0x40u; }
-    __device__ void palette(uint32_t i, uint32_t v) {
-        if (lane == 0) L->pal[i] = (uint8_t)v;
-        __syncthreads();
-        bg_stale = sp_stale = true;
-    }
-    __device__ void slot_pages(int32_t j, uint32_t pk) {
-        if (lane == 0) L->pages[j] = pk;
-    }
-    __device__ void sprite_pages(uint32_t n, uint32_t pk) {
-        if (lane == 0) L->pages[34 + n] = pk;
-    }
-    // The latched sprite line expanded into L->sp (before the line's first sync; the compose reads and clears it).
-    __device__ void expand_sprites(const Rs& s) {
-        if (!s.spork) return;
-        const uint32_t k = (uint32_t)lane >> 3, p = (uint32_t)lane & 7u;
-        if (k < drawn_n) {
-            const uint32_t e = L->spr[drawn][k];
-            const uint32_t attr = (e >> 16) & 0xFFu, b = (attr & 0x40u) ? p : 7u - p;
-            const uint32_t val = ((e >> b) & 1u) | (((e >> (8u + b)) & 1u) << 1);
-            const uint32_t x = (e >> 24) + p;
-            if (val && x < 256u)
-                atomicMax(&L->sp[x], ((7u - k) << 8) | ((attr & 0x20u) << 2) | ((attr & 3u) << 2) | val);
-        }
-    }
-    // A new line (general path): the last two fetches move to F[0], F[1]; nothing drawn yet (0xFF reads as
-    // transparent); the sprite line expanded.
-    __device__ void line_begin(const Rs& s, bool) {
-        const uint32_t carry = lane < 2 ? L->f[lane ? hb : ha] : 0u;
-        __syncthreads();
-        if (lane < 2) L->f[lane] = carry;
-        L->px[lane] = 0xFFFFFFFFu;
-        ha = 0;
-        hb = 1;
-        expand_sprites(s);
-        __syncthreads();
-    }
-    // Pixels [o, o + n) the backdrop (o and n multiples of 8).
-    __device__ void fill(int32_t o, int32_t n) {
-        const int32_t x = 4 * lane;
-        if (x >= o && x < o + n) L->px[lane] = back() * 0x01010101u;
-    }
-    __device__ void off_run(int32_t out, int32_t n, bool) {
-        fill(out, n);
-        __syncthreads();
-    }
-    // The two plane bytes of pattern address pa (a row of plane 0; pa + 8 is plane 1) through the packed pages,
-    // plane 0 in the low byte: one 16-bit load with CHR ROM (kPairs), two byte loads with CHR RAM.
-    template <bool kPairs>
-    __device__ uint32_t pattern_of(uint32_t lo, uint32_t hi, uint32_t pa) {
-        if constexpr (!kPairs) {
-            return chr_pk(chr_rom, chr_ram, lo, hi, pa) | (chr_pk(chr_rom, chr_ram, lo, hi, pa + 8u) << 8);
-        } else {
-            // the 1 KB slot's page: byte (pa >> 10) & 7 of hi:lo, one byte permute
-            const uint32_t page = __builtin_amdgcn_perm(hi, lo, (pa >> 10) & 7u) & 0xFFu;
-            return chr_pairs[page * 512u + ((pa & 0x3F0u) >> 1) + (pa & 7u)];
-        }
-    }
-    __device__ uint32_t pattern(uint32_t lo, uint32_t hi, uint32_t pa) {
-        return chr_pairs ? pattern_of<true>(lo, hi, pa) : pattern_of<false>(lo, hi, pa);
-    }
-    // Slot j's tile (nametable tile and attribute, both pattern bytes) fetched at v into F[j + 2].
-    __device__ void fetch_slot(const Rs& s, uint32_t v, uint32_t j, uint32_t lo, uint32_t hi) {
-        const uint32_t ntb = 0x2000u | (v & 0x0C00u), col = v & 31u;
-        const uint32_t tile = L->nt[nt_slot(s.nt_map, ntb | (v & 0x3FFu))];
-        const uint32_t at = L->nt[nt_slot(s.nt_map, ntb | 0x3C0u | (col >> 2) | ((v & 0x380u) >> 4))];
-        const uint32_t sel = (at >> ((col & 2u) | ((v & 0x40u) >> 4))) & 3u;
-        const uint32_t pa = tile * 16u + ((s.ctrl & 0x10u) << 8) + ((v >> 12) & 7u);
-        L->f[j + 2u] = pattern(lo, hi, pa) | (sel << 16);
-    }
-    // The background palette as 16 bytes in four words, entry 4a + v: palette a's colour v, and for v = 0 the
-    // backdrop with bit 6 set (the transparency mark the sprite priority test reads). Wave-uniform.
-    // (The tables are written by every active lane, the same 16 bytes: callers may be in lane-divergent code.)
-    __device__ void bg_table(uint32_t t[4]) {
-        if (bg_stale) {
-            const uint4 p = reinterpret_cast<const uint4*>(L->pal)[0];
-            const uint32_t b = back();
-            L->tab[0] = make_uint4((uni(p.x) & 0x3F3F3F00u) | b, (uni(p.y) & 0x3F3F3F00u) | b,
-                                   (uni(p.z) & 0x3F3F3F00u) | b, (uni(p.w) & 0x3F3F3F00u) | b);
-            bg_stale = false;
-        }
-        const uint4 q = L->tab[0];
-        t[0] = uni(q.x);
-        t[1] = uni(q.y);
-        t[2] = uni(q.z);
-        t[3] = uni(q.w);
-    }
-    // 4 background pixels, leftmost in the low byte: kk0..kk0 + 3 of the 8 a slot shifts out from fetches p2 (older),
-    // p1 with fine x fx; pixel q is bit 15 - fx - kk0 - q of the two 16-bit plane pairs, with p2's attribute while
-    // fx + kk0 + q < 8, else p1's. All four at once: the planes' 4 bits bit-reversed into place and spread one to a
-    // byte, the attribute chosen per byte by a mask, and the colours looked up 4 at a time by byte permutes of the
-    // palette table.
-    __device__ uint32_t shift4(uint32_t p2, uint32_t p1, uint32_t kk0, uint32_t fx, const uint32_t t[4]) {
-        const uint32_t sh = fx + kk0;   // 0..11
-        const uint32_t lo16 = ((p2 & 0xFFu) << 8) | (p1 & 0xFFu), hi16 = (p2 & 0xFF00u) | ((p1 >> 8) & 0xFFu);
-        const uint32_t lo4 = __builtin_bitreverse32(lo16 << (16u + sh)) & 0xFu;   // pixel q at bit q
-        const uint32_t hi4 = __builtin_bitreverse32(hi16 << (16u + sh)) & 0xFu;
-        const uint32_t val = ((lo4 * 0x00204081u) & 0x01010101u) | (((hi4 * 0x00204081u) & 0x01010101u) << 1);
-        const int32_t b = 8 - (int32_t)sh;   // pixels q < b take p2's attribute
-        const uint32_t m = b >= 4 ? 0xFFFFFFFFu : b <= 0 ? 0u : (1u << (8 * b)) - 1u;
-        const uint32_t attr = ((((p2 >> 16) & 3u) * 0x01010101u) & m) | ((((p1 >> 16) & 3u) * 0x01010101u) & ~m);
-        const uint32_t idx = (attr << 2) | val;   // palette entry per byte, 0..15
-        const uint32_t sel = idx & 0x07070707u;
-        const uint32_t lo = __builtin_amdgcn_perm(t[1], t[0], sel), hi = __builtin_amdgcn_perm(t[3], t[2], sel);
-        const uint32_t mh = ((idx >> 3) & 0x01010101u) * 0xFFu;
-        return (lo & ~mh) | (hi & mh);
-    }
-    __device__ void on_run(const Rs& s, int32_t first, int32_t last, int32_t out, bool pixels) {
-        __syncthreads();   // the walker's page and palette writes
-        if (lane >= first && lane < last) {
-            const uint32_t pk = mmc2 ? L->pages[lane] : 0u;
-            fetch_slot(s, v_steps(s.v, (uint32_t)(lane - first)), (uint32_t)lane, mmc2 ? pk : s.chr_lo,
-                       mmc2 ? pk : s.chr_hi);
-        }
-        __syncthreads();
-        if (pixels) {
-            // lane j writes pixels 4j..4j+3 where they fall in the run's output, [out, out + 8 (last - from))
-            const int32_t from = first > 2 ? first : 2, x = 4 * lane;
-            if (last > from && x >= out && x < out + 8 * (last - from)) {
-                const int32_t k = from + (x - out) / 8;   // the slot that shifts out pixel x
-                const int32_t j = k - first;
-                const uint32_t p1 = L->f[j >= 1 ? (uint32_t)k + 1u : hb];
-                const uint32_t p2 = L->f[j >= 2 ? (uint32_t)k : (j == 1 ? hb : ha)];
-                uint32_t t[4];
-                bg_table(t);
-                L->px[lane] = shift4(p2, p1, (uint32_t)((x - out) & 7), s.fx, t);
-            }
-            const bool clip = first <= 2 && last > 2 && !(s.mask & 0x02u), bg_off = !(s.mask & 0x08u);
-            if (clip || bg_off) {
-                __syncthreads();
-                if (clip) fill(0, 8);
-                if (bg_off) {
-                    int32_t f = first - 2, n = last - first;
-                    if (f < 0) {
-                        n += f;
-                        f = 0;
-                    }
-                    fill(8 * f, 8 * n);
-                }
-            }
-        }
-        if (last - first >= 2) {
-            ha = (uint32_t)last;
-            hb = (uint32_t)last + 1u;
-        } else {
-            ha = hb;
-            hb = (uint32_t)first + 2u;
-        }
-        __syncthreads();
-    }
-    __device__ int32_t find_hit(int32_t x, uint32_t bits, int32_t end) {
-        const int32_t xi = x + lane;
-        const bool hit = lane < 8 && xi < end && ((bits >> (7 - lane)) & 1u) &&
-                         !(reinterpret_cast<const uint8_t*>(L->px)[xi] & 0x40u);
-        const uint64_t b = __ballot(hit);
-        return b ? x + (int32_t)__builtin_ctzll(b) : -1;
-    }
-    // The lanes' part of FetchSpriteData: lane i is OAM entry i; the first eight on line l + 1 are fetched into the
-    // buffer not latched. Returns the ballot of the entries on the line (read the fetch after a sync).
-    __device__ uint64_t sprite_fetch_lanes(const Rs& s, int32_t l) {
-        const uint32_t ctrl = s.ctrl, h = (ctrl & 0x20u) ? 16u : 8u;
-        const uint32_t e = reinterpret_cast<const uint32_t*>(L->oam)[lane];
-        const uint32_t row = (uint32_t)(l - (int32_t)(e & 0xFFu));
-        const uint64_t sel = __ballot(row < h);
-        const uint32_t rank = __builtin_amdgcn_mbcnt_hi((uint32_t)(sel >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)sel, 0u));
-        const uint32_t target = fetched == drawn ? drawn ^ 1u : fetched;
-        if (row < h && rank < 8u) {
-            const uint32_t tile = (e >> 8) & 0xFFu;
-            const uint32_t table8 = (ctrl & 0x08u) && !(ctrl & 0x20u) ? 0x1000u : 0u;
-            const uint32_t base = h == 16u ? ((tile & 1u) << 12) + ((tile & 0xFEu) << 4) : (tile << 4) + table8;
-            // the row's offset, row + (row & 8), or with vertical flip (attribute bit 7) 7 (+ 16 for 8x16) minus it:
-            // flip = all ones negates it (x ^ flip) - flip and adds the 7 (+ 16)
-            const uint32_t r2 = row + (row & 8u), flip = (uint32_t)((int32_t)(e << 8) >> 31);
-            const uint32_t pa = (base + (flip & (7u + ((ctrl & 0x20u) >> 1))) + ((r2 ^ flip) - flip)) & 0x1FFFu;
-            const uint32_t pk = mmc2 ? L->pages[34 + rank] : 0u;
-            const uint32_t lo = mmc2 ? pk : s.chr_lo, hi = mmc2 ? pk : s.chr_hi;
-            L->spr[target][rank] = pattern(lo, hi, pa) | (e & 0xFFFF0000u);
-        }
-        fetched = target;
-        return sel;
-    }
-    // What RefreshSprites needs of the fetch (after the sync).
-    __device__ void sprite_fetch_done(Rs& s, uint64_t sel) {
-        const uint32_t n = (uint32_t)__builtin_popcountll(sel);
-        s.f_n = n < 8u ? n : 8u;
-        s.f_blurp = (uint32_t)(sel & 1u);
-        if (s.f_n) {
-            const uint32_t e0 = uni(L->spr[fetched][0]);
-            s.f_bits = (e0 & 0xFFu) | ((e0 >> 8) & 0xFFu);
-            s.f_attr = (e0 >> 16) & 0xFFu;
-            s.f_x = e0 >> 24;
-        }
-    }
-    __device__ void fetch_sprites(Rs& s, int32_t l) {
-        if (mmc2) __syncthreads();   // the walker's page writes
-        const uint64_t sel = sprite_fetch_lanes(s, l);
-        __syncthreads();
-        sprite_fetch_done(s, sel);
-    }
-    __device__ void latch_table() {
-        const uint4 p = reinterpret_cast<const uint4*>(L->pal)[1];
-        L->tab[1] = make_uint4(uni(p.x) & 0x3F3F3F3Fu, uni(p.y) & 0x3F3F3F3Fu, uni(p.z) & 0x3F3F3F3Fu,
-                               uni(p.w) & 0x3F3F3F3Fu);
-        sp_stale = false;
-    }
-    // RefreshSprites: the fetched line is the one drawn next, with the sprite palette of the moment (read by the next
-    // line's compose, after its syncs).
-    __device__ void latch_sprites(const Rs& s) {
-        drawn = fetched;
-        drawn_n = s.f_n;
-        if (sp_stale) latch_table();
-    }
-    // CopySprites (with sprites on at the line's end and a latched line waiting) over the background pixels w of
-    // this lane, greyscale while rendering, and the observation row (rl/csrc/nes_machine.cuh:133-155: lines 8..231,
-    // x 8..247) with the line's emphasis (patch:1637-1661). Clears the lane's part of the sprite line.
-    __device__ void sprite_table(uint32_t t[4]) {
-        const uint4 q = L->tab[1];
-        t[0] = uni(q.x);
-        t[1] = uni(q.y);
-        t[2] = uni(q.z);
-        t[3] = uni(q.w);
-    }
-    // spt: the latched sprite palette (sprite_table). The line's emphasis is the caller's (the mask at this point).
-    __device__ void compose(Rs& s, int32_t l, uint32_t w, uint8_t* obs, const uint32_t spt[4]) {
-        const bool expanded = s.spork != 0, sprites = (s.mask & 0x10u) && expanded;
-        if (sprites) s.spork = 0;
-        const uint32_t keep = (s.mask & 0x01u) && rs_rendering(s) ? 0x30u : 0x3Fu;
-        if (expanded) {
-            const uint4 sp = reinterpret_cast<const uint4*>(L->sp)[lane];
-            reinterpret_cast<uint4*>(L->sp)[lane] = make_uint4(0u, 0u, 0u, 0u);
-            if (sprites) {
-                // the four pixels at once, one per byte: a sprite pixel (value != 0) shows in front, or behind a
-                // transparent background pixel (bit 6, the backdrop mark), except in the left 8 with sprite
-                // clipping; its colour from the latched sprite palette by byte permutes (entry = palette << 2 | value)
-                const uint32_t eb = (sp.x & 0xFFu) | ((sp.y & 0xFFu) << 8) | ((sp.z & 0xFFu) << 16) | (sp.w << 24);
-                const uint32_t opaque = (eb | (eb >> 1)) & 0x01010101u;
-                const uint32_t front = ~(eb >> 7) & 0x01010101u, clear_bg = (w >> 6) & 0x01010101u;
-                const bool clipped = !(s.mask & 0x04u) && lane < 2;
-                const uint32_t show = clipped ? 0u : (opaque & (front | clear_bg)) * 0xFFu;
-                const uint32_t sel = eb & 0x07070707u;
-                const uint32_t lo = __builtin_amdgcn_perm(spt[1], spt[0], sel), hi = __builtin_amdgcn_perm(spt[3], spt[2], sel);
-                const uint32_t hm = ((eb >> 3) & 0x01010101u) * 0xFFu;
-                w = (w & ~show) | (((lo & ~hm) | (hi & hm)) & show);
-            }
-        }
-        if (l < 8) return;
-        w &= keep * 0x01010101u;
-        const int32_t y = l - 8;
-        if (lane >= 2 && lane < 62) reinterpret_cast<uint32_t*>(obs + y * RLE_OBS_W)[lane - 2] = w;
-    }
-    // Emphasis of rows y0 .. y1 - 1 (the lines' mask bits 5-7).
-    __device__ void emphasis(uint8_t* emph, int32_t y0, int32_t y1, uint32_t mask) {
-        for (int32_t y = y0 + lane; y < y1; y += 64) emph[y] = (uint8_t)((mask >> 5) & 7u);
-    }
-    // The line's sprite-0 check (replay_dev.h rs_check at the line's end, where the whole line is drawn): the first
-    // pixel in [sphitx, min(sphitx + 8, 255)) where sprite 0's pixel is set and the background pixel is not
-    // transparent (bit 6, the backdrop mark), over the background pixels w the lanes hold (4 each).
-    __device__ void check_hit(Rs& s, uint32_t w) {
-        const int32_t x0 = s.sphitx, end = x0 + 8 < 255 ? x0 + 8 : 255;
-        uint32_t first = 4u;
-        for (uint32_t q = 0; q < 4u; ++q) {
-            const int32_t x = 4 * lane + (int32_t)q;
-            const bool in = x >= x0 && x < end;
-            const uint32_t bit = in ? (s.sphit_bits >> (uint32_t)(7 - (x - x0))) & 1u : 0u;
-            if (first == 4u && bit && !((w >> (8u * q)) & 0x40u)) first = q;
-        }
-        const uint64_t b = __ballot(first < 4u);
-        if (b) {
-            const int ln = (int)__builtin_ctzll(b);
-            s.hit = 1;
-            s.hit_x = 4 * ln + __builtin_amdgcn_readlane((int)first, ln);
-            s.sphitx = kNoCheck;
-        }
-    }
-    // Lines l .. stop - 1, a run with no write from the first one's lead-in to the last one's end (and no MMC2
-    // latches): each line is one run of the 34 slots with the state as it is, the sprite-0 check (if one is due)
-    // against the drawn line, FetchSpriteData, Fixit1/Fixit2 and RefreshSprites in closed form. ctrl, mask, the
-    // palette, the CHR pages and the nametable map hold for the whole run, so what follows from them is set up once:
-    //   - background: lane j fetches tile slot (j + 1) / 2, so lanes 2i and 2i + 1 hold slots i and i + 1 between
-    //     them, the two fetches that lane 2i's pixels 8i..8i+3 and lane 2i + 1's 8i+4..8i+7 shift out (pixel x from
-    //     slots x / 8 and x / 8 + 1), and one swap within the lane pair (DPP) gives each lane both. The tile and
-    //     attribute are read again only when v's row of tiles changes (every 8 lines), the pattern row every line;
-    //   - sprites: lane i keeps OAM entry i and its pattern row base; FetchSpriteData is one ballot over the lanes;
-    //   - the lanes expand this line's sprites, sync once, and each composes its 4 pixels in registers.
-    // With rendering off the lines are the backdrop: nothing is fetched, v stays, no sprite is drawn and no sprite-0
-    // check can hit (the backdrop is transparent).
-    template <bool kPairs>
-    __device__ void fast_run(Rs& s, int32_t l, int32_t stop, uint8_t* obs, uint8_t* emph) {
-        uint32_t t[4];
-        bg_table(t);
-        const uint32_t back4 = (t[0] & 0xFFu) * 0x01010101u;
-        const uint32_t mask = s.mask;
-        if (!rs_rendering(s)) {
-            const uint32_t row4 = back4 & 0x3F3F3F3Fu;
-            for (int32_t y = (l > 8 ? l : 8) - 8; y < stop - 8; ++y)
-                if (lane >= 2 && lane < 62) reinterpret_cast<uint32_t*>(obs + y * RLE_OBS_W)[lane - 2] = row4;
-            emphasis(emph, (l > 8 ? l : 8) - 8, stop - 8, mask);
-            s.sphitx = kNoCheck;
-            return;
-        }
-        const uint32_t ctrl = s.ctrl, h = (ctrl & 0x20u) ? 16u : 8u, ptab = (ctrl & 0x10u) << 8;
-        const bool bg_on = (mask & 0x08u) && (lane >= 2 || (mask & 0x02u)), spr_on = (mask & 0x10u) != 0;
-        // this lane's OAM entry: its pattern row is sb + row (+ 8 for the lower tile of 8x16), vertical flip negating
-        // the row (flip = all ones: (r ^ flip) - flip, and sb adds the 7 or 23)
-        const uint32_t e = reinterpret_cast<const uint32_t*>(L->oam)[lane];
-        const uint32_t st = (e >> 8) & 0xFFu, table8 = (ctrl & 0x08u) && !(ctrl & 0x20u) ? 0x1000u : 0u;
-        const uint32_t flip = (uint32_t)((int32_t)(e << 8) >> 31);
-        const uint32_t sb = (h == 16u ? ((st & 1u) << 12) + ((st & 0xFEu) << 4) : (st << 4) + table8) +
-                            (flip & (7u + ((ctrl & 0x20u) >> 1)));
-        const uint32_t slot = ((uint32_t)lane + 1u) >> 1, kk0 = ((uint32_t)lane & 1u) * 4u;
-        // the latched sprite palette. With sprites on, the line before the run ended with RefreshSprites: it latched
-        // the palette as it is now, or latched nothing (no sprite is drawn before a latch in the run, which takes this
-        // same palette), so the table can be brought up to date here. With sprites off nothing is latched or drawn in
-        // the run, and the table keeps the palette of the last latch for the lines after it.
-        if (spr_on && sp_stale) latch_table();
-        uint32_t spt[4];
-        sprite_table(spt);
-        uint32_t key = 0xFFFFFFFFu, tb = 0, tsel = 0, vl = s.v;
-        const int32_t l0 = l;
-        for (; l < stop; ++l) {
-            vl = s.v;
-            if ((vl & 0x0FFFu) != key) {   // a new row of tiles (or the run's first line)
-                key = vl & 0x0FFFu;
-                const uint32_t vs = v_steps(vl, slot);
-                const uint32_t ntb = 0x2000u | (vs & 0x0C00u), col = vs & 31u;
-                const uint32_t tile = L->nt[nt_slot(s.nt_map, ntb | (vs & 0x3FFu))];
-                const uint32_t at = L->nt[nt_slot(s.nt_map, ntb | 0x3C0u | (col >> 2) | ((vs & 0x380u) >> 4))];
-                tsel = ((at >> ((col & 2u) | ((vs & 0x40u) >> 4))) & 3u) << 16;
-                tb = tile * 16u + ptab;
-            }
-            const uint32_t mine = pattern_of<kPairs>(s.chr_lo, s.chr_hi, tb + ((vl >> 12) & 7u)) | tsel;
-            const uint32_t other = (uint32_t)__builtin_amdgcn_mov_dpp((int)mine, 0xB1, 0xF, 0xF, false);   // lane ^ 1
-            // FetchSpriteData for line l + 1 into the buffer not latched
-            const uint32_t row = (uint32_t)(l - (int32_t)(e & 0xFFu));
-            const uint64_t sel = __ballot(row < h);
-            const uint32_t rank = __builtin_amdgcn_mbcnt_hi((uint32_t)(sel >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)sel, 0u));
-            const uint32_t target = fetched == drawn ? drawn ^ 1u : fetched;
-            // (every lane fetches its entry's row, only the first eight on the line keep it)
-            const uint32_t r2 = row + (row & 8u);
-            const uint32_t sp = pattern_of<kPairs>(s.chr_lo, s.chr_hi, (sb + ((r2 ^ flip) - flip)) & 0x1FFFu) |
-                                (e & 0xFFFF0000u);
-            if (row < h && rank < 8u) L->spr[target][rank] = sp;
-            fetched = target;
-            expand_sprites(s);
-            __syncthreads();
-            uint32_t w = back4;
-            if (bg_on) w = shift4(lane & 1 ? other : mine, lane & 1 ? mine : other, kk0, s.fx, t);
-            if (s.sphitx != kNoCheck) check_hit(s, w);
-            compose(s, l, w, obs, spt);
-            // the end of the line: Fixit1 and Fixit2 (v from t horizontally), the next line's sprites, RefreshSprites
-            s.sphitx = kNoCheck;
-            s.v = (y_step(vl) & 0x7BE0u) | (s.t & 0x041Fu);
-            // what RefreshSprites needs of the fetch (sprite_fetch_done): with sprite 0 on the line it is the first
-            // one fetched, lane 0's
-            const uint32_t n = (uint32_t)__builtin_popcountll(sel);
-            s.f_n = n < 8u ? n : 8u;
-            s.f_blurp = (uint32_t)(sel & 1u);
-            if (s.f_blurp) {
-                const uint32_t e0 = (uint32_t)__builtin_amdgcn_readlane((int)sp, 0);
-                s.f_bits = (e0 & 0xFFu) | ((e0 >> 8) & 0xFFu);
-                s.f_attr = (e0 >> 16) & 0xFFu;
-                s.f_x = e0 >> 24;
-            }
-            if (spr_on) {
-                s.spork = 0;
-                if (s.f_n != 0) {
-                    latch_sprites(s);
-                    if (s.f_blurp && !s.hit && s.f_bits) {
-                        uint32_t b = s.f_bits;
-                        if (s.f_attr & 0x40u) b = __builtin_bitreverse32(b) >> 24;
-                        s.sphitx = (int32_t)s.f_x;
-                        s.sphit_bits = b;
-                    }
-                    s.spork = 1;
-                }
-            }
-        }
-        emphasis(emph, (l0 > 8 ? l0 : 8) - 8, stop - 8, mask);
-        // the last line's slots 32 and 33, where a line with writes after the run starts from (F[34], F[35])
-        if (lane < 2) fetch_slot(s, v_steps(vl, 32u + (uint32_t)lane), 32u + (uint32_t)lane, s.chr_lo, s.chr_hi);
-        ha = 34u;
-        hb = 35u;
-    }
-};
-
 // One console-frame per wavefront (blockDim 64): the picture of the frame the console has logged, drawn from its
-// nametables and OAM as of the frame's vblank stop.
+// nametables and OAM as of the frame's vblank stop (render_dev.h draw_frame).
 template <bool kBank>
 __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(8, 8))) void k_render(RenderArgs a) {
-    __shared__ __align__(16) RenderLds L;
+    __shared__ __align__(16) struct {
+        uint8_t nt[NES_NT_BYTES];
+        uint8_t oam[NES_OAM_BYTES];
+        RenderScratch r;
+    } L;
     const int count = slot_count(a.g, a.use_list, a.e0, a.e1);
     const int k = (int)blockIdx.x;
     if (k >= count) return;
@@ -516,34 +96,9 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(8, 8))) void
     const uint8_t* chr_ram = kBank && a.bank_chr ? a.bank_chr + (size_t)e * NES_CHRRAM_BYTES : rec->chr_ram;
     wave_copy16(L.nt, kBank ? bk->nt : rec->nt, NES_NT_BYTES, lane);
     wave_copy16(L.oam, kBank ? bk->oam : rec->oam, NES_OAM_BYTES, lane);
-    if (lane < 8) reinterpret_cast<uint32_t*>(L.pal)[lane] = log[6 + lane];
-    if (lane < 2) L.f[lane] = 0;
-    if (lane < 16) L.spr[lane >> 3][lane & 7] = 0;
-    reinterpret_cast<uint4*>(L.sp)[lane] = make_uint4(0u, 0u, 0u, 0u);
-    __syncthreads();
-    const bool mmc2 = a.g.cart.board == NES_BOARD_MMC2;
-    RenderSink sink{&L, log, a.g.cart.chr, chr_ram, a.g.cart.chr_pairs, lane, mmc2, 0u, 1u, 0u, 0u, 0u, true, true};
-    Rs s;
-    rs_load(s, sink, log, uni(log_n), mmc2 ? a.g.cart.chr_pages1 : 0u);
-    rs_begin_frame(s, sink);
     uint8_t* obs = a.o.obs + ((size_t)ge * RLE_FRAMES + a.f) * RLE_OBS_PIXELS;
     uint8_t* emph = a.o.emph + ((size_t)ge * RLE_FRAMES + a.f) * RLE_OBS_H;
-    for (int32_t l = 0; l < 232; ++l) {
-        if (!mmc2 && s.next >= (l + 1) * 341 - NES_LINE_LEAD) {
-            // lines l .. stop - 1 end before the next write's line (its lead-in included)
-            const int32_t stop = s.next >= 232 * 341 - NES_LINE_LEAD ? 232 : (s.next + NES_LINE_LEAD) / 341;
-            if (sink.chr_pairs) sink.fast_run<true>(s, l, stop, obs, emph);
-            else sink.fast_run<false>(s, l, stop, obs, emph);
-            l = stop - 1;
-            continue;
-        }
-        rs_line(s, sink, l, true);
-        uint32_t spt[4];
-        sink.sprite_table(spt);
-        sink.compose(s, l, L.px[lane], obs, spt);
-        if (l >= 8) sink.emphasis(emph, l - 8, l - 7, s.mask);
-        rs_end_of_line(s, sink, l, true);
-    }
+    draw_frame<true>(&L.r, L.nt, L.oam, log, log_n, a.g.cart, chr_ram, obs, emph, lane);
 }
 
 // ----------------------------------------------------------------------------------------- finish
@@ -1025,7 +580,8 @@ struct JitSlot {
     bool bank = false, banked = false;   // built for frames drawn from frame banks; for a banked-PRG board
     uint32_t blocks = 0, instructions = 0;
     hipModule_t mod = nullptr;
-    hipFunction_t fn = nullptr;
+    hipFunction_t fn = nullptr;        // k_emu_jit: frames drawn from frame banks (a bank translation only)
+    hipFunction_t fn_draw = nullptr;   // k_emu_jit_draw: frames the emulator's waves draw themselves
     bool failed = false;
 };
 
@@ -1269,7 +825,7 @@ JitSlot* jit_slot(const Env& env, const GameK& g) {
 // Whether the translated kernel can be launched: loads its module on the env's device the first time its job has
 // compiled. A failed compile or load leaves the game on the library's own kernel (the results are the same).
 bool jit_ready(const Env& env, JitSlot& j) {
-    if (j.fn) return true;
+    if (j.fn_draw) return true;
     if (j.failed || !j.job) return false;
     const int st = j.job->state.load(std::memory_order_acquire);
     if (st == 0) return false;
@@ -1281,12 +837,13 @@ bool jit_ready(const Env& env, JitSlot& j) {
     (void)hipGetDevice(&cur);
     if (cur != env.device) (void)hipSetDevice(env.device);
     const bool ok = hipModuleLoadData(&j.mod, j.job->code.data()) == hipSuccess &&
-                    hipModuleGetFunction(&j.fn, j.mod, "k_emu_jit") == hipSuccess;
+                    (!j.bank || hipModuleGetFunction(&j.fn, j.mod, "k_emu_jit") == hipSuccess) &&
+                    hipModuleGetFunction(&j.fn_draw, j.mod, "k_emu_jit_draw") == hipSuccess;
     if (!ok) {
         (void)hipGetLastError();
         if (j.mod) (void)hipModuleUnload(j.mod);
         j.mod = nullptr;
-        j.fn = nullptr;
+        j.fn = j.fn_draw = nullptr;
         j.failed = true;
     }
     if (cur >= 0 && cur != env.device) (void)hipSetDevice(cur);
@@ -1389,8 +946,10 @@ FinishArgs finish_args(const Env& env, const GameK& g, int e0, int e1, const Out
     return FinishArgs{g, env.e, o, env.s, e0, e1};
 }
 
+// bank >= 0: a decision frame whose picture is drawn from frame bank `bank`; draw: a decision frame the emulator's
+// waves draw themselves.
 void launch_emu(const Env& env, const GameK& g, const Outs& o, int mode, int f, bool use_list, int e0, int e1,
-                hipStream_t st, int bank = -1) {
+                hipStream_t st, int bank = -1, bool draw = false) {
     EmuArgs a{g, env.e, o, env.s, env.optab, mode, f, use_list ? 1 : 0, e0, e1, 0, 0, nullptr, env.budget,
               bank >= 0 ? g.bank[bank] : nullptr, bank >= 0 ? g.bank_chr[bank] : nullptr};
     const int blocks = use_list ? g.n : e1 - e0;
@@ -1398,11 +957,13 @@ void launch_emu(const Env& env, const GameK& g, const Outs& o, int mode, int f, 
     // decision frames of a fixed-PRG cart run its translated kernel once that is compiled and loaded, when it was
     // built for the way this launch's frame is drawn
     JitSlot* js = mode == EMU_DECISION && blocks > 0 ? jit_slot(env, g) : nullptr;
-    if (js && js->bank == (a.bank != nullptr) && jit_ready(env, *js)) {
+    hipFunction_t fn = nullptr;
+    if (js && jit_ready(env, *js)) fn = draw ? js->fn_draw : a.bank ? js->fn : nullptr;
+    if (fn) {
         a.g.cart.fetchw = js->fetchw;
         void* args[] = {&a};
         env.clock.run(cls, st, [&] {
-            (void)hipModuleLaunchKernel(js->fn, (unsigned)blocks, 1, 1, 64, 1, 1, 0, st, args, nullptr);
+            (void)hipModuleLaunchKernel(fn, (unsigned)blocks, 1, 1, 64, 1, 1, 0, st, args, nullptr);
         });
         trace("emu_jit", st);
         return;
@@ -1412,11 +973,14 @@ void launch_emu(const Env& env, const GameK& g, const Outs& o, int mode, int f, 
             // the fast path knows two kinds of board: fixed 32 KB PRG (NROM, CNROM) and banked PRG (the rest)
             const bool nrom = g.cart.board == NES_BOARD_NROM || g.cart.board == NES_BOARD_CNROM;
             if (a.bank) {
-                if (nrom) hipLaunchKernelGGL((k_emu_w<NES_BOARD_NROM, true>), dim3(blocks), dim3(64), 0, st, a);
-                else hipLaunchKernelGGL((k_emu_w<NES_BOARD_MMC3, true>), dim3(blocks), dim3(64), 0, st, a);
+                if (nrom) hipLaunchKernelGGL((k_emu_w<NES_BOARD_NROM, true, false>), dim3(blocks), dim3(64), 0, st, a);
+                else hipLaunchKernelGGL((k_emu_w<NES_BOARD_MMC3, true, false>), dim3(blocks), dim3(64), 0, st, a);
+            } else if (draw) {
+                if (nrom) hipLaunchKernelGGL((k_emu_w<NES_BOARD_NROM, false, true>), dim3(blocks), dim3(64), 0, st, a);
+                else hipLaunchKernelGGL((k_emu_w<NES_BOARD_MMC3, false, true>), dim3(blocks), dim3(64), 0, st, a);
             } else {
-                if (nrom) hipLaunchKernelGGL((k_emu_w<NES_BOARD_NROM, false>), dim3(blocks), dim3(64), 0, st, a);
-                else hipLaunchKernelGGL((k_emu_w<NES_BOARD_MMC3, false>), dim3(blocks), dim3(64), 0, st, a);
+                if (nrom) hipLaunchKernelGGL((k_emu_w<NES_BOARD_NROM, false, false>), dim3(blocks), dim3(64), 0, st, a);
+                else hipLaunchKernelGGL((k_emu_w<NES_BOARD_MMC3, false, false>), dim3(blocks), dim3(64), 0, st, a);
             }
         });
     trace(mode == EMU_DECISION ? "emu" : mode == EMU_IDLE ? "emu_idle" : "emu_restart", st);
@@ -1475,9 +1039,8 @@ void decision_phases(const Env& env, const GameK& g, const RenderPipe& p, const 
     const bool draw = !env.s.no_render;
     const bool pipelined = draw && env.games.size() == 1 && n <= env.one_round;
     for (int f = 0; f < RLE_FRAMES; ++f) {
-        if (!pipelined) {
-            launch_emu(env, g, o, EMU_DECISION, f, false, e0, e1, st);
-            launch_render(env, g, o, f, false, false, e0, e1, st);
+        if (!pipelined || f == RLE_FRAMES - 1) {   // emulated and drawn by the same waves
+            launch_emu(env, g, o, EMU_DECISION, f, false, e0, e1, st, -1, true);
             continue;
         }
         launch_emu(env, g, o, EMU_DECISION, f, false, e0, e1, st, f);
@@ -1551,9 +1114,9 @@ void build_restart_templates(Env& env, GameK& g) {
         const EmuArgs a{t, env.e, o, s, env.optab, EMU_TEMPLATE, f, 0, 0, count, 0,
                         g.tmpl_target + (uint64_t)f * NES_FRAME_DOTS, const_cast<uint32_t*>(g.rst_fault), env.budget};
         if (g.cart.board == NES_BOARD_NROM || g.cart.board == NES_BOARD_CNROM)
-            hipLaunchKernelGGL((k_emu_w<NES_BOARD_NROM, false>), dim3(count), dim3(64), 0, 0, a);
+            hipLaunchKernelGGL((k_emu_w<NES_BOARD_NROM, false, false>), dim3(count), dim3(64), 0, 0, a);
         else
-            hipLaunchKernelGGL((k_emu_w<NES_BOARD_MMC3, false>), dim3(count), dim3(64), 0, 0, a);
+            hipLaunchKernelGGL((k_emu_w<NES_BOARD_MMC3, false, false>), dim3(count), dim3(64), 0, 0, a);
         const RenderArgs r{t, env.e, o, s, f, 0, 0, 0, count};
         hipLaunchKernelGGL(k_render<false>, dim3(count), dim3(64), 0, 0, r);
     }
@@ -1572,9 +1135,9 @@ void boot_game(Env& env, GameH& gh, const uint8_t* pads, size_t npads) {
         EmuArgs a{one, env.e, env.o, env.s, env.optab, EMU_BOOT, 0, 0, index, index + 1, pad, target, fault,
                   env.budget};
         if (g.cart.board == NES_BOARD_NROM || g.cart.board == NES_BOARD_CNROM)
-            hipLaunchKernelGGL((k_emu_w<NES_BOARD_NROM, false>), dim3(1), dim3(64), 0, 0, a);
+            hipLaunchKernelGGL((k_emu_w<NES_BOARD_NROM, false, false>), dim3(1), dim3(64), 0, 0, a);
         else
-            hipLaunchKernelGGL((k_emu_w<NES_BOARD_MMC3, false>), dim3(1), dim3(64), 0, 0, a);
+            hipLaunchKernelGGL((k_emu_w<NES_BOARD_MMC3, false, false>), dim3(1), dim3(64), 0, 0, a);
         target += NES_FRAME_DOTS;
     };
     for (size_t i = 0; i < npads; ++i) frame(g.recs, g.n, pads[i]);
@@ -2108,7 +1671,7 @@ int rlenv_jit_status(void* h, int gi, int32_t* out) {
     Env& env = *static_cast<Env*>(h);
     if (gi < 0 || gi >= (int)env.games.size()) { g_error = "jit_status: bad game"; return 1; }
     const JitSlot* j = env.games[gi].jit.get();
-    const int st = !j ? 0 : j->fn ? 2 : (j->failed || (j->job && j->job->state.load() == 2)) ? 3 : 1;
+    const int st = !j ? 0 : j->fn_draw ? 2 : (j->failed || (j->job && j->job->state.load() == 2)) ? 3 : 1;
     out[0] = st;
     out[1] = j ? (int32_t)j->blocks : 0;
     out[2] = j ? (int32_t)j->instructions : 0;
