@@ -54,6 +54,9 @@ struct Con {
     uint64_t dmc_event;
     uint32_t prg0, prg1, prg2, prg3;   // PRG byte offsets of $8000/$A000/$C000/$E000
     uint32_t nt_map;                   // 4 x 2 bits
+    // wave_dev.h run_until_wave's own state, parked here while a burst of fast instructions runs
+    uint64_t b_dmc_event, b_target;
+    uint32_t b_instructions, b_pending, b_to_event, b_ecyc, b_dmc_in, b_why, b_budget, b_nmi, b_irq;
 };
 
 struct Cart {

@@ -541,6 +541,20 @@ __device__ __forceinline__ uint32_t run_until_wave(Con& cs, const Mem& m, const 
                               1u) - 1u);
             const uint32_t lm1_0 = lm1;
             uint32_t v = lm1 << 14, take;
+            // What no instruction of the burst touches waits in LDS until the burst ends: left in registers it would
+            // crowd the burst's own values (the 6502 registers and flags) out of the scalar registers and into
+            // vector-register lanes.
+            cs.b_dmc_event = dmc_event;
+            cs.b_target = target;
+            cs.b_instructions = instructions;
+            cs.b_pending = pending;
+            cs.b_to_event = to_event;
+            cs.b_ecyc = ecyc;
+            cs.b_dmc_in = dmc_in;
+            cs.b_why = why;
+            cs.b_budget = budget;
+            cs.b_nmi = nmi;
+            cs.b_irq = irq;
             for (;;) {
 #ifdef RLENV_JIT_INC
                 ConstU32* e = (ConstU32*)((ConstU8*)m.cart.fetchw + h.pc);
@@ -562,6 +576,17 @@ __device__ __forceinline__ uint32_t run_until_wave(Con& cs, const Mem& m, const 
 #ifdef RLENV_JIT_INC
         burst_end:
 #endif
+            dmc_event = uni64(cs.b_dmc_event);
+            target = uni64(cs.b_target);
+            instructions = uni(cs.b_instructions);
+            pending = uni(cs.b_pending);
+            to_event = uni(cs.b_to_event);
+            ecyc = uni(cs.b_ecyc);
+            dmc_in = uni(cs.b_dmc_in);
+            why = uni(cs.b_why);
+            budget = uni(cs.b_budget);
+            nmi = uni(cs.b_nmi);
+            irq = uni(cs.b_irq);
             cyc = (take + 1u) >> 14;               // 0 for kGeneric
             lm1 = v >> 14;
             const uint32_t n = (v & 0x3FFFu) + 1u;
