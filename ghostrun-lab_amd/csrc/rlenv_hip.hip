@@ -290,9 +290,11 @@ __global__ __launch_bounds__(256) void k_reset_copy(FinishArgs a) {
 }
 
 // First tracker update of restarted envs; masks and dropout timeline of every env (rl/csrc/rlenv_core.cuh:138-148,
-// 327-342). The last block clears the restart list for the next decision.
+// 327-342). Thread 0 empties the restart list for the next decision's finish: every kernel that reads it (the copy,
+// the restart frames) ran before this one, and this one does not.
 __global__ __launch_bounds__(256) void k_reset_finish(FinishArgs a) {
     const int k = (int)(blockIdx.x * blockDim.x + threadIdx.x);
+    if (k == 0) *a.g.list_count = 0;
     if (k < a.e1 - a.e0) {
         const int e = a.e0 + k, ge = a.g.offset + e;
         if (a.e.resetting[ge]) {
@@ -1020,7 +1022,6 @@ void restart_phases(const Env& env, const GameK& g, const Outs& o, int e0, int e
     }
     env.clock.run(KC_RESET_FINISH, st,
                   [&] { hipLaunchKernelGGL(k_reset_finish, dim3((n + 255) / 256), dim3(256), 0, st, fa); });
-    hipLaunchKernelGGL(k_list_clear, dim3(1), dim3(1), 0, st, g.list_count);
     trace("reset_finish", st);
 }
 
