@@ -113,6 +113,7 @@ struct EmuArgs {
     uint32_t budget;       // instructions per frame (NES_BUDGET; smaller only for diagnostics)
     FrameBank* bank;       // decision frames drawn from a bank: the bank this frame's render state goes to
     uint8_t* bank_chr;
+    int finish;            // the decision's last frame, with kDraw: its waves also do the finish (finish_env)
 };
 
 __device__ __forceinline__ int slot_count(const GameK& g, int use_list, int e0, int e1) {
@@ -120,6 +121,142 @@ __device__ __forceinline__ int slot_count(const GameK& g, int use_list, int e0, 
 }
 __device__ __forceinline__ int slot_env(const GameK& g, int use_list, int e0, int k) {
     return use_list ? g.list[k] : e0 + k;
+}
+
+__device__ __forceinline__ uint64_t ram_hash(const uint8_t* ram) {
+    const uint4* w = reinterpret_cast<const uint4*>(ram);
+    uint64_t h = 0;
+    for (uint32_t k = 0; k < 128u; ++k) {
+        const uint4 q = w[k];
+        h += ev::mix64(((uint64_t)(4u * k) << 32) | q.x);
+        h += ev::mix64(((uint64_t)(4u * k + 1u) << 32) | q.y);
+        h += ev::mix64(((uint64_t)(4u * k + 2u) << 32) | q.z);
+        h += ev::mix64(((uint64_t)(4u * k + 3u) << 32) | q.w);
+    }
+    return h;
+}
+
+// RL part of the restart (rl/csrc/rlenv_core.cuh:208-263 without the record copy, which k_reset_copy does).
+__device__ __forceinline__ void reset_rl(const GameK& g, const EnvArrays& e, const Settings& s, int ge) {
+    const uint32_t ep = ++e.episode[ge];
+    const uint64_t seed = ev::ep_seed(s.run_seed, (uint32_t)ge, ep);
+    const uint64_t sseed = ev::mix64(seed ^ 0x5717C4A55EEDull);
+    uint64_t ctr = 0;
+    int idle = 0;
+    if (s.idle_max > 0) idle = (int)ev::rnd_below(sseed, ctr, (uint32_t)(s.idle_max + 1));
+    // a level start? (rl/csrc/rlenv_core.cuh:220-236: drawn only when level starts are on, after the idle count)
+    int lv = -1;
+    const LevelK& L = g.lv;
+    if (L.cap > 0 && L.thresh != 0 && ev::rnd32(sseed, ctr) < L.thresh) {
+        uint32_t saved = 0;
+        for (int q = 0; q < L.cap; ++q) saved += L.deaths[q] >= 0 ? 1u : 0u;
+        if (L.weighted) {
+            const uint32_t u = ev::rnd32(sseed, ctr);
+            for (int q = 0; q < L.cap && lv < 0; ++q)
+                if (u < L.cdf[q]) lv = q;
+        } else if (saved > 0) {
+            uint32_t pick = ev::rnd_below(sseed, ctr, saved);
+            for (int q = 0; q < L.cap && lv < 0; ++q)
+                if (L.deaths[q] >= 0 && pick-- == 0) lv = q;
+        }
+    }
+    e.sticky_seed[ge] = sseed;
+    e.sticky_ctr[ge] = ctr;
+    if (lv >= 0) {
+        e.target[ge] = L.target[lv];
+        e.ep_frame[ge] = L.frame[lv];
+        e.st[ge] = L.st[lv].st;
+        e.rd[ge] = L.st[lv].rd;
+    } else {
+        const int k = idle <= s.idle_tmpl ? idle : 0;
+        e.target[ge] = g.tmpl_target + (uint64_t)k * NES_FRAME_DOTS;
+        e.ep_frame[ge] = (uint32_t)k;
+        e.st[ge] = Rl10State{};
+        e.rd[ge] = Rl10Reader{};   // the reader and its key set restart too (rl/csrc/reward10.cuh:531-532)
+    }
+    if (e.ep_start) e.ep_start[ge] = lv;
+    e.fault[ge] = 0;
+    ev::drop_reset(e.drop[ge], seed, s.dropout != 0, s.gap_p32);   // in place: a local copy of the ring spills
+    e.prev_applied[ge] = 0;
+    e.ep_idle[ge] = idle;
+    e.resetting[ge] = 1;
+}
+
+// ram_hash by the 64 lanes of a wave (RAM in LDS): lane j hashes words 8j..8j+7, and the sums are added across the
+// lanes (the hash is a sum, so the order does not matter). Every lane returns the hash.
+__device__ __forceinline__ uint64_t ram_hash_wave(const uint8_t* ram, int lane) {
+    const uint4* w = reinterpret_cast<const uint4*>(ram) + 2 * lane;
+    uint64_t h = 0;
+    for (uint32_t i = 0; i < 2u; ++i) {
+        const uint4 q = w[i];
+        const uint32_t k = 8u * (uint32_t)lane + 4u * i;
+        h += ev::mix64(((uint64_t)k << 32) | q.x);
+        h += ev::mix64(((uint64_t)(k + 1u) << 32) | q.y);
+        h += ev::mix64(((uint64_t)(k + 2u) << 32) | q.z);
+        h += ev::mix64(((uint64_t)(k + 3u) << 32) | q.w);
+    }
+    for (int d = 32; d >= 1; d >>= 1) {
+        const uint32_t lo = (uint32_t)__shfl_xor((int)(uint32_t)h, d), hi = (uint32_t)__shfl_xor((int)(uint32_t)(h >> 32), d);
+        h += (uint64_t)lo | ((uint64_t)hi << 32);
+    }
+    return h;
+}
+
+// The finish of one env's decision (rl/csrc/rlenv_core.cuh:267-310): the tracker over the console's RAM as the
+// decision left it, the outputs, the episode end (done, synthetic ends, level clear, fault) and the RL part of a
+// restart. True when the env restarts (the caller adds it to the restart list). The RAM hash is the caller's.
+template <class A>
+__device__ __forceinline__ bool finish_env(const A& a, int e, int ge, const uint8_t* ram) {
+    Rl10State& st = a.e.st[ge];   // in place (a copy in registers spills under the console-frame kernel's 64 VGPRs)
+    const ev::Out u = ev::observe_update(a.g.game, ram, RLE_FRAMES, st, &a.e.rd[ge],
+                                         a.g.keys + (size_t)e * a.g.kcap, a.g.kcap);
+    const bool faulted = a.e.fault[ge] != 0;
+    const bool level_clear = !u.done && !faulted && a.s.episode_level_end >= 0 && (u.events & ev::EV_LEVEL) &&
+                             u.event_level == a.s.episode_level_end + 1;
+    bool synthetic = false;
+    if (a.s.end_p32 != 0 && !u.done && !faulted && !level_clear) {
+        uint64_t ctr = (uint64_t)(uint32_t)a.e.ep_len[ge];
+        const uint64_t es = ev::mix64(ev::ep_seed(a.s.run_seed, (uint32_t)ge, a.e.episode[ge]) ^ 0xE9D5EEDull);
+        synthetic = ev::rnd32(es, ctr) < a.s.end_p32;
+    }
+    const bool done = u.done || faulted || level_clear || synthetic;
+    const float r = faulted ? 0.0f : (float)u.reward;
+    a.o.reward[ge] = r;
+    if (a.o.parts)
+        for (int q = 0; q < RLE_PARTS; ++q) a.o.parts[(size_t)ge * RLE_PARTS + q] = faulted ? 0.0f : (float)u.part[q];
+    a.o.done[ge] = done ? 1 : 0;
+    a.o.events[ge] = u.events;
+    const float ret = a.e.ep_ret[ge] + r;
+    a.e.ep_ret[ge] = ret;
+    const int32_t len = a.e.ep_len[ge] + 1;
+    a.e.ep_len[ge] = len;
+    if (u.event_level > a.e.ep_maxlvl[ge]) a.e.ep_maxlvl[ge] = u.event_level;
+    ev::drop_advance(a.e.drop[ge], a.s.dropout != 0, a.s.gap_p32);   // in place (no local copy of the ring)
+    // level-start claim: the arrival with the fewest deaths, then the lowest env index (rlenv_core.cuh:288-291)
+    if (a.g.lv.cap > 0 && !done && (u.events & ev::EV_LEVEL) && u.event_level >= 0 && u.event_level < a.g.lv.levels) {
+        const unsigned long long dd = (unsigned long long)(uint32_t)(st.deaths < 0 ? 0 : st.deaths);
+        atomicMin(&a.g.lv.claim[u.event_level], (dd << 32) | (uint32_t)e);
+    }
+    if (a.o.level_out) a.o.level_out[ge] = st.has_best_level ? st.best_level : -1;
+    if (a.o.progress_out)
+        a.o.progress_out[ge] = st.has_prev && st.prev.progress_valid ? (float)(st.prev.progress / rl10_game(a.g.game).progress_unit)
+                                                                      : __builtin_nanf("");
+    if (done) {
+        if (a.o.start_out) a.o.start_out[ge] = a.e.ep_start ? a.e.ep_start[ge] : -1;
+        float* inf = a.o.info + (size_t)ge * RLE_INFO;
+        inf[0] = ret;
+        inf[1] = (float)len;
+        inf[2] = (float)(faulted ? RLE_END_FAULT : level_clear ? RLE_END_LEVEL_CLEAR
+                                                               : synthetic ? RLE_END_SYNTHETIC : st.end_reason);
+        inf[3] = (float)st.deaths;
+        inf[4] = (float)a.e.ep_maxlvl[ge];
+        inf[5] = st.overflow ? 1.0f : 0.0f;
+        inf[6] = (float)a.e.ep_idle[ge];
+        inf[7] = (float)a.e.episode[ge];
+        reset_rl(a.g, a.e, a.s, ge);
+        return true;
+    }
+    return false;
 }
 
 // Per-frame pad byte of a decision frame (rl/csrc/rlenv_core.cuh:181-191): sticky repeat, dropout, turbo phase.
@@ -176,7 +313,8 @@ static_assert(sizeof(RenderScratch) <= NES_RAM_BYTES && offsetof(WaveLds, ram) %
 // others).
 // kBank: a decision frame whose picture is drawn from a frame bank (its render state is copied there at the end).
 // kDraw: a decision frame whose picture the same wave draws once the frame is emulated and the console copied out
-// (render_dev.h, the render's scratch laid over the CPU RAM in LDS, the nametables and OAM where the frame left them).
+// (render_dev.h, the render's scratch laid over the CPU RAM in LDS, the nametables and OAM where the frame left them);
+// for the decision's last frame (a.finish) the wave also does the env's finish first.
 template <uint32_t B, bool kBank, bool kDraw = false>
 __device__ __forceinline__ void emu_body(const EmuArgs& a) {
     __shared__ __align__(16) WaveLds L;
@@ -251,15 +389,26 @@ __device__ __forceinline__ void emu_body(const EmuArgs& a) {
         if (a.bank_chr) wave_copy16(a.bank_chr + (size_t)e * NES_CHRRAM_BYTES, rec->chr_ram, NES_CHRRAM_BYTES, lane);
     }
     if constexpr (kDraw) {
-        if (a.mode == EMU_DECISION && !a.s.no_render) {
-            // the frame log and CHR RAM lane 0 wrote are read by vector loads after this sync, and the copy-out's
-            // reads of the RAM are done before the scratch overwrites it
+        const bool draw = a.mode == EMU_DECISION && !a.s.no_render, finish = a.mode == EMU_DECISION && a.finish;
+        if (draw || finish) {
+            // the frame log, CHR RAM and RAM written above are read after this sync, and the copy-out's reads of the
+            // RAM are done before the scratch overwrites it
             const uint32_t log_n = uni(L.cs.log_n);
             __syncthreads();
-            uint8_t* obs = a.o.obs + ((size_t)ge * RLE_FRAMES + a.f) * RLE_OBS_PIXELS;
-            uint8_t* emph = a.o.emph + ((size_t)ge * RLE_FRAMES + a.f) * RLE_OBS_H;
-            draw_frame<false>(reinterpret_cast<RenderScratch*>(L.ram), L.nt, L.oam, rec->log, log_n, a.g.cart,
-                              rec->chr_ram, obs, emph, lane);
+            if (finish) {   // the decision's finish (k_finish's work), in the waves of its last frame
+                const uint64_t h = a.o.ram_hash ? ram_hash_wave(L.ram, lane) : 0;
+                if (lane == 0) {
+                    if (a.o.ram_hash) a.o.ram_hash[ge] = h;
+                    if (finish_env(a, e, ge, rec->ram)) a.g.list[atomicAdd(a.g.list_count, 1u)] = e;
+                }
+                __syncthreads();   // (the hash has read the RAM before the scratch overwrites it)
+            }
+            if (draw) {
+                uint8_t* obs = a.o.obs + ((size_t)ge * RLE_FRAMES + a.f) * RLE_OBS_PIXELS;
+                uint8_t* emph = a.o.emph + ((size_t)ge * RLE_FRAMES + a.f) * RLE_OBS_H;
+                draw_frame<false>(reinterpret_cast<RenderScratch*>(L.ram), L.nt, L.oam, rec->log, log_n, a.g.cart,
+                                  rec->chr_ram, obs, emph, lane);
+            }
         }
     }
 }

@@ -291,9 +291,7 @@ __device__ inline Out observe_update(int game, const uint8_t* ram, int frames, R
         smb_gather(ram, b15);
         sig = smb_signals(b15);
     } else {
-        Rl10Reader r = *rd;
-        sig = rl10_observe(game, ram, &st, &r, keys, cap);
-        *rd = r;
+        sig = rl10_observe(game, ram, &st, rd, keys, cap);   // the reader in place
     }
     return update(sig, frames, st, rl10_game(game));
 }

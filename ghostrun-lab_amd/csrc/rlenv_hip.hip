@@ -2,9 +2,10 @@
 //
 // One decision of one game is this launch sequence on the caller's stream (the reference's phase order,
 // rl/csrc/rlenv_core.cuh:389-414 and rl/csrc/rlenv.cu:145-170):
-//   4 x (k_emu_w: one emulated frame of every console, k_render: its picture into obs slot f)
-//   k_finish: reward10 update, outputs, dropout advance; finished episodes reset their RL state and join the
-//             restart list (wave ballot + one atomic per wave)
+//   4 x k_emu_w: one emulated frame of every console and its picture into obs slot f - drawn by the same waves
+//     (emu_kernel.h, kDraw), or for frames 0-2 of a one-game env of one round of waves by k_render on a render
+//     stream from a frame bank (kBank); the last frame's waves also do the finish (finish_env: reward10 update,
+//     outputs, dropout advance; finished episodes reset their RL state and join the restart list)
 //   k_reset_copy: boot snapshot (or idle template) -> console record, one workgroup per listed console
 //   4 x (k_emu_w, k_render) over the restart list only (neutral frames of the new episode)
 //   k_reset_finish: first tracker update of new episodes; masks and dropout timeline of every env
@@ -110,65 +111,6 @@ struct FinishArgs {
     int e0, e1;
 };
 
-__device__ __forceinline__ uint64_t ram_hash(const uint8_t* ram) {
-    const uint4* w = reinterpret_cast<const uint4*>(ram);
-    uint64_t h = 0;
-    for (uint32_t k = 0; k < 128u; ++k) {
-        const uint4 q = w[k];
-        h += ev::mix64(((uint64_t)(4u * k) << 32) | q.x);
-        h += ev::mix64(((uint64_t)(4u * k + 1u) << 32) | q.y);
-        h += ev::mix64(((uint64_t)(4u * k + 2u) << 32) | q.z);
-        h += ev::mix64(((uint64_t)(4u * k + 3u) << 32) | q.w);
-    }
-    return h;
-}
-
-// RL part of the restart (rl/csrc/rlenv_core.cuh:208-263 without the record copy, which k_reset_copy does).
-__device__ __forceinline__ void reset_rl(const GameK& g, const EnvArrays& e, const Settings& s, int ge) {
-    const uint32_t ep = ++e.episode[ge];
-    const uint64_t seed = ev::ep_seed(s.run_seed, (uint32_t)ge, ep);
-    const uint64_t sseed = ev::mix64(seed ^ 0x5717C4A55EEDull);
-    uint64_t ctr = 0;
-    int idle = 0;
-    if (s.idle_max > 0) idle = (int)ev::rnd_below(sseed, ctr, (uint32_t)(s.idle_max + 1));
-    // a level start? (rl/csrc/rlenv_core.cuh:220-236: drawn only when level starts are on, after the idle count)
-    int lv = -1;
-    const LevelK& L = g.lv;
-    if (L.cap > 0 && L.thresh != 0 && ev::rnd32(sseed, ctr) < L.thresh) {
-        uint32_t saved = 0;
-        for (int q = 0; q < L.cap; ++q) saved += L.deaths[q] >= 0 ? 1u : 0u;
-        if (L.weighted) {
-            const uint32_t u = ev::rnd32(sseed, ctr);
-            for (int q = 0; q < L.cap && lv < 0; ++q)
-                if (u < L.cdf[q]) lv = q;
-        } else if (saved > 0) {
-            uint32_t pick = ev::rnd_below(sseed, ctr, saved);
-            for (int q = 0; q < L.cap && lv < 0; ++q)
-                if (L.deaths[q] >= 0 && pick-- == 0) lv = q;
-        }
-    }
-    e.sticky_seed[ge] = sseed;
-    e.sticky_ctr[ge] = ctr;
-    if (lv >= 0) {
-        e.target[ge] = L.target[lv];
-        e.ep_frame[ge] = L.frame[lv];
-        e.st[ge] = L.st[lv].st;
-        e.rd[ge] = L.st[lv].rd;
-    } else {
-        const int k = idle <= s.idle_tmpl ? idle : 0;
-        e.target[ge] = g.tmpl_target + (uint64_t)k * NES_FRAME_DOTS;
-        e.ep_frame[ge] = (uint32_t)k;
-        e.st[ge] = Rl10State{};
-        e.rd[ge] = Rl10Reader{};   // the reader and its key set restart too (rl/csrc/reward10.cuh:531-532)
-    }
-    if (e.ep_start) e.ep_start[ge] = lv;
-    e.fault[ge] = 0;
-    ev::drop_reset(e.drop[ge], seed, s.dropout != 0, s.gap_p32);   // in place: a local copy of the ring spills
-    e.prev_applied[ge] = 0;
-    e.ep_idle[ge] = idle;
-    e.resetting[ge] = 1;
-}
-
 __device__ __forceinline__ void list_append(const GameK& g, bool want, int e) {
     // one atomic per wavefront: the lanes that restart take consecutive list entries
     const uint64_t b = __ballot(want);
@@ -179,69 +121,6 @@ __device__ __forceinline__ void list_append(const GameK& g, bool want, int e) {
     if (lane == leader) base = atomicAdd(g.list_count, (uint32_t)__popcll(b));
     base = __shfl(base, leader);
     if (want) g.list[base + (uint32_t)__popcll(b & ((1ull << lane) - 1ull))] = e;
-}
-
-__global__ __launch_bounds__(256) void k_finish(FinishArgs a) {
-    const int k = (int)(blockIdx.x * blockDim.x + threadIdx.x);
-    const bool valid = k < a.e1 - a.e0;
-    const int e = a.e0 + (valid ? k : 0);
-    const int ge = a.g.offset + e;
-    bool restart = false;
-    if (valid) {
-        const NesRec* rec = &a.g.recs[e];
-        if (a.o.ram_hash) a.o.ram_hash[ge] = ram_hash(rec->ram);
-        Rl10State st = a.e.st[ge];
-        const ev::Out u = ev::observe_update(a.g.game, rec->ram, RLE_FRAMES, st, &a.e.rd[ge],
-                                             a.g.keys + (size_t)e * a.g.kcap, a.g.kcap);
-        a.e.st[ge] = st;
-        const bool faulted = a.e.fault[ge] != 0;
-        const bool level_clear = !u.done && !faulted && a.s.episode_level_end >= 0 && (u.events & ev::EV_LEVEL) &&
-                                 u.event_level == a.s.episode_level_end + 1;
-        bool synthetic = false;
-        if (a.s.end_p32 != 0 && !u.done && !faulted && !level_clear) {
-            uint64_t ctr = (uint64_t)(uint32_t)a.e.ep_len[ge];
-            const uint64_t es = ev::mix64(ev::ep_seed(a.s.run_seed, (uint32_t)ge, a.e.episode[ge]) ^ 0xE9D5EEDull);
-            synthetic = ev::rnd32(es, ctr) < a.s.end_p32;
-        }
-        const bool done = u.done || faulted || level_clear || synthetic;
-        const float r = faulted ? 0.0f : (float)u.reward;
-        a.o.reward[ge] = r;
-        if (a.o.parts)
-            for (int q = 0; q < RLE_PARTS; ++q) a.o.parts[(size_t)ge * RLE_PARTS + q] = faulted ? 0.0f : (float)u.part[q];
-        a.o.done[ge] = done ? 1 : 0;
-        a.o.events[ge] = u.events;
-        const float ret = a.e.ep_ret[ge] + r;
-        a.e.ep_ret[ge] = ret;
-        const int32_t len = a.e.ep_len[ge] + 1;
-        a.e.ep_len[ge] = len;
-        if (u.event_level > a.e.ep_maxlvl[ge]) a.e.ep_maxlvl[ge] = u.event_level;
-        ev::drop_advance(a.e.drop[ge], a.s.dropout != 0, a.s.gap_p32);   // in place (no local copy of the ring)
-        // level-start claim: the arrival with the fewest deaths, then the lowest env index (rlenv_core.cuh:288-291)
-        if (a.g.lv.cap > 0 && !done && (u.events & ev::EV_LEVEL) && u.event_level >= 0 && u.event_level < a.g.lv.levels) {
-            const unsigned long long dd = (unsigned long long)(uint32_t)(st.deaths < 0 ? 0 : st.deaths);
-            atomicMin(&a.g.lv.claim[u.event_level], (dd << 32) | (uint32_t)e);
-        }
-        if (a.o.level_out) a.o.level_out[ge] = st.has_best_level ? st.best_level : -1;
-        if (a.o.progress_out)
-            a.o.progress_out[ge] = st.has_prev && st.prev.progress_valid ? (float)(st.prev.progress / rl10_game(a.g.game).progress_unit)
-                                                                          : __builtin_nanf("");
-        if (done) {
-            if (a.o.start_out) a.o.start_out[ge] = a.e.ep_start ? a.e.ep_start[ge] : -1;
-            float* inf = a.o.info + (size_t)ge * RLE_INFO;
-            inf[0] = ret;
-            inf[1] = (float)len;
-            inf[2] = (float)(faulted ? RLE_END_FAULT : level_clear ? RLE_END_LEVEL_CLEAR
-                                                                   : synthetic ? RLE_END_SYNTHETIC : st.end_reason);
-            inf[3] = (float)st.deaths;
-            inf[4] = (float)a.e.ep_maxlvl[ge];
-            inf[5] = st.overflow ? 1.0f : 0.0f;
-            inf[6] = (float)a.e.ep_idle[ge];
-            inf[7] = (float)a.e.episode[ge];
-            reset_rl(a.g, a.e, a.s, ge);
-            restart = true;
-        }
-    }
-    list_append(a.g, restart, e);
 }
 
 // Start: every env of the range restarts (rl/csrc/rlenv_core.cuh:400-404).
@@ -949,11 +828,11 @@ FinishArgs finish_args(const Env& env, const GameK& g, int e0, int e1, const Out
 }
 
 // bank >= 0: a decision frame whose picture is drawn from frame bank `bank`; draw: a decision frame the emulator's
-// waves draw themselves.
+// waves draw themselves, and with finish the decision's last, whose waves also do the finish.
 void launch_emu(const Env& env, const GameK& g, const Outs& o, int mode, int f, bool use_list, int e0, int e1,
-                hipStream_t st, int bank = -1, bool draw = false) {
+                hipStream_t st, int bank = -1, bool draw = false, bool finish = false) {
     EmuArgs a{g, env.e, o, env.s, env.optab, mode, f, use_list ? 1 : 0, e0, e1, 0, 0, nullptr, env.budget,
-              bank >= 0 ? g.bank[bank] : nullptr, bank >= 0 ? g.bank_chr[bank] : nullptr};
+              bank >= 0 ? g.bank[bank] : nullptr, bank >= 0 ? g.bank_chr[bank] : nullptr, finish ? 1 : 0};
     const int blocks = use_list ? g.n : e1 - e0;
     const int cls = mode == EMU_DECISION ? KC_EMU : mode == EMU_IDLE ? KC_EMU_IDLE : KC_EMU_RESTART;
     // decision frames of a fixed-PRG cart run its translated kernel once that is compiled and loaded, when it was
@@ -1040,8 +919,8 @@ void decision_phases(const Env& env, const GameK& g, const RenderPipe& p, const 
     const bool draw = !env.s.no_render;
     const bool pipelined = draw && env.games.size() == 1 && n <= env.one_round;
     for (int f = 0; f < RLE_FRAMES; ++f) {
-        if (!pipelined || f == RLE_FRAMES - 1) {   // emulated and drawn by the same waves
-            launch_emu(env, g, o, EMU_DECISION, f, false, e0, e1, st, -1, true);
+        if (!pipelined || f == RLE_FRAMES - 1) {   // emulated and drawn by the same waves; the last one finishes too
+            launch_emu(env, g, o, EMU_DECISION, f, false, e0, e1, st, -1, true, f == RLE_FRAMES - 1);
             continue;
         }
         launch_emu(env, g, o, EMU_DECISION, f, false, e0, e1, st, f);
@@ -1050,9 +929,7 @@ void decision_phases(const Env& env, const GameK& g, const RenderPipe& p, const 
         launch_render(env, g, o, f, false, false, e0, e1, p.stream, f);
     }
     if (pipelined) (void)hipEventRecord(p.drawn, p.stream);
-    const FinishArgs fa = finish_args(env, g, e0, e1, o);
-    env.clock.run(KC_FINISH, st, [&] { hipLaunchKernelGGL(k_finish, dim3((n + 255) / 256), dim3(256), 0, st, fa); });
-    trace("finish", st);
+    const FinishArgs fa = finish_args(env, g, e0, e1, o);   // (the finish itself ran in the last frame's waves)
     if (g.lv.cap > 0) {   // level-start saves, before any restart (restarts read the saves of earlier decisions)
         env.clock.run(KC_ARCHIVE, st,
                       [&] { hipLaunchKernelGGL(k_archive, dim3(g.lv.levels), dim3(256), 0, st, fa); });
