@@ -157,9 +157,18 @@ inline JitProgram jit_translate_fixed(const std::vector<uint8_t>& prg) {
         const Block& b = *kept[i];
         const uint32_t last = b.ins.back(), grp = grp_of(last), mode = kOptab.t[rd(last)] & 15u;
         std::string end;
+        bool branch_end = false;
         if (grp == G_BR) {
-            snprintf(buf, sizeof buf, "if (h.pc == 0x%Xu) ", (target_of(last) & 0x1FFFFu) << 3);
-            end = buf + go(b.start, target_of(last)) + " " + go(b.start, b.stop);
+            // the block's branch itself: taken or not, each with its cycle count and next pc as constants (pc and
+            // target times 8, a page crossing when they differ in bits 8-15; fx's own arithmetic)
+            const uint32_t tgt = (target_of(last) & 0x1FFFFu) << 3, nxt = (last + 2u) << 3;
+            const uint32_t cyc = (kOptab.t[rd(last)] >> 4) & 15u, cross = ((nxt ^ tgt) & (0xFF00u << 3)) ? 1u : 0u;
+            snprintf(buf, sizeof buf, "if (br_taken<kOptab.t[0x%02Xu]>(h)) { v -= 0x%Xu; h.pc = 0x%Xu; ", rd(last),
+                     ((cyc + 1u + cross) << 14) - 1u, tgt);
+            end = buf + go(b.start, target_of(last));
+            snprintf(buf, sizeof buf, " } v -= 0x%Xu; h.pc = 0x%Xu; ", (cyc << 14) - 1u, nxt);
+            end += buf + go(b.start, b.stop);
+            branch_end = true;
         } else if (grp == G_JMP || grp == G_JSR) {
             end = mode == M_ABS ? go(b.start, rd16(last + 1u)) : std::string("continue;");
         } else if (grp == G_RTS || grp == G_RTI) {
@@ -178,7 +187,8 @@ inline JitProgram jit_translate_fixed(const std::vector<uint8_t>& prg) {
         snprintf(buf, sizeof buf, ") { JIT_ONE(0x%02Xu, 0x%Xu, 0x%Xu) }\n", rd(b.start), b.start << 3,
                  operand(b.start));
         p.cases += "    if (v < " + mx + buf;
-        for (uint32_t x : b.ins) {
+        for (size_t j = 0; j + (branch_end ? 1u : 0u) < b.ins.size(); ++j) {
+            const uint32_t x = b.ins[j];
             snprintf(buf, sizeof buf, "    JIT_STEP(0x%02Xu, 0x%Xu, 0x%Xu)\n", rd(x), x << 3, operand(x));
             p.cases += buf;
         }
@@ -303,11 +313,23 @@ inline JitProgram jit_translate_banked(const std::vector<uint8_t>& prg) {
         const Block& b = kept[i];
         const uint32_t last = b.ins.back(), grp = grp_of(last);
         std::string end;
+        bool branch_end = false;
         if (grp == G_BR) {
-            // (taken to another page, the branch leaves the block as needing the generic step)
+            // taken to another page, the branch leaves the block as needing the generic step (its JIT_STEP); on its
+            // page, taken or not each with its cycle count and next pc as constants, as in the fixed translation
             const uint32_t tgt = target_of(last);
-            snprintf(buf, sizeof buf, "if (h.pc == 0x%Xu) ", (tgt << 3));
-            end = same_page(last, tgt) ? buf + go(b.start, tgt) + " " + go(b.start, b.stop) : go(b.start, b.stop);
+            if (same_page(last, tgt)) {
+                const uint32_t cyc = (kOptab.t[rd(last)] >> 4) & 15u;
+                const uint32_t cross = (((last + 2u) ^ tgt) & 0xFF00u) ? 1u : 0u;
+                snprintf(buf, sizeof buf, "if (br_taken<kOptab.t[0x%02Xu]>(h)) { v -= 0x%Xu; h.pc = 0x%Xu; ", rd(last),
+                         ((cyc + 1u + cross) << 14) - 1u, tgt << 3);
+                end = buf + go(b.start, tgt);
+                snprintf(buf, sizeof buf, " } v -= 0x%Xu; h.pc = 0x%Xu; ", (cyc << 14) - 1u, (last + 2u) << 3);
+                end += buf + go(b.start, b.stop);
+                branch_end = true;
+            } else {
+                end = go(b.start, b.stop);
+            }
         } else if (grp == G_JMP || grp == G_JSR || grp == G_RTS || grp == G_RTI) {
             end = "continue;";
         } else {
@@ -324,7 +346,8 @@ inline JitProgram jit_translate_banked(const std::vector<uint8_t>& prg) {
         snprintf(buf, sizeof buf, ") { JIT_ONE(0x%02Xu, 0x%Xu, 0x%Xu) }\n", rd(b.start), b.start << 3,
                  operand(b.start));
         p.cases += "    if (v < " + mx + buf;
-        for (uint32_t x : b.ins) {
+        for (size_t j = 0; j + (branch_end ? 1u : 0u) < b.ins.size(); ++j) {
+            const uint32_t x = b.ins[j];
             snprintf(buf, sizeof buf, "    JIT_STEP(0x%02Xu, 0x%Xu, 0x%Xu)\n", rd(x), x << 3, operand(x));
             p.cases += buf;
         }

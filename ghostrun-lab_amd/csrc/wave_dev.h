@@ -181,6 +181,18 @@ constexpr uint32_t kGeneric = 0xFFFFFFFFu;
 // branch's target times 8 (NROM) or its sign-extended offset times 8 (banked boards); JMP's and JSR's target (times 8
 // on NROM);
 // else lo | hi << 8. HOT: a hot key (a branch that stays on its page).
+// Whether the conditional branch of descriptor D is taken: its flag (N and Z from the lazy nz, the others from p) has
+// the value the branch tests for.
+template <uint32_t D>
+__device__ __forceinline__ bool br_taken(const Hot& h) {
+    constexpr uint32_t sub = (D >> 12) & 15u, bit = sub & 7u;
+    bool set;
+    if constexpr (bit == 7u) set = h.nz >= 0x80u;
+    else if constexpr (bit == 1u) set = (h.nz & 0xFFu) == 0u;
+    else set = ((h.p >> bit) & 1u) != 0;
+    return set == ((sub & 8u) != 0);
+}
+
 template <uint32_t B, uint32_t D, bool HOT = false>
 __device__ __forceinline__ uint32_t fx(Hot& h, const Mem& m, Con& cs, uint32_t pcs, uint32_t base) {
     constexpr uint32_t PS = kPcShift;
@@ -296,12 +308,7 @@ __device__ __forceinline__ uint32_t fx(Hot& h, const Mem& m, Con& cs, uint32_t p
             hset(h, dst, res);
             hnz(h, res);
         } else if constexpr (grp == G_BR) {
-            constexpr uint32_t bit = sub & 7u;
-            bool set;
-            if constexpr (bit == 7u) set = h.nz >= 0x80u;
-            else if constexpr (bit == 1u) set = (h.nz & 0xFFu) == 0u;
-            else set = ((h.p >> bit) & 1u) != 0;
-            if (set == ((sub & 8u) != 0)) {
+            if (br_taken<D>(h)) {
                 const uint32_t tgt = nrom ? base : npc + base;   // wrapped when stored
                 if constexpr (!nrom && !HOT) {
                     if ((npc ^ tgt) >> 16) return kGeneric;   // to another 8 KB page: bits 13+ of the PRG offset
