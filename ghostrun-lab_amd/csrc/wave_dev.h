@@ -36,6 +36,7 @@ typedef __attribute__((address_space(4))) const uint8_t ConstU8;
 // the reload after the generic step, which is the only place the PRG mapping changes.
 struct Hot {
     uint32_t pc, a, x, y, sp, p, nz;
+    uint32_t ctl;   // controller 1: shift register | strobe << 8
     uint64_t cycles;
     uint32_t prg0, prg1, prg2, prg3;
     uint32_t pd;
@@ -88,12 +89,15 @@ __device__ __forceinline__ void hot_load(Hot& h, const Con& c) {
     h.prg0 = uni(c.prg0); h.prg1 = uni(c.prg1); h.prg2 = uni(c.prg2); h.prg3 = uni(c.prg3);
     h.pd = 0;
     h.pc = hot_pcs<B>(h, uni(c.pc));
+    h.ctl = uni(c.shift) | (uni(c.strobe) << 8);
 }
 // (the PRG offsets change only in the generic step, which writes them to the console state itself)
 template <uint32_t B>
 __device__ __forceinline__ void hot_store(const Hot& h, Con& c) {
     c.pc = hot_cpu<B>(h, h.pc) & 0xFFFFu; c.a = h.a; c.x = h.x; c.y = h.y; c.sp = h.sp; c.p = hflags(h);
     c.cycles = h.cycles;
+    c.shift = h.ctl & 0xFFu;
+    c.strobe = h.ctl >> 8;
 }
 
 __device__ __forceinline__ uint32_t hget(const Hot& h, uint32_t code, uint32_t opd) {
@@ -125,14 +129,13 @@ __device__ __forceinline__ uint32_t hpull(Hot& h, const Mem& m) {
 
 // Controller port 1 ($4016), one of the two I/O registers the fast path serves itself: the same read and write as
 // the bus (nes_dev.h io_read / io_write), on the console state in LDS.
-__device__ __forceinline__ uint32_t port_read(Con& cs) {
+__device__ __forceinline__ uint32_t port_read(Hot& h, const Con& cs) {
     uint32_t bit;
-    if (uni(cs.strobe)) {
+    if (h.ctl >> 8) {
         bit = uni(cs.pad) & 1u;
     } else {
-        const uint32_t s = uni(cs.shift);
-        bit = s & 1u;
-        cs.shift = (s >> 1) | 0x80u;
+        bit = h.ctl & 1u;
+        h.ctl = (h.ctl >> 1) | 0x80u;
     }
     return 0x40u | bit;
 }
@@ -147,9 +150,8 @@ __device__ __forceinline__ uint32_t status_read(Con& cs) {
     cs.open_bus = v;
     return v;
 }
-__device__ __forceinline__ void port_write(Con& cs, uint32_t v) {
-    cs.strobe = v & 1u;
-    if (v & 1u) cs.shift = uni(cs.pad);
+__device__ __forceinline__ void port_write(Hot& h, const Con& cs, uint32_t v) {
+    h.ctl = (v & 1u) ? (uni(cs.pad) | 0x100u) : (h.ctl & 0xFFu);
 }
 
 // Byte offset in the PRG image of CPU address `addr` ($8000-$FFFF). NROM maps the image linearly (mirrored).
@@ -260,7 +262,7 @@ __device__ __forceinline__ uint32_t fx(Hot& h, const Mem& m, Con& cs, uint32_t p
             } else {
                 if (ea < 0x2000u) opd = rd8(m, ea & 0x7FFu);
                 else if (ea >= 0x8000u) opd = prg_wide(m, prg_index<B>(h, m, ea)) & 0xFFu;
-                else if (ea == 0x4016u) opd = port_read(cs);
+                else if (ea == 0x4016u) opd = port_read(h, cs);
                 else if ((ea & 0xE007u) == 0x2002u) opd = status_read(cs);
                 else if (ea >= 0x6000u && m.cart.board != NES_BOARD_MMC1) opd = prg_ram_read(m, ea);
                 else return kGeneric;
@@ -369,7 +371,7 @@ __device__ __forceinline__ uint32_t fx(Hot& h, const Mem& m, Con& cs, uint32_t p
             else if constexpr (zpage) m.ram[ea & 0x7FFu] = (uint8_t)res;
             else if (ea < 0x2000u) m.ram[ea & 0x7FFu] = (uint8_t)res;
             else if (ea >= 0x6000u) m.rec->prg_ram[ea - 0x6000u] = (uint8_t)res;   // (a read-modify-write: here)
-            else port_write(cs, res);
+            else port_write(h, cs, res);
         }
         h.pc = npc;
         return (cyc << 14) - 1u;   // the caller adds the cycles and services the DMC, as cpu_step does after its count
