@@ -36,6 +36,7 @@ typedef __attribute__((address_space(4))) const uint8_t ConstU8;
 // the reload after the generic step, which is the only place the PRG mapping changes.
 struct Hot {
     uint32_t pc, a, x, y, sp, p, nz;
+    uint32_t c, v;  // the carry (0 or 1) and V in bit 7 (lazy, as N and Z in nz); p's own C and V bits are stale
     uint32_t ctl;   // controller 1: shift register | strobe << 8
     uint64_t cycles;
     uint32_t prg0, prg1, prg2, prg3;
@@ -54,9 +55,15 @@ __device__ __forceinline__ uint32_t nz_of_p(uint32_t p) {
     return ((p & FL_N) << 1) | ((p & FL_Z) ? 0u : 1u);
 }
 
-// p with N and Z rebuilt from the lazy value.
+// p with N, Z, C and V rebuilt from the values kept apart.
 __device__ __forceinline__ uint32_t hflags(const Hot& h) {
-    return (h.p & ~(FL_N | FL_Z)) | (h.nz >= 0x80u ? FL_N : 0u) | ((h.nz & 0xFFu) ? 0u : FL_Z);
+    return (h.p & ~(FL_N | FL_Z | FL_C | FL_V)) | (h.nz >= 0x80u ? FL_N : 0u) | ((h.nz & 0xFFu) ? 0u : FL_Z) | h.c |
+           ((h.v >> 1) & FL_V);
+}
+// C and V kept apart from a status byte p.
+__device__ __forceinline__ void hcv(Hot& h, uint32_t p) {
+    h.c = p & FL_C;
+    h.v = (p & FL_V) << 1;
 }
 
 // pcs of CPU address `pc` (on the banked boards also pd, from the PRG offsets in h).
@@ -85,6 +92,7 @@ template <uint32_t B>
 __device__ __forceinline__ void hot_load(Hot& h, const Con& c) {
     h.a = uni(c.a); h.x = uni(c.x); h.y = uni(c.y); h.sp = uni(c.sp); h.p = uni(c.p);
     h.nz = nz_of_p(h.p);
+    hcv(h, h.p);
     h.cycles = uni64(c.cycles);
     h.prg0 = uni(c.prg0); h.prg1 = uni(c.prg1); h.prg2 = uni(c.prg2); h.prg3 = uni(c.prg3);
     h.pd = 0;
@@ -191,6 +199,8 @@ __device__ __forceinline__ bool br_taken(const Hot& h) {
     bool set;
     if constexpr (bit == 7u) set = h.nz >= 0x80u;
     else if constexpr (bit == 1u) set = (h.nz & 0xFFu) == 0u;
+    else if constexpr (bit == 0u) set = h.c != 0u;
+    else if constexpr (bit == 6u) set = (h.v & 0x80u) != 0u;
     else set = ((h.p >> bit) & 1u) != 0;
     return set == ((sub & 8u) != 0);
 }
@@ -286,27 +296,27 @@ __device__ __forceinline__ uint32_t fx(Hot& h, const Mem& m, Con& cs, uint32_t p
                 hnz(h, h.a);
             } else if constexpr (sub <= 4) {
                 const uint32_t mv = sub == 4 ? (opd ^ 0xFFu) : opd;
-                const uint32_t sum = h.a + mv + (h.p & FL_C);
-                const uint32_t ov = (~(h.a ^ mv) & (h.a ^ sum) & 0x80u) ? FL_V : 0u;
-                h.p = (h.p & ~(FL_C | FL_V)) | (sum >> 8) | ov;
+                const uint32_t sum = h.a + mv + h.c;
+                h.v = ~(h.a ^ mv) & (h.a ^ sum);   // bit 7: the signed overflow
+                h.c = sum >> 8;
                 h.a = sum & 0xFFu;
                 hnz(h, h.a);
             } else if constexpr (sub == 5) {
                 const uint32_t r = hget(h, src, 0);
-                h.p = (h.p & ~FL_C) | (r >= opd ? FL_C : 0u);
+                h.c = r >= opd ? 1u : 0u;
                 hnz(h, (r - opd) & 0xFFu);
             } else {
-                h.p = (h.p & ~FL_V) | (opd & FL_V);
+                h.v = opd << 1;                               // V from the operand's bit 6
                 h.nz = (h.a & opd) | ((opd & 0x80u) << 1);   // N from the operand, Z from A & operand
             }
         } else if constexpr (grp == G_SHIFT) {
-            const uint32_t in = hget(h, src, opd), cin = h.p & FL_C;
+            const uint32_t in = hget(h, src, opd), cin = h.c;
             uint32_t cout;
             if constexpr (sub == 0) { res = (in << 1) & 0xFFu; cout = in >> 7; }
             else if constexpr (sub == 1) { res = in >> 1; cout = in & 1u; }
             else if constexpr (sub == 2) { res = ((in << 1) | cin) & 0xFFu; cout = in >> 7; }
             else { res = (in >> 1) | (cin << 7); cout = in & 1u; }
-            h.p = (h.p & ~FL_C) | cout;
+            h.c = cout;
             hset(h, dst, res);
             hnz(h, res);
         } else if constexpr (grp == G_BR) {
@@ -320,8 +330,10 @@ __device__ __forceinline__ uint32_t fx(Hot& h, const Mem& m, Con& cs, uint32_t p
                 npc = tgt;
             }
         } else if constexpr (grp == G_FLAG) {
-            constexpr uint32_t bitm = 1u << (sub & 7u);
-            h.p = (sub & 8u) ? (h.p | bitm) : (h.p & ~bitm);
+            constexpr uint32_t bit = sub & 7u, bitm = 1u << bit;
+            if constexpr (bit == 0u) h.c = (sub & 8u) ? 1u : 0u;
+            else if constexpr (bit == 6u) h.v = (sub & 8u) ? 0x80u : 0u;
+            else h.p = (sub & 8u) ? (h.p | bitm) : (h.p & ~bitm);
         } else if constexpr (grp == G_PUSH) {
             hpush(h, m, src == R_A ? h.a : (hflags(h) | FL_B | FL_U));
         } else if constexpr (grp == G_PULL) {
@@ -332,6 +344,7 @@ __device__ __forceinline__ uint32_t fx(Hot& h, const Mem& m, Con& cs, uint32_t p
             } else {
                 h.p = (v & ~FL_B) | FL_U;
                 h.nz = nz_of_p(h.p);
+                hcv(h, h.p);
             }
         } else if constexpr (grp == G_JMP) {
             if constexpr (mode == M_IND) {
@@ -363,6 +376,7 @@ __device__ __forceinline__ uint32_t fx(Hot& h, const Mem& m, Con& cs, uint32_t p
         } else if constexpr (grp == G_RTI) {
             h.p = (hpull(h, m) & ~FL_B) | FL_U;
             h.nz = nz_of_p(h.p);
+            hcv(h, h.p);
             const uint32_t l8 = hpull(h, m), h8 = hpull(h, m);
             npc = hot_pcs<B>(h, (h8 << 8) | l8);
         }
