@@ -398,8 +398,14 @@ __device__ __forceinline__ void emu_body(const EmuArgs& a) {
             if (finish) {   // the decision's finish (k_finish's work), in the waves of its last frame
                 const uint64_t h = a.o.ram_hash ? ram_hash_wave(L.ram, lane) : 0;
                 if (lane == 0) {
-                    if (a.o.ram_hash) a.o.ram_hash[ge] = h;
-                    if (finish_env(a, e, ge, rec->ram)) a.g.list[atomicAdd(a.g.list_count, 1u)] = e;
+                    // The finish's arguments are read here from the kernel-argument segment (every kernel that runs
+                    // emu_body takes its EmuArgs as its only parameter, so they start the segment), through an
+                    // address the compiler cannot see through: read from `a`, they are loaded at the kernel's start
+                    // and held through the emulation, and the translated kernels then spill to scratch.
+                    const EmuArgs* fa = (const EmuArgs*)__builtin_amdgcn_kernarg_segment_ptr();
+                    asm volatile("" : "+s"(fa));
+                    if (fa->o.ram_hash) fa->o.ram_hash[ge] = h;
+                    if (finish_env(*fa, e, ge, rec->ram)) fa->g.list[atomicAdd(fa->g.list_count, 1u)] = e;
                 }
                 __syncthreads();   // (the hash has read the RAM before the scratch overwrites it)
             }

@@ -60,6 +60,29 @@ inline bool jit_always_generic(uint32_t a, uint32_t op, uint32_t b1, uint32_t b2
     return false;
 }
 
+// The most a fast instruction of opcode op takes off the burst counter (wave_dev.h jit_maxtake).
+inline uint32_t jit_take_max(uint32_t op) {
+    const uint32_t d = kOptab.t[op];
+    return ((((d >> 4) & 15u) + ((d & D_PEN) ? 1u : 0u) + (((d >> 8) & 15u) == G_BR ? 2u : 0u)) << 14) - 1u;
+}
+
+// A status poll: a block of two instructions, a read of $2002 (BIT, LDA, LDX or LDY absolute, at any mirror) and a
+// branch on bit 7 or 6 of the flags (BPL, BMI, BVC, BVS) back to the read. The status changes only at PPU events,
+// which a burst stops short of, and a read after the first leaves the console as it found it (the vblank flag and
+// the write toggle already clear, the open bus the same), so within a burst the iterations after the first are
+// alike: the translation takes as many of them at once as the burst's room allows. The counter then stands where
+// iterating would leave it (below the block's room), and the block goes on as before.
+inline std::string jit_poll_skip(uint32_t op0, uint32_t addr, uint32_t op1, bool to_self, uint32_t cyc_taken) {
+    const bool poll = to_self && (op0 == 0x2Cu || op0 == 0xADu || op0 == 0xAEu || op0 == 0xACu) &&
+                      (addr & 0xE007u) == 0x2002u && (op1 == 0x10u || op1 == 0x30u || op1 == 0x50u || op1 == 0x70u);
+    if (!poll) return std::string();
+    const uint32_t room = jit_take_max(op0) + jit_take_max(op1);
+    const uint32_t iter = ((((kOptab.t[op0] >> 4) & 15u) + cyc_taken) << 14) - 2u;   // two instructions
+    char buf[160];
+    snprintf(buf, sizeof buf, "if (v >= 0x%Xu) v -= ((v - 0x%Xu) / 0x%Xu + 1u) * 0x%Xu; ", room, room, iter, iter);
+    return buf;
+}
+
 // The blocks of a fixed PRG image: the CPU sees byte prg[a & (size - 1)] at $8000-$FFFF (size 16 or 32 KB).
 inline JitProgram jit_translate_fixed(const std::vector<uint8_t>& prg) {
     const uint32_t mask = (uint32_t)prg.size() - 1u;
@@ -165,7 +188,10 @@ inline JitProgram jit_translate_fixed(const std::vector<uint8_t>& prg) {
             const uint32_t cyc = (kOptab.t[rd(last)] >> 4) & 15u, cross = ((nxt ^ tgt) & (0xFF00u << 3)) ? 1u : 0u;
             snprintf(buf, sizeof buf, "if (br_taken<kOptab.t[0x%02Xu]>(h)) { v -= 0x%Xu; h.pc = 0x%Xu; ", rd(last),
                      ((cyc + 1u + cross) << 14) - 1u, tgt);
-            end = buf + go(b.start, target_of(last));
+            const std::string skip = b.ins.size() == 2u ? jit_poll_skip(rd(b.start), rd16(b.start + 1u), rd(last),
+                                                                         target_of(last) == b.start, cyc + 1u + cross)
+                                                        : std::string();
+            end = buf + skip + go(b.start, target_of(last));
             snprintf(buf, sizeof buf, " } v -= 0x%Xu; h.pc = 0x%Xu; ", (cyc << 14) - 1u, nxt);
             end += buf + go(b.start, b.stop);
             branch_end = true;
@@ -323,7 +349,10 @@ inline JitProgram jit_translate_banked(const std::vector<uint8_t>& prg) {
                 const uint32_t cross = (((last + 2u) ^ tgt) & 0xFF00u) ? 1u : 0u;
                 snprintf(buf, sizeof buf, "if (br_taken<kOptab.t[0x%02Xu]>(h)) { v -= 0x%Xu; h.pc = 0x%Xu; ", rd(last),
                          ((cyc + 1u + cross) << 14) - 1u, tgt << 3);
-                end = buf + go(b.start, tgt);
+                const std::string skip = b.ins.size() == 2u ? jit_poll_skip(rd(b.start), rd16(b.start + 1u), rd(last),
+                                                                             tgt == b.start, cyc + 1u + cross)
+                                                            : std::string();
+                end = buf + skip + go(b.start, tgt);
                 snprintf(buf, sizeof buf, " } v -= 0x%Xu; h.pc = 0x%Xu; ", (cyc << 14) - 1u, (last + 2u) << 3);
                 end += buf + go(b.start, b.stop);
                 branch_end = true;

@@ -13,6 +13,8 @@ cartridges generated here from a seed:
   lives, score, dying, mode) from the pad, idling in a JMP-to-self loop with its logic in the NMI as SMB does,
   so rewards, deaths, level changes, game over and the idle fast-forward all run.
 * ``dmc_cart(seed)`` - NROM-128 playing DMC samples (rate and loop changes, starts, stops, status polls).
+* ``poll_cart(seed)`` - NROM-128 with NMI off that polls instead: its main loop waits for vblank on $2002 bit 7,
+  does the vblank work, waits for the sprite-0 flag to clear and then to be set (bit 6) and splits the scroll.
 * ``fault_cart(nmis)`` - NROM-128 that hits an unofficial opcode after `nmis` frames (the emulator-fault end).
 * ``mmc2_cart(seed)`` - MMC2 (mapper 9): 128 KB PRG in 8 KB banks, 128 KB CHR ROM, nametables and sprites rich in
   the latch tiles $FD/$FE, CHR bank and mirroring rewrites, CPU-driven latch flips through $2006/$2007.
@@ -282,6 +284,56 @@ def nrom_cart(seed: int = 0, blocks: int = 24) -> bytes:
     a.label('nmi')
     _nmi_common(a)
     _nmi_end(a)
+    a.label('irq')
+    a.op('RTI')
+    for name, t in (('t_pal', pal), ('t_nt', nt), ('t_oam', oam), ('t_mix', mix)):
+        a.label(name)
+        a.data(bytes(int(v) for v in t))
+    code = a.assemble()
+    assert len(code) <= 0x3FFA, len(code)
+    prg = bytearray(16384)
+    prg[:len(code)] = code
+    vec = (a.labels['nmi'], a.labels['reset'], a.labels['irq'])
+    prg[0x3FFA:0x4000] = bytes(sum(((v & 0xFF, v >> 8) for v in vec), ()))
+    chr_ = rng.integers(0, 256, 8192, dtype=np.uint8).tobytes()
+    return ines(bytes(prg), chr_, 0, vertical=True)
+
+
+def poll_cart(seed: int = 0, blocks: int = 12) -> bytes:
+    """NROM-128 cartridge with NMI off: every frame of its main loop waits for vblank with BIT $2002 / BPL, writes the
+    OAM (DMA), the sprite's position, four nametable bytes and the scroll, waits for the sprite-0 flag to clear (BIT /
+    BVS) and to be set again (BIT / BVC), splits the scroll there, then reads the pad and runs the filler blocks.
+    Sprite 0 sits over the random background at (x, 96), so its hit comes on every frame."""
+    rng = np.random.default_rng([0x504F4C4C, seed])
+    pal, nt, oam, mix = _tables(rng)
+    oam[0], oam[1], oam[2], oam[3] = 95, int(rng.integers(1, 256)), 0, int(rng.integers(16, 200))
+    a = Asm(0xC000)
+    tables = dict(pal='t_pal', nt='t_nt', oam='t_oam')
+    a.label('reset')
+    _reset_common(a, 0x10, tables)
+    a.label('main')
+    a.label('p_vb'); a.op('BIT', 'abs', 0x2002); a.op('BPL', 'rel', 'p_vb')
+    a.op('LDA', 'imm', 0); a.op('STA', 'abs', 0x2003); a.op('LDA', 'imm', OAM_PAGE >> 8); a.op('STA', 'abs', 0x4014)
+    a.op('LDA', 'zp', PY); a.op('STA', 'abs', OAM_PAGE + 4); a.op('LDA', 'zp', PX); a.op('STA', 'abs', OAM_PAGE + 7)
+    a.op('LDA', 'abs', 0x2002)
+    a.op('LDA', 'zp', NTP_HI); a.op('STA', 'abs', 0x2006); a.op('LDA', 'zp', NTP_LO); a.op('STA', 'abs', 0x2006)
+    for v in (CNT_LO, CNT_HI, ACNT, PAD):
+        a.op('LDA', 'zp', v); a.op('STA', 'abs', 0x2007)
+    a.op('LDA', 'zp', NTP_LO); a.op('CLC'); a.op('ADC', 'imm', 4); a.op('STA', 'zp', NTP_LO)
+    a.op('LDA', 'zp', NTP_HI); a.op('ADC', 'imm', 0); a.op('AND', 'imm', 0x03); a.op('ORA', 'imm', 0x20)
+    a.op('STA', 'zp', NTP_HI)
+    a.op('LDA', 'imm', 0); a.op('STA', 'abs', 0x2005); a.op('STA', 'abs', 0x2005)
+    a.op('LDA', 'zp', CTRL_SHADOW); a.op('STA', 'abs', 0x2000)
+    a.label('p_s0c'); a.op('BIT', 'abs', 0x2002); a.op('BVS', 'rel', 'p_s0c')
+    a.label('p_s0h'); a.op('BIT', 'abs', 0x2002); a.op('BVC', 'rel', 'p_s0h')
+    a.op('LDA', 'zp', PX); a.op('STA', 'abs', 0x2005); a.op('LDA', 'imm', 0); a.op('STA', 'abs', 0x2005)
+    a.op('INC', 'zp', FRAMES)
+    _read_pad(a, 'm')
+    _pad_moves(a, 't_mix')
+    _filler(a, rng, blocks, 'f', 't_mix')
+    a.op('JMP', 'abs', 'main')
+    a.label('nmi')
+    a.op('RTI')
     a.label('irq')
     a.op('RTI')
     for name, t in (('t_pal', pal), ('t_nt', nt), ('t_oam', oam), ('t_mix', mix)):

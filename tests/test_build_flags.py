@@ -68,8 +68,9 @@ def test_product_device_code_has_no_packed_fp32_and_no_scratch(tmp_path):
 
 @pytest.mark.skipif(not Path(HIPCC).exists(), reason='hipcc not installed')
 def test_translated_kernel_device_code_has_no_packed_fp32_and_no_scratch(tmp_path):
-    """The kernel the library compiles at run time from a cartridge's translated blocks (jit.h), here the blocks of
-    the benchmark cart (rl.synth.nrom_cart(1)) as rlenv_jit_translate writes them, built with the same flags."""
+    """The kernels the library compiles at run time from a cartridge's translated blocks (jit.h: frames drawn from
+    frame banks, and frames the emulator's waves draw themselves, with the decision's finish), here the blocks of the
+    benchmark cart (rl.synth.nrom_cart(1)) as rlenv_jit_translate writes them, built with the same flags."""
     import ctypes
     from rl import synth
     from rl.rlenv import bind_library
@@ -84,13 +85,15 @@ def test_translated_kernel_device_code_has_no_packed_fp32_and_no_scratch(tmp_pat
     src = tmp_path / 'jit.hip'
     src.write_text('#define RLENV_JIT_INC "jit_blocks.inc"\n#include "emu_kernel.h"\n'
                    'extern "C" __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(8, 8)))\n'
-                   'void k_emu_jit(nd::EmuArgs a) { nd::emu_body<NES_BOARD_NROM, true>(a); }\n')
+                   'void k_emu_jit(nd::EmuArgs a) { nd::emu_body<NES_BOARD_NROM, true, false>(a); }\n'
+                   'extern "C" __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(8, 8)))\n'
+                   'void k_emu_jit_draw(nd::EmuArgs a) { nd::emu_body<NES_BOARD_NROM, false, true>(a); }\n')
     flags = makefile_flags()
     remarks = []
     asm = device_asm(src, tmp_path / 'jit.s', [f'-I{ROOT / "include"}', f'-I{CSRC}', f'-I{tmp_path}'] +
                      [f for f in flags if not f.startswith('--offload-arch') and f != '-O3' and f != '-std=c++17'],
                      remarks)
-    assert 'k_emu_jit' in asm and not PACKED.search(asm)
+    assert 'k_emu_jit' in asm and 'k_emu_jit_draw' in asm and not PACKED.search(asm)
     scratch = [int(x) for x in re.findall(r'ScratchSize \[bytes/lane\]: (\d+)', remarks[0])]
     occupancy = [int(x) for x in re.findall(r'Occupancy \[waves/SIMD\]: (\d+)', remarks[0])]
-    assert scratch == [0] and occupancy == [8], (scratch, occupancy)
+    assert scratch == [0, 0] and occupancy == [8, 8], (scratch, occupancy)

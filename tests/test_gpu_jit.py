@@ -78,6 +78,18 @@ def test_translated_cnrom_bank_switches(conflicts):
 
 
 @pytest.mark.gpu
+def test_translated_status_polls():
+    """The poll cart (NMI off) waits every frame for vblank and for the sprite-0 flag to clear and to be set by polling
+    $2002; the translation takes each poll's repeated iterations within a burst at once (jit.h jit_poll_skip), and
+    the consoles, instruction counter and cycles included, must still equal the oracle's."""
+    print('case: translated poll cart seed 1, 16 consoles, raw pads, sticky, Geometric(1/8) ends, 20 decisions',
+          flush=True)
+    cpu, gpu, _ = translated_pair(16, synth.poll_cart(1), seed=53, sticky=True, idle_max=1, dropout=True,
+                                  pad_mode=True, end_prob=1 / 8)
+    run(cpu, gpu, 20, 53, True)
+
+
+@pytest.mark.gpu
 def test_translated_instruction_budget_exit():
     print('case: translated NROM seed 3, RLENV_BUDGET 3000, 8 consoles, 10 decisions', flush=True)
     os.environ['RLENV_BUDGET'] = '3000'

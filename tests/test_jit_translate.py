@@ -1,0 +1,59 @@
+"""The block translation (ghostrun-lab_amd/csrc/jit.h) as text, on the CPU: where it takes a status poll's repeated
+iterations at once, and that its closed form leaves the burst counter where iterating the block would."""
+import ctypes
+import re
+
+import pytest
+
+from helpers import HIP_LIB
+from rl import synth
+from rl.rlenv import bind_library
+
+SKIP = re.compile(r'if \(v >= 0x([0-9A-F]+)u\) v -= \(\(v - 0x([0-9A-F]+)u\) / 0x([0-9A-F]+)u \+ 1u\) \* 0x([0-9A-F]+)u;')
+
+
+def translate(rom):
+    lib = bind_library(HIP_LIB)
+    out = (ctypes.c_int32 * 4)()
+    text = ctypes.create_string_buffer(1 << 21)
+    assert lib.rlenv_jit_translate(rom, len(rom), 0, out, text, len(text)) == 0
+    return text.value.decode()
+
+
+def blocks(text):
+    return re.findall(r'case 0x[0-9A-F]+u: JB_\d+: \{ +// \$([0-9A-F]{4}), (\d+) instructions\n(.*?)\n\}', text, re.S)
+
+
+def test_status_polls_and_only_they_take_their_iterations_at_once():
+    """poll_cart polls $2002 twice at boot (BIT / BPL) and three times a frame (BIT / BPL, BIT / BVS, BIT / BVC); the
+    benchmark cart only at boot. Every block with the skip is a read of $2002 and a branch back to it, two
+    instructions; no other block has one."""
+    for rom, expect in ((synth.poll_cart(1), 5), (synth.nrom_cart(1), 2)):
+        text = translate(rom)
+        found = 0
+        for start, n, body in blocks(text):
+            if SKIP.search(body):
+                found += 1
+                steps = re.findall(r'JIT_STEP\(0x([0-9A-F]{2})u, 0x[0-9A-F]+u, 0x([0-9A-F]+)u\)', body)
+                assert n == '2' and len(steps) == 1, body
+                op, addr = int(steps[0][0], 16), int(steps[0][1], 16)
+                assert op in (0x2C, 0xAD, 0xAE, 0xAC) and addr & 0xE007 == 0x2002, body
+                taken = re.search(r'br_taken<kOptab\.t\[0x([0-9A-F]{2})u\]>\(h\)\) \{ v -= 0x[0-9A-F]+u; h\.pc = 0x([0-9A-F]+)u;',
+                                  body)
+                assert int(taken.group(1), 16) in (0x10, 0x30, 0x50, 0x70) and int(taken.group(2), 16) == int(start, 16) << 3
+        assert found == expect, (found, expect)
+
+
+@pytest.mark.parametrize('cross', [0, 1])
+def test_skip_leaves_the_counter_where_iterating_would(cross):
+    """The burst counter v holds (room - 1) << 14 | instructions run; the poll block runs while v >= its room R (the
+    entry test) and takes D = (7 + cross) << 14 - 2 off it per pass (BIT 4 cycles, a taken branch 3 or 4, two
+    instructions). For every v, the closed form the translation emits equals taking D off while v >= R."""
+    R = ((4 << 14) - 1) + ((4 << 14) - 1)            # jit_maxtake(BIT abs) + jit_maxtake(BPL)
+    D = ((4 + 3 + cross) << 14) - 2
+    for v in list(range(0, 4 * R, 997)) + [R - 1, R, R + 1, R + D - 1, R + D, (0x7FFF << 14) | 0x3FFF]:
+        it = v
+        while it >= R:
+            it -= D
+        closed = v - ((v - R) // D + 1) * D if v >= R else v
+        assert closed == it, v
