@@ -306,6 +306,17 @@ struct WaveLds {
 static_assert(sizeof(RenderScratch) <= NES_RAM_BYTES && offsetof(WaveLds, ram) % 16 == 0,
               "the render's scratch fits over the CPU RAM");
 
+// The kernel's arguments for what runs after the emulation, read there from the kernel-argument segment (every
+// kernel that runs emu_body takes its EmuArgs as its only parameter, so they start the segment) through an address
+// the compiler cannot see through. Read from the parameter, they are loaded at the kernel's start and held through
+// the emulation in scalar registers that the burst loop needs (the decision's finish pushed the translated
+// emulate-and-draw kernel into scratch; the frame bank's pointers cost the translated frame 1 %).
+__device__ __forceinline__ const EmuArgs& late_args() {
+    const EmuArgs* p = (const EmuArgs*)__builtin_amdgcn_kernarg_segment_ptr();
+    asm volatile("" : "+s"(p));
+    return *p;
+}
+
 // One console per wavefront (blockDim 64): the console index comes from blockIdx only, so every emulator value is
 // wave-uniform; lane 0 runs the 6502 on the scalar unit (SGPRs, uniform branches) with the console's memories in
 // LDS, the 64 lanes copy them in and out. Eight waves per SIMD: 8192 consoles fill 256 CUs x 4 SIMDs x 8 in one
@@ -381,12 +392,13 @@ __device__ __forceinline__ void emu_body(const EmuArgs& a) {
     wave_copy16(rec->oam, L.oam, NES_OAM_BYTES, lane);
     wave_copy16(rec->pal, L.pal, NES_PAL_BYTES, lane);
     if constexpr (kBank) {   // the frame's render state (the log lane 0 wrote before the sync above)
-        FrameBank* b = &a.bank[e];
+        const EmuArgs& la = late_args();
+        FrameBank* b = &la.bank[e];
         wave_copy16(b->log, rec->log, NES_LOG_WORDS * 4u, lane);
         wave_copy16(b->nt, L.nt, NES_NT_BYTES, lane);
         wave_copy16(b->oam, L.oam, NES_OAM_BYTES, lane);
         if (lane == 0) b->log_n = L.cs.log_n;
-        if (a.bank_chr) wave_copy16(a.bank_chr + (size_t)e * NES_CHRRAM_BYTES, rec->chr_ram, NES_CHRRAM_BYTES, lane);
+        if (la.bank_chr) wave_copy16(la.bank_chr + (size_t)e * NES_CHRRAM_BYTES, rec->chr_ram, NES_CHRRAM_BYTES, lane);
     }
     if constexpr (kDraw) {
         const bool draw = a.mode == EMU_DECISION && !a.s.no_render, finish = a.mode == EMU_DECISION && a.finish;
@@ -398,14 +410,9 @@ __device__ __forceinline__ void emu_body(const EmuArgs& a) {
             if (finish) {   // the decision's finish (k_finish's work), in the waves of its last frame
                 const uint64_t h = a.o.ram_hash ? ram_hash_wave(L.ram, lane) : 0;
                 if (lane == 0) {
-                    // The finish's arguments are read here from the kernel-argument segment (every kernel that runs
-                    // emu_body takes its EmuArgs as its only parameter, so they start the segment), through an
-                    // address the compiler cannot see through: read from `a`, they are loaded at the kernel's start
-                    // and held through the emulation, and the translated kernels then spill to scratch.
-                    const EmuArgs* fa = (const EmuArgs*)__builtin_amdgcn_kernarg_segment_ptr();
-                    asm volatile("" : "+s"(fa));
-                    if (fa->o.ram_hash) fa->o.ram_hash[ge] = h;
-                    if (finish_env(*fa, e, ge, rec->ram)) fa->g.list[atomicAdd(fa->g.list_count, 1u)] = e;
+                    const EmuArgs& fa = late_args();
+                    if (fa.o.ram_hash) fa.o.ram_hash[ge] = h;
+                    if (finish_env(fa, e, ge, rec->ram)) fa.g.list[atomicAdd(fa.g.list_count, 1u)] = e;
                 }
                 __syncthreads();   // (the hash has read the RAM before the scratch overwrites it)
             }
