@@ -161,12 +161,13 @@ struct RenderSink {
         const uint32_t val = ((lo4 * 0x00204081u) & 0x01010101u) | (((hi4 * 0x00204081u) & 0x01010101u) << 1);
         const int32_t b = 8 - (int32_t)sh;   // pixels q < b take p2's attribute
         const uint32_t m = b >= 4 ? 0xFFFFFFFFu : b <= 0 ? 0u : (1u << (8 * b)) - 1u;
-        const uint32_t attr = ((((p2 >> 16) & 3u) * 0x01010101u) & m) | ((((p1 >> 16) & 3u) * 0x01010101u) & ~m);
+        // (byte selects by v_perm_b32, whose selector byte k picks byte k of {src0:src1}, src1 the low four: full
+        // rate, where spreading a byte by a 32-bit multiply is a quarter-rate instruction)
+        const uint32_t attr = __builtin_amdgcn_perm((p1 >> 16) & 3u, (p2 >> 16) & 3u, ~m & 0x04040404u);
         const uint32_t idx = (attr << 2) | val;   // palette entry per byte, 0..15
         const uint32_t sel = idx & 0x07070707u;
         const uint32_t lo = __builtin_amdgcn_perm(t[1], t[0], sel), hi = __builtin_amdgcn_perm(t[3], t[2], sel);
-        const uint32_t mh = ((idx >> 3) & 0x01010101u) * 0xFFu;
-        return (lo & ~mh) | (hi & mh);
+        return __builtin_amdgcn_perm(hi, lo, 0x03020100u | ((idx >> 1) & 0x04040404u));   // entries 8..15 from hi
     }
     __device__ void on_run(const Rs& s, int32_t first, int32_t last, int32_t out, bool pixels) {
         __syncthreads();   // the walker's page and palette writes
@@ -299,11 +300,11 @@ struct RenderSink {
                 const uint32_t opaque = (eb | (eb >> 1)) & 0x01010101u;
                 const uint32_t front = ~(eb >> 7) & 0x01010101u, clear_bg = (w >> 6) & 0x01010101u;
                 const bool clipped = !(s.mask & 0x04u) && lane < 2;
-                const uint32_t show = clipped ? 0u : (opaque & (front | clear_bg)) * 0xFFu;
+                const uint32_t show = clipped ? 0u : opaque & (front | clear_bg);
                 const uint32_t sel = eb & 0x07070707u;
                 const uint32_t lo = __builtin_amdgcn_perm(spt[1], spt[0], sel), hi = __builtin_amdgcn_perm(spt[3], spt[2], sel);
-                const uint32_t hm = ((eb >> 3) & 0x01010101u) * 0xFFu;
-                w = (w & ~show) | (((lo & ~hm) | (hi & hm)) & show);
+                const uint32_t col = __builtin_amdgcn_perm(hi, lo, 0x03020100u | ((eb >> 1) & 0x04040404u));
+                w = __builtin_amdgcn_perm(col, w, 0x03020100u | (show << 2));   // the shown bytes from col
             }
         }
         if (l < 8) return;
