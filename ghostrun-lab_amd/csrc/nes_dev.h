@@ -669,10 +669,19 @@ __device__ inline void io_write(Con& c, const Mem& m, Access& ac, uint32_t a, ui
     } else if (a == 0x4014u) {
         // OAM DMA: 256 bytes of CPU page v through the bus (normally RAM in LDS)
         uint8_t* oam = m.oam;
-        for (uint32_t i = 0; i < 256u; ++i) {
-            const uint32_t src = (v << 8) | i;
-            const uint32_t b = src < 0x2000u ? m.ram[src & 0x7FFu] : bus_read(c, m, ac, src);
-            oam[(c.oam_addr + i) & 0xFFu] = (uint8_t)b;
+        if (v < 0x20u && (c.oam_addr & 15u) == 0u && ((unsigned long long)oam & 15u) == 0u && ((unsigned long long)m.ram & 15u) == 0u) {
+            // a RAM page (no side effect on the bus) to a 16-byte-aligned OAM address: 16 moves of 16 bytes, OAM
+            // wrapping at its end, instead of 256 of one byte
+            const uint4* from = reinterpret_cast<const uint4*>(m.ram + ((v << 8) & 0x7FFu));
+            uint4* to = reinterpret_cast<uint4*>(oam);
+            const uint32_t d0 = c.oam_addr >> 4;
+            for (uint32_t j = 0; j < 16u; ++j) to[(d0 + j) & 15u] = from[j];
+        } else {
+            for (uint32_t i = 0; i < 256u; ++i) {
+                const uint32_t src = (v << 8) | i;
+                const uint32_t b = src < 0x2000u ? m.ram[src & 0x7FFu] : bus_read(c, m, ac, src);
+                oam[(c.oam_addr + i) & 0xFFu] = (uint8_t)b;
+            }
         }
         ac.dma = true;
     } else if (a == 0x4016u) {

@@ -57,3 +57,17 @@ def test_skip_leaves_the_counter_where_iterating_would(cross):
             it -= D
         closed = v - ((v - R) // D + 1) * D if v >= R else v
         assert closed == it, v
+
+
+def test_translation_compiles_with_hiprtc():
+    """The benchmark cart's translation through hiprtc, as rlenv_create compiles it (hiprtc needs no GPU): the
+    device headers embedded in the library must build in hiprtc's environment too, where only what they include
+    themselves is declared (a host-only typedef compiled with hipcc and failed there)."""
+    lib = bind_library(HIP_LIB)
+    lib.rlenv_error.restype = ctypes.c_char_p
+    rom = synth.nrom_cart(1)
+    out = (ctypes.c_int32 * 4)()
+    text = ctypes.create_string_buffer(1 << 21)
+    r = lib.rlenv_jit_translate(rom, len(rom), 1, out, text, len(text))
+    assert r == 0, (lib.rlenv_error() or b'').decode()[:2000]
+    assert out[0] > 0 and out[3] > 0, list(out)   # blocks, code bytes
