@@ -564,14 +564,15 @@ __device__ __forceinline__ uint32_t run_until_wave(Con& cs, const Mem& m, const 
                               1u) - 1u);
             const uint32_t lm1_0 = lm1;
             uint32_t v = lm1 << 14, take;
-            // The wave's issue priority from the dots left to the frame's target, a quarter frame a step: the
-            // arbiter takes the oldest wave first among equals, so without this the waves of a CU finish far apart
-            // and the last ones run with too few others to hide their latency.
+            // The wave's issue priority from the dots left to the frame's target (half a frame or more, a quarter,
+            // an eighth, less): the arbiter takes the oldest wave first among equals, so without this the waves of a
+            // CU finish far apart and the last ones run with too few others to hide their latency; the steps halve
+            // toward the end, where the spread is left.
             {
                 const uint64_t left = target - abs_dot(cs);
-                if (left >= 3u * (NES_FRAME_DOTS / 4u)) __builtin_amdgcn_s_setprio(3);
-                else if (left >= 2u * (NES_FRAME_DOTS / 4u)) __builtin_amdgcn_s_setprio(2);
-                else if (left >= NES_FRAME_DOTS / 4u) __builtin_amdgcn_s_setprio(1);
+                if (left >= NES_FRAME_DOTS / 2u) __builtin_amdgcn_s_setprio(3);
+                else if (left >= NES_FRAME_DOTS / 4u) __builtin_amdgcn_s_setprio(2);
+                else if (left >= NES_FRAME_DOTS / 8u) __builtin_amdgcn_s_setprio(1);
                 else __builtin_amdgcn_s_setprio(0);
             }
             // What no instruction of the burst touches waits in LDS until the burst ends: left in registers it would
