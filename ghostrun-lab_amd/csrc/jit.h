@@ -67,14 +67,16 @@ inline uint32_t jit_take_max(uint32_t op) {
 }
 
 // A status poll: a block of two instructions, a read of $2002 (BIT, LDA, LDX or LDY absolute, at any mirror) and a
-// branch on bit 7 or 6 of the flags (BPL, BMI, BVC, BVS) back to the read. The status changes only at PPU events,
-// which a burst stops short of, and a read after the first leaves the console as it found it (the vblank flag and
-// the write toggle already clear, the open bus the same), so within a burst the iterations after the first are
-// alike: the translation takes as many of them at once as the burst's room allows. The counter then stands where
-// iterating would leave it (below the block's room), and the block goes on as before.
+// branch back to the read that the read's own side effect cannot turn: BPL (taken while bit 7, the vblank flag, is
+// clear, and the read leaves it clear), BVC or BVS (bit 6, the sprite-0 flag, which a read does not touch). The
+// status changes only at PPU events, which a burst stops short of, and a read after the first leaves the console as
+// it found it (the vblank flag and the write toggle already clear, the open bus the same), so within a burst the
+// iterations after the first are alike: the translation takes as many of them at once as the burst's room allows.
+// The counter then stands where iterating would leave it (below the block's room), and the block goes on as before.
+// BMI is not one: taken, its read saw the vblank flag set and cleared it, so the next iteration falls through.
 inline std::string jit_poll_skip(uint32_t op0, uint32_t addr, uint32_t op1, bool to_self, uint32_t cyc_taken) {
     const bool poll = to_self && (op0 == 0x2Cu || op0 == 0xADu || op0 == 0xAEu || op0 == 0xACu) &&
-                      (addr & 0xE007u) == 0x2002u && (op1 == 0x10u || op1 == 0x30u || op1 == 0x50u || op1 == 0x70u);
+                      (addr & 0xE007u) == 0x2002u && (op1 == 0x10u || op1 == 0x50u || op1 == 0x70u);
     if (!poll) return std::string();
     const uint32_t room = jit_take_max(op0) + jit_take_max(op1);
     const uint32_t iter = ((((kOptab.t[op0] >> 4) & 15u) + cyc_taken) << 14) - 2u;   // two instructions

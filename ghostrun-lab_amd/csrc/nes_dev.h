@@ -120,11 +120,27 @@ __device__ __forceinline__ Mem mem_of(NesRec* rec, uint8_t* ram, const Cart& car
     return Mem{rec, ram, rec->nt, rec->oam, rec->pal, cart, nullptr};
 }
 
+// One of four wave-uniform values by index i (0-3), as one scalar sequence. Written as C (nested selects), the
+// compiler splits it into a branch on bit 1 and an s_cselect on bit 0 at the join, with SCC live across the branch;
+// in a kernel large enough that the branch is relaxed into an s_getpc / s_add_u32 / s_addc_u32 / s_setpc jump, the
+// jump's adds overwrite SCC and the join selects the wrong value (seen in translated kernels of banked carts: a read
+// of $8000-$9FFF through the $A000 window). Here SCC lives only inside the statement. A constant index folds. The
+// operands are scalar registers: wave-uniform values, read from LDS through uni() where they come from there.
 __device__ __forceinline__ uint32_t sel4(uint32_t i, uint32_t a, uint32_t b, uint32_t c, uint32_t d) {
-    return i & 2u ? (i & 1u ? d : c) : (i & 1u ? b : a);
+    if (__builtin_constant_p(i)) return i & 2u ? (i & 1u ? d : c) : (i & 1u ? b : a);
+    uint32_t r, t;
+    asm("s_bitcmp1_b32 %2, 0\n\t"
+        "s_cselect_b32 %0, %4, %3\n\t"
+        "s_cselect_b32 %1, %6, %5\n\t"
+        "s_bitcmp1_b32 %2, 1\n\t"
+        "s_cselect_b32 %0, %1, %0"
+        : "=&s"(r), "=&s"(t)
+        : "s"(i), "s"(a), "s"(b), "s"(c), "s"(d)
+        : "scc");
+    return r;
 }
 __device__ __forceinline__ uint32_t prg_off(const Con& c, uint32_t addr) {
-    return sel4((addr >> 13) & 3u, c.prg0, c.prg1, c.prg2, c.prg3);
+    return sel4(uni((addr >> 13) & 3u), uni(c.prg0), uni(c.prg1), uni(c.prg2), uni(c.prg3));
 }
 __device__ __forceinline__ uint32_t prg_byte(const Con& c, const Mem& m, uint32_t addr) {
     return m.cart.prgw[prg_off(c, addr) + (addr & 0x1FFFu)] & 0xFFu;

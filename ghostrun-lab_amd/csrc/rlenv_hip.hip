@@ -22,10 +22,12 @@
 
 #include <atomic>
 #include <chrono>
+#include <condition_variable>
 #include <cstdio>
 #include <cstdlib>
 #include <ctime>
 #include <cstring>
+#include <deque>
 #include <map>
 #include <memory>
 #include <mutex>
@@ -37,6 +39,7 @@
 #include "emu_kernel.h"
 #include "env_dev.h"
 #include "jit.h"
+#include "jit_check.h"
 #include "nes_dev.h"
 #include "optab.h"
 #include "render_dev.h"
@@ -438,10 +441,28 @@ struct JitHeader { const char* name; const char* text; };
 const JitHeader kJitHeaders[] = {
 #include "jit_headers.inc"
 };
-// hiprtc options: the Makefile's device flags.
+// hiprtc options: the Makefile's device flags, then the words of RLENV_JIT_EXTRA (diagnostics; tests pass
+// "-mllvm -amdgpu-s-branch-bits=5", which relaxes nearly every branch into a far jump, to check that the kernels
+// hold no far-jump hazard whatever the layout).
 const char* const kJitOptions[] = {"--offload-arch=gfx950", "-O3", "-std=c++17", "-ffp-contract=off", "-fno-fast-math",
                                    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops", "-mllvm",
                                    "-structurizecfg-skip-uniform-regions=true"};
+std::vector<std::string> jit_options() {
+    std::vector<std::string> o(std::begin(kJitOptions), std::end(kJitOptions));
+    if (const char* extra = std::getenv("RLENV_JIT_EXTRA")) {
+        std::string w;
+        for (const char* c = extra;; ++c) {
+            if (*c == 0 || *c == ' ') {
+                if (!w.empty()) o.push_back(w);
+                w.clear();
+                if (*c == 0) break;
+            } else {
+                w += *c;
+            }
+        }
+    }
+    return o;
+}
 
 // One translation compiled for gfx950, shared by every env of the process whose translation has the same text; with
 // RLENV_JIT_CACHE=<directory> the code object is also kept there, named by a hash of everything it is built from.
@@ -451,6 +472,7 @@ struct JitJob {
     std::vector<char> code;
     std::string error;
     double seconds = 0;
+    int far_jumps = 0, hazards = 0;   // jit_check.h: far jumps in the code object, and those into live SCC
 };
 
 // A game's translated kernel: its job, the fetch table with the blocks' keys, the variant it was built for (decision
@@ -471,14 +493,28 @@ uint64_t fnv1a(const char* p, size_t n, uint64_t h = 0xcbf29ce484222325ull) {
     return h;
 }
 
+// A compiled code object is used only when jit_check.h finds no far jump into live SCC in it (a miscompile that
+// gives wrong results silently); otherwise the job fails and its game keeps the library's own kernel.
+bool jit_validate(JitJob& job) {
+    std::string where;
+    job.hazards = jit_far_branch_hazards(job.code, &job.far_jumps, &where);
+    if (job.hazards == 0) return true;
+    job.error = job.hazards < 0 ? std::string("jit check: the code object could not be disassembled")
+                                : "jit check: " + std::to_string(job.hazards) + " of " +
+                                      std::to_string(job.far_jumps) + " far jumps land where SCC is live (" + where +
+                                      ")";
+    return false;
+}
+
 void jit_compile(JitJob& job) {
     const auto t0 = std::chrono::steady_clock::now();
+    const std::vector<std::string> opts = jit_options();
     std::string path;
     if (const char* dir = std::getenv("RLENV_JIT_CACHE"); dir && *dir) {
         uint64_t h = fnv1a(job.source.data(), job.source.size());
         h = fnv1a(job.blocks.data(), job.blocks.size(), h);
         for (const JitHeader& hd : kJitHeaders) h = fnv1a(hd.text, strlen(hd.text), h);
-        for (const char* o : kJitOptions) h = fnv1a(o, strlen(o), h);
+        for (const std::string& o : opts) h = fnv1a(o.c_str(), o.size(), h);
         char name[48];
         snprintf(name, sizeof name, "/rlenv_jit_%016llx.hsaco", (unsigned long long)h);
         path = std::string(dir) + name;
@@ -488,8 +524,9 @@ void jit_compile(JitJob& job) {
             while ((n = fread(buf, 1, sizeof buf, f)) > 0) job.code.insert(job.code.end(), buf, buf + n);
             fclose(f);
             if (!job.code.empty()) {
+                const bool ok = jit_validate(job);
                 job.seconds = std::chrono::duration<double>(std::chrono::steady_clock::now() - t0).count();
-                job.state.store(1, std::memory_order_release);
+                job.state.store(ok ? 1 : 2, std::memory_order_release);
                 return;
             }
         }
@@ -504,8 +541,11 @@ void jit_compile(JitJob& job) {
     hiprtcProgram prog = nullptr;
     hiprtcResult r = hiprtcCreateProgram(&prog, job.source.c_str(), "rlenv_jit.hip", (int)texts.size(), texts.data(),
                                          names.data());
-    if (r == HIPRTC_SUCCESS)
-        r = hiprtcCompileProgram(prog, (int)(sizeof kJitOptions / sizeof kJitOptions[0]), kJitOptions);
+    if (r == HIPRTC_SUCCESS) {
+        std::vector<const char*> o;
+        for (const std::string& w : opts) o.push_back(w.c_str());
+        r = hiprtcCompileProgram(prog, (int)o.size(), o.data());
+    }
     bool ok = r == HIPRTC_SUCCESS;
     if (ok) {
         size_t n = 0;
@@ -522,6 +562,7 @@ void jit_compile(JitJob& job) {
         }
     }
     if (prog) hiprtcDestroyProgram(&prog);
+    ok = ok && jit_validate(job);
     if (ok && !path.empty()) {   // written aside, then renamed: a reader never sees half a file
         const std::string tmp = path + ".tmp" + std::to_string((unsigned long long)std::hash<std::thread::id>{}(
                                                     std::this_thread::get_id()));
@@ -533,6 +574,67 @@ void jit_compile(JitJob& job) {
     }
     job.seconds = std::chrono::duration<double>(std::chrono::steady_clock::now() - t0).count();
     job.state.store(ok ? 1 : 2, std::memory_order_release);
+}
+
+// The compile queue: one worker thread per process compiles the translations in the order they were asked for
+// (hiprtc runs one compile at a time in a process anyway), so rlenv_create returns once its games are booted and a
+// game's decision frames switch to the translated kernel at a call boundary after its compile (jit_refresh). The
+// thread is started on first use and detached; a handler registered with atexit at that point (after the compiler
+// library's own initialisation, so it runs before its teardown) drops the jobs not started and waits for the one in
+// flight, so that no compile runs while the process tears down.
+struct JitQueue {
+    std::mutex lock;
+    std::condition_variable cv;
+    std::deque<std::shared_ptr<JitJob>> jobs;
+    bool started = false, stopping = false, busy = false;
+};
+JitQueue& jit_queue() {
+    static JitQueue* q = new JitQueue();   // never destroyed: the worker may use it during exit
+    return *q;
+}
+void jit_worker() {
+    JitQueue& q = jit_queue();
+    std::unique_lock<std::mutex> hold(q.lock);
+    for (;;) {
+        q.cv.wait(hold, [&] { return q.stopping || !q.jobs.empty(); });
+        if (q.stopping) return;
+        std::shared_ptr<JitJob> job = q.jobs.front();
+        q.jobs.pop_front();
+        q.busy = true;
+        hold.unlock();
+        jit_compile(*job);
+        hold.lock();
+        q.busy = false;
+        q.cv.notify_all();
+    }
+}
+void jit_drain_at_exit() {
+    JitQueue& q = jit_queue();
+    std::unique_lock<std::mutex> hold(q.lock);
+    q.stopping = true;
+    for (const auto& job : q.jobs) {
+        job->error = "the process exited before the compile";
+        job->state.store(2, std::memory_order_release);
+    }
+    q.jobs.clear();
+    q.cv.notify_all();
+    q.cv.wait(hold, [&] { return !q.busy; });
+}
+void jit_enqueue(const std::shared_ptr<JitJob>& job) {
+    JitQueue& q = jit_queue();
+    std::lock_guard<std::mutex> hold(q.lock);
+    if (q.stopping) {
+        job->error = "the process is exiting";
+        job->state.store(2, std::memory_order_release);
+        return;
+    }
+    if (!q.started) {
+        q.started = true;
+        std::atexit(jit_drain_at_exit);
+        std::thread(jit_worker).detach();
+    }
+    q.jobs.push_back(job);
+    q.cv.notify_all();
 }
 
 // The job of (blocks, source): this process's existing one (fresh = false), or a new one the caller compiles.
@@ -704,7 +806,8 @@ JitSlot* jit_slot(const Env& env, const GameK& g) {
 }
 
 // Whether the translated kernel can be launched: loads its module on the env's device the first time its job has
-// compiled. A failed compile or load leaves the game on the library's own kernel (the results are the same).
+// compiled. A failed compile or load leaves the game on the library's own kernel (the results are the same). Called
+// only between decisions (jit_refresh, jit_wait, jit_status), so that the frames of one decision run one kernel.
 bool jit_ready(const Env& env, JitSlot& j) {
     if (j.fn_draw) return true;
     if (j.failed || !j.job) return false;
@@ -729,6 +832,13 @@ bool jit_ready(const Env& env, JitSlot& j) {
     }
     if (cur >= 0 && cur != env.device) (void)hipSetDevice(cur);
     return ok;
+}
+
+// At the start of a call that launches decision frames: the games whose compile has finished since switch to their
+// translated kernels.
+void jit_refresh(const Env& env) {
+    for (const GameH& gh : env.games)
+        if (gh.jit && !gh.jit->fn_draw && !gh.jit->failed) (void)jit_ready(env, *gh.jit);
 }
 
 // The address of `scratch` on each device, taken once with that device current.
@@ -839,7 +949,7 @@ void launch_emu(const Env& env, const GameK& g, const Outs& o, int mode, int f, 
     // built for the way this launch's frame is drawn
     JitSlot* js = mode == EMU_DECISION && blocks > 0 ? jit_slot(env, g) : nullptr;
     hipFunction_t fn = nullptr;
-    if (js && jit_ready(env, *js)) fn = draw ? js->fn_draw : a.bank ? js->fn : nullptr;
+    if (js && js->fn_draw) fn = draw ? js->fn_draw : a.bank ? js->fn : nullptr;
     if (fn) {
         a.g.cart.fetchw = js->fetchw;
         void* args[] = {&a};
@@ -1112,12 +1222,13 @@ void* rlenv_create(int ngames, const int* game_ids, const uint8_t* const* roms, 
         e.ep_maxlvl = env->mem.zeros<int32_t>(N);
         e.ep_idle = env->mem.zeros<int32_t>(N);
         e.resetting = env->mem.zeros<uint8_t>(N);
-        // translated kernels (jit.h): RLENV_JIT=0 (or off) none; by default the fixed-PRG games of at least
-        // kJitMinEnvs envs (a smaller one gains less than the compile takes); all: every game of that size, banked
-        // boards too (their translations are larger: tens of seconds of compile each); sync: every game
+        // translated kernels (jit.h): by default every game of at least kJitMinEnvs envs (a smaller one gains less
+        // than the compile takes), compiled in the background; RLENV_JIT=fixed: only the fixed-PRG games of that
+        // size (a banked cart's translation is larger, tens of seconds of compile); sync: every game, compiled
+        // before rlenv_create returns; 0 (or off): none
         const char* jv = std::getenv("RLENV_JIT");
-        const int jit_mode = !jv ? 1 : (!strcmp(jv, "0") || !strcmp(jv, "off")) ? 0 : !strcmp(jv, "sync") ? 3
-                             : !strcmp(jv, "all") ? 2 : 1;
+        const int jit_mode = !jv ? 2 : (!strcmp(jv, "0") || !strcmp(jv, "off")) ? 0 : !strcmp(jv, "sync") ? 3
+                             : !strcmp(jv, "fixed") ? 1 : 2;
         std::vector<std::string> jit_cases((size_t)ngames);
         int offset = 0;
         for (int i = 0; i < ngames; ++i) {
@@ -1223,8 +1334,8 @@ void* rlenv_create(int ngames, const int* game_ids, const uint8_t* const* roms, 
         }
         env->gs.create(env->games.size());
         if (hipDeviceSynchronize() != hipSuccess || check("create")) throw std::runtime_error(g_error);
-        // the translations' kernels, compiled in parallel (one thread per new translation) before the env is returned
-        std::vector<std::shared_ptr<JitJob>> fresh;
+        // the translations' kernels: queued for the process's compile thread (a translation another env already
+        // asked for is not compiled again); with RLENV_JIT=sync compiled and loaded before the env is returned
         for (size_t i = 0; i < env->games.size(); ++i) {
             GameH& gh = env->games[i];
             if (!gh.jit) continue;
@@ -1232,19 +1343,15 @@ void* rlenv_create(int ngames, const int* game_ids, const uint8_t* const* roms, 
             gh.jit->bank = env->games.size() == 1 && gh.k.n <= env->one_round;
             bool is_new = false;
             gh.jit->job = jit_job(std::move(jit_cases[i]), jit_module_source(gh.jit->bank, gh.jit->banked), is_new);
-            if (is_new) fresh.push_back(gh.jit->job);
+            if (is_new) jit_enqueue(gh.jit->job);
         }
-        {
-            std::vector<std::thread> workers;
-            for (const auto& job : fresh) workers.emplace_back([job] { jit_compile(*job); });
-            for (std::thread& t : workers) t.join();
-        }
-        for (GameH& gh : env->games)
-            if (gh.jit) {
-                while (gh.jit->job->state.load(std::memory_order_acquire) == 0)   // another env's compile of it
-                    std::this_thread::sleep_for(std::chrono::milliseconds(5));
-                (void)jit_ready(*env, *gh.jit);
-            }
+        if (jit_mode == 3)
+            for (GameH& gh : env->games)
+                if (gh.jit) {
+                    while (gh.jit->job->state.load(std::memory_order_acquire) == 0)
+                        std::this_thread::sleep_for(std::chrono::milliseconds(5));
+                    (void)jit_ready(*env, *gh.jit);
+                }
         return env;
     } catch (const std::exception& ex) {
         g_error = ex.what();
@@ -1289,12 +1396,15 @@ int rlenv_start(void* h, void* stream) {
 
 int rlenv_step(void* h, void* stream) {
     Env& env = *static_cast<Env*>(h);
+    jit_refresh(env);
     const int bad = for_games(env, static_cast<hipStream_t>(stream), [&](size_t gi, hipStream_t st) {
         decision_phases(env, env.games[gi].k, env.gs.render[gi], env.o, 0, env.games[gi].k.n, st);
     });
     return bad ? 1 : check("step");
 }
 
+// (a translation whose compile finished is not loaded here: loading a module allocates; rlenv_step, rlenv_jit_wait
+// and rlenv_jit_status load it)
 int rlenv_step_static(void* h, void* stream) {
     Env& env = *static_cast<Env*>(h);
     if (env.games.size() > kStaticGames || (uint32_t)env.total > kStaticEnvs) {
@@ -1315,6 +1425,7 @@ int rlenv_step_static(void* h, void* stream) {
 int rlenv_step_game(void* h, int gi, uint8_t* obs, uint8_t* emph, void* stream) {
     Env& env = *static_cast<Env*>(h);
     if (gi < 0 || gi >= (int)env.games.size()) { g_error = "step_game: bad game"; return 1; }
+    jit_refresh(env);
     Outs o = env.o;
     o.obs = obs;
     o.emph = emph;
@@ -1327,6 +1438,7 @@ int rlenv_step_range(void* h, int gi, int start, int count, uint8_t* obs, uint8_
     if (gi < 0 || gi >= (int)env.games.size()) { g_error = "step_range: bad game"; return 1; }
     const GameK& g = env.games[gi].k;
     if (start < 0 || count <= 0 || start + count > g.n) { g_error = "step_range: bad range"; return 1; }
+    jit_refresh(env);
     Outs o = env.o;
     o.obs = obs;
     o.emph = emph;
@@ -1521,6 +1633,8 @@ int rlenv_jit_translate(const uint8_t* rom, size_t rom_size, int compile, int32_
         out[1] = (int32_t)jp.instructions;
         out[2] = -1;
         out[3] = 0;
+        out[4] = 0;
+        out[5] = 0;
         if (text && text_cap) {
             const size_t n = std::min(text_cap - 1, jp.cases.size());
             memcpy(text, jp.cases.data(), n);
@@ -1533,6 +1647,8 @@ int rlenv_jit_translate(const uint8_t* rom, size_t rom_size, int compile, int32_
             jit_compile(job);
             out[2] = (int32_t)(job.seconds * 1000.0);
             out[3] = (int32_t)job.code.size();
+            out[4] = job.far_jumps;
+            out[5] = job.hazards;
             if (job.state.load() != 1) {
                 g_error = job.error;
                 return 1;
@@ -1545,16 +1661,32 @@ int rlenv_jit_translate(const uint8_t* rom, size_t rom_size, int compile, int32_
     }
 }
 
+int rlenv_jit_check(const char* code, size_t size, int32_t* out, char* where, size_t where_cap) {
+    const std::vector<char> co(code, code + size);
+    std::string w;
+    int far = 0;
+    out[1] = jit_far_branch_hazards(co, &far, &w);
+    out[0] = far;
+    if (where && where_cap) {
+        const size_t n = std::min(where_cap - 1, w.size());
+        memcpy(where, w.data(), n);
+        where[n] = 0;
+    }
+    return 0;
+}
+
 int rlenv_jit_status(void* h, int gi, int32_t* out) {
     Env& env = *static_cast<Env*>(h);
     if (gi < 0 || gi >= (int)env.games.size()) { g_error = "jit_status: bad game"; return 1; }
-    const JitSlot* j = env.games[gi].jit.get();
+    JitSlot* j = env.games[gi].jit.get();
+    if (j && !j->fn_draw && !j->failed) (void)jit_ready(env, *j);
     const int st = !j ? 0 : j->fn_draw ? 2 : (j->failed || (j->job && j->job->state.load() == 2)) ? 3 : 1;
     out[0] = st;
     out[1] = j ? (int32_t)j->blocks : 0;
     out[2] = j ? (int32_t)j->instructions : 0;
     out[3] = j && j->job && j->job->state.load() != 0 ? (int32_t)(j->job->seconds * 1000.0) : -1;
     out[4] = j && j->bank ? 1 : 0;
+    out[5] = j && j->job && j->job->state.load() != 0 ? j->job->far_jumps : -1;
     return 0;
 }
 

@@ -92,6 +92,7 @@ _ABI = {
     'rlenv_jit_wait': (_I, [_P], True),
     'rlenv_jit_status': (_I, [_P, _I, _P], True),
     'rlenv_jit_translate': (_I, [_P, _SZ, _I, _P, _P, _SZ], True),
+    'rlenv_jit_check': (_I, [_P, _SZ, _P, _P, _SZ], True),
     'rl_host_alloc': (_P, [_SZ], True),
     'rl_host_free': (_VOID, [_P], True),
     'rl_memcpy_async': (_I, [_P, _P, _SZ, _P], True),
@@ -261,20 +262,22 @@ class RlEnv:
 
     # ------------------------------------------------------------------ translated kernels
     def jit_wait(self):
-        """Wait until the translated kernel of every fixed-PRG game (include/rlenv_api.h rlenv_jit_wait) is compiled
-        and loaded; an error if a compile failed."""
+        """Wait until the translated kernel of every translated game (include/rlenv_api.h rlenv_jit_wait) is compiled
+        and loaded; an error if a compile, its far-jump check or its load failed."""
         self._check(self.lib.rlenv_jit_wait(self.h))
 
     def jit_status(self, gi=0) -> dict:
         """State of game gi's translated kernel: state ('none', 'compiling', 'loaded', 'failed'), blocks,
-        instructions, compile_ms (-1 while compiling), bank (built for frames drawn from frame banks)."""
-        out = (ctypes.c_int32 * 5)()
+        instructions, compile_ms (-1 while compiling), bank (built for frames drawn from frame banks), far_jumps
+        (in its code object; -1 while compiling)."""
+        out = (ctypes.c_int32 * 6)()
         self._check(self.lib.rlenv_jit_status(self.h, gi, out))
         return dict(state=('none', 'compiling', 'loaded', 'failed')[out[0]], blocks=out[1], instructions=out[2],
-                    compile_ms=out[3], bank=bool(out[4]))
+                    compile_ms=out[3], bank=bool(out[4]), far_jumps=out[5])
 
     def set_episode_level_end(self, level):
-        """End episodes (reason level_clear) on reaching `level`; 0 = never."""
+        """End episodes (reason level_clear) on reaching level `level` + 1 (0: on reaching level 1); -1 = never, the
+        default (rl/rlenv.py:323-324)."""
         self.lib.rlenv_set_episode_level_end(self.h, int(level))
 
     def set_no_render(self, v: bool):

@@ -299,11 +299,15 @@ def nrom_cart(seed: int = 0, blocks: int = 24) -> bytes:
     return ines(bytes(prg), chr_, 0, vertical=True)
 
 
-def poll_cart(seed: int = 0, blocks: int = 12) -> bytes:
+def poll_cart(seed: int = 0, blocks: int = 12, bmi: bool = False) -> bytes:
     """NROM-128 cartridge with NMI off: every frame of its main loop waits for vblank with BIT $2002 / BPL, writes the
     OAM (DMA), the sprite's position, four nametable bytes and the scroll, waits for the sprite-0 flag to clear (BIT /
     BVS) and to be set again (BIT / BVC), splits the scroll there, then reads the pad and runs the filler blocks.
-    Sprite 0 sits over the random background at (x, 96), so its hit comes on every frame."""
+    Sprite 0 sits over the random background at (x, 96), so its hit comes on every frame.
+
+    bmi: the loop then also spins for 10 + (pad & 7) times 1,284 cycles, which ends before, inside or after vblank
+    depending on the pad, and waits on BIT $2002 / BMI back to itself: inside vblank that read sees the flag set,
+    clears it and branches, and the next read falls through."""
     rng = np.random.default_rng([0x504F4C4C, seed])
     pal, nt, oam, mix = _tables(rng)
     oam[0], oam[1], oam[2], oam[3] = 95, int(rng.integers(1, 256)), 0, int(rng.integers(16, 200))
@@ -331,6 +335,12 @@ def poll_cart(seed: int = 0, blocks: int = 12) -> bytes:
     _read_pad(a, 'm')
     _pad_moves(a, 't_mix')
     _filler(a, rng, blocks, 'f', 't_mix')
+    if bmi:
+        a.op('LDA', 'zp', PAD); a.op('AND', 'imm', 7); a.op('CLC'); a.op('ADC', 'imm', 10); a.op('TAY')
+        a.label('p_dy'); a.op('LDX', 'imm', 0)
+        a.label('p_dx'); a.op('DEX'); a.op('BNE', 'rel', 'p_dx')
+        a.op('DEY'); a.op('BNE', 'rel', 'p_dy')
+        a.label('p_bm'); a.op('BIT', 'abs', 0x2002); a.op('BMI', 'rel', 'p_bm')
     a.op('JMP', 'abs', 'main')
     a.label('nmi')
     a.op('RTI')

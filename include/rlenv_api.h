@@ -107,22 +107,35 @@ int rlenv_kernel_times(void* h, double* ms, int64_t* count, int n);
  * cart's 6502 code into blocks of the interpreter's per-opcode handlers with constant operands (by CPU address on
  * NROM and CNROM, by PRG offset on the banked boards) and compiles them at run time (hiprtc; the games' compiles in
  * parallel, each translation once per process) into a copy of the console-frame kernel that the game's decision
- * frames then use; a console's results are the same on either kernel. Which games: by default the fixed-PRG games
- * of at least 1024 envs; RLENV_JIT=all: every game of at least 1024 envs (a banked cart's translation is larger,
- * tens of seconds of compile); RLENV_JIT=sync: every game; RLENV_JIT=0 (or off): none. Compiles of one process run
- * one at a time. RLENV_JIT_CACHE=<directory>: compiled code objects are also kept there, for later processes.
- *  jit_wait: 0 when every translated game runs translated decision frames (those drawn the way its translation was
- *    built for: from frame banks in a one-game env of one round of waves, from the records otherwise); non-zero,
- *    with the compile error in rlenv_error, when a compile or load failed (that game keeps the library's own
- *    kernel).
- *  jit_status: out[5] = state (0 no translation, 1 compiling, 2 loaded, 3 failed), blocks, instructions, compile
- *    milliseconds (-1 while compiling), 1 if built for frames drawn from frame banks.
- *  jit_translate: the translation of an iNES image (needs no GPU): out[4] = blocks, instructions, compile
- *    milliseconds and code-object bytes (-1 and 0 without compile); text (if not null): the generated blocks,
- *    NUL-terminated, cut at text_cap. Non-zero for an image that does not parse or a failed compile. */
+ * frames then use; a console's results are the same on either kernel. Which games: by default every game of at least
+ * 1024 envs; RLENV_JIT=fixed: only the fixed-PRG games of that size; RLENV_JIT=sync: every game; RLENV_JIT=0 (or off):
+ * none. The compiles run on one thread of the process, one at a time, in the order asked for, while rlenv_create
+ * returns at once (RLENV_JIT=sync: after them); a game's decision frames switch to its translated kernel at the first
+ * rlenv_step, rlenv_step_game, rlenv_step_range, rlenv_jit_wait or rlenv_jit_status after its compile (never in the
+ * middle of a decision; rlenv_step_static allocates nothing and so loads nothing). A compiled code object is used
+ * only if it holds no far jump into live SCC (a compiler fault, see rlenv_jit_check); else that game keeps the
+ * library's kernel. RLENV_JIT_CACHE=<directory>: compiled code objects are also kept there, for later processes.
+ * RLENV_JIT_EXTRA: further compile options, separated by spaces (diagnostics).
+ *  jit_wait: waits for the env's compiles; 0 when every translated game runs translated decision frames (those drawn
+ *    the way its translation was built for: from frame banks in a one-game env of one round of waves, from the
+ *    records otherwise); non-zero, with the compile error in rlenv_error, when a compile, its check or its load
+ *    failed (that game keeps the library's own kernel).
+ *  jit_status: out[6] = state (0 no translation, 1 compiling, 2 loaded, 3 failed), blocks, instructions, compile
+ *    milliseconds (-1 while compiling), 1 if built for frames drawn from frame banks, far jumps in the code object
+ *    (-1 while compiling).
+ *  jit_translate: the translation of an iNES image (needs no GPU): out[6] = blocks, instructions, compile
+ *    milliseconds, code-object bytes, far jumps and far jumps into live SCC (-1 and 0s without compile); text (if
+ *    not null): the generated blocks, NUL-terminated, cut at text_cap. Non-zero for an image that does not parse, a
+ *    failed compile or a code object that fails the check.
+ *  jit_check: the far-jump check of a gfx950 code object (an ELF as hiprtc returns it): a branch too far for its
+ *    16-bit offset is compiled to s_getpc_b64 / s_add_u32 / s_addc_u32 / s_setpc_b64, whose adds overwrite SCC,
+ *    and the compiler does not make sure that the code at the target does not read SCC first. out[2] = far jumps,
+ *    those whose target reads SCC before writing it (-1: not a code object it can disassemble); where (if not
+ *    null): the first such target, NUL-terminated. */
 int rlenv_jit_wait(void* h);
 int rlenv_jit_status(void* h, int gi, int32_t* out);
 int rlenv_jit_translate(const uint8_t* rom, size_t rom_size, int compile, int32_t* out, char* text, size_t text_cap);
+int rlenv_jit_check(const char* code, size_t size, int32_t* out, char* where, size_t where_cap);
 
 /* The reward10 SMB tracker on its own (benchmark config "reward10 standalone"): T steps of N envs.
  * ram15: u8 [T, N, 16], per env-step the 15 RAM bytes the SMB reader reads, in the order

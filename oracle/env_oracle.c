@@ -1169,6 +1169,6 @@ int rlenv_kernel_times(void* h, double* ms, int64_t* count, int n) {
 int rlenv_jit_wait(void* h) { (void)h; return 0; }
 int rlenv_jit_status(void* h, int gi, int32_t* out) {
     (void)h; (void)gi;
-    out[0] = 0; out[1] = 0; out[2] = 0; out[3] = -1; out[4] = 0;
+    out[0] = 0; out[1] = 0; out[2] = 0; out[3] = -1; out[4] = 0; out[5] = -1;
     return 0;
 }

@@ -77,7 +77,7 @@ def test_translated_kernel_device_code_has_no_packed_fp32_and_no_scratch(tmp_pat
     from helpers import HIP_LIB
     lib = bind_library(HIP_LIB)
     rom = synth.nrom_cart(1)
-    out = (ctypes.c_int32 * 4)()
+    out = (ctypes.c_int32 * 6)()
     text = ctypes.create_string_buffer(1 << 20)
     assert lib.rlenv_jit_translate(rom, len(rom), 0, out, text, len(text)) == 0
     assert out[0] > 50 and out[1] > 200 and len(text.value) < len(text) - 1

@@ -90,6 +90,18 @@ def test_translated_status_polls():
 
 
 @pytest.mark.gpu
+def test_translated_bmi_status_poll():
+    """The poll cart's BMI variant: a pad-dependent delay ends before, inside or after vblank, then BIT $2002 / BMI
+    back to itself; inside vblank the first read clears the flag and branches and the second falls through (a pass
+    in about nine on the oracle). Taken at once, the repeated iterations would run the console past the next PPU
+    event."""
+    print('case: translated poll cart seed 1 with the BMI poll, 16 consoles, raw pads, 24 decisions', flush=True)
+    cpu, gpu, _ = translated_pair(16, synth.poll_cart(1, bmi=True), seed=54, sticky=False, idle_max=0,
+                                  dropout=False, pad_mode=True)
+    run(cpu, gpu, 24, 54, True)
+
+
+@pytest.mark.gpu
 def test_translated_instruction_budget_exit():
     print('case: translated NROM seed 3, RLENV_BUDGET 3000, 8 consoles, 10 decisions', flush=True)
     os.environ['RLENV_BUDGET'] = '3000'
