@@ -51,7 +51,6 @@ import numpy as np
 ROOT = Path(__file__).resolve().parent
 sys.path.insert(0, str(ROOT / 'ghostrun-lab_amd'))
 
-METRIC = 'emulated NES frames/sec and decisions/sec at 8192 consoles, 1 MI355X'
 ORACLE_LIB = ROOT / 'oracle' / '_build' / 'liboracle_rlenv.so'
 COUNTERS = ROOT / 'profiles' / 'counters.json'
 HBM_PEAK_GBPS = 8000.0
@@ -59,26 +58,37 @@ CLOCK_HZ = 2.4e9                           # MI355X peak engine clock
 CUS = 256
 SALU_PEAK = CUS * CLOCK_HZ                 # one scalar instruction per CU per clock
 VALU_PEAK = CUS * CLOCK_HZ                 # one wave64 vector instruction per CU per clock (4 SIMDs x 1/4)
+# The library's kernel classes (include/rlenv_api.h rlenv_kernel_times), in its order.
 KERNELS = ('k_emu', 'k_render', 'k_finish', 'k_reset_copy', 'k_emu_restart', 'k_render_restart', 'k_reset_finish',
-           'k_emu_idle', 'k_archive')
+           'k_emu_idle', 'k_archive', 'k_emu_draw')
 
-# Algorithmic bytes per console per launch (outputs written + inputs read by the path, not state traffic).
+# Algorithmic bytes per console per decision (outputs written + inputs read by the path, not state traffic).
 PICTURE_BYTES = 224 * 240 + 224            # one frame's colour indices + emphasis
+PAD_BYTES = 2 + 1                          # a frame's action read and pad byte written
+FINISH_BYTES = 4 + 1 + 4 + 28 + 8          # reward, done, events, parts, RAM hash
 DECISION_BYTES = 4 * (PICTURE_BYTES + 1) + 2 + 4 + 1 + 4 + 28 + 19 + 360   # 216,358 B per console per decision
-FRAME_UNIT_BYTES = DECISION_BYTES / 4      # 54,089.5 B: the algorithmic bytes of one emulated frame
 PACK6_BYTES = 4 * 224 * 240 * 3 // 4 + 896 + 420                       # 162,596 B per console per decision
 RL10_STEP_BYTES = 20                                                      # 15 RAM bytes read + f32 reward + done
+# Algorithmic bytes each kernel class writes or reads itself, per console per launch, and per console per decision
+# on top of that (the decision's finish, in the last frame's launch).
 ALG_BYTES = {
-    'k_emu': FRAME_UNIT_BYTES,              # the frame unit: one launch emulates one frame of every console
-    'k_render': PICTURE_BYTES,
-    'k_finish': 4 + 1 + 4 + 28 + 8,         # reward, done, events, parts, RAM hash
-    'k_reset_copy': 0,
-    'k_emu_restart': 0,
-    'k_render_restart': 0,
-    'k_reset_finish': 19 + 360,             # masks, timeline
-    'k_emu_idle': 0,
-    'k_archive': 0,
+    'k_emu': (PAD_BYTES, 0),                        # frames drawn elsewhere: the emulation's own inputs and outputs
+    'k_emu_draw': (PICTURE_BYTES + PAD_BYTES, FINISH_BYTES),   # emulated and drawn; the last frame also finishes
+    'k_render': (PICTURE_BYTES, 0),
+    'k_finish': (FINISH_BYTES, 0),
+    'k_reset_copy': (0, 0),
+    'k_emu_restart': (0, 0),
+    'k_render_restart': (0, 0),
+    'k_reset_finish': (19 + 360, 0),                 # masks, timeline
+    'k_emu_idle': (0, 0),
+    'k_archive': (0, 0),
 }
+EMULATORS = ('k_emu', 'k_emu_draw')
+
+
+def metric(consoles):
+    """BASELINE's metric, at the workload's console count."""
+    return f'emulated NES frames/sec and decisions/sec at {consoles} consoles, 1 MI355X'
 
 WORKLOADS = {
     'nrom128-raw-frames': dict(consoles=8192, cart='nrom', sticky=True, dropout=False, end_prob=0.0, pack6=None),
@@ -307,7 +317,7 @@ def bench_env(args, name, K, W, baseline):
                             f', copied to {args.host_slots} pinned host slots' if w['pack6'] == 'host' else '')) +
                ' + emphasis + RAM hash',
                episode_ends_in_timed_region=ends_timed)
-    out = dict(metric=METRIC, value=round(decisions, 1), unit='decisions/s', frames_per_s=round(4 * decisions, 1),
+    out = dict(metric=metric(N), value=round(decisions, 1), unit='decisions/s', frames_per_s=round(4 * decisions, 1),
                n_gpus=1, steps=K, warmup=W, ms_per_step=round(dt * 1e3 / K, 3), higher_is_better=True,
                scaling='weak', vs_baseline=None, dtype='u8',
                data='synthetic: seed-generated cartridges (rl.synth), uniform random pad bytes', config=cfg,
@@ -316,11 +326,11 @@ def bench_env(args, name, K, W, baseline):
     if translated:   # fixed-PRG games whose decision frames ran their translated kernel
         out['translated'] = translated
     if kern:
-        out['roofline'] = _roofline(name, kern, N, K, dt, out_bytes, out['emulated_instructions_per_s'])
+        out['roofline'] = _roofline(name, kern, N, K, dt, out_bytes)
         out['kernels'] = kern
         counters = _counters(name)
         if counters:
-            out['counters'] = counters
+            out['counters_profiling_session'] = counters
     if not args.no_cpu:
         cpu_kw = dict(kw, roms={first: carts[first]}, boot={first: bytes(BOOT_FRAMES)})
         parity, base, one = _cpu_env(args, w, first, cpu_kw, pads_host, snap, ncmp, W, baseline)
@@ -343,37 +353,43 @@ def _kernel_times(env, N, K, dt):
         if c == 0:
             continue
         per = m / c
-        alg = ALG_BYTES[name] * N / games   # a launch covers one game's consoles
+        per_launch, per_decision = ALG_BYTES[name]
+        # a launch covers one game's consoles; the per-decision bytes spread over the class's launches of a decision
+        alg = (per_launch + per_decision * K / c) * N / games
         kern[name] = dict(ms_per_launch=round(per, 4), launches_per_step=round(c / K, 3), ms_per_step=round(m / K, 3),
                           share=round(m / (dt * 1e3), 4), alg_bytes_per_launch=round(alg),
                           achieved_gbps=round(alg / (per * 1e-3) / 1e9, 3))
     return kern
 
 
-def _roofline(name, kern, n, K, dt, out_bytes, ips):
-    """The dominant kernel against HBM (its algorithmic bytes per launch over its average launch time), the whole
-    step against HBM (the decision's algorithmic bytes over the measured step time), and the emulator kernel's
-    scalar and vector issue against one instruction per CU per clock each (instructions per emulated instruction from
-    the committed counter run of the same workload, emulated instructions and kernel time from this run)."""
+def _roofline(name, kern, n, K, dt, out_bytes):
+    """The dominant kernel (the most time per step): its algorithmic bytes per launch over its average launch time
+    against HBM (the `bound`/`frac` of the line), what actually limits it (`limiter`) with its scalar and vector issue
+    fractions, and the whole step against HBM. Issue: the kernel's SALU and VALU instructions per launch from the
+    committed counter run of the same workload (profiles/counters.json, a deterministic workload) over this run's
+    average launch time, against one instruction per CU per clock each (256 CUs at 2.4 GHz)."""
     dom = max(kern, key=lambda k: kern[k]['ms_per_step'])
     d = kern[dom]
     step_gbps = out_bytes * n * K / dt / 1e9
+    hbm_frac = d['achieved_gbps'] / HBM_PEAK_GBPS
     r = dict(kernel=dom, bound='hbm', achieved=d['achieved_gbps'], peak=HBM_PEAK_GBPS, unit='GB/s',
-             frac=round(d['achieved_gbps'] / HBM_PEAK_GBPS, 6), traffic=_traffic(dom, n) if name == HEADLINE else None,
-             step_achieved_gbps=round(step_gbps, 3), step_frac=round(step_gbps / HBM_PEAK_GBPS, 6))
-    c = (_counters(name) or {}).get('k_emu')
-    emu = kern.get('k_emu')
-    restart = kern.get('k_emu_restart', {}).get('ms_per_step', 0.0) + kern.get('k_emu_idle', {}).get('ms_per_step', 0.0)
-    if c and emu and restart <= 0.05 * emu['ms_per_step']:
-        per = c['per_emulated_instruction']
-        emu_s = emu['ms_per_step'] * K / 1e3
-        ips_kernel = ips * dt / emu_s              # emulated instructions per second of k_emu time
-        r['emu_issue'] = dict(kernel='k_emu', salu_per_instruction=per['salu'], valu_per_instruction=per['valu'],
-                              salu_frac=round(ips_kernel * per['salu'] / SALU_PEAK, 4),
-                              valu_frac=round(ips_kernel * per['valu'] / VALU_PEAK, 4),
-                              counter_SALUBusy_pct=c.get('SALUBusy_pct'), counter_VALUBusy_pct=c.get('VALUBusy_pct'),
-                              counter_VALUUtilization_pct=c.get('VALUUtilization_pct'),
-                              note='one console per wavefront, the 6502 on the scalar unit: bound by scalar issue')
+             frac=round(hbm_frac, 6), traffic=_traffic(dom, n) if name == HEADLINE else None,
+             step_achieved_gbps=round(step_gbps, 3),
+             step_frac=round(step_gbps / HBM_PEAK_GBPS, 6))
+    c = (_counters(name) or {}).get(dom)
+    if dom in EMULATORS and c and c.get('insts_salu') and c.get('dispatches'):
+        per_s = d['ms_per_launch'] * 1e-3
+        salu = c['insts_salu'] / c['dispatches'] / per_s / SALU_PEAK
+        valu = c['insts_valu'] / c['dispatches'] / per_s / VALU_PEAK
+        r['limiter'] = 'salu' if salu >= max(valu, hbm_frac) else 'valu' if valu >= hbm_frac else 'hbm'
+        r['issue'] = dict(salu_frac=round(salu, 4), valu_frac=round(valu, 4), hbm_frac=round(hbm_frac, 6),
+                          salu_per_launch=c['insts_salu'] // c['dispatches'],
+                          valu_per_launch=c['insts_valu'] // c['dispatches'],
+                          salu_per_emulated_instruction=(c.get('per_emulated_instruction') or {}).get('salu'),
+                          counter_SALUBusy_pct=c.get('SALUBusy_pct'), counter_VALUBusy_pct=c.get('VALUBusy_pct'),
+                          counter_VALUUtilization_pct=c.get('VALUUtilization_pct'),
+                          note='one console per wavefront, the 6502 on the scalar unit: bound by scalar issue; '
+                               'traffic is the console state staged through LDS, not algorithmic bytes')
     if name == 'rollout-pack6':
         r['host_link_gbps'] = round(PACK6_BYTES * n * K / dt / 1e9, 3)
         r['note'] = 'every decision\'s packed frames cross the host link (PCIe 5 x16, about 63 GB/s each way)'
@@ -385,16 +401,17 @@ def _summary():
 
 
 def _counters(workload):
-    """Issue and utilisation figures of the frame kernels from the committed counter summary, if present."""
-    keep = ('kernel', 'SALUBusy_pct', 'VALUBusy_pct', 'VALUUtilization_pct', 'per_emulated_instruction',
-            'wave_state_pct')
+    """Issue and utilisation figures of the frame kernels from the committed counter summary, if present (figures of
+    the profiling session, not of this run)."""
+    keep = ('kernel', 'dispatches', 'insts_salu', 'insts_valu', 'SALUBusy_pct', 'VALUBusy_pct', 'VALUUtilization_pct',
+            'per_emulated_instruction', 'wave_state_pct')
     w = _summary().get('workloads', {}).get(workload)
     return {k: {f: v[f] for f in keep if f in v} for k, v in w.items()} if w else None
 
 
 def _traffic(kernel, n):
     """HBM bytes per launch of `kernel` from the committed counter summary (FETCH_SIZE + WRITE_SIZE scaled by the
-    copy-kernel calibration), scaled to n consoles; None when no summary covers it."""
+    copy-kernel calibration, taken on the headline workload), scaled to n consoles; None when it does not cover it."""
     t = _summary().get('traffic', {}).get(kernel)
     return round(t['bytes_per_console_launch'] * n) if t else None
 

@@ -289,17 +289,55 @@ __device__ inline void map_write(Con& c, const Mem& m, uint32_t addr, uint32_t v
     }
 }
 
-__device__ inline void mmc3_clock(Con& c, const Mem& m) {
+// The MMC3 scanline counter (patch:1881-1903): a clock reloads the counter from the latch when it is 0 or a reload
+// was asked for ($C001), else decrements it, and raises the IRQ line when it is then 0 with the IRQ enabled. Registers:
+// mreg[11] latch, [12] counter, [13] IRQ enabled, [14] reload asked for.
+//
+// The counter of n >= 1 clocks in closed form: the first clock leaves c1 (the latch after a reload or from 0, else the
+// counter less one); the counter then counts down to 0, which it reaches at clock c1 + 1, and runs the cycle latch,
+// latch - 1, ..., 0 of latch + 1 clocks from there. *zero: whether some clock of the n left it at 0 (the IRQ).
+__host__ __device__ __forceinline__ uint32_t mmc3_after_clocks(uint32_t cnt, uint32_t reload, uint32_t latch,
+                                                                 uint32_t n, bool* zero) {
+    const uint32_t c1 = (cnt == 0u || reload != 0u) ? latch : cnt - 1u;
+    *zero = n >= c1 + 1u;
+    if (n - 1u <= c1) return c1 - (n - 1u);
+    return latch - (n - 2u - c1) % (latch + 1u);
+}
+
+// MMC3 clock dots of one frame: lines 0-239 at dot 266, the pre-render line (261) at dot 256. The number of them at
+// frame dots <= x (x < NES_FRAME_DOTS, the dots of a frame that is not short).
+__host__ __device__ __forceinline__ uint32_t mmc3_clocks_upto(uint32_t x) {
+    const uint32_t line = x / 341u, d = x - line * 341u;
+    if (line < 240u) return line + (d >= 266u ? 1u : 0u);
+    if (line < 261u) return 240u;
+    return 240u + (d >= 256u ? 1u : 0u);
+}
+
+// The clocks of the dots (start, end] (ppu_step's dots: the skipped last dot of a short frame counted) at once. The
+// device settles the PPU lazily (dots_to_event), so a span holds many clocks; nothing reads the counter between them,
+// and what decides them - the mask, the control register and the board's IRQ registers - changes only in the generic
+// step, before which wave_dev.h settles, so applying them together leaves the state of applying them one by one.
+__device__ inline void mmc3_clock_span(Con& c, const Mem& m, uint32_t start, uint32_t end) {
+    const uint32_t n = (end / NES_FRAME_DOTS) * 241u + mmc3_clocks_upto(end % NES_FRAME_DOTS) -
+                       (start / NES_FRAME_DOTS) * 241u - mmc3_clocks_upto(start % NES_FRAME_DOTS);
+    if (n == 0u) return;
     uint8_t* r = m.rec->mreg;
-    uint32_t cnt = r[12];
-    if (cnt == 0 || r[14] != 0) {
-        cnt = r[11];
-        r[14] = 0;
-    } else {
-        --cnt;
-    }
-    r[12] = (uint8_t)cnt;
-    if (cnt == 0 && r[13] != 0) c.irq_line = 1;
+    bool zero = false;
+    r[12] = (uint8_t)mmc3_after_clocks(r[12], r[14], r[11], n, &zero);
+    r[14] = 0;
+    if (zero && r[13] != 0) c.irq_line = 1;
+}
+
+// The frame dot of the clock that will raise the IRQ line, if it comes in this frame after frame dot `cur` (clocks
+// on, IRQ enabled, the line not already raised), else NES_FRAME_DOTS.
+__device__ __forceinline__ uint32_t mmc3_irq_dot(const Con& c, const Mem& m, uint32_t cur) {
+    if (!(uni(c.mask) & 0x18u) || (uni(c.ctrl) & 0x38u) == 0x18u || uni(c.irq_line)) return NES_FRAME_DOTS;
+    const uint8_t* r = m.rec->mreg;
+    if (r[13] == 0) return NES_FRAME_DOTS;
+    const uint32_t cnt = r[12];
+    const uint32_t k = (cnt == 0u || r[14] != 0) ? r[11] + 1u : cnt;   // the clock (1st, 2nd, ...) that leaves 0
+    const uint32_t i = mmc3_clocks_upto(cur) + k - 1u;                     // its index in the frame
+    return i < 240u ? i * 341u + 266u : i == 240u ? 261u * 341u + 256u : NES_FRAME_DOTS;
 }
 
 // ---------------------------------------------------------------------------------------------- DMC
@@ -376,11 +414,24 @@ __device__ __forceinline__ uint32_t dots_to_mmc3_clock(uint32_t cur) {
     return 341u - d + 266u;
 }
 
+// Before a generic step on MMC3: the counter's clocks in the `dots` since the last settle, and the frame dot moved on
+// by them (the caller's pending dots become 0). No other event lies in them (the caller settles at its horizon), and
+// the generic step may change what decides the clocks (the mask, the control register, the IRQ registers), so the
+// clocks before the instruction take the values before it, as they do when every clock is settled at its own dot.
+__device__ inline void mmc3_presettle(Con& c, const Mem& m, uint32_t dots) {
+    const uint32_t start = uni(c.frame_dot);
+    if ((uni(c.mask) & 0x18u) && (uni(c.ctrl) & 0x38u) != 0x18u) mmc3_clock_span(c, m, start, start + dots);
+    c.frame_dot = start + dots;
+}
+
 // Dots from the current frame dot to the next PPU event (patch:2001-2037): the frame wrap, vblank, the pre-render
 // line, the $2002 flag set and clear dots, the scheduled sprite-0 check and, on MMC3, the counter clocks. A short
 // frame ends a dot early. Written as a search for the nearest event at an absolute dot (events at or before the
-// current dot count from the next frame), then one difference.
-__device__ inline uint32_t dots_to_event(const Con& c, const Mem& m) {
+// current dot count from the next frame), then one difference. On MMC3 the reference stops at every clock; with
+// every_clock false only the clock that raises the IRQ is an event (mmc3_clock_span applies the others in a span),
+// which changes nothing the CPU can see while it runs instructions; the idle loop's fast-forward stops at every clock
+// as the reference's does (each stop runs one JMP as an instruction, with the DMC's cycle steal).
+__device__ inline uint32_t dots_to_event(const Con& c, const Mem& m, bool every_clock = false) {
     const uint32_t cur = uni(c.frame_dot), skip = (uni(c.log_flags) & NES_LOG_SHORT) ? 1u : 0u;
     const uint32_t frame = NES_FRAME_DOTS - skip;
     uint32_t next = frame;
@@ -395,8 +446,13 @@ __device__ inline uint32_t dots_to_event(const Con& c, const Mem& m) {
     const uint32_t s0 = uni(c.s0_sched) & NES_S0_DOT;
     if (s0 != 0) cand(s0);
     if (m.cart.board == NES_BOARD_MMC3) {
-        uint32_t at = cur + dots_to_mmc3_clock(cur);
-        if (at >= NES_FRAME_DOTS) at -= skip;
+        uint32_t at;
+        if (every_clock) {
+            at = cur + dots_to_mmc3_clock(cur);
+            if (at >= NES_FRAME_DOTS) at -= skip;
+        } else {
+            at = mmc3_irq_dot(c, m, cur);
+        }
         if (at < next) next = at;
     }
     return next - cur;
@@ -497,15 +553,8 @@ __device__ inline void ppu_step(Con& c, const Mem& m, uint32_t dots) {
     }
     if constexpr (B != NES_BOARD_NROM) {
         // FCEUmm clocks the counter while rendering, unless both pattern tables are at $1000 with 8x8 sprites
-        if (m.cart.board == NES_BOARD_MMC3 && (uni(c.mask) & 0x18u) && (uni(c.ctrl) & 0x38u) != 0x18u) {
-            for (uint32_t la = start / 341u; la <= end / 341u; ++la) {
-                const uint32_t line = la % 262u;
-                const uint32_t at = line < 240u ? 266u : 256u;
-                if (line >= 240u && line != 261u) continue;
-                const uint32_t d = la * 341u + at;
-                if (d > start && d <= end) mmc3_clock(c, m);
-            }
-        }
+        if (m.cart.board == NES_BOARD_MMC3 && (uni(c.mask) & 0x18u) && (uni(c.ctrl) & 0x38u) != 0x18u)
+            mmc3_clock_span(c, m, start, end);
     }
     c.frame_dot = end % NES_FRAME_DOTS;
     c.frame = uni(c.frame) + frames;

@@ -664,7 +664,7 @@ struct GameH {
 // Kernel classes of a decision, for the per-kernel clock (rlenv_kernel_times).
 enum KClass : int {
     KC_EMU = 0, KC_RENDER, KC_FINISH, KC_RESET_COPY, KC_EMU_RESTART, KC_RENDER_RESTART, KC_RESET_FINISH, KC_EMU_IDLE,
-    KC_ARCHIVE, KC_COUNT
+    KC_ARCHIVE, KC_EMU_DRAW, KC_COUNT
 };
 
 // Optional per-launch HIP-event clock: when on, every launch of a decision is bracketed by two events on its
@@ -944,7 +944,8 @@ void launch_emu(const Env& env, const GameK& g, const Outs& o, int mode, int f, 
     EmuArgs a{g, env.e, o, env.s, env.optab, mode, f, use_list ? 1 : 0, e0, e1, 0, 0, nullptr, env.budget,
               bank >= 0 ? g.bank[bank] : nullptr, bank >= 0 ? g.bank_chr[bank] : nullptr, finish ? 1 : 0};
     const int blocks = use_list ? g.n : e1 - e0;
-    const int cls = mode == EMU_DECISION ? KC_EMU : mode == EMU_IDLE ? KC_EMU_IDLE : KC_EMU_RESTART;
+    const int cls = mode == EMU_DECISION ? (draw ? KC_EMU_DRAW : KC_EMU) : mode == EMU_IDLE ? KC_EMU_IDLE
+                                                                                             : KC_EMU_RESTART;
     // decision frames of a fixed-PRG cart run its translated kernel once that is compiled and loaded, when it was
     // built for the way this launch's frame is drawn
     JitSlot* js = mode == EMU_DECISION && blocks > 0 ? jit_slot(env, g) : nullptr;
@@ -1691,7 +1692,7 @@ int rlenv_jit_status(void* h, int gi, int32_t* out) {
 }
 
 int rlenv_kernel_times(void* h, double* ms, int64_t* count, int n) {
-    if (n < KC_COUNT) { g_error = "kernel_times: need room for every kernel class (9)"; return 1; }
+    if (n < KC_COUNT) { g_error = "kernel_times: need room for every kernel class (10)"; return 1; }
     for (int i = 0; i < n; ++i) { ms[i] = 0.0; count[i] = 0; }
     if (static_cast<Env*>(h)->clock.drain(ms, count)) { g_error = "kernel_times: event query failed"; return 1; }
     return 0;

@@ -529,7 +529,7 @@ __device__ __forceinline__ uint32_t run_until_wave(Con& cs, const Mem& m, const 
                 // The idle JMP-to-self loop (patch:866-893): whole 3-cycle jumps up to the next PPU event, settled at
                 // once; not with an NMI raised by the settle before it. (h is current: the generic step stored it.)
                 if (!nmi) {
-                    const uint32_t jumps = (uni(dots_to_event(cs, m)) + 8u) / 9u;
+                    const uint32_t jumps = (uni(dots_to_event(cs, m, true)) + 8u) / 9u;
                     if (jumps) {
                         h.cycles += 3u * jumps;
                         if (h.cycles >= dmc_event) {
@@ -643,6 +643,13 @@ __device__ __forceinline__ uint32_t run_until_wave(Con& cs, const Mem& m, const 
         // the generic step: I/O, interrupts, the idle loop, BRK, faults, code outside PRG
         h.cycles += ecyc;
         ecyc = 0;
+        if constexpr (B != NES_BOARD_NROM) {
+            // MMC3: the counter's clocks up to the instruction first (its horizon is only the IRQ's clock)
+            if (m.cart.board == NES_BOARD_MMC3 && pending != 0u) {
+                mmc3_presettle(cs, m, pending);
+                pending = 0;
+            }
+        }
         hot_store<B>(h, cs);
         cs.dmc_event = dmc_event;
         cyc = cpu_step(cs, m, optab, uni(cs.frame_dot) + pending, &fault, &op, &pc0);
@@ -654,6 +661,10 @@ __device__ __forceinline__ uint32_t run_until_wave(Con& cs, const Mem& m, const 
         if (fault) {
             why = 2;
             continue;
+        }
+        if constexpr (B != NES_BOARD_NROM) {
+            // the instruction may have moved the IRQ's clock (a mapper or PPU register write); pending is 0 here
+            if (m.cart.board == NES_BOARD_MMC3) to_event = uni(dots_to_event(cs, m));
         }
         pending += 3u * cyc;
         ++instructions;

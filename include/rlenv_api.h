@@ -98,9 +98,11 @@ void rlenv_bind_ram_hash(void* h, uint64_t* ram_hash);
 int rlenv_read_consoles(void* h, int gi, int first, int count, uint8_t* host_out, void* stream);
 /* Per-kernel clock (no reference counterpart; the measurement harness reads it): when on, every launch of a
  * start/step is bracketed by two HIP events on its stream. rlenv_kernel_times waits for the recorded launches,
- * writes the summed milliseconds and launch counts per kernel class into ms[n] / count[n] (n >= 9; classes:
- * 0 emu, 1 render, 2 finish, 3 reset_copy, 4 emu_restart, 5 render_restart, 6 reset_finish, 7 emu_idle (idle
- * frames of level starts), 8 archive (level-start saves)) and forgets them. */
+ * writes the summed milliseconds and launch counts per kernel class into ms[n] / count[n] (n >= 10; classes:
+ * 0 emu (decision frames drawn by another kernel, from frame banks), 1 render, 2 finish, 3 reset_copy, 4 emu_restart,
+ * 5 render_restart, 6 reset_finish, 7 emu_idle (idle frames of level starts), 8 archive (level-start saves), 9
+ * emu_draw (decision frames emulated and drawn by the same waves, the decision's last one with its finish)) and
+ * forgets them. */
 void rlenv_set_kernel_timing(void* h, int on);
 int rlenv_kernel_times(void* h, double* ms, int64_t* count, int n);
 /* Translated kernels (no reference counterpart: an acceleration inside this library). rlenv_create translates the

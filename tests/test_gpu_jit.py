@@ -153,6 +153,7 @@ def test_translated_equals_interpreter_at_full_size():
     kw = dict(seed=1, sticky=True, idle_max=0, dropout=False, pad_mode=True, ram_hash=True,
               roms={'smb': synth.nrom_cart(1)})
     fast = RlEnv({'smb': 8192}, device='cuda', lib_path=HIP_LIB, **kw)
+    fast.jit_wait()
     assert fast.jit_status(0)['state'] == 'loaded'
     os.environ['RLENV_JIT'] = '0'
     try:

@@ -54,6 +54,7 @@ def test_full_size_console_independence():
     cart = synth.nrom_cart(1)
     kw = dict(seed=1, sticky=False, idle_max=0, dropout=False, pad_mode=True, ram_hash=True, roms={'smb': cart})
     gpu = RlEnv({'smb': 8192}, device='cuda', lib_path=HIP_LIB, **kw)
+    gpu.jit_wait()
     cpu = RlEnv({'smb': 3}, device='cpu', lib_path=ORACLE_LIB, **kw)
     pick = torch.tensor([0, 4095, 8191])
     g = torch.Generator().manual_seed(0)

@@ -97,11 +97,18 @@ def tptr(t):
     return ctypes.c_void_p(t.data_ptr())
 
 
-def subset_run(n, cart, ranges, decisions, act_seed, **kw):
+def subset_run(n, cart, ranges, decisions, act_seed, check_every=1, **kw):
     """n consoles on the GPU, every decision of all of them; the oracle steps only the console ranges (with their own
-    env indices, so their seeds and streams are the same) and every output of those consoles is compared."""
+    env indices, so their seeds and streams are the same) and every output of those consoles is compared (every
+    check_every decisions, and at the last). A game of this size is translated (compiled in the background): the
+    run starts once the translated kernel is loaded, so every decision runs it."""
     kw = dict(kw, ram_hash=True, roms={'smb': cart})
     gpu = RlEnv({'smb': n}, device='cuda', lib_path=HIP_LIB, **kw)
+    gpu.jit_wait()
+    st = gpu.jit_status(0)
+    assert st['state'] == 'loaded', st
+    print(f'  translated: {st["blocks"]} blocks, {st["instructions"]} instructions, compiled in {st["compile_ms"]} '
+          f'ms, {st["far_jumps"]} far jumps', flush=True)
     cpu = RlEnv({'smb': n}, device='cpu', lib_path=ORACLE_LIB, **kw)
     g = torch.Generator().manual_seed(act_seed)
     gpu.start()
@@ -115,6 +122,8 @@ def subset_run(n, cart, ranges, decisions, act_seed, **kw):
         gpu.step()
         for a, b in ranges:
             cpu.step_range(0, a, b - a, cpu.obs, cpu.emph)
+        if (t + 1) % check_every and t != decisions - 1:
+            continue
         torch.cuda.synchronize()
         for k in OUTS:
             want, got = getattr(cpu, k)[rows].numpy(), getattr(gpu, k)[rows.cuda()].cpu().numpy()
@@ -158,8 +167,9 @@ def test_full_size_rollout_shape_subset():
 
 @pytest.mark.gpu
 def test_full_size_mmc3_two_wave_rounds_subset():
-    """The stress shape: 16384 MMC3 consoles (two rounds of waves on one GPU), independent random pads; consoles
-    0-31 (first round) and 16352-16383 (second round) against the oracle for 16 decisions."""
-    print('case: MMC3 seed 1, 16384 consoles, 16 decisions, consoles 0-31 and 16352-16383', flush=True)
+    """The stress shape: 16384 MMC3 consoles (two rounds of waves on one GPU) on the translated kernel of the full-size
+    cart (its far jumps checked), independent random pads; consoles 0-31 (first round) and 16352-16383 (second round)
+    against the oracle for 16 decisions."""
+    print('case: MMC3 seed 1, 16384 consoles, translated, 16 decisions, consoles 0-31 and 16352-16383', flush=True)
     subset_run(16384, synth.mmc3_cart(1), [(0, 32), (16352, 16384)], 16, 43, seed=3, sticky=False, idle_max=0,
                dropout=False, pad_mode=True)
