@@ -52,6 +52,10 @@ ROOT = Path(__file__).resolve().parent
 sys.path.insert(0, str(ROOT / 'ghostrun-lab_amd'))
 
 ORACLE_LIB = ROOT / 'oracle' / '_build' / 'liboracle_rlenv.so'
+# Compiled translations of the workloads' carts (RLENV_JIT_CACHE): a cold cache adds their compiles (tens of seconds
+# each, one at a time) to the env creation, never to the timed region; `bench.py --precompile` fills it on the CPU.
+JIT_CACHE = ROOT / 'ghostrun-lab_amd' / 'csrc' / '_build' / 'jit_cache'
+ONE_ROUND = 256 * 32                       # consoles the MI355X holds in one round of one-console waves
 COUNTERS = ROOT / 'profiles' / 'counters.json'
 HBM_PEAK_GBPS = 8000.0
 CLOCK_HZ = 2.4e9                           # MI355X peak engine clock
@@ -115,11 +119,18 @@ def parse():
     ap.add_argument('--cpu-seconds', type=float, default=10.0)
     ap.add_argument('--no-cpu', action='store_true', help='skip the parity checks and the CPU baseline')
     ap.add_argument('--no-kernel-clock', action='store_true')
+    ap.add_argument('--precompile', action='store_true',
+                    help='compile the workloads\' translated kernels into the translation cache (CPU only) and exit')
     return ap.parse_args()
 
 
 def main():
     args = parse()
+    os.environ.setdefault('RLENV_JIT_CACHE', str(JIT_CACHE))
+    Path(os.environ['RLENV_JIT_CACHE']).mkdir(parents=True, exist_ok=True)
+    if args.precompile:
+        precompile(args)
+        return
     world = int(os.environ.get('WORLD_SIZE', '1'))
     if args.gpus != 1 or world != 1:
         print('bench.py measures one GPU: the environment step runs on a single MI355X and has no multi-GPU path '
@@ -149,6 +160,40 @@ def main():
     if bad:
         print(f'[bench] parity FAILED for {bad}', file=sys.stderr, flush=True)
         sys.exit(3)
+
+
+def _compile_one(job):
+    """One translation through the library, into the cache (a process of its own: compiles in one process run one
+    at a time)."""
+    rom, mode = job
+    from rl.rlenv import bind_library, hip_library
+    lib = bind_library(hip_library())
+    lib.rlenv_error.restype = ctypes.c_char_p
+    out = (ctypes.c_int32 * 6)()
+    t = time.perf_counter()
+    rc = lib.rlenv_jit_translate(rom, len(rom), mode, out, None, 0)
+    return rc, list(out), time.perf_counter() - t, (lib.rlenv_error() or b'').decode()[:300]
+
+
+def precompile(args):
+    """The translations every env workload creates (the frame-bank variant for a one-game env of one round of waves),
+    compiled in parallel processes into RLENV_JIT_CACHE."""
+    from concurrent.futures import ProcessPoolExecutor
+    jobs = {}
+    for name, w in WORKLOADS.items():
+        if name == 'reward10':
+            continue
+        carts = carts_of(w, args.cart_seed)
+        bank = len(carts) == 1 and w['consoles'] <= ONE_ROUND
+        for rom in carts.values():
+            jobs[(rom, 2 if bank else 1)] = name
+    workers = max(1, min(len(jobs), (os.cpu_count() or 2) // 2, 8))
+    print(f'[bench] compiling {len(jobs)} translations into {os.environ["RLENV_JIT_CACHE"]} ({workers} processes)',
+          file=sys.stderr, flush=True)
+    with ProcessPoolExecutor(workers) as pool:
+        for (job, name), (rc, out, sec, err) in zip(jobs.items(), pool.map(_compile_one, list(jobs))):
+            print(f'[bench] {name}: {out[0]} blocks, {out[1]} instructions, {sec:.1f} s, {out[4]} far jumps' +
+                  (f' FAILED: {err}' if rc else ''), file=sys.stderr, flush=True)
 
 
 def run_workload(args, name, steps, warmup, baseline):
@@ -251,10 +296,14 @@ def bench_env(args, name, K, W, baseline):
 
     print(f'[bench] workload {name}: {N} consoles, warmup {W}, timed {K} decisions', file=sys.stderr, flush=True)
     env = RlEnv(counts, device=dev, **kw)
-    # the translated kernels of the fixed-PRG carts (compiled on threads of their own while the env is created):
-    # warmup, parity and the timed region all run them
+    # the translated kernels (compiled on the library's compile thread, or found in the translation cache): warmup,
+    # parity and the timed region all run them; a translation that failed (its compile or its far-jump check)
+    # leaves its game on the library's kernel, as in any env
     t_jit = time.perf_counter()
-    env.jit_wait()
+    try:
+        env.jit_wait()
+    except RuntimeError as ex:
+        print(f'[bench] {ex}', file=sys.stderr, flush=True)
     translated = [dict(game=g, **env.jit_status(gi)) for gi, g in enumerate(counts)]
     translated = [t for t in translated if t['state'] != 'none']
     if translated:
@@ -323,7 +372,7 @@ def bench_env(args, name, K, W, baseline):
                data='synthetic: seed-generated cartridges (rl.synth), uniform random pad bytes', config=cfg,
                emulated_instructions_per_s=round(float(instr1 - instr0) / dt, 1),
                step_output_gbps=round(out_bytes * N * K / dt / 1e9, 3))
-    if translated:   # fixed-PRG games whose decision frames ran their translated kernel
+    if translated:   # games whose decision frames ran their translated kernel (state 'loaded')
         out['translated'] = translated
     if kern:
         out['roofline'] = _roofline(name, kern, N, K, dt, out_bytes)
@@ -510,8 +559,8 @@ def _cpu_env(args, w, game, kw, pads_host, snap, ncmp, W, baseline):
 
 
 def bench_reward10(args, K, W, baseline):
-    """The SMB reward tracker alone (rl10_smb_run): T steps of N envs over seed-generated RAM trajectories, one
-    env per lane; value in env-steps/s."""
+    """The SMB reward tracker alone (rl10_smb_run): T steps of N envs over seed-generated RAM trajectories, timed per
+    call (its three kernels); value in env-steps/s."""
     import torch
     from rl import synth
     from rl.rlenv import hip_library
@@ -560,10 +609,15 @@ def bench_reward10(args, K, W, baseline):
                ms_per_step=round(dt * 1e3 / K, 3), higher_is_better=True, scaling='weak', vs_baseline=None,
                dtype='f64', data='synthetic: seed-generated SMB RAM trajectories (rl.synth.smb_ram15)',
                config=dict(workload='reward10', envs=N, steps_per_run=T, frames_per_step=4),
-               kernels=dict(k_rl10_smb=dict(ms_per_launch=round(kms, 4), alg_bytes_per_launch=alg,
-                                            achieved_gbps=round(achieved, 3))),
-               roofline=dict(kernel='k_rl10_smb', bound='hbm', achieved=round(achieved, 3), peak=HBM_PEAK_GBPS,
-                             unit='GB/s', frac=round(achieved / HBM_PEAK_GBPS, 6), traffic=_traffic('k_rl10_smb', 1)))
+               kernels=dict(rl10_smb_run=dict(ms_per_launch=round(kms, 4), alg_bytes_per_launch=alg,
+                                              achieved_gbps=round(achieved, 3),
+                                              clocks_per_step=round(kms * 1e-3 * CLOCK_HZ / T, 1),
+                                              launches='k_smb_signals, k_smb_chain, k_smb_reward')),
+               roofline=dict(kernel='rl10_smb_run', bound='hbm', achieved=round(achieved, 3), peak=HBM_PEAK_GBPS,
+                             unit='GB/s', frac=round(achieved / HBM_PEAK_GBPS, 6), traffic=None, limiter='latency',
+                             note='k_smb_chain, one env per lane for T steps in order, issues one instruction of a '
+                                  'step every 4 cycles (one wave per SIMD on 128 of them); the signals and the '
+                                  'rewards run over all env-steps in parallel'))
     if not args.no_cpu:
         got_r, got_d = rew.cpu().numpy(), done.cpu().numpy()
         lib_o = _oracle()

@@ -40,6 +40,7 @@
 #include "env_dev.h"
 #include "jit.h"
 #include "jit_check.h"
+#include "smb_tracker.h"
 #include "nes_dev.h"
 #include "optab.h"
 #include "render_dev.h"
@@ -335,44 +336,115 @@ __global__ void k_gather_rows(uint4* __restrict__ dst, const uint4* __restrict__
     for (size_t i = blockIdx.y * blockDim.x + threadIdx.x; i < row_vecs; i += (size_t)gridDim.y * blockDim.x) d[i] = s[i];
 }
 
-// Standalone reward10 SMB tracker: one env per lane, T steps; per step one 16-byte load and a 5-byte result. The loads
-// do not depend on the tracker, so they run ahead: two register buffers of kAhead steps each, one filled while the
-// other is consumed (a register move out of a buffer would wait for its load). 64-lane blocks spread the waves over
-// as many CUs as there are waves (8192 envs: 128 waves).
-constexpr int kAhead = 4;
-__device__ __forceinline__ void smb_step(const uint4& q, int frames, Rl10State& st, float* __restrict__ reward,
-                                         uint8_t* __restrict__ done, size_t at) {
-    uint8_t b[16];
-    memcpy(b, &q, 16);
-    const ev::Out u = ev::update(ev::smb_signals(b), frames, st, rl10_game(RL10_SMB));
-    reward[at] = (float)u.reward;
-    done[at] = u.done ? 1 : 0;
+// Standalone reward10 SMB tracker (smb_tracker.h): the signals and what depends only on them for every env-step in
+// parallel, the tracker state env by env, the rewards in parallel.
+// 1. Four consecutive steps of one env per thread (rows t-1 .. t+3 of ram15 read once).
+__global__ __launch_bounds__(256) void k_smb_signals(const uint8_t* __restrict__ ram15, int T, int N,
+                                                      const Rl10State* __restrict__ state, ev::SmbStep* __restrict__ rec) {
+    const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
+    const size_t groups = (size_t)((T + 3) / 4) * (size_t)N;
+    if (i >= groups) return;
+    const int e = (int)(i % (size_t)N), t0 = (int)(i / (size_t)N) * 4;
+    const uint4* src = reinterpret_cast<const uint4*>(ram15);
+    const Rl10Game G = rl10_game(RL10_SMB);
+    auto signals = [&](int t) {
+        const uint4 q = src[(size_t)t * N + e];
+        uint8_t b[16];
+        memcpy(b, &q, 16);
+        return ev::smb_signals(b);
+    };
+    Rl10Signals p;
+    bool had;
+    if (t0 > 0) {
+        p = signals(t0 - 1);
+        had = true;
+    } else {
+        p = state[e].prev;
+        had = state[e].has_prev != 0;
+    }
+    for (int k = 0; k < 4 && t0 + k < T; ++k) {
+        const Rl10Signals s = signals(t0 + k);
+        rec[(size_t)(t0 + k) * N + e] = ev::smb_step_record(s, p, had, G);
+        p = s;
+        had = true;
+    }
 }
-__global__ __launch_bounds__(64) void k_rl10_smb(const uint8_t* __restrict__ ram15, int T, int N, int frames,
-                                                 Rl10State* __restrict__ state, float* __restrict__ reward,
-                                                 uint8_t* __restrict__ done) {
+// 2. One env per lane (64-lane blocks: as many CUs as waves), its steps in order; the records of kAhead steps are
+// loaded ahead in two register buffers, through row bases that are the same for the whole wave.
+constexpr int kAhead = 4;
+__global__ __launch_bounds__(64) void k_smb_chain(ev::SmbStep* __restrict__ rec, const uint8_t* __restrict__ ram15,
+                                                   int T, int N, int frames, Rl10State* __restrict__ state) {
     const int e = (int)(blockIdx.x * blockDim.x + threadIdx.x);
     if (e >= N) return;
-    const uint4* src = reinterpret_cast<const uint4*>(ram15);
-    // step t's 16 bytes (a step past the end reads the last one again, unused)
-    auto load = [&](int t) { return src[(size_t)min(t, T - 1) * N + e]; };
+    const Rl10Game G = rl10_game(RL10_SMB);
+    const int64_t stall = G.stall_frames >= 0.0 ? (int64_t)__builtin_ceil(G.stall_frames) : -1;
+    auto row = [&](int t) { return rec + (size_t)(uint32_t)min(t, T - 1) * (uint32_t)N; };
+    auto put = [&](int t, const ev::SmbDec& d) { reinterpret_cast<ev::SmbDec*>(row(t))[e] = d; };
     Rl10State st = state[e];
-    uint4 a[kAhead], b[kAhead];
+    ev::SmbChain c{st.done ? 1u : 0u, st.end_reason, st.has_best_level ? st.best_level : -1,
+                   st.has_best_progress ? (int32_t)st.best_progress : ev::kNoBest, ev::kNoBest, st.deaths,
+                   st.idle_frames, st.score_used};
+    ev::SmbStep a[kAhead], b[kAhead];
 #pragma unroll
-    for (int j = 0; j < kAhead; ++j) a[j] = load(j);
+    for (int j = 0; j < kAhead; ++j) a[j] = row(j)[e];
     int t = 0;
     for (; t + 2 * kAhead <= T; t += 2 * kAhead) {
 #pragma unroll
-        for (int j = 0; j < kAhead; ++j) b[j] = load(t + kAhead + j);
+        for (int j = 0; j < kAhead; ++j) b[j] = row(t + kAhead + j)[e];
 #pragma unroll
-        for (int j = 0; j < kAhead; ++j) smb_step(a[j], frames, st, reward, done, (size_t)(t + j) * N + e);
+        for (int j = 0; j < kAhead; ++j) put(t + j, ev::smb_chain_step(a[j], frames, c, stall));
 #pragma unroll
-        for (int j = 0; j < kAhead; ++j) a[j] = load(t + 2 * kAhead + j);
+        for (int j = 0; j < kAhead; ++j) a[j] = row(t + 2 * kAhead + j)[e];
 #pragma unroll
-        for (int j = 0; j < kAhead; ++j) smb_step(b[j], frames, st, reward, done, (size_t)(t + kAhead + j) * N + e);
+        for (int j = 0; j < kAhead; ++j) put(t + kAhead + j, ev::smb_chain_step(b[j], frames, c, stall));
     }
-    for (; t < T; ++t) smb_step(load(t), frames, st, reward, done, (size_t)t * N + e);   // the last T % 8 steps
+    for (; t < T; ++t) put(t, ev::smb_chain_step(row(t)[e], frames, c, stall));   // the last T % 8 steps
+    st.done = (uint8_t)c.done;
+    st.end_reason = (uint8_t)c.end_reason;
+    st.has_best_level = c.best_level >= 0 ? 1 : 0;
+    if (c.best_level >= 0) st.best_level = c.best_level;
+    st.has_best_progress = c.best_progress != ev::kNoBest ? 1 : 0;
+    if (c.last_progress != ev::kNoBest) st.best_progress = (double)c.last_progress;
+    st.deaths = c.deaths;
+    st.idle_frames = c.idle;
+    st.score_used = c.score_used;
+    if (T > 0) {   // update's prev: the signals of the last step
+        const uint4 q = reinterpret_cast<const uint4*>(ram15)[(size_t)(T - 1) * N + e];
+        uint8_t bb[16];
+        memcpy(bb, &q, 16);
+        st.has_prev = 1;
+        st.prev = ev::smb_signals(bb);
+    }
     state[e] = st;
+}
+// 3. The rewards and done flags of every env-step.
+__global__ __launch_bounds__(256) void k_smb_reward(const ev::SmbDec* __restrict__ dec, size_t n, int frames,
+                                                     float* __restrict__ reward, uint8_t* __restrict__ done) {
+    const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= n) return;
+    const ev::SmbDec d = dec[i];
+    reward[i] = (float)ev::smb_reward(d, frames, rl10_game(RL10_SMB));
+    done[i] = (d.flags & ev::DC_DONE) ? 1 : 0;
+}
+
+// The per-step records of rl10_smb_run come from a stream-ordered pool of the device (allocated and freed on the
+// caller's stream, so calls on different streams never share one), which keeps its memory for the next call.
+hipMemPool_t smb_pool(int device) {
+    static std::mutex lock;
+    static std::map<int, hipMemPool_t> pools;
+    std::lock_guard<std::mutex> hold(lock);
+    auto it = pools.find(device);
+    if (it != pools.end()) return it->second;
+    hipMemPoolProps props{};
+    props.allocType = hipMemAllocationTypePinned;
+    props.location.type = hipMemLocationTypeDevice;
+    props.location.id = device;
+    hipMemPool_t pool = nullptr;
+    if (hipMemPoolCreate(&pool, &props) != hipSuccess) throw std::runtime_error("hipMemPoolCreate failed");
+    uint64_t keep = ~0ull;
+    (void)hipMemPoolSetAttribute(pool, hipMemPoolAttrReleaseThreshold, &keep);
+    pools.emplace(device, pool);
+    return pool;
 }
 
 // Standalone reward10 tracker of any game: one env per thread, T steps over the 2 KB RAM of each env-step.
@@ -1644,7 +1716,7 @@ int rlenv_jit_translate(const uint8_t* rom, size_t rom_size, int compile, int32_
         if (compile) {
             JitJob job;
             job.blocks = std::move(jp.cases);
-            job.source = jit_module_source(false, !fixed32);
+            job.source = jit_module_source(compile >= 2, !fixed32);   // 2: with the frame-bank kernel
             jit_compile(job);
             out[2] = (int32_t)(job.seconds * 1000.0);
             out[3] = (int32_t)job.code.size();
@@ -1752,10 +1824,29 @@ int rl_gather_envs(void* dst, const void* src, const int64_t* envs, int n, int T
 
 int rl10_smb_run(const uint8_t* ram15, int T, int N, int frames, void* state, float* reward, uint8_t* done,
                  void* stream) {
-    if (N > 0)
-        hipLaunchKernelGGL(k_rl10_smb, dim3((N + 63) / 64), dim3(64), 0, static_cast<hipStream_t>(stream), ram15, T, N,
-                           frames, static_cast<Rl10State*>(state), reward, done);
-    return check("rl10_smb_run");
+    if (N <= 0 || T <= 0) return check("rl10_smb_run");
+    try {
+        const hipStream_t st = static_cast<hipStream_t>(stream);
+        int device = 0;
+        if (hipGetDevice(&device) != hipSuccess) throw std::runtime_error("hipGetDevice failed");
+        const size_t n = (size_t)T * (size_t)N;
+        void* rec = nullptr;
+        if (hipMallocFromPoolAsync(&rec, n * sizeof(ev::SmbStep), smb_pool(device), st) != hipSuccess)
+            throw std::runtime_error("rl10_smb_run: no device memory for the per-step records");
+        const size_t groups = (size_t)((T + 3) / 4) * (size_t)N;
+        hipLaunchKernelGGL(k_smb_signals, dim3((unsigned)((groups + 255) / 256)), dim3(256), 0, st, ram15, T, N,
+                           static_cast<const Rl10State*>(state), static_cast<ev::SmbStep*>(rec));
+        hipLaunchKernelGGL(k_smb_chain, dim3((N + 63) / 64), dim3(64), 0, st, static_cast<ev::SmbStep*>(rec), ram15, T,
+                           N, frames, static_cast<Rl10State*>(state));
+        hipLaunchKernelGGL(k_smb_reward, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st,
+                           static_cast<const ev::SmbDec*>(rec), n, frames, reward, done);
+        const int bad = check("rl10_smb_run");
+        (void)hipFreeAsync(rec, st);
+        return bad;
+    } catch (const std::exception& ex) {
+        g_error = ex.what();
+        return 1;
+    }
 }
 
 int rl10_run(int game, const uint8_t* ram, int T, int N, const int32_t* frames, void* state, void* reader,

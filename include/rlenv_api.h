@@ -127,8 +127,11 @@ int rlenv_kernel_times(void* h, double* ms, int64_t* count, int n);
  *    (-1 while compiling).
  *  jit_translate: the translation of an iNES image (needs no GPU): out[6] = blocks, instructions, compile
  *    milliseconds, code-object bytes, far jumps and far jumps into live SCC (-1 and 0s without compile); text (if
- *    not null): the generated blocks, NUL-terminated, cut at text_cap. Non-zero for an image that does not parse, a
- *    failed compile or a code object that fails the check.
+ *    not null): the generated blocks, NUL-terminated, cut at text_cap. compile: 0 none, 1 the kernel of decision
+ *    frames drawn by the emulator's waves (the variant of several games or several rounds of waves), 2 with the
+ *    frame-bank kernel too (a one-game env of one round of waves); with RLENV_JIT_CACHE the code object is kept there
+ *    as rlenv_create would keep it, so a later create finds it. Non-zero for an image that does not parse, a failed
+ *    compile or a code object that fails the check.
  *  jit_check: the far-jump check of a gfx950 code object (an ELF as hiprtc returns it): a branch too far for its
  *    16-bit offset is compiled to s_getpc_b64 / s_add_u32 / s_addc_u32 / s_setpc_b64, whose adds overwrite SCC,
  *    and the compiler does not make sure that the code at the target does not read SCC first. out[2] = far jumps,

@@ -820,6 +820,8 @@ static void mmc2_resolve(NesRec* r, const NesCart* c) {
     mapper_sync(r, c);
 }
 
+void orc_mmc2_resolve(NesRec* r, const NesCart* c) { mmc2_resolve(r, c); }
+
 /* ------------------------------------------------------------------------------------------ PPU events */
 
 static uint64_t abs_dot(const NesRec* r) { return (uint64_t)r->frame * NES_FRAME_DOTS + r->frame_dot; }

@@ -82,6 +82,9 @@ void orc_dmc_reset(NesRec* r, uint64_t now);
 /* FCEUmm's sprite-0 hit of the logged frame from the log so far (tests): the frame dot from which an instruction
  * sees the flag (*hit = 1), else the end of sprite 0's lines, or 0 with sprite 0 below the picture. */
 uint32_t orc_sprite0_hit(const NesRec* r, const NesCart* c, int* hit);
+/* MMC2's vblank resolve (tests): the latches the logged frame's own pattern fetches leave, written to the board's
+ * latch registers with the CHR pages they select (patch:1790-1812). */
+void orc_mmc2_resolve(NesRec* r, const NesCart* c);
 /* orc_run_until with an instruction budget other than NES_BUDGET (tests of the budget exit). */
 uint32_t orc_run_until_budget(NesRec* r, const NesCart* c, uint64_t target, uint32_t budget);
 /* Hash of the 2 KB CPU RAM: sum over 32-bit words k of splitmix64(k << 32 | word_k) mod 2^64. */

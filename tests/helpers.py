@@ -53,6 +53,7 @@ def oracle():
         lib.orc_dmc_reset.argtypes = [P, U64]
         lib.orc_sprite0_hit.argtypes = [P, P, P]
         lib.orc_sprite0_hit.restype = U32
+        lib.orc_mmc2_resolve.argtypes = [P, P]
         lib.orc_run_until_budget.argtypes = [P, P, U64, U32]
         lib.orc_run_until_budget.restype = U32
         lib.orc_ram_hash.argtypes = [P]

@@ -179,3 +179,66 @@ def test_reward10_kernel_matches_reference_fixture_and_oracle():
     torch.cuda.synchronize()
     assert np.array_equal(rew.cpu().numpy(), want_r) and np.array_equal(done.cpu().numpy(), want_d)
     assert np.array_equal(state.cpu().numpy(), st)
+
+
+def stress_ram15(seed, n, steps, level_up_at):
+    """SMB RAM trajectories that reach every path of the tracker: synth.smb_ram15 with seeded overlays - a fifth of
+    the envs with a stuck position (idle frames up to the stall end), level steps and skips (end reason 3), wins (2)
+    and game overs (1), dying routines and pits, lives lost, score jumps past the cap and the level's budget, steps
+    out of play, and at step `level_up_at` a level step with the position invalid (the best progress left unset, as
+    update leaves it, at the end of a call)."""
+    ram = synth.smb_ram15(seed, n, steps)
+    rng = np.random.default_rng([0x53545245, seed])
+    stuck = rng.random(n) < 0.2
+    ram[:, stuck, 1:3] = ram[:1, stuck, 1:3]
+    u = rng.random((steps, n, 8))
+    lvl = ram[:, :, 5].astype(np.int64) + np.cumsum((u[:, :, 0] < 4e-3) + 2 * (u[:, :, 1] < 5e-4), axis=0)
+    ram[:, :, 5] = (lvl & 3).astype(np.uint8)
+    ram[:, :, 6] = np.minimum(ram[:, :, 6].astype(np.int64) + (lvl >> 2), 7).astype(np.uint8)
+    win = u[:, :, 2] < 2e-4                                     # mode 2 in world 8 (index 7)
+    ram[:, :, 7] = np.where(win, 2, np.where(u[:, :, 2] > 1 - 3e-4, 3, ram[:, :, 7]))
+    ram[:, :, 6] = np.where(win, 7, ram[:, :, 6])
+    ram[:, :, 0] = np.where(u[:, :, 3] < 0.02, 6, np.where(u[:, :, 3] > 0.99, 11, ram[:, :, 0]))
+    ram[:, :, 3] = np.where(u[:, :, 4] < 0.01, 2, ram[:, :, 3])
+    ram[:, :, 4] = (ram[:, :, 4].astype(np.int64) - (u[:, :, 5] < 2e-3)).astype(np.uint8)
+    ram[:, :, 8] = np.where(u[:, :, 6] < 0.01, 1, ram[:, :, 8])
+    jump = u[:, :, 7] < 5e-3
+    ram[:, :, 9:11] = np.where(jump[:, :, None], rng.integers(0, 10, (steps, n, 2)), ram[:, :, 9:11])
+    ram[level_up_at, :, 5] = (ram[level_up_at, :, 5] + 1) & 3
+    ram[level_up_at, :, 0] = 0
+    return ram
+
+
+@pytest.mark.gpu
+def test_reward10_kernel_every_path_over_split_calls():
+    """rl10_smb_run (the tracker in three passes: signals in parallel, the state env by env, the rewards in
+    parallel) against the oracle's tracker on trajectories that reach every end (level skip, win, game over, stall),
+    deaths, score budgets and rollbacks, over calls of 37, 1, 100 and 118 steps (the state carried between them, a
+    call ending right after a level step that left the best progress unset), 300 envs (a partial wave), 64 frames a
+    step (the stall limit within reach)."""
+    print('case: rl10_smb_run, 300 envs x 256 steps in calls of 37/1/100/118, every tracker path', flush=True)
+    lib = ctypes.CDLL(str(HIP_LIB))
+    lib.rl10_smb_run.argtypes = [ctypes.c_void_p, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_void_p,
+                                 ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p]
+    s = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    N, T, frames = 300, 256, 64
+    ram = stress_ram15(5, N, T, level_up_at=36)
+    st_c = np.zeros(N * 80, np.uint8)
+    st_g = torch.zeros(N * 80, dtype=torch.uint8, device='cuda')
+    t0 = 0
+    for n_steps in (37, 1, 100, 118):
+        part = np.ascontiguousarray(ram[t0:t0 + n_steps])
+        want_r = np.zeros((n_steps, N), np.float32)
+        want_d = np.zeros((n_steps, N), np.uint8)
+        assert oracle().rl10_smb_run(ptr(part), n_steps, N, frames, ptr(st_c), ptr(want_r), ptr(want_d), None) == 0
+        rew = torch.zeros(n_steps, N, dtype=torch.float32, device='cuda')
+        done = torch.zeros(n_steps, N, dtype=torch.uint8, device='cuda')
+        assert lib.rl10_smb_run(tptr(torch.from_numpy(part).cuda()), n_steps, N, frames, tptr(st_g), tptr(rew),
+                                tptr(done), s) == 0
+        torch.cuda.synchronize()
+        assert np.array_equal(rew.cpu().numpy(), want_r), (t0, n_steps)
+        assert np.array_equal(done.cpu().numpy(), want_d), (t0, n_steps)
+        assert np.array_equal(st_g.cpu().numpy(), st_c), (t0, n_steps)
+        t0 += n_steps
+    ends = st_c.reshape(N, 80)[:, 4]          # Rl10State.end_reason
+    assert set(np.unique(ends).tolist()) >= {1, 2, 3, 4}, np.unique(ends, return_counts=True)

@@ -15,7 +15,7 @@ no steal in the idle fast-forward) with the same 4-cycle instruction driver as t
 import numpy as np
 import pytest
 
-from helpers import Console
+from helpers import Console, ptr
 from rl import synth
 
 KB = 1024
@@ -454,6 +454,70 @@ def test_mmc2_renderer_fetch_then_flip_along_the_line():
     want[88:168] = 0x21
     for y in (0, 1, 7):
         assert np.array_equal(pix[y], want), y
+
+
+def resolve_frame(ctrl, mask, nt_cells, sprites, latches=(1, 1), events=(), mreg_latches=None):
+    """A logged frame on an MMC2 console and its vblank resolve (oracle orc_mmc2_resolve): header with ctrl, mask,
+    CHR banks $FD0 = 2, $FE0 = 3, $FD1 = 4, $FE1 = 5 and the given latches; nametable 0 cells {(row, col): tile},
+    every other cell tile 0; sprites [(y, tile)] (the rest of OAM off screen); events [(kind, dot, value, aux)].
+    Returns the latch registers and the CHR pages after the resolve."""
+    con = mmc2_con()
+    for addr, v in ((0xB000, 2), (0xC000, 3), (0xD000, 4), (0xE000, 5)):
+        con.write(addr, v)
+    if mreg_latches is not None:
+        con.mem('mreg', 8)[6:8] = mreg_latches
+    h = con.words('log', 16 + 512)
+    h[:] = 0
+    h[1] = ctrl | (mask << 8)
+    h[5] = 0b01000100                                           # vertical mirroring: nametables 0, 1, 0, 1
+    h[14] = 2 | (3 << 8) | (4 << 16) | (5 << 24)
+    h[15] = latches[0] | (latches[1] << 8)
+    for i, (kind, dot, value, aux) in enumerate(events):
+        h[16 + 2 * i] = kind | (dot << 8) | (4 << 4)             # a 4-cycle instruction
+        h[17 + 2 * i] = value | (aux << 8)
+    con.set('log_n', len(events), 'H')
+    nt = con.mem('nt', 2048)
+    nt[:] = 0
+    for (row, col), tile in nt_cells.items():
+        nt[32 * row + col] = tile
+    oam = con.mem('oam', 256)
+    oam[:] = 0xFF
+    for i, (y, tile) in enumerate(sprites):
+        oam[4 * i:4 * i + 4] = (y, tile, 0, 100)
+    con.lib.orc_mmc2_resolve(ptr(con.rec), con.cart_ptr())
+    return [int(x) for x in con.mem('mreg', 8)[6:8]], pages(con)[1]
+
+
+def test_mmc2_vblank_resolve_known_answers():
+    """The latches a frame's own pattern fetches leave (patch:1790-1812: every line's background slots, then at the
+    line's end the sprites of the next line, lines 0-239, from the latches of the frame's header; the hook of
+    patch:1390-1402: a fetch at $0FD0-$0FDF / $0FE0-$0FEF sets latch 0 to the $FD / $FE bank, $1FDx / $1FEx latch 1).
+    Each case is worked out by hand from those rules: which fetch of a trigger tile comes last in the frame."""
+    bg0, bg1, spr1 = 0x00, 0x10, 0x08                           # ctrl: background table 0 or 1; sprites at $1000
+    on = 0x18
+    # background, half 0: a $FD tile on row 3 (lines 24-31) and a $FE tile on row 10 (lines 80-87): row 10 is
+    # fetched last, so latch 0 ends on $FE (1); swapped, on $FD (0). Latch 1 keeps the header's value.
+    assert resolve_frame(bg0, on, {(3, 5): 0xFD, (10, 7): 0xFE}, [], latches=(0, 0)) == (
+        [1, 0], [12, 13, 14, 15, 16, 17, 18, 19])
+    assert resolve_frame(bg0, on, {(3, 5): 0xFE, (10, 7): 0xFD}, [], latches=(1, 1)) == (
+        [0, 1], [8, 9, 10, 11, 20, 21, 22, 23])
+    # only $xFD0-$xFEF triggers: $FC and $FF tiles fetched after the $FE one change nothing
+    assert resolve_frame(bg0, on, {(3, 5): 0xFE, (20, 1): 0xFC, (25, 9): 0xFF}, [], latches=(0, 0))[0] == [1, 0]
+    # background and sprites both through half 1: the $FE tile on row 29 (lines 232-239) is fetched in every one of
+    # those lines; a $FD sprite at y = 231 is fetched at the ends of lines 231-238 (for lines 232-239), before line
+    # 239's background, so latch 1 ends on $FE; at y = 232 its last fetch is at the end of line 239 (for line 240),
+    # after every background fetch, so latch 1 ends on $FD
+    assert resolve_frame(bg1 | spr1, on, {(29, 4): 0xFE}, [(231, 0xFD)], latches=(0, 0))[0] == [0, 1]
+    assert resolve_frame(bg1 | spr1, on, {(29, 4): 0xFE}, [(232, 0xFD)], latches=(0, 0))[0] == [0, 0]
+    # sprites alone (background off, sprites on): the sprite fetches still run and flip latch 1
+    assert resolve_frame(bg0 | spr1, 0x10, {}, [(100, 0xFE)], latches=(0, 0))[0] == [0, 1]
+    # rendering off: no fetch at all; the latches are the header's, not what the registers held before
+    assert resolve_frame(bg0 | spr1, 0x00, {(3, 5): 0xFD}, [(100, 0xFE)], latches=(1, 0), mreg_latches=(0, 1)) == (
+        [1, 0], [12, 13, 14, 15, 16, 17, 18, 19])
+    # a $2000 write in line 100 (NeSLE dot 100 * 341 + 150) moves the background to half 1: the $FD tile on row 3
+    # sets latch 0, the $FE tile on row 20 (lines 160-167, after the write) sets latch 1
+    ev = [(1, 100 * 341 + 150, bg1, 0)]
+    assert resolve_frame(bg0, on, {(3, 5): 0xFD, (20, 9): 0xFE}, [], latches=(1, 0), events=ev)[0] == [0, 1]
 
 
 def test_mmc2_synthetic_cart_flips_latches_while_rendering():
