@@ -87,7 +87,6 @@ ALG_BYTES = {
     'k_emu_idle': (0, 0),
     'k_archive': (0, 0),
 }
-EMULATORS = ('k_emu', 'k_emu_draw')
 
 
 def metric(consoles):
@@ -413,34 +412,50 @@ def _kernel_times(env, N, K, dt):
 
 def _roofline(name, kern, n, K, dt, out_bytes):
     """The dominant kernel (the most time per step): its algorithmic bytes per launch over its average launch time
-    against HBM (the `bound`/`frac` of the line), what actually limits it (`limiter`) with its scalar and vector issue
-    fractions, and the whole step against HBM. Issue: the kernel's SALU and VALU instructions per launch from the
-    committed counter run of the same workload (profiles/counters.json, a deterministic workload) over this run's
-    average launch time, against one instruction per CU per clock each (256 CUs at 2.4 GHz)."""
+    against HBM (the `bound`/`frac` of the line), and the whole step against HBM. Where the committed counter run of
+    the same workload (profiles/counters.json, a deterministic workload) covers the kernels, what actually limits
+    them: `issue` gives the dominant kernel's SALU and VALU instructions per launch over this run's average launch time,
+    `step_issue` every profiled kernel's instructions per step over this run's step time, each against one instruction
+    per CU per clock (256 CUs at 2.4 GHz), and `limiter` names the largest of the step's scalar issue, vector issue and
+    HBM fractions."""
     dom = max(kern, key=lambda k: kern[k]['ms_per_step'])
     d = kern[dom]
     step_gbps = out_bytes * n * K / dt / 1e9
     hbm_frac = d['achieved_gbps'] / HBM_PEAK_GBPS
     r = dict(kernel=dom, bound='hbm', achieved=d['achieved_gbps'], peak=HBM_PEAK_GBPS, unit='GB/s',
-             frac=round(hbm_frac, 6), traffic=_traffic(dom, n) if name == HEADLINE else None,
+             frac=round(hbm_frac, 6), traffic=_traffic(name, dom, n),
              step_achieved_gbps=round(step_gbps, 3),
              step_frac=round(step_gbps / HBM_PEAK_GBPS, 6))
-    c = (_counters(name) or {}).get(dom)
-    if dom in EMULATORS and c and c.get('insts_salu') and c.get('dispatches'):
+    cs = _counters(name) or {}
+    c = cs.get(dom)
+    if c and c.get('insts_salu') and c.get('dispatches'):
         per_s = d['ms_per_launch'] * 1e-3
-        salu = c['insts_salu'] / c['dispatches'] / per_s / SALU_PEAK
-        valu = c['insts_valu'] / c['dispatches'] / per_s / VALU_PEAK
-        r['limiter'] = 'salu' if salu >= max(valu, hbm_frac) else 'valu' if valu >= hbm_frac else 'hbm'
-        r['issue'] = dict(salu_frac=round(salu, 4), valu_frac=round(valu, 4), hbm_frac=round(hbm_frac, 6),
-                          salu_per_launch=c['insts_salu'] // c['dispatches'],
-                          valu_per_launch=c['insts_valu'] // c['dispatches'],
+        r['issue'] = dict(salu_frac=round(c['insts_salu'] / per_s / SALU_PEAK, 4),
+                          valu_frac=round(c['insts_valu'] / per_s / VALU_PEAK, 4), hbm_frac=round(hbm_frac, 6),
+                          salu_per_launch=c['insts_salu'], valu_per_launch=c['insts_valu'],
                           salu_per_emulated_instruction=(c.get('per_emulated_instruction') or {}).get('salu'),
                           counter_SALUBusy_pct=c.get('SALUBusy_pct'), counter_VALUBusy_pct=c.get('VALUBusy_pct'),
                           counter_VALUUtilization_pct=c.get('VALUUtilization_pct'),
-                          note='one console per wavefront, the 6502 on the scalar unit: bound by scalar issue; '
-                               'traffic is the console state staged through LDS, not algorithmic bytes')
+                          alone_ms_per_launch=c.get('ms_per_dispatch'))
+        if c.get('ms_per_dispatch'):     # the kernel alone (the counter runs serialise launches)
+            alone_s = c['ms_per_dispatch'] * 1e-3
+            r['issue'].update(salu_frac_alone=round(c['insts_salu'] / alone_s / SALU_PEAK, 4),
+                              valu_frac_alone=round(c['insts_valu'] / alone_s / VALU_PEAK, 4))
+    prof = [k for k in kern if k in cs and cs[k].get('insts_salu')]
+    if prof:
+        step_s = dt / K
+        salu = sum(cs[k]['insts_salu'] * kern[k]['launches_per_step'] for k in prof) / step_s / SALU_PEAK
+        valu = sum(cs[k]['insts_valu'] * kern[k]['launches_per_step'] for k in prof) / step_s / VALU_PEAK
+        step_hbm = r['step_frac']
+        r['step_issue'] = dict(salu_frac=round(salu, 4), valu_frac=round(valu, 4), hbm_frac=step_hbm,
+                               kernels=prof)
+        r['limiter'] = 'salu' if salu >= max(valu, step_hbm) else 'valu' if valu >= step_hbm else 'hbm'
+        r['note'] = ('one console per wavefront: the 6502 and the PPU event logic run on the scalar unit, which the '
+                     'renderer\'s per-line control flow shares; the emulator\'s memory traffic is console state staged '
+                     'through LDS, not algorithmic bytes')
     if name == 'rollout-pack6':
         r['host_link_gbps'] = round(PACK6_BYTES * n * K / dt / 1e9, 3)
+        r['limiter'] = 'host link'
         r['note'] = 'every decision\'s packed frames cross the host link (PCIe 5 x16, about 63 GB/s each way)'
     return r
 
@@ -450,19 +465,28 @@ def _summary():
 
 
 def _counters(workload):
-    """Issue and utilisation figures of the frame kernels from the committed counter summary, if present (figures of
-    the profiling session, not of this run)."""
-    keep = ('kernel', 'dispatches', 'insts_salu', 'insts_valu', 'SALUBusy_pct', 'VALUBusy_pct', 'VALUUtilization_pct',
-            'per_emulated_instruction', 'wave_state_pct')
+    """Issue and utilisation figures of the workload's kernels from the committed counter summary, if present
+    (figures of the profiling session, each kernel alone, not of this run)."""
+    keep = ('kernel', 'dispatches', 'ms_per_dispatch', 'insts_salu', 'insts_valu', 'SALUBusy_pct', 'VALUBusy_pct',
+            'VALUUtilization_pct', 'per_emulated_instruction', 'wave_state_pct')   # instructions: per launch
     w = _summary().get('workloads', {}).get(workload)
     return {k: {f: v[f] for f in keep if f in v} for k, v in w.items()} if w else None
 
 
-def _traffic(kernel, n):
-    """HBM bytes per launch of `kernel` from the committed counter summary (FETCH_SIZE + WRITE_SIZE scaled by the
-    copy-kernel calibration, taken on the headline workload), scaled to n consoles; None when it does not cover it."""
-    t = _summary().get('traffic', {}).get(kernel)
-    return round(t['bytes_per_console_launch'] * n) if t else None
+def _traffic(workload, kernel, n):
+    """HBM bytes per launch of `kernel` on `workload` from the committed counter summary (FETCH_SIZE + WRITE_SIZE
+    scaled by the copy-kernel calibration), scaled to n consoles; None when it does not cover them."""
+    t = _summary().get('traffic', {}).get(workload, {}).get(kernel)
+    return round(t['bytes_per_console_launch'] * n) if t and 'consoles' in t else None
+
+
+def _rl10_traffic(env_steps):
+    """HBM bytes of one tracker run (its three kernels) from the committed counter summary, scaled to env_steps."""
+    t = _summary().get('traffic', {}).get('reward10')
+    if not t or not all('env_steps' in v for v in t.values()):
+        return None
+    return round(sum((v['fetch_bytes_per_launch'] + v['write_bytes_per_launch']) / v['env_steps'] for v in t.values())
+                 * env_steps)
 
 
 def _instructions(env) -> int:
@@ -614,7 +638,8 @@ def bench_reward10(args, K, W, baseline):
                                               clocks_per_step=round(kms * 1e-3 * CLOCK_HZ / T, 1),
                                               launches='k_smb_signals, k_smb_chain, k_smb_reward')),
                roofline=dict(kernel='rl10_smb_run', bound='hbm', achieved=round(achieved, 3), peak=HBM_PEAK_GBPS,
-                             unit='GB/s', frac=round(achieved / HBM_PEAK_GBPS, 6), traffic=None, limiter='latency',
+                             unit='GB/s', frac=round(achieved / HBM_PEAK_GBPS, 6), traffic=_rl10_traffic(N * T),
+                             limiter='issue latency',
                              note='k_smb_chain, one env per lane for T steps in order, issues one instruction of a '
                                   'step every 4 cycles (one wave per SIMD on 128 of them); the signals and the '
                                   'rewards run over all env-steps in parallel'))

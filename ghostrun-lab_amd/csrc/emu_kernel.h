@@ -316,6 +316,12 @@ __device__ __forceinline__ const EmuArgs& late_args() {
     asm volatile("" : "+s"(p));
     return *p;
 }
+// The check, where each kernel that runs emu_body is defined: its type is void (EmuArgs), so its one explicit argument
+// is the EmuArgs at offset 0 of the kernel-argument segment that late_args reads (a second parameter, or one before
+// it, would make late_args read other bytes without any error).
+#define ND_EMU_KERNEL_ARGS(...)                                                             \
+    static_assert(__is_same(decltype(&__VA_ARGS__), void (*)(nd::EmuArgs)),                 \
+                  "a kernel that runs emu_body takes its EmuArgs as its only parameter (late_args)")
 
 // One console per wavefront (blockDim 64): the console index comes from blockIdx only, so every emulator value is
 // wave-uniform; lane 0 runs the 6502 on the scalar unit (SGPRs, uniform branches) with the console's memories in

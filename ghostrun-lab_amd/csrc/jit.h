@@ -402,10 +402,11 @@ inline std::string jit_module_source(bool bank, bool banked) {
                "#define RLENV_JIT_INC \"jit_blocks.inc\"\n#include \"emu_kernel.h\"\n") +
            (bank ? std::string("extern \"C\" __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(8, 8)))\n"
                                "void k_emu_jit(nd::EmuArgs a) { nd::emu_body<") +
-                       board + ", true, false>(a); }\n"
+                       board + ", true, false>(a); }\nND_EMU_KERNEL_ARGS(k_emu_jit);\n"
                  : std::string()) +
            "extern \"C\" __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(8, 8)))\n"
-           "void k_emu_jit_draw(nd::EmuArgs a) { nd::emu_body<" + board + ", false, true>(a); }\n";
+           "void k_emu_jit_draw(nd::EmuArgs a) { nd::emu_body<" + board + ", false, true>(a); }\n"
+           "ND_EMU_KERNEL_ARGS(k_emu_jit_draw);\n";
 }
 
 }  // namespace nd

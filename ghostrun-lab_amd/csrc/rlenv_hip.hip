@@ -60,6 +60,7 @@ template <uint32_t B, bool kBank, bool kDraw>
 __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(8, 8))) void k_emu_w(EmuArgs a) {
     emu_body<B, kBank, kDraw>(a);
 }
+ND_EMU_KERNEL_ARGS(k_emu_w<NES_BOARD_NROM, false, false>);
 
 // Power-on of one console record.
 __global__ void k_power_on(NesRec* rec, Cart cart) {
@@ -1758,7 +1759,7 @@ int rlenv_jit_status(void* h, int gi, int32_t* out) {
     out[1] = j ? (int32_t)j->blocks : 0;
     out[2] = j ? (int32_t)j->instructions : 0;
     out[3] = j && j->job && j->job->state.load() != 0 ? (int32_t)(j->job->seconds * 1000.0) : -1;
-    out[4] = j && j->bank ? 1 : 0;
+    out[4] = (j && j->bank ? 1 : 0) | (j && j->banked ? 2 : 0);
     out[5] = j && j->job && j->job->state.load() != 0 ? j->job->far_jumps : -1;
     return 0;
 }

@@ -268,12 +268,14 @@ class RlEnv:
 
     def jit_status(self, gi=0) -> dict:
         """State of game gi's translated kernel: state ('none', 'compiling', 'loaded', 'failed'), blocks,
-        instructions, compile_ms (-1 while compiling), bank (built for frames drawn from frame banks), far_jumps
-        (in its code object; -1 while compiling)."""
+        instructions, compile_ms (-1 while compiling), frame_bank (built for frames drawn from frame banks), banked
+        (a banked-PRG translation: blocks keyed by their PRG bank too), far_jumps (in its code object; -1 while
+        compiling)."""
         out = (ctypes.c_int32 * 6)()
         self._check(self.lib.rlenv_jit_status(self.h, gi, out))
         return dict(state=('none', 'compiling', 'loaded', 'failed')[out[0]], blocks=out[1], instructions=out[2],
-                    compile_ms=out[3], bank=bool(out[4]), far_jumps=out[5])
+                    compile_ms=out[3], frame_bank=bool(out[4] & 1), banked=bool(out[4] & 2),
+                    far_jumps=out[5])
 
     def set_episode_level_end(self, level):
         """End episodes (reason level_clear) on reaching level `level` + 1 (0: on reaching level 1); -1 = never, the

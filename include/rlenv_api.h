@@ -45,7 +45,8 @@ void rlenv_bind_obs(void* h, uint8_t* obs, uint8_t* emph);     /* rlenv_api.h:22
  * progress unit (NaN = not valid). level_deaths: deaths of game gi's saves (-1 = empty), cap entries, to host memory
  * (synchronous). place_save: env_idx[j] (index within game gi) -> slot_idx[j] (skipped where < levels), device
  * arrays, on `stream` after a step. place_copy: slot src[j] -> dst[j], host arrays, synchronous. level_layout: out[5]
- * = bytes of one saved console, key words per env, sizeof(Rl10State), cap, levels. */
+ * = bytes of one saved console, key words per env, bytes of one slot's tracker state (sizeof(Rl10Saved): the tracker and
+ * its game reader), cap, levels. */
 int rlenv_enable_level_starts(void* h, int cap);                                       /* rlenv_api.h:26 */
 int rlenv_enable_places(void* h, int cap, int levels);                                 /* rlenv_api.h:36 */
 void rlenv_set_level_plan(void* h, int gi, double p, const uint32_t* cdf);             /* rlenv_api.h:27 */
@@ -123,8 +124,8 @@ int rlenv_kernel_times(void* h, double* ms, int64_t* count, int n);
  *    records otherwise); non-zero, with the compile error in rlenv_error, when a compile, its check or its load
  *    failed (that game keeps the library's own kernel).
  *  jit_status: out[6] = state (0 no translation, 1 compiling, 2 loaded, 3 failed), blocks, instructions, compile
- *    milliseconds (-1 while compiling), 1 if built for frames drawn from frame banks, far jumps in the code object
- *    (-1 while compiling).
+ *    milliseconds (-1 while compiling), flags (1: built for frames drawn from frame banks, 2: a banked-PRG
+ *    translation, whose blocks are keyed by their PRG bank too), far jumps in the code object (-1 while compiling).
  *  jit_translate: the translation of an iNES image (needs no GPU): out[6] = blocks, instructions, compile
  *    milliseconds, code-object bytes, far jumps and far jumps into live SCC (-1 and 0s without compile); text (if
  *    not null): the generated blocks, NUL-terminated, cut at text_cap. compile: 0 none, 1 the kernel of decision

@@ -66,34 +66,47 @@ def test_product_device_code_has_no_packed_fp32_and_no_scratch(tmp_path):
     assert not [n for n, b in zip(names, scratch) if b], list(zip(names, scratch))
 
 
+TRANSLATED = {   # cart, board class, with the frame-bank kernel (a one-game env of one round of waves)
+    'nrom': (lambda synth: synth.nrom_cart(1), 'NES_BOARD_NROM', True),
+    'poll-bmi': (lambda synth: synth.poll_cart(1, bmi=True), 'NES_BOARD_NROM', False),
+    'mmc3': (lambda synth: synth.mmc3_cart(3, blocks=6, sub_blocks=4), 'NES_BOARD_MMC3', False),
+}
+
+
 @pytest.mark.skipif(not Path(HIPCC).exists(), reason='hipcc not installed')
-def test_translated_kernel_device_code_has_no_packed_fp32_and_no_scratch(tmp_path):
+@pytest.mark.parametrize('case', sorted(TRANSLATED))
+def test_translated_kernel_device_code_has_no_packed_fp32_and_no_scratch(tmp_path, case):
     """The kernels the library compiles at run time from a cartridge's translated blocks (jit.h: frames drawn from
-    frame banks, and frames the emulator's waves draw themselves, with the decision's finish), here the blocks of the
-    benchmark cart (rl.synth.nrom_cart(1)) as rlenv_jit_translate writes them, built with the same flags."""
+    frame banks, and frames the emulator's waves draw themselves, with the decision's finish), built with the same
+    flags: the benchmark cart's (both kernels), the poll cart with its BMI poll, and a banked MMC3 cart's (blocks by
+    PRG offset, the banked board class): no packed FP32, no scratch, 8 waves per SIMD."""
     import ctypes
     from rl import synth
     from rl.rlenv import bind_library
     from helpers import HIP_LIB
+    make, board, bank = TRANSLATED[case]
     lib = bind_library(HIP_LIB)
-    rom = synth.nrom_cart(1)
+    rom = make(synth)
     out = (ctypes.c_int32 * 6)()
-    text = ctypes.create_string_buffer(1 << 20)
+    text = ctypes.create_string_buffer(1 << 21)
     assert lib.rlenv_jit_translate(rom, len(rom), 0, out, text, len(text)) == 0
-    assert out[0] > 50 and out[1] > 200 and len(text.value) < len(text) - 1
+    assert out[0] > 20 and out[1] > 50 and len(text.value) < len(text) - 1
     (tmp_path / 'jit_blocks.inc').write_bytes(text.value)
     src = tmp_path / 'jit.hip'
-    src.write_text('#define RLENV_JIT_INC "jit_blocks.inc"\n#include "emu_kernel.h"\n'
-                   'extern "C" __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(8, 8)))\n'
-                   'void k_emu_jit(nd::EmuArgs a) { nd::emu_body<NES_BOARD_NROM, true, false>(a); }\n'
-                   'extern "C" __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(8, 8)))\n'
-                   'void k_emu_jit_draw(nd::EmuArgs a) { nd::emu_body<NES_BOARD_NROM, false, true>(a); }\n')
+    kernels = (['k_emu_jit'] if bank else []) + ['k_emu_jit_draw']
+    body = '#define RLENV_JIT_INC "jit_blocks.inc"\n#include "emu_kernel.h"\n'
+    if bank:
+        body += ('extern "C" __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(8, 8)))\n'
+                 f'void k_emu_jit(nd::EmuArgs a) {{ nd::emu_body<{board}, true, false>(a); }}\n')
+    body += ('extern "C" __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(8, 8)))\n'
+             f'void k_emu_jit_draw(nd::EmuArgs a) {{ nd::emu_body<{board}, false, true>(a); }}\n')
+    src.write_text(body)
     flags = makefile_flags()
     remarks = []
     asm = device_asm(src, tmp_path / 'jit.s', [f'-I{ROOT / "include"}', f'-I{CSRC}', f'-I{tmp_path}'] +
                      [f for f in flags if not f.startswith('--offload-arch') and f != '-O3' and f != '-std=c++17'],
                      remarks)
-    assert 'k_emu_jit' in asm and 'k_emu_jit_draw' in asm and not PACKED.search(asm)
+    assert all(k in asm for k in kernels) and not PACKED.search(asm)
     scratch = [int(x) for x in re.findall(r'ScratchSize \[bytes/lane\]: (\d+)', remarks[0])]
     occupancy = [int(x) for x in re.findall(r'Occupancy \[waves/SIMD\]: (\d+)', remarks[0])]
-    assert scratch == [0, 0] and occupancy == [8, 8], (scratch, occupancy)
+    assert scratch == [0] * len(kernels) and occupancy == [8] * len(kernels), (scratch, occupancy)

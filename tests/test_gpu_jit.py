@@ -36,7 +36,7 @@ def test_translated_benchmark_cart():
           flush=True)
     cpu, gpu, st = translated_pair(16, synth.nrom_cart(1), seed=5, sticky=True, idle_max=0, dropout=False,
                                    pad_mode=True)
-    assert st['bank']   # one game, one round of waves: decision frames drawn from frame banks
+    assert st['frame_bank'] and not st['banked']   # one game, one round of waves: frames drawn from frame banks
     run(cpu, gpu, 24, 0, True)
 
 
@@ -129,7 +129,7 @@ def test_translated_two_games_from_the_records():
     cpu = RlEnv({'smb': 8, 'tetris': 8}, device='cpu', lib_path=ORACLE_LIB, **kw)
     for gi in range(2):
         st = gpu.jit_status(gi)
-        assert st['state'] == 'loaded' and not st['bank'], st
+        assert st['state'] == 'loaded' and not st['frame_bank'], st
     g = torch.Generator().manual_seed(35)
     cpu.start()
     gpu.start()

@@ -97,7 +97,7 @@ def tptr(t):
     return ctypes.c_void_p(t.data_ptr())
 
 
-def subset_run(n, cart, ranges, decisions, act_seed, check_every=1, **kw):
+def subset_run(n, cart, ranges, decisions, act_seed, check_every=1, banked=None, **kw):
     """n consoles on the GPU, every decision of all of them; the oracle steps only the console ranges (with their own
     env indices, so their seeds and streams are the same) and every output of those consoles is compared (every
     check_every decisions, and at the last). A game of this size is translated (compiled in the background): the
@@ -107,6 +107,7 @@ def subset_run(n, cart, ranges, decisions, act_seed, check_every=1, **kw):
     gpu.jit_wait()
     st = gpu.jit_status(0)
     assert st['state'] == 'loaded', st
+    assert banked is None or st['banked'] == banked, st
     print(f'  translated: {st["blocks"]} blocks, {st["instructions"]} instructions, compiled in {st["compile_ms"]} '
           f'ms, {st["far_jumps"]} far jumps', flush=True)
     cpu = RlEnv({'smb': n}, device='cpu', lib_path=ORACLE_LIB, **kw)
@@ -171,5 +172,5 @@ def test_full_size_mmc3_two_wave_rounds_subset():
     cart (its far jumps checked), independent random pads; consoles 0-31 (first round) and 16352-16383 (second round)
     against the oracle for 16 decisions."""
     print('case: MMC3 seed 1, 16384 consoles, translated, 16 decisions, consoles 0-31 and 16352-16383', flush=True)
-    subset_run(16384, synth.mmc3_cart(1), [(0, 32), (16352, 16384)], 16, 43, seed=3, sticky=False, idle_max=0,
-               dropout=False, pad_mode=True)
+    subset_run(16384, synth.mmc3_cart(1), [(0, 32), (16352, 16384)], 16, 43, banked=True, seed=3, sticky=False,
+               idle_max=0, dropout=False, pad_mode=True)
