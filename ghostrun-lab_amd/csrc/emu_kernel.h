@@ -324,8 +324,9 @@ __device__ __forceinline__ const EmuArgs& late_args() {
                   "a kernel that runs emu_body takes its EmuArgs as its only parameter (late_args)")
 
 // One console per wavefront (blockDim 64): the console index comes from blockIdx only, so every emulator value is
-// wave-uniform; lane 0 runs the 6502 on the scalar unit (SGPRs, uniform branches) with the console's memories in
-// LDS, the 64 lanes copy them in and out. Eight waves per SIMD: 8192 consoles fill 256 CUs x 4 SIMDs x 8 in one
+// wave-uniform; lane 0 (every lane on MMC2) runs the 6502 on the scalar unit (SGPRs, uniform branches) with the
+// console's memories in LDS, the 64 lanes copy them in and out. Eight waves per SIMD: 8192 consoles fill 256 CUs x 4
+// SIMDs x 8 in one
 // round (left to itself the compiler takes 71 VGPRs, 7 waves, and the eighth wave of every SIMD runs after the
 // others).
 // kBank: a decision frame whose picture is drawn from a frame bank (its render state is copied there at the end).
@@ -356,7 +357,12 @@ __device__ __forceinline__ void emu_body(const EmuArgs& a) {
     wave_copy16(L.oam, rec->oam, NES_OAM_BYTES, lane);
     wave_copy16(L.pal, rec->pal, NES_PAL_BYTES, lane);
     __syncthreads();
-    if (lane == 0) {
+    // An MMC2 console is emulated on all 64 lanes, every lane doing the same (every value is wave-uniform, and every
+    // store writes the same value to the same place), so that the line replays of its sprite-0 check and vblank
+    // latch resolve can spread a run's pattern fetches over the lanes (replay_dev.h rs_mmc2_fetches); any other
+    // console on lane 0.
+    const bool wide = B != NES_BOARD_NROM && a.g.cart.board == NES_BOARD_MMC2;
+    if (lane == 0 || wide) {
         uint32_t pad = 0, fault = 0;
         uint64_t target;
         if (a.mode == EMU_BOOT) {

@@ -61,18 +61,17 @@ struct RenderSink {
     }
     __device__ uint32_t nt(uint32_t i) { return uni(ntab[i]); }
     __device__ uint32_t oam(uint32_t i) { return uni(otab[i]); }
+    __device__ uint32_t nt_lane(uint32_t i) { return ntab[i]; }
+    __device__ uint32_t oam_lane(uint32_t i) { return reinterpret_cast<const uint32_t*>(otab)[i]; }
     __device__ uint32_t back() { return ((uint32_t)L->pal[0] & 0x3Fu) | 0x40u; }
     __device__ void palette(uint32_t i, uint32_t v) {
         if (lane == 0) L->pal[i] = (uint8_t)v;
         __syncthreads();
         bg_stale = sp_stale = true;
     }
-    __device__ void slot_pages(int32_t j, uint32_t pk) {
-        if (lane == 0) L->pages[j] = pk;
-    }
-    __device__ void sprite_pages(uint32_t n, uint32_t pk) {
-        if (lane == 0) L->pages[34 + n] = pk;
-    }
+    // MMC2: the pages of slot j's fetch, of the fetch of the line's sprite n (on the lane of the fetch)
+    __device__ void slot_pages(int32_t j, uint32_t pk) { L->pages[j] = pk; }
+    __device__ void sprite_pages(uint32_t n, uint32_t pk) { L->pages[34 + n] = pk; }
     // The latched sprite line expanded into L->sp (before the line's first sync; the compose reads and clears it).
     __device__ void expand_sprites(const Rs& s) {
         if (!s.spork) return;

@@ -16,8 +16,10 @@
 //     0's lines only; tiles are fetched lazily from descriptors of the slots, lines without writes are skipped in
 //     closed form;
 //   - LatchSink (here): MMC2's latch resolve, which needs no pixels at all.
-// MMC2's latch hook after every pattern fetch is run by the walker itself, slot by slot, so the sinks only receive the
-// CHR pages each fetch read through.
+// MMC2's latch hook after every pattern fetch is run by the walker itself, the fetches of a run of slots (or of a
+// sprite line) on the lanes of the wavefront at once, so the sinks only receive the CHR pages each fetch read through.
+// That part needs every lane active: the renderer's waves are, and an MMC2 console's emulation runs on all 64 lanes
+// (emu_kernel.h emu_body).
 #pragma once
 #ifndef __HIPCC_RTC__   // (built in where hiprtc compiles this at run time)
 #include <stdint.h>
@@ -121,13 +123,34 @@ __device__ __forceinline__ void rs_mmc2_select(Rs& s, uint32_t half) {
     if (half) s.chr_hi = pk;
     else s.chr_lo = pk;
 }
-// MMC2: the latch hook of a pattern fetch at a.
-__device__ __forceinline__ void rs_hook(Rs& s, uint32_t a) {
-    const uint32_t t = mmc2_trigger(a);
-    if (t == 0) return;
-    const uint32_t half = t >> 2;
-    s.latch = (s.latch & ~(0xFFu << (8u * half))) | (((t & 3u) - 1u) << (8u * half));
-    rs_mmc2_select(s, half);
+// This lane's index in the wavefront.
+__device__ __forceinline__ uint32_t lane_id() { return __builtin_amdgcn_mbcnt_hi(~0u, __builtin_amdgcn_mbcnt_lo(~0u, 0u)); }
+
+// MMC2: a run of pattern fetches, one per lane in fetch order (lane order, `mine` on the lanes that fetch, at pa),
+// with every lane of the wavefront active. Each fetch reads through its half's pages as the hooks of the fetches
+// before it left them, then flips its half's latch if pa is a trigger (FCEUmm's PPU_hook after the fetch,
+// patch:1390-1402): the page it read through is returned on its lane, and the latches and pages after the whole run
+// are left in s. The same as hooking one fetch at a time: a fetch's pattern address does not depend on the latches.
+__device__ inline uint32_t rs_mmc2_fetches(Rs& s, bool mine, uint32_t pa) {
+    const uint32_t t = mine ? mmc2_trigger(pa) : 0u, half = (pa >> 12) & 1u;
+    const uint64_t t0 = __ballot(t != 0u && (t & 4u) == 0u), t1 = __ballot((t & 4u) != 0u);
+    const uint64_t fe = __ballot((t & 3u) == 2u);   // triggers that set their latch to 1 ($xFE0-$xFEF)
+    const uint64_t before = (half ? t1 : t0) & (((uint64_t)1 << lane_id()) - 1u);
+    uint32_t pk = half ? s.chr_hi : s.chr_lo;
+    if (before) {   // the last trigger of this half before this fetch set the latch
+        const uint32_t bit = (uint32_t)(fe >> (63 - __builtin_clzll(before))) & 1u;
+        const uint32_t bank = (s.creg >> (8u * (2u * half + bit))) & 0xFFu;
+        pk = 0;
+        for (uint32_t i = 0; i < 4u; ++i) pk |= ((bank * 4u + i) & (s.mmc2_pages - 1u)) << (8u * i);
+    }
+    for (uint32_t h = 0; h < 2u; ++h) {
+        const uint64_t th = h ? t1 : t0;
+        if (!th) continue;
+        const uint32_t bit = (uint32_t)(fe >> (63 - __builtin_clzll(th))) & 1u;
+        s.latch = (s.latch & ~(0xFFu << (8u * h))) | (bit << (8u * h));
+        rs_mmc2_select(s, h);
+    }
+    return pk;
 }
 
 // The replay from the log header (patch:1361-1383): `log` = header + events (global memory), `n` events (read through
@@ -220,12 +243,6 @@ __device__ inline void rs_begin_frame(Rs& s, K& k) {
     if (rs_rendering(s)) s.v = s.t;
 }
 
-// Pattern address of tile slot fetch at v.
-template <class K>
-__device__ __forceinline__ uint32_t rs_pattern_addr(const Rs& s, K& k, uint32_t v) {
-    return k.nt(nt_slot(s.nt_map, 0x2000u | (v & 0x0FFFu))) * 16u + ((s.ctrl & 0x10u) << 8) + ((v >> 12) & 7u);
-}
-
 // One line being drawn: the next tile slot, the output position, the vertical step still due.
 struct Ln {
     int32_t tile, out;
@@ -244,12 +261,17 @@ __device__ inline void rs_tiles(Rs& s, K& k, Ln& ln, int32_t last, bool pixels) 
         ln.tile = last;
         return;
     }
-    if (s.mmc2_pages) {
-        for (int32_t j = first; j < last; ++j) {
-            const uint32_t pa = rs_pattern_addr(s, k, v_steps(s.v, (uint32_t)(j - first)));
-            k.slot_pages(j, (pa & 0x1000u) ? s.chr_hi : s.chr_lo);
-            rs_hook(s, pa);
+    if (s.mmc2_pages) {   // lane j fetches slot j
+        const int32_t j = (int32_t)lane_id();
+        const bool mine = j >= first && j < last;
+        uint32_t pa = 0;
+        if (mine) {
+            const uint32_t v = v_steps(s.v, (uint32_t)(j - first));
+            pa = k.nt_lane(nt_slot(s.nt_map, 0x2000u | (v & 0x0FFFu))) * 16u + ((s.ctrl & 0x10u) << 8) + ((v >> 12) & 7u);
         }
+        const uint32_t pk = rs_mmc2_fetches(s, mine, pa);
+        if (mine) k.slot_pages(j, pk);
+        __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");   // the pages, read by other lanes
     }
     k.on_run(s, first, last, ln.out, pixels);
     s.v = v_steps(s.v, (uint32_t)(last - first));
@@ -307,25 +329,29 @@ __device__ inline void rs_line(Rs& s, K& k, int32_t l, bool pixels) {
 }
 
 // Sprite-line fetch for line l + 1 (FetchSpriteData, patch:1671-1700): the sink fetches; MMC2's hooks run here in
-// OAM order (the sink gets each fetch's pages through sprite_pages).
+// OAM order, lane i = OAM entry i, the first eight entries on the line fetching (the sink gets each fetch's pages
+// through sprite_pages, on the lane of the entry, by its rank).
 template <class K>
 __device__ inline void rs_fetch_sprites(Rs& s, K& k, int32_t l) {
     if (s.mmc2_pages) {
         const uint32_t ctrl = s.ctrl, h = (ctrl & 0x20u) ? 16u : 8u;
         const uint32_t table8 = (ctrl & 0x08u) && !(ctrl & 0x20u) ? 0x1000u : 0u;
-        uint32_t n = 0;
-        for (uint32_t i = 0; i < 64u && n < 8u; ++i) {
-            const uint32_t y = k.oam(4u * i), row = (uint32_t)(l - (int32_t)y);
-            if (row >= h) continue;
-            const uint32_t tile = k.oam(4u * i + 1u), attr = k.oam(4u * i + 2u);
-            uint32_t pa = h == 16u ? ((tile & 1u) << 12) + ((tile & 0xFEu) << 4) : (tile << 4) + table8;
+        const uint32_t e = k.oam_lane(lane_id());   // y, tile, attribute, x
+        const uint32_t row = (uint32_t)(l - (int32_t)(e & 0xFFu));
+        const uint64_t on = __ballot(row < h);
+        const uint32_t rank = __builtin_amdgcn_mbcnt_hi((uint32_t)(on >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)on, 0u));
+        const bool mine = row < h && rank < 8u;
+        uint32_t pa = 0;
+        if (mine) {
+            const uint32_t tile = (e >> 8) & 0xFFu, attr = (e >> 16) & 0xFFu;
+            pa = h == 16u ? ((tile & 1u) << 12) + ((tile & 0xFEu) << 4) : (tile << 4) + table8;
             if (attr & 0x80u) pa += 7u - row + ((ctrl & 0x20u) >> 1) - (row & 8u);
             else pa += row + (row & 8u);
             pa &= 0x1FFFu;
-            k.sprite_pages(n, (pa & 0x1000u) ? s.chr_hi : s.chr_lo);
-            rs_hook(s, pa);
-            ++n;
         }
+        const uint32_t pk = rs_mmc2_fetches(s, mine, pa);
+        if (mine) k.sprite_pages(rank, pk);
+        __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
     }
     k.fetch_sprites(s, l);
 }
@@ -383,8 +409,11 @@ struct S0Sink {
     __device__ uint32_t ev(uint32_t i) { return uni(ev_mem[i]); }
     __device__ uint32_t nt(uint32_t i) { return uni(nt_mem[i]); }
     __device__ uint32_t oam(uint32_t i) { return uni(oam_mem[i]); }
+    __device__ uint32_t nt_lane(uint32_t i) { return nt_mem[i]; }
+    __device__ uint32_t oam_lane(uint32_t i) { return reinterpret_cast<const uint32_t*>(oam_mem)[i]; }
     __device__ void palette(uint32_t, uint32_t) {}
     __device__ uint32_t page(int32_t j) { return uni(pages[j]); }
+    // (MMC2 pages: written on the lane of the fetch)
     __device__ void slot_pages(int32_t j, uint32_t pk) { pages[j] = pk; }
     __device__ void sprite_pages(uint32_t n, uint32_t pk) {
         if (n == 0) pages[0] = pk;   // (the run's pages are done with by the time sprites are fetched)
@@ -575,6 +604,8 @@ struct LatchSink {
     __device__ uint32_t ev(uint32_t i) { return uni(ev_mem[i]); }
     __device__ uint32_t nt(uint32_t i) { return uni(nt_mem[i]); }
     __device__ uint32_t oam(uint32_t i) { return uni(oam_mem[i]); }
+    __device__ uint32_t nt_lane(uint32_t i) { return nt_mem[i]; }
+    __device__ uint32_t oam_lane(uint32_t i) { return reinterpret_cast<const uint32_t*>(oam_mem)[i]; }
     __device__ void palette(uint32_t, uint32_t) {}
     __device__ void slot_pages(int32_t, uint32_t) {}
     __device__ void sprite_pages(uint32_t, uint32_t) {}
