@@ -1,11 +1,13 @@
-// Device-side NES console for gfx950: one console per lane, hot registers in VGPRs, the 2 KB CPU RAM in LDS,
-// everything else in the console record in HBM (include/nesrec.h).
+// Device-side NES console for gfx950, one console per wavefront: its registers wave-uniform (scalar registers), its
+// 2 KB CPU RAM, nametables, OAM and palette in the wave's LDS, everything else in the console record in HBM
+// (include/nesrec.h). This file holds the console's generic step and what the fast paths share with it: the bus, the
+// PPU's timing events and frame log, the mappers and the DMC (the fast paths: wave_dev.h, jit.h).
 //
-// The 6502 is table-driven: one 32-bit descriptor per opcode (addressing mode, cycles, operation group and its
-// parameters, read/write/penalty flags) held in LDS. Every instruction runs the same fetch -> effective address
-// -> bus read -> group -> bus write sequence, so lanes on different opcodes diverge only inside the short group
-// switch and inside the bus decode. Instruction fetch is one 32-bit load from a widened PRG image (word i holds
-// PRG bytes i, i+1, i+2), so opcode and both operand bytes arrive in one memory access.
+// The generic 6502 step is table-driven: one 32-bit descriptor per opcode (addressing mode, cycles, operation group
+// and its parameters, read/write/penalty flags) in constant memory, read through the scalar cache. Every instruction
+// runs the same fetch -> effective address -> bus read -> group -> bus write sequence. Instruction fetch is one
+// 32-bit load from a widened PRG image (word i holds PRG bytes i, i+1, i+2), so the opcode and both operand bytes
+// arrive in one memory access.
 //
 // Semantics are those of the reference env's NES machine (kdcyberdude/ghostrun-lab): frame loop
 // rl/csrc/nes_machine.cuh:67-103, instruction step third_party/nesle-extensions.patch:823-862, bus side effects
