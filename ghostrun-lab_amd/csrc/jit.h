@@ -42,7 +42,9 @@ struct JitProgram {
 
 // Whether the instruction (op, b1, b2) at CPU address a always needs the generic step (fx returns kGeneric whatever
 // the registers): its memory class is fixed by a constant address.
-inline bool jit_always_generic(uint32_t a, uint32_t op, uint32_t b1, uint32_t b2) {
+// mmc3: an MMC3 image, whose bank writes at $8000-$9FFF the fast path may take (wave_dev.h mmc3_write_ok, decided at
+// run time: the block leaves before one it does not take).
+inline bool jit_always_generic(uint32_t a, uint32_t op, uint32_t b1, uint32_t b2, bool mmc3 = false) {
     const uint32_t d = kOptab.t[op], mode = d & 15u, grp = (d >> 8) & 15u;
     const bool rd = (d & D_READ) != 0, wr = (d & D_WRITE) != 0;
     if (grp == G_ILL || grp == G_BRK) return true;
@@ -55,7 +57,7 @@ inline bool jit_always_generic(uint32_t a, uint32_t op, uint32_t b1, uint32_t b2
     if (mode != M_ABS || grp == G_JSR) return false;
     const bool prg_ram = ea >= 0x6000u && ea < 0x8000u;   // served by the fast path except on MMC1 (decided then)
     if (rd && wr) return ea >= 0x2000u && !prg_ram;
-    if (wr) return ea >= 0x2000u && ea != 0x4016u && !prg_ram;
+    if (wr) return ea >= 0x2000u && ea != 0x4016u && !prg_ram && !(mmc3 && (ea & 0xE000u) == 0x8000u);
     if (rd) return !(ea < 0x2000u || ea >= 0x8000u || ea == 0x4016u || (ea & 0xE007u) == 0x2002u || prg_ram);
     return false;
 }
@@ -233,7 +235,7 @@ inline JitProgram jit_translate_fixed(const std::vector<uint8_t>& prg) {
 // target found, its offset within its 8 KB window in every page (any bank may be mapped there), and inside a page
 // the branch targets, return points and the instruction after an always-generic one. Blocks are kept in the order
 // they are found from the vectors first, within kJitMaxInstructions.
-inline JitProgram jit_translate_banked(const std::vector<uint8_t>& prg) {
+inline JitProgram jit_translate_banked(const std::vector<uint8_t>& prg, uint32_t board) {
     const uint32_t size = (uint32_t)prg.size(), pages = size >> 13;
     auto rd = [&](uint32_t o) { return o < size ? (uint32_t)prg[o] : 0u; };
     auto rd16 = [&](uint32_t o) { return rd(o) | (rd(o + 1u) << 8); };
@@ -243,7 +245,8 @@ inline JitProgram jit_translate_banked(const std::vector<uint8_t>& prg) {
     // the table holds the generic step's key where an instruction would end on its page's last byte (rlenv_hip.hip);
     // a jump to itself is found at run time (fx compares with the CPU address)
     auto generic = [&](uint32_t o) {
-        return (o & 0x1FFFu) + len_of(o) >= 0x2000u || jit_always_generic(0xFFFFFFFFu, rd(o), rd(o + 1u), rd(o + 2u));
+        return (o & 0x1FFFu) + len_of(o) >= 0x2000u ||
+               jit_always_generic(0xFFFFFFFFu, rd(o), rd(o + 1u), rd(o + 2u), board == NES_BOARD_MMC3);
     };
     auto target_of = [&](uint32_t o) { return o + 2u + (uint32_t)(int32_t)(int8_t)rd(o + 1u); };
     std::vector<int> order(size, -1);   // discovery rank of each leader

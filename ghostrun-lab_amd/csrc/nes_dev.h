@@ -56,6 +56,7 @@ struct Con {
     uint64_t dmc_event;
     uint32_t prg0, prg1, prg2, prg3;   // PRG byte offsets of $8000/$A000/$C000/$E000
     uint32_t nt_map;                   // 4 x 2 bits
+    uint32_t mmc3_sel;                 // MMC3: the bank select register ($8000), as in the record's mreg[8]
     // wave_dev.h run_until_wave's own state, parked here while a burst of fast instructions runs
     uint64_t b_dmc_event, b_target;
     uint32_t b_instructions, b_pending, b_to_event, b_ecyc, b_dmc_in, b_why, b_budget, b_nmi, b_irq;
@@ -264,7 +265,7 @@ __device__ inline void map_write(Con& c, const Mem& m, uint32_t addr, uint32_t v
         map_sync(c, m);
     } else if (m.cart.board == NES_BOARD_MMC3) {
         const uint32_t k = addr & 0xE001u;
-        if (k == 0x8000u) r[8] = (uint8_t)v;
+        if (k == 0x8000u) r[8] = (uint8_t)(c.mmc3_sel = v);
         else if (k == 0x8001u) r[r[8] & 7u] = (uint8_t)v;
         else if (k == 0xA000u) r[9] = (uint8_t)v;
         else {
@@ -1052,6 +1053,7 @@ __device__ inline void con_load(Con& c, const NesRec* r) {
     c.dmc_event = r->dmc_event;
     c.prg0 = r->prg_off[0]; c.prg1 = r->prg_off[1]; c.prg2 = r->prg_off[2]; c.prg3 = r->prg_off[3];
     c.nt_map = r->nt_map[0] | (r->nt_map[1] << 2) | (r->nt_map[2] << 4) | ((uint32_t)r->nt_map[3] << 6);
+    c.mmc3_sel = r->mreg[8];
 }
 
 __device__ inline void con_store(const Con& c, NesRec* r) {

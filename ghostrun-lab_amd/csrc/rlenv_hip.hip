@@ -519,7 +519,7 @@ const JitHeader kJitHeaders[] = {
 // hold no far-jump hazard whatever the layout).
 const char* const kJitOptions[] = {"--offload-arch=gfx950", "-O3", "-std=c++17", "-ffp-contract=off", "-fno-fast-math",
                                    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops", "-mllvm",
-                                   "-structurizecfg-skip-uniform-regions=true"};
+                                   "-structurizecfg-skip-uniform-regions=true", "-mllvm", "-enable-tail-merge=false"};
 std::vector<std::string> jit_options() {
     std::vector<std::string> o(std::begin(kJitOptions), std::end(kJitOptions));
     if (const char* extra = std::getenv("RLENV_JIT_EXTRA")) {
@@ -1370,7 +1370,7 @@ void* rlenv_create(int ngames, const int* game_ids, const uint8_t* const* roms, 
             }
             // the translation, and a fetch table with its blocks' keys (by CPU address, or by PRG offset)
             if (jit_mode == 3 || (jit_mode >= 1 && g.n >= kJitMinEnvs && (fixed32 || jit_mode == 2))) {
-                JitProgram jp = fixed32 ? jit_translate_fixed(img) : jit_translate_banked(p.prg);
+                JitProgram jp = fixed32 ? jit_translate_fixed(img) : jit_translate_banked(p.prg, p.board);
                 if (!jp.leader_addr.empty()) {
                     std::vector<uint32_t> fj(f);
                     for (size_t b = 0; b < jp.leader_addr.size(); ++b)
@@ -1702,7 +1702,7 @@ int rlenv_jit_translate(const uint8_t* rom, size_t rom_size, int compile, int32_
         const bool fixed32 = p.board == NES_BOARD_NROM || p.board == NES_BOARD_CNROM;
         std::vector<uint8_t> img(32768u);   // a fixed image as the CPU sees it: 16 KB mirrored
         for (size_t k = 0; k < img.size(); ++k) img[k] = p.prg[k % p.prg.size()];
-        JitProgram jp = fixed32 ? jit_translate_fixed(img) : jit_translate_banked(p.prg);
+        JitProgram jp = fixed32 ? jit_translate_fixed(img) : jit_translate_banked(p.prg, p.board);
         out[0] = (int32_t)jp.leader_addr.size();
         out[1] = (int32_t)jp.instructions;
         out[2] = -1;

@@ -99,7 +99,7 @@ __device__ __forceinline__ void hot_load(Hot& h, const Con& c) {
     h.pc = hot_pcs<B>(h, uni(c.pc));
     h.ctl = uni(c.shift) | (uni(c.strobe) << 8);
 }
-// (the PRG offsets change only in the generic step, which writes them to the console state itself)
+// (the PRG offsets change only in the generic step and mmc3_write, which write them to the console state themselves)
 template <uint32_t B>
 __device__ __forceinline__ void hot_store(const Hot& h, Con& c) {
     c.pc = hot_cpu<B>(h, h.pc) & 0xFFFFu; c.a = h.a; c.x = h.x; c.y = h.y; c.sp = h.sp; c.p = hflags(h);
@@ -167,6 +167,49 @@ template <uint32_t B>
 __device__ __forceinline__ uint32_t prg_index(const Hot& h, const Mem& m, uint32_t addr) {
     if constexpr (B == NES_BOARD_NROM) return addr & 0x7FFFu;   // the NROM image is 32 KB (16 KB mirrored)
     else return sel4((addr >> 13) & 3u, h.prg0, h.prg1, h.prg2, h.prg3) + (addr & 0x1FFFu);
+}
+
+// MMC3 bank writes the fast path takes (patch:3158-3162 the registers, 3037-3048 the PRG pages; nes_dev.h map_write
+// and map_sync): a bank select ($8000, even) that
+// keeps the PRG and CHR modes (bits 6 and 7), and a bank data write ($8001, odd) to R6 or R7, the switchable PRG
+// pages, unless it switches the page this instruction runs in (the next one is on the same page: kFetchWords).
+// Neither changes a CHR page or the mirroring, so nothing is logged for the renderer, and the IRQ counter is not
+// touched; every other write at $8000+ goes to the generic step. `mmc3_write_ok` only decides (no state change),
+// `mmc3_write` writes: the register, and the PRG page through to the console state, the record and h.
+template <uint32_t B>
+__device__ __forceinline__ bool mmc3_write_ok(const Hot& h, const Mem& m, const Con& cs, uint32_t ea, uint32_t v,
+                                              uint32_t pcs) {
+    if (m.cart.board != NES_BOARD_MMC3) return false;
+    const uint32_t k = ea & 0xE001u, sel = uni(cs.mmc3_sel);
+    if (k == 0x8000u) return ((sel ^ v) & 0xC0u) == 0u;
+    if (k != 0x8001u || (sel & 7u) < 6u) return false;
+    const uint32_t slot = (sel & 7u) == 7u ? 1u : (sel & 0x40u) ? 2u : 0u, cpu = hot_cpu<B>(h, pcs);
+    return cpu < 0x8000u || ((cpu >> 13) & 3u) != slot;
+}
+template <uint32_t B>
+__device__ __forceinline__ void mmc3_write(Hot& h, const Mem& m, Con& cs, uint32_t ea, uint32_t v) {
+    NesRec* r = m.rec;
+    const uint32_t sel = uni(cs.mmc3_sel);
+    if ((ea & 1u) == 0u) {
+        r->mreg[8] = (uint8_t)v;
+        cs.mmc3_sel = v;
+        return;
+    }
+    r->mreg[sel & 7u] = (uint8_t)v;
+    const uint32_t off = (v & (m.cart.prg_pages8 - 1u)) * 8192u;   // map_set_prg
+    if ((sel & 7u) == 7u) {
+        h.prg1 = off;
+        cs.prg1 = off;
+        r->prg_off[1] = off;
+    } else if (sel & 0x40u) {
+        h.prg2 = off;
+        cs.prg2 = off;
+        r->prg_off[2] = off;
+    } else {
+        h.prg0 = off;
+        cs.prg0 = off;
+        r->prg_off[0] = off;
+    }
 }
 
 // A PRG RAM byte ($6000-$7FFF, in the console record), as a scalar; the bus's read (nes_dev.h io_read) with the RAM
@@ -243,7 +286,8 @@ __device__ __forceinline__ uint32_t fx(Hot& h, const Mem& m, Con& cs, uint32_t p
         // Memory class, decided before any side effect (every check below comes before the first state change):
         // RAM, PRG RAM ($6000-$7FFF; on MMC1, whose register can disable it, the generic step), PRG reads, the
         // controller port and PPU status reads run here; any other I/O register, a read-modify-write elsewhere and
-        // any write at $8000+ (a mapper) go to the generic step. Written as chains of single compares: boolean
+        // any write at $8000+ (a mapper) but MMC3's PRG bank writes (mmc3_write_ok) go to the generic step. Written
+        // as chains of single compares: boolean
         // combinations of uniform conditions become lane-mask arithmetic.
         if constexpr (!zpage && rd && wr) {
             if (ea >= 0x2000u) {
@@ -256,8 +300,12 @@ __device__ __forceinline__ uint32_t fx(Hot& h, const Mem& m, Con& cs, uint32_t p
             if (ea >= 0x2000u) {
                 if (ea != 0x4016u) {
                     if (ea < 0x6000u) return kGeneric;
-                    if (ea >= 0x8000u) return kGeneric;
-                    if (m.cart.board == NES_BOARD_MMC1) return kGeneric;
+                    if (ea >= 0x8000u) {
+                        if constexpr (nrom) return kGeneric;
+                        else if (!mmc3_write_ok<B>(h, m, cs, ea, hget(h, src, 0), pcs)) return kGeneric;
+                    } else if (m.cart.board == NES_BOARD_MMC1) {
+                        return kGeneric;
+                    }
                 }
             }
         }
@@ -384,6 +432,7 @@ __device__ __forceinline__ uint32_t fx(Hot& h, const Mem& m, Con& cs, uint32_t p
             if constexpr (mode == M_ZP) m.ram[ea] = (uint8_t)res;
             else if constexpr (zpage) m.ram[ea & 0x7FFu] = (uint8_t)res;
             else if (ea < 0x2000u) m.ram[ea & 0x7FFu] = (uint8_t)res;
+            else if (!nrom && !rd && ea >= 0x8000u) mmc3_write<B>(h, m, cs, ea, res);
             else if (ea >= 0x6000u) m.rec->prg_ram[ea - 0x6000u] = (uint8_t)res;   // (a read-modify-write: here)
             else port_write(h, cs, res);
         }

@@ -5,8 +5,12 @@ adds overwrite SCC; the compiler does not make sure that the code at the target 
 translated kernel of the benchmark's MMC3 cart this happened at the join of the page select (a read of $9Fxx went
 through the $A000 window) and the pictures and RAM differed from the oracle's. The library checks every translated
 code object before it uses it; these tests pin the check on code objects built here: a hand-made far jump into
-s_cselect and its safe twin, the library's own kernels as built, and a translation compiled at run time."""
+s_cselect and its safe twin, the library's own kernels as built, and a translation compiled at run time; and, with
+every branch expanded into a far jump (-amdgpu-s-branch-bits=5), the library's kernels and a translation, which
+hold no such place with the build's flags (-enable-tail-merge=false: merged block tails were where SCC stayed live
+across a jump)."""
 import ctypes
+import os
 import struct
 import subprocess
 from pathlib import Path
@@ -98,3 +102,39 @@ def test_translation_compiled_at_run_time_passes_the_check():
     out = (ctypes.c_int32 * 6)()
     assert lib.rlenv_jit_translate(rom, len(rom), 1, out, None, 0) == 0, lib.rlenv_error()
     assert out[3] > 0 and out[5] == 0, list(out)
+
+
+CSRC = Path(__file__).resolve().parents[1] / 'ghostrun-lab_amd' / 'csrc'
+EVERY_BRANCH_FAR = ['-mllvm', '-amdgpu-s-branch-bits=5']
+
+
+@pytest.mark.skipif(not Path(HIPCC).exists(), reason='hipcc not installed')
+def test_library_kernels_hold_no_far_jump_hazard_with_every_branch_far(tmp_path):
+    """The library's kernels built with the Makefile's device flags and every branch expanded into a far jump: every
+    far jump lands where SCC is written first (with tail merging on, 72 of about 16,000 did not)."""
+    flags = subprocess.run(['make', '-s', '-C', str(CSRC), 'flags'], check=True, capture_output=True,
+                           text=True).stdout.split()
+    assert '-enable-tail-merge=false' in flags
+    flags = [f for f in flags if f not in ('-fPIC', '-shared')]
+    co = tmp_path / 'lib.co'
+    subprocess.run([HIPCC, *flags, *EVERY_BRANCH_FAR, '-I', str(CSRC / '_build'), '--cuda-device-only',
+                    '--no-gpu-bundle-output', '-c', str(CSRC / 'rlenv_hip.hip'), '-o', str(co)],
+                   check=True, capture_output=True, cwd=str(CSRC))
+    far, hazards, where = check(bind_library(HIP_LIB), co.read_bytes())
+    assert far > 10000 and hazards == 0, (far, hazards, where)
+
+
+def test_translation_holds_no_far_jump_hazard_with_every_branch_far():
+    """A banked cart's translation compiled with every branch expanded into a far jump (RLENV_JIT_EXTRA): the check
+    passes (out[5] = 0 hazards among out[4] far jumps)."""
+    lib = bind_library(HIP_LIB)
+    lib.rlenv_error.restype = ctypes.c_char_p
+    rom = synth.mmc3_cart(3, blocks=6, sub_blocks=4)
+    out = (ctypes.c_int32 * 6)()
+    os.environ['RLENV_JIT_EXTRA'] = ' '.join(EVERY_BRANCH_FAR)
+    try:
+        rc = lib.rlenv_jit_translate(rom, len(rom), 1, out, None, 0)
+    finally:
+        del os.environ['RLENV_JIT_EXTRA']
+    assert rc == 0, lib.rlenv_error()
+    assert out[4] > 1000 and out[5] == 0, list(out)
