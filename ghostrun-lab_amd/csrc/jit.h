@@ -42,9 +42,16 @@ struct JitProgram {
 
 // Whether the instruction (op, b1, b2) at CPU address a always needs the generic step (fx returns kGeneric whatever
 // the registers): its memory class is fixed by a constant address.
-// mmc3: an MMC3 image, whose bank writes at $8000-$9FFF the fast path may take (wave_dev.h mmc3_write_ok, decided at
-// run time: the block leaves before one it does not take).
-inline bool jit_always_generic(uint32_t a, uint32_t op, uint32_t b1, uint32_t b2, bool mmc3 = false) {
+// board: the image's board, whose bank writes the fast path may take (wave_dev.h map_write_ok, decided at run time: the
+// block leaves before one it does not take): MMC3 at $8000-$9FFF, MMC2 at $A000-$AFFF, MMC1 and UxROM anywhere at
+// $8000+.
+inline bool jit_fast_bank_write(uint32_t board, uint32_t ea) {
+    if (ea < 0x8000u) return false;
+    if (board == NES_BOARD_MMC3) return (ea & 0xE000u) == 0x8000u;
+    if (board == NES_BOARD_MMC2) return (ea & 0xF000u) == 0xA000u;
+    return board == NES_BOARD_MMC1 || board == NES_BOARD_UXROM;
+}
+inline bool jit_always_generic(uint32_t a, uint32_t op, uint32_t b1, uint32_t b2, uint32_t board = NES_BOARD_NROM) {
     const uint32_t d = kOptab.t[op], mode = d & 15u, grp = (d >> 8) & 15u;
     const bool rd = (d & D_READ) != 0, wr = (d & D_WRITE) != 0;
     if (grp == G_ILL || grp == G_BRK) return true;
@@ -57,7 +64,7 @@ inline bool jit_always_generic(uint32_t a, uint32_t op, uint32_t b1, uint32_t b2
     if (mode != M_ABS || grp == G_JSR) return false;
     const bool prg_ram = ea >= 0x6000u && ea < 0x8000u;   // served by the fast path except on MMC1 (decided then)
     if (rd && wr) return ea >= 0x2000u && !prg_ram;
-    if (wr) return ea >= 0x2000u && ea != 0x4016u && !prg_ram && !(mmc3 && (ea & 0xE000u) == 0x8000u);
+    if (wr) return ea >= 0x2000u && ea != 0x4016u && !prg_ram && !jit_fast_bank_write(board, ea);
     if (rd) return !(ea < 0x2000u || ea >= 0x8000u || ea == 0x4016u || (ea & 0xE007u) == 0x2002u || prg_ram);
     return false;
 }
@@ -246,7 +253,7 @@ inline JitProgram jit_translate_banked(const std::vector<uint8_t>& prg, uint32_t
     // a jump to itself is found at run time (fx compares with the CPU address)
     auto generic = [&](uint32_t o) {
         return (o & 0x1FFFu) + len_of(o) >= 0x2000u ||
-               jit_always_generic(0xFFFFFFFFu, rd(o), rd(o + 1u), rd(o + 2u), board == NES_BOARD_MMC3);
+               jit_always_generic(0xFFFFFFFFu, rd(o), rd(o + 1u), rd(o + 2u), board);
     };
     auto target_of = [&](uint32_t o) { return o + 2u + (uint32_t)(int32_t)(int8_t)rd(o + 1u); };
     std::vector<int> order(size, -1);   // discovery rank of each leader

@@ -56,7 +56,8 @@ struct Con {
     uint64_t dmc_event;
     uint32_t prg0, prg1, prg2, prg3;   // PRG byte offsets of $8000/$A000/$C000/$E000
     uint32_t nt_map;                   // 4 x 2 bits
-    uint32_t mmc3_sel;                 // MMC3: the bank select register ($8000), as in the record's mreg[8]
+    uint32_t map_fast;                 // what the fast path's mapper writes decide on (wave_dev.h map_write_ok), as
+                                       // in the record's mreg: MMC3 the bank select, MMC1 the shift register | count << 8
     // wave_dev.h run_until_wave's own state, parked here while a burst of fast instructions runs
     uint64_t b_dmc_event, b_target;
     uint32_t b_instructions, b_pending, b_to_event, b_ecyc, b_dmc_in, b_why, b_budget, b_nmi, b_irq;
@@ -256,16 +257,18 @@ __device__ inline void map_write(Con& c, const Mem& m, uint32_t addr, uint32_t v
             r[4] = (uint8_t)(r[4] | ((v & 1u) << n));
             if (n + 1u < 5u) {
                 r[5] = (uint8_t)(n + 1u);
+                c.map_fast = r[4] | ((n + 1u) << 8);
                 return;
             }
             r[(addr >> 13) & 3u] = r[4];
             r[4] = 0;
             r[5] = 0;
         }
+        c.map_fast = 0;
         map_sync(c, m);
     } else if (m.cart.board == NES_BOARD_MMC3) {
         const uint32_t k = addr & 0xE001u;
-        if (k == 0x8000u) r[8] = (uint8_t)(c.mmc3_sel = v);
+        if (k == 0x8000u) r[8] = (uint8_t)(c.map_fast = v);
         else if (k == 0x8001u) r[r[8] & 7u] = (uint8_t)v;
         else if (k == 0xA000u) r[9] = (uint8_t)v;
         else {
@@ -1053,7 +1056,9 @@ __device__ inline void con_load(Con& c, const NesRec* r) {
     c.dmc_event = r->dmc_event;
     c.prg0 = r->prg_off[0]; c.prg1 = r->prg_off[1]; c.prg2 = r->prg_off[2]; c.prg3 = r->prg_off[3];
     c.nt_map = r->nt_map[0] | (r->nt_map[1] << 2) | (r->nt_map[2] << 4) | ((uint32_t)r->nt_map[3] << 6);
-    c.mmc3_sel = r->mreg[8];
+    c.map_fast = r->board == NES_BOARD_MMC3   ? r->mreg[8]
+                 : r->board == NES_BOARD_MMC1 ? r->mreg[4] | (r->mreg[5] << 8)
+                                              : 0u;
 }
 
 __device__ inline void con_store(const Con& c, NesRec* r) {

@@ -99,7 +99,7 @@ __device__ __forceinline__ void hot_load(Hot& h, const Con& c) {
     h.pc = hot_pcs<B>(h, uni(c.pc));
     h.ctl = uni(c.shift) | (uni(c.strobe) << 8);
 }
-// (the PRG offsets change only in the generic step and mmc3_write, which write them to the console state themselves)
+// (the PRG offsets change only in the generic step and map_write_fast, which write them to the console state)
 template <uint32_t B>
 __device__ __forceinline__ void hot_store(const Hot& h, Con& c) {
     c.pc = hot_cpu<B>(h, h.pc) & 0xFFFFu; c.a = h.a; c.x = h.x; c.y = h.y; c.sp = h.sp; c.p = hflags(h);
@@ -169,46 +169,93 @@ __device__ __forceinline__ uint32_t prg_index(const Hot& h, const Mem& m, uint32
     else return sel4((addr >> 13) & 3u, h.prg0, h.prg1, h.prg2, h.prg3) + (addr & 0x1FFFu);
 }
 
-// MMC3 bank writes the fast path takes (patch:3158-3162 the registers, 3037-3048 the PRG pages; nes_dev.h map_write
-// and map_sync): a bank select ($8000, even) that
-// keeps the PRG and CHR modes (bits 6 and 7), and a bank data write ($8001, odd) to R6 or R7, the switchable PRG
-// pages, unless it switches the page this instruction runs in (the next one is on the same page: kFetchWords).
-// Neither changes a CHR page or the mirroring, so nothing is logged for the renderer, and the IRQ counter is not
-// touched; every other write at $8000+ goes to the generic step. `mmc3_write_ok` only decides (no state change),
-// `mmc3_write` writes: the register, and the PRG page through to the console state, the record and h.
+// Mapper writes the fast path takes (nes_dev.h map_write and map_sync restate the boards): those that change no CHR
+// page, no mirroring and no IRQ state, and switch no PRG page that the instruction runs in (the next one is on the
+// same page: kFetchWords), so nothing is logged for the renderer:
+//   - MMC3: a bank select ($8000, even) that keeps the PRG and CHR modes (bits 6-7), a bank data write ($8001, odd)
+//     to R6 or R7 (patch:3158-3162 the registers, 3037-3048 the pages);
+//   - MMC1: a serial-port write that only shifts a bit in (a reset, and the fifth write, which loads a register, go
+//     to the generic step; patch:3128-3145);
+//   - UxROM: the 16 KB bank at $8000, ANDed with the byte under the write when the cart declares bus conflicts;
+//   - MMC2: the 8 KB bank at $8000 ($A000-$AFFF; patch:3147-3149).
+// map_write_ok only decides (no state change); map_write_fast writes the register to the record and the PRG pages
+// through to the console state, the record and h. What the decision needs is in the console state (Con::map_fast),
+// not a global load away.
 template <uint32_t B>
-__device__ __forceinline__ bool mmc3_write_ok(const Hot& h, const Mem& m, const Con& cs, uint32_t ea, uint32_t v,
-                                              uint32_t pcs) {
-    if (m.cart.board != NES_BOARD_MMC3) return false;
-    const uint32_t k = ea & 0xE001u, sel = uni(cs.mmc3_sel);
-    if (k == 0x8000u) return ((sel ^ v) & 0xC0u) == 0u;
-    if (k != 0x8001u || (sel & 7u) < 6u) return false;
-    const uint32_t slot = (sel & 7u) == 7u ? 1u : (sel & 0x40u) ? 2u : 0u, cpu = hot_cpu<B>(h, pcs);
-    return cpu < 0x8000u || ((cpu >> 13) & 3u) != slot;
+__device__ __forceinline__ uint32_t map_rom_byte(const Hot& h, const Mem& m, uint32_t ea) {
+    return prg_wide(m, prg_index<B>(h, m, ea)) & 0xFFu;
+}
+// The PRG slots (bit i: the 8 KB page at $8000 + i * $2000) a write of v at ea that the fast path takes switches.
+__device__ __forceinline__ uint32_t map_fast_slots(const Mem& m, const Con& cs, uint32_t ea) {
+    const uint32_t board = m.cart.board;
+    if (board == NES_BOARD_MMC3) {
+        const uint32_t sel = uni(cs.map_fast);
+        return (ea & 1u) == 0u ? 0u : (sel & 7u) == 7u ? 2u : (sel & 0x40u) ? 4u : 1u;
+    }
+    return board == NES_BOARD_UXROM ? 3u : board == NES_BOARD_MMC2 ? 1u : 0u;
 }
 template <uint32_t B>
-__device__ __forceinline__ void mmc3_write(Hot& h, const Mem& m, Con& cs, uint32_t ea, uint32_t v) {
-    NesRec* r = m.rec;
-    const uint32_t sel = uni(cs.mmc3_sel);
-    if ((ea & 1u) == 0u) {
-        r->mreg[8] = (uint8_t)v;
-        cs.mmc3_sel = v;
-        return;
+__device__ __forceinline__ bool map_write_ok(const Hot& h, const Mem& m, const Con& cs, uint32_t ea, uint32_t v,
+                                             uint32_t pcs) {
+    const uint32_t board = m.cart.board;
+    if (board == NES_BOARD_MMC3) {
+        const uint32_t k = ea & 0xE001u, sel = uni(cs.map_fast);
+        if (k == 0x8000u) {
+            if ((sel ^ v) & 0xC0u) return false;
+        } else if (k != 0x8001u || (sel & 7u) < 6u) {
+            return false;
+        }
+    } else if (board == NES_BOARD_MMC1) {
+        return (v & 0x80u) == 0u && (uni(cs.map_fast) >> 8) < 4u;
+    } else if (board == NES_BOARD_MMC2) {
+        if ((ea & 0xF000u) != 0xA000u) return false;
+    } else if (board != NES_BOARD_UXROM) {
+        return false;
     }
-    r->mreg[sel & 7u] = (uint8_t)v;
-    const uint32_t off = (v & (m.cart.prg_pages8 - 1u)) * 8192u;   // map_set_prg
-    if ((sel & 7u) == 7u) {
-        h.prg1 = off;
-        cs.prg1 = off;
-        r->prg_off[1] = off;
-    } else if (sel & 0x40u) {
-        h.prg2 = off;
-        cs.prg2 = off;
-        r->prg_off[2] = off;
-    } else {
+    const uint32_t cpu = hot_cpu<B>(h, pcs);
+    return cpu < 0x8000u || ((map_fast_slots(m, cs, ea) >> ((cpu >> 13) & 3u)) & 1u) == 0u;
+}
+template <uint32_t B>
+__device__ __forceinline__ void map_set_prg_fast(Hot& h, const Mem& m, Con& cs, uint32_t slot, uint32_t page) {
+    const uint32_t off = (page & (m.cart.prg_pages8 - 1u)) * 8192u;   // map_set_prg
+    m.rec->prg_off[slot] = off;
+    if (slot == 0u) {
         h.prg0 = off;
         cs.prg0 = off;
-        r->prg_off[0] = off;
+    } else if (slot == 1u) {
+        h.prg1 = off;
+        cs.prg1 = off;
+    } else {
+        h.prg2 = off;
+        cs.prg2 = off;
+    }
+}
+template <uint32_t B>
+__device__ __forceinline__ void map_write_fast(Hot& h, const Mem& m, Con& cs, uint32_t ea, uint32_t v) {
+    uint8_t* r = m.rec->mreg;
+    const uint32_t board = m.cart.board;
+    if (board == NES_BOARD_MMC3) {
+        const uint32_t sel = uni(cs.map_fast);
+        if ((ea & 1u) == 0u) {
+            r[8] = (uint8_t)v;
+            cs.map_fast = v;
+        } else {
+            r[sel & 7u] = (uint8_t)v;
+            map_set_prg_fast<B>(h, m, cs, (sel & 7u) == 7u ? 1u : (sel & 0x40u) ? 2u : 0u, v);
+        }
+    } else if (board == NES_BOARD_MMC1) {
+        const uint32_t sr = uni(cs.map_fast), n = sr >> 8, bits = (sr & 0xFFu) | ((v & 1u) << n);
+        r[4] = (uint8_t)bits;
+        r[5] = (uint8_t)(n + 1u);
+        cs.map_fast = bits | ((n + 1u) << 8);
+    } else if (board == NES_BOARD_MMC2) {
+        r[4] = (uint8_t)(v & 0x0Fu);
+        map_set_prg_fast<B>(h, m, cs, 0u, v & 0x0Fu);
+    } else {   // UxROM
+        const uint32_t b = m.cart.bus_conflicts ? (v & map_rom_byte<B>(h, m, ea)) : v;
+        r[0] = (uint8_t)b;
+        map_set_prg_fast<B>(h, m, cs, 0u, b * 2u);
+        map_set_prg_fast<B>(h, m, cs, 1u, b * 2u + 1u);
     }
 }
 
@@ -286,7 +333,7 @@ __device__ __forceinline__ uint32_t fx(Hot& h, const Mem& m, Con& cs, uint32_t p
         // Memory class, decided before any side effect (every check below comes before the first state change):
         // RAM, PRG RAM ($6000-$7FFF; on MMC1, whose register can disable it, the generic step), PRG reads, the
         // controller port and PPU status reads run here; any other I/O register, a read-modify-write elsewhere and
-        // any write at $8000+ (a mapper) but MMC3's PRG bank writes (mmc3_write_ok) go to the generic step. Written
+        // any write at $8000+ (a mapper) but the bank writes of map_write_ok go to the generic step. Written
         // as chains of single compares: boolean
         // combinations of uniform conditions become lane-mask arithmetic.
         if constexpr (!zpage && rd && wr) {
@@ -300,9 +347,9 @@ __device__ __forceinline__ uint32_t fx(Hot& h, const Mem& m, Con& cs, uint32_t p
             if (ea >= 0x2000u) {
                 if (ea != 0x4016u) {
                     if (ea < 0x6000u) return kGeneric;
-                    if (ea >= 0x8000u) {
-                        if constexpr (nrom) return kGeneric;
-                        else if (!mmc3_write_ok<B>(h, m, cs, ea, hget(h, src, 0), pcs)) return kGeneric;
+                    if (ea >= 0x8000u) {   // (a bank write is an absolute store; an indexed one: the generic step)
+                        if constexpr (nrom || mode != M_ABS) return kGeneric;
+                        else if (!map_write_ok<B>(h, m, cs, ea, hget(h, src, 0), pcs)) return kGeneric;
                     } else if (m.cart.board == NES_BOARD_MMC1) {
                         return kGeneric;
                     }
@@ -432,7 +479,7 @@ __device__ __forceinline__ uint32_t fx(Hot& h, const Mem& m, Con& cs, uint32_t p
             if constexpr (mode == M_ZP) m.ram[ea] = (uint8_t)res;
             else if constexpr (zpage) m.ram[ea & 0x7FFu] = (uint8_t)res;
             else if (ea < 0x2000u) m.ram[ea & 0x7FFu] = (uint8_t)res;
-            else if (!nrom && !rd && ea >= 0x8000u) mmc3_write<B>(h, m, cs, ea, res);
+            else if (!nrom && !rd && mode == M_ABS && ea >= 0x8000u) map_write_fast<B>(h, m, cs, ea, res);
             else if (ea >= 0x6000u) m.rec->prg_ram[ea - 0x6000u] = (uint8_t)res;   // (a read-modify-write: here)
             else port_write(h, cs, res);
         }
