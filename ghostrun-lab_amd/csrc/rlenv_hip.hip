@@ -371,7 +371,8 @@ __global__ __launch_bounds__(256) void k_smb_signals(const uint8_t* __restrict__
     }
 }
 // 2. One env per lane (64-lane blocks: as many CUs as waves), its steps in order; the records of kAhead steps are
-// loaded ahead in two register buffers, through row bases that are the same for the whole wave.
+// loaded ahead in two register buffers, through row bases that are the same for the whole wave (the buffer holds
+// kAhead rows past the last, which the last loads read and nothing uses).
 constexpr int kAhead = 4;
 __global__ __launch_bounds__(64) void k_smb_chain(ev::SmbStep* __restrict__ rec, const uint8_t* __restrict__ ram15,
                                                    int T, int N, int frames, Rl10State* __restrict__ state) {
@@ -379,10 +380,10 @@ __global__ __launch_bounds__(64) void k_smb_chain(ev::SmbStep* __restrict__ rec,
     if (e >= N) return;
     const Rl10Game G = rl10_game(RL10_SMB);
     const int64_t stall = G.stall_frames >= 0.0 ? (int64_t)__builtin_ceil(G.stall_frames) : -1;
-    auto row = [&](int t) { return rec + (size_t)(uint32_t)min(t, T - 1) * (uint32_t)N; };
+    auto row = [&](int t) { return rec + (size_t)(uint32_t)t * (uint32_t)N; };
     auto put = [&](int t, const ev::SmbDec& d) { reinterpret_cast<ev::SmbDec*>(row(t))[e] = d; };
     Rl10State st = state[e];
-    ev::SmbChain c{st.done ? 1u : 0u, st.end_reason, st.has_best_level ? st.best_level : -1,
+    ev::SmbChain c{st.done ? 1u : 0u, 0u, st.has_best_level ? st.best_level : -1,
                    st.has_best_progress ? (int32_t)st.best_progress : ev::kNoBest, ev::kNoBest, st.deaths,
                    st.idle_frames, st.score_used};
     ev::SmbStep a[kAhead], b[kAhead];
@@ -401,7 +402,7 @@ __global__ __launch_bounds__(64) void k_smb_chain(ev::SmbStep* __restrict__ rec,
     }
     for (; t < T; ++t) put(t, ev::smb_chain_step(row(t)[e], frames, c, stall));   // the last T % 8 steps
     st.done = (uint8_t)c.done;
-    st.end_reason = (uint8_t)c.end_reason;
+    if (c.end_flags) st.end_reason = (uint8_t)ev::smb_end_reason(c.end_flags);   // ended in this call
     st.has_best_level = c.best_level >= 0 ? 1 : 0;
     if (c.best_level >= 0) st.best_level = c.best_level;
     st.has_best_progress = c.best_progress != ev::kNoBest ? 1 : 0;
@@ -1831,8 +1832,9 @@ int rl10_smb_run(const uint8_t* ram15, int T, int N, int frames, void* state, fl
         int device = 0;
         if (hipGetDevice(&device) != hipSuccess) throw std::runtime_error("hipGetDevice failed");
         const size_t n = (size_t)T * (size_t)N;
-        void* rec = nullptr;
-        if (hipMallocFromPoolAsync(&rec, n * sizeof(ev::SmbStep), smb_pool(device), st) != hipSuccess)
+        void* rec = nullptr;   // (kAhead rows past the last: k_smb_chain's last loads)
+        if (hipMallocFromPoolAsync(&rec, (n + (size_t)kAhead * (size_t)N) * sizeof(ev::SmbStep), smb_pool(device), st) !=
+            hipSuccess)
             throw std::runtime_error("rl10_smb_run: no device memory for the per-step records");
         const size_t groups = (size_t)((T + 3) / 4) * (size_t)N;
         hipLaunchKernelGGL(k_smb_signals, dim3((unsigned)((groups + 255) / 256)), dim3(256), 0, st, ram15, T, N,

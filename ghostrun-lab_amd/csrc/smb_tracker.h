@@ -10,8 +10,10 @@
 //    the capped score reward, the rollback and idle conditions - into a 16-byte SmbStep per env-step.
 // 2. k_smb_chain, one env per lane, its T steps in order: the tracker state alone (best level, best progress, score
 //    budget, deaths, idle frames, the end), without branches, with sentinels for the "not seen yet" flags. It writes
-//    over each SmbStep what the step's reward is made of (SmbDec: which terms, the score term, the best progress
-//    before a gain) and leaves the tracker's state.
+//    over each SmbStep what the step's reward needs of the state (SmbDec: the step's flags as the tracker saw them,
+//    and whether it entered a level, gained progress, skipped a level, was at the best level, stalled, was done
+//    after it, scored; the score term; the best progress before a gain) and leaves the tracker's state, its end
+//    reason worked out once from the flags of the step that ended the episode. About 81 instructions a step.
 // 3. k_smb_reward, all env-steps in parallel: the reward, summed in update's order from those terms (so the same
 //    doubles are added in the same order: bit-exact), and the done flag.
 #pragma once
@@ -30,14 +32,14 @@ enum : uint32_t {
     ST_IDLE = 128, ST_HAD = 256
 };
 struct SmbDec {
-    double score;         // the score term, with DC_SCORE
+    double score;         // the score term (min of the capped score reward and the budget left), with DC_SCORE
     int32_t best_before;  // the best progress before a gain, with DC_GAIN
     int16_t progress;
-    uint16_t flags;
+    uint16_t flags;       // the step's ST_ flags as the tracker saw them (none once it is done), then DC_ bits
 };
 enum : uint32_t {
-    DC_LEVEL = 1, DC_GAIN = 2, DC_DEATH = 4, DC_SCORE = 8, DC_ROLLBACK = 16, DC_IDLE = 32, DC_WIN = 64, DC_STALL = 128,
-    DC_DONE = 256
+    DC_LEVEL = 1u << 9, DC_GAIN = 1u << 10, DC_SKIP = 1u << 11, DC_AT_BEST = 1u << 12, DC_STALL = 1u << 13,
+    DC_DONE = 1u << 14, DC_SCORE = 1u << 15
 };
 static_assert(sizeof(SmbStep) == 16 && sizeof(SmbDec) == 16, "16-byte records, one overwritten by the other");
 
@@ -70,7 +72,7 @@ __device__ __forceinline__ SmbStep smb_step_record(const Rl10Signals& s, const R
 // clears has_best_progress, so the value last assigned is kept apart (last_progress, kNoBest: none in this run) for
 // the state written back.
 struct SmbChain {
-    uint32_t done, end_reason;
+    uint32_t done, end_flags;
     int32_t best_level, best_progress, last_progress, deaths;
     int64_t idle;
     double score_used;
@@ -84,53 +86,58 @@ __device__ __forceinline__ SmbDec smb_chain_step(const SmbStep& q, int frames, S
     const uint32_t f = q.flags & (0u - alive);                // a finished tracker sees no flag
     const int32_t level = q.level, progress = q.progress;
     const bool ip = (f & ST_IN_PLAY) != 0;
-    const bool have = s.best_level >= 0;
-    const bool first = ip && !have;
-    const bool skip = ip && have && level > s.best_level + 1;
-    const bool up = ip && have && level == s.best_level + 1;
-    const bool reset = first || up;
-    s.best_level = reset ? level : s.best_level;
-    s.best_progress = reset ? kNoBest : s.best_progress;
+    const int32_t bl = s.best_level;
+    const bool have = bl >= 0;
+    const bool skip = ip && have && level > bl + 1;
+    const bool up = ip && have && level == bl + 1;
+    const bool reset = ip && (!have || level == bl + 1);
+    s.best_level = reset ? level : bl;
+    const int32_t bp = reset ? kNoBest : s.best_progress;
     s.score_used = reset ? 0.0 : s.score_used;
-    const bool pv = ip && level == s.best_level && (f & ST_VALID);
-    const bool better = pv && progress > s.best_progress;    // a first setting or a gain
-    const bool gain = better && s.best_progress != kNoBest;
-    const int32_t before = s.best_progress;
-    s.best_progress = better ? progress : s.best_progress;
+    const bool at_best = level == s.best_level;
+    const bool better = ip && at_best && (f & ST_VALID) && progress > bp;   // a first setting or a gain
+    const bool gain = better && bp != kNoBest;
+    s.best_progress = better ? progress : bp;
     s.last_progress = better ? progress : s.last_progress;
-    const bool death = (f & ST_DEATH) != 0;
-    s.deaths += death ? 1 : 0;
+    const uint32_t death = (f >> 4) & 1u;       // ST_DEATH
+    s.deaths += (int32_t)death;
     const bool fresh = up || gain || death;
-    const double left = kScoreBudget - s.score_used;
-    const double sr = left < q.score_r ? left : q.score_r;
+    const double sr = __builtin_fmin(kScoreBudget - s.score_used, q.score_r);   // (both finite)
     const bool score = (f & ST_SCORE) && sr > 0;
     s.score_used = score ? s.score_used + sr : s.score_used;
-    const bool rollback = (f & ST_ROLLBACK) && !skip && level == s.best_level;
-    const bool idle_pen = !fresh && !skip && (f & ST_IDLE);
     const int64_t idle = (fresh || !(f & ST_HAD)) ? 0 : s.idle + frames;
     s.idle = alive ? idle : s.idle;
     const bool win = (f & ST_WON) != 0;
     const bool over = !win && (f & ST_OVER);
     const bool stall_end = alive && !win && !over && !skip && stall >= 0 && idle >= stall;
-    s.end_reason = win ? 2u : over ? 1u : stall_end ? 4u : skip ? 3u : s.end_reason;
-    s.done = s.done | ((skip || win || over || stall_end) ? 1u : 0u);
-    const uint32_t o = (up ? DC_LEVEL : 0u) | (gain ? DC_GAIN : 0u) | (death ? DC_DEATH : 0u) |
-                       (score ? DC_SCORE : 0u) | (rollback ? DC_ROLLBACK : 0u) | (idle_pen ? DC_IDLE : 0u) |
-                       (win ? DC_WIN : 0u) | (stall_end ? DC_STALL : 0u) | (s.done ? DC_DONE : 0u);
-    return SmbDec{score ? sr : 0.0, before, (int16_t)progress, (uint16_t)o};
+    const bool ends = skip || win || over || stall_end;   // (only while alive: f is 0 after the end)
+    s.done = s.done | (ends ? 1u : 0u);
+    const uint32_t o = f | (up ? DC_LEVEL : 0u) | (gain ? DC_GAIN : 0u) | (skip ? DC_SKIP : 0u) |
+                       (at_best ? DC_AT_BEST : 0u) | (stall_end ? DC_STALL : 0u) | (s.done << 14) |
+                       (score ? DC_SCORE : 0u);
+    s.end_flags = ends ? o : s.end_flags;   // the ending step's flags: the end reason, worked out once at the end
+    return SmbDec{sr, bp, (int16_t)progress, (uint16_t)o};
+}
+
+// update's end reason from the flags of the step that ended the episode: 2 won, 1 game over, 4 stalled, 3 skipped a
+// level (checked in update's order).
+__device__ __forceinline__ uint32_t smb_end_reason(uint32_t f) {
+    return (f & ST_WON) ? 2u : (f & ST_OVER) ? 1u : (f & DC_STALL) ? 4u : 3u;
 }
 
 // Step 3 for one env-step: update's reward, its terms added in update's order.
 __device__ __forceinline__ double smb_reward(const SmbDec& d, int frames, const Rl10Game& G) {
     const uint32_t f = d.flags;
+    const bool death = (f & ST_DEATH) != 0, skip = (f & DC_SKIP) != 0;
+    const bool fresh = (f & (DC_LEVEL | DC_GAIN)) != 0 || death;
     double r = 0.0;
     if (f & DC_LEVEL) r += kWLevel;
     if (f & DC_GAIN) r += kWProgress * ((double)d.progress - (double)d.best_before) / G.progress_unit;
-    if (f & DC_DEATH) r += kWDeath;
+    if (death) r += kWDeath;
     if (f & DC_SCORE) r += d.score;
-    if (f & DC_ROLLBACK) r += kWRollback;
-    if (f & DC_IDLE) r += G.idle_per_frame * frames;
-    if (f & DC_WIN) r += kWWin;
+    if ((f & ST_ROLLBACK) && !skip && (f & DC_AT_BEST)) r += kWRollback;
+    if (!fresh && !skip && (f & ST_IDLE)) r += G.idle_per_frame * frames;
+    if (f & ST_WON) r += kWWin;
     else if (f & DC_STALL) r += kWStall;
     return r;
 }
