@@ -13,7 +13,7 @@
 //    over each SmbStep what the step's reward needs of the state (SmbDec: the step's flags as the tracker saw them,
 //    and whether it entered a level, gained progress, skipped a level, was at the best level, stalled, was done
 //    after it, scored; the score term; the best progress before a gain) and leaves the tracker's state, its end
-//    reason worked out once from the flags of the step that ended the episode. About 81 instructions a step.
+//    reason worked out once from the flags of the step that ended the episode. About 80 instructions a step.
 // 3. k_smb_reward, all env-steps in parallel: the reward, summed in update's order from those terms (so the same
 //    doubles are added in the same order: bit-exact), and the done flag.
 #pragma once
