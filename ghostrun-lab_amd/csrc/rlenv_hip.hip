@@ -932,6 +932,10 @@ uint32_t* scratch_of(int device) {
 
 // Runs f(game index, stream) for every game: on the caller's stream for a one-game env; otherwise each game on its
 // own stream, forked from and joined back to the caller's stream. Returns 0, or 1 with g_error set.
+// The runtime maps more streams than it has hardware queues (4 by default) onto shared queues, which run what they
+// hold in order, and a wait enqueued on the caller's stream becomes a barrier in its queue. So every game's work is
+// enqueued before the caller's stream waits on any game: joined one by one, the games that share the caller's queue
+// would wait behind the join of every game enqueued before them.
 template <class F>
 int for_games(Env& env, hipStream_t st, F&& f) {
     const size_t n = env.games.size();
@@ -945,8 +949,8 @@ int for_games(Env& env, hipStream_t st, F&& f) {
         bad |= hipStreamWaitEvent(gst, env.gs.fork, 0) != hipSuccess;
         f(gi, gst);
         bad |= hipEventRecord(env.gs.done[gi], gst) != hipSuccess;
-        bad |= hipStreamWaitEvent(st, env.gs.done[gi], 0) != hipSuccess;
     }
+    for (size_t gi = 0; gi < n; ++gi) bad |= hipStreamWaitEvent(st, env.gs.done[gi], 0) != hipSuccess;
     if (bad) g_error = "fork/join of the game streams failed";
     return bad ? 1 : 0;
 }
