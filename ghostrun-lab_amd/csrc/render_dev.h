@@ -28,7 +28,8 @@ namespace nd {
 // The render's LDS besides the nametables and OAM (1,720 bytes; the console-frame kernel that draws its own frame lays
 // it over the CPU RAM it has copied out).
 struct RenderScratch {
-    uint32_t px[64];          // the line: palette value, 0x40 | backdrop where the background is transparent
+    uint32_t px[64];          // the line: palette value, 0x40 | backdrop where the background is transparent (in
+                              // fast_run, which draws in registers: where the lanes that fetch no sprite store)
     uint32_t sp[256];         // the sprite line: (7 - rank) << 8 | behind << 7 | palette << 2 | value, 0 = none
     uint32_t f[36];           // fetches: lo | hi << 8 | attribute << 16; 0-1 carried, 2 + j slot j
     uint32_t spr[2][8];       // sprite lines: lo | hi << 8 | attr << 16 | x << 24
@@ -347,7 +348,8 @@ struct RenderSink {
     //   - the lanes expand this line's sprites, sync once, and each composes its 4 pixels in registers.
     // With rendering off the lines are the backdrop: nothing is fetched, v stays, no sprite is drawn and no sprite-0
     // check can hit (the backdrop is transparent).
-    template <bool kPairs>
+    // kSpr: sprites on (mask bit 4) for the run.
+    template <bool kPairs, bool kSpr>
     __device__ void fast_run(Rs& s, int32_t l, int32_t stop, uint8_t* obs, uint8_t* emph) {
         uint32_t t[4];
         bg_table(t);
@@ -362,7 +364,7 @@ struct RenderSink {
             return;
         }
         const uint32_t ctrl = s.ctrl, h = (ctrl & 0x20u) ? 16u : 8u, ptab = (ctrl & 0x10u) << 8;
-        const bool bg_on = (mask & 0x08u) && (lane >= 2 || (mask & 0x02u)), spr_on = (mask & 0x10u) != 0;
+        const bool bg_on = (mask & 0x08u) && (lane >= 2 || (mask & 0x02u)), spr_on = kSpr;
         // this lane's OAM entry: its pattern row is sb + row (+ 8 for the lower tile of 8x16), vertical flip negating
         // the row (flip = all ones: (r ^ flip) - flip, and sb adds the 7 or 23)
         const uint32_t e = reinterpret_cast<const uint32_t*>(otab)[lane];
@@ -378,10 +380,24 @@ struct RenderSink {
         if (spr_on && sp_stale) latch_table();
         uint32_t spt[4];
         sprite_table(spt);
-        uint32_t key = 0xFFFFFFFFu, tb = 0, tsel = 0, vl = s.v;
+        // what else the run holds fixed: greyscale (rendering is on), the left-8 sprite clip, t's horizontal bits
+        const uint32_t keep4 = (mask & 0x01u) ? 0x30303030u : 0x3F3F3F3Fu;
+        const uint32_t show_m = !(mask & 0x04u) && lane < 2 ? 0u : 0xFFFFFFFFu;
+        const uint32_t t_h = s.t & 0x041Fu, kk = (uint32_t)lane >> 3, px = (uint32_t)lane & 7u;
+        // the row's 60 words are stored by all 64 lanes: lanes 0 and 1 store lane 2's word, 62 and 63 lane 61's
+        const int32_t ox = 4 * (lane < 2 ? 0 : lane > 61 ? 59 : lane - 2);
+        // The run's state in registers, written back after it. The two sprite buffers are 0 and 1, so the one a
+        // fetch fills (the one not latched) is drawn ^ 1. spork: a line was latched at the end of the line before
+        // (with sprites on the only way it is set in the run; with sprites off nothing is drawn, so the latched line
+        // is not expanded: the sprite line stays clear, as the compose would leave it).
+        uint32_t vl = s.v, dr = drawn, dr_n = drawn_n, spork = s.spork, tgt = drawn ^ 1u;
+        uint32_t hit = s.hit, sp_bits = s.sphit_bits, f_bits = s.f_bits, f_attr = s.f_attr, f_x = s.f_x;
+        int32_t sphitx = s.sphitx, hit_x = s.hit_x;
+        uint64_t sel = 0;
+        uint32_t key = 0xFFFFFFFFu, tb = 0, tsel = 0, vline = vl;
         const int32_t l0 = l;
         for (; l < stop; ++l) {
-            vl = s.v;
+            vline = vl;
             if ((vl & 0x0FFFu) != key) {   // a new row of tiles (or the run's first line)
                 key = vl & 0x0FFFu;
                 const uint32_t vs = v_steps(vl, slot);
@@ -393,54 +409,109 @@ struct RenderSink {
             }
             const uint32_t mine = pattern_of<kPairs>(s.chr_lo, s.chr_hi, tb + ((vl >> 12) & 7u)) | tsel;
             const uint32_t other = (uint32_t)__builtin_amdgcn_mov_dpp((int)mine, 0xB1, 0xF, 0xF, false);   // lane ^ 1
-            // FetchSpriteData for line l + 1 into the buffer not latched
+            // FetchSpriteData for line l + 1 into buffer tgt (every lane fetches its entry's row, only the first eight
+            // on the line keep it)
             const uint32_t row = (uint32_t)(l - (int32_t)(e & 0xFFu));
-            const uint64_t sel = __ballot(row < h);
+            sel = __ballot(row < h);
             const uint32_t rank = __builtin_amdgcn_mbcnt_hi((uint32_t)(sel >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)sel, 0u));
-            const uint32_t target = fetched == drawn ? drawn ^ 1u : fetched;
-            // (every lane fetches its entry's row, only the first eight on the line keep it)
             const uint32_t r2 = row + (row & 8u);
             const uint32_t sp = pattern_of<kPairs>(s.chr_lo, s.chr_hi, (sb + ((r2 ^ flip) - flip)) & 0x1FFFu) |
                                 (e & 0xFFFF0000u);
-            if (row < h && rank < 8u) L->spr[target][rank] = sp;
-            fetched = target;
-            expand_sprites(s);
-            __syncthreads();
-            uint32_t w = back4;
-            if (bg_on) w = shift4(lane & 1 ? other : mine, lane & 1 ? mine : other, kk0, s.fx, t);
-            if (s.sphitx != kNoCheck) check_hit(s, w);
-            compose(s, l, w, obs, spt);
-            // the end of the line: Fixit1 and Fixit2 (v from t horizontally), the next line's sprites, RefreshSprites
-            s.sphitx = kNoCheck;
-            s.v = (y_step(vl) & 0x7BE0u) | (s.t & 0x041Fu);
-            // what RefreshSprites needs of the fetch (sprite_fetch_done): with sprite 0 on the line it is the first
-            // one fetched, lane 0's
-            const uint32_t n = (uint32_t)__builtin_popcountll(sel);
-            s.f_n = n < 8u ? n : 8u;
-            s.f_blurp = (uint32_t)(sel & 1u);
-            if (s.f_blurp) {
-                const uint32_t e0 = (uint32_t)__builtin_amdgcn_readlane((int)sp, 0);
-                s.f_bits = (e0 & 0xFFu) | ((e0 >> 8) & 0xFFu);
-                s.f_attr = (e0 >> 16) & 0xFFu;
-                s.f_x = e0 >> 24;
-            }
-            if (spr_on) {
-                s.spork = 0;
-                if (s.f_n != 0) {
-                    latch_sprites(s);
-                    if (s.f_blurp && !s.hit && s.f_bits) {
-                        uint32_t b = s.f_bits;
-                        if (s.f_attr & 0x40u) b = __builtin_bitreverse32(b) >> 24;
-                        s.sphitx = (int32_t)s.f_x;
-                        s.sphit_bits = b;
-                    }
-                    s.spork = 1;
+            // (the lanes that keep nothing store into their own word of the line buffer, unused by this path)
+            const uint32_t slot_k = rank + (row < h ? 0u : 8u);
+            *(slot_k < 8u ? &L->spr[tgt][slot_k] : &L->px[lane]) = sp;
+            const uint32_t fetched_now = tgt;
+            const uint32_t bgw = shift4(lane & 1 ? other : mine, lane & 1 ? mine : other, kk0, s.fx, t);
+            uint32_t w = bg_on ? bgw : back4;
+            if (sphitx != kNoCheck) {   // (check_hit on the run's registers: the background pixels)
+                const int32_t end = sphitx + 8 < 255 ? sphitx + 8 : 255;
+                uint32_t first = 4u;
+                for (uint32_t q = 0; q < 4u; ++q) {
+                    const int32_t x = 4 * lane + (int32_t)q;
+                    const bool in = x >= sphitx && x < end;
+                    const uint32_t bit = in ? (sp_bits >> (uint32_t)(7 - (x - sphitx))) & 1u : 0u;
+                    if (first == 4u && bit && !((w >> (8u * q)) & 0x40u)) first = q;
+                }
+                const uint64_t hb_ = __ballot(first < 4u);
+                if (hb_) {
+                    const int ln = (int)__builtin_ctzll(hb_);
+                    hit = 1;
+                    hit_x = 4 * ln + __builtin_amdgcn_readlane((int)first, ln);
                 }
             }
+            if (spr_on && spork) {
+                // this line's sprites: lane 8k + p expands pixel p of latched sprite k (expand_sprites), every lane
+                // issuing its LDS max, a zero (no change) where there is nothing to draw
+                const uint32_t es = L->spr[dr][kk];
+                const uint32_t attr = (es >> 16) & 0xFFu, b = (attr & 0x40u) ? px : 7u - px;
+                const uint32_t x = (es >> 24) + px;
+                uint32_t val = ((es >> b) & 1u) | (((es >> (8u + b)) & 1u) << 1);
+                // (k < drawn_n and x < 256 as sign masks)
+                val &= (uint32_t)((int32_t)(x - 256u) >> 31) & (uint32_t)((int32_t)(kk - dr_n) >> 31);
+                const uint32_t ent = ((7u - kk) << 8) | ((attr & 0x20u) << 2) | ((attr & 3u) << 2) | val;
+                atomicMax(&L->sp[x & 0xFFu], ent & (0u - (val < 1u ? val : 1u)));
+                __syncthreads();
+                // compose: the sprite pixels over the background, the lane's part of L->sp cleared
+                const uint4 spq = reinterpret_cast<const uint4*>(L->sp)[lane];
+                reinterpret_cast<uint4*>(L->sp)[lane] = make_uint4(0u, 0u, 0u, 0u);
+                const uint32_t eb = (spq.x & 0xFFu) | ((spq.y & 0xFFu) << 8) | ((spq.z & 0xFFu) << 16) | (spq.w << 24);
+                const uint32_t opaque = (eb | (eb >> 1)) & 0x01010101u;
+                const uint32_t front = ~(eb >> 7) & 0x01010101u, clear_bg = (w >> 6) & 0x01010101u;
+                const uint32_t show = opaque & (front | clear_bg) & show_m;
+                const uint32_t ssel = eb & 0x07070707u;
+                const uint32_t lo = __builtin_amdgcn_perm(spt[1], spt[0], ssel), hi = __builtin_amdgcn_perm(spt[3], spt[2], ssel);
+                const uint32_t col = __builtin_amdgcn_perm(hi, lo, 0x03020100u | ((eb >> 1) & 0x04040404u));
+                w = __builtin_amdgcn_perm(col, w, 0x03020100u | (show << 2));
+            }
+            if (l >= 8) {
+                uint32_t wo = w & keep4;
+                wo = (uint32_t)__builtin_amdgcn_update_dpp((int)wo, (int)wo, 0xEA, 0x1, 0x1, false);   // 0-3: [2,2,2,3]
+                wo = (uint32_t)__builtin_amdgcn_update_dpp((int)wo, (int)wo, 0x54, 0x8, 0x8, false);   // 60-63: [0,1,1,1]
+                *reinterpret_cast<uint32_t*>(obs + (l - 8) * RLE_OBS_W + ox) = wo;
+            }
+            // the end of the line: Fixit1 and Fixit2 (v from t horizontally), RefreshSprites
+            sphitx = kNoCheck;
+            if (__builtin_expect((vl & 0x7000u) == 0x7000u, 0)) vl = y_step(vl);
+            else vl += 0x1000u;
+            vl = (vl & 0x7BE0u) | t_h;
+            if (spr_on) {
+                const uint32_t n = (uint32_t)__builtin_popcountll(sel);
+                spork = n < 1u ? n : 1u;
+                dr_n = spork ? (n < 8u ? n : 8u) : dr_n;
+                dr = spork ? fetched_now : dr;
+            }
+            if (__builtin_expect((uint32_t)sel & 1u, 0)) {   // sprite 0 fetched for the next line: what RefreshSprites keeps
+                const uint32_t e0 = (uint32_t)__builtin_amdgcn_readlane((int)sp, 0);
+                f_bits = (e0 & 0xFFu) | ((e0 >> 8) & 0xFFu);
+                f_attr = (e0 >> 16) & 0xFFu;
+                f_x = e0 >> 24;
+                if (spr_on && !hit && f_bits) {
+                    sphitx = (int32_t)f_x;
+                    sp_bits = (f_attr & 0x40u) ? __builtin_bitreverse32(f_bits) >> 24 : f_bits;
+                }
+            }
+            tgt = dr ^ 1u;
+            fetched = fetched_now;
         }
         emphasis(emph, (l0 > 8 ? l0 : 8) - 8, stop - 8, mask);
-        // the last line's slots 32 and 33, where a line with writes after the run starts from (F[34], F[35])
-        if (lane < 2) fetch_slot(s, v_steps(vl, 32u + (uint32_t)lane), 32u + (uint32_t)lane, s.chr_lo, s.chr_hi);
+        // the state after the run (sprite_fetch_done, latch_sprites and the check's on the last line)
+        const uint32_t n_last = (uint32_t)__builtin_popcountll(sel);
+        s.v = vl;
+        s.f_n = n_last < 8u ? n_last : 8u;
+        s.f_blurp = (uint32_t)(sel & 1u);
+        s.f_bits = f_bits;
+        s.f_attr = f_attr;
+        s.f_x = f_x;
+        s.spork = spork;
+        s.hit = hit;
+        s.hit_x = hit_x;
+        s.sphitx = sphitx;
+        s.sphit_bits = sp_bits;
+        drawn = dr;
+        drawn_n = dr_n;
+        // the last line's slots 32 and 33, where a line with writes after the run starts from (F[34], F[35]): v
+        // before the line's Fixit1/Fixit2
+        if (lane < 2) fetch_slot(s, v_steps(vline, 32u + (uint32_t)lane), 32u + (uint32_t)lane, s.chr_lo, s.chr_hi);
         ha = 34u;
         hb = 35u;
     }
@@ -469,8 +540,14 @@ __device__ __forceinline__ void draw_frame(RenderScratch* L, uint8_t* nt, uint8_
         if (!mmc2 && s.next >= (l + 1) * 341 - NES_LINE_LEAD) {
             // lines l .. stop - 1 end before the next write's line (its lead-in included)
             const int32_t stop = s.next >= 232 * 341 - NES_LINE_LEAD ? 232 : (s.next + NES_LINE_LEAD) / 341;
-            if (sink.chr_pairs) sink.template fast_run<true>(s, l, stop, obs, emph);
-            else sink.template fast_run<false>(s, l, stop, obs, emph);
+            const bool spr = (s.mask & 0x10u) != 0;
+            if (sink.chr_pairs) {
+                if (spr) sink.template fast_run<true, true>(s, l, stop, obs, emph);
+                else sink.template fast_run<true, false>(s, l, stop, obs, emph);
+            } else {
+                if (spr) sink.template fast_run<false, true>(s, l, stop, obs, emph);
+                else sink.template fast_run<false, false>(s, l, stop, obs, emph);
+            }
             l = stop - 1;
             continue;
         }
