@@ -3,7 +3,7 @@
 // One decision of one game is this launch sequence on the caller's stream (the reference's phase order,
 // rl/csrc/rlenv_core.cuh:389-414 and rl/csrc/rlenv.cu:145-170):
 //   4 x k_emu_w: one emulated frame of every console and its picture into obs slot f - drawn by the same waves
-//     (emu_kernel.h, kDraw), or for frames 0-2 of a one-game env of one round of waves by k_render on a render
+//     (emu_kernel.h, kDraw), or for frames 0-1 of a one-game env of one round of waves by k_render on a render
 //     stream from a frame bank (kBank); the last frame's waves also do the finish (finish_env: reward10 update,
 //     outputs, dropout advance; finished episodes reset their RL state and join the restart list)
 //   k_reset_copy: boot snapshot (or idle template) -> console record, one workgroup per listed console
@@ -797,8 +797,9 @@ struct KernelClock {
 // * with more than one game, one stream per game and the events that fork a call's work from the caller's stream
 //   onto them and join it back (rl/csrc/rlenv.cu:38-40, 173-182): the games step concurrently, so a batch of many
 //   small games fills the GPU as one large game does;
-// * with one game, a render stream, per decision frame f an "emulated" event and one "drawn" event: frame f is drawn
-//   on the render stream from its frame bank while the frames after it are emulated on the caller's stream.
+// * with one game, a render stream, per decision frame f an "emulated" event and one "drawn" event: frames 0 and 1
+//   are drawn on the render stream from their frame banks while the frames after them are emulated on the caller's
+//   stream.
 struct RenderPipe {
     hipStream_t stream = nullptr;
     hipEvent_t emulated[RLE_FRAMES] = {}, drawn = nullptr;
@@ -1096,11 +1097,14 @@ void restart_phases(const Env& env, const GameK& g, const Outs& o, int e0, int e
 
 // A decision of envs [e0, e1) of game g: 4 frames, then the finish, the level saves and the restart pass.
 // Pipelined (a one-game env whose frame launch fits in one round of waves, so that waves retiring from the
-// emulator leave CU slots idle): frame f is drawn on the game's render stream from frame bank f while the frames
-// after it are emulated on `st`, and the restart pass, which writes the pictures of restarted envs, waits until
+// emulator leave CU slots idle): frames 0 and 1 are drawn on the game's render stream from frame banks 0 and 1 while
+// the frames after them are emulated on `st`, frames 2 and 3 by the waves that emulate them (drawn on the render
+// stream too, frame 2 left the render stream's last launch running alone after the emulation: 3.42 against 3.33
+// ms per decision of 8192 consoles), and the restart pass, which writes the pictures of restarted envs, waits until
 // every frame is drawn (so does the next decision, which refills the banks, through it). Otherwise each frame is
 // drawn on `st` after it is emulated: with several rounds of waves, or with other games' streams, the CUs are
 // already kept busy.
+constexpr int kBankFrames = 2;   // decision frames drawn on the render stream when pipelined: 0 .. kBankFrames - 1
 void decision_phases(const Env& env, const GameK& g, const RenderPipe& p, const Outs& o, int e0, int e1,
                      hipStream_t st) {
     const int n = e1 - e0;
@@ -1108,7 +1112,7 @@ void decision_phases(const Env& env, const GameK& g, const RenderPipe& p, const 
     const bool draw = !env.s.no_render;
     const bool pipelined = draw && env.games.size() == 1 && n <= env.one_round;
     for (int f = 0; f < RLE_FRAMES; ++f) {
-        if (!pipelined || f == RLE_FRAMES - 1) {   // emulated and drawn by the same waves; the last one finishes too
+        if (!pipelined || f >= kBankFrames) {   // emulated and drawn by the same waves; the last one finishes too
             launch_emu(env, g, o, EMU_DECISION, f, false, e0, e1, st, -1, true, f == RLE_FRAMES - 1);
             continue;
         }
@@ -1402,7 +1406,7 @@ void* rlenv_create(int ngames, const int* game_ids, const uint8_t* const* roms, 
             g.rst_obs = env->mem.zeros<uint8_t>(tmpl * RLE_FRAMES * RLE_OBS_PIXELS);
             g.rst_emph = env->mem.zeros<uint8_t>(tmpl * RLE_FRAMES * RLE_OBS_H);
             g.rst_fault = env->mem.zeros<uint32_t>(tmpl);
-            for (int b = 0; b < RLE_FRAMES; ++b) {
+            for (int b = 0; b < kBankFrames; ++b) {   // (the banks of the frames drawn on the render stream)
                 g.bank[b] = env->mem.zeros<FrameBank>((size_t)std::max(g.n, 1));
                 g.bank_chr[b] = g.cart.chr ? nullptr : env->mem.zeros<uint8_t>((size_t)g.n * NES_CHRRAM_BYTES);
             }
