@@ -119,6 +119,11 @@ struct RenderSink {
             return chr_pairs[page * 512u + ((pa & 0x3F0u) >> 1) + (pa & 7u)];
         }
     }
+    // The chr_pairs index of pattern address pa (kPairs): its 1 KB page's, the tile's 8 rows, the row.
+    __device__ uint32_t pairs_index(uint32_t lo, uint32_t hi, uint32_t pa) {
+        const uint32_t page = __builtin_amdgcn_perm(hi, lo, (pa >> 10) & 7u) & 0xFFu;
+        return page * 512u + ((pa & 0x3F0u) >> 1) + (pa & 7u);
+    }
     __device__ uint32_t pattern(uint32_t lo, uint32_t hi, uint32_t pa) {
         return chr_pairs ? pattern_of<true>(lo, hi, pa) : pattern_of<false>(lo, hi, pa);
     }
@@ -373,6 +378,12 @@ struct RenderSink {
         const uint32_t sb = (h == 16u ? ((st & 1u) << 12) + ((st & 0xFEu) << 4) : (st << 4) + table8) +
                             (flip & (7u + ((ctrl & 0x20u) >> 1)));
         const uint32_t slot = ((uint32_t)lane + 1u) >> 1, kk0 = ((uint32_t)lane & 1u) * 4u;
+        // (kPairs) the entry's rows in one 1 KB page: row r's pair at sp_i0 + r, or flipped sp_i0 + h - 1 - r. With
+        // pb its row 0's pattern address (16-aligned, 32 for 8x16), the pattern of row r is at pb + r for 8x8, pb + r
+        // + (r & 8) for 8x16 (the tile after), whose pair index is that of pb plus r; flipped the rows run backwards.
+        const uint32_t sp_i0 = kPairs ? pairs_index(s.chr_lo, s.chr_hi, sb - (flip & (7u + ((ctrl & 0x20u) >> 1)))) +
+                                            (flip & (h - 1u))
+                                      : 0u;
         // the latched sprite palette. With sprites on, the line before the run ended with RefreshSprites: it latched
         // the palette as it is now, or latched nothing (no sprite is drawn before a latch in the run, which takes this
         // same palette), so the table can be brought up to date here. With sprites off nothing is latched or drawn in
@@ -406,17 +417,25 @@ struct RenderSink {
                 const uint32_t at = ntab[nt_slot(s.nt_map, ntb | 0x3C0u | (col >> 2) | ((vs & 0x380u) >> 4))];
                 tsel = ((at >> ((col & 2u) | ((vs & 0x40u) >> 4))) & 3u) << 16;
                 tb = tile * 16u + ptab;
+                if constexpr (kPairs) tb = pairs_index(s.chr_lo, s.chr_hi, tb);   // (fine y adds to the index)
             }
-            const uint32_t mine = pattern_of<kPairs>(s.chr_lo, s.chr_hi, tb + ((vl >> 12) & 7u)) | tsel;
-            const uint32_t other = (uint32_t)__builtin_amdgcn_mov_dpp((int)mine, 0xB1, 0xF, 0xF, false);   // lane ^ 1
             // FetchSpriteData for line l + 1 into buffer tgt (every lane fetches its entry's row, only the first eight
             // on the line keep it)
             const uint32_t row = (uint32_t)(l - (int32_t)(e & 0xFFu));
             sel = __ballot(row < h);
             const uint32_t rank = __builtin_amdgcn_mbcnt_hi((uint32_t)(sel >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)sel, 0u));
-            const uint32_t r2 = row + (row & 8u);
-            const uint32_t sp = pattern_of<kPairs>(s.chr_lo, s.chr_hi, (sb + ((r2 ^ flip) - flip)) & 0x1FFFu) |
-                                (e & 0xFFFF0000u);
+            uint32_t spp;
+            if constexpr (kPairs) {
+                const uint32_t rc = row < h ? row : 0u;   // (an entry off the line reads its row 0: in bounds)
+                spp = chr_pairs[sp_i0 + ((rc ^ flip) - flip)];
+            } else {
+                const uint32_t r2 = row + (row & 8u);
+                spp = pattern_of<kPairs>(s.chr_lo, s.chr_hi, (sb + ((r2 ^ flip) - flip)) & 0x1FFFu);
+            }
+            const uint32_t sp = spp | (e & 0xFFFF0000u);
+            const uint32_t mine = (kPairs ? (uint32_t)chr_pairs[tb + ((vl >> 12) & 7u)]
+                                          : pattern_of<kPairs>(s.chr_lo, s.chr_hi, tb + ((vl >> 12) & 7u))) | tsel;
+            const uint32_t other = (uint32_t)__builtin_amdgcn_mov_dpp((int)mine, 0xB1, 0xF, 0xF, false);   // lane ^ 1
             // (the lanes that keep nothing store into their own word of the line buffer, unused by this path)
             const uint32_t slot_k = rank + (row < h ? 0u : 8u);
             *(slot_k < 8u ? &L->spr[tgt][slot_k] : &L->px[lane]) = sp;
