@@ -299,6 +299,47 @@ def nrom_cart(seed: int = 0, blocks: int = 24) -> bytes:
     return ines(bytes(prg), chr_, 0, vertical=True)
 
 
+# (ctrl, mask) of the modes cart's frames, FRAMES & 7: 8x8 and 8x16 sprites from either pattern table, sprites or
+# the background off, the left column clipped for either or both, greyscale and emphasis.
+MODES = ((0x90, 0x1E), (0xB0, 0x1E), (0x90, 0x0E), (0xB0, 0x16), (0x98, 0x18), (0xB8, 0x1A), (0x90, 0x1F),
+         (0xB0, 0x3E))
+
+
+def modes_cart(seed: int = 0, blocks: int = 12) -> bytes:
+    """NROM-128 cartridge like nrom_cart whose NMI also sets the next frame's PPU mode from MODES by its frame counter
+    (both writes inside vblank, so every visible line of a frame is drawn in one mode)."""
+    rng = np.random.default_rng([0x4D4F4445, seed])
+    pal, nt, oam, mix = _tables(rng)
+    a = Asm(0xC000)
+    tables = dict(pal='t_pal', nt='t_nt', oam='t_oam')
+    a.label('reset')
+    _reset_common(a, 0x90, tables)
+    a.label('main')
+    _read_pad(a, 'm')
+    _pad_moves(a, 't_mix')
+    _filler(a, rng, blocks, 'f', 't_mix')
+    a.op('JMP', 'abs', 'main')
+    a.label('nmi')
+    _nmi_common(a)
+    a.op('LDA', 'zp', FRAMES); a.op('AND', 'imm', 7); a.op('TAX')
+    a.op('LDA', 'abx', 't_ctrl'); a.op('STA', 'abs', 0x2000); a.op('LDA', 'abx', 't_mask'); a.op('STA', 'abs', 0x2001)
+    _nmi_end(a)
+    a.label('irq')
+    a.op('RTI')
+    for name, t in (('t_pal', pal), ('t_nt', nt), ('t_oam', oam), ('t_mix', mix), ('t_ctrl', [c for c, _ in MODES]),
+                    ('t_mask', [m for _, m in MODES])):
+        a.label(name)
+        a.data(bytes(int(v) for v in t))
+    code = a.assemble()
+    assert len(code) <= 0x3FFA, len(code)
+    prg = bytearray(16384)
+    prg[:len(code)] = code
+    vec = (a.labels['nmi'], a.labels['reset'], a.labels['irq'])
+    prg[0x3FFA:0x4000] = bytes(sum(((v & 0xFF, v >> 8) for v in vec), ()))
+    chr_ = rng.integers(0, 256, 8192, dtype=np.uint8).tobytes()
+    return ines(bytes(prg), chr_, 0, vertical=True)
+
+
 def poll_cart(seed: int = 0, blocks: int = 12, bmi: bool = False) -> bytes:
     """NROM-128 cartridge with NMI off: every frame of its main loop waits for vblank with BIT $2002 / BPL, writes the
     OAM (DMA), the sprite's position, four nametable bytes and the scroll, waits for the sprite-0 flag to clear (BIT /

@@ -211,3 +211,22 @@ def test_parts_sum_to_reward_and_rewards_happen():
         assert torch.allclose(o['parts'].sum(1), o['reward'], atol=1e-6)
         nz += int((o['reward'] != 0).sum())
     assert nz > 200
+
+
+def test_modes_cart_cycles_the_ppu_modes():
+    """The modes cart sets each frame's PPU mode in vblank from its frame counter (synth.MODES: 8x8 and 8x16 sprites,
+    sprites or background off, clipped left columns, then a grey frame and a red-emphasis one in every 8). Over 24
+    frames of 2 consoles the emphasis frames come 8 apart, every row of such a frame carries red (1) and no row of any
+    other frame has emphasis, and the frame before each is grey (only the 0x30 bits of a colour index)."""
+    e = env(2, synth.modes_cart(1), pad_mode=True, sticky=False, idle_max=0, dropout=False)
+    e.start()
+    obs, emph = [], []
+    for o in drive(e, 6, 1):
+        obs += [o['obs'][:, f] for f in range(4)]
+        emph += [o['emph'][:, f] for f in range(4)]
+    red = [k for k, m in enumerate(emph) if (m == 1).all()]
+    assert len(red) == 3 and red[1] - red[0] == 8 and red[2] - red[1] == 8, red
+    assert all((m == 0).all() for k, m in enumerate(emph) if k not in red)
+    for k in red:
+        assert k > 0 and ((obs[k - 1] & 0x0F) == 0).all() and (obs[k - 1] != 0).any()
+        assert (obs[k] & 0x0F).any()

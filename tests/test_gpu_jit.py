@@ -41,6 +41,16 @@ def test_translated_benchmark_cart():
 
 
 @pytest.mark.gpu
+def test_translated_modes_cart():
+    print('case: translated modes cart seed 2, 16 consoles, raw pads, sticky, 20 decisions (every sprite and mask '
+          'mode, one a frame)', flush=True)
+    cpu, gpu, st = translated_pair(16, synth.modes_cart(2), seed=12, sticky=True, idle_max=0, dropout=False,
+                                   pad_mode=True)
+    assert st['frame_bank'] and not st['banked']
+    run(cpu, gpu, 20, 6, True)
+
+
+@pytest.mark.gpu
 def test_translated_smb_like_idle_loop_and_ends():
     print('case: translated SMB-like seed 2, 24 consoles, raw pads, level end 0, Geometric(1/16) ends, idle 0..3, '
           '40 decisions', flush=True)

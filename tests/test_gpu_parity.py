@@ -61,6 +61,14 @@ def test_nrom_moves_dropout_idle_ends():
 
 
 @pytest.mark.gpu
+def test_modes_cart_every_sprite_and_mask_mode():
+    print('case: modes cart seed 1, 16 consoles, raw pads, sticky, 20 decisions (8x8 / 8x16 sprites, sprites or '
+          'background off, clipped left columns, greyscale, emphasis, one mode a frame)', flush=True)
+    cpu, gpu = pair(16, synth.modes_cart(1), seed=11, sticky=True, idle_max=0, dropout=False, pad_mode=True)
+    run(cpu, gpu, 20, 5, True)
+
+
+@pytest.mark.gpu
 def test_mmc3_stress():
     print('case: MMC3 seed 3, 16 consoles, raw pads, IRQ + sprite-0 + bank switches', flush=True)
     cpu, gpu = pair(16, synth.mmc3_cart(3), seed=9, sticky=True, idle_max=0, dropout=False, pad_mode=True)

@@ -297,6 +297,29 @@ def test_sprite_at_oam_y_is_drawn_from_the_next_line():
     assert pix[10, 12] == 0x16 and pix[9, 12] == 0x00 and pix[10, 13] == 0x00
 
 
+def test_tall_sprites_take_the_tile_pair_and_flip_as_one():
+    """8x16 sprites (ctrl bit 5): tile byte 3 selects the pattern table at $1000 (bit 0) and the tiles 2 (rows 0-7)
+    and 3 (rows 8-15). Tile 2's row 0 has its leftmost pixel set, tile 3's row 7 its rightmost. Drawn from line
+    y + 1: unflipped, line 10 shows the first and line 25 the second; flipped vertically the 16 rows run backwards
+    across both tiles (line 10 shows tile 3's row 7); flipped horizontally the leftmost pixel moves to x + 7."""
+    def pic(attr):
+        p = Picture(mask=0x14, ctrl=0x20)
+        p.chr_view[0x1000 + 2 * 16 + 0] = 0x80
+        p.chr_view[0x1000 + 3 * 16 + 7] = 0x01
+        p.palette(0x11, 0x16)
+        p.oam[0:4] = (9, 3, attr, 12)
+        return p.render()
+    pix = pic(0x00)
+    assert pix[10, 12] == 0x16 and pix[25, 19] == 0x16
+    assert (pix[10] == 0x16).sum() == 1 and (pix[25] == 0x16).sum() == 1 and (pix[11:25] == 0x16).sum() == 0
+    pix = pic(0x80)
+    assert pix[10, 19] == 0x16 and pix[25, 12] == 0x16
+    assert (pix[10] == 0x16).sum() == 1 and (pix[25] == 0x16).sum() == 1 and (pix[11:25] == 0x16).sum() == 0
+    pix = pic(0x40)
+    assert pix[10, 19] == 0x16 and pix[25, 12] == 0x16
+    assert (pix[26] == 0x16).sum() == 0 and (pix[9] == 0x16).sum() == 0
+
+
 def test_scroll_written_in_hblank_takes_effect_on_the_next_line():
     """$2005 = 8 by a 4-cycle store from dot 240 of line 100: position 240 + 39 = 279 is past the line's pixels
     (272), so line 100 keeps the old scroll and the horizontal copy at its end brings coarse x 1 to line 101."""
