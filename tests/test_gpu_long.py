@@ -3,6 +3,8 @@
 * the reference's own equality gate (rl/tests/gpu_check.py:28-53): all twelve games, 4 consoles each, sticky moves,
   button dropout, idle_max 30 (rl/rlenv.py:173, the default: 31 restart templates a game), moves drawn by
   random_legal from the masks, 300 decisions, every output every decision and `info` at every done;
+* the CPU build's configuration (64 NROM consoles, raw pads, sticky) for its 500 decisions, every console every 50
+  decisions;
 * the GPU configuration (8192 NROM consoles, raw pads, sticky) for its 1024 decisions, consoles 0-63 and 8128-8191
   every 64 decisions;
 * the divergence/mapper stress configuration (16384 MMC3 consoles, two rounds of waves, translated) for its 512
@@ -67,6 +69,14 @@ def test_reference_equality_gate_shape():
         gpu.step()
     print(f'  {dones} finished episodes', flush=True)
     assert dones > 0
+
+
+@pytest.mark.gpu
+def test_cpu_config_full_length():
+    print('case: NROM seed 1, 64 consoles, raw pads, sticky, 500 decisions, every console every 50', flush=True)
+    from test_gpu_parity import pair, run
+    cpu, gpu = pair(64, synth.nrom_cart(1), seed=1, sticky=True, idle_max=0, dropout=False, pad_mode=True)
+    run(cpu, gpu, 500, 72, True, check_every=50)
 
 
 @pytest.mark.gpu
