@@ -348,9 +348,13 @@ struct RenderSink {
     //   - background: lane j fetches tile slot (j + 1) / 2, so lanes 2i and 2i + 1 hold slots i and i + 1 between
     //     them, the two fetches that lane 2i's pixels 8i..8i+3 and lane 2i + 1's 8i+4..8i+7 shift out (pixel x from
     //     slots x / 8 and x / 8 + 1), and one swap within the lane pair (DPP) gives each lane both. The tile and
-    //     attribute are read again only when v's row of tiles changes (every 8 lines), the pattern row every line;
-    //   - sprites: lane i keeps OAM entry i and its pattern row base; FetchSpriteData is one ballot over the lanes;
-    //   - the lanes expand this line's sprites, sync once, and each composes its 4 pixels in registers.
+    //     attribute (with CHR ROM the row of tiles' pair index) are read again only when v's row of tiles changes
+    //     (every 8 lines), the pattern row every line;
+    //   - sprites: lane i keeps OAM entry i and its pattern row base (with CHR ROM its row 0's pair index);
+    //     FetchSpriteData is one ballot over the lanes;
+    //   - the lanes expand this line's sprites, sync once, and each composes its 4 pixels in registers;
+    //   - the run's state (v, the latched sprite line, the sprite-0 check) stays in scalar registers, with selects
+    //     and masks rather than lane-divergent branches: the CU's scalar unit is what the emulator's waves need.
     // With rendering off the lines are the backdrop: nothing is fetched, v stays, no sprite is drawn and no sprite-0
     // check can hit (the backdrop is transparent).
     // kSpr: sprites on (mask bit 4) for the run.
