@@ -63,10 +63,21 @@ inline bool jit_always_generic(uint32_t a, uint32_t op, uint32_t b1, uint32_t b2
     }
     if (mode != M_ABS || grp == G_JSR) return false;
     const bool prg_ram = ea >= 0x6000u && ea < 0x8000u;   // served by the fast path except on MMC1 (decided then)
+    // a PPU register write: the fast path takes those of a burst between vblank and the pre-render line (wave_dev.h
+    // ppu_write_quiet); the others end the burst at run time
+    const bool ppu = ea >= 0x2000u && ea < 0x4000u;
     if (rd && wr) return ea >= 0x2000u && !prg_ram;
-    if (wr) return ea >= 0x2000u && ea != 0x4016u && !prg_ram && !jit_fast_bank_write(board, ea);
+    if (wr) return ea >= 0x2000u && ea != 0x4016u && !ppu && !prg_ram && !jit_fast_bank_write(board, ea);
     if (rd) return !(ea < 0x2000u || ea >= 0x8000u || ea == 0x4016u || (ea & 0xE007u) == 0x2002u || prg_ram);
     return false;
+}
+
+// An absolute store to a PPU register: the last instruction of its block, so that when it needs the generic step
+// (outside a quiet burst: wave_dev.h ppu_write_quiet) the burst resumes at a block's start, the instruction after it.
+inline bool jit_ppu_store(uint32_t op, uint32_t b1, uint32_t b2) {
+    const uint32_t d = kOptab.t[op], ea = b1 | (b2 << 8);
+    return (d & 15u) == M_ABS && (d & D_WRITE) && !(d & D_READ) && ((d >> 8) & 15u) != G_JMP &&
+           ((d >> 8) & 15u) != G_JSR && ea >= 0x2000u && ea < 0x4000u;
 }
 
 // The most a fast instruction of opcode op takes off the burst counter (wave_dev.h jit_maxtake).
@@ -121,6 +132,10 @@ inline JitProgram jit_translate_fixed(const std::vector<uint8_t>& prg) {
             const uint32_t grp = grp_of(a), mode = kOptab.t[rd(a)] & 15u;
             if (generic(a)) {
                 if (grp != G_ILL && grp != G_BRK && grp != G_JMP) entry(next_of(a));
+                break;
+            }
+            if (jit_ppu_store(rd(a), rd(a + 1u), rd(a + 2u))) {
+                entry(next_of(a));
                 break;
             }
             if (grp == G_BR) {
@@ -275,6 +290,10 @@ inline JitProgram jit_translate_banked(const std::vector<uint8_t>& prg, uint32_t
                 const uint32_t grp = grp_of(o), mode = kOptab.t[rd(o)] & 15u, next = o + len_of(o);
                 if (generic(o)) {
                     if (grp != G_ILL && grp != G_BRK && grp != G_JMP && same_page(o, next)) entry(next);
+                    break;
+                }
+                if (jit_ppu_store(rd(o), rd(o + 1u), rd(o + 2u))) {
+                    if (same_page(o, next)) entry(next);
                     break;
                 }
                 if (grp == G_BR) {

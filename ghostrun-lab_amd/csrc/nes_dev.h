@@ -58,9 +58,10 @@ struct Con {
     uint32_t nt_map;                   // 4 x 2 bits
     uint32_t map_fast;                 // what the fast path's mapper writes decide on (wave_dev.h map_write_ok), as
                                        // in the record's mreg: MMC3 the bank select, MMC1 the shift register | count << 8
-    // wave_dev.h run_until_wave's own state, parked here while a burst of fast instructions runs
+    // wave_dev.h run_until_wave's own state, parked here while a burst of fast instructions runs; b_quiet: the burst
+    // starts between vblank and the pre-render line (wave_dev.h ppu_write_quiet)
     uint64_t b_dmc_event, b_target;
-    uint32_t b_instructions, b_pending, b_to_event, b_ecyc, b_dmc_in, b_why, b_budget, b_nmi, b_irq;
+    uint32_t b_instructions, b_pending, b_to_event, b_ecyc, b_dmc_in, b_why, b_budget, b_nmi, b_irq, b_quiet;
 };
 
 struct Cart {

@@ -161,6 +161,29 @@ __device__ __forceinline__ uint32_t status_read(Con& cs) {
 __device__ __forceinline__ void port_write(Hot& h, const Con& cs, uint32_t v) {
     h.ctl = (v & 1u) ? (uni(cs.pad) | 0x100u) : (h.ctl & 0xFFu);
 }
+// PPU register writes ($2000-$3FFF) in a burst that starts between vblank and the pre-render line (cs.b_quiet): the
+// frame log is off from vblank to the pre-render line (nes_dev.h cpu_step's log_on), a burst ends short of the next
+// PPU event (vblank, the $2002 clear, the pre-render line, the sprite-0 check, an MMC3 clock: dots_to_event), and
+// what the writes feed - the log header, the sprite-0 schedule, MMC3's clocks, which fall on visible lines and the
+// pre-render line - is taken at those events, so such a write is the bus's own (nes_dev.h ppu_reg_write) with nothing
+// logged. Whether the fast path can take it, decided before any state changes: not a $2000 write that raises an NMI
+// (the NMI is taken before the next instruction, by the generic step), not MMC2's $2006 / $2007 (the VRAM address
+// flips its latches).
+template <uint32_t B>
+__device__ __forceinline__ bool ppu_write_quiet(const Mem& m, const Con& cs, uint32_t reg, uint32_t v) {
+    if (!uni(cs.b_quiet)) return false;
+    if (reg == 0u && !(uni(cs.ctrl) & 0x80u) && (v & 0x80u) && (uni(cs.status) & 0x80u)) return false;
+    if constexpr (B != NES_BOARD_NROM)
+        if (m.cart.board == NES_BOARD_MMC2 && reg >= 6u) return false;
+    return true;
+}
+__device__ __forceinline__ void ppu_write(const Mem& m, Con& cs, uint32_t reg, uint32_t v) {
+    Access ac;
+    ac.now = 0;
+    ac.log_on = false;
+    ac.dma = false;
+    ppu_reg_write(cs, m, ac, reg, v);
+}
 
 // Byte offset in the PRG image of CPU address `addr` ($8000-$FFFF). NROM maps the image linearly (mirrored).
 template <uint32_t B>
@@ -295,7 +318,9 @@ __device__ __forceinline__ bool br_taken(const Hot& h) {
     return set == ((sub & 8u) != 0);
 }
 
-template <uint32_t B, uint32_t D, bool HOT = false>
+// PPU: absolute PPU register writes of a quiet burst here too (ppu_write_quiet; the translated blocks' instructions,
+// whose register is known when the block is compiled; other stores there and elsewhere: the generic step).
+template <uint32_t B, uint32_t D, bool HOT = false, bool PPU = false>
 __device__ __forceinline__ uint32_t fx(Hot& h, const Mem& m, Con& cs, uint32_t pcs, uint32_t base) {
     constexpr uint32_t PS = kPcShift;
     constexpr bool nrom = B == NES_BOARD_NROM;
@@ -346,7 +371,10 @@ __device__ __forceinline__ uint32_t fx(Hot& h, const Mem& m, Con& cs, uint32_t p
         if constexpr (!zpage && wr && !rd) {
             if (ea >= 0x2000u) {
                 if (ea != 0x4016u) {
-                    if (ea < 0x6000u) return kGeneric;
+                    if (ea < 0x4000u) {
+                        if constexpr (!PPU || mode != M_ABS) return kGeneric;
+                        else if (!ppu_write_quiet<B>(m, cs, ea & 7u, hget(h, src, 0))) return kGeneric;
+                    } else if (ea < 0x6000u) return kGeneric;
                     if (ea >= 0x8000u) {   // (a bank write is an absolute store; an indexed one: the generic step)
                         if constexpr (nrom || mode != M_ABS) return kGeneric;
                         else if (!map_write_ok<B>(h, m, cs, ea, hget(h, src, 0), pcs)) return kGeneric;
@@ -479,6 +507,7 @@ __device__ __forceinline__ uint32_t fx(Hot& h, const Mem& m, Con& cs, uint32_t p
             if constexpr (mode == M_ZP) m.ram[ea] = (uint8_t)res;
             else if constexpr (zpage) m.ram[ea & 0x7FFu] = (uint8_t)res;
             else if (ea < 0x2000u) m.ram[ea & 0x7FFu] = (uint8_t)res;
+            else if (PPU && mode == M_ABS && !rd && ea < 0x4000u) ppu_write(m, cs, ea & 7u, res);
             else if (!nrom && !rd && mode == M_ABS && ea >= 0x8000u) map_write_fast<B>(h, m, cs, ea, res);
             else if (ea >= 0x6000u) m.rec->prg_ram[ea - 0x6000u] = (uint8_t)res;   // (a read-modify-write: here)
             else port_write(h, cs, res);
@@ -569,11 +598,11 @@ constexpr uint32_t jit_maxtake(uint32_t op) {
 // One instruction of a block (inside the block's room), and the block's first instruction alone (no room for the
 // block: the interpreter's own test ends the burst).
 #define JIT_STEP(op, pcs, base)                              \
-    t = fx<B, kOptab.t[op]>(h, m, cs, pcs, base);            \
+    t = fx<B, kOptab.t[op], false, true>(h, m, cs, pcs, base); \
     if (t == kGeneric) { take = t; goto burst_end; }          \
     v -= t;
 #define JIT_ONE(op, pcs, base)                               \
-    t = fx<B, kOptab.t[op]>(h, m, cs, pcs, base);            \
+    t = fx<B, kOptab.t[op], false, true>(h, m, cs, pcs, base); \
     if (v < t) { take = t; goto burst_end; }                  \
     v -= t;                                                   \
     continue;
@@ -685,6 +714,10 @@ __device__ __forceinline__ uint32_t run_until_wave(Con& cs, const Mem& m, const 
             cs.b_budget = budget;
             cs.b_nmi = nmi;
             cs.b_irq = irq;
+            {
+                const uint32_t d0 = uni(cs.frame_dot) + pending;   // the burst's first dot (< the next event)
+                cs.b_quiet = d0 >= NES_VBLANK_DOT && d0 < NES_PRERENDER_DOT ? 1u : 0u;
+            }
             for (;;) {
 #ifdef RLENV_JIT_INC
                 ConstU32* e = (ConstU32*)((ConstU8*)m.cart.fetchw + h.pc);
