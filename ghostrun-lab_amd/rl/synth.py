@@ -13,6 +13,9 @@ cartridges generated here from a seed:
   lives, score, dying, mode) from the pad, idling in a JMP-to-self loop with its logic in the NMI as SMB does,
   so rewards, deaths, level changes, game over and the idle fast-forward all run.
 * ``dmc_cart(seed)`` - NROM-128 playing DMC samples (rate and loop changes, starts, stops, status polls).
+* ``vblank_io_cart(seed)`` - NROM-128 whose NMI writes every PPU register in vblank (OAM through $2003/$2004 with
+  the address wrapping, palette mirrors, a column with the increment of 32, register mirrors, an indexed store) and
+  every fourth frame takes a nested NMI by turning NMI off and on while the vblank flag is up.
 * ``poll_cart(seed)`` - NROM-128 with NMI off that polls instead: its main loop waits for vblank on $2002 bit 7,
   does the vblank work, waits for the sprite-0 flag to clear and then to be set (bit 6) and splits the scroll.
 * ``fault_cart(nmis)`` - NROM-128 that hits an unofficial opcode after `nmis` frames (the emulator-fault end).
@@ -328,6 +331,94 @@ def modes_cart(seed: int = 0, blocks: int = 12) -> bytes:
     a.op('RTI')
     for name, t in (('t_pal', pal), ('t_nt', nt), ('t_oam', oam), ('t_mix', mix), ('t_ctrl', [c for c, _ in MODES]),
                     ('t_mask', [m for _, m in MODES])):
+        a.label(name)
+        a.data(bytes(int(v) for v in t))
+    code = a.assemble()
+    assert len(code) <= 0x3FFA, len(code)
+    prg = bytearray(16384)
+    prg[:len(code)] = code
+    vec = (a.labels['nmi'], a.labels['reset'], a.labels['irq'])
+    prg[0x3FFA:0x4000] = bytes(sum(((v & 0xFF, v >> 8) for v in vec), ()))
+    chr_ = rng.integers(0, 256, 8192, dtype=np.uint8).tobytes()
+    return ines(bytes(prg), chr_, 0, vertical=True)
+
+
+NMI_DEPTH, NESTED = 0x26, 0x27           # the vblank I/O cart's NMI nesting flag and its count of nested NMIs
+
+
+def vblank_io_cart(seed: int = 0, blocks: int = 12) -> bytes:
+    """NROM-128 cartridge like nrom_cart whose NMI, between vblank and the pre-render line, uses every PPU register
+    write there is: every fourth frame it turns NMI off and on again before reading $2002, so the still-raised vblank
+    flag takes a second (nested) NMI, which counts itself in NESTED and returns; then the OAM DMA and an OAM patch
+    through $2003/$2004 (the entry of sprite (FRAMES & 15) + 2, and every eighth frame four bytes from $FE on, which
+    wrap into sprite 0), one palette entry (FRAMES & 31, the $3F10 mirrors included), six nametable bytes down a
+    column with the increment of 32 through the $2007 mirror $2FFF, one byte by an indexed store (STA $2000,X), a
+    buffered $2007 read, the four counter bytes and the scroll through the $2005 mirror $3FFD, and the mask through
+    $3FF9."""
+    rng = np.random.default_rng([0x56494F00, seed])
+    pal, nt, oam, mix = _tables(rng)
+    a = Asm(0xC000)
+    tables = dict(pal='t_pal', nt='t_nt', oam='t_oam')
+    a.label('reset')
+    _reset_common(a, 0x90, tables)
+    a.label('main')
+    _read_pad(a, 'm')
+    _pad_moves(a, 't_mix')
+    _filler(a, rng, blocks, 'f', 't_mix')
+    a.op('JMP', 'abs', 'main')
+    a.label('nmi')
+    a.op('PHA'); a.op('TXA'); a.op('PHA'); a.op('TYA'); a.op('PHA')
+    a.op('LDA', 'zp', NMI_DEPTH); a.op('BEQ', 'rel', 'vio_first')
+    a.op('INC', 'zp', NESTED); a.op('JMP', 'abs', 'vio_out')
+    a.label('vio_first')
+    a.op('INC', 'zp', NMI_DEPTH)
+    a.op('LDA', 'zp', FRAMES); a.op('AND', 'imm', 3); a.op('BNE', 'rel', 'vio_dma')
+    a.op('LDA', 'imm', 0x10); a.op('STA', 'abs', 0x2000); a.op('LDA', 'imm', 0x90); a.op('STA', 'abs', 0x2000)
+    a.label('vio_dma')
+    a.op('LDA', 'imm', 0); a.op('STA', 'abs', 0x2003); a.op('LDA', 'imm', OAM_PAGE >> 8); a.op('STA', 'abs', 0x4014)
+    # sprite (FRAMES & 15) + 2: y, tile, attributes, x
+    a.op('LDA', 'zp', FRAMES); a.op('AND', 'imm', 15); a.op('CLC'); a.op('ADC', 'imm', 2); a.op('ASL', 'acc')
+    a.op('ASL', 'acc'); a.op('STA', 'abs', 0x2003)
+    a.op('LDA', 'zp', PY); a.op('CLC'); a.op('ADC', 'imm', 16); a.op('STA', 'abs', 0x2004)
+    a.op('LDA', 'zp', CNT_LO); a.op('STA', 'abs', 0x2004)
+    a.op('LDA', 'zp', FRAMES); a.op('AND', 'imm', 0xE3); a.op('STA', 'abs', 0x2004)
+    a.op('LDA', 'zp', PX); a.op('EOR', 'imm', 0x55); a.op('STA', 'abs', 0x2004)
+    a.op('LDA', 'zp', FRAMES); a.op('AND', 'imm', 7); a.op('BNE', 'rel', 'vio_nowrap')
+    a.op('LDA', 'imm', 0xFE); a.op('STA', 'abs', 0x2003)
+    for v in (0x21, 0x40, 0x30, 0x00):    # sprite 63's attributes and x, then sprite 0's y and tile
+        a.op('LDA', 'imm', v); a.op('EOR', 'zp', FRAMES); a.op('STA', 'abs', 0x2004)
+    a.label('vio_nowrap')
+    a.op('LDA', 'zp', PY); a.op('STA', 'abs', OAM_PAGE + 4); a.op('LDA', 'zp', PX); a.op('STA', 'abs', OAM_PAGE + 7)
+    a.op('LDA', 'abs', 0x2002)
+    # palette entry FRAMES & 31
+    a.op('LDA', 'imm', 0x3F); a.op('STA', 'abs', 0x2006); a.op('LDA', 'zp', FRAMES); a.op('AND', 'imm', 0x1F)
+    a.op('STA', 'abs', 0x2006); a.op('LDA', 'zp', CNT_LO); a.op('EOR', 'zp', PAD); a.op('STA', 'abs', 0x2007)
+    # a column: nametable 1 or 3 (FRAMES bit 5; the counter bytes below go to nametable 0), column FRAMES & 31,
+    # 6 bytes with the increment of 32
+    a.op('LDA', 'imm', 0x94); a.op('STA', 'abs', 0x2000)
+    a.op('LDA', 'zp', FRAMES); a.op('LSR', 'acc'); a.op('LSR', 'acc'); a.op('AND', 'imm', 0x08); a.op('ORA', 'imm', 0x24)
+    a.op('STA', 'abs', 0x2006); a.op('LDA', 'zp', FRAMES); a.op('AND', 'imm', 0x1F); a.op('STA', 'abs', 0x2006)
+    a.op('LDX', 'imm', 6)
+    a.label('vio_col')
+    a.op('TXA'); a.op('EOR', 'zp', FRAMES); a.op('STA', 'abs', 0x2FFF); a.op('DEX'); a.op('BNE', 'rel', 'vio_col')
+    a.op('LDA', 'imm', 0x90); a.op('STA', 'abs', 0x2000)
+    a.op('LDX', 'imm', 7); a.op('LDA', 'zp', PAD); a.op('STA', 'abx', 0x2000)
+    a.op('LDA', 'abs', 0x2007)
+    a.op('LDA', 'zp', NTP_HI); a.op('STA', 'abs', 0x2006); a.op('LDA', 'zp', NTP_LO); a.op('STA', 'abs', 0x2006)
+    for v in (CNT_LO, CNT_HI, ACNT, PAD):
+        a.op('LDA', 'zp', v); a.op('STA', 'abs', 0x2007)
+    a.op('LDA', 'zp', NTP_LO); a.op('CLC'); a.op('ADC', 'imm', 4); a.op('STA', 'zp', NTP_LO)
+    a.op('LDA', 'zp', NTP_HI); a.op('ADC', 'imm', 0); a.op('AND', 'imm', 0x03); a.op('ORA', 'imm', 0x20)
+    a.op('STA', 'zp', NTP_HI)
+    a.op('LDA', 'zp', PX); a.op('STA', 'abs', 0x3FFD); a.op('LDA', 'imm', 0); a.op('STA', 'abs', 0x3FFD)
+    a.op('LDA', 'zp', CTRL_SHADOW); a.op('STA', 'abs', 0x2000); a.op('LDA', 'imm', 0x1E); a.op('STA', 'abs', 0x3FF9)
+    a.op('INC', 'zp', FRAMES); a.op('LDA', 'imm', 1); a.op('STA', 'zp', NMIFLAG)
+    a.op('LDA', 'imm', 0); a.op('STA', 'zp', NMI_DEPTH)
+    a.label('vio_out')
+    _nmi_end(a)
+    a.label('irq')
+    a.op('RTI')
+    for name, t in (('t_pal', pal), ('t_nt', nt), ('t_oam', oam), ('t_mix', mix)):
         a.label(name)
         a.data(bytes(int(v) for v in t))
     code = a.assemble()

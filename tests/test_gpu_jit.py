@@ -51,6 +51,16 @@ def test_translated_modes_cart():
 
 
 @pytest.mark.gpu
+def test_translated_vblank_io_cart():
+    print('case: translated vblank I/O cart seed 2, 16 consoles, raw pads, sticky, 20 decisions (every PPU register '
+          'written between vblank and the pre-render line, nested NMIs)', flush=True)
+    cpu, gpu, st = translated_pair(16, synth.vblank_io_cart(2), seed=14, sticky=True, idle_max=0, dropout=False,
+                                   pad_mode=True)
+    assert st['frame_bank'] and not st['banked']
+    run(cpu, gpu, 20, 6, True)
+
+
+@pytest.mark.gpu
 def test_translated_smb_like_idle_loop_and_ends():
     print('case: translated SMB-like seed 2, 24 consoles, raw pads, level end 0, Geometric(1/16) ends, idle 0..3, '
           '40 decisions', flush=True)

@@ -69,6 +69,14 @@ def test_modes_cart_every_sprite_and_mask_mode():
 
 
 @pytest.mark.gpu
+def test_vblank_io_cart_every_ppu_register_in_vblank():
+    print('case: vblank I/O cart seed 1, 16 consoles, raw pads, sticky, 20 decisions (OAM through $2003/$2004, palette '
+          'mirrors, a column with the increment of 32, register mirrors, an indexed store, nested NMIs)', flush=True)
+    cpu, gpu = pair(16, synth.vblank_io_cart(1), seed=13, sticky=True, idle_max=0, dropout=False, pad_mode=True)
+    run(cpu, gpu, 20, 5, True)
+
+
+@pytest.mark.gpu
 def test_mmc3_stress():
     print('case: MMC3 seed 3, 16 consoles, raw pads, IRQ + sprite-0 + bank switches', flush=True)
     cpu, gpu = pair(16, synth.mmc3_cart(3), seed=9, sticky=True, idle_max=0, dropout=False, pad_mode=True)

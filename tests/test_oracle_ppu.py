@@ -574,3 +574,40 @@ def test_parity_carts_split_lines_mid_line_and_hit_sprite0(make):
         con.lib.orc_sprite0_hit(con.rec.ctypes.data, con.cart_ptr(), ctypes.byref(hit))
         hits += hit.value
     assert mid >= 10 and hits >= 10, (mid, hits)
+
+
+def test_vblank_io_cart_writes_every_ppu_register_in_vblank():
+    """The vblank I/O cart's NMI, stepped one instruction at a time on the oracle over 24 frames: by the time it
+    counts its frame, the OAM holds the sprite it wrote through $2003/$2004 (and, every eighth frame, the four bytes
+    from $FE on, wrapping into sprite 0), the palette entry FRAMES & 31 (its $3F10 mirror folded) holds the byte
+    written through $2006/$2007, the nametable column holds its six bytes 32 apart (written through the $2007 mirror
+    $2FFF) and the byte of the indexed store below them, and a nested NMI has been taken exactly in the frames whose
+    counter is a multiple of 4 (NMI turned off and on while the vblank flag was up)."""
+    con = Console(synth.vblank_io_cart(1))
+    ram = con.ram()
+    checked, nested_frames = 0, 0
+    for _ in range(400000):
+        depth = int(ram[synth.NMI_DEPTH])
+        con.step()
+        if depth == 0 and ram[synth.NMI_DEPTH] == 1 and ram[synth.FRAMES] >= 2:   # the first NMI's INC NMI_DEPTH
+            f, px, py, cnt, pad, nested = (int(ram[k]) for k in (synth.FRAMES, synth.PX, synth.PY, synth.CNT_LO,
+                                                                 synth.PAD, synth.NESTED))
+            while ram[synth.FRAMES] == f:
+                con.step()
+            oam, pal, nt = con.mem('oam', 256), con.mem('pal', 32), con.mem('nt', 2048)
+            s = ((f & 15) + 2) * 4
+            assert list(oam[s:s + 4]) == [(py + 16) & 0xFF, cnt, f & 0xE3, px ^ 0x55], f
+            if f % 8 == 0:
+                assert list(oam[[0xFE, 0xFF, 0, 1]]) == [0x21 ^ f, 0x40 ^ f, 0x30 ^ f, f], f
+            i = f & 31
+            assert pal[i & 0x0F if (i & 0x13) == 0x10 else i] == (cnt ^ pad) & 0x3F, f
+            base = 1024 + (f & 31)                          # nametable 1 or 3: one under vertical mirroring
+            assert [int(nt[base + 32 * k]) for k in range(6)] == [(6 - k) ^ f for k in range(6)], f
+            assert nt[base + 192] == pad, f
+            took = int(ram[synth.NESTED]) - nested
+            assert took == (1 if f % 4 == 0 else 0), f
+            nested_frames += took
+            checked += 1
+            if checked == 24:
+                break
+    assert checked == 24 and nested_frames == 6, (checked, nested_frames)
