@@ -1,7 +1,8 @@
 """HIP library vs the CPU oracle on the paths the other parity tests leave out: the DMC sample channel, the emulator
 fault end, the instruction-budget exit, rlenv_step_game on a two-game env, and the benchmark shapes at full size
 (8192 NROM consoles with sticky moves; the rollout shape with Geometric ends and button dropout; 16384 MMC3
-consoles, two rounds of waves), checked on console subsets that the oracle steps with rlenv_step_range."""
+consoles, two rounds of waves; twelve games of 3072 consoles on their own carts and streams), checked on console
+subsets that the oracle steps with rlenv_step_range."""
 import ctypes
 import os
 
@@ -174,3 +175,62 @@ def test_full_size_mmc3_two_wave_rounds_subset():
     print('case: MMC3 seed 1, 16384 consoles, translated, 16 decisions, consoles 0-31 and 16352-16383', flush=True)
     subset_run(16384, synth.mmc3_cart(1), [(0, 32), (16352, 16384)], 16, 43, banked=True, seed=3, sticky=False,
                idle_max=0, dropout=False, pad_mode=True)
+
+
+# The twelve-games workload's carts: the SMB-like cart for the first game, then a board per game in turn, seeds 1..12.
+TWELVE_BOARDS = ('smb_like', 'nrom', 'mmc1', 'uxrom', 'cnrom', 'mmc3', 'mmc2', 'nrom', 'mmc1', 'uxrom', 'cnrom', 'mmc3')
+
+
+@pytest.mark.gpu
+def test_full_size_twelve_games_subset():
+    """The multi-game shape: 12 games x 3072 consoles, each game on its own full-size seed-generated cart and its own
+    translated kernel (banked boards included), every game stepping on its own stream; in every game consoles 0-7 and
+    3064-3071 against the oracle (rlenv_step_range per game) for 12 decisions, every output and, at the end, every
+    console record. The compiled translations come from the translation cache in the build folder when it holds
+    them (a compile otherwise)."""
+    from rl.rlenv import GAMES
+    print('case: twelve games x 3072 consoles (full-size carts, all translated), sticky, 12 decisions, consoles 0-7 '
+          'and 3064-3071 of every game', flush=True)
+    cache = os.path.join(os.path.dirname(HIP_LIB), 'jit_cache')
+    own_cache = 'RLENV_JIT_CACHE' not in os.environ and os.path.isdir(cache)
+    make = dict(smb_like=synth.smb_like_cart, nrom=synth.nrom_cart, mmc1=synth.mmc1_cart, uxrom=synth.uxrom_cart,
+                cnrom=synth.cnrom_cart, mmc3=synth.mmc3_cart, mmc2=synth.mmc2_cart)
+    roms = {g: make[b](1 + i) for i, (g, b) in enumerate(zip(GAMES, TWELVE_BOARDS))}
+    n = 3072
+    counts = {g: n for g in GAMES}
+    kw = dict(seed=1, sticky=True, idle_max=0, dropout=False, pad_mode=True, ram_hash=True, roms=roms,
+              boot={g: bytes(4) for g in GAMES})
+    if own_cache:
+        os.environ['RLENV_JIT_CACHE'] = cache
+    try:
+        gpu = RlEnv(counts, device='cuda', lib_path=HIP_LIB, **kw)
+        gpu.jit_wait()
+    finally:
+        if own_cache:
+            del os.environ['RLENV_JIT_CACHE']
+    for gi, g in enumerate(GAMES):
+        st = gpu.jit_status(gi)
+        assert st['state'] == 'loaded', (g, st)
+    cpu = RlEnv(counts, device='cpu', lib_path=ORACLE_LIB, **kw)
+    ranges = [(0, 8), (n - 8, n)]
+    rows = torch.cat([torch.arange(gi * n + a, gi * n + b) for gi in range(len(GAMES)) for a, b in ranges])
+    g = torch.Generator().manual_seed(44)
+    gpu.start()
+    cpu.start()
+    for t in range(12):
+        act = torch.randint(0, 256, (len(GAMES) * n,), generator=g, dtype=torch.int16)
+        gpu.actions.copy_(act.cuda())
+        cpu.actions.copy_(act)
+        gpu.step()
+        for gi in range(len(GAMES)):
+            for a, b in ranges:
+                cpu.step_range(gi, a, b - a, cpu.obs, cpu.emph)
+        torch.cuda.synchronize()
+        for k in OUTS:
+            want, got = getattr(cpu, k)[rows].numpy(), getattr(gpu, k)[rows.cuda()].cpu().numpy()
+            if not np.array_equal(want, got):
+                bad = np.argwhere(want != got)
+                raise AssertionError(f'decision {t}: {k} differs at {len(bad)} places, first {bad[:3].tolist()}')
+    for gi in range(len(GAMES)):
+        for a, b in ranges:
+            assert np.array_equal(cpu.consoles(gi, a, b - a), gpu.consoles(gi, a, b - a)), (GAMES[gi], a, b)
