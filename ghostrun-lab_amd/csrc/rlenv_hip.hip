@@ -1835,6 +1835,29 @@ int rl_gather_envs(void* dst, const void* src, const int64_t* envs, int n, int T
     return 0;
 }
 
+int rl_stream_create(void** stream) {
+    hipStream_t s = nullptr;
+    if (!stream) { g_error = "stream_create: null output"; return 1; }
+    const hipError_t e = hipStreamCreateWithFlags(&s, hipStreamNonBlocking);
+    if (e != hipSuccess) {
+        (void)hipGetLastError();
+        g_error = std::string("stream_create: ") + hipGetErrorString(e);
+        return 1;
+    }
+    *stream = s;
+    return 0;
+}
+int rl_stream_destroy(void* stream) {
+    if (!stream) { g_error = "stream_destroy: null stream"; return 1; }
+    const hipError_t e = hipStreamDestroy(static_cast<hipStream_t>(stream));
+    if (e != hipSuccess) {
+        (void)hipGetLastError();
+        g_error = std::string("stream_destroy: ") + hipGetErrorString(e);
+        return 1;
+    }
+    return 0;
+}
+
 int rl10_smb_run(const uint8_t* ram15, int T, int N, int frames, void* state, float* reward, uint8_t* done,
                  void* stream) {
     if (N <= 0 || T <= 0) return check("rl10_smb_run");

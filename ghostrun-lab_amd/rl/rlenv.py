@@ -98,6 +98,8 @@ _ABI = {
     'rl_memcpy_async': (_I, [_P, _P, _SZ, _P], True),
     'rl_gather_rows': (_I, [_P, _P, _P, _I, _SZ, _P], True),
     'rl_gather_envs': (_I, [_P, _P, _P, _I, _I, _I, _SZ, _P], True),
+    'rl_stream_create': (_I, [_P], True),
+    'rl_stream_destroy': (_I, [_P], True),
 }
 
 

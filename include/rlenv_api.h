@@ -82,6 +82,12 @@ int rl_gather_rows(void* dst, const void* src, const int64_t* rows, int nrows, s
                    void* stream);                                                  /* rlenv.cu:400-409 */
 int rl_gather_envs(void* dst, const void* src, const int64_t* envs, int n, int T, int N, size_t row_bytes,
                    void* stream);                                                  /* rlenv.cu:411-421 */
+/* Streams for the rollout store's copies (no reference counterpart; the reference trainer's streams are torch's):
+ * a stream at the default priority that does not wait for the null stream, and its release. torch's own streams
+ * are never destroyed, and the runtime spreads streams over its hardware queues by how many each already serves, so
+ * a store whose streams outlive it changes where every later stream of the process runs. */
+int rl_stream_create(void** stream);
+int rl_stream_destroy(void* stream);
 
 /* Additions of this build for the benchmark workloads (no reference counterpart):
  *  pad mode 1: actions hold raw pad bytes (0..255) instead of move ids; sticky repeats the previous frame's
