@@ -185,12 +185,12 @@ TWELVE_BOARDS = ('smb_like', 'nrom', 'mmc1', 'uxrom', 'cnrom', 'mmc3', 'mmc2', '
 def test_full_size_twelve_games_subset():
     """The multi-game shape: 12 games x 3072 consoles, each game on its own full-size seed-generated cart and its own
     translated kernel (banked boards included), every game stepping on its own stream; in every game consoles 0-7 and
-    3064-3071 against the oracle (rlenv_step_range per game) for 12 decisions, every output and, at the end, every
-    console record. The compiled translations come from the translation cache in the build folder when it holds
+    3064-3071 against the oracle (rlenv_step_range per game) for 40 decisions (the SMB-like game's episodes end and
+    restart among them), every output and, at the end, every console record. The compiled translations come from the translation cache in the build folder when it holds
     them (a compile otherwise)."""
     from rl.rlenv import GAMES
-    print('case: twelve games x 3072 consoles (full-size carts, all translated), sticky, 12 decisions, consoles 0-7 '
-          'and 3064-3071 of every game', flush=True)
+    print('case: twelve games x 3072 consoles (full-size carts, all translated), sticky, consoles 0-7 '
+          'and 3064-3071 of every game, 40 decisions', flush=True)
     cache = os.path.join(os.path.dirname(HIP_LIB), 'jit_cache')
     own_cache = 'RLENV_JIT_CACHE' not in os.environ and os.path.isdir(cache)
     make = dict(smb_like=synth.smb_like_cart, nrom=synth.nrom_cart, mmc1=synth.mmc1_cart, uxrom=synth.uxrom_cart,
@@ -217,7 +217,8 @@ def test_full_size_twelve_games_subset():
     g = torch.Generator().manual_seed(44)
     gpu.start()
     cpu.start()
-    for t in range(12):
+    ends = 0
+    for t in range(40):
         act = torch.randint(0, 256, (len(GAMES) * n,), generator=g, dtype=torch.int16)
         gpu.actions.copy_(act.cuda())
         cpu.actions.copy_(act)
@@ -231,6 +232,8 @@ def test_full_size_twelve_games_subset():
             if not np.array_equal(want, got):
                 bad = np.argwhere(want != got)
                 raise AssertionError(f'decision {t}: {k} differs at {len(bad)} places, first {bad[:3].tolist()}')
+        ends += int(cpu.done[rows].sum())
+    assert ends > 0, 'no episode ended in the checked consoles'
     for gi in range(len(GAMES)):
         for a, b in ranges:
             assert np.array_equal(cpu.consoles(gi, a, b - a), gpu.consoles(gi, a, b - a)), (GAMES[gi], a, b)
