@@ -374,7 +374,7 @@ def bench_env(args, name, K, W, baseline):
     if translated:   # games whose decision frames ran their translated kernel (state 'loaded')
         out['translated'] = translated
     if kern:
-        out['roofline'] = _roofline(name, kern, N, K, dt, out_bytes)
+        out['roofline'] = _roofline(name, kern, N, K, dt, out_bytes, games=len(counts))
         out['kernels'] = kern
         counters = _counters(name)
         if counters:
@@ -410,7 +410,7 @@ def _kernel_times(env, N, K, dt):
     return kern
 
 
-def _roofline(name, kern, n, K, dt, out_bytes):
+def _roofline(name, kern, n, K, dt, out_bytes, games=1):
     """The dominant kernel (the most time per step): its algorithmic bytes per launch over its average launch time
     against HBM (the `bound`/`frac` of the line), and the whole step against HBM. Where the committed counter run of
     the same workload (profiles/counters.json, a deterministic workload) covers the kernels, what actually limits
@@ -453,6 +453,10 @@ def _roofline(name, kern, n, K, dt, out_bytes):
         r['note'] = ('one console per wavefront: the 6502 and the PPU event logic run on the scalar unit, which the '
                      'renderer\'s per-line control flow shares; the emulator\'s memory traffic is console state staged '
                      'through LDS, not algorithmic bytes')
+    if games > 1:
+        r['note'] = ('the games step on streams of their own, which share the runtime\'s hardware queues, so a launch\'s '
+                     'event-clock time includes other games\' launches queued between its events: the kernel\'s '
+                     'achieved figure is a lower bound, the step figures are exact')
     if name == 'rollout-pack6':
         r['host_link_gbps'] = round(PACK6_BYTES * n * K / dt / 1e9, 3)
         r['limiter'] = 'host link'
