@@ -214,3 +214,25 @@ def test_translated_banked_boards(board):
                                    end_prob=1 / 8)
     print(f'  {st["blocks"]} blocks, {st["instructions"]} instructions, compiled in {st["compile_ms"]} ms', flush=True)
     run(cpu, gpu, 16, 51, True)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize('cart', ['nrom', 'cnrom', 'smb_like', 'poll', 'modes', 'vblank_io', 'mmc3', 'mmc1', 'uxrom',
+                                  'mmc2', 'seam'])
+def test_translated_seed_sweep(cart):
+    """Every cart generator at a seed no other translated test uses, translated (the banked boards at a smaller size,
+    to keep the compiles short): sticky repeats, button dropout, idle frames and Geometric(1/10) episode ends, every
+    output and record against the oracle every third decision."""
+    small = dict(blocks=6, sub_blocks=4)
+    make = {'nrom': lambda: synth.nrom_cart(21), 'cnrom': lambda: synth.cnrom_cart(21),
+            'smb_like': lambda: synth.smb_like_cart(21), 'poll': lambda: synth.poll_cart(21),
+            'modes': lambda: synth.modes_cart(21), 'vblank_io': lambda: synth.vblank_io_cart(21),
+            'mmc3': lambda: synth.mmc3_cart(21, **small), 'mmc1': lambda: synth.mmc1_cart(21, **small),
+            'uxrom': lambda: synth.uxrom_cart(21, **small), 'mmc2': lambda: synth.mmc2_cart(21, **small),
+            'seam': lambda: synth.seam_cart(21, blocks=4, sub_blocks=3)}
+    print(f'case: translated {cart} cart seed 21, 16 consoles, sticky, dropout, idle 0..1, ends 1/10, 12 decisions',
+          flush=True)
+    cpu, gpu, st = translated_pair(16, make[cart](), seed=21, sticky=True, idle_max=1, dropout=True, pad_mode=True,
+                                   end_prob=1 / 10, dropout_gap=1 / 8)
+    print(f'  {st["blocks"]} blocks, {st["instructions"]} instructions, compiled in {st["compile_ms"]} ms', flush=True)
+    run(cpu, gpu, 12, 121, True, check_every=3)

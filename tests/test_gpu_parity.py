@@ -136,3 +136,22 @@ def test_mmc3_code_across_prg_windows(seed):
           'branches across them, JMP ($04FF), code in RAM, 16 decisions', flush=True)
     cpu, gpu = pair(16, synth.seam_cart(seed), seed=30 + seed, sticky=True, idle_max=1, dropout=False, pad_mode=True)
     run(cpu, gpu, 16, 11 + seed, True)
+
+
+SWEEP = {'nrom': synth.nrom_cart, 'cnrom': synth.cnrom_cart, 'uxrom': synth.uxrom_cart, 'mmc1': synth.mmc1_cart,
+         'mmc3': synth.mmc3_cart, 'mmc2': synth.mmc2_cart, 'smb_like': synth.smb_like_cart, 'seam': synth.seam_cart,
+         'poll': synth.poll_cart, 'modes': synth.modes_cart, 'vblank_io': synth.vblank_io_cart}
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize('seed', [21, 22])
+@pytest.mark.parametrize('cart', sorted(SWEEP))
+def test_seed_sweep_every_cart_generator(cart, seed):
+    """Every cart generator at two seeds no other test uses, at its default size, on the library's kernels (16
+    consoles are below the translation threshold): raw pads with sticky repeats, button dropout, idle frames and
+    Geometric(1/10) episode ends, every output and record against the oracle every third decision."""
+    print(f'case: {cart} cart seed {seed}, 16 consoles, sticky, dropout, idle 0..1, ends 1/10, 12 decisions',
+          flush=True)
+    cpu, gpu = pair(16, SWEEP[cart](seed), seed=seed, sticky=True, idle_max=1, dropout=True, pad_mode=True,
+                    end_prob=1 / 10, dropout_gap=1 / 8)
+    run(cpu, gpu, 12, seed + 100, True, check_every=3)
