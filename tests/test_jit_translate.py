@@ -84,3 +84,26 @@ def test_translation_compiles_with_hiprtc():
     r = lib.rlenv_jit_translate(rom, len(rom), 1, out, text, len(text))
     assert r == 0, (lib.rlenv_error() or b'').decode()[:2000]
     assert out[0] > 0 and out[3] > 0, list(out)   # blocks, code bytes
+
+
+def test_ppu_register_stores_end_their_blocks():
+    """An absolute store to a PPU register ($2000-$3FFF, the mirrors included) takes the generic step outside the
+    part of a frame between vblank and the pre-render line, and the burst then resumes at the next instruction, so
+    the translation makes that instruction a leader: such a store is the last instruction of its block. The vblank
+    I/O cart stores to every register, through mirrors too; an indexed store (STA $2000,X) is not absolute and stays
+    inside its block."""
+    text = translate(synth.vblank_io_cart(1))
+    stores, ended = 0, 0
+    regs = set()
+    for start, n, body in blocks(text):
+        steps = re.findall(r'JIT_STEP\(0x([0-9A-F]{2})u, 0x[0-9A-F]+u, 0x([0-9A-F]+)u\)', body)
+        for i, (op, base) in enumerate(steps):
+            op, base = int(op, 16), int(base, 16)
+            if op in (0x8D, 0x8E, 0x8C) and 0x2000 <= base < 0x4000:
+                stores += 1
+                regs.add(base & 7)
+                assert i == len(steps) - 1, body
+                tail = body[body.rfind('JIT_STEP'):]
+                assert 'JIT_STEP' not in tail[8:] and ('goto JB_' in tail or 'continue;' in tail), body
+                ended += 1
+    assert stores == ended and stores >= 30 and regs == {0, 1, 3, 4, 5, 6, 7}, (stores, sorted(regs))
